@@ -1,0 +1,408 @@
+"""`cuda_rasterizer` -- drop-in for the reference extension module of the same name.
+
+The reference builds a pybind11 module with seven functions
+(src/cuda/rasterizer.cpp:442-464) that src/cuda/wrapper.py imports.  This
+package exposes the same seven functions with the same positional signatures,
+tensor layouts and return tuples, implemented by hand-written gfx950 HIP
+kernels behind a C ABI (libgsraster.so, include/gs_rasterizer.h).  Outputs are
+allocated with PyTorch on the first input's device; kernels run on the current
+HIP stream of that device.
+
+Behavioural notes relative to the reference:
+- Culling and blending inclusion follow the reference's Torch rasterizer
+  (src/torch_rasterizer.py), the repository's correctness oracle: strict
+  near/far and image-bound tests, non-finite covariances culled,
+  E < chi_squared_threshold.
+- project_points_backward returns the exact derivative (the reference kernel
+  doubles the Jacobian off-diagonal term, src/cuda/kernel.cu:384-394).
+- Inputs are made contiguous; wrong dtype, device or shape raises RuntimeError
+  (the reference raises only on dtype).
+- rasterize_backward accepts an optional `rendered_image` (the forward output)
+  to skip recomputing each pixel's colour.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import RasterizerError
+
+__all__ = [
+    "project_points",
+    "project_points_backward",
+    "evaluate_spherical_harmonics",
+    "evaluate_spherical_harmonics_backward",
+    "compute_tile_intersection",
+    "compute_tile_intersection_debug",
+    "rasterize",
+    "rasterize_backward",
+    "RasterizerError",
+]
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _prep(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple, device) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if device is not None and t.device != device:
+        raise RuntimeError(f"{name}: expected device {device}, got {t.device}")
+    if tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+    return t.contiguous()
+
+
+def _device_of(t: torch.Tensor) -> torch.device:
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"expected a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"cuda_rasterizer runs on the GPU only; got a tensor on {t.device} "
+            "(there is no CPU fallback)"
+        )
+    return t.device
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def project_points(
+    points_world,
+    scales,
+    quaternions,
+    opacities,
+    world_to_camera,
+    intrinsic,
+    near_plane,
+    far_plane,
+    min_opacity,
+    min_radius,
+    max_radius,
+    width,
+    height,
+):
+    """Reference: src/cuda/rasterizer.cpp:140-191.
+
+    Returns (points_image[N,2], depths[N], cov_image[N,3], cov_inv_image[N,3],
+    radii[N,2] float32, mask[N] bool).
+    """
+    dev = _device_of(points_world)
+    n = points_world.shape[0]
+    f32 = torch.float32
+    points_world = _prep(points_world, "points_world", f32, (n, 3), dev)
+    scales = _prep(scales, "scales", f32, (n, 3), dev)
+    quaternions = _prep(quaternions, "quaternions", f32, (n, 4), dev)
+    opacities = _prep(opacities, "opacities", f32, (n,), dev)
+    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
+    intrinsic = _prep(intrinsic, "intrinsic", f32, (3, 3), dev)
+    points_image = torch.empty((n, 2), dtype=f32, device=dev)
+    depths = torch.empty((n,), dtype=f32, device=dev)
+    cov_image = torch.empty((n, 3), dtype=f32, device=dev)
+    cov_inv_image = torch.empty((n, 3), dtype=f32, device=dev)
+    radii = torch.empty((n, 2), dtype=f32, device=dev)
+    mask = torch.empty((n,), dtype=torch.bool, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("project_points", dev)
+        _lib.check(
+            _lib.load().gs_project_points(
+                _ptr(points_world), _ptr(scales), _ptr(quaternions), _ptr(opacities),
+                _ptr(world_to_camera), _ptr(intrinsic), n, float(near_plane), float(far_plane),
+                float(min_opacity), float(min_radius), float(max_radius), int(width), int(height),
+                _ptr(points_image), _ptr(depths), _ptr(cov_image), _ptr(cov_inv_image),
+                _ptr(radii), _ptr(mask), _stream(dev),
+            ),
+            "project_points",
+        )
+        _lib.timer.stop(ev, dev)
+    return points_image, depths, cov_image, cov_inv_image, radii, mask
+
+
+def project_points_backward(
+    grad_points_image,
+    grad_cov_inv_image,
+    points_world,
+    scales,
+    quaternions,
+    opacities,
+    world_to_camera,
+    intrinsic,
+    width,
+    height,
+    cov_image,
+    mask,
+):
+    """Reference: src/cuda/rasterizer.cpp:193-232.
+
+    Returns (grad_points_world[N,3], grad_scales[N,3], grad_quaternions[N,4]).
+    """
+    dev = _device_of(points_world)
+    n = points_world.shape[0]
+    f32 = torch.float32
+    grad_points_image = _prep(grad_points_image, "grad_points_image", f32, (n, 2), dev)
+    grad_cov_inv_image = _prep(grad_cov_inv_image, "grad_cov_inv_image", f32, (n, 3), dev)
+    points_world = _prep(points_world, "points_world", f32, (n, 3), dev)
+    scales = _prep(scales, "scales", f32, (n, 3), dev)
+    quaternions = _prep(quaternions, "quaternions", f32, (n, 4), dev)
+    opacities = _prep(opacities, "opacities", f32, (n,), dev)
+    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
+    intrinsic = _prep(intrinsic, "intrinsic", f32, (3, 3), dev)
+    cov_image = _prep(cov_image, "cov_image", f32, (n, 3), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    g_means = torch.empty((n, 3), dtype=f32, device=dev)
+    g_scales = torch.empty((n, 3), dtype=f32, device=dev)
+    g_quats = torch.empty((n, 4), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("project_points_backward", dev)
+        _lib.check(
+            _lib.load().gs_project_points_backward(
+                _ptr(grad_points_image), _ptr(grad_cov_inv_image), _ptr(points_world),
+                _ptr(scales), _ptr(quaternions), _ptr(opacities), _ptr(world_to_camera),
+                _ptr(intrinsic), n, int(width), int(height), _ptr(cov_image), _ptr(mask),
+                _ptr(g_means), _ptr(g_scales), _ptr(g_quats), _stream(dev),
+            ),
+            "project_points_backward",
+        )
+        _lib.timer.stop(ev, dev)
+    return g_means, g_scales, g_quats
+
+
+def evaluate_spherical_harmonics(
+    camera_pos, points_world, sh_coeffs_dc, sh_coeffs_rest, mask, sh_sigmoid=False
+):
+    """Reference: src/cuda/rasterizer.cpp:234-257.  Returns colors[N,3] (0 where masked)."""
+    dev = _device_of(points_world)
+    n = points_world.shape[0]
+    f32 = torch.float32
+    camera_pos = _prep(camera_pos, "camera_pos", f32, (3,), dev)
+    points_world = _prep(points_world, "points_world", f32, (n, 3), dev)
+    sh_coeffs_dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+    sh_coeffs_rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    colors = torch.empty((n, 3), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("evaluate_sh", dev)
+        _lib.check(
+            _lib.load().gs_evaluate_sh(
+                _ptr(camera_pos), _ptr(points_world), _ptr(sh_coeffs_dc), _ptr(sh_coeffs_rest),
+                _ptr(mask), n, 1 if sh_sigmoid else 0, _ptr(colors), _stream(dev),
+            ),
+            "evaluate_spherical_harmonics",
+        )
+        _lib.timer.stop(ev, dev)
+    return colors
+
+
+def evaluate_spherical_harmonics_backward(
+    grad_colors,
+    camera_pos,
+    points_world,
+    sh_coeffs_dc,
+    sh_coeffs_rest,
+    colors,
+    mask,
+    sh_sigmoid,
+):
+    """Reference: src/cuda/rasterizer.cpp:259-290.
+
+    Returns (grad_points_world[N,3], grad_sh_coeffs_dc[N,3], grad_sh_coeffs_rest[N,15,3]).
+    """
+    dev = _device_of(points_world)
+    n = points_world.shape[0]
+    f32 = torch.float32
+    grad_colors = _prep(grad_colors, "grad_colors", f32, (n, 3), dev)
+    camera_pos = _prep(camera_pos, "camera_pos", f32, (3,), dev)
+    points_world = _prep(points_world, "points_world", f32, (n, 3), dev)
+    sh_coeffs_dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+    sh_coeffs_rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    colors = _prep(colors, "colors", f32, (n, 3), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    g_means = torch.empty((n, 3), dtype=f32, device=dev)
+    g_dc = torch.empty((n, 3), dtype=f32, device=dev)
+    g_rest = torch.empty((n, 15, 3), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("evaluate_sh_backward", dev)
+        _lib.check(
+            _lib.load().gs_evaluate_sh_backward(
+                _ptr(grad_colors), _ptr(camera_pos), _ptr(points_world), _ptr(sh_coeffs_dc),
+                _ptr(sh_coeffs_rest), _ptr(colors), _ptr(mask), n, 1 if sh_sigmoid else 0,
+                _ptr(g_means), _ptr(g_dc), _ptr(g_rest), _stream(dev),
+            ),
+            "evaluate_spherical_harmonics_backward",
+        )
+        _lib.timer.stop(ev, dev)
+    return g_means, g_dc, g_rest
+
+
+def _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, debug):
+    dev = _device_of(points_image)
+    n = points_image.shape[0]
+    f32 = torch.float32
+    points_image = _prep(points_image, "points_image", f32, (n, 2), dev)
+    radii = _prep(radii, "radii", f32, (n, 2), dev)
+    depths = _prep(depths, "depths", f32, (n,), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    width, height, tile_size = int(width), int(height), int(tile_size)
+    if tile_size <= 0 or width <= 0 or height <= 0:
+        raise RuntimeError("compute_tile_intersection: width, height and tile_size must be > 0")
+    n_tiles = ((width + tile_size - 1) // tile_size) * ((height + tile_size - 1) // tile_size)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        stream = _stream(dev)
+        sz = ctypes.c_size_t(0)
+        _lib.check(lib.gs_bin_count_workspace_size(n, ctypes.byref(sz)), "workspace query")
+        ws_count = torch.empty((max(sz.value, 1),), dtype=torch.uint8, device=dev)
+        total = torch.empty((1,), dtype=torch.int64, device=dev)
+        ev = _lib.timer.record("bin_count", dev)
+        _lib.check(
+            lib.gs_bin_count(
+                _ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
+                tile_size, _ptr(ws_count), sz.value, _ptr(total), stream,
+            ),
+            "compute_tile_intersection (count)",
+        )
+        _lib.timer.stop(ev, dev)
+        k = int(total.item())  # the one host synchronisation (src/cuda/rasterizer.cpp:322)
+        sz2 = ctypes.c_size_t(0)
+        _lib.check(lib.gs_bin_sort_workspace_size(n, k, n_tiles, ctypes.byref(sz2)), "workspace query")
+        ws_sort = torch.empty((max(sz2.value, 1),), dtype=torch.uint8, device=dev)
+        indexing_offset = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
+        gaussian_ids_sorted = torch.empty((k,), dtype=torch.int32, device=dev)
+        sorted_keys = torch.empty((k,), dtype=torch.int64, device=dev) if debug else None
+        tiles_touched = torch.empty((n,), dtype=torch.int32, device=dev) if debug else None
+        ev = _lib.timer.record("bin_sort", dev)
+        _lib.check(
+            lib.gs_bin_sort(
+                _ptr(points_image), _ptr(radii), _ptr(depths), n, width, height, tile_size, k,
+                _ptr(ws_count), _ptr(ws_sort), sz2.value, _ptr(indexing_offset),
+                _ptr(gaussian_ids_sorted), _ptr(sorted_keys), _ptr(tiles_touched), stream,
+            ),
+            "compute_tile_intersection (sort)",
+        )
+        _lib.timer.stop(ev, dev)
+    if debug:
+        return indexing_offset, gaussian_ids_sorted, sorted_keys, tiles_touched
+    return indexing_offset, gaussian_ids_sorted
+
+
+def compute_tile_intersection(points_image, radii, depths, mask, width, height, tile_size=16):
+    """Reference: src/cuda/rasterizer.cpp:292-359.
+
+    Returns (indexing_offset[T] int32, gaussian_ids_sorted[K] int32) with
+    T = ceil(W/ts)*ceil(H/ts): entries ordered by (tile, depth bits, Gaussian
+    index); indexing_offset[t] = number of entries whose tile is < t.
+    """
+    return _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, False)
+
+
+def compute_tile_intersection_debug(points_image, radii, depths, mask, width, height, tile_size=16):
+    """compute_tile_intersection plus the sorted 64-bit keys (tile << 32 | depth bits,
+    as int64) and tiles_touched per Gaussian (int32), for parity checks."""
+    return _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, True)
+
+
+def _blend_inputs(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities,
+                  colors):
+    dev = _device_of(points_image)
+    n = points_image.shape[0]
+    f32 = torch.float32
+    indexing_offset = _prep(indexing_offset, "indexing_offset", torch.int32,
+                            (indexing_offset.shape[0],), dev)
+    gaussian_ids_sorted = _prep(gaussian_ids_sorted, "gaussian_ids_sorted", torch.int32,
+                                (gaussian_ids_sorted.shape[0],), dev)
+    points_image = _prep(points_image, "points_image", f32, (n, 2), dev)
+    cov_inv_image = _prep(cov_inv_image, "cov_inv_image", f32, (n, 3), dev)
+    opacities = _prep(opacities, "opacities", f32, (n,), dev)
+    colors = _prep(colors, "colors", f32, (n, 3), dev)
+    return dev, n, indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors
+
+
+def rasterize(
+    indexing_offset,
+    gaussian_ids_sorted,
+    points_image,
+    cov_inv_image,
+    opacities,
+    colors,
+    width,
+    height,
+    tile_size,
+    alpha_threshold,
+    transmittance_threshold,
+    chi_squared_threshold,
+):
+    """Reference: src/cuda/rasterizer.cpp:361-395.  Returns image[H,W,3] (un-clamped)."""
+    dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
+        indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
+    width, height = int(width), int(height)
+    image = torch.empty((height, width, 3), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("rasterize", dev)
+        _lib.check(
+            _lib.load().gs_rasterize(
+                _ptr(off), _ptr(ids), off.shape[0], ids.shape[0], _ptr(pts), _ptr(conic),
+                _ptr(opac), _ptr(col), n, width, height, int(tile_size), float(alpha_threshold),
+                float(transmittance_threshold), float(chi_squared_threshold), _ptr(image),
+                _stream(dev),
+            ),
+            "rasterize",
+        )
+        _lib.timer.stop(ev, dev)
+    return image
+
+
+def rasterize_backward(
+    grad_rendered_image,
+    indexing_offset,
+    gaussian_ids_sorted,
+    points_image,
+    cov_inv_image,
+    opacities,
+    colors,
+    width,
+    height,
+    tile_size,
+    alpha_threshold,
+    transmittance_threshold,
+    chi_squared_threshold,
+    rendered_image=None,
+):
+    """Reference: src/cuda/rasterizer.cpp:397-440.
+
+    Returns (grad_points_image[N,2], grad_cov_inv_image[N,3], grad_opacities[N],
+    grad_colors[N,3]).  `rendered_image`, if given, must be rasterize()'s
+    output for the same inputs.
+    """
+    dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
+        indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
+    width, height = int(width), int(height)
+    f32 = torch.float32
+    grad = _prep(grad_rendered_image, "grad_rendered_image", f32, (height, width, 3), dev)
+    img = None
+    if rendered_image is not None:
+        img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
+    g_pts = torch.empty((n, 2), dtype=f32, device=dev)
+    g_conic = torch.empty((n, 3), dtype=f32, device=dev)
+    g_opac = torch.empty((n,), dtype=f32, device=dev)
+    g_col = torch.empty((n, 3), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("rasterize_backward", dev)
+        _lib.check(
+            _lib.load().gs_rasterize_backward(
+                _ptr(grad), _ptr(img), _ptr(off), _ptr(ids), off.shape[0], ids.shape[0],
+                _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, int(tile_size),
+                float(alpha_threshold), float(transmittance_threshold),
+                float(chi_squared_threshold), _ptr(g_pts), _ptr(g_conic), _ptr(g_opac),
+                _ptr(g_col), _stream(dev),
+            ),
+            "rasterize_backward",
+        )
+        _lib.timer.stop(ev, dev)
+    return g_pts, g_conic, g_opac, g_col

@@ -1,0 +1,108 @@
+"""ctypes binding of libgsraster.so (C ABI declared in include/gs_rasterizer.h)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgsraster.so")
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+_PSZ = ctypes.POINTER(ctypes.c_size_t)
+
+# name -> argtypes (all functions return int status)
+SIGNATURES = {
+    "gs_abi_version": [],
+    "gs_project_points": [_P] * 6 + [_I64, _F, _F, _F, _F, _F, _I32, _I32] + [_P] * 6 + [_P],
+    "gs_project_points_backward": [_P] * 8 + [_I64, _I32, _I32] + [_P] * 5 + [_P],
+    "gs_evaluate_sh": [_P] * 5 + [_I64, _I32, _P, _P],
+    "gs_evaluate_sh_backward": [_P] * 7 + [_I64, _I32] + [_P] * 3 + [_P],
+    "gs_bin_count_workspace_size": [_I64, _PSZ],
+    "gs_bin_count": [_P] * 4 + [_I64, _I32, _I32, _I32, _P, _SZ, _P, _P],
+    "gs_bin_sort_workspace_size": [_I64, _I64, _I32, _PSZ],
+    "gs_bin_sort": [_P] * 3 + [_I64, _I32, _I32, _I32, _I64, _P, _P, _SZ] + [_P] * 4 + [_P],
+    "gs_rasterize": [_P, _P, _I32, _I64] + [_P] * 4 + [_I64, _I32, _I32, _I32, _F, _F, _F, _P, _P],
+    "gs_rasterize_backward": [_P] * 4 + [_I32, _I64] + [_P] * 4
+    + [_I64, _I32, _I32, _I32, _F, _F, _F]
+    + [_P] * 4
+    + [_P],
+}
+
+_lib = None
+
+
+class RasterizerError(RuntimeError):
+    """A gs_* entry point returned a non-zero status."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"cuda_rasterizer: HIP library not found at {LIB_PATH}; build it with "
+            "`python 3dgs_from_scratch_amd/build_lib.py` (or __graft_entry__.build())"
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    lib.gs_status_string.argtypes = [ctypes.c_int]
+    lib.gs_status_string.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+class StageTimer:
+    """Opt-in HIP-event timing of entry points on the stream they launch on.
+
+    While enabled, each instrumented call records a (start, end) event pair on
+    the device's current stream around the library call; `summary()` returns
+    {stage: (calls, total_ms)} after synchronising.
+    """
+
+    def __init__(self):
+        self.enabled = False
+        self.events: dict = {}
+
+    def reset(self):
+        self.events = {}
+
+    def record(self, stage: str, device):
+        import torch
+
+        if not self.enabled:
+            return None
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record(torch.cuda.current_stream(device))
+        self.events.setdefault(stage, []).append(ev)
+        return ev
+
+    def stop(self, ev, device):
+        import torch
+
+        if ev is not None:
+            ev[1].record(torch.cuda.current_stream(device))
+
+    def summary(self) -> dict:
+        import torch
+
+        torch.cuda.synchronize()
+        return {k: (len(v), sum(a.elapsed_time(b) for a, b in v)) for k, v in self.events.items()}
+
+
+timer = StageTimer()
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().gs_status_string(status).decode()
+        raise RasterizerError(f"{what} failed: {msg} (status {status})")

@@ -1,0 +1,138 @@
+"""Autograd glue and `render()`, the counterpart of src/cuda/wrapper.py.
+
+Same three autograd Functions (ProjectPointsFunction, SphericalHarmonicsFunction,
+RasterizeFunction) and the same `render` signature and return values
+(src/cuda/wrapper.py:12-294): render(...) -> (image[H,W,3] in [0,255],
+points_img[N,2], radii[N,2]).  `points_img` is a non-leaf tensor whose
+`.grad` (after `retain_grad()`) is dL/d(points_img), as the reference's
+densification strategy expects (src/strategy.py:47-68).
+
+Difference from the reference glue: RasterizeFunction saves its forward image
+and hands it to the backward kernel, so the backward does not recompute each
+pixel's colour (src/cuda/kernel.cu:1032-1060 replays the whole forward pass).
+"""
+
+from __future__ import annotations
+
+import torch
+
+import cuda_rasterizer as _cr
+
+
+class ProjectPointsFunction(torch.autograd.Function):
+    """src/cuda/wrapper.py:12-85."""
+
+    @staticmethod
+    def forward(ctx, means, scales, quaternions, opacities, world_to_camera, intrinsic,
+                near_plane, far_plane, min_opacity, min_radius, max_radius, width, height):
+        points_img, depths, cov_img, cov_inv_img, radii, mask = _cr.project_points(
+            means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
+            far_plane, min_opacity, min_radius, max_radius, width, height)
+        ctx.save_for_backward(means, scales, quaternions, opacities, world_to_camera, intrinsic,
+                              cov_img, mask)
+        ctx.width = width
+        ctx.height = height
+        return points_img, depths, cov_inv_img, radii, mask
+
+    @staticmethod
+    def backward(ctx, grad_points_img, grad_depths, grad_cov_inv_img, grad_radii, grad_mask):
+        means, scales, quaternions, opacities, world_to_camera, intrinsic, cov_img, mask = (
+            ctx.saved_tensors)
+        if grad_points_img is None:
+            grad_points_img = torch.zeros((means.shape[0], 2), dtype=means.dtype,
+                                          device=means.device)
+        if grad_cov_inv_img is None:
+            grad_cov_inv_img = torch.zeros((means.shape[0], 3), dtype=means.dtype,
+                                           device=means.device)
+        g_means, g_scales, g_quats = _cr.project_points_backward(
+            grad_points_img, grad_cov_inv_img, means, scales, quaternions, opacities,
+            world_to_camera, intrinsic, ctx.width, ctx.height, cov_img, mask)
+        return (g_means, g_scales, g_quats) + (None,) * 10
+
+
+class SphericalHarmonicsFunction(torch.autograd.Function):
+    """src/cuda/wrapper.py:88-118."""
+
+    @staticmethod
+    def forward(ctx, camera_pos, means, sh_coeffs_dc, sh_coeffs_rest, mask, sh_sigmoid=False):
+        colors = _cr.evaluate_spherical_harmonics(camera_pos, means, sh_coeffs_dc,
+                                                  sh_coeffs_rest, mask, sh_sigmoid)
+        ctx.save_for_backward(camera_pos, means, sh_coeffs_dc, sh_coeffs_rest, colors, mask)
+        ctx.sh_sigmoid = sh_sigmoid
+        return colors
+
+    @staticmethod
+    def backward(ctx, grad_colors):
+        camera_pos, means, sh_coeffs_dc, sh_coeffs_rest, colors, mask = ctx.saved_tensors
+        g_means, g_dc, g_rest = _cr.evaluate_spherical_harmonics_backward(
+            grad_colors, camera_pos, means, sh_coeffs_dc, sh_coeffs_rest, colors, mask,
+            ctx.sh_sigmoid)
+        return None, g_means, g_dc, g_rest, None, None
+
+
+class RasterizeFunction(torch.autograd.Function):
+    """src/cuda/wrapper.py:121-220."""
+
+    @staticmethod
+    def forward(ctx, indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities,
+                colors, width, height, tile_size, alpha_threshold, transmittance_threshold,
+                chi_squared_threshold):
+        image = _cr.rasterize(indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img,
+                              opacities, colors, width, height, tile_size, alpha_threshold,
+                              transmittance_threshold, chi_squared_threshold)
+        ctx.save_for_backward(indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img,
+                              opacities, colors, image)
+        ctx.params = (width, height, tile_size, alpha_threshold, transmittance_threshold,
+                      chi_squared_threshold)
+        return image
+
+    @staticmethod
+    def backward(ctx, grad_image):
+        offsets, ids, points_img, cov_inv_img, opacities, colors, image = ctx.saved_tensors
+        g_pts, g_conic, g_opac, g_col = _cr.rasterize_backward(
+            grad_image, offsets, ids, points_img, cov_inv_img, opacities, colors, *ctx.params,
+            rendered_image=image)
+        return None, None, g_pts, g_conic, g_opac, g_col, None, None, None, None, None, None
+
+
+def render(
+    world_to_camera,
+    intrinsic,
+    width,
+    height,
+    means,
+    scales,
+    quaternions,
+    opacities,
+    sh_coeffs_dc,
+    sh_coeffs_rest,
+    near_plane=0.01,
+    far_plane=100.0,
+    min_opacity=1 / 255,
+    min_radius=0.5,
+    max_radius=128.0,
+    alpha_threshold=1e-4,
+    transmittance_threshold=1e-4,
+    chi_squared_threshold=9.21,  # 99% confidence interval for 2 DOF
+    sh_sigmoid=False,
+):
+    """src/cuda/wrapper.py:223-294.  Returns (image*255 clamped, points_img, radii)."""
+    points_img, depths, cov_inv_img, radii, mask = ProjectPointsFunction.apply(
+        means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
+        far_plane, min_opacity, min_radius, max_radius, width, height)
+
+    camera_pos = -world_to_camera[:3, :3].t() @ world_to_camera[:3, 3]
+    colors = SphericalHarmonicsFunction.apply(camera_pos, means, sh_coeffs_dc, sh_coeffs_rest,
+                                              mask, sh_sigmoid)
+    if not sh_sigmoid:
+        colors = torch.clamp_min(colors + 0.5, 0.0)
+
+    tile_size = 16
+    indexing_offset, gaussian_ids_sorted = _cr.compute_tile_intersection(
+        points_img.detach(), radii, depths, mask, width, height, tile_size)
+
+    image = RasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img,
+                                    cov_inv_img, opacities, colors, width, height, tile_size,
+                                    alpha_threshold, transmittance_threshold,
+                                    chi_squared_threshold)
+    return image.clamp(0, 1) * 255, points_img, radii

@@ -1,0 +1,346 @@
+"""Benchmark of the MI355X Gaussian-splatting rasterizer (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+
+One step = render() forward + L1 loss + backward through all six parameter
+groups (no optimizer step: BASELINE.md times "fwd+bwd"), on the headline
+configuration 3 (1M Gaussians, SH degree 3, 1920x1080, fp32) with synthetic
+inputs already resident in HBM.  Prints ONE JSON line.
+
+Scene generators for BASELINE configurations 1-5 live here too (tests import
+them).  Every tensor is drawn on the CPU with torch.Generator().manual_seed(seed)
+in a fixed order -- means, log-scales, quaternions, opacity logits, SH dc, SH
+rest, cameras, target -- then copied to the device.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "3dgs_from_scratch_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+
+METRIC = "fwd+bwd ms/iter at 1M Gaussians 1080p SH3; achieved HBM GB/s vs peak"
+
+
+# ------------------------------------------------------------------ scenes
+
+def _intrinsic(f, width, height):
+    return torch.tensor([[f, 0.0, width / 2], [0.0, f, height / 2], [0.0, 0.0, 1.0]])
+
+
+def look_at(azimuth: float, elevation: float, dist: float) -> torch.Tensor:
+    """OpenCV world->camera matrix for a camera on a sphere looking at the origin."""
+    c = torch.tensor([dist * math.cos(elevation) * math.cos(azimuth), dist * math.sin(elevation),
+                      dist * math.cos(elevation) * math.sin(azimuth)], dtype=torch.float64)
+    f = -c / c.norm()
+    up = torch.tensor([0.0, -1.0, 0.0], dtype=torch.float64)
+    right = torch.linalg.cross(f, up)
+    right = right / right.norm()
+    down = torch.linalg.cross(f, right)
+    R = torch.stack([right, down, f])
+    M = torch.eye(4, dtype=torch.float64)
+    M[:3, :3] = R
+    M[:3, 3] = -R @ c
+    return M.float()
+
+
+def _sh(g, n, degree):
+    dc = torch.randn(n, 3, generator=g) * 0.3
+    rest = torch.randn(n, 15, 3, generator=g) * 0.05 if degree else torch.zeros(n, 15, 3)
+    return dc, rest
+
+
+def config1(seed: int = 0) -> dict:
+    """10k Gaussians, SH0, 256x256, fx=fy=300, means U([-1,1]^2 x [2,6]) in camera space."""
+    g = torch.Generator().manual_seed(seed)
+    n, W, H = 10_000, 256, 256
+    means = torch.empty(n, 3)
+    means[:, :2] = torch.rand(n, 2, generator=g) * 2 - 1
+    means[:, 2] = torch.rand(n, generator=g) * 4 + 2
+    log_scales = torch.randn(n, 3, generator=g) * 0.5 - 4.0
+    quats = torch.randn(n, 4, generator=g)
+    logits = torch.randn(n, generator=g)
+    dc, rest = _sh(g, n, 0)
+    cam = dict(w2c=torch.eye(4), K=_intrinsic(300.0, W, H), width=W, height=H, near=0.01)
+    target = torch.rand(H, W, 3, generator=g)
+    return dict(params=dict(means=means, log_scales=log_scales, quats_raw=quats,
+                            opacity_logits=logits, sh_dc=dc, sh_rest=rest),
+                camera=cam, target=target, name="config1")
+
+
+def config2(seed: int = 0, n: int = 100_000, cameras: int = 8) -> dict:
+    """100k Gaussians in a ball of radius 1.5, SH3, 800x800, fx=fy=1100, 8 orbit cameras
+    at distance 4 (azimuth U[0,2pi), elevation U[-pi/3,pi/3])."""
+    g = torch.Generator().manual_seed(seed)
+    W = H = 800
+    d = torch.randn(n, 3, generator=g)
+    d = d / d.norm(dim=1, keepdim=True)
+    means = d * 1.5 * torch.rand(n, 1, generator=g) ** (1 / 3)
+    log_scales = torch.randn(n, 3, generator=g) * 0.6 - 4.5
+    quats = torch.randn(n, 4, generator=g)
+    logits = torch.randn(n, generator=g) * 1.5
+    dc, rest = _sh(g, n, 3)
+    az = torch.rand(cameras, generator=g) * 2 * math.pi
+    el = (torch.rand(cameras, generator=g) * 2 - 1) * math.pi / 3
+    cams = [dict(w2c=look_at(float(a), float(e), 4.0), K=_intrinsic(1100.0, W, H), width=W,
+                 height=H, near=0.01) for a, e in zip(az, el)]
+    targets = [torch.rand(H, W, 3, generator=g) for _ in range(cameras)]
+    return dict(params=dict(means=means, log_scales=log_scales, quats_raw=quats,
+                            opacity_logits=logits, sh_dc=dc, sh_rest=rest),
+                cameras=cams, targets=targets, camera=cams[0], target=targets[0], name="config2")
+
+
+def config3(n: int = 1_000_000, seed: int = 0, big_fraction: float = 0.0) -> dict:
+    """Headline: 1M Gaussians, SH3, 1920x1080, fx=fy=1400, camera at the origin looking +z,
+    near 0.2.  70% clustered (sigma 0.3) around 50 centres inside the frustum
+    (z~U[2,10], x~U[-0.6,0.6]z, y~U[-0.35,0.35]z), 30% uniform in [-10,10]^3.
+    log-scale ~ N(-3.5, 0.8) (a `big_fraction` of them ~ N(-1, 0.3): config 4),
+    opacity logit ~ N(0, 1.5)."""
+    g = torch.Generator().manual_seed(seed)
+    W, H = 1920, 1080
+    n_cl = int(round(0.7 * n))
+    cz = torch.rand(50, generator=g) * 8 + 2
+    cx = (torch.rand(50, generator=g) * 1.2 - 0.6) * cz
+    cy = (torch.rand(50, generator=g) * 0.7 - 0.35) * cz
+    centres = torch.stack([cx, cy, cz], dim=1)
+    which = torch.randint(0, 50, (n_cl,), generator=g)
+    clustered = centres[which] + torch.randn(n_cl, 3, generator=g) * 0.3
+    uniform = torch.rand(n - n_cl, 3, generator=g) * 20 - 10
+    means = torch.cat([clustered, uniform], dim=0)
+    log_scales = torch.randn(n, 3, generator=g) * 0.8 - 3.5
+    if big_fraction > 0:
+        big = torch.rand(n, generator=g) < big_fraction
+        log_scales[big] = torch.randn(int(big.sum()), 3, generator=g) * 0.3 - 1.0
+    quats = torch.randn(n, 4, generator=g)
+    logits = torch.randn(n, generator=g) * 1.5
+    dc, rest = _sh(g, n, 3)
+    cam = dict(w2c=torch.eye(4), K=_intrinsic(1400.0, W, H), width=W, height=H, near=0.2)
+    target = torch.rand(H, W, 3, generator=g)
+    return dict(params=dict(means=means, log_scales=log_scales, quats_raw=quats,
+                            opacity_logits=logits, sh_dc=dc, sh_rest=rest),
+                camera=cam, target=target, name="config3" if big_fraction == 0 else "config4")
+
+
+def config4(seed: int = 0) -> dict:
+    """3M Gaussians, configuration-3 distributions with 5% log-scales ~ N(-1, 0.3)."""
+    return config3(n=3_000_000, seed=seed, big_fraction=0.05)
+
+
+CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4}
+
+
+# --------------------------------------------------------------- GPU leg
+
+def activated(p: dict):
+    """scripts/train.py:135-143."""
+    scales = torch.exp(p["log_scales"])
+    q = p["quats_raw"]
+    quats = q / torch.norm(q, dim=1, keepdim=True).clamp_min(1e-12)
+    opac = torch.sigmoid(p["opacity_logits"])
+    return scales, quats, opac
+
+
+def gpu_step(render, leaves: dict, cam: dict, target: torch.Tensor):
+    """render + L1 loss + backward; returns (loss, image, points_img)."""
+    for t in leaves.values():
+        t.grad = None
+    scales, quats, opac = activated(leaves)
+    image, points_img, radii = render(cam["w2c"], cam["K"], cam["width"], cam["height"],
+                                      leaves["means"], scales, quats, opac, leaves["sh_dc"],
+                                      leaves["sh_rest"], near_plane=cam["near"])
+    loss = torch.nn.functional.l1_loss(image / 255.0, target)
+    loss.backward()
+    return loss, image
+
+
+def run_gpu(scene: dict, steps: int, warmup: int) -> dict:
+    from cuda_rasterizer import _lib
+    from cuda_rasterizer.wrapper import render
+
+    dev = torch.device("cuda:0")
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in scene["params"].items()}
+    cam = dict(scene["camera"])
+    cam["w2c"] = cam["w2c"].to(dev)
+    cam["K"] = cam["K"].to(dev)
+    target = scene["target"].to(dev)
+    for _ in range(warmup):
+        gpu_step(render, leaves, cam, target)
+    torch.cuda.synchronize()
+
+    # timed region: wall clock with a synchronize on both sides, plus HIP events
+    # around every library entry point on the stream it runs on
+    _lib.timer.reset()
+    _lib.timer.enabled = True
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss, image = gpu_step(render, leaves, cam, target)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.timer.enabled = False
+    stages = _lib.timer.summary()
+    ms = (t1 - t0) * 1e3 / steps
+
+    # workload statistics of one step
+    from cuda_rasterizer import compute_tile_intersection, project_points
+    with torch.no_grad():
+        scales, quats, opac = activated(leaves)
+        pts, depths, _, _, radii, mask = project_points(
+            leaves["means"], scales, quats, opac, cam["w2c"], cam["K"], cam["near"], 100.0,
+            1 / 255, 0.5, 128.0, cam["width"], cam["height"])
+        off, ids = compute_tile_intersection(pts, radii, depths, mask, cam["width"], cam["height"], 16)
+    return dict(ms=ms, stages={k: (c, t / steps) for k, (c, t) in stages.items()},
+                n=scene["params"]["means"].shape[0], n_visible=int(mask.sum()), keys=int(ids.numel()),
+                loss=float(loss), width=cam["width"], height=cam["height"])
+
+
+# ----------------------------------------------------------- roofline
+
+def algorithmic_bytes(stage: str, n: int, n_vis: int, k: int, hw: int) -> float:
+    """Bytes one call of each entry point must move at minimum: every API tensor
+    read once and written once (the per-Gaussian layouts of the API)."""
+    if stage == "project_points":
+        return n * (12 + 12 + 16 + 4) + n * (8 + 4 + 12 + 12 + 8 + 1)
+    if stage == "evaluate_sh":
+        return n * (12 + 12 + 180 + 1) + n * 12
+    if stage == "evaluate_sh_backward":
+        return n * (12 + 12 + 180 + 12 + 1) + n * (12 + 12 + 180)
+    if stage == "project_points_backward":
+        return n * (8 + 12 + 12 + 12 + 16 + 12 + 1) + n * (12 + 12 + 16)
+    if stage == "bin_count":  # points, radii, depths, mask in; 4 sort passes over N (key+id)
+        return n * 21 + 4 * n * 16 + n * 16
+    if stage == "bin_sort":  # emit 8 B/key, two tile passes over (key, id), ranges
+        return k * 8 + 2 * k * 16 + k * 4
+    return 0.0
+
+
+def roofline(res: dict) -> dict:
+    n, nv, k, hw = res["n"], res["n_visible"], res["keys"], res["width"] * res["height"]
+    per_stage = {}
+    for stage, (calls, ms) in res["stages"].items():
+        b = algorithmic_bytes(stage, n, nv, k, hw)
+        per_stage[stage] = dict(ms=round(ms, 4), calls_per_step=calls // max(res.get("steps", 1), 1))
+        if b and ms > 0:
+            per_stage[stage]["gbs"] = round(b / (ms * 1e-3) / 1e9, 1)
+    dominant = max(res["stages"].items(), key=lambda kv: kv[1][1])[0]
+    return dict(dominant=dominant, per_stage=per_stage)
+
+
+# -------------------------------------------------------------- CPU leg
+
+def cpu_baseline(scene: dict, sample_tiles: int = 48, seed: int = 0) -> dict:
+    """The oracle (a restatement of src/torch_rasterizer.py) timed on the host CPU.
+
+    Full fwd+bwd at the headline size does not fit in host RAM (autograd keeps
+    ~15 KB per (tile, Gaussian) key), so the sample is: the whole vectorised
+    preprocess + binning for all N Gaussians, plus fwd+bwd of `sample_tiles`
+    randomly chosen non-empty tiles; per-tile time is scaled to all non-empty
+    tiles.  Reports ms per full iteration.
+    """
+    import numpy as np
+
+    from oracle import render as orender
+
+    torch.set_num_threads(max(1, os.cpu_count() or 1))
+    leaves = {k: v.clone().requires_grad_(True) for k, v in scene["params"].items()}
+    cam = scene["camera"]
+    W, H = cam["width"], cam["height"]
+    t0 = time.perf_counter()
+    scales, quats, opac = activated(leaves)
+    out = orender.render_stages(cam["w2c"], cam["K"], W, H, leaves["means"], scales, quats, opac,
+                                leaves["sh_dc"], leaves["sh_rest"], near_plane=cam["near"], tiles=[])
+    t_pre = time.perf_counter() - t0
+    off = out["indexing_offset"].numpy()
+    k = int(out["gaussian_ids_sorted"].numel())
+    ends = np.append(off[1:], k)
+    nonempty = np.nonzero(ends > off)[0]
+    rng = np.random.default_rng(seed)
+    tiles = sorted(rng.choice(nonempty, size=min(sample_tiles, len(nonempty)), replace=False).tolist())
+    # time fwd+bwd of the sampled tiles (preprocess graph reused, its backward included once)
+    from oracle import blend
+
+    t1 = time.perf_counter()
+    raw = blend.rasterize(out["indexing_offset"], out["gaussian_ids_sorted"], out["points_image"],
+                          out["conic"], torch.where(out["proj"]["keep"], opac, torch.zeros_like(opac)),
+                          out["colors"], W, H, 16, 1e-4, 1e-4, 9.21, tiles=tiles)
+    loss = torch.nn.functional.l1_loss(raw.clamp(0, 1), scene["target"])
+    loss.backward()
+    t_tiles = time.perf_counter() - t1
+    total_s = t_pre + t_tiles * len(nonempty) / max(len(tiles), 1)
+    return dict(value=round(total_s * 1e3, 1), unit="ms/iter", cores=torch.get_num_threads(),
+                kind="port",
+                sample=(f"oracle (restated src/torch_rasterizer.py) on the same {scene['name']} inputs: "
+                        f"full preprocess+binning of {scene['params']['means'].shape[0]} Gaussians "
+                        f"({t_pre:.1f} s) + fwd+bwd of {len(tiles)} random non-empty tiles "
+                        f"({t_tiles:.1f} s) scaled to all {len(nonempty)} non-empty tiles; "
+                        f"cpu={platform.processor() or platform.machine()}"))
+
+
+# ------------------------------------------------------------------- main
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3, choices=[1, 3, 4])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-tiles", type=int, default=48)
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU design is described in DESIGN.md but not built)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 2
+
+    scene = CONFIGS[args.config]()
+    res = run_gpu(scene, args.steps, args.warmup)
+    res["steps"] = args.steps
+    rl = roofline(res)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(scene, args.cpu_sample_tiles)
+    line = {
+        "metric": METRIC,
+        "value": round(res["ms"], 3),
+        "unit": "ms/iter",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms"], 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{scene['name']}: {res['n']} Gaussians SH3 "
+                               f"{res['width']}x{res['height']} fwd+bwd L1",
+                   "gaussians": res["n"], "visible": res["n_visible"], "keys": res["keys"],
+                   "resolution": [res["width"], res["height"]]},
+        "gaussians_per_s": round(res["n"] / (res["ms"] * 1e-3), 1),
+        "stages": rl["per_stage"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,173 @@
+/*
+ * gs_rasterizer.h — C ABI of the MI355X (gfx950) Gaussian-splatting rasterizer.
+ *
+ * Every entry point takes raw device pointers, element counts and the caller's
+ * HIP stream, enqueues its kernels on that stream and returns an int status:
+ *   0            success
+ *   > 0          a hipError_t reported by the HIP runtime (launch or API failure)
+ *   < 0          one of the GS_ERR_* argument errors below (nothing was launched)
+ * No entry point allocates device memory; scratch space is passed in by the
+ * caller (query its size with the *_workspace_size functions).  No entry point
+ * synchronises the stream.  Outputs are written in full (culled / masked
+ * entries are written as zero), so callers need not pre-clear them, except
+ * where an entry point documents accumulation.
+ *
+ * Layouts follow the reference extension module `cuda_rasterizer`
+ * (src/cuda/rasterizer.cpp:442-464): fp32 row-major AoS tensors, quaternions
+ * in (x, y, z, w) order, world_to_camera a row-major 4x4 world->camera matrix
+ * (OpenCV axes, u = fx*x/z + cx), intrinsic a row-major 3x3 matrix, masks one
+ * byte per Gaussian (0/1), ids and tile offsets int32.
+ */
+#ifndef GS_RASTERIZER_H
+#define GS_RASTERIZER_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    GS_OK = 0,
+    GS_ERR_INVALID_ARGUMENT = -1,   /* negative size, null required pointer, bad tile size */
+    GS_ERR_WORKSPACE_TOO_SMALL = -2,/* workspace_bytes below the *_workspace_size result */
+    GS_ERR_TOO_MANY_KEYS = -3,      /* more than INT32_MAX (tile, Gaussian) keys */
+    GS_ERR_UNSUPPORTED = -4,        /* argument combination this build does not implement */
+};
+
+/* Human-readable text for a status returned by any gs_* function. */
+const char *gs_status_string(int status);
+
+/* Version of this ABI (incremented on any signature change). */
+int gs_abi_version(void);
+
+/* ---------------------------------------------------------------- preprocess */
+
+/*
+ * Projection of N Gaussians into the image plane.
+ * Replaces cuda_rasterizer.project_points (src/cuda/rasterizer.cpp:140-191,
+ * kernel src/cuda/kernel.cu:411-500); culling follows the Torch rasterizer
+ * (src/torch_rasterizer.py:47-144): keep iff opacity >= min_opacity,
+ * near < z < far, the 2D covariance is finite, min_radius <= r <= max_radius
+ * and -r_u < u < W + r_u, -r_v < v < H + r_v.
+ * Outputs (N rows each): points_image (u,v), depths (z), cov_image (a,b,c),
+ * cov_inv_image (conic A,B,C), radii (r_u,r_v), mask (1 = kept).
+ */
+int gs_project_points(const float *means, const float *scales, const float *quaternions,
+                      const float *opacities, const float *world_to_camera,
+                      const float *intrinsic, int64_t n, float near_plane, float far_plane,
+                      float min_opacity, float min_radius, float max_radius, int32_t width,
+                      int32_t height, float *points_image, float *depths, float *cov_image,
+                      float *cov_inv_image, float *radii, uint8_t *mask, hipStream_t stream);
+
+/*
+ * Gradient of project_points w.r.t. means, scales and quaternions.
+ * Replaces cuda_rasterizer.project_points_backward
+ * (src/cuda/rasterizer.cpp:193-232, kernel src/cuda/kernel.cu:502-543); the
+ * Jacobian term is the exact derivative of the forward (the reference's
+ * kernel.cu:381-394 doubles the off-diagonal term; this one does not).
+ */
+int gs_project_points_backward(const float *grad_points_image, const float *grad_cov_inv_image,
+                               const float *means, const float *scales,
+                               const float *quaternions, const float *opacities,
+                               const float *world_to_camera, const float *intrinsic, int64_t n,
+                               int32_t width, int32_t height, const float *cov_image,
+                               const uint8_t *mask, float *grad_means, float *grad_scales,
+                               float *grad_quaternions, hipStream_t stream);
+
+/*
+ * Degree-3 real spherical harmonics -> RGB along the view direction
+ * normalize(mean - camera_pos).  Replaces
+ * cuda_rasterizer.evaluate_spherical_harmonics (src/cuda/rasterizer.cpp:234-257,
+ * kernel src/cuda/kernel.cu:545-617).  sh_rest is (N,15,3).  Masked rows are 0.
+ * sh_sigmoid != 0 applies a sigmoid to the result.
+ */
+int gs_evaluate_sh(const float *camera_pos, const float *means, const float *sh_dc,
+                   const float *sh_rest, const uint8_t *mask, int64_t n, int32_t sh_sigmoid,
+                   float *colors, hipStream_t stream);
+
+/*
+ * Gradient of gs_evaluate_sh.  Replaces
+ * cuda_rasterizer.evaluate_spherical_harmonics_backward
+ * (src/cuda/rasterizer.cpp:259-290, kernel src/cuda/kernel.cu:619-782).
+ */
+int gs_evaluate_sh_backward(const float *grad_colors, const float *camera_pos,
+                            const float *means, const float *sh_dc, const float *sh_rest,
+                            const float *colors, const uint8_t *mask, int64_t n,
+                            int32_t sh_sigmoid, float *grad_means, float *grad_sh_dc,
+                            float *grad_sh_rest, hipStream_t stream);
+
+/* ------------------------------------------------------------------- binning */
+
+/*
+ * compute_tile_intersection (src/cuda/rasterizer.cpp:292-359) in two phases
+ * around the one host read of the key count K:
+ *
+ *   gs_bin_count: tiles_touched per Gaussian (kernel.cu:784-818 semantics),
+ *     a stable sort of the visible Gaussians by depth bits, and an exclusive
+ *     scan of tiles_touched in that order.  Writes K to *total_keys (a device
+ *     int64).  Keeps its state in `workspace`, which gs_bin_sort reads.
+ *   gs_bin_sort: emits one (tile, Gaussian) entry per touched tile in depth
+ *     order, stably sorts them by tile id and extracts the per-tile ranges.
+ *     The result equals a stable sort of the reference's 64-bit keys
+ *     (tile_id << 32 | depth_bits) emitted in Gaussian order (kernel.cu:820-914):
+ *     entries ordered by (tile, depth bits, Gaussian index).
+ *     indexing_offset[t] = number of entries with tile < t (n_tiles entries).
+ *     Optional outputs (may be NULL): sorted_keys (K uint64, the 64-bit keys
+ *     in sorted order) and tiles_touched (N int32).
+ */
+int gs_bin_count_workspace_size(int64_t n, size_t *bytes);
+int gs_bin_count(const float *points_image, const float *radii, const float *depths,
+                 const uint8_t *mask, int64_t n, int32_t width, int32_t height,
+                 int32_t tile_size, void *workspace, size_t workspace_bytes,
+                 int64_t *total_keys, hipStream_t stream);
+int gs_bin_sort_workspace_size(int64_t n, int64_t k, int32_t n_tiles, size_t *bytes);
+int gs_bin_sort(const float *points_image, const float *radii, const float *depths, int64_t n,
+                int32_t width, int32_t height, int32_t tile_size, int64_t k,
+                const void *count_workspace, void *workspace, size_t workspace_bytes,
+                int32_t *indexing_offset, int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
+                int32_t *tiles_touched, hipStream_t stream);
+
+/* --------------------------------------------------------------------- blend */
+
+/*
+ * Front-to-back alpha compositing of each tile's sorted Gaussian list.
+ * Replaces cuda_rasterizer.rasterize (src/cuda/rasterizer.cpp:361-395, kernel
+ * src/cuda/kernel.cu:916-987) with the Torch rasterizer's inclusion rules
+ * (src/torch_rasterizer.py:262-282): a Gaussian contributes to pixel (x,y)
+ * (integer coordinates) iff E < chi_squared_threshold, alpha >= alpha_threshold
+ * and the transmittance before it is >= transmittance_threshold.
+ * image is (H,W,3), un-clamped, no background.  n_tiles = length of
+ * indexing_offset, k = length of gaussian_ids_sorted.
+ */
+int gs_rasterize(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                 int32_t n_tiles, int64_t k, const float *points_image,
+                 const float *cov_inv_image, const float *opacities, const float *colors,
+                 int64_t n, int32_t width, int32_t height, int32_t tile_size,
+                 float alpha_threshold, float transmittance_threshold,
+                 float chi_squared_threshold, float *image, hipStream_t stream);
+
+/*
+ * Gradient of gs_rasterize w.r.t. points_image, cov_inv_image, opacities and
+ * colors.  Replaces cuda_rasterizer.rasterize_backward
+ * (src/cuda/rasterizer.cpp:397-440, kernel src/cuda/kernel.cu:989-1111).
+ * `image` is the forward output for the same inputs, or NULL (the kernel then
+ * recomputes it).  The four gradient outputs are overwritten.
+ */
+int gs_rasterize_backward(const float *grad_image, const float *image,
+                          const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                          int32_t n_tiles, int64_t k, const float *points_image,
+                          const float *cov_inv_image, const float *opacities,
+                          const float *colors, int64_t n, int32_t width, int32_t height,
+                          int32_t tile_size, float alpha_threshold,
+                          float transmittance_threshold, float chi_squared_threshold,
+                          float *grad_points_image, float *grad_cov_inv_image,
+                          float *grad_opacities, float *grad_colors, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GS_RASTERIZER_H */

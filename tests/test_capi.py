@@ -1,0 +1,107 @@
+"""CPU tests of the C-ABI library and the Python host layer (no GPU calls)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import helpers  # noqa: F401  (sets sys.path via conftest)
+import cuda_rasterizer
+from cuda_rasterizer import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gs_rasterizer.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gs_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} missing: run __graft_entry__.build() first")
+    return _lib.load()
+
+
+def test_header_declares_the_seven_reference_stages():
+    names = declared_functions()
+    for required in ["gs_project_points", "gs_project_points_backward", "gs_evaluate_sh",
+                     "gs_evaluate_sh_backward", "gs_bin_count", "gs_bin_sort", "gs_rasterize",
+                     "gs_rasterize_backward"]:
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(raw, n)]
+    assert not missing, missing
+    assert set(_lib.SIGNATURES) | {"gs_status_string"} >= set(declared_functions())
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.gs_abi_version() == 1
+    assert lib.gs_status_string(0) == b"success"
+    for code in (-1, -2, -3, -4):
+        assert lib.gs_status_string(code) not in (b"", b"unknown status")
+    assert lib.gs_status_string(-99) == b"unknown status"
+
+
+def test_workspace_queries(lib):
+    sz = ctypes.c_size_t(0)
+    assert lib.gs_bin_count_workspace_size(0, ctypes.byref(sz)) == 0
+    small = sz.value
+    assert lib.gs_bin_count_workspace_size(1_000_000, ctypes.byref(sz)) == 0
+    assert sz.value >= 1_000_000 * 36 and sz.value > small
+    assert lib.gs_bin_sort_workspace_size(1000, 20_000_000, 8160, ctypes.byref(sz)) == 0
+    assert sz.value >= 20_000_000 * 12
+    assert lib.gs_bin_count_workspace_size(-1, ctypes.byref(sz)) == -1
+
+
+def test_invalid_arguments_rejected_on_host(lib):
+    null = None
+    # negative sizes / bad image sizes never reach the device
+    assert lib.gs_project_points(*([null] * 6), -1, 0.01, 100.0, 0.0, 0.5, 128.0, 64, 64,
+                                 *([null] * 6), null) == -1
+    assert lib.gs_project_points(*([null] * 6), 10, 0.01, 100.0, 0.0, 0.5, 128.0, 0, 64,
+                                 *([null] * 6), null) == -1
+    assert lib.gs_project_points(*([null] * 6), 10, 0.01, 100.0, 0.0, 0.5, 128.0, 64, 64,
+                                 *([null] * 6), null) == -1  # null buffers
+    assert lib.gs_evaluate_sh(*([null] * 5), -3, 0, null, null) == -1
+    assert lib.gs_rasterize(null, null, 4, 10, *([null] * 4), 10, 32, 32, 16, 1e-4, 1e-4, 9.21,
+                            null, null) == -1
+    assert lib.gs_rasterize(null, null, 4, 2**31, *([null] * 4), 10, 32, 32, 16, 1e-4, 1e-4,
+                            9.21, null, null) == -3
+    assert lib.gs_rasterize(null, null, 4, 10, *([null] * 4), 10, 64, 64, 64, 1e-4, 1e-4, 9.21,
+                            null, null) == -4  # 64x64 tile: more than 1024 threads
+    # more offset entries than the image has tiles
+    assert lib.gs_rasterize(null, null, 5, 0, *([null] * 4), 0, 32, 32, 16, 1e-4, 1e-4, 9.21,
+                            null, null) == -1
+    assert lib.gs_bin_sort(null, null, null, 10, 64, 64, 16, 2**31, null, null, 0, null, null,
+                           null, null, null) == -3
+    sz = ctypes.c_size_t(0)
+    assert lib.gs_bin_count(null, null, null, null, 10, 64, 64, 16, null, 0, null, null) == -1
+
+
+def test_python_layer_refuses_cpu_tensors():
+    """No CPU fallback: the product path raises on host tensors."""
+    n = 4
+    with pytest.raises(RuntimeError, match="GPU only"):
+        cuda_rasterizer.project_points(torch.zeros(n, 3), torch.ones(n, 3), torch.zeros(n, 4),
+                                       torch.ones(n), torch.eye(4), torch.eye(3), 0.01, 100.0,
+                                       1 / 255, 0.5, 128.0, 16, 16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        cuda_rasterizer.compute_tile_intersection(torch.zeros(n, 2), torch.ones(n, 2),
+                                                  torch.ones(n), torch.ones(n, dtype=torch.bool),
+                                                  16, 16, 16)
+
+
+def test_status_to_exception():
+    with pytest.raises(_lib.RasterizerError, match="invalid argument"):
+        _lib.check(-1, "probe")

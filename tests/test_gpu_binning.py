@@ -1,0 +1,121 @@
+"""GPU parity: compute_tile_intersection vs the numpy oracle, bit-exact.
+
+Checked: indexing_offset, gaussian_ids_sorted, the sorted 64-bit keys
+(tile << 32 | depth bits) and tiles_touched.  Cases: random splats with depth
+ties, image sizes that are not tile multiples, tile sizes 8/16/32, the
+reference's two constant fixtures (hand-derived layouts), empty inputs, a
+fully culled frame, and the headline configuration's full size (1M Gaussians
+at 1920x1080).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import helpers
+import cuda_rasterizer as cr
+from oracle import binning, preprocess
+
+pytestmark = pytest.mark.gpu
+
+
+def _random_splats(n, width, height, seed, rmax=40.0):
+    g = np.random.default_rng(seed)
+    pts = np.stack([g.uniform(-30, width + 30, n), g.uniform(-30, height + 30, n)], 1).astype(np.float32)
+    radii = g.uniform(0.5, rmax, (n, 2)).astype(np.float32)
+    depths = g.uniform(0.2, 10.0, n).astype(np.float32)
+    depths[::5] = depths[3]  # many exact depth ties
+    mask = g.uniform(size=n) > 0.15
+    return pts, radii, depths, mask
+
+
+def _check(gpu, pts, radii, depths, mask, width, height, tile):
+    ref_off, ref_ids, ref_keys, ref_counts = binning.tile_layout(pts, radii, depths, mask, width,
+                                                                 height, tile)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    off, ids, keys, touched = cr.compute_tile_intersection_debug(d(pts), d(radii), d(depths),
+                                                                 d(mask), width, height, tile)
+    assert np.array_equal(off.cpu().numpy(), ref_off)
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    assert np.array_equal(keys.cpu().numpy().view(np.uint64), ref_keys)
+    assert np.array_equal(touched.cpu().numpy().astype(np.int64), ref_counts)
+    off2, ids2 = cr.compute_tile_intersection(d(pts), d(radii), d(depths), d(mask), width, height,
+                                              tile)
+    assert torch.equal(off2, off) and torch.equal(ids2, ids)
+    return len(ref_ids)
+
+
+@pytest.mark.parametrize("n,width,height,tile", [
+    (1, 64, 64, 16),
+    (1000, 64, 48, 16),
+    (5000, 100, 37, 16),
+    (20000, 256, 256, 16),
+    (3000, 64, 64, 8),
+    (3000, 200, 90, 32),
+    (50000, 800, 800, 16),
+])
+def test_layout_random_bitexact(gpu, n, width, height, tile):
+    pts, radii, depths, mask = _random_splats(n, width, height, seed=n + width)
+    k = _check(gpu, pts, radii, depths, mask, width, height, tile)
+    assert k > 0
+
+
+@pytest.mark.parametrize("name", ["multitile", "truncated"])
+def test_layout_reference_fixtures(gpu, name):
+    f = helpers.fixture_tensors(name)
+    off, ids = cr.compute_tile_intersection(f["points_image"].to(gpu), f["radii"].to(gpu),
+                                            f["depths"].to(gpu), f["mask"].to(gpu), f["width"],
+                                            f["height"], f["tile_size"])
+    assert off.cpu().tolist() == f["expected_indexing_offset"]
+    assert ids.cpu().tolist() == f["expected_gaussian_ids_sorted"]
+
+
+def test_layout_empty_inputs(gpu):
+    z2 = torch.zeros(0, 2, device=gpu)
+    off, ids = cr.compute_tile_intersection(z2, z2, torch.zeros(0, device=gpu),
+                                            torch.zeros(0, dtype=torch.bool, device=gpu), 40, 40, 16)
+    assert off.cpu().tolist() == [0] * 9 and ids.numel() == 0
+    pts, radii, depths, _ = _random_splats(100, 40, 40, seed=3)
+    none = np.zeros(100, dtype=bool)
+    k = _check(gpu, pts, radii, depths, none, 40, 40, 16)
+    assert k == 0
+
+
+def test_layout_from_projection_end_to_end(gpu):
+    """Projection on the GPU then binning on the GPU equals the oracle's chain
+    (the projection is bit-exact, so the integer layout must be too)."""
+    p, cam, _ = helpers.scene_orbit(30_000, 800, 800, 1100.0, seed=4)
+    scales, quats, opac = helpers.activated(p)
+    args = (cam["w2c"], cam["K"], 0.01, 100.0, 1 / 255, 0.5, 128.0, cam["width"], cam["height"])
+    pts, depths, _, _, radii, mask = preprocess.project_points(p["means"], scales, quats, opac, *args)
+    ref = binning.tile_layout(pts.detach().numpy(), radii.detach().numpy(), depths.detach().numpy(),
+                              mask.numpy(), 800, 800, 16)
+    d = lambda t: t.to(gpu)  # noqa: E731
+    g_pts, g_depths, _, _, g_radii, g_mask = cr.project_points(
+        d(p["means"]), d(scales), d(quats), d(opac), d(args[0]), d(args[1]), *args[2:])
+    off, ids, keys, touched = cr.compute_tile_intersection_debug(g_pts, g_radii, g_depths, g_mask,
+                                                                 800, 800, 16)
+    assert np.array_equal(off.cpu().numpy(), ref[0])
+    assert np.array_equal(ids.cpu().numpy(), ref[1])
+    assert np.array_equal(keys.cpu().numpy().view(np.uint64), ref[2])
+
+
+def test_layout_headline_size_bitexact(gpu):
+    """Full-size check at the headline configuration (1M
+    Gaussians, 1920x1080): projection on the GPU, then the GPU layout against the
+    numpy oracle on the GPU's own projected values."""
+    import bench
+
+    scene = bench.config3()
+    p = scene["params"]
+    scales, quats, opac = helpers.activated(p)
+    cam = scene["camera"]
+    d = lambda t: t.to(gpu)  # noqa: E731
+    g_pts, g_depths, _, _, g_radii, g_mask = cr.project_points(
+        d(p["means"]), d(scales), d(quats), d(opac), d(cam["w2c"]), d(cam["K"]), cam["near"], 100.0,
+        1 / 255, 0.5, 128.0, cam["width"], cam["height"])
+    pts, radii, depths, mask = (t.cpu().numpy() for t in (g_pts, g_radii, g_depths, g_mask))
+    k = _check(gpu, pts, radii, depths, mask, cam["width"], cam["height"], 16)
+    assert k > 5_000_000

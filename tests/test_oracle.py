@@ -1,0 +1,314 @@
+"""CPU tests of the oracle itself (no GPU).
+
+How each oracle function is pinned, independently of its own formulas:
+- render (oracle/render.py): against golden vectors written by the reference's
+  own src/torch_rasterizer.py (tests/golden/make_golden.py): image and the six
+  parameter gradients of an L1 loss, four scenes (SH0, SH3 orbit, sigmoid,
+  large splats).
+- projection (oracle/preprocess.py): closed forms (isotropic Gaussian on the
+  optical axis; frustum clamp active off-axis) and the identity conic * cov = I.
+- quaternion_to_rotation_matrix: identity quaternion, orthonormality, det +1,
+  and the 90-degree rotation about z.
+- SH basis: direction KATs and orthonormality of the 16 real SH functions over
+  the sphere (a wrong constant breaks it); the signs by the golden vectors.
+- binning (oracle/binning.py): vectorised form vs the loop restatement of
+  build_reference_tile_layout, and hand-derived layouts of the reference's two
+  constant fixtures.
+- blend (oracle/blend.py): per-tile vectorised form vs the brute-force pixel
+  loop (values and autograd gradients) and a one-Gaussian closed form.
+- planted mistakes (low-pass constant, SH sign, transmittance threshold) must
+  make the golden comparison fail.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import helpers
+from oracle import binning, blend, preprocess
+from oracle import render as orender
+
+GOLDEN_CASES = ["box_sh0", "orbit_sh3", "sigmoid", "e2e_large"]
+
+
+def _golden_run(name):
+    case = helpers.load_golden()[name]
+    p, cam, target = helpers.golden_case_tensors(case)
+    image, loss, grads, _, _ = helpers.forward_backward(
+        orender.render, p, cam, target, "cpu", loss_kind=str(case["loss_kind"]),
+        sh_sigmoid=bool(case["sh_sigmoid"]))
+    return case, image, loss, grads
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_oracle_matches_reference_golden(name):
+    case, image, loss, grads = _golden_run(name)
+    ref_img = torch.from_numpy(case["image"])
+    assert helpers.max_abs(image / 255.0, ref_img / 255.0) <= 1e-5
+    assert abs(float(loss) - float(case["loss"])) <= 1e-6 * max(1.0, abs(float(case["loss"])))
+    for k in helpers.PARAMS:
+        ref = torch.from_numpy(case["grad_" + k])
+        if float(ref.norm()) == 0.0:
+            assert float(grads[k].norm()) == 0.0
+            continue
+        assert helpers.rel_l2(grads[k], ref) <= 1e-4, k
+
+
+def test_golden_scenes_are_nontrivial():
+    """The golden scenes exercise what they claim: visible splats, multi-tile
+    Gaussians, partial tiles, non-zero SH-rest gradients."""
+    g = helpers.load_golden()
+    for name in GOLDEN_CASES:
+        assert float(np.abs(g[name]["image"]).max()) > 10.0
+    assert float(np.abs(g["orbit_sh3"]["grad_sh_rest"]).max()) > 0.0
+    assert int(g["orbit_sh3"]["width"]) % 16 != 0 and int(g["orbit_sh3"]["height"]) % 16 != 0
+
+
+# ---------------------------------------------------------------- planted mistakes
+
+def _golden_image_error(name):
+    case, image, _, grads = _golden_run(name)
+    img_err = helpers.max_abs(image / 255.0, torch.from_numpy(case["image"]) / 255.0)
+    grad_err = max(helpers.rel_l2(grads[k], torch.from_numpy(case["grad_" + k]))
+                   for k in helpers.PARAMS if float(np.abs(case["grad_" + k]).max()) > 0)
+    return img_err, grad_err
+
+
+def test_planted_lowpass_mistake_is_caught(monkeypatch):
+    monkeypatch.setattr(preprocess, "LOW_PASS_FILTER", 0.31)
+    img_err, grad_err = _golden_image_error("box_sh0")
+    assert img_err > 1e-4 or grad_err > 1e-3
+
+
+def test_planted_sh_sign_mistake_is_caught(monkeypatch):
+    monkeypatch.setattr(preprocess, "SH_C1", -preprocess.SH_C1)
+    img_err, grad_err = _golden_image_error("orbit_sh3")
+    assert img_err > 1e-4 or grad_err > 1e-3
+
+
+def test_planted_transmittance_mistake_is_caught(monkeypatch):
+    monkeypatch.setattr(blend, "TRANSMITTANCE_EPS", 1e-2)
+    img_err, grad_err = _golden_image_error("e2e_large")
+    assert img_err > 1e-4 or grad_err > 1e-3
+
+
+# ------------------------------------------------------------------ projection
+
+def test_quaternion_kats():
+    R = preprocess.quaternion_to_rotation_matrix(torch.tensor([[0.0, 0.0, 0.0, 1.0]]))
+    assert torch.equal(R[0], torch.eye(3))
+    s = math.sqrt(0.5)  # 90 degrees about z: x -> y
+    R = preprocess.quaternion_to_rotation_matrix(torch.tensor([[0.0, 0.0, s, s]]))[0]
+    assert torch.allclose(R @ torch.tensor([1.0, 0.0, 0.0]), torch.tensor([0.0, 1.0, 0.0]), atol=1e-6)
+    q = torch.randn(1000, 4, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    q = q / q.norm(dim=1, keepdim=True)
+    R = preprocess.quaternion_to_rotation_matrix(q)
+    eye = torch.eye(3, dtype=torch.float64).expand_as(R)
+    assert torch.allclose(R @ R.transpose(1, 2), eye, atol=1e-12)
+    assert torch.allclose(torch.linalg.det(R), torch.ones(1000, dtype=torch.float64), atol=1e-12)
+
+
+def _project_single(mean, scale, quat, K, width, height, w2c=None):
+    w2c = torch.eye(4) if w2c is None else w2c
+    return preprocess.project(torch.tensor([mean]), torch.tensor([scale]), torch.tensor([quat]),
+                              torch.tensor([0.9]), w2c, K, width, height)
+
+
+def test_projection_isotropic_on_axis_closed_form():
+    fx, fy, W, H = 300.0, 250.0, 256, 192
+    K = torch.tensor([[fx, 0, W / 2], [0, fy, H / 2], [0, 0, 1.0]])
+    sigma, z = 0.05, 3.0
+    p = _project_single([0.0, 0.0, z], [sigma] * 3, [0.0, 0.0, 0.0, 1.0], K, W, H)
+    a = (fx * sigma / z) ** 2 + 0.3
+    c = (fy * sigma / z) ** 2 + 0.3
+    assert math.isclose(float(p["a"]), a, rel_tol=1e-6)
+    assert math.isclose(float(p["c"]), c, rel_tol=1e-6)
+    assert abs(float(p["b"])) < 1e-9
+    assert math.isclose(float(p["u"]), W / 2, rel_tol=1e-7)
+    assert math.isclose(float(p["A"]), 1 / a, rel_tol=1e-6)
+    assert math.isclose(float(p["C"]), 1 / c, rel_tol=1e-6)
+    assert math.isclose(float(p["ru"]), 3 * math.sqrt(a), rel_tol=1e-6)
+    assert bool(p["keep"])
+
+
+def test_projection_frustum_clamp_closed_form():
+    """Off-axis point beyond 1.3x the half-width: the Jacobian's x/z is clamped."""
+    fx = fy = 100.0
+    W = H = 100
+    K = torch.tensor([[fx, 0, 50.0], [0, fy, 50.0], [0, 0, 1.0]])
+    lim = 1.3 * 50.0 / fx  # 0.65
+    x, z, s = 2.0, 2.0, 0.02  # x/z = 1.0 > lim
+    p = _project_single([x, 0.0, z], [s, 2 * s, 3 * s], [0.0, 0.0, 0.0, 1.0], K, W, H)
+    S = np.diag([s * s, 4 * s * s, 9 * s * s])
+    J = np.array([[fx / z, 0.0, -fx * lim / z], [0.0, fy / z, 0.0]])
+    cov = J @ S @ J.T
+    assert math.isclose(float(p["a"]), cov[0, 0] + 0.3, rel_tol=1e-5)
+    assert math.isclose(float(p["c"]), cov[1, 1] + 0.3, rel_tol=1e-5)
+    assert not bool(p["keep"])  # u = 150 > W + r_u: culled
+
+
+def test_conic_inverts_covariance():
+    pr, cam, _ = helpers.scene_box(500, 64, 64, 75.0, seed=5, log_scale=(-2.5, 0.5))
+    sc, q, o = helpers.activated(pr)
+    p = preprocess.project(pr["means"], sc, q, o, cam["w2c"], cam["K"], 64, 64)
+    k = p["keep"]
+    a, b, c = p["a"][k].double(), p["b"][k].double(), p["c"][k].double()
+    A, B, C = p["A"][k].double(), p["B"][k].double(), p["C"][k].double()
+    assert k.sum() > 100
+    assert torch.allclose(A * a + B * b, torch.ones_like(a), atol=1e-4)
+    assert torch.allclose(A * b + B * c, torch.zeros_like(a), atol=1e-4)
+    assert torch.allclose(B * b + C * c, torch.ones_like(a), atol=1e-4)
+
+
+def test_projection_culls():
+    K = helpers.intrinsic(100.0, 64, 64)
+    q = [0.0, 0.0, 0.0, 1.0]
+    means = torch.tensor([[0.0, 0.0, 2.0],    # visible
+                          [0.0, 0.0, 0.005],  # in front of the near plane
+                          [0.0, 0.0, 200.0],  # beyond far
+                          [5.0, 0.0, 2.0],    # off image
+                          [0.0, 0.0, 2.0],    # opacity below 1/255
+                          [0.0, 0.0, 2.0]])   # radius above max_radius
+    scales = torch.tensor([[0.02] * 3] * 5 + [[5.0] * 3])
+    opac = torch.tensor([0.5, 0.5, 0.5, 0.5, 0.001, 0.5])
+    quats = torch.tensor([q] * 6)
+    p = preprocess.project(means, scales, quats, opac, torch.eye(4), K, 64, 64)
+    assert p["keep"].tolist() == [True, False, False, False, False, False]
+
+
+# ------------------------------------------------------------------------- SH
+
+def test_sh_basis_direction_kats():
+    b = preprocess.sh_basis_rest(torch.tensor([[0.0, 0.0, 1.0]], dtype=torch.float64))[0]
+    expect = torch.zeros(15, dtype=torch.float64)
+    expect[1] = preprocess.SH_C1
+    expect[5] = 2 * preprocess.SH_C2_zz
+    expect[11] = 2 * preprocess.SH_C3_zzz
+    assert torch.allclose(b, expect, atol=1e-15)
+    b = preprocess.sh_basis_rest(torch.tensor([[1.0, 0.0, 0.0]], dtype=torch.float64))[0]
+    expect = torch.zeros(15, dtype=torch.float64)
+    expect[2] = -preprocess.SH_C1
+    expect[5] = -preprocess.SH_C2_zz
+    expect[7] = preprocess.SH_C2_xx_yy
+    expect[12] = -preprocess.SH_C3_xzz
+    expect[14] = preprocess.SH_C3_xxx_xyy
+    assert torch.allclose(b, expect, atol=1e-15)
+
+
+def test_sh_basis_orthonormal_on_sphere():
+    """Real SH of degree <= 3 are orthonormal on S^2; checks every constant.
+
+    Exception: the reference's l=3, m=-3 term is C * y * (x^2 - y^2)
+    (src/gaussian.py:43, src/cuda/kernel.cu:586), not the textbook
+    C * y * (3x^2 - y^2); it is reproduced for parity and pinned by a KAT instead.
+    """
+    n = 400_000
+    i = torch.arange(n, dtype=torch.float64) + 0.5
+    zz = 1 - 2 * i / n
+    phi = math.pi * (1 + 5 ** 0.5) * i
+    r = torch.sqrt(1 - zz * zz)
+    dirs = torch.stack([r * torch.cos(phi), r * torch.sin(phi), zz], dim=1)
+    Y = torch.cat([torch.full((n, 1), preprocess.SH_C0, dtype=torch.float64),
+                   preprocess.sh_basis_rest(dirs)], dim=1)
+    keep = [j for j in range(16) if j != 9]
+    Y = Y[:, keep]
+    gram = (Y.t() @ Y) * (4 * math.pi / n)
+    assert torch.allclose(gram, torch.eye(15, dtype=torch.float64), atol=1e-4)
+
+
+def test_sh_reference_m_minus3_term():
+    x, y, z = 0.48, 0.6, 0.64  # unit vector
+    b = preprocess.sh_basis_rest(torch.tensor([[x, y, z]], dtype=torch.float64))[0]
+    assert math.isclose(float(b[8]), preprocess.SH_C3_yxx_yyy * y * (x * x - y * y), rel_tol=1e-12)
+
+
+# -------------------------------------------------------------------- binning
+
+def _random_splats(n, width, height, seed, rmax=40.0):
+    g = np.random.default_rng(seed)
+    pts = np.stack([g.uniform(-20, width + 20, n), g.uniform(-20, height + 20, n)], 1).astype(np.float32)
+    radii = g.uniform(0.5, rmax, (n, 2)).astype(np.float32)
+    depths = g.uniform(0.2, 10.0, n).astype(np.float32)
+    depths[::7] = depths[0]  # ties in depth
+    mask = g.uniform(size=n) > 0.2
+    return pts, radii, depths, mask
+
+
+@pytest.mark.parametrize("width,height,tile", [(64, 48, 16), (100, 37, 16), (64, 64, 8)])
+def test_binning_vectorized_matches_loop(width, height, tile):
+    pts, radii, depths, mask = _random_splats(300, width, height, seed=width + height)
+    off, ids, keys, counts = binning.tile_layout(pts, radii, depths, mask, width, height, tile)
+    off2, ids2 = binning.tile_layout_loop(pts, radii, depths, mask, width, height, tile)
+    assert off.tolist() == off2
+    assert ids.tolist() == ids2
+    assert np.all(np.diff(keys.astype(np.float64)) >= 0)
+    assert int(counts.sum()) == len(ids)
+
+
+@pytest.mark.parametrize("name", ["multitile", "truncated"])
+def test_layout_fixture_hand_values(name):
+    """expected_* in layout_fixtures.json were derived by hand:
+    multitile -- G0 (15.5,15.5) r10.5: u,v in [5,26] -> tiles {0,1,3,4}; G1 r(9.8,9.2):
+    u [6,26], v [6,25] -> {0,1,3,4}; G2 (31.2,7.5): u [22,39] -> tx 1..2, v [0,15] -> {1,2};
+    G3 (7.5,31.2): u [0,15], v [22,40] -> {3,6}; G4 (39,39) r4.5: [34,43] -> {8}.
+    Depth order G4 < G2 < G0 < G1 < G3 gives tile lists 0:[0,1] 1:[2,0,1] 2:[2]
+    3:[0,1,3] 4:[0,1] 6:[3] 8:[4].  truncated -- every Gaussian spans tiles {0,1,3,4},
+    depths increase with the index."""
+    f = helpers.fixture_tensors(name)
+    off, ids, _, _ = binning.tile_layout(f["points_image"].numpy(), f["radii"].numpy(),
+                                         f["depths"].numpy(), f["mask"].numpy(), f["width"],
+                                         f["height"], f["tile_size"])
+    assert off.tolist() == f["expected_indexing_offset"]
+    assert ids.tolist() == f["expected_gaussian_ids_sorted"]
+    off2, ids2 = binning.tile_layout_loop(f["points_image"].tolist(), f["radii"].tolist(),
+                                          f["depths"].tolist(), f["mask"].tolist(), f["width"],
+                                          f["height"], f["tile_size"])
+    assert off2 == f["expected_indexing_offset"] and ids2 == f["expected_gaussian_ids_sorted"]
+
+
+def test_binning_empty_and_all_culled():
+    off, ids, keys, counts = binning.tile_layout(np.zeros((0, 2)), np.zeros((0, 2)), np.zeros(0),
+                                                 np.zeros(0, bool), 32, 32, 16)
+    assert off.tolist() == [0, 0, 0, 0] and len(ids) == 0
+    pts, radii, depths, _ = _random_splats(50, 32, 32, seed=1)
+    off, ids, _, _ = binning.tile_layout(pts, radii, depths, np.zeros(50, bool), 32, 32, 16)
+    assert off.tolist() == [0, 0, 0, 0] and len(ids) == 0
+
+
+# ---------------------------------------------------------------------- blend
+
+@pytest.mark.parametrize("name", ["multitile", "truncated"])
+def test_blend_vectorized_matches_bruteforce(name):
+    f = helpers.fixture_tensors(name)
+    off = torch.tensor(f["expected_indexing_offset"], dtype=torch.int32)
+    ids = torch.tensor(f["expected_gaussian_ids_sorted"], dtype=torch.int32)
+    args = (f["width"], f["height"], f["tile_size"], f["alpha_threshold"],
+            f["transmittance_threshold"], f["chi_squared_threshold"])
+    ins = [f[k].clone().requires_grad_(True) for k in ("points_image", "cov_inv_image", "opacities", "colors")]
+    img = blend.rasterize(off, ids, *ins, *args)
+    (img * f["upstream"]).sum().backward()
+    g1 = [t.grad.clone() for t in ins]
+    ins2 = [f[k].clone().requires_grad_(True) for k in ("points_image", "cov_inv_image", "opacities", "colors")]
+    img2 = blend.rasterize_bruteforce(off, ids, *ins2, *args)
+    (img2 * f["upstream"]).sum().backward()
+    assert helpers.max_abs(img, img2) <= 1e-6
+    assert float(img.abs().max()) > 0.1
+    for a, b in zip(g1, [t.grad for t in ins2]):
+        assert helpers.rel_l2(a, b) <= 1e-5
+
+
+def test_blend_single_gaussian_closed_form():
+    o, col = 0.7, torch.tensor([[0.2, 0.5, 0.9]])
+    pts = torch.tensor([[5.0, 6.0]])
+    conic = torch.tensor([[0.5, 0.1, 0.25]])
+    off = torch.tensor([0], dtype=torch.int32)
+    ids = torch.tensor([0], dtype=torch.int32)
+    img = blend.rasterize(off, ids, pts, conic, torch.tensor([o]), col, 16, 16, 16, 1e-4, 1e-4, 9.21)
+    assert torch.allclose(img[6, 5], o * col[0], atol=1e-7)
+    E = 0.5 * 1 * 1 + 2 * 0.1 * 1 * 2 + 0.25 * 2 * 2  # pixel (6, 8): du=1, dv=2
+    assert torch.allclose(img[8, 6], o * math.exp(-0.5 * E) * col[0], atol=1e-7)
+    assert float(img[0, 15].abs().max()) == 0.0  # E = 0.5*100+... > 9.21
