@@ -1,11 +1,14 @@
 // Tile blending: front-to-back alpha compositing and its gradient.
 //
-// One workgroup per 16x16 tile: 256 threads = 4 wave64s, each wave owning a
-// 16x4 strip of pixels (one pixel per lane).  The tile's depth-sorted Gaussian
-// list is walked in batches of 256 records staged in LDS; a wave skips a
-// Gaussian whose chi-square ellipse misses its strip (uniform branch), and the
-// workgroup stops as soon as every pixel's transmittance fell below the
-// threshold (__syncthreads_and per batch, per-lane break inside a batch).
+// One wave64 per 16x16 tile.  Lane l owns the four pixels
+// (x0 + l%16, y0 + l/16 + 4s), s = 0..3, i.e. one pixel in each 16x4 strip of
+// the tile.  The tile's depth-sorted Gaussian list is walked in batches of 64
+// records staged in LDS (one record per lane); for each Gaussian the wave tests
+// (uniformly) which strips its chi-square ellipse reaches and evaluates only
+// those, and it stops once the transmittance of all 256 pixels fell below the
+// threshold.  Tiles are assigned to workgroups XCD by XCD (the dispatcher
+// places workgroup b on XCD b % 8) so that neighbouring tiles, which share
+// Gaussians, run on the same XCD and share its L2.
 //
 // Decision quantities (E, alpha, T) are computed with separately rounded ops in
 // the Torch rasterizer's order (src/torch_rasterizer.py:255-278) -- this file
@@ -15,19 +18,20 @@
 // The backward walks the list in the same front-to-back order.  With
 // S_i = sum_{k>i} w_k (g.c_k) = g.C - sum_{k<=i} w_k (g.c_k), where C is the
 // pixel's forward colour, dL/dalpha_i = T_i (g.c_i) - S_i / (1 - alpha_i + eps).
-// Per-pixel contributions are summed over each wave with a butterfly, the four
-// wave partials are combined in LDS, and one float atomic per (tile, Gaussian,
-// field) goes to HBM (the reference issues one per pixel: kernel.cu:1098-1106).
+// A lane sums its four pixels' contributions in registers, the wave reduces the
+// nine fields with DPP row butterflies plus two permlane swaps, and lane 0
+// issues one float atomic per (tile, Gaussian, field) (the reference issues one
+// per pixel: src/cuda/kernel.cu:1098-1106).
 
 #include "gs_common.h"
 
 namespace gs {
 
 constexpr int kTile = 16;
-constexpr int kBlendThreads = 256;
-constexpr int kBatch = 256;
-constexpr int kBlendWaves = kBlendThreads / kWave;
-constexpr int kGradFields = 9;  // du, dv, dA, dB, dC, dopacity, dr, dg, db
+constexpr int kStrips = 4;       // 16x4 strips per tile; one pixel of each per lane
+constexpr int kBatch = kWave;    // records staged per batch (one per lane)
+constexpr int kGradFields = 9;   // du, dv, dA, dB, dC, dopacity, dr, dg, db
+constexpr int kXcds = 8;
 
 struct TileSpan {
     int32_t start, end;
@@ -44,6 +48,14 @@ __device__ __forceinline__ TileSpan tile_span(const int32_t *__restrict__ offset
     s.start = min(max(a, 0), kk);
     s.end = min(max(b, s.start), kk);
     return s;
+}
+
+// Bijection workgroup -> tile giving XCD x the contiguous tile range
+// [x*base + min(x, rem), ...) of length base + (x < rem).
+__device__ __forceinline__ int tile_of_block(int b, int n_tiles) {
+    const int base = n_tiles / kXcds, rem = n_tiles % kXcds;
+    const int x = b % kXcds, i = b / kXcds;
+    return x * base + min(x, rem) + i;
 }
 
 // Conservative half-extents of the ellipse {E < chi_eff} of conic (A, B, C),
@@ -100,209 +112,242 @@ __device__ __forceinline__ void stage_record(BatchLds &s, int slot, int g, int64
                               __int_as_float(g));
 }
 
-// Front-to-back accumulation of the pixel colour over the tile's list.
-// Every thread of the workgroup must call it (it contains barriers).
+// Strips [s_lo, s_hi] of the tile reached by the ellipse of record (geo, aux);
+// false when the ellipse misses the tile.  Wave-uniform.
+__device__ __forceinline__ bool strip_range(float4 geo, float4 aux, float x0, float y0, int &s_lo,
+                                            int &s_hi) {
+    if (geo.x + aux.z < x0 || geo.x - aux.z > x0 + (kTile - 1)) return false;
+    const float ylo = geo.y - aux.w - y0, yhi = geo.y + aux.w - y0;
+    if (yhi < 0.0f || ylo > (float)(kTile - 1)) return false;
+    s_lo = ylo <= 0.0f ? 0 : ((int)ylo >> 2);
+    s_hi = yhi >= (float)(kTile - 1) ? kStrips - 1 : ((int)yhi >> 2);
+    return true;
+}
+
+// Pixel geometry of one lane.
+struct LanePixels {
+    float fx;             // pixel x
+    float fy0;            // pixel y of strip 0 (strip s adds 4s)
+    float x0, y0;         // tile origin
+    bool inside[kStrips];
+};
+
+__device__ __forceinline__ LanePixels lane_pixels(int tile, int tiles_x, int width, int height) {
+    LanePixels p;
+    const int lane = threadIdx.x;
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const int px = tx * kTile + (lane & 15);
+    const int py = ty * kTile + (lane >> 4);
+    p.fx = (float)px;
+    p.fy0 = (float)py;
+    p.x0 = (float)(tx * kTile);
+    p.y0 = (float)(ty * kTile);
+#pragma unroll
+    for (int s = 0; s < kStrips; ++s) p.inside[s] = px < width && py + 4 * s < height;
+    return p;
+}
+
+__device__ __forceinline__ bool wave_all(bool x) { return __ballot(!x) == 0; }
+
+// Front-to-back accumulation of the lane's four pixels over the tile's list.
+// All 64 lanes must call it (it contains barriers).
 __device__ __forceinline__ void blend_accumulate(
     BatchLds &s, TileSpan span, const int32_t *__restrict__ ids, int64_t n,
     const float *__restrict__ points, const float *__restrict__ conics,
-    const float *__restrict__ opac, const float *__restrict__ colors, float fx, float fy,
-    float wx0, float wx1, float wy0, float wy1, bool done, float alpha_thr, float T_thr,
-    float chi, float &cr, float &cg, float &cb) {
-    float T = 1.0f;
-    cr = cg = cb = 0.0f;
+    const float *__restrict__ opac, const float *__restrict__ colors, const LanePixels &pix,
+    float alpha_thr, float T_thr, float chi, float (&cr)[kStrips], float (&cg)[kStrips],
+    float (&cb)[kStrips]) {
+    float T[kStrips];
+    bool dn[kStrips];
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        T[q] = 1.0f;
+        cr[q] = cg[q] = cb[q] = 0.0f;
+        dn[q] = !pix.inside[q] || !(1.0f >= T_thr);
+    }
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
-        if (__syncthreads_and(done)) break;
+        if (wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
+        __syncthreads();  // previous batch fully read before restaging
         const int32_t i = b0 + (int32_t)threadIdx.x;
         if (i < span.end)
             stage_record(s, threadIdx.x, ids[i], n, points, conics, opac, colors, chi, alpha_thr);
         __syncthreads();
         const int cnt = min(kBatch, span.end - b0);
-        if (!done) {
-            for (int j = 0; j < cnt; ++j) {
-                const float4 geo = s.geo[j];
-                const float4 aux = s.aux[j];
-                if (geo.x + aux.z < wx0 || geo.x - aux.z > wx1 || geo.y + aux.w < wy0 ||
-                    geo.y - aux.w > wy1)
-                    continue;
-                const float du = fx - geo.x, dv = fy - geo.y;
+        for (int j = 0; j < cnt; ++j) {
+            const float4 geo = s.geo[j];
+            const float4 aux = s.aux[j];
+            int s_lo, s_hi;
+            if (!strip_range(geo, aux, pix.x0, pix.y0, s_lo, s_hi)) continue;
+            const float4 col = s.col[j];
+            const float du = pix.fx - geo.x;
+#pragma unroll
+            for (int q = 0; q < kStrips; ++q) {
+                if (q < s_lo || q > s_hi) continue;  // uniform
+                if (dn[q]) continue;
+                const float dv = (pix.fy0 + (float)(4 * q)) - geo.y;
                 const float E = conic_exponent(geo.z, geo.w, aux.x, du, dv);
                 if (!(E < chi)) continue;
                 const float alpha = __expf(-0.5f * E) * aux.y;
                 if (alpha < alpha_thr) continue;
-                const float4 col = s.col[j];
-                const float w = alpha * T;
-                cr = fmaf(w, col.x, cr);
-                cg = fmaf(w, col.y, cg);
-                cb = fmaf(w, col.z, cb);
-                T = T * ((1.0f - alpha) + kTransmittanceEps);
-                if (T < T_thr) {
-                    done = true;
-                    break;
-                }
+                const float w = alpha * T[q];
+                cr[q] = fmaf(w, col.x, cr[q]);
+                cg[q] = fmaf(w, col.y, cg[q]);
+                cb[q] = fmaf(w, col.z, cb[q]);
+                T[q] = T[q] * ((1.0f - alpha) + kTransmittanceEps);
+                if (T[q] < T_thr) dn[q] = true;
             }
+            if ((j & 7) == 7 && wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
         }
     }
 }
 
-__global__ __launch_bounds__(kBlendThreads) void blend_forward_kernel(
+__global__ __launch_bounds__(kWave) void blend_forward_kernel(
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image) {
     __shared__ BatchLds s;
-    const int tile = blockIdx.x;
-    const int tx = tile % tiles_x, ty = tile / tiles_x;
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int px = tx * kTile + (lane & 15);
-    const int py = ty * kTile + wave * 4 + (lane >> 4);
-    const bool inside = px < width && py < height;
-    const float wx0 = (float)(tx * kTile), wx1 = wx0 + (kTile - 1);
-    const float wy0 = (float)(ty * kTile + wave * 4), wy1 = wy0 + 3.0f;
+    const int tile = tile_of_block(blockIdx.x, n_tiles);
+    const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
-    const bool done = !inside || !(1.0f >= T_thr);
-    float cr, cg, cb;
-    blend_accumulate(s, span, ids, n, points, conics, opac, colors, (float)px, (float)py, wx0,
-                     wx1, wy0, wy1, done, alpha_thr, T_thr, chi, cr, cg, cb);
-    if (inside) {
-        const int64_t o = ((int64_t)py * width + px) * 3;
-        image[o] = cr;
-        image[o + 1] = cg;
-        image[o + 2] = cb;
+    float cr[kStrips], cg[kStrips], cb[kStrips];
+    blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr, chi, cr,
+                     cg, cb);
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        if (!pix.inside[q]) continue;
+        const int64_t o = ((int64_t)(pix.fy0 + 4 * q) * width + (int64_t)pix.fx) * 3;
+        image[o] = cr[q];
+        image[o + 1] = cg[q];
+        image[o + 2] = cb[q];
     }
 }
 
+// Sum over the 64 lanes, result in every lane: butterflies inside each 16-lane
+// row with DPP (xor 1, xor 2, half-mirror, mirror), then the gfx950 permlane
+// swaps exchange rows 0<->1, 2<->3 and halves 0-31 <-> 32-63.
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
-    return x;
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                      false, false);
+    x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                      false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
-struct BackLds {
-    BatchLds rec;
-    float partial[kGradFields][kBlendWaves][kBatch];
-};
-
-__global__ __launch_bounds__(kBlendThreads) void blend_backward_kernel(
+__global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const float *__restrict__ grad_image, const float *__restrict__ image,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr, float chi, float *__restrict__ g_points,
     float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors) {
-    __shared__ BackLds s;
-    const int tile = blockIdx.x;
-    const int tx = tile % tiles_x, ty = tile / tiles_x;
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int px = tx * kTile + (lane & 15);
-    const int py = ty * kTile + wave * 4 + (lane >> 4);
-    const bool inside = px < width && py < height;
-    const float fx = (float)px, fy = (float)py;
-    const float wx0 = (float)(tx * kTile), wx1 = wx0 + (kTile - 1);
-    const float wy0 = (float)(ty * kTile + wave * 4), wy1 = wy0 + 3.0f;
+    __shared__ BatchLds s;
+    const int tile = tile_of_block(blockIdx.x, n_tiles);
+    const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
     if (span.end <= span.start) return;  // uniform across the workgroup
 
-    float gr = 0.f, gg = 0.f, gb = 0.f, cr = 0.f, cg = 0.f, cb = 0.f;
-    const int64_t pix = ((int64_t)py * width + px) * 3;
-    if (inside) {
-        gr = grad_image[pix];
-        gg = grad_image[pix + 1];
-        gb = grad_image[pix + 2];
-    }
-    const bool never = !inside || !(1.0f >= T_thr);
-    if (image) {
-        if (inside) {
-            cr = image[pix];
-            cg = image[pix + 1];
-            cb = image[pix + 2];
+    float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips], T[kStrips], acc[kStrips];
+    bool dn[kStrips];
+    float cr[kStrips], cg[kStrips], cb[kStrips];
+    if (!image)
+        blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr,
+                         chi, cr, cg, cb);
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        gr[q] = gg[q] = gb[q] = 0.0f;
+        if (pix.inside[q]) {
+            const int64_t o = ((int64_t)(pix.fy0 + 4 * q) * width + (int64_t)pix.fx) * 3;
+            gr[q] = grad_image[o];
+            gg[q] = grad_image[o + 1];
+            gb[q] = grad_image[o + 2];
+            if (image) {
+                cr[q] = image[o];
+                cg[q] = image[o + 1];
+                cb[q] = image[o + 2];
+            }
+        } else {
+            cr[q] = cg[q] = cb[q] = 0.0f;
         }
-    } else {
-        blend_accumulate(s.rec, span, ids, n, points, conics, opac, colors, fx, fy, wx0, wx1,
-                         wy0, wy1, never, alpha_thr, T_thr, chi, cr, cg, cb);
+        gC[q] = gr[q] * cr[q] + gg[q] * cg[q] + gb[q] * cb[q];
+        T[q] = 1.0f;
+        acc[q] = 0.0f;
+        dn[q] = !pix.inside[q] || !(1.0f >= T_thr) ||
+                (gr[q] == 0.0f && gg[q] == 0.0f && gb[q] == 0.0f);
     }
-    const float gC = gr * cr + gg * cg + gb * cb;
-    bool done = never || (gr == 0.0f && gg == 0.0f && gb == 0.0f);
-    float T = 1.0f, acc = 0.0f;
 
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
-        if (__syncthreads_and(done)) break;
+        if (wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
+        __syncthreads();
         const int32_t i = b0 + (int32_t)threadIdx.x;
         if (i < span.end)
-            stage_record(s.rec, threadIdx.x, ids[i], n, points, conics, opac, colors, chi,
-                         alpha_thr);
-        {
-            float *p = &s.partial[0][0][0];
-            for (int q = threadIdx.x; q < kGradFields * kBlendWaves * kBatch; q += kBlendThreads)
-                p[q] = 0.0f;
-        }
+            stage_record(s, threadIdx.x, ids[i], n, points, conics, opac, colors, chi, alpha_thr);
         __syncthreads();
         const int cnt = min(kBatch, span.end - b0);
         for (int j = 0; j < cnt; ++j) {
-            if (__ballot(!done) == 0) break;  // whole wave finished
-            const float4 geo = s.rec.geo[j];
-            const float4 aux = s.rec.aux[j];
-            if (geo.x + aux.z < wx0 || geo.x - aux.z > wx1 || geo.y + aux.w < wy0 ||
-                geo.y - aux.w > wy1)
-                continue;
+            const float4 geo = s.geo[j];
+            const float4 aux = s.aux[j];
+            int s_lo, s_hi;
+            if (!strip_range(geo, aux, pix.x0, pix.y0, s_lo, s_hi)) continue;
+            const float4 col = s.col[j];
+            const float du = pix.fx - geo.x;
+            const float B = 0.5f * geo.w;
             float v[kGradFields] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
             bool hit = false;
-            if (!done) {
-                const float du = fx - geo.x, dv = fy - geo.y;
+#pragma unroll
+            for (int q = 0; q < kStrips; ++q) {
+                if (q < s_lo || q > s_hi) continue;  // uniform
+                if (dn[q]) continue;
+                const float dv = (pix.fy0 + (float)(4 * q)) - geo.y;
                 const float E = conic_exponent(geo.z, geo.w, aux.x, du, dv);
-                if (E < chi) {
-                    const float G = __expf(-0.5f * E);
-                    const float alpha = G * aux.y;
-                    if (alpha >= alpha_thr) {
-                        hit = true;
-                        const float4 col = s.rec.col[j];
-                        const float w = alpha * T;
-                        const float gcol = fmaf(gr, col.x, fmaf(gg, col.y, gb * col.z));
-                        const float acc_new = fmaf(w, gcol, acc);
-                        const float suffix = gC - acc_new;
-                        const float one_m = (1.0f - alpha) + kTransmittanceEps;
-                        const float dalpha = T * gcol - suffix / one_m;
-                        const float h = alpha * dalpha;
-                        const float B = 0.5f * geo.w;
-                        v[0] = h * fmaf(geo.z, du, B * dv);
-                        v[1] = h * fmaf(B, du, aux.x * dv);
-                        v[2] = -0.5f * h * du * du;
-                        v[3] = -h * du * dv;
-                        v[4] = -0.5f * h * dv * dv;
-                        v[5] = G * dalpha;
-                        v[6] = w * gr;
-                        v[7] = w * gg;
-                        v[8] = w * gb;
-                        acc = acc_new;
-                        T = T * one_m;
-                        if (T < T_thr) done = true;
-                    }
+                if (!(E < chi)) continue;
+                const float G = __expf(-0.5f * E);
+                const float alpha = G * aux.y;
+                if (alpha < alpha_thr) continue;
+                hit = true;
+                const float w = alpha * T[q];
+                const float gcol = fmaf(gr[q], col.x, fmaf(gg[q], col.y, gb[q] * col.z));
+                const float acc_new = fmaf(w, gcol, acc[q]);
+                const float one_m = (1.0f - alpha) + kTransmittanceEps;
+                const float dalpha = T[q] * gcol - (gC[q] - acc_new) / one_m;
+                const float h = alpha * dalpha;
+                const float hdu = h * du, hdv = h * dv;
+                v[0] += hdu;
+                v[1] += hdv;
+                v[2] = fmaf(hdu, du, v[2]);
+                v[3] = fmaf(hdu, dv, v[3]);
+                v[4] = fmaf(hdv, dv, v[4]);
+                v[5] = fmaf(G, dalpha, v[5]);
+                v[6] = fmaf(w, gr[q], v[6]);
+                v[7] = fmaf(w, gg[q], v[7]);
+                v[8] = fmaf(w, gb[q], v[8]);
+                acc[q] = acc_new;
+                T[q] = T[q] * one_m;
+                if (T[q] < T_thr) dn[q] = true;
+            }
+            if (__ballot(hit) != 0) {
+#pragma unroll
+                for (int f = 0; f < kGradFields; ++f) v[f] = wave_sum(v[f]);
+                if (threadIdx.x == 0) {
+                    const int g = __float_as_int(col.w);
+                    // dE/du = -2(A du + B dv): sum h (A du + B dv) = A sum h du + B sum h dv
+                    unsafeAtomicAdd(g_points + 2 * g, fmaf(geo.z, v[0], B * v[1]));
+                    unsafeAtomicAdd(g_points + 2 * g + 1, fmaf(B, v[0], aux.x * v[1]));
+                    unsafeAtomicAdd(g_conics + 3 * g, -0.5f * v[2]);
+                    unsafeAtomicAdd(g_conics + 3 * g + 1, -v[3]);
+                    unsafeAtomicAdd(g_conics + 3 * g + 2, -0.5f * v[4]);
+                    unsafeAtomicAdd(g_opac + g, v[5]);
+                    unsafeAtomicAdd(g_colors + 3 * g, v[6]);
+                    unsafeAtomicAdd(g_colors + 3 * g + 1, v[7]);
+                    unsafeAtomicAdd(g_colors + 3 * g + 2, v[8]);
                 }
             }
-            if (__ballot(hit) == 0) continue;
-#pragma unroll
-            for (int f = 0; f < kGradFields; ++f) {
-                const float t = wave_sum(v[f]);
-                if (lane == 0) s.partial[f][wave][j] = t;
-            }
-        }
-        __syncthreads();
-        for (int q = threadIdx.x; q < kGradFields * cnt; q += kBlendThreads) {
-            const int f = q / cnt, j = q % cnt;
-            const float t = s.partial[f][0][j] + s.partial[f][1][j] + s.partial[f][2][j] +
-                            s.partial[f][3][j];
-            if (t != 0.0f) {
-                const int g = __float_as_int(s.rec.col[j].w);
-                float *dst;
-                if (f < 2)
-                    dst = g_points + 2 * g + f;
-                else if (f < 5)
-                    dst = g_conics + 3 * g + (f - 2);
-                else if (f == 5)
-                    dst = g_opac + g;
-                else
-                    dst = g_colors + 3 * g + (f - 6);
-                unsafeAtomicAdd(dst, t);
-            }
+            if ((j & 7) == 7 && wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
         }
     }
 }
@@ -461,7 +506,7 @@ extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gauss
     if (k > 0 && (!points_image || !cov_inv_image || !opacities || !colors))
         return GS_ERR_INVALID_ARGUMENT;
     if (tile_size == kTile) {
-        hipLaunchKernelGGL(blend_forward_kernel, dim3(n_tiles), dim3(kBlendThreads), 0, stream,
+        hipLaunchKernelGGL(blend_forward_kernel, dim3(n_tiles), dim3(kWave), 0, stream,
                            indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
@@ -501,7 +546,7 @@ extern "C" int gs_rasterize_backward(
         return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     if (tile_size == kTile) {
-        hipLaunchKernelGGL(blend_backward_kernel, dim3(n_tiles), dim3(kBlendThreads), 0, stream,
+        hipLaunchKernelGGL(blend_backward_kernel, dim3(n_tiles), dim3(kWave), 0, stream,
                            grad_image, image, indexing_offset, gaussian_ids_sorted, n_tiles, k,
                            n, points_image, cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,

@@ -34,6 +34,31 @@ __device__ __forceinline__ Camera load_camera(const float *__restrict__ w2c,
     return c;
 }
 
+// IEEE correctly rounded fp32 square root.  The device sqrtf is accurate to
+// about 1 ulp but not correctly rounded (and the compiler folds
+// (float)sqrt((double)x) back into sqrtf), so the candidate is corrected with an
+// exact midpoint test: the midpoint m of two adjacent floats has 25 significant
+// bits, so m*m is exact in double, and sqrt(x) < m <=> x < m*m.
+__device__ __forceinline__ float sqrt_rn(float x) {
+    float s = sqrtf(x);
+    if (!(x > 0.0f) || !isfinite(x)) return s;  // 0, negatives, NaN, inf
+    const double xd = (double)x;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const float lo = __uint_as_float(__float_as_uint(s) - 1u);
+        const float hi = __uint_as_float(__float_as_uint(s) + 1u);
+        const double mlo = 0.5 * ((double)s + (double)lo);
+        const double mhi = 0.5 * ((double)s + (double)hi);
+        if (xd < mlo * mlo)
+            s = lo;
+        else if (xd > mhi * mhi)
+            s = hi;
+        else
+            break;
+    }
+    return s;
+}
+
 // min(max(x, lo), hi) propagating NaN like torch.clamp (fminf/fmaxf drop NaN).
 __device__ __forceinline__ float clamp_nan(float x, float lo, float hi) {
     return x < lo ? lo : (x > hi ? hi : x);
@@ -135,8 +160,8 @@ __device__ __forceinline__ Projection project_gaussian(const Camera &cam, float 
     const float A = p.c * inv_det;
     const float B = -p.b * inv_det;
     const float C = p.a * inv_det;
-    const float ru = sqrtf(fmaxf(p.a, 1e-12f)) * kSigmaExtent;
-    const float rv = sqrtf(fmaxf(p.c, 1e-12f)) * kSigmaExtent;
+    const float ru = sqrt_rn(fmaxf(p.a, 1e-12f)) * kSigmaExtent;
+    const float rv = sqrt_rn(fmaxf(p.c, 1e-12f)) * kSigmaExtent;
     const float r = fmaxf(ru, rv);
     const bool keep = finite_cov && isfinite(ru) && isfinite(rv) && r >= min_radius &&
                       r <= max_radius && p.u > -ru && p.u < (float)width + ru && p.v > -rv &&

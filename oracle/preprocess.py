@@ -112,6 +112,13 @@ def view_directions(means: torch.Tensor, camera_pos: torch.Tensor) -> torch.Tens
     return d / torch.norm(d, dim=1, keepdim=True)
 
 
+def sqrt_rn(x: torch.Tensor) -> torch.Tensor:
+    """IEEE correctly rounded fp32 square root (torch's CPU float32 sqrt goes
+    through MKL VML and is not correctly rounded for large tensors; the float64
+    root rounded once to float32 is, since 53 >= 2*24 + 2)."""
+    return torch.sqrt(x.double()).float()
+
+
 def camera_position(world_to_camera: torch.Tensor) -> torch.Tensor:
     """-R^T t.  src/torch_rasterizer.py:60, src/cuda/wrapper.py:260."""
     return -world_to_camera[:3, :3].t() @ world_to_camera[:3, 3]
@@ -200,8 +207,8 @@ def project(means, scales, quaternions, opacities, world_to_camera, intrinsic, w
     A = c * inv_det
     B = -b * inv_det
     C = a * inv_det
-    ru = torch.sqrt(torch.clamp_min(a, 1e-12)) * SIGMA_EXTENT
-    rv = torch.sqrt(torch.clamp_min(c, 1e-12)) * SIGMA_EXTENT
+    ru = sqrt_rn(torch.clamp_min(a, 1e-12)) * SIGMA_EXTENT
+    rv = sqrt_rn(torch.clamp_min(c, 1e-12)) * SIGMA_EXTENT
     with torch.no_grad():
         r = torch.maximum(ru, rv)
         finite = torch.isfinite(a) & torch.isfinite(b) & torch.isfinite(c)

@@ -26,7 +26,8 @@ def _random_splats(n, width, height, seed, rmax=40.0):
     pts = np.stack([g.uniform(-30, width + 30, n), g.uniform(-30, height + 30, n)], 1).astype(np.float32)
     radii = g.uniform(0.5, rmax, (n, 2)).astype(np.float32)
     depths = g.uniform(0.2, 10.0, n).astype(np.float32)
-    depths[::5] = depths[3]  # many exact depth ties
+    if n > 3:
+        depths[::5] = depths[3]  # many exact depth ties
     mask = g.uniform(size=n) > 0.15
     return pts, radii, depths, mask
 

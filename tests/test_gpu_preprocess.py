@@ -120,3 +120,22 @@ def test_sh_forward_backward(gpu, sh_sigmoid):
                                                    d(mask), sh_sigmoid)
     for nm, a, b in zip(["means", "dc", "rest"], got, [t.grad for t in leaves]):
         assert helpers.rel_l2(a, b) <= 1e-4, nm
+
+
+def test_project_points_bitexact_headline(gpu):
+    """BASELINE config 3 at full size (1M Gaussians, 1920x1080, near 0.2): every
+    projection output bit-identical to the oracle."""
+    import bench
+
+    scene = bench.config3()
+    p, cam = scene["params"], scene["camera"]
+    scales, quats, opac = helpers.activated(p)
+    args = (cam["w2c"], cam["K"], cam["near"], FAR, MIN_O, MIN_R, MAX_R, cam["width"], cam["height"])
+    with torch.no_grad():
+        ref = preprocess.project_points(p["means"], scales, quats, opac, *args)
+    out = cr.project_points(p["means"].to(gpu), scales.to(gpu), quats.to(gpu), opac.to(gpu),
+                            args[0].to(gpu), args[1].to(gpu), *args[2:])
+    for nm, a, b in zip(["points_image", "depths", "cov_image", "cov_inv_image", "radii", "mask"],
+                        out, ref):
+        assert helpers.same(a, b), nm
+    assert int(ref[5].sum()) > 500_000
