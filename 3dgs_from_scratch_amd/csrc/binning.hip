@@ -5,8 +5,8 @@
 // in Gaussian order and stably sorts all 64 bits.  The same order -- (tile,
 // depth bits, Gaussian index) -- is produced here with far less sort traffic:
 //   1. a stable sort of the N per-Gaussian depth keys (32 bits, N entries),
-//   2. key emission in that depth order (tile id only, K entries),
-//   3. a stable sort of the K tile ids over ceil(log2(n_tiles)) bits.
+//   2. the (tile, Gaussian) entries of the Gaussians in that depth order,
+//   3. a stable sort of those K entries by tile id (ceil(log2(n_tiles)) bits).
 // A stable sort by tile of a sequence already ordered by (depth, index) is
 // ordered by (tile, depth, index).
 //
@@ -17,6 +17,12 @@
 //   downsweep stable local ranks from the same ballot matching, a scatter into
 //             LDS in digit order, and contiguous runs written to HBM.
 // No pass waits on another workgroup, so no launch can deadlock.
+//
+// The K entries of step 2 are never written unsorted: the first tile pass
+// generates each block's 4096 entries on the fly from the depth-ordered
+// Gaussians (per-block first Gaussian + a search in LDS), once to build the
+// histogram and once to scatter.  Tile ids are stored as 16-bit keys whenever
+// n_tiles <= 65536.
 
 #include "wave_ops.h"
 #include "preprocess_math.h"
@@ -24,15 +30,20 @@
 namespace gs {
 
 constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
-constexpr int kSortTile = kSortThreads * kSortItems;  // keys per workgroup per pass
 constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int kRadixMaxBits = 8;
 constexpr int kRadixMax = 1 << kRadixMaxBits;
+constexpr int kEmitItems = 16;  // entries per thread in the fused first tile pass
+constexpr int kEmitTile = kSortThreads * kEmitItems;
+constexpr int kDepthItems = 16;  // keys per thread in the depth sort (N-sized)
+constexpr int kTileItems = 16;  // keys per thread in later tile passes (K-sized)
 
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;
+constexpr int kDirectMaxBlocks = 256;  // passes with <= 256 blocks skip the histogram scan
+
+inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // ------------------------------------------------------------------ scan
 
@@ -54,28 +65,29 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const T *__re
     if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
-// Exclusive scan of kScanTile consecutive elements per workgroup, offset by
+// Exclusive scan of NT*ITEMS consecutive elements per workgroup, offset by
 // `offsets[blockIdx.x]` (or 0 when offsets is null).  In-place safe.  The last
 // workgroup writes the grand total to *total when total is not null.
-template <typename T>
-__global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(
-    const T *in, T *out, int64_t n, const T *__restrict__ offsets, T *__restrict__ total) {
-    __shared__ T tmp[kScanThreads / kWave + 1];
-    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
-    T v[kScanItems];
+template <typename T, int NT, int ITEMS>
+__global__ __launch_bounds__(NT) void scan_apply_kernel(const T *in, T *out, int64_t n,
+                                                        const T *__restrict__ offsets,
+                                                        T *__restrict__ total) {
+    __shared__ T tmp[NT / kWave + 1];
+    const int64_t base = (int64_t)blockIdx.x * (NT * ITEMS) + (int64_t)threadIdx.x * ITEMS;
+    T v[ITEMS];
     T acc = 0;
 #pragma unroll
-    for (int it = 0; it < kScanItems; ++it) {
+    for (int it = 0; it < ITEMS; ++it) {
         const int64_t i = base + it;
         v[it] = i < n ? in[i] : (T)0;
         acc += v[it];
     }
     T block_total;
-    T run = block_exclusive_scan<T, kScanThreads>(acc, tmp, block_total);
+    T run = block_exclusive_scan<T, NT>(acc, tmp, block_total);
     const T off = offsets ? offsets[blockIdx.x] : (T)0;
     run += off;
 #pragma unroll
-    for (int it = 0; it < kScanItems; ++it) {
+    for (int it = 0; it < ITEMS; ++it) {
         const int64_t i = base + it;
         if (i < n) out[i] = run;
         run += v[it];
@@ -89,35 +101,34 @@ size_t scan_workspace_bytes(int64_t n) {
     size_t bytes = 0;
     while (n > kScanTile) {
         const int64_t nb = (n + kScanTile - 1) / kScanTile;
-        bytes += ((nb * sizeof(T) + 255) / 256) * 256;
+        bytes += align256(nb * sizeof(T));
         n = nb;
     }
     return bytes;
 }
 
 // Exclusive scan of n elements (out may alias in).  Writes the total to
-// *total (device pointer) when not null.
+// *total (device pointer) when not null.  One launch up to kScanTile elements,
+// reduce / scan-of-sums / apply above.
 template <typename T>
 int scan_exclusive(const T *in, T *out, int64_t n, T *total, void *ws, hipStream_t stream) {
-    if (n <= 0) {
-        return total ? zero_bytes(total, sizeof(T), stream) : GS_OK;
-    }
+    if (n <= 0) return total ? zero_bytes(total, sizeof(T), stream) : GS_OK;
     const int64_t nb = (n + kScanTile - 1) / kScanTile;
     if (nb == 1) {
-        hipLaunchKernelGGL(scan_apply_kernel<T>, dim3(1), dim3(kScanThreads), 0, stream, in, out,
-                           n, (const T *)nullptr, total);
+        hipLaunchKernelGGL((scan_apply_kernel<T, kScanThreads, kScanItems>), dim3(1),
+                           dim3(kScanThreads), 0, stream, in, out, n, (const T *)nullptr, total);
         return launch_status();
     }
     T *sums = reinterpret_cast<T *>(ws);
-    void *ws_next = reinterpret_cast<char *>(ws) + ((nb * sizeof(T) + 255) / 256) * 256;
+    void *ws_next = reinterpret_cast<char *>(ws) + align256(nb * sizeof(T));
     hipLaunchKernelGGL(scan_reduce_kernel<T>, dim3(nb), dim3(kScanThreads), 0, stream, in, n,
                        sums);
     int st = launch_status();
     if (st) return st;
     st = scan_exclusive<T>(sums, sums, nb, (T *)nullptr, ws_next, stream);
     if (st) return st;
-    hipLaunchKernelGGL(scan_apply_kernel<T>, dim3(nb), dim3(kScanThreads), 0, stream, in, out, n,
-                       (const T *)sums, total);
+    hipLaunchKernelGGL((scan_apply_kernel<T, kScanThreads, kScanItems>), dim3(nb),
+                       dim3(kScanThreads), 0, stream, in, out, n, (const T *)sums, total);
     return launch_status();
 }
 
@@ -127,116 +138,186 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t key, int shift, uint32_t d
     return (key >> shift) & dmask;
 }
 
-// hist[d * nblocks + block] = number of keys of this block with digit d.
-__global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
-    const uint32_t *__restrict__ keys, int64_t n, int shift, int nbits, int nblocks,
-    uint32_t *__restrict__ hist) {
-    __shared__ uint32_t counts[kRadixMax];
-    const int radix = 1 << nbits;
-    const uint32_t dmask = (uint32_t)radix - 1u;
-    for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
-    __syncthreads();
-    const int wave = threadIdx.x / kWave;
-    const int lane = __lane_id();
-    const int64_t base = (int64_t)blockIdx.x * kSortTile + (int64_t)wave * (kSortTile / kSortWaves);
-    for (int it = 0; it < kSortItems; ++it) {
-        const int64_t i = base + it * kWave + lane;
-        const bool valid = i < n;
-        const uint32_t d = valid ? digit_of(keys[i], shift, dmask) : 0u;
-        const uint64_t active = __ballot(valid);
-        const uint64_t peers = match_digit(d, nbits, active);
-        if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&counts[d], (uint32_t)__popcll(peers));
-    }
-    __syncthreads();
-    for (int d = threadIdx.x; d < radix; d += kSortThreads)
-        hist[(int64_t)d * nblocks + blockIdx.x] = counts[d];
+struct SortLds {
+    uint32_t wave_count[kSortWaves][kRadixMax];
+    uint32_t global_start[kRadixMax];
+    uint32_t local_start[kRadixMax];
+    uint32_t skeys[kEmitTile];
+    uint32_t svals[kEmitTile];
+    uint32_t scan_tmp[kSortThreads / kWave + 1];
+};
+
+// Key slot `it` of this thread: index within the block = wave*(64*ITEMS) + it*64 + lane,
+// so one load instruction covers 64 consecutive keys and keys stay in index order
+// (slot-major inside a wave, wave-major across the block).
+template <int ITEMS>
+__device__ __forceinline__ int slot_index(int it) {
+    return (threadIdx.x / kWave) * (kWave * ITEMS) + it * kWave + (threadIdx.x % kWave);
 }
 
-// Stable scatter of one pass.  `offsets` is the exclusive scan of the
-// histogram table (digit-major), i.e. the first output slot of (digit, block).
-__global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
-    const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ vals_in,
-    uint32_t *__restrict__ keys_out, uint32_t *__restrict__ vals_out, int64_t n, int shift,
-    int nbits, int nblocks, const uint32_t *__restrict__ offsets) {
-    __shared__ uint32_t wave_count[kSortWaves][kRadixMax];
-    __shared__ uint32_t global_start[kRadixMax];
-    __shared__ uint32_t local_start[kRadixMax];
-    __shared__ uint32_t skeys[kSortTile];
-    __shared__ uint32_t svals[kSortTile];
-    __shared__ uint32_t scan_tmp[kSortThreads / kWave + 1];
+// Adds the block's digit counts (keys in registers) to `counts` (LDS, zeroed).
+template <int ITEMS>
+__device__ __forceinline__ void block_count_digits(const uint32_t (&k)[ITEMS],
+                                                   const bool (&valid)[ITEMS], int shift,
+                                                   int nbits, uint32_t *counts) {
+    const uint32_t dmask = (1u << nbits) - 1u;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+        const uint32_t d = digit_of(k[it], shift, dmask);
+        const uint64_t active = __ballot(valid[it]);
+        const uint64_t peers = match_digit(d, nbits, active);
+        if (valid[it] && (peers & lanemask_lt()) == 0)
+            atomicAdd(&counts[d], (uint32_t)__popcll(peers));
+    }
+}
 
+// Per-pass histogram tables.  Digit-major (d * nblocks + b) is scanned into
+// first output slots by scan_exclusive; block-major (b * radix + d) is summed
+// directly by every downsweep block when the pass has <= kDirectMaxBlocks blocks.
+template <bool DIRECT>
+__device__ __forceinline__ int64_t hist_index(int d, int b, int nblocks, int radix) {
+    return DIRECT ? (int64_t)b * radix + d : (int64_t)d * nblocks + b;
+}
+
+// Stable rank of the block's keys (registers) by digit, staged through LDS in
+// digit order and written to keys_out/vals_out.  `table` is the scanned
+// digit-major histogram (first output slot of (digit, block)) or, for DIRECT,
+// the raw block-major histogram from which the slots are summed here.  When
+// counts_out is set, counts_out[dst] = touched[value] is written as well.
+template <typename KeyT, int ITEMS, bool DIRECT>
+__device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
+                                              const uint32_t (&v)[ITEMS],
+                                              const bool (&valid)[ITEMS], int shift, int nbits,
+                                              int nblocks, const uint32_t *__restrict__ table,
+                                              KeyT *__restrict__ keys_out,
+                                              uint32_t *__restrict__ vals_out, int64_t n,
+                                              bool write_keys, SortLds &s,
+                                              const uint32_t *__restrict__ touched = nullptr,
+                                              uint64_t *__restrict__ counts_out = nullptr) {
     const int radix = 1 << nbits;
     const uint32_t dmask = (uint32_t)radix - 1u;
     const int wave = threadIdx.x / kWave;
-    const int lane = __lane_id();
     for (int d = threadIdx.x; d < radix; d += kSortThreads) {
 #pragma unroll
-        for (int w = 0; w < kSortWaves; ++w) wave_count[w][d] = 0;
-        global_start[d] = offsets[(int64_t)d * nblocks + blockIdx.x];
+        for (int w = 0; w < kSortWaves; ++w) s.wave_count[w][d] = 0;
+        if (!DIRECT) s.global_start[d] = table[hist_index<false>(d, blockIdx.x, nblocks, radix)];
+    }
+    if (DIRECT) {
+        uint32_t before = 0, total = 0;
+        if ((int)threadIdx.x < radix) {
+            // 16 independent loads in flight per round (the rows are L2 resident)
+            for (int b0 = 0; b0 < nblocks; b0 += 16) {
+                uint32_t h[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    h[q] = b0 + q < nblocks
+                               ? table[hist_index<true>(threadIdx.x, b0 + q, nblocks, radix)]
+                               : 0u;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    total += h[q];
+                    before += b0 + q < (int)blockIdx.x ? h[q] : 0u;
+                }
+            }
+        }
+        uint32_t grand;
+        const uint32_t base =
+            block_exclusive_scan<uint32_t, kSortThreads>(total, s.scan_tmp, grand);
+        if ((int)threadIdx.x < radix) s.global_start[threadIdx.x] = base + before;
     }
     __syncthreads();
-
-    const int64_t block_base = (int64_t)blockIdx.x * kSortTile;
-    const int64_t base = block_base + (int64_t)wave * (kSortTile / kSortWaves);
-    uint32_t k[kSortItems], v[kSortItems], rank[kSortItems];
+    uint32_t rank[ITEMS];
 #pragma unroll
-    for (int it = 0; it < kSortItems; ++it) {
-        const int64_t i = base + it * kWave + lane;
-        const bool valid = i < n;
-        k[it] = valid ? keys_in[i] : 0u;
-        v[it] = valid ? vals_in[i] : 0u;
-    }
-#pragma unroll
-    for (int it = 0; it < kSortItems; ++it) {
-        const int64_t i = base + it * kWave + lane;
-        const bool valid = i < n;
+    for (int it = 0; it < ITEMS; ++it) {
         const uint32_t d = digit_of(k[it], shift, dmask);
-        const uint64_t active = __ballot(valid);
+        const uint64_t active = __ballot(valid[it]);
         const uint64_t peers = match_digit(d, nbits, active);
-        const uint32_t before = valid ? wave_count[wave][d] : 0u;
+        const uint32_t before = valid[it] ? s.wave_count[wave][d] : 0u;
         const uint32_t r = (uint32_t)__popcll(peers & lanemask_lt());
-        if (valid && r == 0) wave_count[wave][d] = before + (uint32_t)__popcll(peers);
+        if (valid[it] && r == 0) s.wave_count[wave][d] = before + (uint32_t)__popcll(peers);
         rank[it] = before + r;
     }
     __syncthreads();
-
-    // per-digit exclusive prefix over the waves, then over the digits
     uint32_t digit_total = 0;
     if (threadIdx.x < radix) {
 #pragma unroll
         for (int w = 0; w < kSortWaves; ++w) {
-            const uint32_t c = wave_count[w][threadIdx.x];
-            wave_count[w][threadIdx.x] = digit_total;
+            const uint32_t c = s.wave_count[w][threadIdx.x];
+            s.wave_count[w][threadIdx.x] = digit_total;
             digit_total += c;
         }
     }
     uint32_t block_count;
-    const uint32_t ls = block_exclusive_scan<uint32_t, kSortThreads>(digit_total, scan_tmp,
-                                                                      block_count);
-    if (threadIdx.x < radix) local_start[threadIdx.x] = ls;
+    const uint32_t ls =
+        block_exclusive_scan<uint32_t, kSortThreads>(digit_total, s.scan_tmp, block_count);
+    if (threadIdx.x < radix) s.local_start[threadIdx.x] = ls;
     __syncthreads();
-
 #pragma unroll
-    for (int it = 0; it < kSortItems; ++it) {
-        const int64_t i = base + it * kWave + lane;
-        if (i < n) {
+    for (int it = 0; it < ITEMS; ++it) {
+        if (valid[it]) {
             const uint32_t d = digit_of(k[it], shift, dmask);
-            const uint32_t p = local_start[d] + wave_count[wave][d] + rank[it];
-            skeys[p] = k[it];
-            svals[p] = v[it];
+            const uint32_t p = s.local_start[d] + s.wave_count[wave][d] + rank[it];
+            s.skeys[p] = k[it];
+            s.svals[p] = v[it];
         }
     }
     __syncthreads();
-
     for (uint32_t p = threadIdx.x; p < block_count; p += kSortThreads) {
-        const uint32_t key = skeys[p];
+        const uint32_t key = s.skeys[p];
         const uint32_t d = digit_of(key, shift, dmask);
-        const uint32_t dst = global_start[d] + (p - local_start[d]);
+        const uint32_t dst = s.global_start[d] + (p - s.local_start[d]);
         if (dst < (uint64_t)n) {  // always true for a consistent histogram; guards the store
-            keys_out[dst] = key;
-            vals_out[dst] = svals[p];
+            const uint32_t val = s.svals[p];
+            if (write_keys) keys_out[dst] = (KeyT)key;
+            vals_out[dst] = val;
+            if (counts_out) counts_out[dst] = val < (uint64_t)n ? touched[val] : 0u;
         }
     }
+}
+
+// hist[d * nblocks + block] = number of keys of this block with digit d.
+template <typename KeyT, int ITEMS, bool DIRECT>
+__global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
+    const KeyT *__restrict__ keys, int64_t n, int shift, int nbits, int nblocks,
+    uint32_t *__restrict__ hist) {
+    __shared__ uint32_t counts[kRadixMax];
+    const int radix = 1 << nbits;
+    for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
+    const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
+    uint32_t k[ITEMS];
+    bool valid[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+        const int64_t i = base + slot_index<ITEMS>(it);
+        valid[it] = i < n;
+        k[it] = valid[it] ? (uint32_t)keys[i] : 0u;
+    }
+    __syncthreads();
+    block_count_digits<ITEMS>(k, valid, shift, nbits, counts);
+    __syncthreads();
+    for (int d = threadIdx.x; d < radix; d += kSortThreads)
+        hist[hist_index<DIRECT>(d, blockIdx.x, nblocks, radix)] = counts[d];
+}
+
+template <typename KeyT, int ITEMS, bool DIRECT>
+__global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
+    const KeyT *__restrict__ keys_in, const uint32_t *__restrict__ vals_in,
+    KeyT *__restrict__ keys_out, uint32_t *__restrict__ vals_out, int64_t n, int shift,
+    int nbits, int nblocks, const uint32_t *__restrict__ table, int write_keys,
+    const uint32_t *__restrict__ touched, uint64_t *__restrict__ counts_out) {
+    __shared__ SortLds s;
+    const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
+    uint32_t k[ITEMS], v[ITEMS];
+    bool valid[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+        const int64_t i = base + slot_index<ITEMS>(it);
+        valid[it] = i < n;
+        k[it] = valid[it] ? (uint32_t)keys_in[i] : 0u;
+        v[it] = valid[it] ? vals_in[i] : 0u;
+    }
+    block_scatter<KeyT, ITEMS, DIRECT>(k, v, valid, shift, nbits, nblocks, table, keys_out,
+                                       vals_out, n, write_keys != 0, s, touched, counts_out);
 }
 
 struct SortPlan {
@@ -244,130 +325,239 @@ struct SortPlan {
     int bits_per_pass;
 };
 
+// At least one pass (a 0-bit pass is a stable copy).
 inline SortPlan plan_sort(int total_bits) {
     SortPlan p;
-    if (total_bits <= 0) {
-        p.passes = 0;
-        p.bits_per_pass = 0;
-        return p;
-    }
-    p.passes = (total_bits + kRadixMaxBits - 1) / kRadixMaxBits;
-    p.bits_per_pass = (total_bits + p.passes - 1) / p.passes;
+    p.passes = total_bits <= 0 ? 1 : (total_bits + kRadixMaxBits - 1) / kRadixMaxBits;
+    p.bits_per_pass = total_bits <= 0 ? 0 : (total_bits + p.passes - 1) / p.passes;
     return p;
 }
 
-inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+inline int pass_bits(const SortPlan &plan, int total_bits, int p) {
+    const int rest = total_bits - p * plan.bits_per_pass;
+    return rest < plan.bits_per_pass ? (rest > 0 ? rest : 0) : plan.bits_per_pass;
+}
 
-size_t radix_sort_workspace_bytes(int64_t n) {
-    const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
-    const int64_t entries = nblocks * kRadixMax;
+template <int ITEMS>
+inline int64_t sort_blocks(int64_t n) {
+    return (n + kSortThreads * ITEMS - 1) / (kSortThreads * ITEMS);
+}
+
+template <int ITEMS>
+size_t radix_workspace_bytes(int64_t n) {
+    const int64_t entries = sort_blocks<ITEMS>(n) * kRadixMax;
     return align256(entries * sizeof(uint32_t)) + scan_workspace_bytes<uint32_t>(entries);
 }
 
-// Stable LSD sort of (keys, vals) by the low total_bits bits of the keys.
-// Ping-pongs between (ka, va) and (kb, vb); the result ends in (ka, va) when
-// the pass count is even and in (kb, vb) when odd (*result_in_b says which).
-int radix_sort_pairs(uint32_t *ka, uint32_t *va, uint32_t *kb, uint32_t *vb, int64_t n,
-                     int total_bits, void *ws, bool *result_in_b, hipStream_t stream) {
-    const SortPlan plan = plan_sort(total_bits);
-    *result_in_b = (plan.passes % 2) == 1;
-    if (n <= 1 || plan.passes == 0) {
-        if (*result_in_b && n > 0) {  // keep the documented result location
-            hipError_t e = hipMemcpyAsync(kb, ka, n * sizeof(uint32_t), hipMemcpyDeviceToDevice,
-                                          stream);
-            if (e == hipSuccess)
-                e = hipMemcpyAsync(vb, va, n * sizeof(uint32_t), hipMemcpyDeviceToDevice, stream);
-            if (e != hipSuccess) return (int)e;
-        }
-        return GS_OK;
-    }
-    const int nblocks = (int)((n + kSortTile - 1) / kSortTile);
+// One LSD pass from arrays.  With hist_ready the histogram table of this pass
+// (layout by `direct`) was already written into ws by the caller.  With
+// counts_out, counts_out[dst] = touched[value] is written next to the values.
+template <typename KeyT, int ITEMS>
+int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout, int64_t n,
+               int shift, int nbits, bool write_keys, void *ws, hipStream_t stream,
+               bool hist_ready = false, const uint32_t *touched = nullptr,
+               uint64_t *counts_out = nullptr) {
+    const int nblocks = (int)sort_blocks<ITEMS>(n);
+    const bool direct = nblocks <= kDirectMaxBlocks;
     const int64_t entries = (int64_t)nblocks * kRadixMax;
     uint32_t *hist = reinterpret_cast<uint32_t *>(ws);
     void *scan_ws = reinterpret_cast<char *>(ws) + align256(entries * sizeof(uint32_t));
-    for (int p = 0; p < plan.passes; ++p) {
-        const int shift = p * plan.bits_per_pass;
-        const int nbits = (total_bits - shift) < plan.bits_per_pass ? (total_bits - shift)
-                                                                     : plan.bits_per_pass;
-        const bool from_a = (p % 2) == 0;
-        uint32_t *kin = from_a ? ka : kb, *vin = from_a ? va : vb;
-        uint32_t *kout = from_a ? kb : ka, *vout = from_a ? vb : va;
-        hipLaunchKernelGGL(radix_upsweep_kernel, dim3(nblocks), dim3(kSortThreads), 0, stream,
-                           kin, n, shift, nbits, nblocks, hist);
-        int st = launch_status();
-        if (st) return st;
-        const int64_t used = (int64_t)nblocks << nbits;
-        st = scan_exclusive<uint32_t>(hist, hist, used, (uint32_t *)nullptr, scan_ws, stream);
-        if (st) return st;
-        hipLaunchKernelGGL(radix_downsweep_kernel, dim3(nblocks), dim3(kSortThreads), 0, stream,
-                           kin, vin, kout, vout, n, shift, nbits, nblocks, hist);
+    int st;
+    if (!hist_ready) {
+        if (direct)
+            hipLaunchKernelGGL((radix_upsweep_kernel<KeyT, ITEMS, true>), dim3(nblocks),
+                               dim3(kSortThreads), 0, stream, kin, n, shift, nbits, nblocks, hist);
+        else
+            hipLaunchKernelGGL((radix_upsweep_kernel<KeyT, ITEMS, false>), dim3(nblocks),
+                               dim3(kSortThreads), 0, stream, kin, n, shift, nbits, nblocks, hist);
         st = launch_status();
         if (st) return st;
     }
-    return GS_OK;
+    if (direct) {
+        hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, true>), dim3(nblocks),
+                           dim3(kSortThreads), 0, stream, kin, vin, kout, vout, n, shift, nbits,
+                           nblocks, hist, write_keys ? 1 : 0, touched, counts_out);
+        return launch_status();
+    }
+    st = scan_exclusive<uint32_t>(hist, hist, (int64_t)nblocks << nbits, (uint32_t *)nullptr,
+                                  scan_ws, stream);
+    if (st) return st;
+    hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, false>), dim3(nblocks),
+                       dim3(kSortThreads), 0, stream, kin, vin, kout, vout, n, shift, nbits,
+                       nblocks, hist, write_keys ? 1 : 0, touched, counts_out);
+    return launch_status();
 }
 
 // ------------------------------------------------------------- binning
 
-// tiles_touched and depth sort keys per Gaussian (src/cuda/kernel.cu:784-818).
-// Gaussians without tiles get the key 0xFFFFFFFF (sorted last; they emit nothing).
-__global__ __launch_bounds__(256) void count_tiles_kernel(
+// tiles_touched and depth sort keys per Gaussian (src/cuda/kernel.cu:784-818),
+// fused with the histogram of the first depth-sort pass.  Gaussians without
+// tiles get the key 0xFFFFFFFF (sorted last; they emit nothing).
+template <int ITEMS, bool DIRECT>
+__global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int64_t n, const float *__restrict__ points_image, const float *__restrict__ radii,
     const float *__restrict__ depths, const uint8_t *__restrict__ mask, int width, int height,
     int tile_size, uint32_t *__restrict__ touched, uint32_t *__restrict__ depth_keys,
-    uint32_t *__restrict__ ids) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    uint32_t cnt = 0;
-    if (mask[i]) {
-        TileRect r;
-        if (tile_rect(points_image[2 * i], points_image[2 * i + 1], radii[2 * i],
-                      radii[2 * i + 1], width, height, tile_size, r))
-            cnt = (uint32_t)((r.tx1 - r.tx0 + 1) * (r.ty1 - r.ty0 + 1));
+    uint32_t *__restrict__ ids, int nbits, int nblocks, uint32_t *__restrict__ hist) {
+    __shared__ uint32_t counts[kRadixMax];
+    const int radix = 1 << nbits;
+    for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
+    const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
+    uint32_t k[ITEMS];
+    bool valid[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+        const int64_t i = base + slot_index<ITEMS>(it);
+        valid[it] = i < n;
+        k[it] = 0u;
+        if (!valid[it]) continue;
+        uint32_t cnt = 0;
+        if (mask[i]) {
+            TileRect r;
+            if (tile_rect(points_image[2 * i], points_image[2 * i + 1], radii[2 * i],
+                          radii[2 * i + 1], width, height, tile_size, r))
+                cnt = (uint32_t)((r.tx1 - r.tx0 + 1) * (r.ty1 - r.ty0 + 1));
+        }
+        k[it] = cnt ? __float_as_uint(depths[i]) : 0xFFFFFFFFu;
+        touched[i] = cnt;
+        depth_keys[i] = k[it];
+        ids[i] = (uint32_t)i;
     }
-    touched[i] = cnt;
-    depth_keys[i] = cnt ? __float_as_uint(depths[i]) : 0xFFFFFFFFu;
-    ids[i] = (uint32_t)i;
+    __syncthreads();
+    block_count_digits<ITEMS>(k, valid, 0, nbits, counts);
+    __syncthreads();
+    for (int d = threadIdx.x; d < radix; d += kSortThreads)
+        hist[hist_index<DIRECT>(d, blockIdx.x, nblocks, radix)] = counts[d];
 }
 
-__global__ __launch_bounds__(256) void gather_counts_kernel(int64_t n,
-                                                            const uint32_t *__restrict__ order,
-                                                            const uint32_t *__restrict__ touched,
-                                                            uint64_t *__restrict__ counts) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const uint32_t g = order[i];
-    counts[i] = g < (uint64_t)n ? touched[g] : 0u;
-}
-
-// One thread per Gaussian in depth order; writes its tiles row-major.
-__global__ __launch_bounds__(256) void emit_keys_kernel(
-    int64_t n, int64_t k, const uint32_t *__restrict__ order, const uint64_t *__restrict__ offsets,
-    const uint32_t *__restrict__ touched, const float *__restrict__ points_image,
-    const float *__restrict__ radii, int width, int height, int tile_size, int tiles_x,
-    uint32_t *__restrict__ tile_keys, uint32_t *__restrict__ gauss_ids) {
+// block_first[b] = depth-order position of the Gaussian whose entries contain
+// entry b * kEmitTile (entries are laid out Gaussian after Gaussian), and
+// block_first[ceil(k / kEmitTile)] = the last Gaussian with entries.
+__global__ __launch_bounds__(256) void block_first_kernel(int64_t n, int64_t k,
+                                                          const uint32_t *__restrict__ order,
+                                                          const uint64_t *__restrict__ offsets,
+                                                          const uint32_t *__restrict__ touched,
+                                                          uint32_t *__restrict__ block_first) {
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= n) return;
     const uint32_t g = order[r];
-    if (g >= (uint64_t)n || touched[g] == 0) return;
-    TileRect rect;
-    if (!tile_rect(points_image[2 * g], points_image[2 * g + 1], radii[2 * g], radii[2 * g + 1],
-                   width, height, tile_size, rect))
-        return;
-    uint64_t o = offsets[r];
-    const uint64_t o_end = o + touched[g];
-    for (int ty = rect.ty0; ty <= rect.ty1; ++ty)
-        for (int tx = rect.tx0; tx <= rect.tx1; ++tx) {
-            if (o >= o_end || o >= (uint64_t)k) return;  // guards the stores
-            tile_keys[o] = (uint32_t)(ty * tiles_x + tx);
-            gauss_ids[o] = g;
-            ++o;
+    const uint64_t c = g < (uint64_t)n ? touched[g] : 0u;
+    if (c == 0) return;
+    const uint64_t off = offsets[r];
+    const uint64_t end = off + c < (uint64_t)k ? off + c : (uint64_t)k;
+    for (uint64_t b = (off + kEmitTile - 1) / kEmitTile; b * kEmitTile < end; ++b)
+        block_first[b] = (uint32_t)r;
+    if (off < (uint64_t)k && end == (uint64_t)k)
+        block_first[((uint64_t)k + kEmitTile - 1) / kEmitTile] = (uint32_t)r;
+}
+
+struct EmitArgs {
+    const uint32_t *order;    // Gaussians in depth order
+    const uint64_t *offsets;  // first entry of each depth-ordered Gaussian
+    const uint32_t *touched;  // tiles per Gaussian (by Gaussian id)
+    const uint32_t *block_first;
+    const float *points;
+    const float *radii;
+    int64_t n, k;
+    int width, height, tile_size, tiles_x;
+};
+
+constexpr int kEmitGroup = 1024;  // depth-ordered Gaussians staged per round (4 per thread)
+
+struct EmitLds {
+    int32_t off[kEmitGroup];  // first entry relative to the block start (clamped)
+    int32_t end[kEmitGroup];
+    uint32_t gid[kEmitGroup];
+    uint32_t origin[kEmitGroup];  // tx0 | ty0 << 16 of the tile rectangle
+    uint16_t nx[kEmitGroup];      // rectangle width in tiles
+};
+
+// Writes the entries [b*kEmitTile, (b+1)*kEmitTile) of the depth-ordered
+// (tile, Gaussian) sequence -- entry o of Gaussian r is its o-th tile in
+// row-major order -- to keys_out / vals_out, and the block's histogram of the
+// low `nbits` tile bits (the first sort pass) to hist.  The block's Gaussians
+// block_first[b] .. block_first[b + 1] are staged up to 1024 per round; each
+// wave then writes the entries of every 4th staged Gaussian lane-parallel
+// (coalesced runs) and counts digits with LDS atomics.
+template <typename KeyT, bool DIRECT>
+__global__ __launch_bounds__(kSortThreads) void emit_entries_kernel(
+    EmitArgs a, int nbits, int nblocks, uint32_t *__restrict__ hist, KeyT *__restrict__ keys_out,
+    uint32_t *__restrict__ vals_out) {
+    __shared__ EmitLds e;
+    __shared__ uint32_t counts[kRadixMax];
+    const int radix = 1 << nbits;
+    const uint32_t dmask = (uint32_t)radix - 1u;
+    for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
+    const int64_t block_base = (int64_t)blockIdx.x * kEmitTile;
+    const int64_t left = a.k - block_base;
+    const int count = (int)(left < kEmitTile ? left : kEmitTile);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    KeyT *kout = keys_out + block_base;
+    uint32_t *vout = vals_out + block_base;
+    int64_t r0 = a.block_first[blockIdx.x];
+    const int64_t r_last = a.block_first[blockIdx.x + 1];  // inclusive
+    for (;;) {
+#pragma unroll
+        for (int q = 0; q < kEmitGroup / kSortThreads; ++q) {
+            const int j = threadIdx.x + q * kSortThreads;
+            const int64_t r = r0 + j;
+            int32_t off = 0x7fffffff, end = 0x7fffffff;
+            if (r <= r_last && r < a.n) {
+                const uint32_t g = a.order[r];
+                const uint32_t c = g < (uint64_t)a.n ? a.touched[g] : 0u;
+                int64_t o = (int64_t)a.offsets[r] - block_base;
+                int64_t oe = o + (int64_t)c;
+                o = o > 0x3fffffff ? 0x3fffffff : o;
+                oe = oe > 0x3fffffff ? 0x3fffffff : oe;
+                off = (int32_t)o;
+                end = (int32_t)oe;
+                TileRect rect{0, 0, 0, 0};
+                if (c > 0)
+                    tile_rect(a.points[2 * g], a.points[2 * g + 1], a.radii[2 * g],
+                              a.radii[2 * g + 1], a.width, a.height, a.tile_size, rect);
+                e.gid[j] = g;
+                e.origin[j] = (uint32_t)rect.tx0 | ((uint32_t)rect.ty0 << 16);
+                e.nx[j] = (uint16_t)(rect.tx1 - rect.tx0 + 1);
+            }
+            e.off[j] = off;
+            e.end[j] = end;
         }
+        __syncthreads();
+        for (int j = wave; j < kEmitGroup; j += kSortWaves) {
+            const int32_t goff = e.off[j];
+            if (goff >= count) break;  // later Gaussians start even later
+            const int32_t lo = goff > 0 ? goff : 0;
+            const int32_t hi = e.end[j] < count ? e.end[j] : count;
+            const int32_t nx = e.nx[j] > 0 ? (int32_t)e.nx[j] : 1;
+            const uint32_t origin = e.origin[j];
+            const int32_t tx0 = (int32_t)(origin & 0xffffu), ty0 = (int32_t)(origin >> 16);
+            const uint32_t g = e.gid[j];
+            // row = floor((local + 0.5) / nx): the true quotient is at least 0.5/nx away
+            // from an integer and the float error is below that for local < 2^22
+            const float rcp = 1.0f / (float)nx;
+            for (int32_t idx = lo + lane; idx < hi; idx += kWave) {
+                const int32_t local = idx - goff;
+                const int32_t row = (int32_t)(((float)local + 0.5f) * rcp);
+                const int32_t col = local - row * nx;
+                const uint32_t t = (uint32_t)((ty0 + row) * a.tiles_x + tx0 + col);
+                kout[idx] = (KeyT)t;
+                vout[idx] = g;
+                atomicAdd(&counts[t & dmask], 1u);
+            }
+        }
+        const bool more = r0 + kEmitGroup <= r_last;
+        __syncthreads();
+        if (!more) break;
+        r0 += kEmitGroup;
+    }
+    for (int d = threadIdx.x; d < radix; d += kSortThreads)
+        hist[hist_index<DIRECT>(d, blockIdx.x, nblocks, radix)] = counts[d];
 }
 
 // indexing_offset[t] = first sorted position whose tile is >= t.
+template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_ranges_kernel(int n_tiles,
-                                                          const uint32_t *__restrict__ tiles,
+                                                          const KeyT *__restrict__ tiles,
                                                           int64_t k,
                                                           int32_t *__restrict__ offsets) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -375,7 +565,7 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(int n_tiles,
     int64_t lo = 0, hi = k;
     while (lo < hi) {
         const int64_t mid = (lo + hi) >> 1;
-        if (tiles[mid] < (uint32_t)t)
+        if ((uint32_t)tiles[mid] < (uint32_t)t)
             lo = mid + 1;
         else
             hi = mid;
@@ -383,8 +573,9 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(int n_tiles,
     offsets[t] = (int32_t)lo;
 }
 
+template <typename KeyT>
 __global__ __launch_bounds__(256) void sorted_keys_kernel(int64_t k, int64_t n,
-                                                          const uint32_t *__restrict__ tiles,
+                                                          const KeyT *__restrict__ tiles,
                                                           const int32_t *__restrict__ ids,
                                                           const float *__restrict__ depths,
                                                           uint64_t *__restrict__ keys) {
@@ -392,7 +583,7 @@ __global__ __launch_bounds__(256) void sorted_keys_kernel(int64_t k, int64_t n,
     if (i >= k) return;
     const int32_t g = ids[i];
     const uint32_t bits = (g >= 0 && g < n) ? __float_as_uint(depths[g]) : 0u;
-    keys[i] = ((uint64_t)tiles[i] << 32) | (uint64_t)bits;
+    keys[i] = ((uint64_t)(uint32_t)tiles[i] << 32) | (uint64_t)bits;
 }
 
 __global__ __launch_bounds__(256) void copy_u32_to_i32_kernel(int64_t n,
@@ -433,25 +624,34 @@ inline CountWs carve_count(void *base, int64_t n) {
     w.dvals_b = c.take<uint32_t>(n);
     w.counts = c.take<uint64_t>(n);
     w.offsets = c.take<uint64_t>(n + 1);
-    w.sort_ws = c.take<char>((int64_t)radix_sort_workspace_bytes(n));
+    w.sort_ws = c.take<char>((int64_t)radix_workspace_bytes<kDepthItems>(n));
     w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint64_t>(n));
     w.bytes = align256(c.off);
     return w;
 }
 
+// The depth sort is 4 passes of 8 bits, so its result ends in the (a) buffers.
+constexpr int kDepthBits = 32;
+
+inline bool use_u16_keys(int tile_bits) { return tile_bits <= 16; }
+
 struct SortWs {
-    uint32_t *tkeys_a, *tkeys_b, *tvals_tmp;
-    void *sort_ws;
+    void *keys_a, *keys_b;  // tile keys (u16 or u32)
+    uint32_t *vals_tmp;
+    uint32_t *block_first;
+    void *pass_ws;  // histogram table + scan scratch of each pass
     size_t bytes;
 };
 
-inline SortWs carve_sort(void *base, int64_t k) {
+inline SortWs carve_sort(void *base, int64_t k, int tile_bits) {
     Carve c{reinterpret_cast<char *>(base)};
     SortWs w;
-    w.tkeys_a = c.take<uint32_t>(k);
-    w.tkeys_b = c.take<uint32_t>(k);
-    w.tvals_tmp = c.take<uint32_t>(k);
-    w.sort_ws = c.take<char>((int64_t)radix_sort_workspace_bytes(k));
+    const int64_t kb = use_u16_keys(tile_bits) ? 2 : 4;
+    w.keys_a = c.take<char>(k * kb);
+    w.keys_b = c.take<char>(k * kb);
+    w.vals_tmp = c.take<uint32_t>(k);
+    w.block_first = c.take<uint32_t>((k + kEmitTile - 1) / kEmitTile + 1);
+    w.pass_ws = c.take<char>((int64_t)radix_workspace_bytes<kTileItems>(k));
     w.bytes = align256(c.off);
     return w;
 }
@@ -460,6 +660,58 @@ inline int bits_for(int64_t max_value) {
     int b = 0;
     while (b < 63 && (max_value >> b) != 0) ++b;
     return b;
+}
+
+// Entry generation (with the first pass's histogram), then the sort passes;
+// the last pass writes the caller's gaussian_ids_sorted and the sorted keys
+// end in keys_b.
+template <typename KeyT>
+int tile_sort(const EmitArgs &a, const SortWs &w, int tile_bits, int n_tiles,
+              int32_t *indexing_offset, int32_t *ids_out, uint64_t *sorted_keys,
+              const float *depths, hipStream_t stream) {
+    static_assert(kEmitTile == kSortThreads * kTileItems, "entry blocks must be sort blocks");
+    const SortPlan plan = plan_sort(tile_bits);
+    const int P = plan.passes;
+    const int nblocks = (int)sort_blocks<kTileItems>(a.k);
+    const bool direct = nblocks <= kDirectMaxBlocks;
+    KeyT *ka = reinterpret_cast<KeyT *>(w.keys_a), *kb = reinterpret_cast<KeyT *>(w.keys_b);
+    uint32_t *out = reinterpret_cast<uint32_t *>(ids_out);
+    // pass p writes (kb, out) when P-1-p is even, (ka, vals_tmp) otherwise; the
+    // entries (pass -1) go to the other set than pass 0
+    auto keys_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? kb : ka; };
+    auto vals_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? out : w.vals_tmp; };
+
+    hipLaunchKernelGGL(block_first_kernel, dim3(ceil_div(a.n, 256)), dim3(256), 0, stream, a.n,
+                       a.k, a.order, a.offsets, a.touched, w.block_first);
+    int st = launch_status();
+    if (st) return st;
+    uint32_t *hist = reinterpret_cast<uint32_t *>(w.pass_ws);
+    const int nb0 = pass_bits(plan, tile_bits, 0);
+    if (direct)
+        hipLaunchKernelGGL((emit_entries_kernel<KeyT, true>), dim3(nblocks), dim3(kSortThreads), 0,
+                           stream, a, nb0, nblocks, hist, keys_for(-1), vals_for(-1));
+    else
+        hipLaunchKernelGGL((emit_entries_kernel<KeyT, false>), dim3(nblocks), dim3(kSortThreads),
+                           0, stream, a, nb0, nblocks, hist, keys_for(-1), vals_for(-1));
+    st = launch_status();
+    if (st) return st;
+    for (int p = 0; p < P; ++p) {
+        st = radix_pass<KeyT, kTileItems>(keys_for(p - 1), vals_for(p - 1), keys_for(p),
+                                          vals_for(p), a.k, p * plan.bits_per_pass,
+                                          pass_bits(plan, tile_bits, p), true, w.pass_ws, stream,
+                                          p == 0);
+        if (st) return st;
+    }
+    hipLaunchKernelGGL(tile_ranges_kernel<KeyT>, dim3(ceil_div(n_tiles, 256)), dim3(256), 0,
+                       stream, n_tiles, kb, a.k, indexing_offset);
+    st = launch_status();
+    if (st) return st;
+    if (sorted_keys) {
+        hipLaunchKernelGGL(sorted_keys_kernel<KeyT>, dim3(ceil_div(a.k, 256)), dim3(256), 0,
+                           stream, a.k, a.n, kb, ids_out, depths, sorted_keys);
+        st = launch_status();
+    }
+    return st;
 }
 
 }  // namespace gs
@@ -481,34 +733,52 @@ extern "C" int gs_bin_count(const float *points_image, const float *radii, const
     if (n > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;  // Gaussian ids are int32
     const CountWs w = carve_count(workspace, n);
     if (n > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
-    if (n == 0) {
-        return zero_bytes(total_keys, sizeof(int64_t), stream);
-    }
+    if (n == 0) return zero_bytes(total_keys, sizeof(int64_t), stream);
     if (!points_image || !radii || !depths || !mask) return GS_ERR_INVALID_ARGUMENT;
-    const int grid = ceil_div(n, 256);
-    hipLaunchKernelGGL(count_tiles_kernel, dim3(grid), dim3(256), 0, stream, n, points_image,
-                       radii, depths, mask, width, height, tile_size, w.touched, w.dkeys_a,
-                       w.dvals_a);
+    const SortPlan plan = plan_sort(kDepthBits);
+    const int nblocks = (int)sort_blocks<kDepthItems>(n);
+    const int nb0 = pass_bits(plan, kDepthBits, 0);
+    uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
+    if (nblocks <= kDirectMaxBlocks)
+        hipLaunchKernelGGL((count_tiles_kernel<kDepthItems, true>), dim3(nblocks),
+                           dim3(kSortThreads), 0, stream, n, points_image, radii, depths, mask,
+                           width, height, tile_size, w.touched, w.dkeys_a, w.dvals_a, nb0,
+                           nblocks, hist);
+    else
+        hipLaunchKernelGGL((count_tiles_kernel<kDepthItems, false>), dim3(nblocks),
+                           dim3(kSortThreads), 0, stream, n, points_image, radii, depths, mask,
+                           width, height, tile_size, w.touched, w.dkeys_a, w.dvals_a, nb0,
+                           nblocks, hist);
     int st = launch_status();
     if (st) return st;
-    bool in_b = false;
-    st = radix_sort_pairs(w.dkeys_a, w.dvals_a, w.dkeys_b, w.dvals_b, n, 32, w.sort_ws, &in_b,
-                          stream);
-    if (st) return st;
-    const uint32_t *order = in_b ? w.dvals_b : w.dvals_a;
-    hipLaunchKernelGGL(gather_counts_kernel, dim3(grid), dim3(256), 0, stream, n, order,
-                       w.touched, w.counts);
-    st = launch_status();
-    if (st) return st;
+    // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes no
+    // keys but the tile counts in depth order
+    for (int p = 0; p < plan.passes; ++p) {
+        const bool from_a = (p % 2) == 0;
+        const bool last = p + 1 == plan.passes;
+        st = radix_pass<uint32_t, kDepthItems>(
+            from_a ? w.dkeys_a : w.dkeys_b, from_a ? w.dvals_a : w.dvals_b,
+            from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, n,
+            p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream,
+            p == 0, last ? w.touched : nullptr, last ? w.counts : nullptr);
+        if (st) return st;
+    }
     return scan_exclusive<uint64_t>(w.counts, w.offsets, n,
                                     reinterpret_cast<uint64_t *>(total_keys), w.scan_ws, stream);
 }
 
+static int tile_bits_of(int32_t width, int32_t height, int32_t tile_size, int *n_tiles) {
+    const int64_t tx = (width + tile_size - 1) / tile_size;
+    const int64_t ty = (height + tile_size - 1) / tile_size;
+    if (tx * ty > 0x7fffffffLL) return -1;
+    *n_tiles = (int)(tx * ty);
+    return bits_for((int64_t)*n_tiles - 1);
+}
+
 extern "C" int gs_bin_sort_workspace_size(int64_t n, int64_t k, int32_t n_tiles, size_t *bytes) {
     (void)n;
-    (void)n_tiles;
-    if (k < 0 || !bytes) return GS_ERR_INVALID_ARGUMENT;
-    *bytes = carve_sort(nullptr, k).bytes;
+    if (k < 0 || n_tiles < 0 || !bytes) return GS_ERR_INVALID_ARGUMENT;
+    *bytes = carve_sort(nullptr, k, bits_for((int64_t)n_tiles - 1)).bytes;
     return GS_OK;
 }
 
@@ -521,14 +791,14 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
     if (n < 0 || k < 0 || width <= 0 || height <= 0 || tile_size <= 0)
         return GS_ERR_INVALID_ARGUMENT;
     if (k > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
-    const int tiles_x = (width + tile_size - 1) / tile_size;
-    const int tiles_y = (height + tile_size - 1) / tile_size;
-    const int64_t n_tiles64 = (int64_t)tiles_x * tiles_y;
-    if (n_tiles64 > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;
-    const int n_tiles = (int)n_tiles64;
+    int n_tiles = 0;
+    const int tile_bits = tile_bits_of(width, height, tile_size, &n_tiles);
+    if (tile_bits < 0) return GS_ERR_INVALID_ARGUMENT;
     if (!indexing_offset) return GS_ERR_INVALID_ARGUMENT;
+    if ((width + tile_size - 1) / tile_size > 65535 || (height + tile_size - 1) / tile_size > 65535)
+        return GS_ERR_UNSUPPORTED;  // tile rectangles are staged with 16-bit coordinates
     const CountWs cw = carve_count(const_cast<void *>(count_workspace), n);
-    const SortWs w = carve_sort(workspace, k);
+    const SortWs w = carve_sort(workspace, k, tile_bits);
     if (k > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
     if (n > 0 && !count_workspace) return GS_ERR_INVALID_ARGUMENT;
     if (tiles_touched && n > 0) {
@@ -537,39 +807,25 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         int st = launch_status();
         if (st) return st;
     }
-    if (k == 0) {
-        return zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)n_tiles, stream);
-    }
-    if (!points_image || !radii || !gaussian_ids_sorted || (sorted_keys && !depths))
+    if (k == 0) return zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)n_tiles, stream);
+    if (!points_image || !radii || !gaussian_ids_sorted || (sorted_keys && !depths) || n == 0)
         return GS_ERR_INVALID_ARGUMENT;
-
-    const int tile_bits = bits_for((int64_t)n_tiles - 1);
-    const SortPlan plan = plan_sort(tile_bits);
-    // Values ping-pong between the caller's output and a workspace buffer so
-    // that the last pass lands in the caller's output.
-    uint32_t *out_vals = reinterpret_cast<uint32_t *>(gaussian_ids_sorted);
-    uint32_t *va = (plan.passes % 2 == 0) ? out_vals : w.tvals_tmp;
-    uint32_t *vb = (plan.passes % 2 == 0) ? w.tvals_tmp : out_vals;
-
-    // order of Gaussians by depth: result location of the count phase's sort
-    const uint32_t *order = (plan_sort(32).passes % 2 == 1) ? cw.dvals_b : cw.dvals_a;
-    hipLaunchKernelGGL(emit_keys_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream, n, k, order,
-                       cw.offsets, cw.touched, points_image, radii, width, height, tile_size,
-                       tiles_x, w.tkeys_a, va);
-    int st = launch_status();
-    if (st) return st;
-    bool in_b = false;
-    st = radix_sort_pairs(w.tkeys_a, va, w.tkeys_b, vb, k, tile_bits, w.sort_ws, &in_b, stream);
-    if (st) return st;
-    const uint32_t *sorted_tiles = in_b ? w.tkeys_b : w.tkeys_a;
-    hipLaunchKernelGGL(tile_ranges_kernel, dim3(ceil_div(n_tiles, 256)), dim3(256), 0, stream,
-                       n_tiles, sorted_tiles, k, indexing_offset);
-    st = launch_status();
-    if (st) return st;
-    if (sorted_keys) {
-        hipLaunchKernelGGL(sorted_keys_kernel, dim3(ceil_div(k, 256)), dim3(256), 0, stream, k, n,
-                           sorted_tiles, gaussian_ids_sorted, depths, sorted_keys);
-        st = launch_status();
-    }
-    return st;
+    EmitArgs a;
+    a.order = cw.dvals_a;  // depth order (even number of depth passes)
+    a.offsets = cw.offsets;
+    a.touched = cw.touched;
+    a.block_first = w.block_first;
+    a.points = points_image;
+    a.radii = radii;
+    a.n = n;
+    a.k = k;
+    a.width = width;
+    a.height = height;
+    a.tile_size = tile_size;
+    a.tiles_x = (width + tile_size - 1) / tile_size;
+    if (use_u16_keys(tile_bits))
+        return tile_sort<uint16_t>(a, w, tile_bits, n_tiles, indexing_offset, gaussian_ids_sorted,
+                                   sorted_keys, depths, stream);
+    return tile_sort<uint32_t>(a, w, tile_bits, n_tiles, indexing_offset, gaussian_ids_sorted,
+                               sorted_keys, depths, stream);
 }

@@ -59,7 +59,10 @@ def test_workspace_queries(lib):
     small = sz.value
     assert lib.gs_bin_count_workspace_size(1_000_000, ctypes.byref(sz)) == 0
     assert sz.value >= 1_000_000 * 36 and sz.value > small
+    # two 16-bit key buffers + one 32-bit id buffer per entry while tile ids fit 16 bits
     assert lib.gs_bin_sort_workspace_size(1000, 20_000_000, 8160, ctypes.byref(sz)) == 0
+    assert sz.value >= 20_000_000 * 8
+    assert lib.gs_bin_sort_workspace_size(1000, 20_000_000, 70_000, ctypes.byref(sz)) == 0
     assert sz.value >= 20_000_000 * 12
     assert lib.gs_bin_count_workspace_size(-1, ctypes.byref(sz)) == -1
 
