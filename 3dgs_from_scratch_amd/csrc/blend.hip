@@ -464,6 +464,45 @@ __global__ void blend_backward_generic_kernel(
     }
 }
 
+// Work of the reference blend loop (src/cuda/kernel.cu:954-982) for the
+// roofline: per pixel, the list entries visited until the transmittance test
+// stops it (`visited`, including entries culled by the chi-square or alpha
+// test) and the entries that were composited (`composited`).  One thread per
+// pixel; totals are added to the two counters.
+__global__ void blend_work_kernel(const int32_t *__restrict__ offsets,
+                                  const int32_t *__restrict__ ids, int n_tiles, int64_t k,
+                                  int64_t n, const float *__restrict__ points,
+                                  const float *__restrict__ conics,
+                                  const float *__restrict__ opac, int tiles_x, int width,
+                                  int height, int ts, float alpha_thr, float T_thr, float chi,
+                                  unsigned long long *__restrict__ visited,
+                                  unsigned long long *__restrict__ composited) {
+    const int tile = blockIdx.x;
+    const int px = (tile % tiles_x) * ts + (int)threadIdx.x % ts;
+    const int py = (tile / tiles_x) * ts + (int)threadIdx.x / ts;
+    unsigned long long v = 0, c = 0;
+    if (px < width && py < height && 1.0f >= T_thr) {
+        const TileSpan span = tile_span(offsets, n_tiles, k, tile);
+        float T = 1.0f;
+        for (int32_t i = span.start; i < span.end; ++i) {
+            ++v;
+            const int g = ids[i];
+            if (g < 0 || (int64_t)g >= n) continue;
+            const float du = (float)px - points[2 * g], dv = (float)py - points[2 * g + 1];
+            const float B = conics[3 * g + 1];
+            const float E = conic_exponent(conics[3 * g], B + B, conics[3 * g + 2], du, dv);
+            if (!(E < chi)) continue;
+            const float alpha = __expf(-0.5f * E) * opac[g];
+            if (alpha < alpha_thr) continue;
+            ++c;
+            T = T * ((1.0f - alpha) + kTransmittanceEps);
+            if (T < T_thr) break;
+        }
+    }
+    if (v) atomicAdd(visited, v);
+    if (c) atomicAdd(composited, c);
+}
+
 }  // namespace gs
 
 using namespace gs;
@@ -528,13 +567,14 @@ extern "C" int gs_rasterize_backward(
     const float *cov_inv_image, const float *opacities, const float *colors, int64_t n,
     int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
     float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
-    float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, hipStream_t stream) {
+    float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
+    hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size);
     if (st) return st;
     if (n > 0 && (!grad_points_image || !grad_cov_inv_image || !grad_opacities || !grad_colors))
         return GS_ERR_INVALID_ARGUMENT;
-    if (n > 0) {
+    if (n > 0 && !accumulate) {
         st = zero_bytes(grad_points_image, (size_t)n * 2 * sizeof(float), stream);
         if (!st) st = zero_bytes(grad_cov_inv_image, (size_t)n * 3 * sizeof(float), stream);
         if (!st) st = zero_bytes(grad_opacities, (size_t)n * sizeof(float), stream);
@@ -559,5 +599,30 @@ extern "C" int gs_rasterize_backward(
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
                            grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors);
     }
+    return launch_status();
+}
+
+extern "C" int gs_rasterize_work(const int32_t *indexing_offset,
+                                 const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k,
+                                 const float *points_image, const float *cov_inv_image,
+                                 const float *opacities, int64_t n, int32_t width, int32_t height,
+                                 int32_t tile_size, float alpha_threshold,
+                                 float transmittance_threshold, float chi_squared_threshold,
+                                 uint64_t *visited, uint64_t *composited, hipStream_t stream) {
+    int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
+                              tile_size);
+    if (st) return st;
+    if (!visited || !composited) return GS_ERR_INVALID_ARGUMENT;
+    st = zero_bytes(visited, sizeof(uint64_t), stream);
+    if (!st) st = zero_bytes(composited, sizeof(uint64_t), stream);
+    if (st || n_tiles == 0 || k == 0) return st;
+    if (!points_image || !cov_inv_image || !opacities) return GS_ERR_INVALID_ARGUMENT;
+    const int tiles_x = (width + tile_size - 1) / tile_size;
+    hipLaunchKernelGGL(blend_work_kernel, dim3(n_tiles), dim3(tile_size * tile_size), 0, stream,
+                       indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
+                       cov_inv_image, opacities, tiles_x, width, height, tile_size,
+                       alpha_threshold, transmittance_threshold, chi_squared_threshold,
+                       reinterpret_cast<unsigned long long *>(visited),
+                       reinterpret_cast<unsigned long long *>(composited));
     return launch_status();
 }

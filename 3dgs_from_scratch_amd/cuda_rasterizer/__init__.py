@@ -39,6 +39,7 @@ __all__ = [
     "compute_tile_intersection_debug",
     "rasterize",
     "rasterize_backward",
+    "rasterize_work",
     "RasterizerError",
 ]
 
@@ -388,10 +389,11 @@ def rasterize_backward(
     img = None
     if rendered_image is not None:
         img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
-    g_pts = torch.empty((n, 2), dtype=f32, device=dev)
-    g_conic = torch.empty((n, 3), dtype=f32, device=dev)
-    g_opac = torch.empty((n,), dtype=f32, device=dev)
-    g_col = torch.empty((n, 3), dtype=f32, device=dev)
+    # zeroed here so that the library call (and its timing events) is the blend kernel alone
+    g_pts = torch.zeros((n, 2), dtype=f32, device=dev)
+    g_conic = torch.zeros((n, 3), dtype=f32, device=dev)
+    g_opac = torch.zeros((n,), dtype=f32, device=dev)
+    g_col = torch.zeros((n, 3), dtype=f32, device=dev)
     with torch.cuda.device(dev):
         ev = _lib.timer.record("rasterize_backward", dev)
         _lib.check(
@@ -400,9 +402,33 @@ def rasterize_backward(
                 _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, int(tile_size),
                 float(alpha_threshold), float(transmittance_threshold),
                 float(chi_squared_threshold), _ptr(g_pts), _ptr(g_conic), _ptr(g_opac),
-                _ptr(g_col), _stream(dev),
+                _ptr(g_col), 1, _stream(dev),
             ),
             "rasterize_backward",
         )
         _lib.timer.stop(ev, dev)
     return g_pts, g_conic, g_opac, g_col
+
+
+def rasterize_work(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities,
+                   width, height, tile_size, alpha_threshold, transmittance_threshold,
+                   chi_squared_threshold):
+    """Work of the reference blend loop for these inputs (measurement helper):
+    returns (visited, composited) -- (pixel, list entry) pairs walked before each
+    pixel's transmittance test stopped it, and pairs actually blended."""
+    colors = torch.zeros((points_image.shape[0], 3), dtype=torch.float32, device=points_image.device)
+    dev, n, off, ids, pts, conic, opac, _ = _blend_inputs(
+        indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
+    counters = torch.empty((2,), dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(
+            _lib.load().gs_rasterize_work(
+                _ptr(off), _ptr(ids), off.shape[0], ids.shape[0], _ptr(pts), _ptr(conic),
+                _ptr(opac), n, int(width), int(height), int(tile_size), float(alpha_threshold),
+                float(transmittance_threshold), float(chi_squared_threshold), _ptr(counters),
+                counters.data_ptr() + 8, _stream(dev),
+            ),
+            "rasterize_work",
+        )
+    visited, composited = counters.tolist()
+    return visited, composited

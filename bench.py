@@ -196,63 +196,140 @@ def run_gpu(scene: dict, steps: int, warmup: int) -> dict:
     ms = (t1 - t0) * 1e3 / steps
 
     # workload statistics of one step
-    from cuda_rasterizer import compute_tile_intersection, project_points
+    from cuda_rasterizer import compute_tile_intersection, project_points, rasterize_work
     with torch.no_grad():
         scales, quats, opac = activated(leaves)
-        pts, depths, _, _, radii, mask = project_points(
+        pts, depths, _, conic, radii, mask = project_points(
             leaves["means"], scales, quats, opac, cam["w2c"], cam["K"], cam["near"], 100.0,
             1 / 255, 0.5, 128.0, cam["width"], cam["height"])
         off, ids = compute_tile_intersection(pts, radii, depths, mask, cam["width"], cam["height"], 16)
-    return dict(ms=ms, stages={k: (c, t / steps) for k, (c, t) in stages.items()},
+        visited, composited = rasterize_work(off, ids, pts, conic, opac, cam["width"],
+                                             cam["height"], 16, 1e-4, 1e-4, 9.21)
+    return dict(ms=ms, stages={k: (c, t / steps) for k, (c, t) in stages.items()}, steps=steps,
                 n=scene["params"]["means"].shape[0], n_visible=int(mask.sum()), keys=int(ids.numel()),
+                n_tiles=int(off.numel()), visited=visited, composited=composited,
                 loss=float(loss), width=cam["width"], height=cam["height"])
 
 
 # ----------------------------------------------------------- roofline
 
-def algorithmic_bytes(stage: str, n: int, n_vis: int, k: int, hw: int) -> float:
-    """Bytes one call of each entry point must move at minimum: every API tensor
-    read once and written once (the per-Gaussian layouts of the API)."""
-    if stage == "project_points":
+# FP32 flops per evaluated (pixel, list entry) pair of the reference blend loop
+# (src/cuda/kernel.cu:954-982 forward; :1063-1106 backward), exp counted as one
+BLEND_FLOP_PER_PAIR = {"rasterize": 22.0, "rasterize_backward": 70.0}
+HBM_STAGES = ("project_points", "evaluate_sh", "bin_count", "bin_sort", "evaluate_sh_backward",
+              "project_points_backward")
+
+
+def sort_passes(n_tiles: int) -> int:
+    """8-bit digit passes a 64-bit (tile << 32 | depth) radix sort needs: ceil((32 + bits(T)) / 8)."""
+    return math.ceil((32 + math.ceil(math.log2(max(n_tiles, 2)))) / 8)
+
+
+def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> float:
+    """Bytes one call of an entry point must move: every API tensor read once and
+    written once at full size; binning is charged the conventional 64-bit-key
+    pipeline (count + scan 33 B/G, emit 12 B/key, P 8-bit radix passes of
+    24 B/key, ranges 8 B/key + 4 B/tile)."""
+    if stage == "project_points":  # means, scales, quats, opac -> uv, z, cov, conic, radii, mask
         return n * (12 + 12 + 16 + 4) + n * (8 + 4 + 12 + 12 + 8 + 1)
-    if stage == "evaluate_sh":
+    if stage == "evaluate_sh":  # means, dc, rest, mask -> colours
         return n * (12 + 12 + 180 + 1) + n * 12
-    if stage == "evaluate_sh_backward":
+    if stage == "evaluate_sh_backward":  # grad, means, rest, colours, mask -> grads of means, dc, rest
         return n * (12 + 12 + 180 + 12 + 1) + n * (12 + 12 + 180)
-    if stage == "project_points_backward":
+    if stage == "project_points_backward":  # grads uv/conic, means, scales, quats, cov, mask -> 3 grads
         return n * (8 + 12 + 12 + 12 + 16 + 12 + 1) + n * (12 + 12 + 16)
-    if stage == "bin_count":  # points, radii, depths, mask in; 4 sort passes over N (key+id)
-        return n * 21 + 4 * n * 16 + n * 16
-    if stage == "bin_sort":  # emit 8 B/key, two tile passes over (key, id), ranges
-        return k * 8 + 2 * k * 16 + k * 4
+    if stage == "bin_count":
+        return n * (21 + 4 + 8)
+    if stage == "bin_sort":
+        return k * 12 + 24 * k * sort_passes(n_tiles) + k * 8 + 4 * n_tiles
+    if stage == "rasterize":
+        return k * 40 + 12 * hw
+    if stage == "rasterize_backward":
+        return 12 * hw + k * 76 + 36 * n
     return 0.0
 
 
-def roofline(res: dict) -> dict:
-    n, nv, k, hw = res["n"], res["n_visible"], res["keys"], res["width"] * res["height"]
+# kernel that implements each single-kernel entry point
+STAGE_KERNEL = {"rasterize": "blend_forward_kernel", "rasterize_backward": "blend_backward_kernel",
+                "project_points": "project_points_kernel", "evaluate_sh": "sh_forward_kernel",
+                "evaluate_sh_backward": "sh_backward_kernel",
+                "project_points_backward": "project_points_backward_kernel"}
+
+
+def profiled_traffic(stage: str, workload: str):
+    """HBM bytes per launch of `stage`'s kernel for `workload`, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary profiles/hbm_traffic_<workload>.md
+    (line `traffic_bytes_per_launch[<kernel>]: <bytes>`), or None without one."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.md")
+    kernel = STAGE_KERNEL.get(stage)
+    if kernel is None or not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\[" + re.escape(kernel) + r"\]:\s*([0-9.eE+]+)",
+                  open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def roofline(res: dict, workload: str) -> dict:
+    n, k, nt = res["n"], res["keys"], res["n_tiles"]
+    hw = res["width"] * res["height"]
+    steps = res["steps"]
     per_stage = {}
     for stage, (calls, ms) in res["stages"].items():
-        b = algorithmic_bytes(stage, n, nv, k, hw)
-        per_stage[stage] = dict(ms=round(ms, 4), calls_per_step=calls // max(res.get("steps", 1), 1))
+        b = algorithmic_bytes(stage, n, k, nt, hw)
+        per_call = ms / max(calls / steps, 1)
+        row = dict(ms=round(ms, 4), calls_per_step=calls // steps)
         if b and ms > 0:
-            per_stage[stage]["gbs"] = round(b / (ms * 1e-3) / 1e9, 1)
+            row["gbs"] = round(b / (per_call * 1e-3) / 1e9, 1)
+        if stage in BLEND_FLOP_PER_PAIR and ms > 0:
+            row["tflops"] = round(res["visited"] * BLEND_FLOP_PER_PAIR[stage] / (per_call * 1e-3) / 1e12, 2)
+        per_stage[stage] = row
+
     dominant = max(res["stages"].items(), key=lambda kv: kv[1][1])[0]
-    return dict(dominant=dominant, per_stage=per_stage)
+    calls, ms = res["stages"][dominant]
+    per_launch_s = ms / max(calls / steps, 1) * 1e-3
+    traffic = profiled_traffic(dominant, workload)
+    if dominant in BLEND_FLOP_PER_PAIR:
+        achieved = res["visited"] * BLEND_FLOP_PER_PAIR[dominant] / per_launch_s / 1e12
+        main = dict(bound="valu", achieved=round(achieved, 3), peak=FP32_PEAK_TFLOPS,
+                    unit="TFLOP/s", frac=round(achieved / FP32_PEAK_TFLOPS, 4), traffic=traffic,
+                    kernel=dominant, launch_ms=round(per_launch_s * 1e3, 4),
+                    work=f"{res['visited']} evaluated (pixel, entry) pairs x "
+                         f"{BLEND_FLOP_PER_PAIR[dominant]:g} flop")
+    else:
+        achieved = algorithmic_bytes(dominant, n, k, nt, hw) / per_launch_s / 1e9
+        main = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic, kernel=dominant,
+                    launch_ms=round(per_launch_s * 1e3, 4))
+
+    # HBM-bound stages together (preprocess fwd/bwd, binning and sort)
+    hb = sum(algorithmic_bytes(s, n, k, nt, hw) * res["stages"][s][0] / steps
+             for s in HBM_STAGES if s in res["stages"])
+    ht = sum(res["stages"][s][1] for s in HBM_STAGES if s in res["stages"]) * 1e-3
+    hbm = dict(achieved=round(hb / ht / 1e9, 1) if ht else None, peak=HBM_PEAK_GBS, unit="GB/s",
+               frac=round(hb / ht / 1e9 / HBM_PEAK_GBS, 4) if ht else None, bytes=int(hb),
+               ms=round(ht * 1e3, 4), sort_passes_charged=sort_passes(nt))
+    return dict(dominant=dominant, roofline=main, hbm_stages=hbm, per_stage=per_stage)
 
 
 # -------------------------------------------------------------- CPU leg
 
-def cpu_baseline(scene: dict, sample_tiles: int = 48, seed: int = 0) -> dict:
+def cpu_baseline(scene: dict, budget_s: float = 12.0, batch_tiles: int = 128, seed: int = 0) -> dict:
     """The oracle (a restatement of src/torch_rasterizer.py) timed on the host CPU.
 
     Full fwd+bwd at the headline size does not fit in host RAM (autograd keeps
-    ~15 KB per (tile, Gaussian) key), so the sample is: the whole vectorised
-    preprocess + binning for all N Gaussians, plus fwd+bwd of `sample_tiles`
-    randomly chosen non-empty tiles; per-tile time is scaled to all non-empty
+    ~15 KB per (tile, Gaussian) key), so the run is bounded: the whole
+    preprocess + binning forward for all N Gaussians, then fwd+bwd of the blend
+    over batches of randomly chosen non-empty tiles until `budget_s` seconds of
+    blend work have run (blend inputs are detached leaves, so each batch's
+    backward stops there), then the preprocess backward once from the
+    accumulated gradients.  The blend time per tile is scaled to all non-empty
     tiles.  Reports ms per full iteration.
     """
     import numpy as np
 
+    from oracle import blend
     from oracle import render as orender
 
     torch.set_num_threads(max(1, os.cpu_count() or 1))
@@ -263,34 +340,63 @@ def cpu_baseline(scene: dict, sample_tiles: int = 48, seed: int = 0) -> dict:
     scales, quats, opac = activated(leaves)
     out = orender.render_stages(cam["w2c"], cam["K"], W, H, leaves["means"], scales, quats, opac,
                                 leaves["sh_dc"], leaves["sh_rest"], near_plane=cam["near"], tiles=[])
+    keep = out["proj"]["keep"]
+    blend_in = [out["points_image"], out["conic"], torch.where(keep, opac, torch.zeros_like(opac)),
+                out["colors"]]
     t_pre = time.perf_counter() - t0
+
     off = out["indexing_offset"].numpy()
     k = int(out["gaussian_ids_sorted"].numel())
     ends = np.append(off[1:], k)
     nonempty = np.nonzero(ends > off)[0]
-    rng = np.random.default_rng(seed)
-    tiles = sorted(rng.choice(nonempty, size=min(sample_tiles, len(nonempty)), replace=False).tolist())
-    # time fwd+bwd of the sampled tiles (preprocess graph reused, its backward included once)
-    from oracle import blend
+    order = np.random.default_rng(seed).permutation(nonempty)
+    sub = [t.detach().requires_grad_(True) for t in blend_in]
+    done, t_tiles = 0, 0.0
+    while done < len(order) and t_tiles < budget_s:
+        batch = sorted(order[done:done + batch_tiles].tolist())
+        t1 = time.perf_counter()
+        raw = blend.rasterize(out["indexing_offset"], out["gaussian_ids_sorted"], *sub, W, H, 16,
+                              1e-4, 1e-4, 9.21, tiles=batch)
+        torch.nn.functional.l1_loss(raw.clamp(0, 1), scene["target"]).backward()
+        t_tiles += time.perf_counter() - t1
+        done += len(batch)
 
-    t1 = time.perf_counter()
-    raw = blend.rasterize(out["indexing_offset"], out["gaussian_ids_sorted"], out["points_image"],
-                          out["conic"], torch.where(out["proj"]["keep"], opac, torch.zeros_like(opac)),
-                          out["colors"], W, H, 16, 1e-4, 1e-4, 9.21, tiles=tiles)
-    loss = torch.nn.functional.l1_loss(raw.clamp(0, 1), scene["target"])
-    loss.backward()
-    t_tiles = time.perf_counter() - t1
-    total_s = t_pre + t_tiles * len(nonempty) / max(len(tiles), 1)
+    t2 = time.perf_counter()
+    torch.autograd.backward(blend_in, [t.grad for t in sub])
+    t_pre_bwd = time.perf_counter() - t2
+    total_s = t_pre + t_pre_bwd + t_tiles * len(nonempty) / max(done, 1)
     return dict(value=round(total_s * 1e3, 1), unit="ms/iter", cores=torch.get_num_threads(),
                 kind="port",
                 sample=(f"oracle (restated src/torch_rasterizer.py) on the same {scene['name']} inputs: "
-                        f"full preprocess+binning of {scene['params']['means'].shape[0]} Gaussians "
-                        f"({t_pre:.1f} s) + fwd+bwd of {len(tiles)} random non-empty tiles "
-                        f"({t_tiles:.1f} s) scaled to all {len(nonempty)} non-empty tiles; "
-                        f"cpu={platform.processor() or platform.machine()}"))
+                        f"preprocess+binning forward of all {scene['params']['means'].shape[0]} "
+                        f"Gaussians ({t_pre:.1f} s), blend fwd+bwd of {done} random non-empty tiles "
+                        f"({t_tiles:.1f} s) scaled to all {len(nonempty)} non-empty tiles, "
+                        f"preprocess backward ({t_pre_bwd:.1f} s); cpu={cpu_model()}"))
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 # ------------------------------------------------------------------- main
+
+def copy_calibration(mib: int) -> int:
+    """A plain device copy of known size: under rocprofv3 --pmc its FETCH_SIZE and
+    WRITE_SIZE per dispatch give the counters' scale (expected: mib * 1024 KiB each)."""
+    src = torch.full((mib * 2**18,), 1.5, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(4):  # an elementwise kernel (not a DMA copy): reads and writes mib MiB
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 4}), flush=True)
+    return 0
+
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
@@ -299,7 +405,10 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=[1, 3, 4])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-tiles", type=int, default=48)
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of CPU blend work in the cpu_baseline sample")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 4 device copies of MIB MiB (scales FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -310,13 +419,15 @@ def main(argv=None):
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 2
 
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
+
     scene = CONFIGS[args.config]()
     res = run_gpu(scene, args.steps, args.warmup)
-    res["steps"] = args.steps
-    rl = roofline(res)
+    rl = roofline(res, scene["name"])
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(scene, args.cpu_sample_tiles)
+        cpu = cpu_baseline(scene, args.cpu_budget)
     line = {
         "metric": METRIC,
         "value": round(res["ms"], 3),
@@ -335,6 +446,9 @@ def main(argv=None):
                    "gaussians": res["n"], "visible": res["n_visible"], "keys": res["keys"],
                    "resolution": [res["width"], res["height"]]},
         "gaussians_per_s": round(res["n"] / (res["ms"] * 1e-3), 1),
+        "roofline": rl["roofline"],
+        "hbm_stages": rl["hbm_stages"],
+        "blend_pairs": {"visited": res["visited"], "composited": res["composited"]},
         "stages": rl["per_stage"],
         "cpu_baseline": cpu,
     }

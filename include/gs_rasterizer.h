@@ -154,7 +154,9 @@ int gs_rasterize(const int32_t *indexing_offset, const int32_t *gaussian_ids_sor
  * colors.  Replaces cuda_rasterizer.rasterize_backward
  * (src/cuda/rasterizer.cpp:397-440, kernel src/cuda/kernel.cu:989-1111).
  * `image` is the forward output for the same inputs, or NULL (the kernel then
- * recomputes it).  The four gradient outputs are overwritten.
+ * recomputes it).  accumulate == 0: the four gradient outputs are overwritten;
+ * accumulate != 0: the gradients are added to their current contents (e.g. to
+ * sum over cameras into buffers the caller zeroed once).
  */
 int gs_rasterize_backward(const float *grad_image, const float *image,
                           const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
@@ -164,7 +166,23 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
                           int32_t tile_size, float alpha_threshold,
                           float transmittance_threshold, float chi_squared_threshold,
                           float *grad_points_image, float *grad_cov_inv_image,
-                          float *grad_opacities, float *grad_colors, hipStream_t stream);
+                          float *grad_opacities, float *grad_colors, int32_t accumulate,
+                          hipStream_t stream);
+
+/*
+ * Measurement entry (no counterpart in the reference): the work of the
+ * reference blend loop (src/cuda/kernel.cu:954-982) for the same inputs as
+ * gs_rasterize.  *visited = sum over pixels of the list entries walked until
+ * the transmittance test stops the pixel; *composited = entries that passed
+ * the chi-square and alpha tests and were blended.  Both are device uint64
+ * counters (overwritten).  Used to express blend throughput in flop/s.
+ */
+int gs_rasterize_work(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                      int32_t n_tiles, int64_t k, const float *points_image,
+                      const float *cov_inv_image, const float *opacities, int64_t n,
+                      int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
+                      float transmittance_threshold, float chi_squared_threshold,
+                      uint64_t *visited, uint64_t *composited, hipStream_t stream);
 
 #ifdef __cplusplus
 }
