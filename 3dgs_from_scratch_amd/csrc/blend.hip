@@ -86,31 +86,103 @@ struct BatchLds {
     float4 col[kBatch];  // r, g, b, (gaussian id bits)
 };
 
-// Stages Gaussian g into LDS slot `slot`.  An id outside [0, n) stages a record
-// that every wave culls (it contributes nothing).
-__device__ __forceinline__ void stage_record(BatchLds &s, int slot, int g, int64_t n,
-                                             const float *__restrict__ points,
-                                             const float *__restrict__ conics,
-                                             const float *__restrict__ opac,
-                                             const float *__restrict__ colors, float chi,
+// One lane's Gaussian record of the next batch, fetched into registers while
+// the current batch is processed (id < 0: empty slot).
+struct Record {
+    float u, v, A, B, C, o, r, g, b;
+    int id;
+};
+
+__device__ __forceinline__ int32_t fetch_id(int32_t i, int32_t end,
+                                            const int32_t *__restrict__ ids) {
+    return i < end ? ids[i] : -1;
+}
+
+__device__ __forceinline__ Record fetch_record(int32_t g, int64_t n,
+                                               const float *__restrict__ points,
+                                               const float *__restrict__ conics,
+                                               const float *__restrict__ opac,
+                                               const float *__restrict__ colors) {
+    Record r;
+    r.id = -1;
+    r.u = r.v = r.A = r.B = r.C = r.o = r.r = r.g = r.b = 0.0f;
+    if (g >= 0 && (int64_t)g < n) {
+        r.id = g;
+        r.u = points[2 * g];
+        r.v = points[2 * g + 1];
+        r.A = conics[3 * g];
+        r.B = conics[3 * g + 1];
+        r.C = conics[3 * g + 2];
+        r.o = opac[g];
+        r.r = colors[3 * g];
+        r.g = colors[3 * g + 1];
+        r.b = colors[3 * g + 2];
+    }
+    return r;
+}
+
+// Stages the lane's record into LDS slot `slot`.  An empty record stages a
+// Gaussian at infinity that every wave culls.
+__device__ __forceinline__ void stage_record(BatchLds &s, int slot, const Record &r, float chi,
                                              float alpha_thr) {
-    if (g < 0 || (int64_t)g >= n) {
+    if (r.id < 0) {
         const float inf = __builtin_inff();
         s.geo[slot] = make_float4(inf, inf, 0.0f, 0.0f);
         s.aux[slot] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         s.col[slot] = make_float4(0.0f, 0.0f, 0.0f, __int_as_float(0));
         return;
     }
-    const float u = points[2 * g], v = points[2 * g + 1];
-    const float A = conics[3 * g], B = conics[3 * g + 1], C = conics[3 * g + 2];
-    const float o = opac[g];
     float ex, ey;
-    ellipse_extent(A, B, C, o, chi, alpha_thr, ex, ey);
-    s.geo[slot] = make_float4(u, v, A, B + B);
-    s.aux[slot] = make_float4(C, o, ex, ey);
-    s.col[slot] = make_float4(colors[3 * g], colors[3 * g + 1], colors[3 * g + 2],
-                              __int_as_float(g));
+    ellipse_extent(r.A, r.B, r.C, r.o, chi, alpha_thr, ex, ey);
+    s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
+    s.aux[slot] = make_float4(r.C, r.o, ex, ey);
+    s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
 }
+
+// Software pipeline over a tile's list in batches of kBatch.  With kRecords,
+// the ids of batch b+2 and the records of batch b+1 are in flight while batch
+// b is processed; without, only the ids of batch b+1 (fewer registers).
+template <bool kRecords>
+struct BatchPipe {
+    int32_t next_id;  // this lane's id in the batch after the next one to stage
+    Record rec;       // this lane's record of the next batch to stage (kRecords)
+
+    __device__ __forceinline__ void start(TileSpan span, const int32_t *__restrict__ ids,
+                                          int64_t n, const float *__restrict__ points,
+                                          const float *__restrict__ conics,
+                                          const float *__restrict__ opac,
+                                          const float *__restrict__ colors) {
+        const int32_t lane = (int32_t)threadIdx.x;
+        if (kRecords) {
+            const int32_t g0 = fetch_id(span.start + lane, span.end, ids);
+            next_id = fetch_id(span.start + kBatch + lane, span.end, ids);
+            rec = fetch_record(g0, n, points, conics, opac, colors);
+        } else {
+            next_id = fetch_id(span.start + lane, span.end, ids);
+        }
+    }
+
+    // Stages the batch starting at b0 and fetches ahead.
+    __device__ __forceinline__ void advance(BatchLds &s, int32_t b0, TileSpan span,
+                                            const int32_t *__restrict__ ids, int64_t n,
+                                            const float *__restrict__ points,
+                                            const float *__restrict__ conics,
+                                            const float *__restrict__ opac,
+                                            const float *__restrict__ colors, float chi,
+                                            float alpha_thr) {
+        const int32_t lane = (int32_t)threadIdx.x;
+        if (!kRecords) rec = fetch_record(next_id, n, points, conics, opac, colors);
+        __syncthreads();  // previous batch fully read before restaging
+        stage_record(s, threadIdx.x, rec, chi, alpha_thr);
+        __syncthreads();
+        if (kRecords) {
+            rec = fetch_record(next_id, n, points, conics, opac, colors);
+            next_id = fetch_id(b0 + 2 * kBatch + lane, span.end, ids);
+        } else {
+            next_id = fetch_id(b0 + kBatch + lane, span.end, ids);
+        }
+    }
+};
 
 // Strips [s_lo, s_hi] of the tile reached by the ellipse of record (geo, aux);
 // false when the ellipse misses the tile.  Wave-uniform.
@@ -119,15 +191,16 @@ __device__ __forceinline__ bool strip_range(float4 geo, float4 aux, float x0, fl
     if (geo.x + aux.z < x0 || geo.x - aux.z > x0 + (kTile - 1)) return false;
     const float ylo = geo.y - aux.w - y0, yhi = geo.y + aux.w - y0;
     if (yhi < 0.0f || ylo > (float)(kTile - 1)) return false;
-    s_lo = ylo <= 0.0f ? 0 : ((int)ylo >> 2);
-    s_hi = yhi >= (float)(kTile - 1) ? kStrips - 1 : ((int)yhi >> 2);
+    s_lo = __builtin_amdgcn_readfirstlane(ylo <= 0.0f ? 0 : ((int)ylo >> 2));
+    s_hi = __builtin_amdgcn_readfirstlane(yhi >= (float)(kTile - 1) ? kStrips - 1
+                                                                     : ((int)yhi >> 2));
     return true;
 }
 
 // Pixel geometry of one lane.
 struct LanePixels {
     float fx;             // pixel x
-    float fy0;            // pixel y of strip 0 (strip s adds 4s)
+    float fy[kStrips];    // pixel y in strip s
     float x0, y0;         // tile origin
     bool inside[kStrips];
 };
@@ -139,39 +212,47 @@ __device__ __forceinline__ LanePixels lane_pixels(int tile, int tiles_x, int wid
     const int px = tx * kTile + (lane & 15);
     const int py = ty * kTile + (lane >> 4);
     p.fx = (float)px;
-    p.fy0 = (float)py;
     p.x0 = (float)(tx * kTile);
     p.y0 = (float)(ty * kTile);
 #pragma unroll
-    for (int s = 0; s < kStrips; ++s) p.inside[s] = px < width && py + 4 * s < height;
+    for (int s = 0; s < kStrips; ++s) {
+        p.fy[s] = (float)(py + 4 * s);
+        p.inside[s] = px < width && py + 4 * s < height;
+    }
     return p;
 }
 
-__device__ __forceinline__ bool wave_all(bool x) { return __ballot(!x) == 0; }
+__device__ __forceinline__ bool wave_any(bool x) { return __ballot(x) != 0; }
+
+// Some pixel of the wave still composites: !(T < T_thr) (NaN stays active).
+__device__ __forceinline__ bool any_active(const float (&T)[kStrips], float T_thr) {
+    return wave_any(!(T[0] < T_thr) || !(T[1] < T_thr) || !(T[2] < T_thr) || !(T[3] < T_thr));
+}
 
 // Front-to-back accumulation of the lane's four pixels over the tile's list.
-// All 64 lanes must call it (it contains barriers).
+// All 64 lanes must call it (it contains barriers).  Branch-free per strip:
+// an entry that fails the chi-square or alpha test leaves T and the colour
+// unchanged through selects (T * (1 - 0 + 1e-10) would also be exact, but the
+// colour update must not touch a non-finite colour of a skipped Gaussian).
 __device__ __forceinline__ void blend_accumulate(
     BatchLds &s, TileSpan span, const int32_t *__restrict__ ids, int64_t n,
     const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, const LanePixels &pix,
     float alpha_thr, float T_thr, float chi, float (&cr)[kStrips], float (&cg)[kStrips],
     float (&cb)[kStrips]) {
+    // a pixel is active while !(T < T_thr); pixels outside the image start at -inf
     float T[kStrips];
-    bool dn[kStrips];
 #pragma unroll
     for (int q = 0; q < kStrips; ++q) {
-        T[q] = 1.0f;
+        T[q] = pix.inside[q] ? 1.0f : -__builtin_inff();
         cr[q] = cg[q] = cb[q] = 0.0f;
-        dn[q] = !pix.inside[q] || !(1.0f >= T_thr);
     }
+    if (span.end <= span.start) return;
+    BatchPipe<true> pipe;
+    pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
-        if (wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
-        __syncthreads();  // previous batch fully read before restaging
-        const int32_t i = b0 + (int32_t)threadIdx.x;
-        if (i < span.end)
-            stage_record(s, threadIdx.x, ids[i], n, points, conics, opac, colors, chi, alpha_thr);
-        __syncthreads();
+        if (!any_active(T, T_thr)) break;
+        pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi, alpha_thr);
         const int cnt = min(kBatch, span.end - b0);
         for (int j = 0; j < cnt; ++j) {
             const float4 geo = s.geo[j];
@@ -180,23 +261,25 @@ __device__ __forceinline__ void blend_accumulate(
             if (!strip_range(geo, aux, pix.x0, pix.y0, s_lo, s_hi)) continue;
             const float4 col = s.col[j];
             const float du = pix.fx - geo.x;
+            const float Adudu = (geo.z * du) * du;  // (A du) du, as in the oracle's A*du*du
+            const float B2du = geo.w * du;
 #pragma unroll
             for (int q = 0; q < kStrips; ++q) {
                 if (q < s_lo || q > s_hi) continue;  // uniform
-                if (dn[q]) continue;
-                const float dv = (pix.fy0 + (float)(4 * q)) - geo.y;
-                const float E = conic_exponent(geo.z, geo.w, aux.x, du, dv);
-                if (!(E < chi)) continue;
+                const float dv = pix.fy[q] - geo.y;
+                const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
+                const bool ok = !(T[q] < T_thr) && (E < chi);
+                if (!wave_any(ok)) continue;
                 const float alpha = __expf(-0.5f * E) * aux.y;
-                if (alpha < alpha_thr) continue;
+                const bool inc = ok && !(alpha < alpha_thr);
                 const float w = alpha * T[q];
-                cr[q] = fmaf(w, col.x, cr[q]);
-                cg[q] = fmaf(w, col.y, cg[q]);
-                cb[q] = fmaf(w, col.z, cb[q]);
-                T[q] = T[q] * ((1.0f - alpha) + kTransmittanceEps);
-                if (T[q] < T_thr) dn[q] = true;
+                cr[q] = inc ? fmaf(w, col.x, cr[q]) : cr[q];
+                cg[q] = inc ? fmaf(w, col.y, cg[q]) : cg[q];
+                cb[q] = inc ? fmaf(w, col.z, cb[q]) : cb[q];
+                const float Tn = T[q] * ((1.0f - alpha) + kTransmittanceEps);
+                T[q] = inc ? Tn : T[q];
             }
-            if ((j & 7) == 7 && wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
+            if ((j & 7) == 7 && !any_active(T, T_thr)) break;
         }
     }
 }
@@ -216,29 +299,123 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
 #pragma unroll
     for (int q = 0; q < kStrips; ++q) {
         if (!pix.inside[q]) continue;
-        const int64_t o = ((int64_t)(pix.fy0 + 4 * q) * width + (int64_t)pix.fx) * 3;
+        const int64_t o = ((int64_t)pix.fy[q] * width + (int64_t)pix.fx) * 3;
         image[o] = cr[q];
         image[o + 1] = cg[q];
         image[o + 2] = cb[q];
     }
 }
 
-// Sum over the 64 lanes, result in every lane: butterflies inside each 16-lane
-// row with DPP (xor 1, xor 2, half-mirror, mirror), then the gfx950 permlane
-// swaps exchange rows 0<->1, 2<->3 and halves 0-31 <-> 32-63.
-__device__ __forceinline__ float wave_sum(float x) {
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
-    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
-                                                      false, false);
-    x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
-                                                      false, false);
-    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+// ------------------------------------------------- wave reductions (gfx950)
+
+#define GS_DPP(x, ctrl) \
+    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), (ctrl), 0xF, 0xF, false))
+
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // reverse each 8-lane half row
+constexpr int kDppMirror = 0x140;     // reverse each 16-lane row
+constexpr int kDppRor8 = 0x128;       // rotate each row by 8 lanes
+
+// a + b where the two 32-lane halves are exchanged between them first:
+// lanes 0-31 get a[l] + a[l+32], lanes 32-63 get b[l-32] + b[l].
+__device__ __forceinline__ float swap32_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Rows (16 lanes) r0..r3: result rows are a.r0+a.r1, b.r0+b.r1, a.r2+a.r3, b.r2+b.r3.
+__device__ __forceinline__ float swap16_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Lane that holds field f's wave total after wave_sum9 (the others hold partials):
+// f0 0, f1 32, f2 16, f3 48, f4 8, f5 40, f6 24, f7 56, f8 4.
+__device__ __forceinline__ int sum9_field_of_lane(int lane) {
+    switch (lane) {
+    case 0: return 0;
+    case 32: return 1;
+    case 16: return 2;
+    case 48: return 3;
+    case 8: return 4;
+    case 40: return 5;
+    case 24: return 6;
+    case 56: return 7;
+    case 4: return 8;
+    default: return -1;
+    }
+}
+
+// Wave sums of nine per-lane values by transposition: each exchange step halves
+// the lanes a field is spread over and doubles the fields a register holds, so
+// the nine sums cost 9 swaps/selects and 14 adds instead of nine full
+// reductions.  All 64 lanes must be active.
+__device__ __forceinline__ float wave_sum9(const float (&f)[kGradFields], bool hi8,
+                                           bool f8_lane) {
+    const float p0 = swap32_add(f[0], f[1]);  // halves: f0 | f1
+    const float p1 = swap32_add(f[2], f[3]);  // f2 | f3
+    const float p2 = swap32_add(f[4], f[5]);  // f4 | f5
+    const float p3 = swap32_add(f[6], f[7]);  // f6 | f7
+    const float p4 = swap32_add(f[8], 0.0f);  // f8 | 0
+    const float q0 = swap16_add(p0, p1);      // rows: f0 f2 f1 f3
+    const float q1 = swap16_add(p2, p3);      // rows: f4 f6 f5 f7
+    float q2 = swap16_add(p4, 0.0f);          // rows: f8 0 0 0
+    // low 8 lanes of each row take q0's row field, high 8 lanes q1's
+    const float x = hi8 ? q1 : q0, y = hi8 ? q0 : q1;
+    float r = x + GS_DPP(y, kDppRor8);
+    r += GS_DPP(r, kDppXor1);
+    r += GS_DPP(r, kDppXor2);
+    r += GS_DPP(r, kDppHalfMirror);
+    q2 += GS_DPP(q2, kDppXor1);
+    q2 += GS_DPP(q2, kDppXor2);
+    q2 += GS_DPP(q2, kDppHalfMirror);
+    q2 += GS_DPP(q2, kDppMirror);
+    return f8_lane ? q2 : r;
+}
+
+// Destination of the lane's field after wave_sum9: out[stride * g] += value * (fa * o + fb).
+struct GradTarget {
+    float *base;
+    int stride;
+    float fa, fb;
+    bool active;
+};
+
+__device__ __forceinline__ GradTarget grad_target(int lane, float *g_points, float *g_conics,
+                                                  float *g_opac, float *g_colors) {
+    GradTarget t;
+    const int f = sum9_field_of_lane(lane);
+    t.active = f >= 0;
+    t.base = g_points;
+    t.stride = 2;
+    t.fa = 1.0f;
+    t.fb = 0.0f;
+    switch (f) {
+    case 0: t.base = g_points; break;
+    case 1: t.base = g_points + 1; break;
+    case 2: t.base = g_conics; t.stride = 3; t.fa = -0.5f; break;
+    case 3: t.base = g_conics + 1; t.stride = 3; t.fa = -1.0f; break;
+    case 4: t.base = g_conics + 2; t.stride = 3; t.fa = -0.5f; break;
+    case 5: t.base = g_opac; t.stride = 1; t.fa = 0.0f; t.fb = 1.0f; break;
+    case 6: t.base = g_colors; t.stride = 3; t.fa = 0.0f; t.fb = 1.0f; break;
+    case 7: t.base = g_colors + 1; t.stride = 3; t.fa = 0.0f; t.fb = 1.0f; break;
+    case 8: t.base = g_colors + 2; t.stride = 3; t.fa = 0.0f; t.fb = 1.0f; break;
+    default: break;
+    }
+    return t;
+}
+
+// Backward of the front-to-back blend, walking the list in the same order.
+// With h = alpha dalpha = o G dalpha, the per-pixel terms of the gradients are
+//   d/du = h (A du + B dv), d/dv = h (B du + C dv),
+//   d/dA = -h du^2 / 2, d/dB = -h du dv, d/dC = -h dv^2 / 2,
+//   d/do = G dalpha, d/dc = w g.
+// A lane's four pixels share du, so it keeps sG = sum G dalpha, s1 = sum G dalpha dv,
+// s2 = sum G dalpha dv^2 and the colour sums, and forms the nine fields (up to the
+// uniform factor o, applied after the wave sum) once per Gaussian.
 __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const float *__restrict__ grad_image, const float *__restrict__ image,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
@@ -253,7 +430,6 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     if (span.end <= span.start) return;  // uniform across the workgroup
 
     float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips], T[kStrips], acc[kStrips];
-    bool dn[kStrips];
     float cr[kStrips], cg[kStrips], cb[kStrips];
     if (!image)
         blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr,
@@ -262,7 +438,7 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     for (int q = 0; q < kStrips; ++q) {
         gr[q] = gg[q] = gb[q] = 0.0f;
         if (pix.inside[q]) {
-            const int64_t o = ((int64_t)(pix.fy0 + 4 * q) * width + (int64_t)pix.fx) * 3;
+            const int64_t o = ((int64_t)pix.fy[q] * width + (int64_t)pix.fx) * 3;
             gr[q] = grad_image[o];
             gg[q] = grad_image[o + 1];
             gb[q] = grad_image[o + 2];
@@ -275,19 +451,23 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
             cr[q] = cg[q] = cb[q] = 0.0f;
         }
         gC[q] = gr[q] * cr[q] + gg[q] * cg[q] + gb[q] * cb[q];
-        T[q] = 1.0f;
         acc[q] = 0.0f;
-        dn[q] = !pix.inside[q] || !(1.0f >= T_thr) ||
-                (gr[q] == 0.0f && gg[q] == 0.0f && gb[q] == 0.0f);
+        // active while !(T < T_thr); pixels outside the image or with a zero
+        // gradient (skipped as in src/cuda/kernel.cu:1028-1030) start at -inf
+        const bool live = pix.inside[q] && !(gr[q] == 0.0f && gg[q] == 0.0f && gb[q] == 0.0f);
+        T[q] = live ? 1.0f : -__builtin_inff();
     }
 
+    const int lane = threadIdx.x;
+    const bool hi8 = (lane & 8) != 0;
+    const bool f8_lane = lane == 4;
+    const GradTarget tgt = grad_target(lane, g_points, g_conics, g_opac, g_colors);
+
+    BatchPipe<false> pipe;
+    pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
-        if (wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
-        __syncthreads();
-        const int32_t i = b0 + (int32_t)threadIdx.x;
-        if (i < span.end)
-            stage_record(s, threadIdx.x, ids[i], n, points, conics, opac, colors, chi, alpha_thr);
-        __syncthreads();
+        if (!any_active(T, T_thr)) break;
+        pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi, alpha_thr);
         const int cnt = min(kBatch, span.end - b0);
         for (int j = 0; j < cnt; ++j) {
             const float4 geo = s.geo[j];
@@ -296,58 +476,62 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
             if (!strip_range(geo, aux, pix.x0, pix.y0, s_lo, s_hi)) continue;
             const float4 col = s.col[j];
             const float du = pix.fx - geo.x;
-            const float B = 0.5f * geo.w;
-            float v[kGradFields] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            bool hit = false;
+            const float Adudu = (geo.z * du) * du;
+            const float B2du = geo.w * du;
+            float sG = 0.0f, s1 = 0.0f, s2 = 0.0f, sr = 0.0f, sg = 0.0f, sb = 0.0f;
+            uint64_t hit = 0;
 #pragma unroll
             for (int q = 0; q < kStrips; ++q) {
                 if (q < s_lo || q > s_hi) continue;  // uniform
-                if (dn[q]) continue;
-                const float dv = (pix.fy0 + (float)(4 * q)) - geo.y;
-                const float E = conic_exponent(geo.z, geo.w, aux.x, du, dv);
-                if (!(E < chi)) continue;
+                const float dv = pix.fy[q] - geo.y;
+                const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
+                const bool ok = !(T[q] < T_thr) && (E < chi);
+                if (!wave_any(ok)) continue;
                 const float G = __expf(-0.5f * E);
                 const float alpha = G * aux.y;
-                if (alpha < alpha_thr) continue;
-                hit = true;
+                const bool inc = ok && !(alpha < alpha_thr);
                 const float w = alpha * T[q];
                 const float gcol = fmaf(gr[q], col.x, fmaf(gg[q], col.y, gb[q] * col.z));
                 const float acc_new = fmaf(w, gcol, acc[q]);
                 const float one_m = (1.0f - alpha) + kTransmittanceEps;
-                const float dalpha = T[q] * gcol - (gC[q] - acc_new) / one_m;
-                const float h = alpha * dalpha;
-                const float hdu = h * du, hdv = h * dv;
-                v[0] += hdu;
-                v[1] += hdv;
-                v[2] = fmaf(hdu, du, v[2]);
-                v[3] = fmaf(hdu, dv, v[3]);
-                v[4] = fmaf(hdv, dv, v[4]);
-                v[5] = fmaf(G, dalpha, v[5]);
-                v[6] = fmaf(w, gr[q], v[6]);
-                v[7] = fmaf(w, gg[q], v[7]);
-                v[8] = fmaf(w, gb[q], v[8]);
-                acc[q] = acc_new;
-                T[q] = T[q] * one_m;
-                if (T[q] < T_thr) dn[q] = true;
+                // dalpha = T gcol - (gC - acc_new) / (1 - alpha + eps)
+                const float dalpha =
+                    fmaf(acc_new - gC[q], __builtin_amdgcn_rcpf(one_m), T[q] * gcol);
+                const float Gd = inc ? G * dalpha : 0.0f;
+                const float ws = inc ? w : 0.0f;
+                sG += Gd;
+                const float t = Gd * dv;
+                s1 += t;
+                s2 = fmaf(t, dv, s2);
+                sr = fmaf(ws, gr[q], sr);
+                sg = fmaf(ws, gg[q], sg);
+                sb = fmaf(ws, gb[q], sb);
+                acc[q] = inc ? acc_new : acc[q];
+                const float Tn = T[q] * one_m;
+                T[q] = inc ? Tn : T[q];
+                hit |= __ballot(inc);
             }
-            if (__ballot(hit) != 0) {
-#pragma unroll
-                for (int f = 0; f < kGradFields; ++f) v[f] = wave_sum(v[f]);
-                if (threadIdx.x == 0) {
+            if (hit != 0) {
+                const float B = 0.5f * geo.w;
+                const float a = du * sG;
+                float f[kGradFields];
+                f[0] = fmaf(geo.z, a, B * s1);   // d/du / o
+                f[1] = fmaf(B, a, aux.x * s1);   // d/dv / o
+                f[2] = du * a;                   // d/dA / (-o/2)
+                f[3] = du * s1;                  // d/dB / (-o)
+                f[4] = s2;                       // d/dC / (-o/2)
+                f[5] = sG;                       // d/dopacity
+                f[6] = sr;
+                f[7] = sg;
+                f[8] = sb;
+                const float total = wave_sum9(f, hi8, f8_lane);
+                if (tgt.active) {
                     const int g = __float_as_int(col.w);
-                    // dE/du = -2(A du + B dv): sum h (A du + B dv) = A sum h du + B sum h dv
-                    unsafeAtomicAdd(g_points + 2 * g, fmaf(geo.z, v[0], B * v[1]));
-                    unsafeAtomicAdd(g_points + 2 * g + 1, fmaf(B, v[0], aux.x * v[1]));
-                    unsafeAtomicAdd(g_conics + 3 * g, -0.5f * v[2]);
-                    unsafeAtomicAdd(g_conics + 3 * g + 1, -v[3]);
-                    unsafeAtomicAdd(g_conics + 3 * g + 2, -0.5f * v[4]);
-                    unsafeAtomicAdd(g_opac + g, v[5]);
-                    unsafeAtomicAdd(g_colors + 3 * g, v[6]);
-                    unsafeAtomicAdd(g_colors + 3 * g + 1, v[7]);
-                    unsafeAtomicAdd(g_colors + 3 * g + 2, v[8]);
+                    unsafeAtomicAdd(tgt.base + (int64_t)tgt.stride * g,
+                                    total * fmaf(tgt.fa, aux.y, tgt.fb));
                 }
             }
-            if ((j & 7) == 7 && wave_all(dn[0] && dn[1] && dn[2] && dn[3])) break;
+            if ((j & 7) == 7 && !any_active(T, T_thr)) break;
         }
     }
 }
@@ -509,9 +693,11 @@ using namespace gs;
 
 static int check_blend_args(const int32_t *indexing_offset, const int32_t *ids, int32_t n_tiles,
                             int64_t k, int64_t n, int32_t width, int32_t height,
-                            int32_t tile_size) {
+                            int32_t tile_size, float alpha_thr, float T_thr, float chi) {
     if (n < 0 || k < 0 || n_tiles < 0 || width <= 0 || height <= 0 || tile_size <= 0)
         return GS_ERR_INVALID_ARGUMENT;
+    // NaN thresholds would make every comparison false (pixels never stop)
+    if (alpha_thr != alpha_thr || T_thr != T_thr || chi != chi) return GS_ERR_INVALID_ARGUMENT;
     if (k > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
     if (tile_size * tile_size > 1024) return GS_ERR_UNSUPPORTED;
     const int64_t tiles_x = (width + tile_size - 1) / tile_size;
@@ -531,7 +717,8 @@ extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gauss
                             float transmittance_threshold, float chi_squared_threshold,
                             float *image, hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
-                              tile_size);
+                              tile_size, alpha_threshold,
+                              transmittance_threshold, chi_squared_threshold);
     if (st) return st;
     if (!image) return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
@@ -570,7 +757,8 @@ extern "C" int gs_rasterize_backward(
     float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
     hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
-                              tile_size);
+                              tile_size, alpha_threshold,
+                              transmittance_threshold, chi_squared_threshold);
     if (st) return st;
     if (n > 0 && (!grad_points_image || !grad_cov_inv_image || !grad_opacities || !grad_colors))
         return GS_ERR_INVALID_ARGUMENT;
@@ -610,7 +798,8 @@ extern "C" int gs_rasterize_work(const int32_t *indexing_offset,
                                  float transmittance_threshold, float chi_squared_threshold,
                                  uint64_t *visited, uint64_t *composited, hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
-                              tile_size);
+                              tile_size, alpha_threshold,
+                              transmittance_threshold, chi_squared_threshold);
     if (st) return st;
     if (!visited || !composited) return GS_ERR_INVALID_ARGUMENT;
     st = zero_bytes(visited, sizeof(uint64_t), stream);

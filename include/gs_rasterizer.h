@@ -140,7 +140,8 @@ int gs_bin_sort(const float *points_image, const float *radii, const float *dept
  * (integer coordinates) iff E < chi_squared_threshold, alpha >= alpha_threshold
  * and the transmittance before it is >= transmittance_threshold.
  * image is (H,W,3), un-clamped, no background.  n_tiles = length of
- * indexing_offset, k = length of gaussian_ids_sorted.
+ * indexing_offset, k = length of gaussian_ids_sorted.  NaN thresholds are
+ * rejected with GS_ERR_INVALID_ARGUMENT (here and in the blend entries below).
  */
 int gs_rasterize(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
                  int32_t n_tiles, int64_t k, const float *points_image,

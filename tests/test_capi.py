@@ -83,6 +83,8 @@ def test_invalid_arguments_rejected_on_host(lib):
                             9.21, null, null) == -3
     assert lib.gs_rasterize(null, null, 4, 10, *([null] * 4), 10, 64, 64, 64, 1e-4, 1e-4, 9.21,
                             null, null) == -4  # 64x64 tile: more than 1024 threads
+    assert lib.gs_rasterize(null, null, 4, 10, *([null] * 4), 10, 32, 32, 16, 1e-4,
+                            float("nan"), 9.21, null, null) == -1  # NaN threshold
     # more offset entries than the image has tiles
     assert lib.gs_rasterize(null, null, 5, 0, *([null] * 4), 0, 32, 32, 16, 1e-4, 1e-4, 9.21,
                             null, null) == -1
