@@ -224,6 +224,15 @@ __device__ __forceinline__ LanePixels lane_pixels(int tile, int tiles_x, int wid
 
 __device__ __forceinline__ bool wave_any(bool x) { return __ballot(x) != 0; }
 
+// clamp(x, 0, 1) keeping NaN, as torch.clamp.
+__device__ __forceinline__ float clamp01(float x) { return x < 0.0f ? 0.0f : (x > 1.0f ? 1.0f : x); }
+
+// Gradient of display = clamp(image, 0, 1) * 255 w.r.t. image: torch's clamp
+// passes it where 0 <= image <= 1.
+__device__ __forceinline__ float display_grad(float g, float raw) {
+    return (raw >= 0.0f && raw <= 1.0f) ? g * 255.0f : 0.0f;
+}
+
 // Some pixel of the wave still composites: !(T < T_thr) (NaN stays active).
 __device__ __forceinline__ bool any_active(const float (&T)[kStrips], float T_thr) {
     return wave_any(!(T[0] < T_thr) || !(T[1] < T_thr) || !(T[2] < T_thr) || !(T[3] < T_thr));
@@ -288,7 +297,8 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
-    int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image) {
+    int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image,
+    float *__restrict__ display) {
     __shared__ BatchLds s;
     const int tile = tile_of_block(blockIdx.x, n_tiles);
     const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
@@ -303,6 +313,11 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
         image[o] = cr[q];
         image[o + 1] = cg[q];
         image[o + 2] = cb[q];
+        if (display) {  // image.clamp(0, 1) * 255 (src/cuda/wrapper.py:294)
+            display[o] = clamp01(cr[q]) * 255.0f;
+            display[o + 1] = clamp01(cg[q]) * 255.0f;
+            display[o + 2] = clamp01(cb[q]) * 255.0f;
+        }
     }
 }
 
@@ -416,6 +431,8 @@ __device__ __forceinline__ GradTarget grad_target(int lane, float *g_points, flo
 // A lane's four pixels share du, so it keeps sG = sum G dalpha, s1 = sum G dalpha dv,
 // s2 = sum G dalpha dv^2 and the colour sums, and forms the nine fields (up to the
 // uniform factor o, applied after the wave sum) once per Gaussian.
+// kDisplay: grad_image is the gradient of clamp(image, 0, 1) * 255 (image required).
+template <bool kDisplay>
 __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const float *__restrict__ grad_image, const float *__restrict__ image,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
@@ -446,6 +463,11 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
                 cr[q] = image[o];
                 cg[q] = image[o + 1];
                 cb[q] = image[o + 2];
+            }
+            if (kDisplay) {
+                gr[q] = display_grad(gr[q], cr[q]);
+                gg[q] = display_grad(gg[q], cg[q]);
+                gb[q] = display_grad(gb[q], cb[q]);
             }
         } else {
             cr[q] = cg[q] = cb[q] = 0.0f;
@@ -709,23 +731,26 @@ static int check_blend_args(const int32_t *indexing_offset, const int32_t *ids, 
     return GS_OK;
 }
 
-extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
-                            int32_t n_tiles, int64_t k, const float *points_image,
-                            const float *cov_inv_image, const float *opacities,
-                            const float *colors, int64_t n, int32_t width, int32_t height,
-                            int32_t tile_size, float alpha_threshold,
-                            float transmittance_threshold, float chi_squared_threshold,
-                            float *image, hipStream_t stream) {
+static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                          int32_t n_tiles, int64_t k, const float *points_image,
+                          const float *cov_inv_image, const float *opacities, const float *colors,
+                          int64_t n, int32_t width, int32_t height, int32_t tile_size,
+                          float alpha_threshold, float transmittance_threshold,
+                          float chi_squared_threshold, float *image, float *display,
+                          hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
-                              tile_size, alpha_threshold,
-                              transmittance_threshold, chi_squared_threshold);
+                              tile_size, alpha_threshold, transmittance_threshold,
+                              chi_squared_threshold);
     if (st) return st;
     if (!image) return GS_ERR_INVALID_ARGUMENT;
+    if (display && tile_size != kTile) return GS_ERR_UNSUPPORTED;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     const int tiles_y = (height + tile_size - 1) / tile_size;
     if (n_tiles < tiles_x * tiles_y) {
         // pixels of tiles without an offset entry stay zero (the reference zero-initialises)
-        st = zero_bytes(image, (size_t)width * height * 3 * sizeof(float), stream);
+        const size_t bytes = (size_t)width * height * 3 * sizeof(float);
+        st = zero_bytes(image, bytes, stream);
+        if (!st && display) st = zero_bytes(display, bytes, stream);
         if (st) return st;
     }
     if (n_tiles == 0) return GS_OK;
@@ -736,7 +761,7 @@ extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gauss
                            indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
-                           image);
+                           image, display);
     } else {
         hipLaunchKernelGGL(blend_forward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, indexing_offset,
@@ -748,20 +773,49 @@ extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gauss
     return launch_status();
 }
 
-extern "C" int gs_rasterize_backward(
+extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                            int32_t n_tiles, int64_t k, const float *points_image,
+                            const float *cov_inv_image, const float *opacities,
+                            const float *colors, int64_t n, int32_t width, int32_t height,
+                            int32_t tile_size, float alpha_threshold,
+                            float transmittance_threshold, float chi_squared_threshold,
+                            float *image, hipStream_t stream) {
+    return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
+                          cov_inv_image, opacities, colors, n, width, height, tile_size,
+                          alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
+                          nullptr, stream);
+}
+
+extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
+                                    const int32_t *gaussian_ids_sorted, int32_t n_tiles,
+                                    int64_t k, const float *points_image,
+                                    const float *cov_inv_image, const float *opacities,
+                                    const float *colors, int64_t n, int32_t width,
+                                    int32_t height, int32_t tile_size, float alpha_threshold,
+                                    float transmittance_threshold, float chi_squared_threshold,
+                                    float *image, float *display, hipStream_t stream) {
+    if (!display) return GS_ERR_INVALID_ARGUMENT;
+    return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
+                          cov_inv_image, opacities, colors, n, width, height, tile_size,
+                          alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
+                          display, stream);
+}
+
+static int rasterize_backward_impl(
     const float *grad_image, const float *image, const int32_t *indexing_offset,
     const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k, const float *points_image,
     const float *cov_inv_image, const float *opacities, const float *colors, int64_t n,
     int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
     float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
     float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
-    hipStream_t stream) {
+    bool display, hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
-                              tile_size, alpha_threshold,
-                              transmittance_threshold, chi_squared_threshold);
+                              tile_size, alpha_threshold, transmittance_threshold,
+                              chi_squared_threshold);
     if (st) return st;
     if (n > 0 && (!grad_points_image || !grad_cov_inv_image || !grad_opacities || !grad_colors))
         return GS_ERR_INVALID_ARGUMENT;
+    if (display && (!image || tile_size != kTile)) return GS_ERR_INVALID_ARGUMENT;
     if (n > 0 && !accumulate) {
         st = zero_bytes(grad_points_image, (size_t)n * 2 * sizeof(float), stream);
         if (!st) st = zero_bytes(grad_cov_inv_image, (size_t)n * 3 * sizeof(float), stream);
@@ -774,11 +828,20 @@ extern "C" int gs_rasterize_backward(
         return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     if (tile_size == kTile) {
-        hipLaunchKernelGGL(blend_backward_kernel, dim3(n_tiles), dim3(kWave), 0, stream,
-                           grad_image, image, indexing_offset, gaussian_ids_sorted, n_tiles, k,
-                           n, points_image, cov_inv_image, opacities, colors, tiles_x, width, height,
-                           alpha_threshold, transmittance_threshold, chi_squared_threshold,
-                           grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors);
+        if (display)
+            hipLaunchKernelGGL(blend_backward_kernel<true>, dim3(n_tiles), dim3(kWave), 0, stream,
+                               grad_image, image, indexing_offset, gaussian_ids_sorted, n_tiles,
+                               k, n, points_image, cov_inv_image, opacities, colors, tiles_x,
+                               width, height, alpha_threshold, transmittance_threshold,
+                               chi_squared_threshold, grad_points_image, grad_cov_inv_image,
+                               grad_opacities, grad_colors);
+        else
+            hipLaunchKernelGGL(blend_backward_kernel<false>, dim3(n_tiles), dim3(kWave), 0,
+                               stream, grad_image, image, indexing_offset, gaussian_ids_sorted,
+                               n_tiles, k, n, points_image, cov_inv_image, opacities, colors,
+                               tiles_x, width, height, alpha_threshold, transmittance_threshold,
+                               chi_squared_threshold, grad_points_image, grad_cov_inv_image,
+                               grad_opacities, grad_colors);
     } else {
         hipLaunchKernelGGL(blend_backward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, grad_image, image,
@@ -788,6 +851,38 @@ extern "C" int gs_rasterize_backward(
                            grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors);
     }
     return launch_status();
+}
+
+extern "C" int gs_rasterize_backward(
+    const float *grad_image, const float *image, const int32_t *indexing_offset,
+    const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k, const float *points_image,
+    const float *cov_inv_image, const float *opacities, const float *colors, int64_t n,
+    int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
+    float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
+    float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
+    hipStream_t stream) {
+    return rasterize_backward_impl(grad_image, image, indexing_offset, gaussian_ids_sorted,
+                                   n_tiles, k, points_image, cov_inv_image, opacities, colors, n,
+                                   width, height, tile_size, alpha_threshold,
+                                   transmittance_threshold, chi_squared_threshold,
+                                   grad_points_image, grad_cov_inv_image, grad_opacities,
+                                   grad_colors, accumulate, false, stream);
+}
+
+extern "C" int gs_rasterize_display_backward(
+    const float *grad_display, const float *image, const int32_t *indexing_offset,
+    const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k, const float *points_image,
+    const float *cov_inv_image, const float *opacities, const float *colors, int64_t n,
+    int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
+    float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
+    float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
+    hipStream_t stream) {
+    return rasterize_backward_impl(grad_display, image, indexing_offset, gaussian_ids_sorted,
+                                   n_tiles, k, points_image, cov_inv_image, opacities, colors, n,
+                                   width, height, tile_size, alpha_threshold,
+                                   transmittance_threshold, chi_squared_threshold,
+                                   grad_points_image, grad_cov_inv_image, grad_opacities,
+                                   grad_colors, accumulate, true, stream);
 }
 
 extern "C" int gs_rasterize_work(const int32_t *indexing_offset,

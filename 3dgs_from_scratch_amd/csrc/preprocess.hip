@@ -74,92 +74,190 @@ __global__ __launch_bounds__(kPreBlock) void project_points_backward_kernel(
     grad_quats[4 * i + 3] = gq[3];
 }
 
-// SH evaluation (src/gaussian.py:24-61; data flow of src/cuda/kernel.cu:545-617).
-// The API's output is the raw SH sum (or its sigmoid); the caller applies the
-// max(c + 0.5, 0) shift (src/cuda/wrapper.py:264-265).
-__global__ __launch_bounds__(kPreBlock) void sh_forward_kernel(
-    int64_t n, const float *__restrict__ cam_pos, const float *__restrict__ means,
-    const float *__restrict__ sh_dc, const float *__restrict__ sh_rest,
-    const uint8_t *__restrict__ mask, int sh_sigmoid, float *__restrict__ colors) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// ---------------------------------------------------------------- SH
+// SH evaluation (src/gaussian.py:24-61; data flow of src/cuda/kernel.cu:545-617)
+// and its gradient (src/cuda/kernel.cu:619-782), one thread per Gaussian.  The
+// backward moves the kShBlock sh_rest rows of its block (45 floats each,
+// 180 B) between HBM and LDS with coalesced 16-byte accesses and reads /
+// writes them per Gaussian in LDS, so each gradient line is written once
+// (per-thread 180-byte row stores write partially filled lines, measured at
+// 1.5x the gradient's bytes).  The forward only loads its rows and reads them
+// directly (measured faster than staging).
+//
+// Output modes: kShRaw (the API's raw sum), kShSigmoid (its sigmoid) and
+// kShRender (max(raw + 0.5, 0) as render() applies it, src/cuda/wrapper.py:264-265;
+// masked rows are then 0.5, as 0 + 0.5 is in the reference).  The camera
+// position is either given or computed as -R^T t from world_to_camera.
+
+constexpr int kShBlock = 128;
+constexpr int kRest = 45;
+enum ShMode { kShRaw = 0, kShSigmoid = 1, kShRender = 2 };
+
+__device__ __forceinline__ void camera_position(const float *__restrict__ cam_pos,
+                                                const float *__restrict__ w2c, float &cx,
+                                                float &cy, float &cz) {
+    if (cam_pos) {
+        cx = cam_pos[0];
+        cy = cam_pos[1];
+        cz = cam_pos[2];
+    } else {  // -R^T t, R = rows 0..2 / cols 0..2, t = column 3 (row-major 4x4)
+        cx = -(w2c[0] * w2c[3] + w2c[4] * w2c[7] + w2c[8] * w2c[11]);
+        cy = -(w2c[1] * w2c[3] + w2c[5] * w2c[7] + w2c[9] * w2c[11]);
+        cz = -(w2c[2] * w2c[3] + w2c[6] * w2c[7] + w2c[10] * w2c[11]);
+    }
+}
+
+// Copies `count` (<= kShBlock * kRest) floats between global memory and LDS with
+// the block's threads: every thread issues all its loads before its stores (a
+// fully unrolled register stage), 16 bytes per access when the global side is
+// 16-byte aligned.
+template <bool kToLds>
+__device__ __forceinline__ void block_copy(float *__restrict__ lds, float *__restrict__ glob,
+                                           int count) {
+    constexpr int kMax4 = kShBlock * kRest / 4;
+    constexpr int kIters = (kMax4 + kShBlock - 1) / kShBlock;
+    static_assert(kShBlock * kRest % 4 == 0, "rows of a block must fill whole float4s");
+    const int tid = threadIdx.x;  // count >= kRest, so n4 >= 11 below
+    float *src = kToLds ? glob : lds;
+    float *dst = kToLds ? lds : glob;
+    if ((reinterpret_cast<uintptr_t>(glob) & 15) == 0) {
+        const int n4 = count >> 2;
+        const float4 *s4 = reinterpret_cast<const float4 *>(src);
+        float4 *d4 = reinterpret_cast<float4 *>(dst);
+        float4 v[kIters];
+#pragma unroll
+        for (int it = 0; it < kIters; ++it) {  // unconditional (clamped) loads stay in registers
+            v[it] = s4[min(tid + it * kShBlock, n4 - 1)];
+        }
+#pragma unroll
+        for (int it = 0; it < kIters; ++it) {
+            const int i = tid + it * kShBlock;
+            if (i < n4) d4[i] = v[it];
+        }
+        for (int i = (n4 << 2) + tid; i < count; i += kShBlock) dst[i] = src[i];
+    } else {  // misaligned caller view: plain loop
+        for (int i = tid; i < count; i += kShBlock) dst[i] = src[i];
+    }
+}
+
+__global__ __launch_bounds__(kShBlock) void sh_forward_kernel(
+    int64_t n, const float *__restrict__ cam_pos, const float *__restrict__ w2c,
+    const float *__restrict__ means, const float *__restrict__ sh_dc,
+    const float *__restrict__ sh_rest, const uint8_t *__restrict__ mask, int mode,
+    float *__restrict__ colors) {
+    const int64_t i = (int64_t)blockIdx.x * kShBlock + threadIdx.x;
     if (i >= n) return;
     float rgb[3] = {0.f, 0.f, 0.f};
     if (mask[i]) {
-        const float dx = means[3 * i] - cam_pos[0];
-        const float dy = means[3 * i + 1] - cam_pos[1];
-        const float dz = means[3 * i + 2] - cam_pos[2];
+        float cx, cy, cz;
+        camera_position(cam_pos, w2c, cx, cy, cz);
+        const float dx = means[3 * i] - cx;
+        const float dy = means[3 * i + 1] - cy;
+        const float dz = means[3 * i + 2] - cz;
         const float norm = sqrtf(dx * dx + dy * dy + dz * dz);
         float b[15];
         sh_basis_rest(dx / norm, dy / norm, dz / norm, b);
-        const float *rest = sh_rest + 45 * i;
+        const float *rest = sh_rest + kRest * i;  // 15 x 12-byte loads per thread
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             float acc = kShC0 * sh_dc[3 * i + c];
 #pragma unroll
             for (int k = 0; k < 15; ++k) acc += b[k] * rest[3 * k + c];
-            rgb[c] = sh_sigmoid ? 1.0f / (1.0f + expf(-acc)) : acc;
+            rgb[c] = acc;
         }
     }
-    colors[3 * i] = rgb[0];
-    colors[3 * i + 1] = rgb[1];
-    colors[3 * i + 2] = rgb[2];
-}
-
-// SH gradient (data flow of src/cuda/kernel.cu:619-782).
-__global__ __launch_bounds__(kPreBlock) void sh_backward_kernel(
-    int64_t n, const float *__restrict__ grad_colors, const float *__restrict__ cam_pos,
-    const float *__restrict__ means, const float *__restrict__ sh_rest,
-    const float *__restrict__ colors, const uint8_t *__restrict__ mask, int sh_sigmoid,
-    float *__restrict__ grad_means, float *__restrict__ grad_dc,
-    float *__restrict__ grad_rest) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    float *gr = grad_rest + 45 * i;
-    if (!mask[i]) {
-        grad_means[3 * i] = grad_means[3 * i + 1] = grad_means[3 * i + 2] = 0.0f;
-        grad_dc[3 * i] = grad_dc[3 * i + 1] = grad_dc[3 * i + 2] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 45; ++k) gr[k] = 0.0f;
-        return;
-    }
-    float g[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        g[c] = grad_colors[3 * i + c];
-        if (sh_sigmoid) {
-            const float s = colors[3 * i + c];
-            g[c] *= s * (1.0f - s);
+        float v = rgb[c];
+        if (mode == kShSigmoid && mask[i]) v = 1.0f / (1.0f + expf(-v));
+        if (mode == kShRender) {
+            v = v + 0.5f;
+            v = v < 0.0f ? 0.0f : v;  // clamp_min keeping NaN
         }
-        grad_dc[3 * i + c] = kShC0 * g[c];
+        colors[3 * i + c] = v;
     }
-    const float dx = means[3 * i] - cam_pos[0];
-    const float dy = means[3 * i + 1] - cam_pos[1];
-    const float dz = means[3 * i + 2] - cam_pos[2];
-    const float norm = sqrtf(dx * dx + dy * dy + dz * dz);
-    const float x = dx / norm, y = dy / norm, z = dz / norm;
-    float b[15], bx[15], by[15], bz[15];
-    sh_basis_rest(x, y, z, b);
-    sh_basis_rest_grad(x, y, z, bx, by, bz);
-    const float *rest = sh_rest + 45 * i;
-    float gdx = 0.f, gdy = 0.f, gdz = 0.f;
+}
+
+__global__ __launch_bounds__(kShBlock) void sh_backward_kernel(
+    int64_t n, const float *__restrict__ grad_colors, const float *__restrict__ cam_pos,
+    const float *__restrict__ w2c, const float *__restrict__ means,
+    const float *__restrict__ sh_dc, const float *__restrict__ sh_rest,
+    const float *__restrict__ colors, const uint8_t *__restrict__ mask, int mode,
+    float *__restrict__ grad_means, float *__restrict__ grad_dc,
+    float *__restrict__ grad_rest) {
+    __shared__ __align__(16) float rest_lds[kShBlock * kRest];
+    const int64_t first = (int64_t)blockIdx.x * kShBlock;
+    const int nb = (int)min((int64_t)kShBlock, n - first);
+    block_copy<true>(rest_lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb);
+    __syncthreads();
+    const int t = threadIdx.x;
+    float *lrest = rest_lds + kRest * t;  // row read in full below, then overwritten by its gradient
+    if (t < nb) {
+        const int64_t i = first + t;
+        float gm[3] = {0.f, 0.f, 0.f}, gdc[3] = {0.f, 0.f, 0.f};
+        if (mask[i]) {
+            float cx, cy, cz;
+            camera_position(cam_pos, w2c, cx, cy, cz);
+            const float dx = means[3 * i] - cx;
+            const float dy = means[3 * i + 1] - cy;
+            const float dz = means[3 * i + 2] - cz;
+            const float norm = sqrtf(dx * dx + dy * dy + dz * dz);
+            const float x = dx / norm, y = dy / norm, z = dz / norm;
+            float b[15], bx[15], by[15], bz[15];
+            sh_basis_rest(x, y, z, b);
+            sh_basis_rest_grad(x, y, z, bx, by, bz);
+            float g[3];
 #pragma unroll
-    for (int k = 0; k < 15; ++k) {
-        gr[3 * k] = b[k] * g[0];
-        gr[3 * k + 1] = b[k] * g[1];
-        gr[3 * k + 2] = b[k] * g[2];
-        const float gk = g[0] * rest[3 * k] + g[1] * rest[3 * k + 1] + g[2] * rest[3 * k + 2];
-        gdx += gk * bx[k];
-        gdy += gk * by[k];
-        gdz += gk * bz[k];
+            for (int c = 0; c < 3; ++c) {
+                g[c] = grad_colors[3 * i + c];
+                if (mode == kShSigmoid) {
+                    const float s = colors[3 * i + c];
+                    g[c] *= s * (1.0f - s);
+                } else if (mode == kShRender) {
+                    // clamp_min(raw + 0.5, 0) passes the gradient where raw + 0.5 >= 0
+                    float raw = kShC0 * sh_dc[3 * i + c];
+#pragma unroll
+                    for (int k = 0; k < 15; ++k) raw += b[k] * lrest[3 * k + c];
+                    if (!(raw + 0.5f >= 0.0f)) g[c] = 0.0f;
+                }
+                gdc[c] = kShC0 * g[c];
+            }
+            float gdx = 0.f, gdy = 0.f, gdz = 0.f;
+#pragma unroll
+            for (int k = 0; k < 15; ++k) {
+                const float gk = g[0] * lrest[3 * k] + g[1] * lrest[3 * k + 1] +
+                                 g[2] * lrest[3 * k + 2];
+                gdx += gk * bx[k];
+                gdy += gk * by[k];
+                gdz += gk * bz[k];
+            }
+#pragma unroll
+            for (int k = 0; k < 15; ++k) {
+                lrest[3 * k] = b[k] * g[0];
+                lrest[3 * k + 1] = b[k] * g[1];
+                lrest[3 * k + 2] = b[k] * g[2];
+            }
+            // dir = d / |d| -> (I - dir dir^T) / |d|
+            const float dot = x * gdx + y * gdy + z * gdz;
+            gm[0] = (gdx - x * dot) / norm;
+            gm[1] = (gdy - y * dot) / norm;
+            gm[2] = (gdz - z * dot) / norm;
+        } else {
+#pragma unroll
+            for (int k = 0; k < kRest; ++k) lrest[k] = 0.0f;
+        }
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            grad_means[3 * i + c] = gm[c];
+            grad_dc[3 * i + c] = gdc[c];
+        }
     }
-    // dir = d / |d| -> (I - dir dir^T) / |d|
-    const float dot = x * gdx + y * gdy + z * gdz;
-    grad_means[3 * i] = (gdx - x * dot) / norm;
-    grad_means[3 * i + 1] = (gdy - y * dot) / norm;
-    grad_means[3 * i + 2] = (gdz - z * dot) / norm;
+    __syncthreads();
+    block_copy<false>(rest_lds, grad_rest + kRest * first, kRest * nb);
 }
 
 }  // namespace gs
+
 
 using namespace gs;
 
@@ -204,17 +302,41 @@ extern "C" int gs_project_points_backward(
     return launch_status();
 }
 
+static int launch_sh_forward(const float *camera_pos, const float *w2c, const float *means,
+                             const float *sh_dc, const float *sh_rest, const uint8_t *mask,
+                             int64_t n, int mode, float *colors, hipStream_t stream) {
+    if (n < 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GS_OK;
+    if ((!camera_pos && !w2c) || !means || !sh_dc || !sh_rest || !mask || !colors)
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(sh_forward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
+                       stream, n, camera_pos, w2c, means, sh_dc, sh_rest, mask, mode, colors);
+    return launch_status();
+}
+
+static int launch_sh_backward(const float *grad_colors, const float *camera_pos,
+                              const float *w2c, const float *means, const float *sh_dc,
+                              const float *sh_rest, const float *colors, const uint8_t *mask,
+                              int64_t n, int mode, float *grad_means, float *grad_sh_dc,
+                              float *grad_sh_rest, hipStream_t stream) {
+    if (n < 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GS_OK;
+    if (!grad_colors || (!camera_pos && !w2c) || !means || !sh_rest || !mask || !grad_means ||
+        !grad_sh_dc || !grad_sh_rest || (mode == kShSigmoid && !colors) ||
+        (mode == kShRender && !sh_dc))
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(sh_backward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
+                       stream, n, grad_colors, camera_pos, w2c, means, sh_dc, sh_rest, colors,
+                       mask, mode, grad_means, grad_sh_dc, grad_sh_rest);
+    return launch_status();
+}
+
 extern "C" int gs_evaluate_sh(const float *camera_pos, const float *means, const float *sh_dc,
                               const float *sh_rest, const uint8_t *mask, int64_t n,
                               int32_t sh_sigmoid, float *colors, hipStream_t stream) {
-    if (n < 0) return GS_ERR_INVALID_ARGUMENT;
-    if (n == 0) return GS_OK;
-    if (!camera_pos || !means || !sh_dc || !sh_rest || !mask || !colors)
-        return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(sh_forward_kernel, dim3(ceil_div(n, kPreBlock)), dim3(kPreBlock), 0,
-                       stream, n, camera_pos, means, sh_dc, sh_rest, mask, (int)sh_sigmoid,
-                       colors);
-    return launch_status();
+    if (!camera_pos && n > 0) return GS_ERR_INVALID_ARGUMENT;
+    return launch_sh_forward(camera_pos, nullptr, means, sh_dc, sh_rest, mask, n,
+                             sh_sigmoid ? kShSigmoid : kShRaw, colors, stream);
 }
 
 extern "C" int gs_evaluate_sh_backward(const float *grad_colors, const float *camera_pos,
@@ -223,14 +345,29 @@ extern "C" int gs_evaluate_sh_backward(const float *grad_colors, const float *ca
                                        const uint8_t *mask, int64_t n, int32_t sh_sigmoid,
                                        float *grad_means, float *grad_sh_dc,
                                        float *grad_sh_rest, hipStream_t stream) {
-    (void)sh_dc;  // the gradient is linear in the coefficients
-    if (n < 0) return GS_ERR_INVALID_ARGUMENT;
-    if (n == 0) return GS_OK;
-    if (!grad_colors || !camera_pos || !means || !sh_rest || !mask || !grad_means ||
-        !grad_sh_dc || !grad_sh_rest || (sh_sigmoid && !colors))
-        return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(sh_backward_kernel, dim3(ceil_div(n, kPreBlock)), dim3(kPreBlock), 0,
-                       stream, n, grad_colors, camera_pos, means, sh_rest, colors, mask,
-                       (int)sh_sigmoid, grad_means, grad_sh_dc, grad_sh_rest);
-    return launch_status();
+    if (!camera_pos && n > 0) return GS_ERR_INVALID_ARGUMENT;
+    return launch_sh_backward(grad_colors, camera_pos, nullptr, means, sh_dc, sh_rest, colors,
+                              mask, n, sh_sigmoid ? kShSigmoid : kShRaw, grad_means,
+                              grad_sh_dc, grad_sh_rest, stream);
+}
+
+extern "C" int gs_evaluate_sh_render(const float *world_to_camera, const float *means,
+                                     const float *sh_dc, const float *sh_rest,
+                                     const uint8_t *mask, int64_t n, float *colors,
+                                     hipStream_t stream) {
+    if (!world_to_camera && n > 0) return GS_ERR_INVALID_ARGUMENT;
+    return launch_sh_forward(nullptr, world_to_camera, means, sh_dc, sh_rest, mask, n,
+                             kShRender, colors, stream);
+}
+
+extern "C" int gs_evaluate_sh_render_backward(const float *grad_colors,
+                                              const float *world_to_camera, const float *means,
+                                              const float *sh_dc, const float *sh_rest,
+                                              const uint8_t *mask, int64_t n,
+                                              float *grad_means, float *grad_sh_dc,
+                                              float *grad_sh_rest, hipStream_t stream) {
+    if (!world_to_camera && n > 0) return GS_ERR_INVALID_ARGUMENT;
+    return launch_sh_backward(grad_colors, nullptr, world_to_camera, means, sh_dc, sh_rest,
+                              nullptr, mask, n, kShRender, grad_means, grad_sh_dc, grad_sh_rest,
+                              stream);
 }

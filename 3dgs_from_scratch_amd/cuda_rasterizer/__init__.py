@@ -40,6 +40,10 @@ __all__ = [
     "rasterize",
     "rasterize_backward",
     "rasterize_work",
+    "evaluate_spherical_harmonics_render",
+    "evaluate_spherical_harmonics_render_backward",
+    "rasterize_display",
+    "rasterize_display_backward",
     "RasterizerError",
 ]
 
@@ -359,6 +363,13 @@ def rasterize(
     return image
 
 
+def _zeroed_blend_grads(n, dev):
+    """Four zeroed gradient outputs (N,2), (N,3), (N,), (N,3) carved from one buffer."""
+    buf = torch.zeros((9 * n,), dtype=torch.float32, device=dev)
+    return (buf[: 2 * n].view(n, 2), buf[2 * n : 5 * n].view(n, 3), buf[5 * n : 6 * n],
+            buf[6 * n :].view(n, 3))
+
+
 def rasterize_backward(
     grad_rendered_image,
     indexing_offset,
@@ -389,11 +400,9 @@ def rasterize_backward(
     img = None
     if rendered_image is not None:
         img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
-    # zeroed here so that the library call (and its timing events) is the blend kernel alone
-    g_pts = torch.zeros((n, 2), dtype=f32, device=dev)
-    g_conic = torch.zeros((n, 3), dtype=f32, device=dev)
-    g_opac = torch.zeros((n,), dtype=f32, device=dev)
-    g_col = torch.zeros((n, 3), dtype=f32, device=dev)
+    # zeroed here (one fill) so that the library call and its timing events are the
+    # blend kernel alone
+    g_pts, g_conic, g_opac, g_col = _zeroed_blend_grads(n, dev)
     with torch.cuda.device(dev):
         ev = _lib.timer.record("rasterize_backward", dev)
         _lib.check(
@@ -432,3 +441,119 @@ def rasterize_work(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_i
         )
     visited, composited = counters.tolist()
     return visited, composited
+
+
+# ------------------------------------------------------------- render() fusions
+# Fused forms of the glue render() puts around the seven functions
+# (src/cuda/wrapper.py:223-294).  Results equal the unfused sequence; used by
+# cuda_rasterizer.wrapper.render.
+
+
+def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs_dc,
+                                        sh_coeffs_rest, mask):
+    """max(evaluate_spherical_harmonics(-R^T t, ...) + 0.5, 0) in one kernel
+    (src/cuda/wrapper.py:260-265).  Masked rows are 0.5."""
+    dev = _device_of(points_world)
+    n = points_world.shape[0]
+    f32 = torch.float32
+    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
+    points_world = _prep(points_world, "points_world", f32, (n, 3), dev)
+    sh_coeffs_dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+    sh_coeffs_rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    colors = torch.empty((n, 3), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("evaluate_sh_render", dev)
+        _lib.check(
+            _lib.load().gs_evaluate_sh_render(
+                _ptr(world_to_camera), _ptr(points_world), _ptr(sh_coeffs_dc),
+                _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(colors), _stream(dev),
+            ),
+            "evaluate_spherical_harmonics_render",
+        )
+        _lib.timer.stop(ev, dev)
+    return colors
+
+
+def evaluate_spherical_harmonics_render_backward(grad_colors, world_to_camera, points_world,
+                                                 sh_coeffs_dc, sh_coeffs_rest, mask):
+    """Gradient of evaluate_spherical_harmonics_render.  Returns
+    (grad_points_world[N,3], grad_sh_coeffs_dc[N,3], grad_sh_coeffs_rest[N,15,3])."""
+    dev = _device_of(points_world)
+    n = points_world.shape[0]
+    f32 = torch.float32
+    grad_colors = _prep(grad_colors, "grad_colors", f32, (n, 3), dev)
+    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
+    points_world = _prep(points_world, "points_world", f32, (n, 3), dev)
+    sh_coeffs_dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+    sh_coeffs_rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    g_means = torch.empty((n, 3), dtype=f32, device=dev)
+    g_dc = torch.empty((n, 3), dtype=f32, device=dev)
+    g_rest = torch.empty((n, 15, 3), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("evaluate_sh_render_backward", dev)
+        _lib.check(
+            _lib.load().gs_evaluate_sh_render_backward(
+                _ptr(grad_colors), _ptr(world_to_camera), _ptr(points_world), _ptr(sh_coeffs_dc),
+                _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(g_means), _ptr(g_dc), _ptr(g_rest),
+                _stream(dev),
+            ),
+            "evaluate_spherical_harmonics_render_backward",
+        )
+        _lib.timer.stop(ev, dev)
+    return g_means, g_dc, g_rest
+
+
+def rasterize_display(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
+                      opacities, colors, width, height, tile_size, alpha_threshold,
+                      transmittance_threshold, chi_squared_threshold):
+    """rasterize() that also returns clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294).
+    Returns (image[H,W,3] un-clamped, display[H,W,3])."""
+    dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
+        indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
+    width, height = int(width), int(height)
+    image = torch.empty((height, width, 3), dtype=torch.float32, device=dev)
+    display = torch.empty((height, width, 3), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("rasterize_display", dev)
+        _lib.check(
+            _lib.load().gs_rasterize_display(
+                _ptr(off), _ptr(ids), off.shape[0], ids.shape[0], _ptr(pts), _ptr(conic),
+                _ptr(opac), _ptr(col), n, width, height, int(tile_size), float(alpha_threshold),
+                float(transmittance_threshold), float(chi_squared_threshold), _ptr(image),
+                _ptr(display), _stream(dev),
+            ),
+            "rasterize_display",
+        )
+        _lib.timer.stop(ev, dev)
+    return image, display
+
+
+def rasterize_display_backward(grad_display, indexing_offset, gaussian_ids_sorted, points_image,
+                               cov_inv_image, opacities, colors, width, height, tile_size,
+                               alpha_threshold, transmittance_threshold, chi_squared_threshold,
+                               rendered_image):
+    """Gradient of rasterize_display's display output; `rendered_image` (its
+    un-clamped image) is required.  Returns the four gradients of rasterize_backward."""
+    dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
+        indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
+    width, height = int(width), int(height)
+    f32 = torch.float32
+    grad = _prep(grad_display, "grad_display", f32, (height, width, 3), dev)
+    img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
+    g_pts, g_conic, g_opac, g_col = _zeroed_blend_grads(n, dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("rasterize_display_backward", dev)
+        _lib.check(
+            _lib.load().gs_rasterize_display_backward(
+                _ptr(grad), _ptr(img), _ptr(off), _ptr(ids), off.shape[0], ids.shape[0],
+                _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, int(tile_size),
+                float(alpha_threshold), float(transmittance_threshold),
+                float(chi_squared_threshold), _ptr(g_pts), _ptr(g_conic), _ptr(g_opac),
+                _ptr(g_col), 1, _stream(dev),
+            ),
+            "rasterize_display_backward",
+        )
+        _lib.timer.stop(ev, dev)
+    return g_pts, g_conic, g_opac, g_col

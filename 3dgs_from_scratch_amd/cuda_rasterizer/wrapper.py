@@ -7,9 +7,16 @@ points_img[N,2], radii[N,2]).  `points_img` is a non-leaf tensor whose
 `.grad` (after `retain_grad()`) is dL/d(points_img), as the reference's
 densification strategy expects (src/strategy.py:47-68).
 
-Difference from the reference glue: RasterizeFunction saves its forward image
-and hands it to the backward kernel, so the backward does not recompute each
-pixel's colour (src/cuda/kernel.cu:1032-1060 replays the whole forward pass).
+Differences from the reference glue (same values and gradients):
+- RasterizeFunction saves its forward image and hands it to the backward
+  kernel, so the backward does not recompute each pixel's colour
+  (src/cuda/kernel.cu:1032-1060 replays the whole forward pass).
+- render() uses fused kernels for the glue around the seven functions: the
+  camera position, SH and max(c + 0.5, 0) in one kernel (RenderColorsFunction),
+  and the blend writing clamp(image, 0, 1) * 255 itself, with the clamp's
+  gradient applied inside the blend backward (RenderRasterizeFunction).
+- ProjectPointsFunction marks depths, radii and mask non-differentiable, so
+  autograd allocates no zero gradients for them.
 """
 
 from __future__ import annotations
@@ -32,12 +39,16 @@ class ProjectPointsFunction(torch.autograd.Function):
                               cov_img, mask)
         ctx.width = width
         ctx.height = height
+        ctx.mark_non_differentiable(depths, radii, mask)
+        ctx.set_materialize_grads(False)
         return points_img, depths, cov_inv_img, radii, mask
 
     @staticmethod
     def backward(ctx, grad_points_img, grad_depths, grad_cov_inv_img, grad_radii, grad_mask):
         means, scales, quaternions, opacities, world_to_camera, intrinsic, cov_img, mask = (
             ctx.saved_tensors)
+        if grad_points_img is None and grad_cov_inv_img is None:
+            return (None,) * 13
         if grad_points_img is None:
             grad_points_img = torch.zeros((means.shape[0], 2), dtype=means.dtype,
                                           device=means.device)
@@ -68,6 +79,52 @@ class SphericalHarmonicsFunction(torch.autograd.Function):
             grad_colors, camera_pos, means, sh_coeffs_dc, sh_coeffs_rest, colors, mask,
             ctx.sh_sigmoid)
         return None, g_means, g_dc, g_rest, None, None
+
+
+class RenderColorsFunction(torch.autograd.Function):
+    """Camera position, SH and max(c + 0.5, 0) of render() (src/cuda/wrapper.py:260-265)
+    as one kernel each way."""
+
+    @staticmethod
+    def forward(ctx, world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask):
+        colors = _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_coeffs_dc,
+                                                         sh_coeffs_rest, mask)
+        ctx.save_for_backward(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask)
+        return colors
+
+    @staticmethod
+    def backward(ctx, grad_colors):
+        world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask = ctx.saved_tensors
+        g_means, g_dc, g_rest = _cr.evaluate_spherical_harmonics_render_backward(
+            grad_colors, world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask)
+        return None, g_means, g_dc, g_rest, None
+
+
+class RenderRasterizeFunction(torch.autograd.Function):
+    """rasterize followed by clamp(0, 1) * 255 (src/cuda/wrapper.py:268-294) in the
+    blend kernels; returns the display image."""
+
+    @staticmethod
+    def forward(ctx, indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities,
+                colors, width, height, tile_size, alpha_threshold, transmittance_threshold,
+                chi_squared_threshold):
+        image, display = _cr.rasterize_display(
+            indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities, colors,
+            width, height, tile_size, alpha_threshold, transmittance_threshold,
+            chi_squared_threshold)
+        ctx.save_for_backward(indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img,
+                              opacities, colors, image)
+        ctx.params = (width, height, tile_size, alpha_threshold, transmittance_threshold,
+                      chi_squared_threshold)
+        return display
+
+    @staticmethod
+    def backward(ctx, grad_display):
+        offsets, ids, points_img, cov_inv_img, opacities, colors, image = ctx.saved_tensors
+        g_pts, g_conic, g_opac, g_col = _cr.rasterize_display_backward(
+            grad_display, offsets, ids, points_img, cov_inv_img, opacities, colors, *ctx.params,
+            rendered_image=image)
+        return None, None, g_pts, g_conic, g_opac, g_col, None, None, None, None, None, None
 
 
 class RasterizeFunction(torch.autograd.Function):
@@ -121,18 +178,20 @@ def render(
         means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
         far_plane, min_opacity, min_radius, max_radius, width, height)
 
-    camera_pos = -world_to_camera[:3, :3].t() @ world_to_camera[:3, 3]
-    colors = SphericalHarmonicsFunction.apply(camera_pos, means, sh_coeffs_dc, sh_coeffs_rest,
-                                              mask, sh_sigmoid)
-    if not sh_sigmoid:
-        colors = torch.clamp_min(colors + 0.5, 0.0)
+    if sh_sigmoid:
+        camera_pos = -world_to_camera[:3, :3].t() @ world_to_camera[:3, 3]
+        colors = SphericalHarmonicsFunction.apply(camera_pos, means, sh_coeffs_dc,
+                                                  sh_coeffs_rest, mask, True)
+    else:  # max(sh + 0.5, 0), fused
+        colors = RenderColorsFunction.apply(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest,
+                                            mask)
 
     tile_size = 16
     indexing_offset, gaussian_ids_sorted = _cr.compute_tile_intersection(
         points_img.detach(), radii, depths, mask, width, height, tile_size)
 
-    image = RasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img,
-                                    cov_inv_img, opacities, colors, width, height, tile_size,
-                                    alpha_threshold, transmittance_threshold,
-                                    chi_squared_threshold)
-    return image.clamp(0, 1) * 255, points_img, radii
+    display = RenderRasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img,
+                                            cov_inv_img, opacities, colors, width, height,
+                                            tile_size, alpha_threshold, transmittance_threshold,
+                                            chi_squared_threshold)
+    return display, points_img, radii

@@ -215,9 +215,10 @@ def run_gpu(scene: dict, steps: int, warmup: int) -> dict:
 
 # FP32 flops per evaluated (pixel, list entry) pair of the reference blend loop
 # (src/cuda/kernel.cu:954-982 forward; :1063-1106 backward), exp counted as one
-BLEND_FLOP_PER_PAIR = {"rasterize": 22.0, "rasterize_backward": 70.0}
-HBM_STAGES = ("project_points", "evaluate_sh", "bin_count", "bin_sort", "evaluate_sh_backward",
-              "project_points_backward")
+BLEND_FLOP_PER_PAIR = {"rasterize": 22.0, "rasterize_backward": 70.0, "rasterize_display": 22.0,
+                       "rasterize_display_backward": 70.0}
+HBM_STAGES = ("project_points", "evaluate_sh", "evaluate_sh_render", "bin_count", "bin_sort",
+              "evaluate_sh_backward", "evaluate_sh_render_backward", "project_points_backward")
 
 
 def sort_passes(n_tiles: int) -> int:
@@ -232,10 +233,12 @@ def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> floa
     24 B/key, ranges 8 B/key + 4 B/tile)."""
     if stage == "project_points":  # means, scales, quats, opac -> uv, z, cov, conic, radii, mask
         return n * (12 + 12 + 16 + 4) + n * (8 + 4 + 12 + 12 + 8 + 1)
-    if stage == "evaluate_sh":  # means, dc, rest, mask -> colours
+    if stage in ("evaluate_sh", "evaluate_sh_render"):  # means, dc, rest, mask -> colours
         return n * (12 + 12 + 180 + 1) + n * 12
     if stage == "evaluate_sh_backward":  # grad, means, rest, colours, mask -> grads of means, dc, rest
         return n * (12 + 12 + 180 + 12 + 1) + n * (12 + 12 + 180)
+    if stage == "evaluate_sh_render_backward":  # grad, means, dc, rest, mask -> the same grads
+        return n * (12 + 12 + 12 + 180 + 1) + n * (12 + 12 + 180)
     if stage == "project_points_backward":  # grads uv/conic, means, scales, quats, cov, mask -> 3 grads
         return n * (8 + 12 + 12 + 12 + 16 + 12 + 1) + n * (12 + 12 + 16)
     if stage == "bin_count":
@@ -244,15 +247,21 @@ def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> floa
         return k * 12 + 24 * k * sort_passes(n_tiles) + k * 8 + 4 * n_tiles
     if stage == "rasterize":
         return k * 40 + 12 * hw
-    if stage == "rasterize_backward":
+    if stage == "rasterize_display":  # + the clamped x255 image
+        return k * 40 + 24 * hw
+    if stage in ("rasterize_backward", "rasterize_display_backward"):
         return 12 * hw + k * 76 + 36 * n
     return 0.0
 
 
 # kernel that implements each single-kernel entry point
-STAGE_KERNEL = {"rasterize": "blend_forward_kernel", "rasterize_backward": "blend_backward_kernel",
+STAGE_KERNEL = {"rasterize": "blend_forward_kernel", "rasterize_display": "blend_forward_kernel",
+                "rasterize_backward": "blend_backward_kernel<false>",
+                "rasterize_display_backward": "blend_backward_kernel<true>",
                 "project_points": "project_points_kernel", "evaluate_sh": "sh_forward_kernel",
+                "evaluate_sh_render": "sh_forward_kernel",
                 "evaluate_sh_backward": "sh_backward_kernel",
+                "evaluate_sh_render_backward": "sh_backward_kernel",
                 "project_points_backward": "project_points_backward_kernel"}
 
 

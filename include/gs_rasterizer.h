@@ -170,6 +170,49 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
                           float *grad_opacities, float *grad_colors, int32_t accumulate,
                           hipStream_t stream);
 
+/* ------------------------------------------------------- render() fusions */
+
+/*
+ * Fused forms of what render() does around the seven functions
+ * (src/cuda/wrapper.py:223-294); each equals the unfused sequence.  No
+ * counterpart in the reference extension.
+ *
+ * gs_evaluate_sh_render: colors = max(gs_evaluate_sh(camera_pos, ...) + 0.5, 0)
+ *   with camera_pos = -R^T t taken from world_to_camera
+ *   (src/cuda/wrapper.py:260-265); masked rows are 0.5.
+ * gs_evaluate_sh_render_backward: its gradient (the clamp passes the gradient
+ *   where raw + 0.5 >= 0, as torch.clamp_min does).
+ * gs_rasterize_display: gs_rasterize that also writes
+ *   display = clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294); tile_size 16.
+ * gs_rasterize_display_backward: gs_rasterize_backward given the gradient of
+ *   display (image required): the image gradient is grad_display * 255 where
+ *   0 <= image <= 1, else 0.
+ */
+int gs_evaluate_sh_render(const float *world_to_camera, const float *means, const float *sh_dc,
+                          const float *sh_rest, const uint8_t *mask, int64_t n, float *colors,
+                          hipStream_t stream);
+int gs_evaluate_sh_render_backward(const float *grad_colors, const float *world_to_camera,
+                                   const float *means, const float *sh_dc, const float *sh_rest,
+                                   const uint8_t *mask, int64_t n, float *grad_means,
+                                   float *grad_sh_dc, float *grad_sh_rest, hipStream_t stream);
+int gs_rasterize_display(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                         int32_t n_tiles, int64_t k, const float *points_image,
+                         const float *cov_inv_image, const float *opacities, const float *colors,
+                         int64_t n, int32_t width, int32_t height, int32_t tile_size,
+                         float alpha_threshold, float transmittance_threshold,
+                         float chi_squared_threshold, float *image, float *display,
+                         hipStream_t stream);
+int gs_rasterize_display_backward(const float *grad_display, const float *image,
+                                  const int32_t *indexing_offset,
+                                  const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k,
+                                  const float *points_image, const float *cov_inv_image,
+                                  const float *opacities, const float *colors, int64_t n,
+                                  int32_t width, int32_t height, int32_t tile_size,
+                                  float alpha_threshold, float transmittance_threshold,
+                                  float chi_squared_threshold, float *grad_points_image,
+                                  float *grad_cov_inv_image, float *grad_opacities,
+                                  float *grad_colors, int32_t accumulate, hipStream_t stream);
+
 /*
  * Measurement entry (no counterpart in the reference): the work of the
  * reference blend loop (src/cuda/kernel.cu:954-982) for the same inputs as

@@ -81,3 +81,62 @@ def test_render_empty_frame(gpu):
     assert float(img.abs().max()) == 0.0
     assert float(radii.abs().max()) == 0.0
     assert all(float(g.abs().max()) == 0.0 for g in grads.values())
+
+
+def test_fused_colors_equal_unfused_sequence(gpu):
+    """evaluate_spherical_harmonics_render == clamp_min(evaluate_sh(-R^T t) + 0.5, 0),
+    forward and gradient (autograd through the unfused torch sequence)."""
+    import cuda_rasterizer as cr
+
+    p, cam, _ = helpers.scene_orbit(4_000, 160, 120, 220.0, seed=11)
+    g = torch.Generator().manual_seed(5)
+    n = 4_000
+    means = p["means"].to(gpu)
+    dc = (torch.randn(n, 3, generator=g) * 2.0).to(gpu)  # many colours below -0.5 (clamped)
+    rest = p["sh_rest"].to(gpu)
+    mask = (torch.rand(n, generator=g) > 0.2).to(gpu)
+    w2c = cam["w2c"].to(gpu)
+    fused = cr.evaluate_spherical_harmonics_render(w2c, means, dc, rest, mask)
+    cam_pos = -w2c[:3, :3].t() @ w2c[:3, 3]
+    raw = cr.evaluate_spherical_harmonics(cam_pos, means, dc, rest, mask)
+    unfused = torch.clamp_min(raw + 0.5, 0.0)
+    assert float((unfused == 0).float().mean()) > 0.05  # the clamp is exercised
+    assert helpers.max_abs(fused, unfused) <= 1e-6
+    assert torch.all(fused[~mask] == 0.5)
+
+    up = torch.randn(n, 3, generator=g).to(gpu)
+    gm, gdc, grest = cr.evaluate_spherical_harmonics_render_backward(up, w2c, means, dc, rest, mask)
+    clamp_grad = up * ((raw + 0.5) >= 0)
+    rm, rdc, rrest = cr.evaluate_spherical_harmonics_backward(clamp_grad, cam_pos, means, dc, rest,
+                                                              raw, mask, False)
+    for a, b in ((gm, rm), (gdc, rdc), (grest, rrest)):
+        assert helpers.rel_l2(a, b) <= 1e-5
+
+
+def test_display_blend_equals_clamp_of_image(gpu):
+    """rasterize_display: the image is rasterize()'s, display = clamp(image,0,1)*255
+    exactly; its backward equals rasterize_backward of the clamp's gradient."""
+    import cuda_rasterizer as cr
+
+    p, cam, _ = helpers.scene_orbit(6_000, 160, 120, 220.0, seed=12, log_scale=(-3.5, 0.5),
+                                    opacity_std=3.0)
+    scales, quats, opac = helpers.activated(p)
+    d = lambda t: t.to(gpu)  # noqa: E731
+    pts, depths, _, conic, radii, mask = cr.project_points(
+        d(p["means"]), d(scales), d(quats), d(opac), d(cam["w2c"]), d(cam["K"]), 0.01, 100.0,
+        1 / 255, 0.5, 128.0, 160, 120)
+    colors = (torch.rand(6_000, 3, generator=torch.Generator().manual_seed(2)) * 3.0).to(gpu)
+    off, ids = cr.compute_tile_intersection(pts, radii, depths, mask, 160, 120, 16)
+    args = (160, 120, 16, 1e-4, 1e-4, 9.21)
+    ins = (off, ids, pts, conic, d(opac), colors)
+    image = cr.rasterize(*ins, *args)
+    image2, display = cr.rasterize_display(*ins, *args)
+    assert torch.equal(image, image2)
+    assert torch.equal(display, image.clamp(0, 1) * 255)
+    assert float((image > 1).float().mean()) > 0.01  # the upper clamp is exercised
+    up = torch.randn(120, 160, 3, generator=torch.Generator().manual_seed(3)).to(gpu)
+    got = cr.rasterize_display_backward(up, *ins, *args, rendered_image=image)
+    want = cr.rasterize_backward(up * 255 * ((image >= 0) & (image <= 1)), *ins, *args,
+                                 rendered_image=image)
+    for a, b in zip(got, want):
+        assert helpers.rel_l2(a, b) <= 1e-6
