@@ -33,15 +33,19 @@ constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int kRadixMaxBits = 8;
 constexpr int kRadixMax = 1 << kRadixMaxBits;
-constexpr int kEmitItems = 16;  // entries per thread in the fused first tile pass
-constexpr int kEmitTile = kSortThreads * kEmitItems;
-constexpr int kDepthItems = 16;  // keys per thread in the depth sort (N-sized)
-constexpr int kTileItems = 16;  // keys per thread in later tile passes (K-sized)
+constexpr int kSortItems = 16;  // keys per thread in a radix pass
+constexpr int kSortTile = kSortThreads * kSortItems;
+constexpr int kDepthItems = kSortItems;  // the depth sort (N keys)
+constexpr int kTileItems = kSortItems;   // the supertile sort (M keys)
+
+constexpr int kSuper = 8;                       // supertile edge, in tiles
+constexpr int kSuperLocal = kSuper * kSuper;    // tiles per supertile (one mask bit each)
+constexpr int kL2Threads = 256;                 // supertile-list positions per level-2 block
+constexpr int kL2Waves = kL2Threads / kWave;
 
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;
-constexpr int kDirectMaxBlocks = 256;  // passes with <= 256 blocks skip the histogram scan
 
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -142,8 +146,8 @@ struct SortLds {
     uint32_t wave_count[kSortWaves][kRadixMax];
     uint32_t global_start[kRadixMax];
     uint32_t local_start[kRadixMax];
-    uint32_t skeys[kEmitTile];
-    uint32_t svals[kEmitTile];
+    uint32_t skeys[kSortTile];
+    uint32_t svals[kSortTile];
     uint32_t scan_tmp[kSortThreads / kWave + 1];
 };
 
@@ -171,20 +175,39 @@ __device__ __forceinline__ void block_count_digits(const uint32_t (&k)[ITEMS],
     }
 }
 
-// Per-pass histogram tables.  Digit-major (d * nblocks + b) is scanned into
-// first output slots by scan_exclusive; block-major (b * radix + d) is summed
-// directly by every downsweep block when the pass has <= kDirectMaxBlocks blocks.
-template <bool DIRECT>
-__device__ __forceinline__ int64_t hist_index(int d, int b, int nblocks, int radix) {
-    return DIRECT ? (int64_t)b * radix + d : (int64_t)d * nblocks + b;
+// Per-pass histogram table, digit-major: entry d * nblocks + b counts the keys
+// of block b with digit d; digit_scan_kernel turns it in place into the first
+// output position of (digit, block).
+__device__ __forceinline__ int64_t hist_index(int d, int b, int nblocks) {
+    return (int64_t)d * nblocks + b;
+}
+
+// Block d scans column d of the histogram table over the nblocks blocks in
+// place (first position of (d, block) among the keys with digit d) and writes
+// the column total to totals[d].  The downsweep adds the keys of smaller digits.
+__global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
+    uint32_t *__restrict__ table, int nblocks, uint32_t *__restrict__ totals) {
+    __shared__ uint32_t tmp[kScanThreads / kWave + 1];
+    const int d = blockIdx.x;
+    uint32_t run = 0;
+    uint32_t *col = table + (int64_t)d * nblocks;
+    for (int b0 = 0; b0 < nblocks; b0 += kScanThreads) {
+        const int b = b0 + threadIdx.x;
+        const uint32_t c = b < nblocks ? col[b] : 0u;
+        uint32_t chunk;
+        const uint32_t excl = block_exclusive_scan<uint32_t, kScanThreads>(c, tmp, chunk);
+        if (b < nblocks) col[b] = run + excl;
+        run += chunk;
+    }
+    if (threadIdx.x == 0) totals[d] = run;
 }
 
 // Stable rank of the block's keys (registers) by digit, staged through LDS in
-// digit order and written to keys_out/vals_out.  `table` is the scanned
-// digit-major histogram (first output slot of (digit, block)) or, for DIRECT,
-// the raw block-major histogram from which the slots are summed here.  When
-// counts_out is set, counts_out[dst] = touched[value] is written as well.
-template <typename KeyT, int ITEMS, bool DIRECT>
+// digit order and written to keys_out/vals_out.  `table` holds the position of
+// each (digit, block) among the keys of its digit, `totals` the keys per digit.
+// When counts_out is set,
+// counts_out[dst] = touched[value] is written as well.
+template <typename KeyT, int ITEMS>
 __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               const uint32_t (&v)[ITEMS],
                                               const bool (&valid)[ITEMS], int shift, int nbits,
@@ -192,38 +215,22 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               KeyT *__restrict__ keys_out,
                                               uint32_t *__restrict__ vals_out, int64_t n,
                                               bool write_keys, SortLds &s,
+                                              const uint32_t *__restrict__ totals,
                                               const uint32_t *__restrict__ touched = nullptr,
                                               uint64_t *__restrict__ counts_out = nullptr) {
     const int radix = 1 << nbits;
     const uint32_t dmask = (uint32_t)radix - 1u;
     const int wave = threadIdx.x / kWave;
-    for (int d = threadIdx.x; d < radix; d += kSortThreads) {
+    static_assert(kRadixMax <= kSortThreads, "one digit per thread");
+    const int dt = threadIdx.x;
+    const uint32_t tot = dt < radix ? totals[dt] : 0u;
+    const uint32_t first = dt < radix ? table[hist_index(dt, blockIdx.x, nblocks)] : 0u;
+    uint32_t all_keys;
+    const uint32_t smaller = block_exclusive_scan<uint32_t, kSortThreads>(tot, s.scan_tmp, all_keys);
+    if (dt < radix) {
 #pragma unroll
-        for (int w = 0; w < kSortWaves; ++w) s.wave_count[w][d] = 0;
-        if (!DIRECT) s.global_start[d] = table[hist_index<false>(d, blockIdx.x, nblocks, radix)];
-    }
-    if (DIRECT) {
-        uint32_t before = 0, total = 0;
-        if ((int)threadIdx.x < radix) {
-            // 16 independent loads in flight per round (the rows are L2 resident)
-            for (int b0 = 0; b0 < nblocks; b0 += 16) {
-                uint32_t h[16];
-#pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    h[q] = b0 + q < nblocks
-                               ? table[hist_index<true>(threadIdx.x, b0 + q, nblocks, radix)]
-                               : 0u;
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    total += h[q];
-                    before += b0 + q < (int)blockIdx.x ? h[q] : 0u;
-                }
-            }
-        }
-        uint32_t grand;
-        const uint32_t base =
-            block_exclusive_scan<uint32_t, kSortThreads>(total, s.scan_tmp, grand);
-        if ((int)threadIdx.x < radix) s.global_start[threadIdx.x] = base + before;
+        for (int w = 0; w < kSortWaves; ++w) s.wave_count[w][dt] = 0;
+        s.global_start[dt] = smaller + first;
     }
     __syncthreads();
     uint32_t rank[ITEMS];
@@ -276,7 +283,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
 }
 
 // hist[d * nblocks + block] = number of keys of this block with digit d.
-template <typename KeyT, int ITEMS, bool DIRECT>
+template <typename KeyT, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
     const KeyT *__restrict__ keys, int64_t n, int shift, int nbits, int nblocks,
     uint32_t *__restrict__ hist) {
@@ -296,15 +303,16 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
     block_count_digits<ITEMS>(k, valid, shift, nbits, counts);
     __syncthreads();
     for (int d = threadIdx.x; d < radix; d += kSortThreads)
-        hist[hist_index<DIRECT>(d, blockIdx.x, nblocks, radix)] = counts[d];
+        hist[hist_index(d, blockIdx.x, nblocks)] = counts[d];
 }
 
-template <typename KeyT, int ITEMS, bool DIRECT>
+template <typename KeyT, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const KeyT *__restrict__ keys_in, const uint32_t *__restrict__ vals_in,
     KeyT *__restrict__ keys_out, uint32_t *__restrict__ vals_out, int64_t n, int shift,
-    int nbits, int nblocks, const uint32_t *__restrict__ table, int write_keys,
-    const uint32_t *__restrict__ touched, uint64_t *__restrict__ counts_out) {
+    int nbits, int nblocks, const uint32_t *__restrict__ table,
+    const uint32_t *__restrict__ totals, int write_keys, const uint32_t *__restrict__ touched,
+    uint64_t *__restrict__ counts_out) {
     __shared__ SortLds s;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS], v[ITEMS];
@@ -316,8 +324,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
         k[it] = valid[it] ? (uint32_t)keys_in[i] : 0u;
         v[it] = valid[it] ? vals_in[i] : 0u;
     }
-    block_scatter<KeyT, ITEMS, DIRECT>(k, v, valid, shift, nbits, nblocks, table, keys_out,
-                                       vals_out, n, write_keys != 0, s, touched, counts_out);
+    block_scatter<KeyT, ITEMS>(k, v, valid, shift, nbits, nblocks, table, keys_out, vals_out, n,
+                               write_keys != 0, s, totals, touched, counts_out);
 }
 
 struct SortPlan {
@@ -343,216 +351,143 @@ inline int64_t sort_blocks(int64_t n) {
     return (n + kSortThreads * ITEMS - 1) / (kSortThreads * ITEMS);
 }
 
+// Histogram table of one pass, then the kRadixMax digit totals.
+
 template <int ITEMS>
-size_t radix_workspace_bytes(int64_t n) {
-    const int64_t entries = sort_blocks<ITEMS>(n) * kRadixMax;
-    return align256(entries * sizeof(uint32_t)) + scan_workspace_bytes<uint32_t>(entries);
+size_t radix_table_bytes(int64_t n) {
+    return align256((size_t)sort_blocks<ITEMS>(n) * kRadixMax * sizeof(uint32_t));
 }
 
-// One LSD pass from arrays.  With hist_ready the histogram table of this pass
-// (layout by `direct`) was already written into ws by the caller.  With
-// counts_out, counts_out[dst] = touched[value] is written next to the values.
+template <int ITEMS>
+size_t radix_workspace_bytes(int64_t n) {
+    return radix_table_bytes<ITEMS>(n) + align256(kRadixMax * sizeof(uint32_t));
+}
+
+template <int ITEMS>
+uint32_t *radix_totals(void *ws, int64_t n) {
+    return reinterpret_cast<uint32_t *>(reinterpret_cast<char *>(ws) +
+                                        radix_table_bytes<ITEMS>(n));
+}
+
+// One LSD pass from arrays: histogram (unless the caller already wrote this
+// pass's table: hist_ready), digit scan, scatter.  With counts_out, counts_out[dst] = touched[value] is written next to
+// the values.
 template <typename KeyT, int ITEMS>
 int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout, int64_t n,
                int shift, int nbits, bool write_keys, void *ws, hipStream_t stream,
                bool hist_ready = false, const uint32_t *touched = nullptr,
                uint64_t *counts_out = nullptr) {
     const int nblocks = (int)sort_blocks<ITEMS>(n);
-    const bool direct = nblocks <= kDirectMaxBlocks;
-    const int64_t entries = (int64_t)nblocks * kRadixMax;
     uint32_t *hist = reinterpret_cast<uint32_t *>(ws);
-    void *scan_ws = reinterpret_cast<char *>(ws) + align256(entries * sizeof(uint32_t));
+    uint32_t *totals = radix_totals<ITEMS>(ws, n);
     int st;
     if (!hist_ready) {
-        if (direct)
-            hipLaunchKernelGGL((radix_upsweep_kernel<KeyT, ITEMS, true>), dim3(nblocks),
-                               dim3(kSortThreads), 0, stream, kin, n, shift, nbits, nblocks, hist);
-        else
-            hipLaunchKernelGGL((radix_upsweep_kernel<KeyT, ITEMS, false>), dim3(nblocks),
-                               dim3(kSortThreads), 0, stream, kin, n, shift, nbits, nblocks, hist);
+        hipLaunchKernelGGL((radix_upsweep_kernel<KeyT, ITEMS>), dim3(nblocks), dim3(kSortThreads),
+                           0, stream, kin, n, shift, nbits, nblocks, hist);
         st = launch_status();
         if (st) return st;
     }
-    if (direct) {
-        hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, true>), dim3(nblocks),
-                           dim3(kSortThreads), 0, stream, kin, vin, kout, vout, n, shift, nbits,
-                           nblocks, hist, write_keys ? 1 : 0, touched, counts_out);
-        return launch_status();
-    }
-    st = scan_exclusive<uint32_t>(hist, hist, (int64_t)nblocks << nbits, (uint32_t *)nullptr,
-                                  scan_ws, stream);
+    hipLaunchKernelGGL(digit_scan_kernel, dim3(1 << nbits), dim3(kScanThreads), 0, stream, hist,
+                       nblocks, totals);
+    st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, false>), dim3(nblocks),
-                       dim3(kSortThreads), 0, stream, kin, vin, kout, vout, n, shift, nbits,
-                       nblocks, hist, write_keys ? 1 : 0, touched, counts_out);
+    hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS>), dim3(nblocks), dim3(kSortThreads),
+                       0, stream, kin, vin, kout, vout, n, shift, nbits, nblocks, hist,
+                       (const uint32_t *)totals, write_keys ? 1 : 0, touched, counts_out);
     return launch_status();
 }
 
 // ------------------------------------------------------------- binning
 
+// Tile rectangle packed as (tx0 | tx1 << 16, ty0 | ty1 << 16); tile coordinates
+// fit 16 bits (gs_bin_sort rejects larger grids).
+__device__ __forceinline__ uint2 pack_rect(const TileRect &r) {
+    return make_uint2((uint32_t)r.tx0 | ((uint32_t)r.tx1 << 16),
+                      (uint32_t)r.ty0 | ((uint32_t)r.ty1 << 16));
+}
+
+__device__ __forceinline__ TileRect unpack_rect(uint2 p) {
+    TileRect r;
+    r.tx0 = (int)(p.x & 0xffffu);
+    r.tx1 = (int)(p.x >> 16);
+    r.ty0 = (int)(p.y & 0xffffu);
+    r.ty1 = (int)(p.y >> 16);
+    return r;
+}
+
 // tiles_touched and depth sort keys per Gaussian (src/cuda/kernel.cu:784-818),
-// fused with the histogram of the first depth-sort pass.  Gaussians without
-// tiles get the key 0xFFFFFFFF (sorted last; they emit nothing).
-template <int ITEMS, bool DIRECT>
+// fused with the histogram of the first depth-sort pass.  Also writes the
+// number of supertiles (kSuper x kSuper tiles) each Gaussian touches and adds
+// the block's total of tiles_touched to *total_tiles (K).  Gaussians without
+// tiles get the depth key 0xFFFFFFFF (sorted last; they emit nothing).
+template <int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int64_t n, const float *__restrict__ points_image, const float *__restrict__ radii,
     const float *__restrict__ depths, const uint8_t *__restrict__ mask, int width, int height,
-    int tile_size, uint32_t *__restrict__ touched, uint32_t *__restrict__ depth_keys,
-    uint32_t *__restrict__ ids, int nbits, int nblocks, uint32_t *__restrict__ hist) {
+    int tile_size, uint32_t *__restrict__ touched, uint32_t *__restrict__ super_touched,
+    uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys, uint32_t *__restrict__ ids,
+    int nbits, int nblocks, uint32_t *__restrict__ hist,
+    unsigned long long *__restrict__ total_tiles) {
     __shared__ uint32_t counts[kRadixMax];
+    __shared__ uint64_t sum_tmp[kSortThreads / kWave + 1];
     const int radix = 1 << nbits;
     for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS];
     bool valid[ITEMS];
+    uint64_t my_tiles = 0;
+    // all loads first (clamped index, no control dependence) so they overlap
+    float2 pt[ITEMS], rd[ITEMS];
+    float dp[ITEMS];
+    uint8_t mk[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+        const int64_t i0 = base + slot_index<ITEMS>(it);
+        const int64_t i = i0 < n ? i0 : n - 1;
+        pt[it] = reinterpret_cast<const float2 *>(points_image)[i];
+        rd[it] = reinterpret_cast<const float2 *>(radii)[i];
+        dp[it] = depths[i];
+        mk[it] = mask[i];
+    }
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t i = base + slot_index<ITEMS>(it);
         valid[it] = i < n;
         k[it] = 0u;
         if (!valid[it]) continue;
-        uint32_t cnt = 0;
-        if (mask[i]) {
-            TileRect r;
-            if (tile_rect(points_image[2 * i], points_image[2 * i + 1], radii[2 * i],
-                          radii[2 * i + 1], width, height, tile_size, r))
-                cnt = (uint32_t)((r.tx1 - r.tx0 + 1) * (r.ty1 - r.ty0 + 1));
+        uint32_t cnt = 0, scnt = 0;
+        TileRect r{0, 0, 0, 0};
+        if (mk[it] && tile_rect(pt[it].x, pt[it].y, rd[it].x, rd[it].y, width, height,
+                                tile_size, r)) {
+            cnt = (uint32_t)((r.tx1 - r.tx0 + 1) * (r.ty1 - r.ty0 + 1));
+            scnt = (uint32_t)((r.tx1 / kSuper - r.tx0 / kSuper + 1) *
+                              (r.ty1 / kSuper - r.ty0 / kSuper + 1));
         }
-        k[it] = cnt ? __float_as_uint(depths[i]) : 0xFFFFFFFFu;
+        k[it] = cnt ? __float_as_uint(dp[it]) : 0xFFFFFFFFu;
         touched[i] = cnt;
+        super_touched[i] = scnt;
+        rects[i] = pack_rect(r);
         depth_keys[i] = k[it];
         ids[i] = (uint32_t)i;
+        my_tiles += cnt;
     }
-    __syncthreads();
+    uint64_t block_tiles;
+    block_exclusive_scan<uint64_t, kSortThreads>(my_tiles, sum_tmp, block_tiles);
+    if (threadIdx.x == 0 && block_tiles) atomicAdd(total_tiles, (unsigned long long)block_tiles);
     block_count_digits<ITEMS>(k, valid, 0, nbits, counts);
     __syncthreads();
     for (int d = threadIdx.x; d < radix; d += kSortThreads)
-        hist[hist_index<DIRECT>(d, blockIdx.x, nblocks, radix)] = counts[d];
-}
-
-// block_first[b] = depth-order position of the Gaussian whose entries contain
-// entry b * kEmitTile (entries are laid out Gaussian after Gaussian), and
-// block_first[ceil(k / kEmitTile)] = the last Gaussian with entries.
-__global__ __launch_bounds__(256) void block_first_kernel(int64_t n, int64_t k,
-                                                          const uint32_t *__restrict__ order,
-                                                          const uint64_t *__restrict__ offsets,
-                                                          const uint32_t *__restrict__ touched,
-                                                          uint32_t *__restrict__ block_first) {
-    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= n) return;
-    const uint32_t g = order[r];
-    const uint64_t c = g < (uint64_t)n ? touched[g] : 0u;
-    if (c == 0) return;
-    const uint64_t off = offsets[r];
-    const uint64_t end = off + c < (uint64_t)k ? off + c : (uint64_t)k;
-    for (uint64_t b = (off + kEmitTile - 1) / kEmitTile; b * kEmitTile < end; ++b)
-        block_first[b] = (uint32_t)r;
-    if (off < (uint64_t)k && end == (uint64_t)k)
-        block_first[((uint64_t)k + kEmitTile - 1) / kEmitTile] = (uint32_t)r;
+        hist[hist_index(d, blockIdx.x, nblocks)] = counts[d];
 }
 
 struct EmitArgs {
+    const uint2 *rects;       // packed tile rectangle per Gaussian
     const uint32_t *order;    // Gaussians in depth order
     const uint64_t *offsets;  // first entry of each depth-ordered Gaussian
-    const uint32_t *touched;  // tiles per Gaussian (by Gaussian id)
-    const uint32_t *block_first;
-    const float *points;
-    const float *radii;
+    const uint32_t *touched;  // entries per Gaussian (by Gaussian id)
     int64_t n, k;
-    int width, height, tile_size, tiles_x;
+    int tiles_x;              // width of the grid the entries index
 };
-
-constexpr int kEmitGroup = 1024;  // depth-ordered Gaussians staged per round (4 per thread)
-
-struct EmitLds {
-    int32_t off[kEmitGroup];  // first entry relative to the block start (clamped)
-    int32_t end[kEmitGroup];
-    uint32_t gid[kEmitGroup];
-    uint32_t origin[kEmitGroup];  // tx0 | ty0 << 16 of the tile rectangle
-    uint16_t nx[kEmitGroup];      // rectangle width in tiles
-};
-
-// Writes the entries [b*kEmitTile, (b+1)*kEmitTile) of the depth-ordered
-// (tile, Gaussian) sequence -- entry o of Gaussian r is its o-th tile in
-// row-major order -- to keys_out / vals_out, and the block's histogram of the
-// low `nbits` tile bits (the first sort pass) to hist.  The block's Gaussians
-// block_first[b] .. block_first[b + 1] are staged up to 1024 per round; each
-// wave then writes the entries of every 4th staged Gaussian lane-parallel
-// (coalesced runs) and counts digits with LDS atomics.
-template <typename KeyT, bool DIRECT>
-__global__ __launch_bounds__(kSortThreads) void emit_entries_kernel(
-    EmitArgs a, int nbits, int nblocks, uint32_t *__restrict__ hist, KeyT *__restrict__ keys_out,
-    uint32_t *__restrict__ vals_out) {
-    __shared__ EmitLds e;
-    __shared__ uint32_t counts[kRadixMax];
-    const int radix = 1 << nbits;
-    const uint32_t dmask = (uint32_t)radix - 1u;
-    for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
-    const int64_t block_base = (int64_t)blockIdx.x * kEmitTile;
-    const int64_t left = a.k - block_base;
-    const int count = (int)(left < kEmitTile ? left : kEmitTile);
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    KeyT *kout = keys_out + block_base;
-    uint32_t *vout = vals_out + block_base;
-    int64_t r0 = a.block_first[blockIdx.x];
-    const int64_t r_last = a.block_first[blockIdx.x + 1];  // inclusive
-    for (;;) {
-#pragma unroll
-        for (int q = 0; q < kEmitGroup / kSortThreads; ++q) {
-            const int j = threadIdx.x + q * kSortThreads;
-            const int64_t r = r0 + j;
-            int32_t off = 0x7fffffff, end = 0x7fffffff;
-            if (r <= r_last && r < a.n) {
-                const uint32_t g = a.order[r];
-                const uint32_t c = g < (uint64_t)a.n ? a.touched[g] : 0u;
-                int64_t o = (int64_t)a.offsets[r] - block_base;
-                int64_t oe = o + (int64_t)c;
-                o = o > 0x3fffffff ? 0x3fffffff : o;
-                oe = oe > 0x3fffffff ? 0x3fffffff : oe;
-                off = (int32_t)o;
-                end = (int32_t)oe;
-                TileRect rect{0, 0, 0, 0};
-                if (c > 0)
-                    tile_rect(a.points[2 * g], a.points[2 * g + 1], a.radii[2 * g],
-                              a.radii[2 * g + 1], a.width, a.height, a.tile_size, rect);
-                e.gid[j] = g;
-                e.origin[j] = (uint32_t)rect.tx0 | ((uint32_t)rect.ty0 << 16);
-                e.nx[j] = (uint16_t)(rect.tx1 - rect.tx0 + 1);
-            }
-            e.off[j] = off;
-            e.end[j] = end;
-        }
-        __syncthreads();
-        for (int j = wave; j < kEmitGroup; j += kSortWaves) {
-            const int32_t goff = e.off[j];
-            if (goff >= count) break;  // later Gaussians start even later
-            const int32_t lo = goff > 0 ? goff : 0;
-            const int32_t hi = e.end[j] < count ? e.end[j] : count;
-            const int32_t nx = e.nx[j] > 0 ? (int32_t)e.nx[j] : 1;
-            const uint32_t origin = e.origin[j];
-            const int32_t tx0 = (int32_t)(origin & 0xffffu), ty0 = (int32_t)(origin >> 16);
-            const uint32_t g = e.gid[j];
-            // row = floor((local + 0.5) / nx): the true quotient is at least 0.5/nx away
-            // from an integer and the float error is below that for local < 2^22
-            const float rcp = 1.0f / (float)nx;
-            for (int32_t idx = lo + lane; idx < hi; idx += kWave) {
-                const int32_t local = idx - goff;
-                const int32_t row = (int32_t)(((float)local + 0.5f) * rcp);
-                const int32_t col = local - row * nx;
-                const uint32_t t = (uint32_t)((ty0 + row) * a.tiles_x + tx0 + col);
-                kout[idx] = (KeyT)t;
-                vout[idx] = g;
-                atomicAdd(&counts[t & dmask], 1u);
-            }
-        }
-        const bool more = r0 + kEmitGroup <= r_last;
-        __syncthreads();
-        if (!more) break;
-        r0 += kEmitGroup;
-    }
-    for (int d = threadIdx.x; d < radix; d += kSortThreads)
-        hist[hist_index<DIRECT>(d, blockIdx.x, nblocks, radix)] = counts[d];
-}
 
 // indexing_offset[t] = first sorted position whose tile is >= t.
 template <typename KeyT>
@@ -573,24 +508,245 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(int n_tiles,
     offsets[t] = (int32_t)lo;
 }
 
-template <typename KeyT>
-__global__ __launch_bounds__(256) void sorted_keys_kernel(int64_t k, int64_t n,
-                                                          const KeyT *__restrict__ tiles,
-                                                          const int32_t *__restrict__ ids,
-                                                          const float *__restrict__ depths,
-                                                          uint64_t *__restrict__ keys) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= k) return;
-    const int32_t g = ids[i];
-    const uint32_t bits = (g >= 0 && g < n) ? __float_as_uint(depths[g]) : 0u;
-    keys[i] = ((uint64_t)(uint32_t)tiles[i] << 32) | (uint64_t)bits;
-}
-
 __global__ __launch_bounds__(256) void copy_u32_to_i32_kernel(int64_t n,
                                                               const uint32_t *__restrict__ in,
                                                               int32_t *__restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = (int32_t)in[i];
+}
+
+// ----------------------------------------------------- level 2: tiles
+
+// Level 1 leaves, for every supertile s, the ids of the Gaussians whose tile
+// rectangle meets s, in depth order (list positions super_off[s] ..
+// super_off[s + 1]).  Level 2 cuts each list into chunks of kL2Threads
+// positions (block b <-> supertile s, chunk b - chunk_start[s]); a lane holds
+// one Gaussian and the 64-bit mask of the supertile's tiles its rectangle
+// covers.  Per local tile j, one ballot gives the lanes (in list order) that
+// write an entry: l2_count_kernel counts them per block and per tile,
+// l2_scatter_kernel writes the ids to
+//   indexing_offset[t] + (entries of t in earlier blocks of s) +
+//   (entries of t in earlier waves of the block) + (rank in the ballot).
+// Within a tile the entries therefore keep the depth order of the lists.
+struct L2Args {
+    const int32_t *super_off;     // n_super: first list position of each supertile
+    const int32_t *super_ids;     // m: Gaussian ids per supertile, depth order
+    const uint32_t *chunk_start;  // n_super + 1: first level-2 block of each supertile
+    const uint2 *block_map;       // per level-2 block: (supertile, first list position)
+    const uint2 *rects;           // packed tile rectangle per Gaussian (count workspace)
+    int64_t n, m, k;
+    int n_super, super_x, tiles_x, tiles_y, width, height, tile_size;
+};
+
+// block_map[b] for the chunks of supertile s (one thread per supertile).
+__global__ __launch_bounds__(256) void l2_map_kernel(int n_super,
+                                                     const int32_t *__restrict__ super_off,
+                                                     const uint32_t *__restrict__ chunk_start,
+                                                     uint2 *__restrict__ block_map) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n_super) return;
+    const uint32_t first = (uint32_t)super_off[s];
+    for (uint32_t b = chunk_start[s], c = 0; b < chunk_start[s + 1]; ++b, ++c)
+        block_map[b] = make_uint2((uint32_t)s, first + c * kL2Threads);
+}
+
+// Tile id of local tile j of supertile s, or -1 outside the tile grid.
+__device__ __forceinline__ int tile_of_local(const L2Args &a, int s, int j) {
+    const int tx = (s % a.super_x) * kSuper + (j % kSuper);
+    const int ty = (s / a.super_x) * kSuper + (j / kSuper);
+    return (tx < a.tiles_x && ty < a.tiles_y) ? ty * a.tiles_x + tx : -1;
+}
+
+// Bit j (= ly * kSuper + lx) set for every tile of supertile s that Gaussian
+// g's tile rectangle covers.
+__device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int s) {
+    if (g < 0 || (int64_t)g >= a.n) return 0;
+    const TileRect r = unpack_rect(a.rects[g]);  // Gaussians in the lists have tiles
+    const int ox = (s % a.super_x) * kSuper, oy = (s / a.super_x) * kSuper;
+    const int x0 = max(r.tx0 - ox, 0), x1 = min(r.tx1 - ox, kSuper - 1);
+    const int y0 = max(r.ty0 - oy, 0), y1 = min(r.ty1 - oy, kSuper - 1);
+    if (x0 > x1 || y0 > y1) return 0;
+    const uint64_t row = ((1ull << (x1 - x0 + 1)) - 1ull) << x0;
+    uint64_t m = 0;
+    for (int y = y0; y <= y1; ++y) m |= row << (y * kSuper);
+    return m;
+}
+
+struct L2Block {
+    int s;
+    uint32_t b;
+    int32_t g;
+    uint64_t mask;
+};
+
+// Block -> supertile, this lane's Gaussian and mask.  Returns false (uniformly)
+// for the blocks past the last chunk (the grid is sized by an upper bound).
+__device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x) {
+    x.b = blockIdx.x;
+    if (x.b >= a.chunk_start[a.n_super]) return false;
+    const uint2 map = a.block_map[x.b];
+    x.s = (int)map.x;
+    const int64_t end = x.s + 1 < a.n_super ? a.super_off[x.s + 1] : a.m;
+    const int64_t e = (int64_t)map.y + threadIdx.x;
+    x.g = -1;
+    x.mask = 0;
+    if (e < end) {
+        x.g = a.super_ids[e];
+        x.mask = local_mask(a, x.g, x.s);
+    }
+    return true;
+}
+
+// Per local tile j, the number of lanes of this wave whose mask has bit j, in lane j.
+__device__ __forceinline__ uint32_t wave_local_counts(uint64_t mask) {
+    const int lane = threadIdx.x % kWave;
+    uint32_t mine = 0;
+#pragma unroll 8
+    for (int j = 0; j < kSuperLocal; ++j) {
+        const uint32_t c = (uint32_t)__popcll(__ballot((mask >> j) & 1ull));
+        mine = lane == j ? c : mine;
+    }
+    return mine;
+}
+
+// counts[t] += entries of tile t in this block; table[b * 64 + j] = the same per local tile.
+__global__ __launch_bounds__(kL2Threads) void l2_count_kernel(L2Args a,
+                                                              uint32_t *__restrict__ table,
+                                                              uint32_t *__restrict__ counts) {
+    __shared__ uint32_t wave_cnt[kL2Waves][kSuperLocal];
+    L2Block x;
+    if (!l2_block(a, x)) return;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    wave_cnt[wave][lane] = wave_local_counts(x.mask);
+    __syncthreads();
+    if (threadIdx.x < kSuperLocal) {
+        const int j = threadIdx.x;
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < kL2Waves; ++w) c += wave_cnt[w][j];
+        table[(int64_t)x.b * kSuperLocal + j] = c;
+        const int t = tile_of_local(a, x.s, j);
+        if (c && t >= 0) atomicAdd(&counts[t], c);
+    }
+}
+
+// table[b * 64 + j] <- first output position of block b's entries of local tile
+// j: indexing_offset of the tile plus its entries in the earlier chunks of the
+// supertile.  One thread per (supertile, local tile).
+__global__ __launch_bounds__(256) void l2_prefix_kernel(L2Args a,
+                                                        const int32_t *__restrict__ tile_offsets,
+                                                        uint32_t *__restrict__ table) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)a.n_super * kSuperLocal) return;
+    const int s = (int)(idx / kSuperLocal), j = (int)(idx % kSuperLocal);
+    const int t = tile_of_local(a, s, j);
+    uint32_t pos = t >= 0 ? (uint32_t)tile_offsets[t] : 0u;
+    const uint32_t q1 = a.chunk_start[s + 1];
+    uint32_t q = a.chunk_start[s];
+    for (; q + 4 <= q1; q += 4) {  // four independent loads per step
+        uint32_t c[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) c[u] = table[(int64_t)(q + u) * kSuperLocal + j];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            table[(int64_t)(q + u) * kSuperLocal + j] = pos;
+            pos += c[u];
+        }
+    }
+    for (; q < q1; ++q) {
+        const uint32_t c = table[(int64_t)q * kSuperLocal + j];
+        table[(int64_t)q * kSuperLocal + j] = pos;
+        pos += c;
+    }
+}
+
+__global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
+                                                                const uint32_t *__restrict__ table,
+                                                                int32_t *__restrict__ ids_out) {
+    __shared__ uint32_t base[kL2Waves][kSuperLocal];
+    L2Block x;
+    if (!l2_block(a, x)) return;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    base[wave][lane] = wave_local_counts(x.mask);
+    __syncthreads();
+    if (threadIdx.x < kSuperLocal) {
+        const int j = threadIdx.x;
+        uint32_t pos = table[(int64_t)x.b * kSuperLocal + j];  // from l2_prefix_kernel
+#pragma unroll
+        for (int w = 0; w < kL2Waves; ++w) {
+            const uint32_t c = base[w][j];
+            base[w][j] = pos;
+            pos += c;
+        }
+    }
+    __syncthreads();
+    const uint64_t below = lanemask_lt();
+#pragma unroll 4
+    for (int j = 0; j < kSuperLocal; ++j) {
+        const bool mine = (x.mask >> j) & 1ull;
+        const uint64_t bal = __ballot(mine);
+        if (mine) {
+            const uint32_t p = base[wave][j] + (uint32_t)__popcll(bal & below);
+            if ((int64_t)p < a.k) ids_out[p] = x.g;
+        }
+    }
+}
+
+// Level-1 entries: for the Gaussian at depth-order position r, one entry per
+// supertile of its rectangle (row-major), at offsets[r].. (thread per position).
+template <typename KeyT>
+__global__ __launch_bounds__(256) void emit_super_kernel(
+    int64_t n, int64_t m, const uint32_t *__restrict__ order,
+    const uint64_t *__restrict__ offsets, const uint32_t *__restrict__ super_touched,
+    const uint2 *__restrict__ rects, int super_x, KeyT *__restrict__ keys_out,
+    uint32_t *__restrict__ vals_out) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const uint32_t g = order[r];
+    if (g >= (uint64_t)n) return;
+    const uint32_t c = super_touched[g];
+    const uint2 packed = rects[g];
+    if (c == 0) return;
+    const TileRect t = unpack_rect(packed);
+    int64_t o = (int64_t)offsets[r];
+    for (int y = t.ty0 / kSuper; y <= t.ty1 / kSuper; ++y)
+        for (int x = t.tx0 / kSuper; x <= t.tx1 / kSuper; ++x, ++o) {
+            if (o >= m) return;
+            keys_out[o] = (KeyT)(y * super_x + x);
+            vals_out[o] = g;
+        }
+}
+
+// Number of level-2 chunks of each supertile list.
+__global__ __launch_bounds__(256) void l2_chunk_count_kernel(int n_super, int64_t m,
+                                                             const int32_t *__restrict__ super_off,
+                                                             uint32_t *__restrict__ chunks) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n_super) return;
+    const int64_t end = s + 1 < n_super ? super_off[s + 1] : m;
+    const int64_t len = end - super_off[s];
+    chunks[s] = (uint32_t)((len + kL2Threads - 1) / kL2Threads);
+}
+
+// keys[i] = tile << 32 | depth bits of ids[i], the tile being the last one
+// whose offset is <= i (the reference's sorted 64-bit keys).
+__global__ __launch_bounds__(256) void keys_from_offsets_kernel(
+    int64_t k, int64_t n, int n_tiles, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ ids, const float *__restrict__ depths,
+    uint64_t *__restrict__ keys) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= k) return;
+    int lo = 0, hi = n_tiles - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((int64_t)offsets[mid] <= i)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const int32_t g = ids[i];
+    const uint32_t bits = (g >= 0 && g < n) ? __float_as_uint(depths[g]) : 0u;
+    keys[i] = ((uint64_t)(uint32_t)lo << 32) | (uint64_t)bits;
 }
 
 // ------------------------------------------------------ workspace layout
@@ -608,7 +764,8 @@ struct Carve {
 };
 
 struct CountWs {
-    uint32_t *touched, *dkeys_a, *dvals_a, *dkeys_b, *dvals_b;
+    uint32_t *touched, *super_touched, *dkeys_a, *dvals_a, *dkeys_b, *dvals_b;
+    uint2 *rects;
     uint64_t *counts, *offsets;
     void *sort_ws, *scan_ws;
     size_t bytes;
@@ -618,6 +775,8 @@ inline CountWs carve_count(void *base, int64_t n) {
     Carve c{reinterpret_cast<char *>(base)};
     CountWs w;
     w.touched = c.take<uint32_t>(n);
+    w.super_touched = c.take<uint32_t>(n);
+    w.rects = c.take<uint2>(n);
     w.dkeys_a = c.take<uint32_t>(n);
     w.dvals_a = c.take<uint32_t>(n);
     w.dkeys_b = c.take<uint32_t>(n);
@@ -635,23 +794,73 @@ constexpr int kDepthBits = 32;
 
 inline bool use_u16_keys(int tile_bits) { return tile_bits <= 16; }
 
+// Level 1: the (supertile, Gaussian) entries and their sort by supertile.
 struct SortWs {
-    void *keys_a, *keys_b;  // tile keys (u16 or u32)
+    void *keys_a, *keys_b;  // supertile keys (u16 or u32)
     uint32_t *vals_tmp;
-    uint32_t *block_first;
-    void *pass_ws;  // histogram table + scan scratch of each pass
+    void *pass_ws;  // histogram table + digit totals of each pass
     size_t bytes;
 };
 
-inline SortWs carve_sort(void *base, int64_t k, int tile_bits) {
-    Carve c{reinterpret_cast<char *>(base)};
+inline SortWs carve_sort(Carve &c, int64_t m, int super_bits) {
     SortWs w;
-    const int64_t kb = use_u16_keys(tile_bits) ? 2 : 4;
-    w.keys_a = c.take<char>(k * kb);
-    w.keys_b = c.take<char>(k * kb);
-    w.vals_tmp = c.take<uint32_t>(k);
-    w.block_first = c.take<uint32_t>((k + kEmitTile - 1) / kEmitTile + 1);
-    w.pass_ws = c.take<char>((int64_t)radix_workspace_bytes<kTileItems>(k));
+    const int64_t kb = use_u16_keys(super_bits) ? 2 : 4;
+    w.keys_a = c.take<char>(m * kb);
+    w.keys_b = c.take<char>(m * kb);
+    w.vals_tmp = c.take<uint32_t>(m);
+    w.pass_ws = c.take<char>((int64_t)radix_workspace_bytes<kTileItems>(m));
+    w.bytes = 0;
+    return w;
+}
+
+// Geometry of the tile and supertile grids.
+struct Grid {
+    int tiles_x, tiles_y, n_tiles;
+    int super_x, super_y, n_super, super_bits;
+};
+
+inline bool make_grid(int32_t width, int32_t height, int32_t tile_size, Grid &g) {
+    const int64_t tx = (width + (int64_t)tile_size - 1) / tile_size;
+    const int64_t ty = (height + (int64_t)tile_size - 1) / tile_size;
+    if (tx * ty > 0x7fffffffLL) return false;
+    g.tiles_x = (int)tx;
+    g.tiles_y = (int)ty;
+    g.n_tiles = (int)(tx * ty);
+    g.super_x = (int)((tx + kSuper - 1) / kSuper);
+    g.super_y = (int)((ty + kSuper - 1) / kSuper);
+    g.n_super = g.super_x * g.super_y;
+    int b = 0;
+    while (b < 31 && ((int64_t)(g.n_super - 1) >> b) != 0) ++b;
+    g.super_bits = b;
+    return true;
+}
+
+inline int64_t l2_blocks_bound(int64_t m, int n_super) {
+    return (m + kL2Threads - 1) / kL2Threads + n_super;
+}
+
+struct BinWs {
+    SortWs lvl1;
+    int32_t *super_off;    // n_super (+1 spare)
+    int32_t *super_ids;    // m
+    uint32_t *chunks;      // n_super + 1: chunk counts, scanned in place to chunk_start
+    uint2 *block_map;      // level-2 block -> (supertile, first list position)
+    uint32_t *table;       // level-2 blocks x 64
+    void *scan_ws;
+    size_t bytes;
+};
+
+inline BinWs carve_bins(void *base, int64_t m, const Grid &g) {
+    Carve c{reinterpret_cast<char *>(base)};
+    BinWs w;
+    w.lvl1 = carve_sort(c, m, g.super_bits);
+    w.super_off = c.take<int32_t>((int64_t)g.n_super + 1);
+    w.super_ids = c.take<int32_t>(m);
+    w.chunks = c.take<uint32_t>((int64_t)g.n_super + 1);
+    w.block_map = c.take<uint2>(l2_blocks_bound(m, g.n_super));
+    w.table = c.take<uint32_t>(l2_blocks_bound(m, g.n_super) * kSuperLocal);
+    const int64_t scan_n = g.n_super > g.n_tiles ? g.n_super : g.n_tiles;
+    w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint32_t>(scan_n));
     w.bytes = align256(c.off);
     return w;
 }
@@ -662,56 +871,33 @@ inline int bits_for(int64_t max_value) {
     return b;
 }
 
-// Entry generation (with the first pass's histogram), then the sort passes;
-// the last pass writes the caller's gaussian_ids_sorted and the sorted keys
-// end in keys_b.
+// Level 1: the (supertile, Gaussian) entries in depth order, stably sorted by
+// supertile id; writes the per-supertile list starts and the sorted ids.
 template <typename KeyT>
-int tile_sort(const EmitArgs &a, const SortWs &w, int tile_bits, int n_tiles,
-              int32_t *indexing_offset, int32_t *ids_out, uint64_t *sorted_keys,
-              const float *depths, hipStream_t stream) {
-    static_assert(kEmitTile == kSortThreads * kTileItems, "entry blocks must be sort blocks");
-    const SortPlan plan = plan_sort(tile_bits);
+int super_sort(const EmitArgs &a, const SortWs &w, int super_bits, int n_super,
+               int32_t *super_off, int32_t *super_ids, hipStream_t stream) {
+    const SortPlan plan = plan_sort(super_bits);
     const int P = plan.passes;
-    const int nblocks = (int)sort_blocks<kTileItems>(a.k);
-    const bool direct = nblocks <= kDirectMaxBlocks;
     KeyT *ka = reinterpret_cast<KeyT *>(w.keys_a), *kb = reinterpret_cast<KeyT *>(w.keys_b);
-    uint32_t *out = reinterpret_cast<uint32_t *>(ids_out);
+    uint32_t *out = reinterpret_cast<uint32_t *>(super_ids);
     // pass p writes (kb, out) when P-1-p is even, (ka, vals_tmp) otherwise; the
     // entries (pass -1) go to the other set than pass 0
     auto keys_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? kb : ka; };
     auto vals_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? out : w.vals_tmp; };
-
-    hipLaunchKernelGGL(block_first_kernel, dim3(ceil_div(a.n, 256)), dim3(256), 0, stream, a.n,
-                       a.k, a.order, a.offsets, a.touched, w.block_first);
+    hipLaunchKernelGGL(emit_super_kernel<KeyT>, dim3(ceil_div(a.n, 256)), dim3(256), 0, stream,
+                       a.n, a.k, a.order, a.offsets, a.touched, a.rects, a.tiles_x, keys_for(-1),
+                       vals_for(-1));
     int st = launch_status();
-    if (st) return st;
-    uint32_t *hist = reinterpret_cast<uint32_t *>(w.pass_ws);
-    const int nb0 = pass_bits(plan, tile_bits, 0);
-    if (direct)
-        hipLaunchKernelGGL((emit_entries_kernel<KeyT, true>), dim3(nblocks), dim3(kSortThreads), 0,
-                           stream, a, nb0, nblocks, hist, keys_for(-1), vals_for(-1));
-    else
-        hipLaunchKernelGGL((emit_entries_kernel<KeyT, false>), dim3(nblocks), dim3(kSortThreads),
-                           0, stream, a, nb0, nblocks, hist, keys_for(-1), vals_for(-1));
-    st = launch_status();
     if (st) return st;
     for (int p = 0; p < P; ++p) {
         st = radix_pass<KeyT, kTileItems>(keys_for(p - 1), vals_for(p - 1), keys_for(p),
                                           vals_for(p), a.k, p * plan.bits_per_pass,
-                                          pass_bits(plan, tile_bits, p), true, w.pass_ws, stream,
-                                          p == 0);
+                                          pass_bits(plan, super_bits, p), true, w.pass_ws, stream);
         if (st) return st;
     }
-    hipLaunchKernelGGL(tile_ranges_kernel<KeyT>, dim3(ceil_div(n_tiles, 256)), dim3(256), 0,
-                       stream, n_tiles, kb, a.k, indexing_offset);
-    st = launch_status();
-    if (st) return st;
-    if (sorted_keys) {
-        hipLaunchKernelGGL(sorted_keys_kernel<KeyT>, dim3(ceil_div(a.k, 256)), dim3(256), 0,
-                           stream, a.k, a.n, kb, ids_out, depths, sorted_keys);
-        st = launch_status();
-    }
-    return st;
+    hipLaunchKernelGGL(tile_ranges_kernel<KeyT>, dim3(ceil_div(n_super, 256)), dim3(256), 0,
+                       stream, n_super, kb, a.k, super_off);
+    return launch_status();
 }
 
 }  // namespace gs
@@ -727,32 +913,28 @@ extern "C" int gs_bin_count_workspace_size(int64_t n, size_t *bytes) {
 extern "C" int gs_bin_count(const float *points_image, const float *radii, const float *depths,
                             const uint8_t *mask, int64_t n, int32_t width, int32_t height,
                             int32_t tile_size, void *workspace, size_t workspace_bytes,
-                            int64_t *total_keys, hipStream_t stream) {
-    if (n < 0 || width <= 0 || height <= 0 || tile_size <= 0 || !total_keys)
+                            int64_t *totals, hipStream_t stream) {
+    if (n < 0 || width <= 0 || height <= 0 || tile_size <= 0 || !totals)
         return GS_ERR_INVALID_ARGUMENT;
     if (n > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;  // Gaussian ids are int32
     const CountWs w = carve_count(workspace, n);
     if (n > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
-    if (n == 0) return zero_bytes(total_keys, sizeof(int64_t), stream);
+    int st = zero_bytes(totals, 2 * sizeof(int64_t), stream);
+    if (st || n == 0) return st;
     if (!points_image || !radii || !depths || !mask) return GS_ERR_INVALID_ARGUMENT;
     const SortPlan plan = plan_sort(kDepthBits);
     const int nblocks = (int)sort_blocks<kDepthItems>(n);
     const int nb0 = pass_bits(plan, kDepthBits, 0);
     uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
-    if (nblocks <= kDirectMaxBlocks)
-        hipLaunchKernelGGL((count_tiles_kernel<kDepthItems, true>), dim3(nblocks),
-                           dim3(kSortThreads), 0, stream, n, points_image, radii, depths, mask,
-                           width, height, tile_size, w.touched, w.dkeys_a, w.dvals_a, nb0,
-                           nblocks, hist);
-    else
-        hipLaunchKernelGGL((count_tiles_kernel<kDepthItems, false>), dim3(nblocks),
-                           dim3(kSortThreads), 0, stream, n, points_image, radii, depths, mask,
-                           width, height, tile_size, w.touched, w.dkeys_a, w.dvals_a, nb0,
-                           nblocks, hist);
-    int st = launch_status();
+    unsigned long long *k_total = reinterpret_cast<unsigned long long *>(totals);
+    hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
+                       stream, n, points_image, radii, depths, mask, width, height, tile_size,
+                       w.touched, w.super_touched, w.rects, w.dkeys_a, w.dvals_a, nb0, nblocks,
+                       hist, k_total);
+    st = launch_status();
     if (st) return st;
     // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes no
-    // keys but the tile counts in depth order
+    // keys but the supertile counts in depth order
     for (int p = 0; p < plan.passes; ++p) {
         const bool from_a = (p % 2) == 0;
         const bool last = p + 1 == plan.passes;
@@ -760,72 +942,125 @@ extern "C" int gs_bin_count(const float *points_image, const float *radii, const
             from_a ? w.dkeys_a : w.dkeys_b, from_a ? w.dvals_a : w.dvals_b,
             from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, n,
             p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream,
-            p == 0, last ? w.touched : nullptr, last ? w.counts : nullptr);
+            p == 0, last ? w.super_touched : nullptr, last ? w.counts : nullptr);
         if (st) return st;
     }
+    // supertile entry offsets in depth order; the total (M) goes to totals[1]
     return scan_exclusive<uint64_t>(w.counts, w.offsets, n,
-                                    reinterpret_cast<uint64_t *>(total_keys), w.scan_ws, stream);
+                                    reinterpret_cast<uint64_t *>(totals + 1), w.scan_ws, stream);
 }
 
-static int tile_bits_of(int32_t width, int32_t height, int32_t tile_size, int *n_tiles) {
-    const int64_t tx = (width + tile_size - 1) / tile_size;
-    const int64_t ty = (height + tile_size - 1) / tile_size;
-    if (tx * ty > 0x7fffffffLL) return -1;
-    *n_tiles = (int)(tx * ty);
-    return bits_for((int64_t)*n_tiles - 1);
-}
-
-extern "C" int gs_bin_sort_workspace_size(int64_t n, int64_t k, int32_t n_tiles, size_t *bytes) {
+extern "C" int gs_bin_sort_workspace_size(int64_t n, int64_t k, int64_t m, int32_t width,
+                                          int32_t height, int32_t tile_size, size_t *bytes) {
     (void)n;
-    if (k < 0 || n_tiles < 0 || !bytes) return GS_ERR_INVALID_ARGUMENT;
-    *bytes = carve_sort(nullptr, k, bits_for((int64_t)n_tiles - 1)).bytes;
+    (void)k;
+    Grid g;
+    if (m < 0 || width <= 0 || height <= 0 || tile_size <= 0 || !bytes ||
+        !make_grid(width, height, tile_size, g))
+        return GS_ERR_INVALID_ARGUMENT;
+    *bytes = carve_bins(nullptr, m, g).bytes;
     return GS_OK;
 }
 
 extern "C" int gs_bin_sort(const float *points_image, const float *radii, const float *depths,
                            int64_t n, int32_t width, int32_t height, int32_t tile_size,
-                           int64_t k, const void *count_workspace, void *workspace,
+                           int64_t k, int64_t m, const void *count_workspace, void *workspace,
                            size_t workspace_bytes, int32_t *indexing_offset,
                            int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
                            int32_t *tiles_touched, hipStream_t stream) {
-    if (n < 0 || k < 0 || width <= 0 || height <= 0 || tile_size <= 0)
+    if (n < 0 || k < 0 || m < 0 || m > k || width <= 0 || height <= 0 || tile_size <= 0)
         return GS_ERR_INVALID_ARGUMENT;
     if (k > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
-    int n_tiles = 0;
-    const int tile_bits = tile_bits_of(width, height, tile_size, &n_tiles);
-    if (tile_bits < 0) return GS_ERR_INVALID_ARGUMENT;
+    Grid g;
+    if (!make_grid(width, height, tile_size, g)) return GS_ERR_INVALID_ARGUMENT;
     if (!indexing_offset) return GS_ERR_INVALID_ARGUMENT;
-    if ((width + tile_size - 1) / tile_size > 65535 || (height + tile_size - 1) / tile_size > 65535)
+    if (g.tiles_x > 65535 || g.tiles_y > 65535)
         return GS_ERR_UNSUPPORTED;  // tile rectangles are staged with 16-bit coordinates
+    if ((k == 0) != (m == 0)) return GS_ERR_INVALID_ARGUMENT;
     const CountWs cw = carve_count(const_cast<void *>(count_workspace), n);
-    const SortWs w = carve_sort(workspace, k, tile_bits);
-    if (k > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
+    const BinWs w = carve_bins(workspace, m, g);
+    if (m > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
     if (n > 0 && !count_workspace) return GS_ERR_INVALID_ARGUMENT;
+    int st;
     if (tiles_touched && n > 0) {
         hipLaunchKernelGGL(copy_u32_to_i32_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream,
                            n, cw.touched, tiles_touched);
-        int st = launch_status();
+        st = launch_status();
         if (st) return st;
     }
-    if (k == 0) return zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)n_tiles, stream);
+    // per-tile entry counts accumulate in indexing_offset, then scan in place
+    st = zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)g.n_tiles, stream);
+    if (st || k == 0) return st;
     if (!points_image || !radii || !gaussian_ids_sorted || (sorted_keys && !depths) || n == 0)
         return GS_ERR_INVALID_ARGUMENT;
+
+    // level 1: (supertile, Gaussian) entries in depth order, stably sorted by supertile
     EmitArgs a;
+    a.rects = cw.rects;
     a.order = cw.dvals_a;  // depth order (even number of depth passes)
     a.offsets = cw.offsets;
-    a.touched = cw.touched;
-    a.block_first = w.block_first;
-    a.points = points_image;
-    a.radii = radii;
+    a.touched = cw.super_touched;
     a.n = n;
-    a.k = k;
-    a.width = width;
-    a.height = height;
-    a.tile_size = tile_size;
-    a.tiles_x = (width + tile_size - 1) / tile_size;
-    if (use_u16_keys(tile_bits))
-        return tile_sort<uint16_t>(a, w, tile_bits, n_tiles, indexing_offset, gaussian_ids_sorted,
-                                   sorted_keys, depths, stream);
-    return tile_sort<uint32_t>(a, w, tile_bits, n_tiles, indexing_offset, gaussian_ids_sorted,
-                               sorted_keys, depths, stream);
+    a.k = m;
+    a.tiles_x = g.super_x;
+    st = use_u16_keys(g.super_bits)
+             ? super_sort<uint16_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
+                                    w.super_ids, stream)
+             : super_sort<uint32_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
+                                    w.super_ids, stream);
+    if (st) return st;
+
+    // level 2: chunk map, per-tile counts, tile offsets, scatter
+    hipLaunchKernelGGL(l2_chunk_count_kernel, dim3(ceil_div(g.n_super, 256)), dim3(256), 0,
+                       stream, g.n_super, m, w.super_off, w.chunks);
+    st = launch_status();
+    if (st) return st;
+    st = scan_exclusive<uint32_t>(w.chunks, w.chunks, g.n_super, w.chunks + g.n_super, w.scan_ws,
+                                  stream);
+    if (st) return st;
+    L2Args l2;
+    l2.super_off = w.super_off;
+    l2.super_ids = w.super_ids;
+    l2.chunk_start = w.chunks;
+    l2.rects = cw.rects;
+    l2.n = n;
+    l2.m = m;
+    l2.k = k;
+    l2.n_super = g.n_super;
+    l2.super_x = g.super_x;
+    l2.tiles_x = g.tiles_x;
+    l2.tiles_y = g.tiles_y;
+    l2.width = width;
+    l2.height = height;
+    l2.tile_size = tile_size;
+    const int64_t nb2 = l2_blocks_bound(m, g.n_super);
+    if (nb2 > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
+    l2.block_map = w.block_map;
+    hipLaunchKernelGGL(l2_map_kernel, dim3(ceil_div(g.n_super, 256)), dim3(256), 0, stream,
+                       g.n_super, w.super_off, w.chunks, w.block_map);
+    st = launch_status();
+    if (st) return st;
+    uint32_t *tile_counts = reinterpret_cast<uint32_t *>(indexing_offset);
+    hipLaunchKernelGGL(l2_count_kernel, dim3((unsigned)nb2), dim3(kL2Threads), 0, stream, l2,
+                       w.table, tile_counts);
+    st = launch_status();
+    if (st) return st;
+    st = scan_exclusive<uint32_t>(tile_counts, tile_counts, g.n_tiles, (uint32_t *)nullptr,
+                                  w.scan_ws, stream);
+    if (st) return st;
+    hipLaunchKernelGGL(l2_prefix_kernel, dim3(ceil_div((int64_t)g.n_super * kSuperLocal, 256)),
+                       dim3(256), 0, stream, l2, indexing_offset, w.table);
+    st = launch_status();
+    if (st) return st;
+    hipLaunchKernelGGL(l2_scatter_kernel, dim3((unsigned)nb2), dim3(kL2Threads), 0, stream, l2,
+                       w.table, gaussian_ids_sorted);
+    st = launch_status();
+    if (st) return st;
+    if (sorted_keys) {
+        hipLaunchKernelGGL(keys_from_offsets_kernel, dim3(ceil_div(k, 256)), dim3(256), 0, stream,
+                           k, n, g.n_tiles, indexing_offset, gaussian_ids_sorted, depths,
+                           sorted_keys);
+        st = launch_status();
+    }
+    return st;
 }

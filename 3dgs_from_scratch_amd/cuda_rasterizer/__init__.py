@@ -264,19 +264,23 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         sz = ctypes.c_size_t(0)
         _lib.check(lib.gs_bin_count_workspace_size(n, ctypes.byref(sz)), "workspace query")
         ws_count = torch.empty((max(sz.value, 1),), dtype=torch.uint8, device=dev)
-        total = torch.empty((1,), dtype=torch.int64, device=dev)
+        totals = torch.empty((2,), dtype=torch.int64, device=dev)
         ev = _lib.timer.record("bin_count", dev)
         _lib.check(
             lib.gs_bin_count(
                 _ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
-                tile_size, _ptr(ws_count), sz.value, _ptr(total), stream,
+                tile_size, _ptr(ws_count), sz.value, _ptr(totals), stream,
             ),
             "compute_tile_intersection (count)",
         )
         _lib.timer.stop(ev, dev)
-        k = int(total.item())  # the one host synchronisation (src/cuda/rasterizer.cpp:322)
+        # the one host synchronisation (src/cuda/rasterizer.cpp:322): K keys, M supertile entries
+        k, m = (int(v) for v in totals.tolist())
+        if k > 2**31 - 1:
+            raise RasterizerError(f"compute_tile_intersection: {k} keys exceed the int32 range")
         sz2 = ctypes.c_size_t(0)
-        _lib.check(lib.gs_bin_sort_workspace_size(n, k, n_tiles, ctypes.byref(sz2)), "workspace query")
+        _lib.check(lib.gs_bin_sort_workspace_size(n, k, m, width, height, tile_size,
+                                                  ctypes.byref(sz2)), "workspace query")
         ws_sort = torch.empty((max(sz2.value, 1),), dtype=torch.uint8, device=dev)
         indexing_offset = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
         gaussian_ids_sorted = torch.empty((k,), dtype=torch.int32, device=dev)
@@ -286,7 +290,7 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         _lib.check(
             lib.gs_bin_sort(
                 _ptr(points_image), _ptr(radii), _ptr(depths), n, width, height, tile_size, k,
-                _ptr(ws_count), _ptr(ws_sort), sz2.value, _ptr(indexing_offset),
+                m, _ptr(ws_count), _ptr(ws_sort), sz2.value, _ptr(indexing_offset),
                 _ptr(gaussian_ids_sorted), _ptr(sorted_keys), _ptr(tiles_touched), stream,
             ),
             "compute_tile_intersection (sort)",

@@ -103,29 +103,33 @@ int gs_evaluate_sh_backward(const float *grad_colors, const float *camera_pos,
 
 /*
  * compute_tile_intersection (src/cuda/rasterizer.cpp:292-359) in two phases
- * around the one host read of the key count K:
+ * around the one host read of the entry counts:
  *
- *   gs_bin_count: tiles_touched per Gaussian (kernel.cu:784-818 semantics),
- *     a stable sort of the visible Gaussians by depth bits, and an exclusive
- *     scan of tiles_touched in that order.  Writes K to *total_keys (a device
- *     int64).  Keeps its state in `workspace`, which gs_bin_sort reads.
- *   gs_bin_sort: emits one (tile, Gaussian) entry per touched tile in depth
- *     order, stably sorts them by tile id and extracts the per-tile ranges.
- *     The result equals a stable sort of the reference's 64-bit keys
- *     (tile_id << 32 | depth_bits) emitted in Gaussian order (kernel.cu:820-914):
- *     entries ordered by (tile, depth bits, Gaussian index).
- *     indexing_offset[t] = number of entries with tile < t (n_tiles entries).
- *     Optional outputs (may be NULL): sorted_keys (K uint64, the 64-bit keys
- *     in sorted order) and tiles_touched (N int32).
+ *   gs_bin_count: tiles_touched per Gaussian (kernel.cu:784-818 semantics), a
+ *     stable sort of the visible Gaussians by depth bits, and the scan that
+ *     places their supertile entries (a supertile is 8 x 8 tiles).  Writes two
+ *     device int64: totals[0] = K, the number of (tile, Gaussian) keys, and
+ *     totals[1] = M, the number of (supertile, Gaussian) entries (M <= K).
+ *     Keeps its state in `workspace`, which gs_bin_sort reads.
+ *   gs_bin_sort: sorts the M entries by supertile (depth order kept), then
+ *     expands every supertile list to its tiles and writes each Gaussian id
+ *     once, at its final position.  The result equals a stable sort of the
+ *     reference's 64-bit keys (tile_id << 32 | depth_bits) emitted in Gaussian
+ *     order (kernel.cu:820-914): entries ordered by (tile, depth bits,
+ *     Gaussian index).  indexing_offset[t] = number of entries with tile < t
+ *     (one int32 per tile).  Optional outputs (may be NULL): sorted_keys (K
+ *     uint64, the 64-bit keys in sorted order) and tiles_touched (N int32).
+ *     The workspace size depends on M and the image/tile geometry only.
  */
 int gs_bin_count_workspace_size(int64_t n, size_t *bytes);
 int gs_bin_count(const float *points_image, const float *radii, const float *depths,
                  const uint8_t *mask, int64_t n, int32_t width, int32_t height,
-                 int32_t tile_size, void *workspace, size_t workspace_bytes,
-                 int64_t *total_keys, hipStream_t stream);
-int gs_bin_sort_workspace_size(int64_t n, int64_t k, int32_t n_tiles, size_t *bytes);
+                 int32_t tile_size, void *workspace, size_t workspace_bytes, int64_t *totals,
+                 hipStream_t stream);
+int gs_bin_sort_workspace_size(int64_t n, int64_t k, int64_t m, int32_t width, int32_t height,
+                               int32_t tile_size, size_t *bytes);
 int gs_bin_sort(const float *points_image, const float *radii, const float *depths, int64_t n,
-                int32_t width, int32_t height, int32_t tile_size, int64_t k,
+                int32_t width, int32_t height, int32_t tile_size, int64_t k, int64_t m,
                 const void *count_workspace, void *workspace, size_t workspace_bytes,
                 int32_t *indexing_offset, int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
                 int32_t *tiles_touched, hipStream_t stream);

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 2
+    assert lib.gs_abi_version() == 3
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -59,11 +59,14 @@ def test_workspace_queries(lib):
     small = sz.value
     assert lib.gs_bin_count_workspace_size(1_000_000, ctypes.byref(sz)) == 0
     assert sz.value >= 1_000_000 * 36 and sz.value > small
-    # two 16-bit key buffers + one 32-bit id buffer per entry while tile ids fit 16 bits
-    assert lib.gs_bin_sort_workspace_size(1000, 20_000_000, 8160, ctypes.byref(sz)) == 0
-    assert sz.value >= 20_000_000 * 8
-    assert lib.gs_bin_sort_workspace_size(1000, 20_000_000, 70_000, ctypes.byref(sz)) == 0
-    assert sz.value >= 20_000_000 * 12
+    # the sort workspace scales with the supertile entries M, not with the keys K:
+    # two 16-bit key buffers + two 32-bit id buffers per entry, plus 64 counters
+    # per 256 entries
+    assert lib.gs_bin_sort_workspace_size(1000, 20_000_000, 1_000_000, 1920, 1080, 16,
+                                          ctypes.byref(sz)) == 0
+    assert 1_000_000 * 12 <= sz.value < 20_000_000 * 4
+    assert lib.gs_bin_sort_workspace_size(1000, 20_000_000, 1_000_000, 1920, 0, 16,
+                                          ctypes.byref(sz)) == -1
     assert lib.gs_bin_count_workspace_size(-1, ctypes.byref(sz)) == -1
 
 
@@ -88,8 +91,10 @@ def test_invalid_arguments_rejected_on_host(lib):
     # more offset entries than the image has tiles
     assert lib.gs_rasterize(null, null, 5, 0, *([null] * 4), 0, 32, 32, 16, 1e-4, 1e-4, 9.21,
                             null, null) == -1
-    assert lib.gs_bin_sort(null, null, null, 10, 64, 64, 16, 2**31, null, null, 0, null, null,
+    assert lib.gs_bin_sort(null, null, null, 10, 64, 64, 16, 2**31, 5, null, null, 0, null, null,
                            null, null, null) == -3
+    assert lib.gs_bin_sort(null, null, null, 10, 64, 64, 16, 5, 6, null, null, 0, null, null,
+                           null, null, null) == -1  # more supertile entries than keys
     sz = ctypes.c_size_t(0)
     assert lib.gs_bin_count(null, null, null, null, 10, 64, 64, 16, null, 0, null, null) == -1
 
