@@ -1,28 +1,30 @@
-// Binning: per-Gaussian tile counts, device scans, LSD radix sort and tile ranges.
+// Binning: per-Gaussian tile counts, a depth sort, and the per-tile lists.
 //
 // The reference (src/cuda/rasterizer.cpp:292-359, src/cuda/kernel.cu:784-914,
 // 1341-1388) emits one 64-bit key (tile_id << 32 | depth_bits) per touched tile
 // in Gaussian order and stably sorts all 64 bits.  The same order -- (tile,
-// depth bits, Gaussian index) -- is produced here with far less sort traffic:
-//   1. a stable sort of the N per-Gaussian depth keys (32 bits, N entries),
-//   2. the (tile, Gaussian) entries of the Gaussians in that depth order,
-//   3. a stable sort of those K entries by tile id (ceil(log2(n_tiles)) bits).
-// A stable sort by tile of a sequence already ordered by (depth, index) is
-// ordered by (tile, depth, index).
+// depth bits, Gaussian index) -- is produced here without ever storing or
+// sorting the K (tile, Gaussian) keys:
+//   1. gs_bin_count: tiles_touched, a packed tile rectangle and the number of
+//      touched supertiles (8 x 8 tiles) per Gaussian; a stable LSD sort of the
+//      N depth keys (32 bits); a scan of the supertile counts in depth order.
+//   2. gs_bin_sort level 1: one (supertile, Gaussian) entry per touched
+//      supertile, in depth order, stably sorted by supertile id -> for every
+//      supertile, the Gaussians meeting it in depth order (M << K entries).
+//   3. gs_bin_sort level 2: each supertile list is cut into 256-entry chunks;
+//      one ballot per local tile counts, then writes, the chunk's Gaussians
+//      covering that tile straight to their final positions.
+// Every stage is stable, so each tile's run is in depth order with ties in
+// Gaussian index order.
 //
-// Radix sort: reduce-then-scan LSD passes of <= 8 bits.  A pass is
-//   upsweep   per-block digit histogram (wave64 ballot matching, one LDS atomic
-//             per distinct digit per wave),
-//   scan      exclusive scan of the digit-major histogram table,
-//   downsweep stable local ranks from the same ballot matching, a scatter into
-//             LDS in digit order, and contiguous runs written to HBM.
-// No pass waits on another workgroup, so no launch can deadlock.
-//
-// The K entries of step 2 are never written unsorted: the first tile pass
-// generates each block's 4096 entries on the fly from the depth-ordered
-// Gaussians (per-block first Gaussian + a search in LDS), once to build the
-// histogram and once to scatter.  Tile ids are stored as 16-bit keys whenever
-// n_tiles <= 65536.
+// Radix sort: LSD passes of <= 8 bits, each
+//   upsweep    per-block digit histogram (wave64 ballot matching, one LDS atomic
+//              per distinct digit per wave), digit-major table,
+//   digit scan one block per digit scans its column and writes the digit total,
+//   downsweep  stable local ranks from the same ballot matching, digit offsets
+//              from the totals, a scatter into LDS in digit order, and
+//              contiguous runs written to HBM.
+// No kernel waits on another workgroup, so no launch can deadlock.
 
 #include "wave_ops.h"
 #include "preprocess_math.h"
