@@ -35,10 +35,10 @@ constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int kRadixMaxBits = 8;
 constexpr int kRadixMax = 1 << kRadixMaxBits;
-constexpr int kSortItems = 16;  // keys per thread in a radix pass
-constexpr int kSortTile = kSortThreads * kSortItems;
-constexpr int kDepthItems = kSortItems;  // the depth sort (N keys)
-constexpr int kTileItems = kSortItems;   // the supertile sort (M keys)
+// Keys per thread in a radix pass: few, so that the N- and M-sized sorts launch
+// enough waves to hide memory latency (these passes are latency-bound).
+constexpr int kDepthItems = 4;  // the depth sort (N keys)
+constexpr int kTileItems = 4;   // the supertile sort (M keys)
 
 constexpr int kSuper = 8;                       // supertile edge, in tiles
 constexpr int kSuperLocal = kSuper * kSuper;    // tiles per supertile (one mask bit each)
@@ -144,12 +144,13 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t key, int shift, uint32_t d
     return (key >> shift) & dmask;
 }
 
+template <int ITEMS>
 struct SortLds {
     uint32_t wave_count[kSortWaves][kRadixMax];
     uint32_t global_start[kRadixMax];
     uint32_t local_start[kRadixMax];
-    uint32_t skeys[kSortTile];
-    uint32_t svals[kSortTile];
+    uint32_t skeys[kSortThreads * ITEMS];
+    uint32_t svals[kSortThreads * ITEMS];
     uint32_t scan_tmp[kSortThreads / kWave + 1];
 };
 
@@ -216,7 +217,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               int nblocks, const uint32_t *__restrict__ table,
                                               KeyT *__restrict__ keys_out,
                                               uint32_t *__restrict__ vals_out, int64_t n,
-                                              bool write_keys, SortLds &s,
+                                              bool write_keys, SortLds<ITEMS> &s,
                                               const uint32_t *__restrict__ totals,
                                               const uint32_t *__restrict__ touched = nullptr,
                                               uint64_t *__restrict__ counts_out = nullptr) {
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     int nbits, int nblocks, const uint32_t *__restrict__ table,
     const uint32_t *__restrict__ totals, int write_keys, const uint32_t *__restrict__ touched,
     uint64_t *__restrict__ counts_out) {
-    __shared__ SortLds s;
+    __shared__ SortLds<ITEMS> s;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS], v[ITEMS];
     bool valid[ITEMS];
@@ -611,7 +612,13 @@ __device__ __forceinline__ uint32_t wave_local_counts(uint64_t mask) {
     return mine;
 }
 
-// counts[t] += entries of tile t in this block; table[b * 64 + j] = the same per local tile.
+// Table entry of (level-2 block b, wave w, local tile j).
+__device__ __forceinline__ int64_t l2_slot(uint32_t b, int w, int j) {
+    return ((int64_t)b * kL2Waves + w) * kSuperLocal + j;
+}
+
+// table[(b, w, j)] = entries of local tile j in wave w of block b;
+// counts[t] += the block's entries of tile t.
 __global__ __launch_bounds__(kL2Threads) void l2_count_kernel(L2Args a,
                                                               uint32_t *__restrict__ table,
                                                               uint32_t *__restrict__ counts) {
@@ -619,22 +626,23 @@ __global__ __launch_bounds__(kL2Threads) void l2_count_kernel(L2Args a,
     L2Block x;
     if (!l2_block(a, x)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    wave_cnt[wave][lane] = wave_local_counts(x.mask);
+    const uint32_t mine = wave_local_counts(x.mask);
+    wave_cnt[wave][lane] = mine;
+    table[l2_slot(x.b, wave, lane)] = mine;
     __syncthreads();
     if (threadIdx.x < kSuperLocal) {
         const int j = threadIdx.x;
         uint32_t c = 0;
 #pragma unroll
         for (int w = 0; w < kL2Waves; ++w) c += wave_cnt[w][j];
-        table[(int64_t)x.b * kSuperLocal + j] = c;
         const int t = tile_of_local(a, x.s, j);
         if (c && t >= 0) atomicAdd(&counts[t], c);
     }
 }
 
-// table[b * 64 + j] <- first output position of block b's entries of local tile
-// j: indexing_offset of the tile plus its entries in the earlier chunks of the
-// supertile.  One thread per (supertile, local tile).
+// table[(b, w, j)] <- first output position of the entries of local tile j in
+// wave w of block b: indexing_offset of the tile plus its entries in the earlier
+// waves and chunks of the supertile.  One thread per (supertile, local tile).
 __global__ __launch_bounds__(256) void l2_prefix_kernel(L2Args a,
                                                         const int32_t *__restrict__ tile_offsets,
                                                         uint32_t *__restrict__ table) {
@@ -644,21 +652,15 @@ __global__ __launch_bounds__(256) void l2_prefix_kernel(L2Args a,
     const int t = tile_of_local(a, s, j);
     uint32_t pos = t >= 0 ? (uint32_t)tile_offsets[t] : 0u;
     const uint32_t q1 = a.chunk_start[s + 1];
-    uint32_t q = a.chunk_start[s];
-    for (; q + 4 <= q1; q += 4) {  // four independent loads per step
-        uint32_t c[4];
+    for (uint32_t q = a.chunk_start[s]; q < q1; ++q) {
+        uint32_t c[kL2Waves];  // independent loads
 #pragma unroll
-        for (int u = 0; u < 4; ++u) c[u] = table[(int64_t)(q + u) * kSuperLocal + j];
+        for (int w = 0; w < kL2Waves; ++w) c[w] = table[l2_slot(q, w, j)];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            table[(int64_t)(q + u) * kSuperLocal + j] = pos;
-            pos += c[u];
+        for (int w = 0; w < kL2Waves; ++w) {
+            table[l2_slot(q, w, j)] = pos;
+            pos += c[w];
         }
-    }
-    for (; q < q1; ++q) {
-        const uint32_t c = table[(int64_t)q * kSuperLocal + j];
-        table[(int64_t)q * kSuperLocal + j] = pos;
-        pos += c;
     }
 }
 
@@ -669,18 +671,7 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
     L2Block x;
     if (!l2_block(a, x)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    base[wave][lane] = wave_local_counts(x.mask);
-    __syncthreads();
-    if (threadIdx.x < kSuperLocal) {
-        const int j = threadIdx.x;
-        uint32_t pos = table[(int64_t)x.b * kSuperLocal + j];  // from l2_prefix_kernel
-#pragma unroll
-        for (int w = 0; w < kL2Waves; ++w) {
-            const uint32_t c = base[w][j];
-            base[w][j] = pos;
-            pos += c;
-        }
-    }
+    base[wave][lane] = table[l2_slot(x.b, wave, lane)];  // from l2_prefix_kernel
     __syncthreads();
     const uint64_t below = lanemask_lt();
 #pragma unroll 4
@@ -847,7 +838,7 @@ struct BinWs {
     int32_t *super_ids;    // m
     uint32_t *chunks;      // n_super + 1: chunk counts, scanned in place to chunk_start
     uint2 *block_map;      // level-2 block -> (supertile, first list position)
-    uint32_t *table;       // level-2 blocks x 64
+    uint32_t *table;       // level-2 blocks x waves x 64
     void *scan_ws;
     size_t bytes;
 };
@@ -860,7 +851,7 @@ inline BinWs carve_bins(void *base, int64_t m, const Grid &g) {
     w.super_ids = c.take<int32_t>(m);
     w.chunks = c.take<uint32_t>((int64_t)g.n_super + 1);
     w.block_map = c.take<uint2>(l2_blocks_bound(m, g.n_super));
-    w.table = c.take<uint32_t>(l2_blocks_bound(m, g.n_super) * kSuperLocal);
+    w.table = c.take<uint32_t>(l2_blocks_bound(m, g.n_super) * kL2Waves * kSuperLocal);
     const int64_t scan_n = g.n_super > g.n_tiles ? g.n_super : g.n_tiles;
     w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint32_t>(scan_n));
     w.bytes = align256(c.off);

@@ -233,6 +233,15 @@ __device__ __forceinline__ float display_grad(float g, float raw) {
     return (raw >= 0.0f && raw <= 1.0f) ? g * 255.0f : 0.0f;
 }
 
+// Gradient w.r.t. display of scale * |display / 255 - t| (torch's l1_loss: sign
+// of the difference, 0 at 0; then the division by 255).
+__device__ __forceinline__ float l1_grad(float t, float raw, float scale) {
+    const float x = (clamp01(raw) * 255.0f) / 255.0f;
+    const float d = x - t;
+    const float sgn = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
+    return (sgn * scale) / 255.0f;
+}
+
 // Some pixel of the wave still composites: !(T < T_thr) (NaN stays active).
 __device__ __forceinline__ bool any_active(const float (&T)[kStrips], float T_thr) {
     return wave_any(!(T[0] < T_thr) || !(T[1] < T_thr) || !(T[2] < T_thr) || !(T[3] < T_thr));
@@ -293,34 +302,6 @@ __device__ __forceinline__ void blend_accumulate(
     }
 }
 
-__global__ __launch_bounds__(kWave) void blend_forward_kernel(
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
-    int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
-    const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
-    int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image,
-    float *__restrict__ display) {
-    __shared__ BatchLds s;
-    const int tile = tile_of_block(blockIdx.x, n_tiles);
-    const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
-    const TileSpan span = tile_span(offsets, n_tiles, k, tile);
-    float cr[kStrips], cg[kStrips], cb[kStrips];
-    blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr, chi, cr,
-                     cg, cb);
-#pragma unroll
-    for (int q = 0; q < kStrips; ++q) {
-        if (!pix.inside[q]) continue;
-        const int64_t o = ((int64_t)pix.fy[q] * width + (int64_t)pix.fx) * 3;
-        image[o] = cr[q];
-        image[o + 1] = cg[q];
-        image[o + 2] = cb[q];
-        if (display) {  // image.clamp(0, 1) * 255 (src/cuda/wrapper.py:294)
-            display[o] = clamp01(cr[q]) * 255.0f;
-            display[o + 1] = clamp01(cg[q]) * 255.0f;
-            display[o + 2] = clamp01(cb[q]) * 255.0f;
-        }
-    }
-}
-
 // ------------------------------------------------- wave reductions (gfx950)
 
 #define GS_DPP(x, ctrl) \
@@ -345,6 +326,16 @@ __device__ __forceinline__ float swap16_add(float a, float b) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
                                                     false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the 64 lanes, in every lane.
+__device__ __forceinline__ float wave_sum(float x) {
+    x += GS_DPP(x, kDppXor1);
+    x += GS_DPP(x, kDppXor2);
+    x += GS_DPP(x, kDppHalfMirror);
+    x += GS_DPP(x, kDppMirror);
+    x = swap16_add(x, x);
+    return swap32_add(x, x);
 }
 
 // Lane that holds field f's wave total after wave_sum9 (the others hold partials):
@@ -391,6 +382,44 @@ __device__ __forceinline__ float wave_sum9(const float (&f)[kGradFields], bool h
     return f8_lane ? q2 : r;
 }
 
+__global__ __launch_bounds__(kWave) void blend_forward_kernel(
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
+    int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
+    const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
+    int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image,
+    float *__restrict__ display, const float *__restrict__ target,
+    float *__restrict__ tile_loss) {
+    __shared__ BatchLds s;
+    const int tile = tile_of_block(blockIdx.x, n_tiles);
+    const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
+    const TileSpan span = tile_span(offsets, n_tiles, k, tile);
+    float cr[kStrips], cg[kStrips], cb[kStrips];
+    blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr, chi, cr,
+                     cg, cb);
+    float l1 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        if (!pix.inside[q]) continue;
+        const int64_t o = ((int64_t)pix.fy[q] * width + (int64_t)pix.fx) * 3;
+        image[o] = cr[q];
+        image[o + 1] = cg[q];
+        image[o + 2] = cb[q];
+        if (display) {  // image.clamp(0, 1) * 255 (src/cuda/wrapper.py:294)
+            const float d[3] = {clamp01(cr[q]) * 255.0f, clamp01(cg[q]) * 255.0f,
+                                clamp01(cb[q]) * 255.0f};
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                display[o + c] = d[c];
+                if (target) l1 += fabsf(d[c] / 255.0f - target[o + c]);  // |display/255 - t|
+            }
+        }
+    }
+    if (tile_loss) {  // per-tile sum of the L1 terms (reduced by gs_l1_finish)
+        l1 = wave_sum(l1);
+        if (threadIdx.x == 0) tile_loss[tile] = l1;
+    }
+}
+
 // Destination of the lane's field after wave_sum9: out[stride * g] += value * (fa * o + fb).
 struct GradTarget {
     float *base;
@@ -431,20 +460,29 @@ __device__ __forceinline__ GradTarget grad_target(int lane, float *g_points, flo
 // A lane's four pixels share du, so it keeps sG = sum G dalpha, s1 = sum G dalpha dv,
 // s2 = sum G dalpha dv^2 and the colour sums, and forms the nine fields (up to the
 // uniform factor o, applied after the wave sum) once per Gaussian.
-// kDisplay: grad_image is the gradient of clamp(image, 0, 1) * 255 (image required).
-template <bool kDisplay>
+// kSeed: kSeedImage  grad_image is the gradient of the image;
+//        kSeedDisplay grad_image is the gradient of display = clamp(image, 0, 1) * 255
+//                     (image required);
+//        kSeedL1      the gradient is that of loss = mean(|display / 255 - target|)
+//                     times *grad_loss: grad_image holds the target (image required).
+enum { kSeedImage = 0, kSeedDisplay = 1, kSeedL1 = 2 };
+
+template <int kSeed>
 __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const float *__restrict__ grad_image, const float *__restrict__ image,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr, float chi, float *__restrict__ g_points,
-    float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors) {
+    float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors,
+    const float *__restrict__ grad_loss, float inv_count) {
     __shared__ BatchLds s;
     const int tile = tile_of_block(blockIdx.x, n_tiles);
     const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
     if (span.end <= span.start) return;  // uniform across the workgroup
+    // d loss / d (display / 255) per element, for kSeedL1
+    const float l1_scale = kSeed == kSeedL1 ? *grad_loss * inv_count : 0.0f;
 
     float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips], T[kStrips], acc[kStrips];
     float cr[kStrips], cg[kStrips], cb[kStrips];
@@ -464,7 +502,12 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
                 cg[q] = image[o + 1];
                 cb[q] = image[o + 2];
             }
-            if (kDisplay) {
+            if (kSeed == kSeedL1) {  // sign(display/255 - t) * g / n, then / 255
+                gr[q] = l1_grad(gr[q], cr[q], l1_scale);
+                gg[q] = l1_grad(gg[q], cg[q], l1_scale);
+                gb[q] = l1_grad(gb[q], cb[q], l1_scale);
+            }
+            if (kSeed != kSeedImage) {
                 gr[q] = display_grad(gr[q], cr[q]);
                 gg[q] = display_grad(gg[q], cg[q]);
                 gb[q] = display_grad(gb[q], cb[q]);
@@ -737,7 +780,7 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                           int64_t n, int32_t width, int32_t height, int32_t tile_size,
                           float alpha_threshold, float transmittance_threshold,
                           float chi_squared_threshold, float *image, float *display,
-                          hipStream_t stream) {
+                          const float *target, float *tile_loss, hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -761,7 +804,7 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                            indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
-                           image, display);
+                           image, display, target, tile_loss);
     } else {
         hipLaunchKernelGGL(blend_forward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, indexing_offset,
@@ -783,7 +826,7 @@ extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gauss
     return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
                           cov_inv_image, opacities, colors, n, width, height, tile_size,
                           alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
-                          nullptr, stream);
+                          nullptr, nullptr, nullptr, stream);
 }
 
 extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
@@ -798,7 +841,50 @@ extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
     return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
                           cov_inv_image, opacities, colors, n, width, height, tile_size,
                           alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
-                          display, stream);
+                          display, nullptr, nullptr, stream);
+}
+
+extern "C" int gs_rasterize_display_l1(
+    const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k,
+    const float *points_image, const float *cov_inv_image, const float *opacities,
+    const float *colors, int64_t n, int32_t width, int32_t height, int32_t tile_size,
+    float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
+    const float *target, float *image, float *display, float *tile_loss, hipStream_t stream) {
+    if (!display || !target || !tile_loss || tile_size != kTile) return GS_ERR_INVALID_ARGUMENT;
+    const int tiles_x = (width + tile_size - 1) / tile_size;
+    const int tiles_y = (height + tile_size - 1) / tile_size;
+    if (n_tiles != tiles_x * tiles_y) return GS_ERR_INVALID_ARGUMENT;  // every tile's loss
+    return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
+                          cov_inv_image, opacities, colors, n, width, height, tile_size,
+                          alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
+                          display, target, tile_loss, stream);
+}
+
+// loss = (sum of the n_tiles partial sums) / count, one workgroup.
+__global__ __launch_bounds__(1024) void l1_finish_kernel(int n_tiles,
+                                                         const float *__restrict__ tile_loss,
+                                                         float inv_count,
+                                                         float *__restrict__ loss) {
+    __shared__ float tmp[1024 / kWave];
+    float acc = 0.0f;
+    for (int t = threadIdx.x; t < n_tiles; t += 1024) acc += tile_loss[t];
+    acc = wave_sum(acc);
+    if (threadIdx.x % kWave == 0) tmp[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float total = 0.0f;
+        for (int w = 0; w < 1024 / kWave; ++w) total += tmp[w];
+        *loss = total * inv_count;
+    }
+}
+
+extern "C" int gs_l1_finish(const float *tile_loss, int32_t n_tiles, int64_t count, float *loss,
+                            hipStream_t stream) {
+    if (n_tiles < 0 || count <= 0 || !loss || (n_tiles > 0 && !tile_loss))
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(l1_finish_kernel, dim3(1), dim3(1024), 0, stream, n_tiles, tile_loss,
+                       (float)(1.0 / (double)count), loss);
+    return launch_status();
 }
 
 static int rasterize_backward_impl(
@@ -808,14 +894,15 @@ static int rasterize_backward_impl(
     int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
     float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
     float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
-    bool display, hipStream_t stream) {
+    int seed, const float *grad_loss, float inv_count, hipStream_t stream) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
     if (st) return st;
     if (n > 0 && (!grad_points_image || !grad_cov_inv_image || !grad_opacities || !grad_colors))
         return GS_ERR_INVALID_ARGUMENT;
-    if (display && (!image || tile_size != kTile)) return GS_ERR_INVALID_ARGUMENT;
+    if (seed != kSeedImage && (!image || tile_size != kTile)) return GS_ERR_INVALID_ARGUMENT;
+    if (seed == kSeedL1 && !grad_loss) return GS_ERR_INVALID_ARGUMENT;
     if (n > 0 && !accumulate) {
         st = zero_bytes(grad_points_image, (size_t)n * 2 * sizeof(float), stream);
         if (!st) st = zero_bytes(grad_cov_inv_image, (size_t)n * 3 * sizeof(float), stream);
@@ -828,20 +915,15 @@ static int rasterize_backward_impl(
         return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     if (tile_size == kTile) {
-        if (display)
-            hipLaunchKernelGGL(blend_backward_kernel<true>, dim3(n_tiles), dim3(kWave), 0, stream,
-                               grad_image, image, indexing_offset, gaussian_ids_sorted, n_tiles,
-                               k, n, points_image, cov_inv_image, opacities, colors, tiles_x,
-                               width, height, alpha_threshold, transmittance_threshold,
-                               chi_squared_threshold, grad_points_image, grad_cov_inv_image,
-                               grad_opacities, grad_colors);
-        else
-            hipLaunchKernelGGL(blend_backward_kernel<false>, dim3(n_tiles), dim3(kWave), 0,
-                               stream, grad_image, image, indexing_offset, gaussian_ids_sorted,
-                               n_tiles, k, n, points_image, cov_inv_image, opacities, colors,
-                               tiles_x, width, height, alpha_threshold, transmittance_threshold,
-                               chi_squared_threshold, grad_points_image, grad_cov_inv_image,
-                               grad_opacities, grad_colors);
+        auto kern = seed == kSeedL1       ? blend_backward_kernel<kSeedL1>
+                    : seed == kSeedDisplay ? blend_backward_kernel<kSeedDisplay>
+                                           : blend_backward_kernel<kSeedImage>;
+        hipLaunchKernelGGL(kern, dim3(n_tiles), dim3(kWave), 0, stream, grad_image, image,
+                           indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
+                           cov_inv_image, opacities, colors, tiles_x, width, height,
+                           alpha_threshold, transmittance_threshold, chi_squared_threshold,
+                           grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors,
+                           grad_loss, inv_count);
     } else {
         hipLaunchKernelGGL(blend_backward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, grad_image, image,
@@ -866,7 +948,7 @@ extern "C" int gs_rasterize_backward(
                                    width, height, tile_size, alpha_threshold,
                                    transmittance_threshold, chi_squared_threshold,
                                    grad_points_image, grad_cov_inv_image, grad_opacities,
-                                   grad_colors, accumulate, false, stream);
+                                   grad_colors, accumulate, kSeedImage, nullptr, 0.0f, stream);
 }
 
 extern "C" int gs_rasterize_display_backward(
@@ -882,7 +964,25 @@ extern "C" int gs_rasterize_display_backward(
                                    width, height, tile_size, alpha_threshold,
                                    transmittance_threshold, chi_squared_threshold,
                                    grad_points_image, grad_cov_inv_image, grad_opacities,
-                                   grad_colors, accumulate, true, stream);
+                                   grad_colors, accumulate, kSeedDisplay, nullptr, 0.0f, stream);
+}
+
+extern "C" int gs_rasterize_l1_backward(
+    const float *target, const float *grad_loss, const float *image,
+    const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted, int32_t n_tiles,
+    int64_t k, const float *points_image, const float *cov_inv_image, const float *opacities,
+    const float *colors, int64_t n, int32_t width, int32_t height, int32_t tile_size,
+    float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
+    float *grad_points_image, float *grad_cov_inv_image, float *grad_opacities,
+    float *grad_colors, int32_t accumulate, hipStream_t stream) {
+    if (!target || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
+    const float inv_count = (float)(1.0 / ((double)width * (double)height * 3.0));
+    return rasterize_backward_impl(target, image, indexing_offset, gaussian_ids_sorted, n_tiles,
+                                   k, points_image, cov_inv_image, opacities, colors, n, width,
+                                   height, tile_size, alpha_threshold, transmittance_threshold,
+                                   chi_squared_threshold, grad_points_image, grad_cov_inv_image,
+                                   grad_opacities, grad_colors, accumulate, kSeedL1, grad_loss,
+                                   inv_count, stream);
 }
 
 extern "C" int gs_rasterize_work(const int32_t *indexing_offset,

@@ -183,7 +183,7 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(
     const float *__restrict__ w2c, const float *__restrict__ means,
     const float *__restrict__ sh_dc, const float *__restrict__ sh_rest,
     const float *__restrict__ colors, const uint8_t *__restrict__ mask, int mode,
-    float *__restrict__ grad_means, float *__restrict__ grad_dc,
+    int accumulate_means, float *__restrict__ grad_means, float *__restrict__ grad_dc,
     float *__restrict__ grad_rest) {
     __shared__ __align__(16) float rest_lds[kShBlock * kRest];
     const int64_t first = (int64_t)blockIdx.x * kShBlock;
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(
         }
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            grad_means[3 * i + c] = gm[c];
+            grad_means[3 * i + c] = accumulate_means ? grad_means[3 * i + c] + gm[c] : gm[c];
             grad_dc[3 * i + c] = gdc[c];
         }
     }
@@ -317,8 +317,8 @@ static int launch_sh_forward(const float *camera_pos, const float *w2c, const fl
 static int launch_sh_backward(const float *grad_colors, const float *camera_pos,
                               const float *w2c, const float *means, const float *sh_dc,
                               const float *sh_rest, const float *colors, const uint8_t *mask,
-                              int64_t n, int mode, float *grad_means, float *grad_sh_dc,
-                              float *grad_sh_rest, hipStream_t stream) {
+                              int64_t n, int mode, int accumulate_means, float *grad_means,
+                              float *grad_sh_dc, float *grad_sh_rest, hipStream_t stream) {
     if (n < 0) return GS_ERR_INVALID_ARGUMENT;
     if (n == 0) return GS_OK;
     if (!grad_colors || (!camera_pos && !w2c) || !means || !sh_rest || !mask || !grad_means ||
@@ -327,7 +327,7 @@ static int launch_sh_backward(const float *grad_colors, const float *camera_pos,
         return GS_ERR_INVALID_ARGUMENT;
     hipLaunchKernelGGL(sh_backward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
                        stream, n, grad_colors, camera_pos, w2c, means, sh_dc, sh_rest, colors,
-                       mask, mode, grad_means, grad_sh_dc, grad_sh_rest);
+                       mask, mode, accumulate_means, grad_means, grad_sh_dc, grad_sh_rest);
     return launch_status();
 }
 
@@ -347,7 +347,7 @@ extern "C" int gs_evaluate_sh_backward(const float *grad_colors, const float *ca
                                        float *grad_sh_rest, hipStream_t stream) {
     if (!camera_pos && n > 0) return GS_ERR_INVALID_ARGUMENT;
     return launch_sh_backward(grad_colors, camera_pos, nullptr, means, sh_dc, sh_rest, colors,
-                              mask, n, sh_sigmoid ? kShSigmoid : kShRaw, grad_means,
+                              mask, n, sh_sigmoid ? kShSigmoid : kShRaw, 0, grad_means,
                               grad_sh_dc, grad_sh_rest, stream);
 }
 
@@ -364,10 +364,95 @@ extern "C" int gs_evaluate_sh_render_backward(const float *grad_colors,
                                               const float *world_to_camera, const float *means,
                                               const float *sh_dc, const float *sh_rest,
                                               const uint8_t *mask, int64_t n,
-                                              float *grad_means, float *grad_sh_dc,
-                                              float *grad_sh_rest, hipStream_t stream) {
+                                              int32_t accumulate_means, float *grad_means,
+                                              float *grad_sh_dc, float *grad_sh_rest,
+                                              hipStream_t stream) {
     if (!world_to_camera && n > 0) return GS_ERR_INVALID_ARGUMENT;
     return launch_sh_backward(grad_colors, nullptr, world_to_camera, means, sh_dc, sh_rest,
-                              nullptr, mask, n, kShRender, grad_means, grad_sh_dc, grad_sh_rest,
-                              stream);
+                              nullptr, mask, n, kShRender, accumulate_means ? 1 : 0, grad_means,
+                              grad_sh_dc, grad_sh_rest, stream);
+}
+
+// ------------------------------------------------------------- activations
+// scripts/train.py:135-143: scales = exp(log_scales), quats = q / max(|q|, 1e-12),
+// opacities = sigmoid(logits).  One thread per Gaussian.
+
+__global__ __launch_bounds__(256) void activate_kernel(int64_t n,
+                                                      const float *__restrict__ log_scales,
+                                                      const float *__restrict__ quats_raw,
+                                                      const float *__restrict__ logits,
+                                                      float *__restrict__ scales,
+                                                      float *__restrict__ quats,
+                                                      float *__restrict__ opac) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) scales[3 * i + c] = expf(log_scales[3 * i + c]);
+    const float4 q = reinterpret_cast<const float4 *>(quats_raw)[i];
+    const float norm = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+    const float r = norm < 1e-12f ? 1e-12f : norm;  // clamp_min(1e-12)
+    reinterpret_cast<float4 *>(quats)[i] = make_float4(q.x / r, q.y / r, q.z / r, q.w / r);
+    opac[i] = 1.0f / (1.0f + expf(-logits[i]));
+}
+
+// Gradients of activate_kernel's outputs mapped to its inputs; a null gradient
+// input counts as zero.
+__global__ __launch_bounds__(256) void activate_backward_kernel(
+    int64_t n, const float *__restrict__ grad_scales, const float *__restrict__ grad_quats,
+    const float *__restrict__ grad_opac, const float *__restrict__ scales,
+    const float *__restrict__ quats_raw, const float *__restrict__ opac,
+    float *__restrict__ grad_log_scales, float *__restrict__ grad_quats_raw,
+    float *__restrict__ grad_logits) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+        grad_log_scales[3 * i + c] = grad_scales ? grad_scales[3 * i + c] * scales[3 * i + c] : 0.0f;
+    const float4 q = reinterpret_cast<const float4 *>(quats_raw)[i];
+    float4 g = grad_quats ? reinterpret_cast<const float4 *>(grad_quats)[i]
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float norm = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+    float4 out;
+    if (norm < 1e-12f) {  // the clamp holds the divisor constant
+        out = make_float4(g.x / 1e-12f, g.y / 1e-12f, g.z / 1e-12f, g.w / 1e-12f);
+    } else {  // d(q/|q|) = (g - qhat (qhat . g)) / |q|
+        const float hx = q.x / norm, hy = q.y / norm, hz = q.z / norm, hw = q.w / norm;
+        const float dot = hx * g.x + hy * g.y + hz * g.z + hw * g.w;
+        out = make_float4((g.x - hx * dot) / norm, (g.y - hy * dot) / norm,
+                          (g.z - hz * dot) / norm, (g.w - hw * dot) / norm);
+    }
+    reinterpret_cast<float4 *>(grad_quats_raw)[i] = out;
+    const float o = opac[i];
+    grad_logits[i] = grad_opac ? grad_opac[i] * (o * (1.0f - o)) : 0.0f;
+}
+
+extern "C" int gs_activate(const float *log_scales, const float *quats_raw,
+                           const float *opacity_logits, int64_t n, float *scales, float *quats,
+                           float *opacities, hipStream_t stream) {
+    if (n < 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GS_OK;
+    if (!log_scales || !quats_raw || !opacity_logits || !scales || !quats || !opacities ||
+        (reinterpret_cast<uintptr_t>(quats_raw) & 15) || (reinterpret_cast<uintptr_t>(quats) & 15))
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(activate_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream, n,
+                       log_scales, quats_raw, opacity_logits, scales, quats, opacities);
+    return launch_status();
+}
+
+extern "C" int gs_activate_backward(const float *grad_scales, const float *grad_quats,
+                                    const float *grad_opacities, const float *scales,
+                                    const float *quats_raw, const float *opacities, int64_t n,
+                                    float *grad_log_scales, float *grad_quats_raw,
+                                    float *grad_opacity_logits, hipStream_t stream) {
+    if (n < 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GS_OK;
+    if (!scales || !quats_raw || !opacities || !grad_log_scales || !grad_quats_raw ||
+        !grad_opacity_logits || (reinterpret_cast<uintptr_t>(quats_raw) & 15) ||
+        (reinterpret_cast<uintptr_t>(grad_quats_raw) & 15) ||
+        (grad_quats && (reinterpret_cast<uintptr_t>(grad_quats) & 15)))
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(activate_backward_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream, n,
+                       grad_scales, grad_quats, grad_opacities, scales, quats_raw, opacities,
+                       grad_log_scales, grad_quats_raw, grad_opacity_logits);
+    return launch_status();
 }

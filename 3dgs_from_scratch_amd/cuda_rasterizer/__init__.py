@@ -44,6 +44,10 @@ __all__ = [
     "evaluate_spherical_harmonics_render_backward",
     "rasterize_display",
     "rasterize_display_backward",
+    "activate",
+    "activate_backward",
+    "rasterize_display_l1",
+    "rasterize_l1_backward",
     "RasterizerError",
 ]
 
@@ -480,9 +484,12 @@ def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs
 
 
 def evaluate_spherical_harmonics_render_backward(grad_colors, world_to_camera, points_world,
-                                                 sh_coeffs_dc, sh_coeffs_rest, mask):
+                                                 sh_coeffs_dc, sh_coeffs_rest, mask,
+                                                 accumulate_means=None):
     """Gradient of evaluate_spherical_harmonics_render.  Returns
-    (grad_points_world[N,3], grad_sh_coeffs_dc[N,3], grad_sh_coeffs_rest[N,15,3])."""
+    (grad_points_world[N,3], grad_sh_coeffs_dc[N,3], grad_sh_coeffs_rest[N,15,3]).
+    With `accumulate_means` (an (N,3) fp32 tensor on the device), the means
+    gradient is added to it in place and it is returned as the first element."""
     dev = _device_of(points_world)
     n = points_world.shape[0]
     f32 = torch.float32
@@ -492,7 +499,14 @@ def evaluate_spherical_harmonics_render_backward(grad_colors, world_to_camera, p
     sh_coeffs_dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
     sh_coeffs_rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
     mask = _prep(mask, "mask", torch.bool, (n,), dev)
-    g_means = torch.empty((n, 3), dtype=f32, device=dev)
+    if accumulate_means is not None:
+        if (accumulate_means.dtype != f32 or accumulate_means.shape != (n, 3)
+                or not accumulate_means.is_contiguous() or accumulate_means.device != dev):
+            raise RuntimeError("accumulate_means must be a contiguous (N,3) fp32 tensor on "
+                               f"{dev}")
+        g_means = accumulate_means
+    else:
+        g_means = torch.empty((n, 3), dtype=f32, device=dev)
     g_dc = torch.empty((n, 3), dtype=f32, device=dev)
     g_rest = torch.empty((n, 15, 3), dtype=f32, device=dev)
     with torch.cuda.device(dev):
@@ -500,8 +514,8 @@ def evaluate_spherical_harmonics_render_backward(grad_colors, world_to_camera, p
         _lib.check(
             _lib.load().gs_evaluate_sh_render_backward(
                 _ptr(grad_colors), _ptr(world_to_camera), _ptr(points_world), _ptr(sh_coeffs_dc),
-                _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(g_means), _ptr(g_dc), _ptr(g_rest),
-                _stream(dev),
+                _ptr(sh_coeffs_rest), _ptr(mask), n, 1 if accumulate_means is not None else 0,
+                _ptr(g_means), _ptr(g_dc), _ptr(g_rest), _stream(dev),
             ),
             "evaluate_spherical_harmonics_render_backward",
         )
@@ -559,5 +573,108 @@ def rasterize_display_backward(grad_display, indexing_offset, gaussian_ids_sorte
             ),
             "rasterize_display_backward",
         )
+        _lib.timer.stop(ev, dev)
+    return g_pts, g_conic, g_opac, g_col
+
+
+# ------------------------------------------------------ fused training step
+# Kernels for the caller-side glue of a training step (activations and the L1
+# loss, scripts/train.py:135-143,187-191); cuda_rasterizer.fused chains them.
+
+
+def activate(log_scales, quats_raw, opacity_logits):
+    """(exp(log_scales), q / max(|q|, 1e-12), sigmoid(logits)) in one kernel."""
+    dev = _device_of(log_scales)
+    n = log_scales.shape[0]
+    f32 = torch.float32
+    log_scales = _prep(log_scales, "log_scales", f32, (n, 3), dev)
+    quats_raw = _prep(quats_raw, "quats_raw", f32, (n, 4), dev)
+    opacity_logits = _prep(opacity_logits, "opacity_logits", f32, (n,), dev)
+    scales = torch.empty((n, 3), dtype=f32, device=dev)
+    quats = torch.empty((n, 4), dtype=f32, device=dev)
+    opac = torch.empty((n,), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("activate", dev)
+        _lib.check(_lib.load().gs_activate(_ptr(log_scales), _ptr(quats_raw), _ptr(opacity_logits),
+                                           n, _ptr(scales), _ptr(quats), _ptr(opac), _stream(dev)),
+                   "activate")
+        _lib.timer.stop(ev, dev)
+    return scales, quats, opac
+
+
+def activate_backward(grad_scales, grad_quats, grad_opacities, scales, quats_raw, opacities):
+    """Gradients of activate's outputs (None = zero) -> (d log_scales, d quats_raw, d logits)."""
+    dev = _device_of(scales)
+    n = scales.shape[0]
+    f32 = torch.float32
+    gs_ = None if grad_scales is None else _prep(grad_scales, "grad_scales", f32, (n, 3), dev)
+    gq = None if grad_quats is None else _prep(grad_quats, "grad_quats", f32, (n, 4), dev)
+    go = None if grad_opacities is None else _prep(grad_opacities, "grad_opacities", f32, (n,), dev)
+    scales = _prep(scales, "scales", f32, (n, 3), dev)
+    quats_raw = _prep(quats_raw, "quats_raw", f32, (n, 4), dev)
+    opacities = _prep(opacities, "opacities", f32, (n,), dev)
+    g_ls = torch.empty((n, 3), dtype=f32, device=dev)
+    g_q = torch.empty((n, 4), dtype=f32, device=dev)
+    g_l = torch.empty((n,), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("activate_backward", dev)
+        _lib.check(_lib.load().gs_activate_backward(
+            _ptr(gs_), _ptr(gq), _ptr(go), _ptr(scales), _ptr(quats_raw), _ptr(opacities), n,
+            _ptr(g_ls), _ptr(g_q), _ptr(g_l), _stream(dev)), "activate_backward")
+        _lib.timer.stop(ev, dev)
+    return g_ls, g_q, g_l
+
+
+def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
+                         opacities, colors, width, height, target, alpha_threshold=1e-4,
+                         transmittance_threshold=1e-4, chi_squared_threshold=9.21):
+    """rasterize_display with tile size 16 plus loss = mean(|display / 255 - target|).
+    Returns (image, display, loss[1] fp32)."""
+    dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
+        indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
+    width, height = int(width), int(height)
+    f32 = torch.float32
+    target = _prep(target, "target", f32, (height, width, 3), dev)
+    image = torch.empty((height, width, 3), dtype=f32, device=dev)
+    display = torch.empty((height, width, 3), dtype=f32, device=dev)
+    n_tiles = off.shape[0]
+    tile_loss = torch.empty((max(n_tiles, 1),), dtype=f32, device=dev)
+    loss = torch.empty((1,), dtype=f32, device=dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("rasterize_display_l1", dev)
+        _lib.check(lib.gs_rasterize_display_l1(
+            _ptr(off), _ptr(ids), n_tiles, ids.shape[0], _ptr(pts), _ptr(conic), _ptr(opac),
+            _ptr(col), n, width, height, 16, float(alpha_threshold), float(transmittance_threshold),
+            float(chi_squared_threshold), _ptr(target), _ptr(image), _ptr(display), _ptr(tile_loss),
+            _stream(dev)), "rasterize_display_l1")
+        _lib.timer.stop(ev, dev)
+        _lib.check(lib.gs_l1_finish(_ptr(tile_loss), n_tiles, height * width * 3, _ptr(loss),
+                                    _stream(dev)), "l1_finish")
+    return image, display, loss
+
+
+def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorted, points_image,
+                          cov_inv_image, opacities, colors, width, height, rendered_image,
+                          alpha_threshold=1e-4, transmittance_threshold=1e-4,
+                          chi_squared_threshold=9.21):
+    """Gradient of rasterize_display_l1's loss (times grad_loss, a 1-element fp32
+    device tensor) w.r.t. the four blend inputs."""
+    dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
+        indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
+    width, height = int(width), int(height)
+    f32 = torch.float32
+    target = _prep(target, "target", f32, (height, width, 3), dev)
+    img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
+    gl = _prep(grad_loss.reshape(1), "grad_loss", f32, (1,), dev)
+    g_pts, g_conic, g_opac, g_col = _zeroed_blend_grads(n, dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("rasterize_l1_backward", dev)
+        _lib.check(_lib.load().gs_rasterize_l1_backward(
+            _ptr(target), _ptr(gl), _ptr(img), _ptr(off), _ptr(ids), off.shape[0], ids.shape[0],
+            _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, 16,
+            float(alpha_threshold), float(transmittance_threshold), float(chi_squared_threshold),
+            _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), 1, _stream(dev)),
+            "rasterize_l1_backward")
         _lib.timer.stop(ev, dev)
     return g_pts, g_conic, g_opac, g_col

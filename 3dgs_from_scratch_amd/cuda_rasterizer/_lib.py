@@ -30,7 +30,14 @@ SIGNATURES = {
     "gs_rasterize_work": [_P, _P, _I32, _I64] + [_P] * 3 + [_I64, _I32, _I32, _I32, _F, _F, _F]
     + [_P, _P, _P],
     "gs_evaluate_sh_render": [_P] * 5 + [_I64, _P, _P],
-    "gs_evaluate_sh_render_backward": [_P] * 6 + [_I64] + [_P] * 3 + [_P],
+    "gs_evaluate_sh_render_backward": [_P] * 6 + [_I64, _I32] + [_P] * 3 + [_P],
+    "gs_activate": [_P] * 3 + [_I64] + [_P] * 3 + [_P],
+    "gs_activate_backward": [_P] * 6 + [_I64] + [_P] * 3 + [_P],
+    "gs_rasterize_display_l1": [_P, _P, _I32, _I64] + [_P] * 4
+    + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 4 + [_P],
+    "gs_l1_finish": [_P, _I32, _I64, _P, _P],
+    "gs_rasterize_l1_backward": [_P] * 5 + [_I32, _I64] + [_P] * 4
+    + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 4 + [_I32, _P],
     "gs_rasterize_display": [_P, _P, _I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F, _P, _P, _P],
     "gs_rasterize_display_backward": [_P] * 4 + [_I32, _I64] + [_P] * 4

@@ -1,0 +1,94 @@
+"""Fused training step: activations + render + L1 loss as one autograd node.
+
+The reference's training step (scripts/train.py:133-227) applies the
+activations in PyTorch (:135-143), calls render() (src/cuda/wrapper.py:223-294)
+and computes an L1 loss on the /255 image (:187-191); autograd then runs
+separate PyTorch kernels for each of those steps.  `render_l1` computes the
+same values with the library's kernels only:
+
+  forward   activate -> project_points -> SH (+0.5, clamp) -> binning ->
+            blend (image, display, per-tile L1 sums) -> loss
+  backward  blend backward seeded by the L1 gradient -> project_points
+            backward -> SH backward (adding into the means gradient) ->
+            activation backward
+
+Values equal the unfused sequence up to floating-point summation order (the
+loss sum and the gradient atomics); tests/test_gpu_fused.py checks both
+against the drop-in path and the CPU oracle.  Only the loss is differentiable;
+the display image, points_img and radii are returned for logging and
+densification (src/strategy.py:47-68 reads dL/d points_img: pass
+`grad2d_norm_accum`, an (N,) fp32 tensor, and the backward adds
+|dL/d points_img| per Gaussian to it).
+"""
+
+from __future__ import annotations
+
+import torch
+
+import cuda_rasterizer as _cr
+
+
+class RenderL1Function(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
+                world_to_camera, intrinsic, target, grad2d_norm_accum, width, height, near_plane,
+                far_plane, min_opacity, min_radius, max_radius, alpha_threshold,
+                transmittance_threshold, chi_squared_threshold):
+        scales, quats, opac = _cr.activate(log_scales, quats_raw, opacity_logits)
+        pts, depths, cov, conic, radii, mask = _cr.project_points(
+            means, scales, quats, opac, world_to_camera, intrinsic, near_plane, far_plane,
+            min_opacity, min_radius, max_radius, width, height)
+        colors = _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_coeffs_dc,
+                                                         sh_coeffs_rest, mask)
+        off, ids = _cr.compute_tile_intersection(pts, radii, depths, mask, width, height, 16)
+        image, display, loss = _cr.rasterize_display_l1(
+            off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
+            transmittance_threshold, chi_squared_threshold)
+        ctx.save_for_backward(means, quats_raw, sh_coeffs_dc, sh_coeffs_rest, world_to_camera,
+                              intrinsic, target, scales, quats, opac, pts, cov, conic, mask,
+                              colors, off, ids, image)
+        ctx.grad2d = grad2d_norm_accum
+        ctx.params = (width, height, alpha_threshold, transmittance_threshold,
+                      chi_squared_threshold)
+        ctx.mark_non_differentiable(display, pts, radii)
+        return loss.reshape(()), display, pts, radii
+
+    @staticmethod
+    def backward(ctx, grad_loss, grad_display, grad_pts, grad_radii):
+        (means, quats_raw, dc, rest, w2c, K, target, scales, quats, opac, pts, cov, conic, mask,
+         colors, off, ids, image) = ctx.saved_tensors
+        width, height, a_thr, t_thr, chi = ctx.params
+        if grad_loss is None:
+            return (None,) * 20
+        g_pts, g_conic, g_opac, g_col = _cr.rasterize_l1_backward(
+            target, grad_loss.reshape(1).to(torch.float32), off, ids, pts, conic, opac, colors,
+            width, height, image, a_thr, t_thr, chi)
+        if ctx.grad2d is not None:
+            ctx.grad2d.add_(g_pts.norm(dim=1))
+        g_means, g_scales, g_quats = _cr.project_points_backward(
+            g_pts, g_conic, means, scales, quats, opac, w2c, K, width, height, cov, mask)
+        _, g_dc, g_rest = _cr.evaluate_spherical_harmonics_render_backward(
+            g_col, w2c, means, dc, rest, mask, accumulate_means=g_means)
+        g_ls, g_qr, g_logit = _cr.activate_backward(g_scales, g_quats, g_opac, scales, quats_raw,
+                                                    opac)
+        return (g_means, g_ls, g_qr, g_logit, g_dc, g_rest) + (None,) * 14
+
+
+def render_l1(world_to_camera, intrinsic, width, height, means, log_scales, quats_raw,
+              opacity_logits, sh_coeffs_dc, sh_coeffs_rest, target, near_plane=0.01,
+              far_plane=100.0, min_opacity=1 / 255, min_radius=0.5, max_radius=128.0,
+              alpha_threshold=1e-4, transmittance_threshold=1e-4, chi_squared_threshold=9.21,
+              grad2d_norm_accum=None):
+    """loss = l1_loss(render(...activations of the raw parameters...)[0] / 255, target).
+
+    Parameters are the raw training leaves of scripts/train.py:135-143
+    (log-scales, un-normalised xyzw quaternions, opacity logits); SH colours use
+    max(c + 0.5, 0) (render's default).  Returns (loss, display[H,W,3] in
+    [0,255], points_img[N,2], radii[N,2]).
+    """
+    return RenderL1Function.apply(
+        means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
+        world_to_camera, intrinsic, target, grad2d_norm_accum, int(width), int(height),
+        float(near_plane), float(far_plane), float(min_opacity), float(min_radius),
+        float(max_radius), float(alpha_threshold), float(transmittance_threshold),
+        float(chi_squared_threshold))

@@ -2,10 +2,14 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
 
-One step = render() forward + L1 loss + backward through all six parameter
-groups (no optimizer step: BASELINE.md times "fwd+bwd"), on the headline
-configuration 3 (1M Gaussians, SH degree 3, 1920x1080, fp32) with synthetic
-inputs already resident in HBM.  Prints ONE JSON line.
+One step = activations of the raw parameters, render forward, L1 loss of the
+/255 image against a target, and backward through all six parameter groups
+(no optimizer step: the metric is "fwd+bwd"), on the headline configuration 3
+(1M Gaussians, SH degree 3, 1920x1080, fp32) with synthetic inputs already
+resident in HBM.  The timed path is the library's fused step
+(cuda_rasterizer.fused.render_l1); the same step written as the reference's
+training loop does it (PyTorch activations and l1_loss around the drop-in
+render()) is timed beside it ("drop_in").  Prints ONE JSON line.
 
 Scene generators for BASELINE configurations 1-5 live here too (tests import
 them).  Every tensor is drawn on the CPU with torch.Generator().manual_seed(seed)
@@ -167,7 +171,24 @@ def gpu_step(render, leaves: dict, cam: dict, target: torch.Tensor):
     return loss, image
 
 
-def run_gpu(scene: dict, steps: int, warmup: int) -> dict:
+def fused_step(leaves: dict, cam: dict, target: torch.Tensor):
+    """The same step through cuda_rasterizer.fused.render_l1 (activations, render and
+    L1 loss as one autograd node of library kernels)."""
+    from cuda_rasterizer.fused import render_l1
+
+    for t in leaves.values():
+        t.grad = None
+    loss, image, _, _ = render_l1(cam["w2c"], cam["K"], cam["width"], cam["height"],
+                                  leaves["means"], leaves["log_scales"], leaves["quats_raw"],
+                                  leaves["opacity_logits"], leaves["sh_dc"], leaves["sh_rest"],
+                                  target, near_plane=cam["near"])
+    loss.backward()
+    return loss, image
+
+
+def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused") -> dict:
+    """Times `steps` steps after `warmup`; path "fused" (fused_step) or "drop-in"
+    (gpu_step: PyTorch activations and loss around the drop-in render())."""
     from cuda_rasterizer import _lib
     from cuda_rasterizer.wrapper import render
 
@@ -177,8 +198,12 @@ def run_gpu(scene: dict, steps: int, warmup: int) -> dict:
     cam["w2c"] = cam["w2c"].to(dev)
     cam["K"] = cam["K"].to(dev)
     target = scene["target"].to(dev)
+    if path == "fused":
+        step = lambda: fused_step(leaves, cam, target)  # noqa: E731
+    else:
+        step = lambda: gpu_step(render, leaves, cam, target)  # noqa: E731
     for _ in range(warmup):
-        gpu_step(render, leaves, cam, target)
+        step()
     torch.cuda.synchronize()
 
     # timed region: wall clock with a synchronize on both sides, plus HIP events
@@ -188,7 +213,7 @@ def run_gpu(scene: dict, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        loss, image = gpu_step(render, leaves, cam, target)
+        loss, image = step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     _lib.timer.enabled = False
@@ -216,9 +241,11 @@ def run_gpu(scene: dict, steps: int, warmup: int) -> dict:
 # FP32 flops per evaluated (pixel, list entry) pair of the reference blend loop
 # (src/cuda/kernel.cu:954-982 forward; :1063-1106 backward), exp counted as one
 BLEND_FLOP_PER_PAIR = {"rasterize": 22.0, "rasterize_backward": 70.0, "rasterize_display": 22.0,
-                       "rasterize_display_backward": 70.0}
-HBM_STAGES = ("project_points", "evaluate_sh", "evaluate_sh_render", "bin_count", "bin_sort",
-              "evaluate_sh_backward", "evaluate_sh_render_backward", "project_points_backward")
+                       "rasterize_display_backward": 70.0, "rasterize_display_l1": 22.0,
+                       "rasterize_l1_backward": 70.0}
+HBM_STAGES = ("activate", "project_points", "evaluate_sh", "evaluate_sh_render", "bin_count",
+              "bin_sort", "evaluate_sh_backward", "evaluate_sh_render_backward",
+              "project_points_backward", "activate_backward")
 
 
 def sort_passes(n_tiles: int) -> int:
@@ -249,15 +276,25 @@ def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> floa
         return k * 40 + 12 * hw
     if stage == "rasterize_display":  # + the clamped x255 image
         return k * 40 + 24 * hw
+    if stage == "rasterize_display_l1":  # + the target read, per-tile loss sums
+        return k * 40 + 36 * hw
     if stage in ("rasterize_backward", "rasterize_display_backward"):
         return 12 * hw + k * 76 + 36 * n
+    if stage == "rasterize_l1_backward":  # image + target read instead of a gradient image
+        return 24 * hw + k * 76 + 36 * n
+    if stage == "activate":  # log-scales, quaternions, logits -> scales, unit quaternions, opacity
+        return n * (12 + 16 + 4) * 2
+    if stage == "activate_backward":  # 3 gradients + scales, quaternions, opacity -> 3 gradients
+        return n * (12 + 16 + 4) * 3
     return 0.0
 
 
 # kernel that implements each single-kernel entry point
 STAGE_KERNEL = {"rasterize": "blend_forward_kernel", "rasterize_display": "blend_forward_kernel",
-                "rasterize_backward": "blend_backward_kernel<false>",
-                "rasterize_display_backward": "blend_backward_kernel<true>",
+                "rasterize_display_l1": "blend_forward_kernel",
+                "rasterize_backward": "blend_backward_kernel<0>",
+                "rasterize_display_backward": "blend_backward_kernel<1>",
+                "rasterize_l1_backward": "blend_backward_kernel<2>",
                 "project_points": "project_points_kernel", "evaluate_sh": "sh_forward_kernel",
                 "evaluate_sh_render": "sh_forward_kernel",
                 "evaluate_sh_backward": "sh_backward_kernel",
@@ -413,6 +450,10 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=[1, 3, 4])
+    ap.add_argument("--path", choices=["fused", "drop-in"], default="fused",
+                    help="the timed step: fused render_l1 (default) or PyTorch glue around render()")
+    ap.add_argument("--no-drop-in", action="store_true",
+                    help="skip timing the drop-in path beside the fused one")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU blend work in the cpu_baseline sample")
@@ -432,8 +473,13 @@ def main(argv=None):
         return copy_calibration(args.copy_calibration)
 
     scene = CONFIGS[args.config]()
-    res = run_gpu(scene, args.steps, args.warmup)
+    res = run_gpu(scene, args.steps, args.warmup, args.path)
     rl = roofline(res, scene["name"])
+    drop_in = None
+    if args.path == "fused" and not args.no_drop_in:
+        d = run_gpu(scene, args.steps, args.warmup, "drop-in")
+        drop_in = {"ms_per_step": round(d["ms"], 3), "loss": d["loss"],
+                   "stages": roofline(d, scene["name"])["per_stage"]}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(scene, args.cpu_budget)
@@ -452,13 +498,15 @@ def main(argv=None):
         "data": "synthetic",
         "config": {"workload": f"{scene['name']}: {res['n']} Gaussians SH3 "
                                f"{res['width']}x{res['height']} fwd+bwd L1",
-                   "gaussians": res["n"], "visible": res["n_visible"], "keys": res["keys"],
-                   "resolution": [res["width"], res["height"]]},
+                   "path": args.path, "gaussians": res["n"], "visible": res["n_visible"],
+                   "keys": res["keys"], "resolution": [res["width"], res["height"]]},
         "gaussians_per_s": round(res["n"] / (res["ms"] * 1e-3), 1),
         "roofline": rl["roofline"],
         "hbm_stages": rl["hbm_stages"],
         "blend_pairs": {"visited": res["visited"], "composited": res["composited"]},
         "stages": rl["per_stage"],
+        "loss": res["loss"],
+        "drop_in": drop_in,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

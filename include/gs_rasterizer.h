@@ -185,7 +185,8 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
  *   with camera_pos = -R^T t taken from world_to_camera
  *   (src/cuda/wrapper.py:260-265); masked rows are 0.5.
  * gs_evaluate_sh_render_backward: its gradient (the clamp passes the gradient
- *   where raw + 0.5 >= 0, as torch.clamp_min does).
+ *   where raw + 0.5 >= 0, as torch.clamp_min does); accumulate_means != 0 adds
+ *   the means gradient to grad_means instead of overwriting it.
  * gs_rasterize_display: gs_rasterize that also writes
  *   display = clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294); tile_size 16.
  * gs_rasterize_display_backward: gs_rasterize_backward given the gradient of
@@ -197,8 +198,9 @@ int gs_evaluate_sh_render(const float *world_to_camera, const float *means, cons
                           hipStream_t stream);
 int gs_evaluate_sh_render_backward(const float *grad_colors, const float *world_to_camera,
                                    const float *means, const float *sh_dc, const float *sh_rest,
-                                   const uint8_t *mask, int64_t n, float *grad_means,
-                                   float *grad_sh_dc, float *grad_sh_rest, hipStream_t stream);
+                                   const uint8_t *mask, int64_t n, int32_t accumulate_means,
+                                   float *grad_means, float *grad_sh_dc, float *grad_sh_rest,
+                                   hipStream_t stream);
 int gs_rasterize_display(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
                          int32_t n_tiles, int64_t k, const float *points_image,
                          const float *cov_inv_image, const float *opacities, const float *colors,
@@ -216,6 +218,53 @@ int gs_rasterize_display_backward(const float *grad_display, const float *image,
                                   float chi_squared_threshold, float *grad_points_image,
                                   float *grad_cov_inv_image, float *grad_opacities,
                                   float *grad_colors, int32_t accumulate, hipStream_t stream);
+
+/* ----------------------------------------------- fused training step */
+
+/*
+ * The caller-side glue of a training step (scripts/train.py:135-143,187-191),
+ * fused: no counterpart in the reference extension.
+ *
+ * gs_activate: scales = exp(log_scales), quaternions = q / max(|q|, 1e-12),
+ *   opacities = sigmoid(logits) (N rows; quaternion rows 16-byte aligned).
+ * gs_activate_backward: maps gradients of those outputs (any may be NULL =
+ *   zero) to log_scales, raw quaternions and logits.
+ * gs_rasterize_display_l1: gs_rasterize_display that also writes, per tile,
+ *   the sum over its pixels of |display / 255 - target| (tile_loss, one float
+ *   per tile; n_tiles must cover the image; tile_size 16).
+ * gs_l1_finish: loss = sum(tile_loss) / count (count = H * W * 3), one float.
+ * gs_rasterize_l1_backward: gs_rasterize_backward seeded by
+ *   loss = mean(|clamp(image, 0, 1) * 255 / 255 - target|) with upstream
+ *   gradient *grad_loss (device float): the image gradient is computed per
+ *   pixel from image and target (image required; tile_size 16).
+ */
+int gs_activate(const float *log_scales, const float *quats_raw, const float *opacity_logits,
+                int64_t n, float *scales, float *quats, float *opacities, hipStream_t stream);
+int gs_activate_backward(const float *grad_scales, const float *grad_quats,
+                         const float *grad_opacities, const float *scales,
+                         const float *quats_raw, const float *opacities, int64_t n,
+                         float *grad_log_scales, float *grad_quats_raw,
+                         float *grad_opacity_logits, hipStream_t stream);
+int gs_rasterize_display_l1(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                            int32_t n_tiles, int64_t k, const float *points_image,
+                            const float *cov_inv_image, const float *opacities,
+                            const float *colors, int64_t n, int32_t width, int32_t height,
+                            int32_t tile_size, float alpha_threshold,
+                            float transmittance_threshold, float chi_squared_threshold,
+                            const float *target, float *image, float *display, float *tile_loss,
+                            hipStream_t stream);
+int gs_l1_finish(const float *tile_loss, int32_t n_tiles, int64_t count, float *loss,
+                 hipStream_t stream);
+int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const float *image,
+                             const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
+                             int32_t n_tiles, int64_t k, const float *points_image,
+                             const float *cov_inv_image, const float *opacities,
+                             const float *colors, int64_t n, int32_t width, int32_t height,
+                             int32_t tile_size, float alpha_threshold,
+                             float transmittance_threshold, float chi_squared_threshold,
+                             float *grad_points_image, float *grad_cov_inv_image,
+                             float *grad_opacities, float *grad_colors, int32_t accumulate,
+                             hipStream_t stream);
 
 /*
  * Measurement entry (no counterpart in the reference): the work of the

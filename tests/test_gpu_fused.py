@@ -1,0 +1,124 @@
+"""GPU parity of the fused training step (cuda_rasterizer.fused.render_l1) and
+its kernels: activations, L1 loss in the blend, L1-seeded blend backward.
+
+References: the drop-in path (PyTorch activations of scripts/train.py:135-143,
+render(), PyTorch l1_loss on the /255 image) on the GPU, and the CPU oracle.
+Tolerances: activations within 2 ulp-level relative error (device expf/sqrt vs
+PyTorch's); loss relative 1e-5 (summation order); image max abs error 1e-4 on
+the [0,1] scale; gradients relative L2 <= 1e-4 against the drop-in path (same
+kernels, different float summation order and activation rounding) and <= 1e-3
+against the oracle (north star).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import helpers
+import cuda_rasterizer as cr
+from cuda_rasterizer.fused import render_l1
+from cuda_rasterizer.wrapper import render
+from oracle import render as orender
+
+pytestmark = pytest.mark.gpu
+
+
+def _raw_leaves(p, dev):
+    return {k: v.clone().to(dev).requires_grad_(True) for k, v in p.items()}
+
+
+def test_activate_matches_torch(gpu):
+    g = torch.Generator().manual_seed(0)
+    n = 5000
+    ls = torch.randn(n, 3, generator=g) - 3.0
+    q = torch.randn(n, 4, generator=g)
+    q[7] = 0.0  # the clamp_min(1e-12) branch
+    q[8] = 1e-14
+    lo = torch.randn(n, generator=g) * 3.0
+    leaves = [t.to(gpu).requires_grad_(True) for t in (ls, q, lo)]
+    scales, quats, opac = helpers.activated(dict(log_scales=leaves[0], quats_raw=leaves[1],
+                                                 opacity_logits=leaves[2]))
+    s2, q2, o2 = cr.activate(*[t.detach() for t in leaves])
+    assert helpers.max_abs(s2 / scales.detach(), torch.ones_like(s2)) <= 1e-6
+    assert helpers.max_abs(q2, quats) <= 1e-6
+    assert helpers.max_abs(o2, opac) <= 1e-6
+    ups = [torch.randn(t.shape, generator=g).to(gpu) for t in (scales, quats, opac)]
+    torch.autograd.backward([scales, quats, opac], ups)
+    got = cr.activate_backward(*ups, s2, leaves[1].detach(), o2)
+    for a, t in zip(got, leaves):
+        assert helpers.rel_l2(a, t.grad) <= 1e-5
+    # absent gradients count as zero
+    g_ls, g_q, g_l = cr.activate_backward(None, None, ups[2], s2, leaves[1].detach(), o2)
+    assert float(g_ls.abs().max()) == 0.0 and float(g_q.abs().max()) == 0.0
+    assert helpers.rel_l2(g_l, leaves[2].grad) <= 1e-5
+
+
+@pytest.mark.parametrize("scene", ["orbit", "box"])
+def test_render_l1_matches_drop_in_path(gpu, scene):
+    if scene == "orbit":
+        p, cam, target = helpers.scene_orbit(20_000, 320, 240, 440.0, seed=21)
+    else:
+        p, cam, target = helpers.scene_box(8_000, 200, 130, 220.0, seed=22, log_scale=(-3.5, 0.6))
+    W, H = cam["width"], cam["height"]
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    # drop-in path
+    a = _raw_leaves(p, gpu)
+    scales, quats, opac = helpers.activated(a)
+    img, pts, _ = render(w2c, K, W, H, a["means"], scales, quats, opac, a["sh_dc"], a["sh_rest"])
+    pts.retain_grad()
+    loss_a = torch.nn.functional.l1_loss(img / 255.0, tgt)
+    loss_a.backward()
+    # fused path
+    b = _raw_leaves(p, gpu)
+    accum = torch.zeros(p["means"].shape[0], device=gpu)
+    loss_b, disp, pts_b, radii_b = render_l1(w2c, K, W, H, b["means"], b["log_scales"],
+                                             b["quats_raw"], b["opacity_logits"], b["sh_dc"],
+                                             b["sh_rest"], tgt, grad2d_norm_accum=accum)
+    loss_b.backward()
+    assert loss_b.shape == ()
+    assert abs(float(loss_b) - float(loss_a)) <= 1e-5 * float(loss_a)
+    assert helpers.max_abs(disp / 255.0, img.detach() / 255.0) <= 1e-4
+    for k in helpers.PARAMS:
+        assert helpers.rel_l2(b[k].grad, a[k].grad) <= 1e-4, k
+    assert helpers.rel_l2(accum, pts.grad.norm(dim=1)) <= 1e-4
+    assert torch.equal(pts_b, pts.detach()) or helpers.max_abs(pts_b, pts.detach()) <= 1e-4
+
+
+def test_render_l1_config1_matches_oracle(gpu):
+    """BASELINE config 1 through the fused path against the CPU oracle."""
+    import bench
+
+    scene = bench.config1()
+    p, cam, target = scene["params"], scene["camera"], scene["target"]
+    cam2 = dict(w2c=cam["w2c"], K=cam["K"], width=cam["width"], height=cam["height"])
+    _, loss_c, grads_c, _, _ = helpers.forward_backward(orender.render, p, cam2, target, "cpu")
+    b = _raw_leaves(p, gpu)
+    loss_b, disp, _, _ = render_l1(cam["w2c"].to(gpu), cam["K"].to(gpu), cam["width"],
+                                   cam["height"], b["means"], b["log_scales"], b["quats_raw"],
+                                   b["opacity_logits"], b["sh_dc"], b["sh_rest"], target.to(gpu))
+    loss_b.backward()
+    assert abs(float(loss_b) - float(loss_c)) <= 1e-5
+    for k in helpers.PARAMS:
+        if float(grads_c[k].norm()) == 0.0:
+            assert float(b[k].grad.norm()) == 0.0, k
+        else:
+            assert helpers.rel_l2(b[k].grad, grads_c[k]) <= 1e-3, k
+
+
+def test_render_l1_repeated_calls_are_stable(gpu):
+    """Two steps in a row on the same leaves give the same loss and gradients."""
+    p, cam, target = helpers.scene_orbit(3_000, 96, 80, 140.0, seed=23)
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    b = _raw_leaves(p, gpu)
+    out = []
+    for _ in range(2):
+        for t in b.values():
+            t.grad = None
+        loss, _, _, _ = render_l1(w2c, K, 96, 80, b["means"], b["log_scales"], b["quats_raw"],
+                                  b["opacity_logits"], b["sh_dc"], b["sh_rest"], tgt)
+        loss.backward()
+        out.append((float(loss), {k: t.grad.clone() for k, t in b.items()}))
+    assert out[0][0] == out[1][0]
+    for k in helpers.PARAMS:
+        assert helpers.rel_l2(out[1][1][k], out[0][1][k]) <= 1e-5, k
