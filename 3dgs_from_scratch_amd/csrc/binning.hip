@@ -42,7 +42,7 @@ constexpr int kTileItems = 4;   // the supertile sort (M keys)
 
 constexpr int kSuper = 8;                       // supertile edge, in tiles
 constexpr int kSuperLocal = kSuper * kSuper;    // tiles per supertile (one mask bit each)
-constexpr int kL2Threads = 256;                 // supertile-list positions per level-2 block
+constexpr int kL2Threads = 512;                 // supertile-list positions per level-2 block
 constexpr int kL2Waves = kL2Threads / kWave;
 
 constexpr int kScanThreads = 256;
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(256) void copy_u32_to_i32_kernel(int64_t n,
 // Level 1 leaves, for every supertile s, the ids of the Gaussians whose tile
 // rectangle meets s, in depth order (list positions super_off[s] ..
 // super_off[s + 1]).  Level 2 cuts each list into chunks of kL2Threads
-// positions (block b <-> supertile s, chunk b - chunk_start[s]); a lane holds
+// (512) positions (block b <-> supertile s, chunk b - chunk_start[s]); a lane holds
 // one Gaussian and the 64-bit mask of the supertile's tiles its rectangle
 // covers.  Per local tile j, one ballot gives the lanes (in list order) that
 // write an entry: l2_count_kernel counts them per block and per tile,

@@ -51,6 +51,7 @@ class RenderL1Function(torch.autograd.Function):
         ctx.params = (width, height, alpha_threshold, transmittance_threshold,
                       chi_squared_threshold)
         ctx.mark_non_differentiable(display, pts, radii)
+        ctx.set_materialize_grads(False)  # no zero gradients for the non-differentiable outputs
         return loss.reshape(()), display, pts, radii
 
     @staticmethod
