@@ -3,10 +3,11 @@
 // One wave64 per 16x16 tile.  Lane l owns the four pixels
 // (x0 + l%16, y0 + l/16 + 4s), s = 0..3, i.e. one pixel in each 16x4 strip of
 // the tile.  The tile's depth-sorted Gaussian list is walked in batches of 64
-// records staged in LDS (one record per lane); for each Gaussian the wave tests
-// (uniformly) which strips its chi-square ellipse reaches and evaluates only
-// those, and it stops once the transmittance of all 256 pixels fell below the
-// threshold.  Tiles are assigned to workgroups XCD by XCD (the dispatcher
+// Gaussians (one per lane); at staging each lane computes which strips the
+// Gaussian's chi-square / alpha ellipse reaches, and only Gaussians reaching
+// the tile are written to LDS (ballot compaction, list order kept) with that
+// strip mask.  The wave evaluates only those strips, and it stops once the
+// transmittance of all 256 pixels fell below the threshold.  Tiles are assigned to workgroups XCD by XCD (the dispatcher
 // places workgroup b on XCD b % 8) so that neighbouring tiles, which share
 // Gaussians, run on the same XCD and share its L2.
 //
@@ -23,7 +24,7 @@
 // issues one float atomic per (tile, Gaussian, field) (the reference issues one
 // per pixel: src/cuda/kernel.cu:1098-1106).
 
-#include "gs_common.h"
+#include "wave_ops.h"
 
 namespace gs {
 
@@ -121,22 +122,37 @@ __device__ __forceinline__ Record fetch_record(int32_t g, int64_t n,
     return r;
 }
 
-// Stages the lane's record into LDS slot `slot`.  An empty record stages a
-// Gaussian at infinity that every wave culls.
-__device__ __forceinline__ void stage_record(BatchLds &s, int slot, const Record &r, float chi,
-                                             float alpha_thr) {
-    if (r.id < 0) {
-        const float inf = __builtin_inff();
-        s.geo[slot] = make_float4(inf, inf, 0.0f, 0.0f);
-        s.aux[slot] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        s.col[slot] = make_float4(0.0f, 0.0f, 0.0f, __int_as_float(0));
-        return;
+// Bit s set for each 16x4 strip of the tile with origin (x0, y0) that the box
+// |x - u| <= ex, |y - v| <= ey reaches; 0 when it misses the tile.
+__device__ __forceinline__ uint32_t strip_mask(float u, float v, float ex, float ey, float x0,
+                                               float y0) {
+    if (u + ex < x0 || u - ex > x0 + (kTile - 1)) return 0u;
+    const float ylo = v - ey - y0, yhi = v + ey - y0;
+    if (yhi < 0.0f || ylo > (float)(kTile - 1)) return 0u;
+    const int s_lo = ylo <= 0.0f ? 0 : ((int)ylo >> 2);
+    const int s_hi = yhi >= (float)(kTile - 1) ? kStrips - 1 : ((int)yhi >> 2);
+    return ((2u << s_hi) - 1u) & ~((1u << s_lo) - 1u);
+}
+
+// Stages the lane's record into the next free LDS slot if its ellipse (with
+// the chi-square and alpha cut-offs) reaches the tile, keeping lane (= list)
+// order, with its strip mask in aux.z.  Returns the number of records staged.
+__device__ __forceinline__ int stage_records(BatchLds &s, const Record &r, float chi,
+                                             float alpha_thr, float x0, float y0) {
+    uint32_t m = 0u;
+    if (r.id >= 0) {
+        float ex, ey;
+        ellipse_extent(r.A, r.B, r.C, r.o, chi, alpha_thr, ex, ey);
+        m = strip_mask(r.u, r.v, ex, ey, x0, y0);
     }
-    float ex, ey;
-    ellipse_extent(r.A, r.B, r.C, r.o, chi, alpha_thr, ex, ey);
-    s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
-    s.aux[slot] = make_float4(r.C, r.o, ex, ey);
-    s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
+    const uint64_t keep = __ballot(m != 0u);
+    if (m != 0u) {
+        const int slot = __popcll(keep & lanemask_lt());
+        s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
+        s.aux[slot] = make_float4(r.C, r.o, __uint_as_float(m), 0.0f);
+        s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
+    }
+    return __popcll(keep);
 }
 
 // Software pipeline over a tile's list in batches of kBatch.  With kRecords,
@@ -162,18 +178,19 @@ struct BatchPipe {
         }
     }
 
-    // Stages the batch starting at b0 and fetches ahead.
-    __device__ __forceinline__ void advance(BatchLds &s, int32_t b0, TileSpan span,
-                                            const int32_t *__restrict__ ids, int64_t n,
-                                            const float *__restrict__ points,
-                                            const float *__restrict__ conics,
-                                            const float *__restrict__ opac,
-                                            const float *__restrict__ colors, float chi,
-                                            float alpha_thr) {
+    // Stages the batch starting at b0 (only records reaching the tile) and
+    // fetches ahead.  Returns the number of staged records.
+    __device__ __forceinline__ int advance(BatchLds &s, int32_t b0, TileSpan span,
+                                           const int32_t *__restrict__ ids, int64_t n,
+                                           const float *__restrict__ points,
+                                           const float *__restrict__ conics,
+                                           const float *__restrict__ opac,
+                                           const float *__restrict__ colors, float chi,
+                                           float alpha_thr, float x0, float y0) {
         const int32_t lane = (int32_t)threadIdx.x;
         if (!kRecords) rec = fetch_record(next_id, n, points, conics, opac, colors);
         __syncthreads();  // previous batch fully read before restaging
-        stage_record(s, threadIdx.x, rec, chi, alpha_thr);
+        const int cnt = stage_records(s, rec, chi, alpha_thr, x0, y0);
         __syncthreads();
         if (kRecords) {
             rec = fetch_record(next_id, n, points, conics, opac, colors);
@@ -181,21 +198,9 @@ struct BatchPipe {
         } else {
             next_id = fetch_id(b0 + kBatch + lane, span.end, ids);
         }
+        return cnt;
     }
 };
-
-// Strips [s_lo, s_hi] of the tile reached by the ellipse of record (geo, aux);
-// false when the ellipse misses the tile.  Wave-uniform.
-__device__ __forceinline__ bool strip_range(float4 geo, float4 aux, float x0, float y0, int &s_lo,
-                                            int &s_hi) {
-    if (geo.x + aux.z < x0 || geo.x - aux.z > x0 + (kTile - 1)) return false;
-    const float ylo = geo.y - aux.w - y0, yhi = geo.y + aux.w - y0;
-    if (yhi < 0.0f || ylo > (float)(kTile - 1)) return false;
-    s_lo = __builtin_amdgcn_readfirstlane(ylo <= 0.0f ? 0 : ((int)ylo >> 2));
-    s_hi = __builtin_amdgcn_readfirstlane(yhi >= (float)(kTile - 1) ? kStrips - 1
-                                                                     : ((int)yhi >> 2));
-    return true;
-}
 
 // Pixel geometry of one lane.
 struct LanePixels {
@@ -270,20 +275,19 @@ __device__ __forceinline__ void blend_accumulate(
     pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
         if (!any_active(T, T_thr)) break;
-        pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi, alpha_thr);
-        const int cnt = min(kBatch, span.end - b0);
+        const int cnt = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
+                                     alpha_thr, pix.x0, pix.y0);
         for (int j = 0; j < cnt; ++j) {
             const float4 geo = s.geo[j];
             const float4 aux = s.aux[j];
-            int s_lo, s_hi;
-            if (!strip_range(geo, aux, pix.x0, pix.y0, s_lo, s_hi)) continue;
+            const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
             const float4 col = s.col[j];
             const float du = pix.fx - geo.x;
             const float Adudu = (geo.z * du) * du;  // (A du) du, as in the oracle's A*du*du
             const float B2du = geo.w * du;
 #pragma unroll
             for (int q = 0; q < kStrips; ++q) {
-                if (q < s_lo || q > s_hi) continue;  // uniform
+                if (!((smask >> q) & 1u)) continue;  // uniform
                 const float dv = pix.fy[q] - geo.y;
                 const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
                 const bool ok = !(T[q] < T_thr) && (E < chi);
@@ -532,13 +536,12 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
         if (!any_active(T, T_thr)) break;
-        pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi, alpha_thr);
-        const int cnt = min(kBatch, span.end - b0);
+        const int cnt = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
+                                     alpha_thr, pix.x0, pix.y0);
         for (int j = 0; j < cnt; ++j) {
             const float4 geo = s.geo[j];
             const float4 aux = s.aux[j];
-            int s_lo, s_hi;
-            if (!strip_range(geo, aux, pix.x0, pix.y0, s_lo, s_hi)) continue;
+            const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
             const float4 col = s.col[j];
             const float du = pix.fx - geo.x;
             const float Adudu = (geo.z * du) * du;
@@ -547,7 +550,7 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
             uint64_t hit = 0;
 #pragma unroll
             for (int q = 0; q < kStrips; ++q) {
-                if (q < s_lo || q > s_hi) continue;  // uniform
+                if (!((smask >> q) & 1u)) continue;  // uniform
                 const float dv = pix.fy[q] - geo.y;
                 const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
                 const bool ok = !(T[q] < T_thr) && (E < chi);

@@ -253,11 +253,18 @@ def sort_passes(n_tiles: int) -> int:
     return math.ceil((32 + math.ceil(math.log2(max(n_tiles, 2)))) / 8)
 
 
+def sort_convention_bytes(n: int, k: int, n_tiles: int) -> float:
+    """Bytes the reference's binning algorithm moves (count + scan 33 B/G, emit
+    12 B/key, P 8-bit radix passes of 24 B/key over 64-bit keys, ranges 8 B/key +
+    4 B/tile).  Reported beside the timing as work done per second; it is not
+    traffic (this build sorts N depth keys and M supertile entries instead)."""
+    return n * 33 + k * 12 + 24 * k * sort_passes(n_tiles) + k * 8 + 4 * n_tiles
+
+
 def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> float:
     """Bytes one call of an entry point must move: every API tensor read once and
-    written once at full size; binning is charged the conventional 64-bit-key
-    pipeline (count + scan 33 B/G, emit 12 B/key, P 8-bit radix passes of
-    24 B/key, ranges 8 B/key + 4 B/tile)."""
+    written once at full size (compute_tile_intersection: points, radii, depths
+    and mask in; the tile offsets and the K ids out)."""
     if stage == "project_points":  # means, scales, quats, opac -> uv, z, cov, conic, radii, mask
         return n * (12 + 12 + 16 + 4) + n * (8 + 4 + 12 + 12 + 8 + 1)
     if stage in ("evaluate_sh", "evaluate_sh_render"):  # means, dc, rest, mask -> colours
@@ -269,9 +276,9 @@ def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> floa
     if stage == "project_points_backward":  # grads uv/conic, means, scales, quats, cov, mask -> 3 grads
         return n * (8 + 12 + 12 + 12 + 16 + 12 + 1) + n * (12 + 12 + 16)
     if stage == "bin_count":
-        return n * (21 + 4 + 8)
+        return n * 21
     if stage == "bin_sort":
-        return k * 12 + 24 * k * sort_passes(n_tiles) + k * 8 + 4 * n_tiles
+        return k * 4 + 4 * n_tiles
     if stage == "rasterize":
         return k * 40 + 12 * hw
     if stage == "rasterize_display":  # + the clamped x255 image
@@ -355,7 +362,11 @@ def roofline(res: dict, workload: str) -> dict:
     ht = sum(res["stages"][s][1] for s in HBM_STAGES if s in res["stages"]) * 1e-3
     hbm = dict(achieved=round(hb / ht / 1e9, 1) if ht else None, peak=HBM_PEAK_GBS, unit="GB/s",
                frac=round(hb / ht / 1e9 / HBM_PEAK_GBS, 4) if ht else None, bytes=int(hb),
-               ms=round(ht * 1e3, 4), sort_passes_charged=sort_passes(nt))
+               ms=round(ht * 1e3, 4))
+    # the reference binning algorithm's bytes per second of this build's binning
+    bt = sum(res["stages"][s][1] for s in ("bin_count", "bin_sort") if s in res["stages"]) * 1e-3
+    if bt:
+        hbm["binning_reference_algorithm_gbs"] = round(sort_convention_bytes(n, k, nt) / bt / 1e9, 1)
     return dict(dominant=dominant, roofline=main, hbm_stages=hbm, per_stage=per_stage)
 
 
