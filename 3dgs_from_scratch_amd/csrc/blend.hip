@@ -59,13 +59,19 @@ __device__ __forceinline__ int tile_of_block(int b, int n_tiles) {
     return x * base + min(x, rem) + i;
 }
 
+// Exponent cut-off of a Gaussian with opacity o: E < chi and o exp(-E/2) >= alpha_thr.
+__device__ __forceinline__ float effective_chi(float o, float chi, float alpha_thr) {
+    float chi_eff = chi;
+    if (alpha_thr > 0.0f && o > 0.0f) chi_eff = fminf(chi_eff, 2.0f * logf(o / alpha_thr));
+    return chi_eff;
+}
+
 // Conservative half-extents of the ellipse {E < chi_eff} of conic (A, B, C),
 // where chi_eff also accounts for alpha >= alpha_thr.  Infinite when the conic
 // is not positive definite (no culling).
 __device__ __forceinline__ void ellipse_extent(float A, float B, float C, float o, float chi,
                                                float alpha_thr, float &ex, float &ey) {
-    float chi_eff = chi;
-    if (alpha_thr > 0.0f && o > 0.0f) chi_eff = fminf(chi_eff, 2.0f * logf(o / alpha_thr));
+    const float chi_eff = effective_chi(o, chi, alpha_thr);
     const float det = A * C - B * B;
     if (det > 0.0f && A > 0.0f && C > 0.0f && isfinite(chi_eff)) {
         const float ce = fmaxf(chi_eff, 0.0f);
@@ -134,6 +140,45 @@ __device__ __forceinline__ uint32_t strip_mask(float u, float v, float ex, float
     return ((2u << s_hi) - 1u) & ~((1u << s_lo) - 1u);
 }
 
+// Minimum of E(dx, dy) = A dx^2 + 2B dx dy + C dy^2 (positive definite) over
+// the rectangle dx in [ax, bx], dy in [ay, by]: 0 if it contains the origin,
+// else the least of the four edge minima (on an edge the quadratic in the free
+// coordinate is minimised at its vertex, clamped to the edge).
+__device__ __forceinline__ float rect_min_exponent(float A, float B, float C, float ax, float bx,
+                                                   float ay, float by) {
+    if (ax <= 0.0f && bx >= 0.0f && ay <= 0.0f && by >= 0.0f) return 0.0f;
+    auto edge_x = [&](float dx) {  // dx fixed, dy free in [ay, by]
+        const float dy = fminf(fmaxf(-B * dx / C, ay), by);
+        return (A * dx * dx + 2.0f * B * dx * dy) + C * dy * dy;
+    };
+    auto edge_y = [&](float dy) {  // dy fixed, dx free in [ax, bx]
+        const float dx = fminf(fmaxf(-B * dy / A, ax), bx);
+        return (A * dx * dx + 2.0f * B * dx * dy) + C * dy * dy;
+    };
+    return fminf(fminf(edge_x(ax), edge_x(bx)), fminf(edge_y(ay), edge_y(by)));
+}
+
+// strip_mask refined per strip by the exact ellipse: a strip stays only if the
+// minimum of the exponent over its pixel rectangle is below the cut-off
+// (chi_eff, with a relative and absolute margin so rounding never drops a
+// contributing pixel).  A non-positive-definite conic keeps the box mask.
+__device__ __forceinline__ uint32_t exact_strip_mask(uint32_t box, float u, float v, float A,
+                                                     float B, float C, float chi_eff, float x0,
+                                                     float y0) {
+    if (box == 0u || !(A > 0.0f && C > 0.0f && A * C - B * B > 0.0f) || !(chi_eff < 1e30f))
+        return box;
+    const float cut = chi_eff * 1.02f + 0.02f;
+    const float ax = x0 - u, bx = x0 + (float)(kTile - 1) - u;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        if (!((box >> q) & 1u)) continue;
+        const float ay = y0 + (float)(4 * q) - v, by = ay + 3.0f;
+        if (rect_min_exponent(A, B, C, ax, bx, ay, by) < cut) m |= 1u << q;
+    }
+    return m;
+}
+
 // Stages the lane's record into the next free LDS slot if its ellipse (with
 // the chi-square and alpha cut-offs) reaches the tile, keeping lane (= list)
 // order, with its strip mask in aux.z.  Returns the number of records staged.
@@ -143,7 +188,8 @@ __device__ __forceinline__ int stage_records(BatchLds &s, const Record &r, float
     if (r.id >= 0) {
         float ex, ey;
         ellipse_extent(r.A, r.B, r.C, r.o, chi, alpha_thr, ex, ey);
-        m = strip_mask(r.u, r.v, ex, ey, x0, y0);
+        m = exact_strip_mask(strip_mask(r.u, r.v, ex, ey, x0, y0), r.u, r.v, r.A, r.B, r.C,
+                             effective_chi(r.o, chi, alpha_thr), x0, y0);
     }
     const uint64_t keep = __ballot(m != 0u);
     if (m != 0u) {
