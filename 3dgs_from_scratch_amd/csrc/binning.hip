@@ -119,6 +119,11 @@ size_t scan_workspace_bytes(int64_t n) {
 template <typename T>
 int scan_exclusive(const T *in, T *out, int64_t n, T *total, void *ws, hipStream_t stream) {
     if (n <= 0) return total ? zero_bytes(total, sizeof(T), stream) : GS_OK;
+    if (n > kScanTile && n <= 1024 * kScanItems) {  // one 1024-thread workgroup
+        hipLaunchKernelGGL((scan_apply_kernel<T, 1024, kScanItems>), dim3(1), dim3(1024), 0,
+                           stream, in, out, n, (const T *)nullptr, total);
+        return launch_status();
+    }
     const int64_t nb = (n + kScanTile - 1) / kScanTile;
     if (nb == 1) {
         hipLaunchKernelGGL((scan_apply_kernel<T, kScanThreads, kScanItems>), dim3(1),
@@ -560,27 +565,34 @@ __device__ __forceinline__ int tile_of_local(const L2Args &a, int s, int j) {
     return (tx < a.tiles_x && ty < a.tiles_y) ? ty * a.tiles_x + tx : -1;
 }
 
+struct L2Block {
+    int s;
+    uint32_t b;
+    int32_t g;
+    uint64_t mask;
+    int lx0, lx1, ly0, ly1;  // the mask as a rectangle of local tiles (empty: lx0 > lx1)
+};
+
 // Bit j (= ly * kSuper + lx) set for every tile of supertile s that Gaussian
-// g's tile rectangle covers.
-__device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int s) {
+// g's tile rectangle covers; the covered local rectangle goes to x.
+__device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int s, L2Block &x) {
+    x.lx0 = x.ly0 = 1;
+    x.lx1 = x.ly1 = 0;
     if (g < 0 || (int64_t)g >= a.n) return 0;
     const TileRect r = unpack_rect(a.rects[g]);  // Gaussians in the lists have tiles
     const int ox = (s % a.super_x) * kSuper, oy = (s / a.super_x) * kSuper;
     const int x0 = max(r.tx0 - ox, 0), x1 = min(r.tx1 - ox, kSuper - 1);
     const int y0 = max(r.ty0 - oy, 0), y1 = min(r.ty1 - oy, kSuper - 1);
     if (x0 > x1 || y0 > y1) return 0;
+    x.lx0 = x0;
+    x.lx1 = x1;
+    x.ly0 = y0;
+    x.ly1 = y1;
     const uint64_t row = ((1ull << (x1 - x0 + 1)) - 1ull) << x0;
     uint64_t m = 0;
     for (int y = y0; y <= y1; ++y) m |= row << (y * kSuper);
     return m;
 }
-
-struct L2Block {
-    int s;
-    uint32_t b;
-    int32_t g;
-    uint64_t mask;
-};
 
 // Block -> supertile, this lane's Gaussian and mask.  Returns false (uniformly)
 // for the blocks past the last chunk (the grid is sized by an upper bound).
@@ -595,21 +607,35 @@ __device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x) {
     x.mask = 0;
     if (e < end) {
         x.g = a.super_ids[e];
-        x.mask = local_mask(a, x.g, x.s);
+        x.mask = local_mask(a, x.g, x.s, x);
+    } else {
+        x.lx0 = x.ly0 = 1;
+        x.lx1 = x.ly1 = 0;
     }
     return true;
 }
 
-// Per local tile j, the number of lanes of this wave whose mask has bit j, in lane j.
-__device__ __forceinline__ uint32_t wave_local_counts(uint64_t mask) {
+// Per local tile j = (ly, lx), the number of lanes of this wave whose rectangle
+// covers it, returned in lane j: the lanes covering row ly and those covering
+// column lx are one ballot each (kSuper + kSuper ballots), and lane j counts
+// their intersection.  `rc` is this wave's 2 * kSuper words of LDS.
+__device__ __forceinline__ uint32_t wave_local_counts(const L2Block &x, uint64_t *rc) {
     const int lane = threadIdx.x % kWave;
-    uint32_t mine = 0;
-#pragma unroll 8
-    for (int j = 0; j < kSuperLocal; ++j) {
-        const uint32_t c = (uint32_t)__popcll(__ballot((mask >> j) & 1ull));
-        mine = lane == j ? c : mine;
+    uint64_t mine_row = 0, mine_col = 0;
+#pragma unroll
+    for (int q = 0; q < kSuper; ++q) {
+        const uint64_t r = __ballot(x.ly0 <= q && q <= x.ly1);
+        const uint64_t c = __ballot(x.lx0 <= q && q <= x.lx1);
+        mine_row = lane == q ? r : mine_row;
+        mine_col = lane == q ? c : mine_col;
     }
-    return mine;
+    if (lane < kSuper) {
+        rc[lane] = mine_row;
+        rc[kSuper + lane] = mine_col;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    return (uint32_t)__popcll(rc[lane / kSuper] & rc[kSuper + lane % kSuper]);
 }
 
 // Table entry of (level-2 block b, wave w, local tile j).
@@ -623,10 +649,11 @@ __global__ __launch_bounds__(kL2Threads) void l2_count_kernel(L2Args a,
                                                               uint32_t *__restrict__ table,
                                                               uint32_t *__restrict__ counts) {
     __shared__ uint32_t wave_cnt[kL2Waves][kSuperLocal];
+    __shared__ uint64_t rowcol[kL2Waves][2 * kSuper];
     L2Block x;
     if (!l2_block(a, x)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t mine = wave_local_counts(x.mask);
+    const uint32_t mine = wave_local_counts(x, rowcol[wave]);
     wave_cnt[wave][lane] = mine;
     table[l2_slot(x.b, wave, lane)] = mine;
     __syncthreads();
