@@ -50,6 +50,26 @@ SIGNATURES = {
     + [_I32, _P],
 }
 
+class GsAdamTensor(ctypes.Structure):
+    """include/gs_rasterizer.h GsAdamTensor."""
+
+    _fields_ = [("param", _P), ("grad", _P), ("exp_avg", _P), ("exp_avg_sq", _P),
+                ("count", _I64), ("step_size", _F), ("bias_correction2_sqrt", _F)]
+
+
+class GsGatherTensor(ctypes.Structure):
+    """include/gs_rasterizer.h GsGatherTensor."""
+
+    _fields_ = [("src", _P), ("dst", _P), ("delta", _P), ("width", _I32), ("zero_fresh", _I32)]
+
+
+SIGNATURES.update({
+    "gs_adam_step": [ctypes.POINTER(GsAdamTensor), _I32, ctypes.c_double, ctypes.c_double,
+                     ctypes.c_double, _P],
+    "gs_accumulate_grad2d": [_P, _P, _I64, _I32, _I32, _P, _P, _P],
+    "gs_gather_rows": [_I64, _P, _P, ctypes.POINTER(GsGatherTensor), _I32, _P],
+})
+
 _lib = None
 
 

@@ -266,6 +266,53 @@ int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const 
                              float *grad_opacities, float *grad_colors, int32_t accumulate,
                              hipStream_t stream);
 
+/* ------------------------------------------------------------ training loop */
+
+/*
+ * Kernels for the optimizer and densification steps of the training loop
+ * (scripts/train.py:17-44,211-222; src/strategy.py:47-229).  No counterpart
+ * in the reference extension (it leaves these to PyTorch).
+ *
+ * gs_adam_step: one launch updates every tensor of the list (torch.optim.Adam
+ *   without weight decay / amsgrad): m = b1 m + (1-b1) g, v = b2 v + (1-b2) g^2,
+ *   p -= step_size * m / (sqrt(v) / bias_correction2_sqrt + eps), with
+ *   step_size = lr / (1 - b1^t) and bias_correction2_sqrt = sqrt(1 - b2^t)
+ *   given per tensor.  grad may be NULL (a zero gradient).  The betas and eps
+ *   are doubles, as the Python scalars of torch.optim.Adam are: 1 - beta is
+ *   formed in double and rounded once to float, as PyTorch does.
+ * gs_accumulate_grad2d: src/strategy.py:47-68 -- for Gaussians whose two radii
+ *   are > 0, grads += |(du * W/2, dv * H/2)| and count += 1.
+ * gs_gather_rows: dst row r = src row src_rows[r] (+ delta row r when delta is
+ *   set) for every tensor of the list, or zeros where fresh_rows[r] != 0 and
+ *   the tensor has zero_fresh (optimizer state of new Gaussians).  Rebuilds
+ *   parameters and optimizer state after prune / clone / split in one launch.
+ */
+typedef struct {
+    float *param;
+    const float *grad;
+    float *exp_avg;
+    float *exp_avg_sq;
+    int64_t count;
+    float step_size;
+    float bias_correction2_sqrt;
+} GsAdamTensor;
+
+typedef struct {
+    const float *src;
+    float *dst;
+    const float *delta;
+    int32_t width;
+    int32_t zero_fresh;
+} GsGatherTensor;
+
+int gs_adam_step(const GsAdamTensor *tensors, int32_t n_tensors, double beta1, double beta2,
+                 double eps, hipStream_t stream);
+int gs_accumulate_grad2d(const float *grad_points_image, const float *radii, int64_t n,
+                         int32_t width, int32_t height, float *grads, float *count,
+                         hipStream_t stream);
+int gs_gather_rows(int64_t n_out, const int32_t *src_rows, const uint8_t *fresh_rows,
+                   const GsGatherTensor *tensors, int32_t n_tensors, hipStream_t stream);
+
 /*
  * Measurement entry (no counterpart in the reference): the work of the
  * reference blend loop (src/cuda/kernel.cu:954-982) for the same inputs as

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 4
+    assert lib.gs_abi_version() == 5
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -97,6 +97,17 @@ def test_invalid_arguments_rejected_on_host(lib):
                            null, null, null) == -1  # more supertile entries than keys
     sz = ctypes.c_size_t(0)
     assert lib.gs_bin_count(null, null, null, null, 10, 64, 64, 16, null, 0, null, null) == -1
+    # training-loop entries: bad hyper-parameters, missing buffers, bad widths
+    t = _lib.GsAdamTensor(None, None, None, None, 10, 0.1, 1.0)
+    assert lib.gs_adam_step(ctypes.byref(t), 1, 0.9, 0.999, 1e-15, null) == -1  # null param
+    assert lib.gs_adam_step(None, 0, 1.0, 0.999, 1e-15, null) == -1  # beta1 = 1
+    assert lib.gs_adam_step(None, 0, 0.9, float("nan"), 1e-15, null) == -1
+    assert lib.gs_adam_step(None, 0, 0.9, 0.999, 1e-15, null) == 0  # empty list
+    assert lib.gs_accumulate_grad2d(null, null, 10, 0, 64, null, null, null) == -1
+    assert lib.gs_accumulate_grad2d(null, null, 10, 64, 64, null, null, null) == -1
+    g = _lib.GsGatherTensor(None, None, None, 0, 0)
+    assert lib.gs_gather_rows(10, None, None, ctypes.byref(g), 1, null) == -1
+    assert lib.gs_gather_rows(-1, None, None, None, 0, null) == -1
 
 
 def test_python_layer_refuses_cpu_tensors():

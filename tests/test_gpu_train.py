@@ -1,0 +1,148 @@
+"""GPU parity of the training-loop kernels (cuda_rasterizer.train) against the
+CPU oracle (oracle/train.py).
+
+FusedAdam: parameters and moments after several steps, relative error <= 1e-5
+(device sqrt / division vs PyTorch CPU rounding).  Densifier.update: bit-level
+agreement of the accumulated gradient norms up to float rounding (rel 1e-6)
+and exact counts.  Densifier.refine / clone_top_and_prune: every rebuilt
+parameter and moment equals the oracle's row map applied with PyTorch
+indexing (bit-exact: pure copies), split offsets checked separately.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import helpers
+from cuda_rasterizer.train import DEFAULT_LR, PARAM_ORDER, Densifier, FusedAdam
+from oracle import train as otrain
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {"means": (3,), "log_scales": (3,), "quats_raw": (4,), "opacity_logits": (),
+          "sh_dc": (3,), "sh_rest": (15, 3)}
+
+
+def _params(n, gen, dev, logits=None, log_scales=None):
+    p = {k: torch.randn((n,) + s, generator=gen) for k, s in SHAPES.items()}
+    if logits is not None:
+        p["opacity_logits"] = logits
+    if log_scales is not None:
+        p["log_scales"] = log_scales
+    return {k: v.to(dev).requires_grad_(True) for k, v in p.items()}
+
+
+def test_fused_adam_matches_oracle(gpu):
+    g = torch.Generator().manual_seed(1)
+    params = _params(5000, g, gpu)
+    ref = {k: v.detach().cpu().clone() for k, v in params.items()}
+    m = {k: torch.zeros_like(v) for k, v in ref.items()}
+    v2 = {k: torch.zeros_like(v) for k, v in ref.items()}
+    opt = FusedAdam(params, means_decay_steps=1000)
+    lr = {k: DEFAULT_LR[k] for k in params}
+    for t in range(1, 6):
+        grads = {k: torch.randn(v.shape, generator=g) * 10.0 ** (-t) for k, v in ref.items()}
+        for k, p in params.items():
+            p.grad = grads[k].to(gpu)
+        opt.step()
+        for k in ref:
+            ref[k], m[k], v2[k] = otrain.adam_step(ref[k], grads[k], m[k], v2[k], t, lr[k], 0.9,
+                                                   0.999, 1e-15)
+        lr["means"] *= 0.01 ** (1 / 1000)
+    for k in PARAM_ORDER:
+        assert helpers.rel_l2(params[k], ref[k]) <= 1e-6, k
+        assert helpers.rel_l2(opt.exp_avg[k], m[k]) <= 1e-5, k
+        assert helpers.rel_l2(opt.exp_avg_sq[k], v2[k]) <= 1e-5, k
+
+
+def test_accumulate_grad2d_matches_oracle(gpu):
+    g = torch.Generator().manual_seed(2)
+    n = 10_000
+    gp = torch.randn(n, 2, generator=g) * 1e-3
+    radii = torch.rand(n, 2, generator=g) * 10.0
+    radii[::7, 0] = 0.0
+    radii[::11, 1] = 0.0
+    d = Densifier(n, gpu)
+    grads, count = torch.zeros(n), torch.zeros(n)
+    for _ in range(3):
+        d.update(gp.to(gpu), radii.to(gpu), 640, 480)
+        grads, count = otrain.accumulate_grad2d(grads, count, gp, radii, 640, 480)
+    assert helpers.rel_l2(d.grads, grads) <= 1e-6
+    assert torch.equal(d.count.cpu(), count)
+
+
+def _opt_with_state(params, gen, dev):
+    opt = FusedAdam(params)
+    for k in params:
+        opt.exp_avg[k] = torch.randn(params[k].shape, generator=gen).to(dev)
+        opt.exp_avg_sq[k] = torch.rand(params[k].shape, generator=gen).to(dev)
+    return opt
+
+
+def _check_rebuild(params, before, opt, st_before, src, fresh, skip_rows=None, skip_keys=()):
+    rows = torch.arange(len(src))
+    keep_rows = rows if skip_rows is None else rows[~skip_rows]
+    for k in PARAM_ORDER:
+        want = before[k][src]
+        got = params[k].detach().cpu()
+        assert got.shape == want.shape, k
+        if k in skip_keys:
+            assert torch.equal(got[keep_rows], want[keep_rows]), k
+        else:
+            assert torch.equal(got, want), k
+        for store, name in ((opt.exp_avg, "m"), (opt.exp_avg_sq, "v")):
+            w = st_before[name][k][src].clone()
+            w[fresh] = 0.0
+            assert torch.equal(store[k].cpu(), w), (k, name)
+        assert params[k].requires_grad and params[k].is_leaf
+
+
+def test_refine_matches_oracle_row_map(gpu):
+    g = torch.Generator().manual_seed(3)
+    n = 4000
+    logits = torch.randn(n, generator=g) * 3.0            # some below logit(0.005)
+    log_scales = torch.randn(n, 3, generator=g) * 0.8 - 4.5  # mix of small and large
+    params = _params(n, g, gpu, logits=logits, log_scales=log_scales)
+    opt = _opt_with_state(params, g, gpu)
+    before = {k: v.detach().cpu().clone() for k, v in params.items()}
+    st_before = {"m": {k: v.cpu().clone() for k, v in opt.exp_avg.items()},
+                 "v": {k: v.cpu().clone() for k, v in opt.exp_avg_sq.items()}}
+    d = Densifier(n, gpu)
+    d.grads = (torch.rand(n, generator=g) * 4e-4).to(gpu)
+    d.count = torch.ones(n).to(gpu)
+    src, fresh, n_split, split_src = otrain.refine_rows(logits, log_scales, d.grads.cpu(),
+                                                        d.count.cpu(), step=600)
+    assert n_split > 0 and bool(fresh.any()) and len(src) != n
+    n_pruned, n_cloned, n_split2 = d.refine(params, opt, step=600,
+                                            generator=torch.Generator(device=gpu).manual_seed(0))
+    assert n_split2 == n_split
+    split_rows = torch.zeros(len(src), dtype=torch.bool)
+    split_rows[len(src) - 2 * n_split:] = True
+    _check_rebuild(params, before, opt, st_before, src, fresh, skip_rows=split_rows,
+                   skip_keys=("means", "log_scales"))
+    # split copies: log-scale = log(scale / 1.6); means offset by samples of norm ~ scale
+    got_ls = params["log_scales"].detach().cpu()[split_rows]
+    want_ls = torch.log(torch.exp(before["log_scales"][split_src]) / 1.6).repeat(2, 1)
+    assert torch.allclose(got_ls, want_ls, rtol=0, atol=1e-5)
+    off = params["means"].detach().cpu()[split_rows] - before["means"][split_src].repeat(2, 1)
+    scale = torch.exp(before["log_scales"][split_src]).max(dim=1).values.repeat(2)
+    assert bool((off.norm(dim=1) <= 6.0 * scale * 3 ** 0.5).all())
+    assert float(d.grads.abs().max()) == 0.0 and d.grads.shape[0] == len(src)
+
+
+def test_clone_top_and_prune_matches_oracle(gpu):
+    g = torch.Generator().manual_seed(4)
+    n = 3000
+    logits = torch.randn(n, generator=g) * 3.0
+    params = _params(n, g, gpu, logits=logits)
+    opt = _opt_with_state(params, g, gpu)
+    before = {k: v.detach().cpu().clone() for k, v in params.items()}
+    st_before = {"m": {k: v.cpu().clone() for k, v in opt.exp_avg.items()},
+                 "v": {k: v.cpu().clone() for k, v in opt.exp_avg_sq.items()}}
+    d = Densifier(n, gpu)
+    d.grads = torch.randperm(n, generator=g).float().to(gpu)  # distinct: top-k is well defined
+    src, fresh = otrain.clone_top_rows(logits, d.grads.cpu(), fraction=0.05)
+    n_pruned, n_top = d.clone_top_and_prune(params, opt, fraction=0.05, jitter=0.0)
+    assert n_top == int(fresh.sum()) and n_pruned == int((torch.sigmoid(logits) < 0.005).sum())
+    _check_rebuild(params, before, opt, st_before, src, fresh)
