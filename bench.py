@@ -9,7 +9,10 @@ One step = activations of the raw parameters, render forward, L1 loss of the
 resident in HBM.  The timed path is the library's fused step
 (cuda_rasterizer.fused.render_l1); the same step written as the reference's
 training loop does it (PyTorch activations and l1_loss around the drop-in
-render()) is timed beside it ("drop_in").  Prints ONE JSON line.
+render()) is timed beside it ("drop_in").  The configuration-5 training
+stress run (2000 steps of render + L1 + backward + Adam with clone / prune
+every 100 steps, through the library and through the reference's loop) is
+reported in the same line as "train_stress".  Prints ONE JSON line.
 
 Scene generators for BASELINE configurations 1-5 live here too (tests import
 them).  Every tensor is drawn on the CPU with torch.Generator().manual_seed(seed)
@@ -144,7 +147,31 @@ def config4(seed: int = 0) -> dict:
     return config3(n=3_000_000, seed=seed, big_fraction=0.05)
 
 
-CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4}
+def config5(seed: int = 0, n: int = 100_000 * 2, steps: int = 2000, n_targets: int = 16) -> dict:
+    """Training-loop stress run: 200k Gaussians with configuration-2 distributions,
+    1280x720 with fx=fy=1000, one orbit camera per step (distance 4, azimuth
+    U[0,2pi), elevation U[-pi/3,pi/3]) and a bank of 16 fixed random targets
+    used round-robin (step % 16)."""
+    g = torch.Generator().manual_seed(seed)
+    W, H = 1280, 720
+    d = torch.randn(n, 3, generator=g)
+    d = d / d.norm(dim=1, keepdim=True)
+    means = d * 1.5 * torch.rand(n, 1, generator=g) ** (1 / 3)
+    log_scales = torch.randn(n, 3, generator=g) * 0.6 - 4.5
+    quats = torch.randn(n, 4, generator=g)
+    logits = torch.randn(n, generator=g) * 1.5
+    dc, rest = _sh(g, n, 3)
+    az = torch.rand(steps, generator=g) * 2 * math.pi
+    el = (torch.rand(steps, generator=g) * 2 - 1) * math.pi / 3
+    w2c = torch.stack([look_at(float(a), float(e), 4.0) for a, e in zip(az, el)])
+    targets = torch.rand(n_targets, H, W, 3, generator=g)
+    cam = dict(w2c=w2c[0], K=_intrinsic(1000.0, W, H), width=W, height=H, near=0.01)
+    return dict(params=dict(means=means, log_scales=log_scales, quats_raw=quats,
+                            opacity_logits=logits, sh_dc=dc, sh_rest=rest),
+                w2c_per_step=w2c, targets=targets, camera=cam, target=targets[0], name="config5")
+
+
+CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
 
 
 # --------------------------------------------------------------- GPU leg
@@ -234,6 +261,127 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused") -> dict:
                 n=scene["params"]["means"].shape[0], n_visible=int(mask.sum()), keys=int(ids.numel()),
                 n_tiles=int(off.numel()), visited=visited, composited=composited,
                 loss=float(loss), width=cam["width"], height=cam["height"])
+
+
+# ------------------------------------------------- configuration 5 (training)
+
+def _torch_clone_top_and_prune(leaves: dict, optims: dict, grads: torch.Tensor, fraction: float,
+                               jitter: float, prune_opacity: float = 0.005):
+    """The configuration-5 rule written the way src/strategy.py:71-229 rebuilds
+    parameters and Adam state (index / cat per tensor, state moved to the new leaf)."""
+    opac = torch.sigmoid(leaves["opacity_logits"])
+    keep = torch.where(~(opac < prune_opacity))[0]
+    n_top = int(round(fraction * grads.shape[0]))
+    top = torch.topk(grads, n_top).indices
+    for name, p in list(leaves.items()):
+        extra = p[top]
+        if name == "means":
+            extra = extra + torch.randn_like(extra) * jitter
+        new = torch.cat([p[keep], extra]).detach().requires_grad_(True)
+        opt = optims[name]
+        state = opt.state.pop(p)
+        for key in ("exp_avg", "exp_avg_sq"):
+            s = state[key]
+            state[key] = torch.cat([s[keep], torch.zeros((n_top,) + s.shape[1:], device=s.device)])
+        opt.param_groups[0]["params"] = [new]
+        opt.state[new] = state
+        leaves[name] = new
+    return int(opac.numel() - keep.numel()), n_top
+
+
+def run_train(scene: dict, path: str = "fused", steps: int | None = None, every: int = 100,
+              fraction: float = 0.05, jitter: float = 0.01) -> dict:
+    """Configuration 5: `steps` training steps (render + L1 + backward + Adam), and
+    every `every` steps clone the top `fraction` by accumulated |dL/d points_img|
+    (means jittered by N(0, jitter)) and prune opacity < 0.005.
+
+    path "fused": render_l1 + FusedAdam + Densifier (library kernels only);
+    path "drop-in": the reference's loop -- PyTorch activations and l1_loss
+    around the drop-in render(), one torch.optim.Adam per group
+    (scripts/train.py:17-44), index/cat rebuilds.  Reports the average step
+    time over the whole run (densification included) and peak HBM."""
+    from cuda_rasterizer.fused import render_l1
+    from cuda_rasterizer.train import Densifier, FusedAdam
+    from cuda_rasterizer.wrapper import render
+
+    dev = torch.device("cuda:0")
+    w2c_all = scene["w2c_per_step"].to(dev)
+    steps = steps or w2c_all.shape[0]
+    targets = scene["targets"].to(dev)
+    cam = scene["camera"]
+    K = cam["K"].to(dev)
+    W, H = cam["width"], cam["height"]
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in scene["params"].items()}
+    gen = torch.Generator(device=dev).manual_seed(0)
+    if path == "fused":
+        opt = FusedAdam(leaves, means_decay_steps=steps)
+        dens = Densifier(leaves["means"].shape[0], dev)
+    else:
+        from cuda_rasterizer.train import DEFAULT_LR
+
+        optims = {k: torch.optim.Adam([{"params": [p], "lr": DEFAULT_LR[k]}], eps=1e-15,
+                                      betas=(0.9, 0.999)) for k, p in leaves.items()}
+        sched = torch.optim.lr_scheduler.ExponentialLR(optims["means"], gamma=0.01 ** (1 / steps))
+        grads = torch.zeros(leaves["means"].shape[0], device=dev)
+    losses, sizes = [], []
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    t0 = time.perf_counter()
+    for step in range(steps):
+        target = targets[step % targets.shape[0]]
+        if path == "fused":
+            loss, _, _, _ = render_l1(w2c_all[step], K, W, H, leaves["means"], leaves["log_scales"],
+                                      leaves["quats_raw"], leaves["opacity_logits"], leaves["sh_dc"],
+                                      leaves["sh_rest"], target, near_plane=cam["near"],
+                                      grad2d_norm_accum=dens.grads)
+            loss.backward()
+            opt.step()
+            opt.zero_grad()
+            if (step + 1) % every == 0:
+                dens.clone_top_and_prune(leaves, opt, fraction, jitter, generator=gen)
+                sizes.append(leaves["means"].shape[0])
+        else:
+            scales, quats, opac = activated(leaves)
+            image, pts, _ = render(w2c_all[step], K, W, H, leaves["means"], scales, quats, opac,
+                                   leaves["sh_dc"], leaves["sh_rest"], near_plane=cam["near"])
+            pts.retain_grad()
+            loss = torch.nn.functional.l1_loss(image / 255.0, target)
+            loss.backward()
+            with torch.no_grad():
+                grads.add_(pts.grad.norm(dim=1))
+            for o in optims.values():
+                o.step()
+                o.zero_grad(set_to_none=True)
+            sched.step()
+            if (step + 1) % every == 0:
+                with torch.no_grad():
+                    _torch_clone_top_and_prune(leaves, optims, grads, fraction, jitter)
+                grads = torch.zeros(leaves["means"].shape[0], device=dev)
+                sizes.append(leaves["means"].shape[0])
+        if step % 100 == 0 or step == steps - 1:
+            losses.append(loss.detach())
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    peak = torch.cuda.max_memory_allocated(dev)
+    return dict(ms=(t1 - t0) * 1e3 / steps, steps=steps, peak_hbm_bytes=int(peak),
+                peak_hbm_above_inputs_bytes=int(peak - base), n_start=scene["params"]["means"].shape[0],
+                n_end=leaves["means"].shape[0], sizes=sizes,
+                loss_first=float(losses[0]), loss_last=float(losses[-1]), width=W, height=H)
+
+
+def train_stress(steps: int = 2000) -> dict:
+    """Configuration 5 through the library (fused) and through the reference's
+    loop around the drop-in render() (drop-in), same scene and schedule."""
+    scene = config5(steps=steps)
+    out = {"workload": f"config5: {steps} steps from {scene['params']['means'].shape[0]} Gaussians "
+                       f"SH3 1280x720, clone top 5% / prune every 100 steps"}
+    for path in ("fused", "drop-in"):
+        r = run_train(scene, path)
+        out[path] = {"ms_per_step": round(r["ms"], 4), "peak_hbm_gib": round(r["peak_hbm_bytes"] / 2**30, 3),
+                     "n_end": r["n_end"], "loss_first": round(r["loss_first"], 5),
+                     "loss_last": round(r["loss_last"], 5)}
+    return out
 
 
 # ----------------------------------------------------------- roofline
@@ -460,12 +608,16 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=[1, 3, 4])
+    ap.add_argument("--config", type=int, default=3, choices=[1, 3, 4, 5],
+                    help="3 (headline, default), 1 or 4; 5 prints only the training stress run")
     ap.add_argument("--path", choices=["fused", "drop-in"], default="fused",
                     help="the timed step: fused render_l1 (default) or PyTorch glue around render()")
     ap.add_argument("--no-drop-in", action="store_true",
                     help="skip timing the drop-in path beside the fused one")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train", action="store_true",
+                    help="skip the configuration-5 training stress run beside the headline")
+    ap.add_argument("--train-steps", type=int, default=2000)
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU blend work in the cpu_baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -483,6 +635,10 @@ def main(argv=None):
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
 
+    if args.config == 5:
+        print(json.dumps(train_stress(args.train_steps)), flush=True)
+        return 0
+
     scene = CONFIGS[args.config]()
     res = run_gpu(scene, args.steps, args.warmup, args.path)
     rl = roofline(res, scene["name"])
@@ -491,6 +647,9 @@ def main(argv=None):
         d = run_gpu(scene, args.steps, args.warmup, "drop-in")
         drop_in = {"ms_per_step": round(d["ms"], 3), "loss": d["loss"],
                    "stages": roofline(d, scene["name"])["per_stage"]}
+    train = None
+    if not args.no_train and args.path == "fused":
+        train = train_stress(args.train_steps)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(scene, args.cpu_budget)
@@ -518,6 +677,7 @@ def main(argv=None):
         "stages": rl["per_stage"],
         "loss": res["loss"],
         "drop_in": drop_in,
+        "train_stress": train,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
