@@ -6,7 +6,8 @@
 // Gaussians (one per lane); at staging each lane computes which strips the
 // Gaussian's chi-square / alpha ellipse reaches, and only Gaussians reaching
 // the tile are written to LDS (ballot compaction, list order kept) with that
-// strip mask.  The wave evaluates only those strips, and it stops once the
+// strip mask and log2 of the opacity (alpha = exp2(E * -log2(e)/2 + log2 o)).
+// The wave evaluates only those strips, and it stops once the
 // transmittance of all 256 pixels fell below the threshold.  Tiles are assigned to workgroups XCD by XCD (the dispatcher
 // places workgroup b on XCD b % 8) so that neighbouring tiles, which share
 // Gaussians, run on the same XCD and share its L2.
@@ -87,11 +88,25 @@ __device__ __forceinline__ float conic_exponent(float A, float B2, float C, floa
     return (A * du * du + B2 * du * dv) + C * dv * dv;
 }
 
+// alpha = o exp(-E/2) = exp2(E * kNegHalfLog2e + log2(o)): one fma and one
+// v_exp_f32 per (entry, pixel).
+constexpr float kNegHalfLog2e = -0.72134752044448170f;
 struct BatchLds {
     float4 geo[kBatch];  // u, v, A, 2B
-    float4 aux[kBatch];  // C, opacity, ex, ey
+    float4 aux[kBatch];  // C, opacity, strip mask, log2(opacity)
     float4 col[kBatch];  // r, g, b, (gaussian id bits)
 };
+
+// log2(o) for the exponent form of alpha; -inf when o <= 0 (alpha 0: skipped,
+// as o exp(-E/2) <= 0 < alpha_thr), NaN stays NaN (alpha NaN: composited, as
+// in the reference).
+__device__ __forceinline__ float log2_opacity(float o) {
+    return o > 0.0f ? __builtin_amdgcn_logf(o) : (o == o ? -__builtin_inff() : o);
+}
+
+__device__ __forceinline__ float alpha_of(float E, float log2o) {
+    return __builtin_amdgcn_exp2f(fmaf(E, kNegHalfLog2e, log2o));
+}
 
 // One lane's Gaussian record of the next batch, fetched into registers while
 // the current batch is processed (id < 0: empty slot).
@@ -179,11 +194,18 @@ __device__ __forceinline__ uint32_t exact_strip_mask(uint32_t box, float u, floa
     return m;
 }
 
+// Result of staging one batch: the number of staged records, and whether one
+// of them has a non-finite colour (the batch then takes the select-based path).
+struct Staged {
+    int count;
+    bool nonfinite;
+};
+
 // Stages the lane's record into the next free LDS slot if its ellipse (with
 // the chi-square and alpha cut-offs) reaches the tile, keeping lane (= list)
-// order, with its strip mask in aux.z.  Returns the number of records staged.
-__device__ __forceinline__ int stage_records(BatchLds &s, const Record &r, float chi,
-                                             float alpha_thr, float x0, float y0) {
+// order, with its strip mask in aux.z and log2 of its opacity in aux.w.
+__device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, float chi,
+                                                float alpha_thr, float x0, float y0) {
     uint32_t m = 0u;
     if (r.id >= 0) {
         float ex, ey;
@@ -192,13 +214,17 @@ __device__ __forceinline__ int stage_records(BatchLds &s, const Record &r, float
                              effective_chi(r.o, chi, alpha_thr), x0, y0);
     }
     const uint64_t keep = __ballot(m != 0u);
+    const bool bad = m != 0u && !(isfinite(r.r) && isfinite(r.g) && isfinite(r.b));
     if (m != 0u) {
         const int slot = __popcll(keep & lanemask_lt());
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
-        s.aux[slot] = make_float4(r.C, r.o, __uint_as_float(m), 0.0f);
+        s.aux[slot] = make_float4(r.C, r.o, __uint_as_float(m), log2_opacity(r.o));
         s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
     }
-    return __popcll(keep);
+    Staged st;
+    st.count = __popcll(keep);
+    st.nonfinite = __ballot(bad) != 0;
+    return st;
 }
 
 // Software pipeline over a tile's list in batches of kBatch.  With kRecords,
@@ -225,8 +251,8 @@ struct BatchPipe {
     }
 
     // Stages the batch starting at b0 (only records reaching the tile) and
-    // fetches ahead.  Returns the number of staged records.
-    __device__ __forceinline__ int advance(BatchLds &s, int32_t b0, TileSpan span,
+    // fetches ahead.
+    __device__ __forceinline__ Staged advance(BatchLds &s, int32_t b0, TileSpan span,
                                            const int32_t *__restrict__ ids, int64_t n,
                                            const float *__restrict__ points,
                                            const float *__restrict__ conics,
@@ -236,7 +262,7 @@ struct BatchPipe {
         const int32_t lane = (int32_t)threadIdx.x;
         if (!kRecords) rec = fetch_record(next_id, n, points, conics, opac, colors);
         __syncthreads();  // previous batch fully read before restaging
-        const int cnt = stage_records(s, rec, chi, alpha_thr, x0, y0);
+        const Staged st = stage_records(s, rec, chi, alpha_thr, x0, y0);
         __syncthreads();
         if (kRecords) {
             rec = fetch_record(next_id, n, points, conics, opac, colors);
@@ -244,7 +270,7 @@ struct BatchPipe {
         } else {
             next_id = fetch_id(b0 + kBatch + lane, span.end, ids);
         }
-        return cnt;
+        return st;
     }
 };
 
@@ -298,22 +324,83 @@ __device__ __forceinline__ bool any_active(const float (&T)[kStrips], float T_th
     return wave_any(!(T[0] < T_thr) || !(T[1] < T_thr) || !(T[2] < T_thr) || !(T[3] < T_thr));
 }
 
+// One staged entry j applied to the lane's four pixels.  Branch-free per
+// strip: an entry that fails the chi-square or alpha test gets weight 0, so
+// C += 0 * c and T -= 0 leave the pixel unchanged; kSafe (a non-finite colour
+// in the batch, where 0 * inf would not be 0) uses selects instead.
+// T_{i+1} = T_i - alpha T_i, i.e. T_i (1 - alpha): the 1e-10 of the
+// reference's 1 - alpha + 1e-10 is below the float resolution of that factor
+// unless alpha is within 1e-7 of 1, where T drops below any threshold either way.
+template <bool kSafe>
+__device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const LanePixels &pix,
+                                            float alpha_thr, float T_thr, float chi,
+                                            float (&T)[kStrips], float (&cr)[kStrips],
+                                            float (&cg)[kStrips], float (&cb)[kStrips]) {
+    const float4 geo = s.geo[j];
+    const float4 aux = s.aux[j];
+    const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
+    const float4 col = s.col[j];
+    const float du = pix.fx - geo.x;
+    const float Adudu = (geo.z * du) * du;  // (A du) du, as in the oracle's A*du*du
+    const float B2du = geo.w * du;
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        if (!((smask >> q) & 1u)) continue;  // uniform
+        const float dv = pix.fy[q] - geo.y;
+        const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
+        const bool ok = !(T[q] < T_thr) && (E < chi);
+        if (!wave_any(ok)) continue;
+        const float alpha = alpha_of(E, aux.w);
+        const bool inc = ok && !(alpha < alpha_thr);
+        if (kSafe) {
+            const float w = alpha * T[q];
+            cr[q] = inc ? fmaf(w, col.x, cr[q]) : cr[q];
+            cg[q] = inc ? fmaf(w, col.y, cg[q]) : cg[q];
+            cb[q] = inc ? fmaf(w, col.z, cb[q]) : cb[q];
+            T[q] = inc ? T[q] - w : T[q];
+        } else {
+            const float w = (inc ? alpha : 0.0f) * T[q];
+            cr[q] = fmaf(w, col.x, cr[q]);
+            cg[q] = fmaf(w, col.y, cg[q]);
+            cb[q] = fmaf(w, col.z, cb[q]);
+            T[q] = T[q] - w;
+        }
+    }
+}
+
+template <bool kSafe>
+__device__ __forceinline__ void blend_batch(const BatchLds &s, int cnt, const LanePixels &pix,
+                                            float alpha_thr, float T_thr, float chi,
+                                            float (&T)[kStrips], float (&cr)[kStrips],
+                                            float (&cg)[kStrips], float (&cb)[kStrips]) {
+    for (int j = 0; j < cnt; ++j) {
+        blend_entry<kSafe>(s, j, pix, alpha_thr, T_thr, chi, T, cr, cg, cb);
+        if ((j & 7) == 7 && !any_active(T, T_thr)) break;
+    }
+}
+
+// Transmittance of a pixel that takes no part (outside the image, or a zero
+// gradient in the backward): inactive for every threshold above -1e30
+// (thresholds are clamped there), and finite, so that a zero weight times it
+// stays zero.
+constexpr float kInactiveT = -3.0e38f;
+
+__device__ __forceinline__ float effective_T_thr(float T_thr) { return fmaxf(T_thr, -1e30f); }
+
 // Front-to-back accumulation of the lane's four pixels over the tile's list.
-// All 64 lanes must call it (it contains barriers).  Branch-free per strip:
-// an entry that fails the chi-square or alpha test leaves T and the colour
-// unchanged through selects (T * (1 - 0 + 1e-10) would also be exact, but the
-// colour update must not touch a non-finite colour of a skipped Gaussian).
+// All 64 lanes must call it (it contains barriers).
 __device__ __forceinline__ void blend_accumulate(
     BatchLds &s, TileSpan span, const int32_t *__restrict__ ids, int64_t n,
     const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, const LanePixels &pix,
-    float alpha_thr, float T_thr, float chi, float (&cr)[kStrips], float (&cg)[kStrips],
+    float alpha_thr, float T_thr_in, float chi, float (&cr)[kStrips], float (&cg)[kStrips],
     float (&cb)[kStrips]) {
-    // a pixel is active while !(T < T_thr); pixels outside the image start at -inf
+    // a pixel is active while !(T < T_thr)
+    const float T_thr = effective_T_thr(T_thr_in);
     float T[kStrips];
 #pragma unroll
     for (int q = 0; q < kStrips; ++q) {
-        T[q] = pix.inside[q] ? 1.0f : -__builtin_inff();
+        T[q] = pix.inside[q] ? 1.0f : kInactiveT;
         cr[q] = cg[q] = cb[q] = 0.0f;
     }
     if (span.end <= span.start) return;
@@ -321,34 +408,12 @@ __device__ __forceinline__ void blend_accumulate(
     pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
         if (!any_active(T, T_thr)) break;
-        const int cnt = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
-                                     alpha_thr, pix.x0, pix.y0);
-        for (int j = 0; j < cnt; ++j) {
-            const float4 geo = s.geo[j];
-            const float4 aux = s.aux[j];
-            const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
-            const float4 col = s.col[j];
-            const float du = pix.fx - geo.x;
-            const float Adudu = (geo.z * du) * du;  // (A du) du, as in the oracle's A*du*du
-            const float B2du = geo.w * du;
-#pragma unroll
-            for (int q = 0; q < kStrips; ++q) {
-                if (!((smask >> q) & 1u)) continue;  // uniform
-                const float dv = pix.fy[q] - geo.y;
-                const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
-                const bool ok = !(T[q] < T_thr) && (E < chi);
-                if (!wave_any(ok)) continue;
-                const float alpha = __expf(-0.5f * E) * aux.y;
-                const bool inc = ok && !(alpha < alpha_thr);
-                const float w = alpha * T[q];
-                cr[q] = inc ? fmaf(w, col.x, cr[q]) : cr[q];
-                cg[q] = inc ? fmaf(w, col.y, cg[q]) : cg[q];
-                cb[q] = inc ? fmaf(w, col.z, cb[q]) : cb[q];
-                const float Tn = T[q] * ((1.0f - alpha) + kTransmittanceEps);
-                T[q] = inc ? Tn : T[q];
-            }
-            if ((j & 7) == 7 && !any_active(T, T_thr)) break;
-        }
+        const Staged st = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
+                                       alpha_thr, pix.x0, pix.y0);
+        if (st.nonfinite)
+            blend_batch<true>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb);
+        else
+            blend_batch<false>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb);
     }
 }
 
@@ -470,11 +535,13 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     }
 }
 
-// Destination of the lane's field after wave_sum9: out[stride * g] += value * (fa * o + fb).
+// Destination of the lane's field after wave_sum9:
+// out[stride * g] += value * (inv_o ? 1 / o : fa).
 struct GradTarget {
     float *base;
     int stride;
-    float fa, fb;
+    float fa;
+    bool inv_o;
     bool active;
 };
 
@@ -486,30 +553,121 @@ __device__ __forceinline__ GradTarget grad_target(int lane, float *g_points, flo
     t.base = g_points;
     t.stride = 2;
     t.fa = 1.0f;
-    t.fb = 0.0f;
+    t.inv_o = false;
     switch (f) {
     case 0: t.base = g_points; break;
     case 1: t.base = g_points + 1; break;
     case 2: t.base = g_conics; t.stride = 3; t.fa = -0.5f; break;
     case 3: t.base = g_conics + 1; t.stride = 3; t.fa = -1.0f; break;
     case 4: t.base = g_conics + 2; t.stride = 3; t.fa = -0.5f; break;
-    case 5: t.base = g_opac; t.stride = 1; t.fa = 0.0f; t.fb = 1.0f; break;
-    case 6: t.base = g_colors; t.stride = 3; t.fa = 0.0f; t.fb = 1.0f; break;
-    case 7: t.base = g_colors + 1; t.stride = 3; t.fa = 0.0f; t.fb = 1.0f; break;
-    case 8: t.base = g_colors + 2; t.stride = 3; t.fa = 0.0f; t.fb = 1.0f; break;
+    case 5: t.base = g_opac; t.stride = 1; t.inv_o = true; break;
+    case 6: t.base = g_colors; t.stride = 3; break;
+    case 7: t.base = g_colors + 1; t.stride = 3; break;
+    case 8: t.base = g_colors + 2; t.stride = 3; break;
     default: break;
     }
     return t;
 }
 
+// Per-lane state of the backward walk: transmittance and the running sum
+// acc = sum_{k<=i} w_k (g.c_k) of the lane's four pixels, their colour
+// gradients g and gC = g.C.
+struct BackwardLane {
+    float T[kStrips], acc[kStrips];
+    float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips];
+};
+
+// One staged entry j: per-strip gradient terms summed over the lane's pixels,
+// then the nine-field wave sum and one atomic per field (lanes of tgt).
+template <bool kSafe>
+__device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const LanePixels &pix,
+                                               float alpha_thr, float T_thr, float chi,
+                                               BackwardLane &L, const GradTarget &tgt, bool hi8,
+                                               bool f8_lane) {
+    const float4 geo = s.geo[j];
+    const float4 aux = s.aux[j];
+    const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
+    const float4 col = s.col[j];
+    const float du = pix.fx - geo.x;
+    const float Adudu = (geo.z * du) * du;
+    const float B2du = geo.w * du;
+    // -0 is the identity of float addition, so the first strip's sums need no add
+    float sH = -0.0f, s1 = -0.0f, s2 = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f;
+    bool hit = false;  // some strip was evaluated (otherwise every field is -0)
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        if (!((smask >> q) & 1u)) continue;  // uniform
+        const float dv = pix.fy[q] - geo.y;
+        const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
+        const bool ok = !(L.T[q] < T_thr) && (E < chi);
+        if (!wave_any(ok)) continue;
+        hit = true;
+        const float alpha = alpha_of(E, aux.w);
+        const bool inc = ok && !(alpha < alpha_thr);
+        const float a = kSafe ? alpha : (inc ? alpha : 0.0f);
+        const float w = a * L.T[q];
+        const float gcol = fmaf(L.gr[q], col.x, fmaf(L.gg[q], col.y, L.gb[q] * col.z));
+        const float acc_new = fmaf(w, gcol, L.acc[q]);
+        const float one_m = (1.0f - a) + kTransmittanceEps;
+        // dalpha = T gcol - (gC - acc_new) / (1 - alpha + eps)
+        const float dalpha = fmaf(acc_new - L.gC[q], __builtin_amdgcn_rcpf(one_m), L.T[q] * gcol);
+        const float h = kSafe ? (inc ? a * dalpha : 0.0f) : a * dalpha;
+        const float ws = kSafe ? (inc ? w : 0.0f) : w;
+        sH += h;
+        const float t = h * dv;
+        s1 += t;
+        s2 = fmaf(t, dv, s2);
+        sr = fmaf(ws, L.gr[q], sr);
+        sg = fmaf(ws, L.gg[q], sg);
+        sb = fmaf(ws, L.gb[q], sb);
+        L.acc[q] = kSafe ? (inc ? acc_new : L.acc[q]) : acc_new;
+        L.T[q] = kSafe ? (inc ? L.T[q] - w : L.T[q]) : L.T[q] - w;
+    }
+    if (hit) {
+        const float B = 0.5f * geo.w;
+        const float ad = du * sH;
+        float f[kGradFields];
+        f[0] = fmaf(geo.z, ad, B * s1);  // d/du
+        f[1] = fmaf(B, ad, aux.x * s1);  // d/dv
+        f[2] = du * ad;                  // d/dA / (-1/2)
+        f[3] = du * s1;                  // d/dB / (-1)
+        f[4] = s2;                       // d/dC / (-1/2)
+        f[5] = sH;                       // d/dopacity * o
+        f[6] = sr;
+        f[7] = sg;
+        f[8] = sb;
+        const float total = wave_sum9(f, hi8, f8_lane);
+        if (tgt.active) {
+            const int g = __float_as_int(col.w);
+            const float scale = tgt.inv_o ? __builtin_amdgcn_rcpf(aux.y) : tgt.fa;
+            unsafeAtomicAdd(tgt.base + (int64_t)tgt.stride * g, total * scale);
+        }
+    }
+}
+
+template <bool kSafe>
+__device__ __forceinline__ void backward_batch(const BatchLds &s, int cnt, const LanePixels &pix,
+                                               float alpha_thr, float T_thr, float chi,
+                                               BackwardLane &L, const GradTarget &tgt, bool hi8,
+                                               bool f8_lane) {
+    for (int j = 0; j < cnt; ++j) {
+        backward_entry<kSafe>(s, j, pix, alpha_thr, T_thr, chi, L, tgt, hi8, f8_lane);
+        if ((j & 7) == 7 && !any_active(L.T, T_thr)) break;
+    }
+}
+
 // Backward of the front-to-back blend, walking the list in the same order.
-// With h = alpha dalpha = o G dalpha, the per-pixel terms of the gradients are
+// With h = alpha dalpha (= o G dalpha), the per-pixel terms of the gradients are
 //   d/du = h (A du + B dv), d/dv = h (B du + C dv),
 //   d/dA = -h du^2 / 2, d/dB = -h du dv, d/dC = -h dv^2 / 2,
-//   d/do = G dalpha, d/dc = w g.
-// A lane's four pixels share du, so it keeps sG = sum G dalpha, s1 = sum G dalpha dv,
-// s2 = sum G dalpha dv^2 and the colour sums, and forms the nine fields (up to the
-// uniform factor o, applied after the wave sum) once per Gaussian.
+//   d/do = h / o, d/dc = w g.
+// A lane's four pixels share du, so it keeps sH = sum h, s1 = sum h dv,
+// s2 = sum h dv^2 and the colour sums, and forms the nine fields once per
+// Gaussian (1/o is applied to the opacity field after the wave sum).  An entry
+// that fails the chi-square or alpha test gets alpha 0, hence h = 0, w = 0 and
+// an unchanged T and partial sum; where that could meet a non-finite value (a
+// record's colour, or a gradient or image value of the tile) the update uses
+// selects instead.
 // kSeed: kSeedImage  grad_image is the gradient of the image;
 //        kSeedDisplay grad_image is the gradient of display = clamp(image, 0, 1) * 255
 //                     (image required);
@@ -523,10 +681,11 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
-    int height, float alpha_thr, float T_thr, float chi, float *__restrict__ g_points,
+    int height, float alpha_thr, float T_thr_in, float chi, float *__restrict__ g_points,
     float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors,
     const float *__restrict__ grad_loss, float inv_count) {
     __shared__ BatchLds s;
+    const float T_thr = effective_T_thr(T_thr_in);
     const int tile = tile_of_block(blockIdx.x, n_tiles);
     const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
@@ -534,44 +693,51 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     // d loss / d (display / 255) per element, for kSeedL1
     const float l1_scale = kSeed == kSeedL1 ? *grad_loss * inv_count : 0.0f;
 
-    float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips], T[kStrips], acc[kStrips];
+    BackwardLane L;
     float cr[kStrips], cg[kStrips], cb[kStrips];
     if (!image)
-        blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr,
+        blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr_in,
                          chi, cr, cg, cb);
+    bool finite = true;
 #pragma unroll
     for (int q = 0; q < kStrips; ++q) {
-        gr[q] = gg[q] = gb[q] = 0.0f;
+        float gr = 0.0f, gg = 0.0f, gb = 0.0f;
         if (pix.inside[q]) {
             const int64_t o = ((int64_t)pix.fy[q] * width + (int64_t)pix.fx) * 3;
-            gr[q] = grad_image[o];
-            gg[q] = grad_image[o + 1];
-            gb[q] = grad_image[o + 2];
+            gr = grad_image[o];
+            gg = grad_image[o + 1];
+            gb = grad_image[o + 2];
             if (image) {
                 cr[q] = image[o];
                 cg[q] = image[o + 1];
                 cb[q] = image[o + 2];
             }
             if (kSeed == kSeedL1) {  // sign(display/255 - t) * g / n, then / 255
-                gr[q] = l1_grad(gr[q], cr[q], l1_scale);
-                gg[q] = l1_grad(gg[q], cg[q], l1_scale);
-                gb[q] = l1_grad(gb[q], cb[q], l1_scale);
+                gr = l1_grad(gr, cr[q], l1_scale);
+                gg = l1_grad(gg, cg[q], l1_scale);
+                gb = l1_grad(gb, cb[q], l1_scale);
             }
             if (kSeed != kSeedImage) {
-                gr[q] = display_grad(gr[q], cr[q]);
-                gg[q] = display_grad(gg[q], cg[q]);
-                gb[q] = display_grad(gb[q], cb[q]);
+                gr = display_grad(gr, cr[q]);
+                gg = display_grad(gg, cg[q]);
+                gb = display_grad(gb, cb[q]);
             }
         } else {
             cr[q] = cg[q] = cb[q] = 0.0f;
         }
-        gC[q] = gr[q] * cr[q] + gg[q] * cg[q] + gb[q] * cb[q];
-        acc[q] = 0.0f;
+        L.gr[q] = gr;
+        L.gg[q] = gg;
+        L.gb[q] = gb;
+        L.gC[q] = gr * cr[q] + gg * cg[q] + gb * cb[q];
+        L.acc[q] = 0.0f;
+        finite = finite && isfinite(gr) && isfinite(gg) && isfinite(gb) && isfinite(L.gC[q]);
         // active while !(T < T_thr); pixels outside the image or with a zero
-        // gradient (skipped as in src/cuda/kernel.cu:1028-1030) start at -inf
-        const bool live = pix.inside[q] && !(gr[q] == 0.0f && gg[q] == 0.0f && gb[q] == 0.0f);
-        T[q] = live ? 1.0f : -__builtin_inff();
+        // gradient (skipped as in src/cuda/kernel.cu:1028-1030) start inactive
+        const bool live = pix.inside[q] && !(gr == 0.0f && gg == 0.0f && gb == 0.0f);
+        L.T[q] = live ? 1.0f : kInactiveT;
     }
+    // the zero-weight update needs finite gradients and image values in the tile
+    const bool tile_nonfinite = __ballot(!finite) != 0;
 
     const int lane = threadIdx.x;
     const bool hi8 = (lane & 8) != 0;
@@ -581,72 +747,13 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     BatchPipe<false> pipe;
     pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
-        if (!any_active(T, T_thr)) break;
-        const int cnt = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
-                                     alpha_thr, pix.x0, pix.y0);
-        for (int j = 0; j < cnt; ++j) {
-            const float4 geo = s.geo[j];
-            const float4 aux = s.aux[j];
-            const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
-            const float4 col = s.col[j];
-            const float du = pix.fx - geo.x;
-            const float Adudu = (geo.z * du) * du;
-            const float B2du = geo.w * du;
-            float sG = 0.0f, s1 = 0.0f, s2 = 0.0f, sr = 0.0f, sg = 0.0f, sb = 0.0f;
-            uint64_t hit = 0;
-#pragma unroll
-            for (int q = 0; q < kStrips; ++q) {
-                if (!((smask >> q) & 1u)) continue;  // uniform
-                const float dv = pix.fy[q] - geo.y;
-                const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
-                const bool ok = !(T[q] < T_thr) && (E < chi);
-                if (!wave_any(ok)) continue;
-                const float G = __expf(-0.5f * E);
-                const float alpha = G * aux.y;
-                const bool inc = ok && !(alpha < alpha_thr);
-                const float w = alpha * T[q];
-                const float gcol = fmaf(gr[q], col.x, fmaf(gg[q], col.y, gb[q] * col.z));
-                const float acc_new = fmaf(w, gcol, acc[q]);
-                const float one_m = (1.0f - alpha) + kTransmittanceEps;
-                // dalpha = T gcol - (gC - acc_new) / (1 - alpha + eps)
-                const float dalpha =
-                    fmaf(acc_new - gC[q], __builtin_amdgcn_rcpf(one_m), T[q] * gcol);
-                const float Gd = inc ? G * dalpha : 0.0f;
-                const float ws = inc ? w : 0.0f;
-                sG += Gd;
-                const float t = Gd * dv;
-                s1 += t;
-                s2 = fmaf(t, dv, s2);
-                sr = fmaf(ws, gr[q], sr);
-                sg = fmaf(ws, gg[q], sg);
-                sb = fmaf(ws, gb[q], sb);
-                acc[q] = inc ? acc_new : acc[q];
-                const float Tn = T[q] * one_m;
-                T[q] = inc ? Tn : T[q];
-                hit |= __ballot(inc);
-            }
-            if (hit != 0) {
-                const float B = 0.5f * geo.w;
-                const float a = du * sG;
-                float f[kGradFields];
-                f[0] = fmaf(geo.z, a, B * s1);   // d/du / o
-                f[1] = fmaf(B, a, aux.x * s1);   // d/dv / o
-                f[2] = du * a;                   // d/dA / (-o/2)
-                f[3] = du * s1;                  // d/dB / (-o)
-                f[4] = s2;                       // d/dC / (-o/2)
-                f[5] = sG;                       // d/dopacity
-                f[6] = sr;
-                f[7] = sg;
-                f[8] = sb;
-                const float total = wave_sum9(f, hi8, f8_lane);
-                if (tgt.active) {
-                    const int g = __float_as_int(col.w);
-                    unsafeAtomicAdd(tgt.base + (int64_t)tgt.stride * g,
-                                    total * fmaf(tgt.fa, aux.y, tgt.fb));
-                }
-            }
-            if ((j & 7) == 7 && !any_active(T, T_thr)) break;
-        }
+        if (!any_active(L.T, T_thr)) break;
+        const Staged st = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
+                                       alpha_thr, pix.x0, pix.y0);
+        if (st.nonfinite || tile_nonfinite)
+            backward_batch<true>(s, st.count, pix, alpha_thr, T_thr, chi, L, tgt, hi8, f8_lane);
+        else
+            backward_batch<false>(s, st.count, pix, alpha_thr, T_thr, chi, L, tgt, hi8, f8_lane);
     }
 }
 

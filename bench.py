@@ -370,13 +370,15 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
                 loss_first=float(losses[0]), loss_last=float(losses[-1]), width=W, height=H)
 
 
-def train_stress(steps: int = 2000) -> dict:
+def train_stress(steps: int = 2000, which: str = "both") -> dict:
     """Configuration 5 through the library (fused) and through the reference's
     loop around the drop-in render() (drop-in), same scene and schedule."""
     scene = config5(steps=steps)
     out = {"workload": f"config5: {steps} steps from {scene['params']['means'].shape[0]} Gaussians "
                        f"SH3 1280x720, clone top 5% / prune every 100 steps"}
     for path in ("fused", "drop-in"):
+        if which not in ("both", path):
+            continue
         r = run_train(scene, path)
         out[path] = {"ms_per_step": round(r["ms"], 4), "peak_hbm_gib": round(r["peak_hbm_bytes"] / 2**30, 3),
                      "n_end": r["n_end"], "loss_first": round(r["loss_first"], 5),
@@ -618,6 +620,8 @@ def main(argv=None):
     ap.add_argument("--no-train", action="store_true",
                     help="skip the configuration-5 training stress run beside the headline")
     ap.add_argument("--train-steps", type=int, default=2000)
+    ap.add_argument("--train-path", choices=["both", "fused", "drop-in"], default="both",
+                    help="which loops the training stress run times")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU blend work in the cpu_baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -636,7 +640,7 @@ def main(argv=None):
         return copy_calibration(args.copy_calibration)
 
     if args.config == 5:
-        print(json.dumps(train_stress(args.train_steps)), flush=True)
+        print(json.dumps(train_stress(args.train_steps, args.train_path)), flush=True)
         return 0
 
     scene = CONFIGS[args.config]()
@@ -649,7 +653,7 @@ def main(argv=None):
                    "stages": roofline(d, scene["name"])["per_stage"]}
     train = None
     if not args.no_train and args.path == "fused":
-        train = train_stress(args.train_steps)
+        train = train_stress(args.train_steps, args.train_path)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(scene, args.cpu_budget)
