@@ -546,16 +546,36 @@ struct L2Args {
     int n_super, super_x, tiles_x, tiles_y, width, height, tile_size;
 };
 
-// block_map[b] for the chunks of supertile s (one thread per supertile).
-__global__ __launch_bounds__(256) void l2_map_kernel(int n_super,
-                                                     const int32_t *__restrict__ super_off,
-                                                     const uint32_t *__restrict__ chunk_start,
-                                                     uint2 *__restrict__ block_map) {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= n_super) return;
-    const uint32_t first = (uint32_t)super_off[s];
-    for (uint32_t b = chunk_start[s], c = 0; b < chunk_start[s + 1]; ++b, ++c)
-        block_map[b] = make_uint2((uint32_t)s, first + c * kL2Threads);
+// One workgroup: chunks of every supertile's list (kL2Threads entries each),
+// their exclusive scan chunk_start (chunk_start[n_super] = all chunks), the
+// block map block_map[b] = (supertile, first list position) of every level-2
+// block, and zeroed per-tile entry counters.  Thread i handles a contiguous
+// run of supertiles.
+constexpr int kPlanThreads = 1024;
+
+__global__ __launch_bounds__(kPlanThreads) void l2_plan_kernel(
+    int n_super, int64_t m, const int32_t *__restrict__ super_off,
+    uint32_t *__restrict__ chunk_start, uint2 *__restrict__ block_map, int n_tiles,
+    uint32_t *__restrict__ tile_counts) {
+    __shared__ uint32_t tmp[kPlanThreads / kWave + 1];
+    for (int t = threadIdx.x; t < n_tiles; t += kPlanThreads) tile_counts[t] = 0u;
+    const int per = (n_super + kPlanThreads - 1) / kPlanThreads;
+    const int s0 = min((int)threadIdx.x * per, n_super), s1 = min(s0 + per, n_super);
+    auto chunks_of = [&](int s) {
+        const int64_t end = s + 1 < n_super ? super_off[s + 1] : m;
+        return (uint32_t)((end - super_off[s] + kL2Threads - 1) / kL2Threads);
+    };
+    uint32_t mine = 0;
+    for (int s = s0; s < s1; ++s) mine += chunks_of(s);
+    uint32_t total;
+    uint32_t b = block_exclusive_scan<uint32_t, kPlanThreads>(mine, tmp, total);
+    for (int s = s0; s < s1; ++s) {
+        chunk_start[s] = b;
+        const uint32_t first = (uint32_t)super_off[s], c = chunks_of(s);
+        for (uint32_t i = 0; i < c; ++i) block_map[b + i] = make_uint2((uint32_t)s, first + i * kL2Threads);
+        b += c;
+    }
+    if (threadIdx.x == 0) chunk_start[n_super] = total;
 }
 
 // Tile id of local tile j of supertile s, or -1 outside the tile grid.
@@ -638,55 +658,93 @@ __device__ __forceinline__ uint32_t wave_local_counts(const L2Block &x, uint64_t
     return (uint32_t)__popcll(rc[lane / kSuper] & rc[kSuper + lane % kSuper]);
 }
 
-// Table entry of (level-2 block b, wave w, local tile j).
-__device__ __forceinline__ int64_t l2_slot(uint32_t b, int w, int j) {
-    return ((int64_t)b * kL2Waves + w) * kSuperLocal + j;
-}
-
-// table[(b, w, j)] = entries of local tile j in wave w of block b;
-// counts[t] += the block's entries of tile t.
+// table[b * kSuperLocal + j] = entries of local tile j in level-2 block b;
+// tile_counts[t] += the same count for tile t.
 __global__ __launch_bounds__(kL2Threads) void l2_count_kernel(L2Args a,
                                                               uint32_t *__restrict__ table,
-                                                              uint32_t *__restrict__ counts) {
+                                                              uint32_t *__restrict__ tile_counts) {
     __shared__ uint32_t wave_cnt[kL2Waves][kSuperLocal];
     __shared__ uint64_t rowcol[kL2Waves][2 * kSuper];
     L2Block x;
     if (!l2_block(a, x)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t mine = wave_local_counts(x, rowcol[wave]);
-    wave_cnt[wave][lane] = mine;
-    table[l2_slot(x.b, wave, lane)] = mine;
+    wave_cnt[wave][lane] = wave_local_counts(x, rowcol[wave]);
     __syncthreads();
     if (threadIdx.x < kSuperLocal) {
         const int j = threadIdx.x;
         uint32_t c = 0;
 #pragma unroll
         for (int w = 0; w < kL2Waves; ++w) c += wave_cnt[w][j];
+        table[(int64_t)x.b * kSuperLocal + j] = c;
         const int t = tile_of_local(a, x.s, j);
-        if (c && t >= 0) atomicAdd(&counts[t], c);
+        if (c && t >= 0) atomicAdd(&tile_counts[t], c);
     }
 }
 
-// table[(b, w, j)] <- first output position of the entries of local tile j in
-// wave w of block b: indexing_offset of the tile plus its entries in the earlier
-// waves and chunks of the supertile.  One thread per (supertile, local tile).
-__global__ __launch_bounds__(256) void l2_prefix_kernel(L2Args a,
-                                                        const int32_t *__restrict__ tile_offsets,
-                                                        uint32_t *__restrict__ table) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)a.n_super * kSuperLocal) return;
-    const int s = (int)(idx / kSuperLocal), j = (int)(idx % kSuperLocal);
-    const int t = tile_of_local(a, s, j);
-    uint32_t pos = t >= 0 ? (uint32_t)tile_offsets[t] : 0u;
-    const uint32_t q1 = a.chunk_start[s + 1];
-    for (uint32_t q = a.chunk_start[s]; q < q1; ++q) {
-        uint32_t c[kL2Waves];  // independent loads
+// Largest tile grid whose entry-count scan each l2_prefix_kernel workgroup
+// computes itself (larger grids use a separate scan into indexing_offset).
+constexpr int kFusedTileScanMax = 16384;
+constexpr int kPrefixBatch = 16;  // chunk rows read per batch (independent loads)
+
+// One workgroup per supertile s.  First the first output position of each of
+// its tiles: the exclusive scan of tile_counts over the tile grid, computed
+// here when the grid has at most kFusedTileScanMax tiles (and written to
+// indexing_offset), else read from indexing_offset.  Then, per local tile j,
+// the exclusive scan of table[b][j] over the supertile's level-2 blocks b,
+// started at that position, in place: wave v scans a contiguous run of
+// blocks, after the sums of the runs before it.
+__global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
+    L2Args a, const uint32_t *__restrict__ tile_counts, int n_tiles, int fused_scan,
+    int32_t *__restrict__ indexing_offset, uint32_t *__restrict__ table) {
+    __shared__ uint32_t tmp[kL2Waves + 1];
+    __shared__ uint32_t thread_base[kL2Threads];
+    __shared__ uint32_t tile_off[kSuperLocal];
+    __shared__ uint32_t run_sum[kL2Waves][kSuperLocal];
+    const int s = blockIdx.x;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int per = (n_tiles + kL2Threads - 1) / kL2Threads;
+    if (fused_scan) {
+        const int t0 = min(tid * per, n_tiles), t1 = min(t0 + per, n_tiles);
+        uint32_t mine = 0;
+        for (int t = t0; t < t1; ++t) mine += tile_counts[t];
+        uint32_t total;
+        thread_base[tid] = block_exclusive_scan<uint32_t, kL2Threads>(mine, tmp, total);
+        __syncthreads();
+    }
+    if (tid < kSuperLocal) {
+        const int t = tile_of_local(a, s, tid);
+        uint32_t off = 0;
+        if (t >= 0) {
+            if (fused_scan) {
+                const int owner = t / per;
+                off = thread_base[owner];
+                for (int u = owner * per; u < t; ++u) off += tile_counts[u];
+                indexing_offset[t] = (int32_t)off;
+            } else {
+                off = (uint32_t)indexing_offset[t];
+            }
+        }
+        tile_off[tid] = off;
+    }
+    // the supertile's blocks [q0, q1); wave v takes [q0 + v * per_w, ...)
+    const uint32_t q0 = a.chunk_start[s], q1 = a.chunk_start[s + 1];
+    const uint32_t per_w = (q1 - q0 + kL2Waves - 1) / kL2Waves;
+    const uint32_t r0 = min(q0 + wave * per_w, q1), r1 = min(r0 + per_w, q1);
+    uint32_t sum = 0;
+    for (uint32_t q = r0; q < r1; ++q) sum += table[(int64_t)q * kSuperLocal + lane];
+    run_sum[wave][lane] = sum;
+    __syncthreads();
+    uint32_t pos = tile_off[lane];
+    for (int w = 0; w < wave; ++w) pos += run_sum[w][lane];
+    for (uint32_t q = r0; q < r1; q += kPrefixBatch) {
+        uint32_t c[kPrefixBatch];
 #pragma unroll
-        for (int w = 0; w < kL2Waves; ++w) c[w] = table[l2_slot(q, w, j)];
+        for (int i = 0; i < kPrefixBatch; ++i)
+            c[i] = q + i < r1 ? table[(int64_t)(q + i) * kSuperLocal + lane] : 0u;
 #pragma unroll
-        for (int w = 0; w < kL2Waves; ++w) {
-            table[l2_slot(q, w, j)] = pos;
-            pos += c[w];
+        for (int i = 0; i < kPrefixBatch; ++i) {
+            if (q + i < r1) table[(int64_t)(q + i) * kSuperLocal + lane] = pos;
+            pos += c[i];
         }
     }
 }
@@ -695,10 +753,21 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
                                                                 const uint32_t *__restrict__ table,
                                                                 int32_t *__restrict__ ids_out) {
     __shared__ uint32_t base[kL2Waves][kSuperLocal];
+    __shared__ uint64_t rowcol[kL2Waves][2 * kSuper];
     L2Block x;
     if (!l2_block(a, x)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    base[wave][lane] = table[l2_slot(x.b, wave, lane)];  // from l2_prefix_kernel
+    base[wave][lane] = wave_local_counts(x, rowcol[wave]);
+    __syncthreads();
+    if (threadIdx.x < kSuperLocal) {  // first position of each wave's entries of tile j
+        uint32_t pos = table[(int64_t)x.b * kSuperLocal + threadIdx.x];  // from l2_prefix_kernel
+#pragma unroll
+        for (int w = 0; w < kL2Waves; ++w) {
+            const uint32_t c = base[w][threadIdx.x];
+            base[w][threadIdx.x] = pos;
+            pos += c;
+        }
+    }
     __syncthreads();
     const uint64_t below = lanemask_lt();
 #pragma unroll 4
@@ -738,16 +807,6 @@ __global__ __launch_bounds__(256) void emit_super_kernel(
 }
 
 // Number of level-2 chunks of each supertile list.
-__global__ __launch_bounds__(256) void l2_chunk_count_kernel(int n_super, int64_t m,
-                                                             const int32_t *__restrict__ super_off,
-                                                             uint32_t *__restrict__ chunks) {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= n_super) return;
-    const int64_t end = s + 1 < n_super ? super_off[s + 1] : m;
-    const int64_t len = end - super_off[s];
-    chunks[s] = (uint32_t)((len + kL2Threads - 1) / kL2Threads);
-}
-
 // keys[i] = tile << 32 | depth bits of ids[i], the tile being the last one
 // whose offset is <= i (the reference's sorted 64-bit keys).
 __global__ __launch_bounds__(256) void keys_from_offsets_kernel(
@@ -861,12 +920,13 @@ inline int64_t l2_blocks_bound(int64_t m, int n_super) {
 
 struct BinWs {
     SortWs lvl1;
-    int32_t *super_off;    // n_super (+1 spare)
-    int32_t *super_ids;    // m
-    uint32_t *chunks;      // n_super + 1: chunk counts, scanned in place to chunk_start
-    uint2 *block_map;      // level-2 block -> (supertile, first list position)
-    uint32_t *table;       // level-2 blocks x waves x 64
-    void *scan_ws;
+    int32_t *super_off;     // n_super (+1 spare)
+    int32_t *super_ids;     // m
+    uint32_t *chunk_start;  // n_super + 1: first level-2 block of each supertile
+    uint2 *block_map;       // level-2 block -> (supertile, first list position)
+    uint32_t *table;        // level-2 blocks x 64 local tiles
+    uint32_t *tile_counts;  // entries per tile
+    void *scan_ws;          // tile-count scan of grids above kFusedTileScanMax tiles
     size_t bytes;
 };
 
@@ -876,11 +936,11 @@ inline BinWs carve_bins(void *base, int64_t m, const Grid &g) {
     w.lvl1 = carve_sort(c, m, g.super_bits);
     w.super_off = c.take<int32_t>((int64_t)g.n_super + 1);
     w.super_ids = c.take<int32_t>(m);
-    w.chunks = c.take<uint32_t>((int64_t)g.n_super + 1);
+    w.chunk_start = c.take<uint32_t>((int64_t)g.n_super + 1);
     w.block_map = c.take<uint2>(l2_blocks_bound(m, g.n_super));
-    w.table = c.take<uint32_t>(l2_blocks_bound(m, g.n_super) * kL2Waves * kSuperLocal);
-    const int64_t scan_n = g.n_super > g.n_tiles ? g.n_super : g.n_tiles;
-    w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint32_t>(scan_n));
+    w.table = c.take<uint32_t>(l2_blocks_bound(m, g.n_super) * kSuperLocal);
+    w.tile_counts = c.take<uint32_t>(g.n_tiles);
+    w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint32_t>(g.n_tiles));
     w.bytes = align256(c.off);
     return w;
 }
@@ -1008,9 +1068,7 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         st = launch_status();
         if (st) return st;
     }
-    // per-tile entry counts accumulate in indexing_offset, then scan in place
-    st = zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)g.n_tiles, stream);
-    if (st || k == 0) return st;
+    if (k == 0) return zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)g.n_tiles, stream);
     if (!points_image || !radii || !gaussian_ids_sorted || (sorted_keys && !depths) || n == 0)
         return GS_ERR_INVALID_ARGUMENT;
 
@@ -1030,18 +1088,18 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
                                     w.super_ids, stream);
     if (st) return st;
 
-    // level 2: chunk map, per-tile counts, tile offsets, scatter
-    hipLaunchKernelGGL(l2_chunk_count_kernel, dim3(ceil_div(g.n_super, 256)), dim3(256), 0,
-                       stream, g.n_super, m, w.super_off, w.chunks);
+    // level 2: block plan, per-tile counts, tile offsets and block prefixes, scatter
+    const int64_t nb2 = l2_blocks_bound(m, g.n_super);
+    if (nb2 > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
+    hipLaunchKernelGGL(l2_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, g.n_super, m,
+                       w.super_off, w.chunk_start, w.block_map, g.n_tiles, w.tile_counts);
     st = launch_status();
-    if (st) return st;
-    st = scan_exclusive<uint32_t>(w.chunks, w.chunks, g.n_super, w.chunks + g.n_super, w.scan_ws,
-                                  stream);
     if (st) return st;
     L2Args l2;
     l2.super_off = w.super_off;
     l2.super_ids = w.super_ids;
-    l2.chunk_start = w.chunks;
+    l2.chunk_start = w.chunk_start;
+    l2.block_map = w.block_map;
     l2.rects = cw.rects;
     l2.n = n;
     l2.m = m;
@@ -1053,23 +1111,18 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
     l2.width = width;
     l2.height = height;
     l2.tile_size = tile_size;
-    const int64_t nb2 = l2_blocks_bound(m, g.n_super);
-    if (nb2 > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
-    l2.block_map = w.block_map;
-    hipLaunchKernelGGL(l2_map_kernel, dim3(ceil_div(g.n_super, 256)), dim3(256), 0, stream,
-                       g.n_super, w.super_off, w.chunks, w.block_map);
-    st = launch_status();
-    if (st) return st;
-    uint32_t *tile_counts = reinterpret_cast<uint32_t *>(indexing_offset);
     hipLaunchKernelGGL(l2_count_kernel, dim3((unsigned)nb2), dim3(kL2Threads), 0, stream, l2,
-                       w.table, tile_counts);
+                       w.table, w.tile_counts);
     st = launch_status();
     if (st) return st;
-    st = scan_exclusive<uint32_t>(tile_counts, tile_counts, g.n_tiles, (uint32_t *)nullptr,
-                                  w.scan_ws, stream);
-    if (st) return st;
-    hipLaunchKernelGGL(l2_prefix_kernel, dim3(ceil_div((int64_t)g.n_super * kSuperLocal, 256)),
-                       dim3(256), 0, stream, l2, indexing_offset, w.table);
+    const bool fused_scan = g.n_tiles <= kFusedTileScanMax;
+    if (!fused_scan) {
+        st = scan_exclusive<uint32_t>(w.tile_counts, reinterpret_cast<uint32_t *>(indexing_offset),
+                                      g.n_tiles, (uint32_t *)nullptr, w.scan_ws, stream);
+        if (st) return st;
+    }
+    hipLaunchKernelGGL(l2_prefix_kernel, dim3(g.n_super), dim3(kL2Threads), 0, stream, l2,
+                       w.tile_counts, g.n_tiles, fused_scan ? 1 : 0, indexing_offset, w.table);
     st = launch_status();
     if (st) return st;
     hipLaunchKernelGGL(l2_scatter_kernel, dim3((unsigned)nb2), dim3(kL2Threads), 0, stream, l2,
