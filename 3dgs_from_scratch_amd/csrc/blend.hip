@@ -60,24 +60,28 @@ __device__ __forceinline__ int tile_of_block(int b, int n_tiles) {
     return x * base + min(x, rem) + i;
 }
 
-// Exponent cut-off of a Gaussian with opacity o: E < chi and o exp(-E/2) >= alpha_thr.
-__device__ __forceinline__ float effective_chi(float o, float chi, float alpha_thr) {
+// Exponent cut-off of a Gaussian with log2 opacity log2o: E < chi and
+// o exp(-E/2) >= alpha_thr, i.e. E <= 2 ln(o / alpha_thr) = 2 ln2 (log2 o -
+// log2 alpha_thr).  Used only for culling, whose tests carry margins well
+// above the error of the hardware log.
+__device__ __forceinline__ float effective_chi(float log2o, float chi, float alpha_thr,
+                                               float log2_alpha_thr) {
     float chi_eff = chi;
-    if (alpha_thr > 0.0f && o > 0.0f) chi_eff = fminf(chi_eff, 2.0f * logf(o / alpha_thr));
+    if (alpha_thr > 0.0f && log2o > -__builtin_inff())
+        chi_eff = fminf(chi_eff, 1.3862943611198906f * (log2o - log2_alpha_thr));
     return chi_eff;
 }
 
-// Conservative half-extents of the ellipse {E < chi_eff} of conic (A, B, C),
-// where chi_eff also accounts for alpha >= alpha_thr.  Infinite when the conic
-// is not positive definite (no culling).
-__device__ __forceinline__ void ellipse_extent(float A, float B, float C, float o, float chi,
-                                               float alpha_thr, float &ex, float &ey) {
-    const float chi_eff = effective_chi(o, chi, alpha_thr);
+// Conservative half-extents of the ellipse {E < chi_eff} of conic (A, B, C).
+// Infinite when the conic is not positive definite (no culling).  Hardware
+// reciprocal and square root: the extents carry a 1% + 0.01 px margin.
+__device__ __forceinline__ void ellipse_extent(float A, float B, float C, float chi_eff,
+                                               float &ex, float &ey) {
     const float det = A * C - B * B;
     if (det > 0.0f && A > 0.0f && C > 0.0f && isfinite(chi_eff)) {
-        const float ce = fmaxf(chi_eff, 0.0f);
-        ex = sqrtf(ce * C / det) * 1.01f + 0.01f;
-        ey = sqrtf(ce * A / det) * 1.01f + 0.01f;
+        const float s = fmaxf(chi_eff, 0.0f) * __builtin_amdgcn_rcpf(det);
+        ex = __builtin_amdgcn_sqrtf(s * C) * 1.01f + 0.01f;
+        ey = __builtin_amdgcn_sqrtf(s * A) * 1.01f + 0.01f;
     } else {
         ex = ey = __builtin_inff();
     }
@@ -158,16 +162,17 @@ __device__ __forceinline__ uint32_t strip_mask(float u, float v, float ex, float
 // Minimum of E(dx, dy) = A dx^2 + 2B dx dy + C dy^2 (positive definite) over
 // the rectangle dx in [ax, bx], dy in [ay, by]: 0 if it contains the origin,
 // else the least of the four edge minima (on an edge the quadratic in the free
-// coordinate is minimised at its vertex, clamped to the edge).
-__device__ __forceinline__ float rect_min_exponent(float A, float B, float C, float ax, float bx,
-                                                   float ay, float by) {
+// coordinate is minimised at its vertex -B dx / C resp. -B dy / A, clamped to
+// the edge; nBC = -B / C and nBA = -B / A).
+__device__ __forceinline__ float rect_min_exponent(float A, float B, float C, float nBC, float nBA,
+                                                   float ax, float bx, float ay, float by) {
     if (ax <= 0.0f && bx >= 0.0f && ay <= 0.0f && by >= 0.0f) return 0.0f;
     auto edge_x = [&](float dx) {  // dx fixed, dy free in [ay, by]
-        const float dy = fminf(fmaxf(-B * dx / C, ay), by);
+        const float dy = fminf(fmaxf(nBC * dx, ay), by);
         return (A * dx * dx + 2.0f * B * dx * dy) + C * dy * dy;
     };
     auto edge_y = [&](float dy) {  // dy fixed, dx free in [ax, bx]
-        const float dx = fminf(fmaxf(-B * dy / A, ax), bx);
+        const float dx = fminf(fmaxf(nBA * dy, ax), bx);
         return (A * dx * dx + 2.0f * B * dx * dy) + C * dy * dy;
     };
     return fminf(fminf(edge_x(ax), edge_x(bx)), fminf(edge_y(ay), edge_y(by)));
@@ -175,21 +180,23 @@ __device__ __forceinline__ float rect_min_exponent(float A, float B, float C, fl
 
 // strip_mask refined per strip by the exact ellipse: a strip stays only if the
 // minimum of the exponent over its pixel rectangle is below the cut-off
-// (chi_eff, with a relative and absolute margin so rounding never drops a
-// contributing pixel).  A non-positive-definite conic keeps the box mask.
+// (chi_eff, with a relative and absolute margin so rounding -- also of the
+// hardware reciprocal placing the edge vertices -- never drops a contributing
+// pixel).  A non-positive-definite conic keeps the box mask.
 __device__ __forceinline__ uint32_t exact_strip_mask(uint32_t box, float u, float v, float A,
                                                      float B, float C, float chi_eff, float x0,
                                                      float y0) {
     if (box == 0u || !(A > 0.0f && C > 0.0f && A * C - B * B > 0.0f) || !(chi_eff < 1e30f))
         return box;
     const float cut = chi_eff * 1.02f + 0.02f;
+    const float nBC = -B * __builtin_amdgcn_rcpf(C), nBA = -B * __builtin_amdgcn_rcpf(A);
     const float ax = x0 - u, bx = x0 + (float)(kTile - 1) - u;
     uint32_t m = 0u;
 #pragma unroll
     for (int q = 0; q < kStrips; ++q) {
         if (!((box >> q) & 1u)) continue;
         const float ay = y0 + (float)(4 * q) - v, by = ay + 3.0f;
-        if (rect_min_exponent(A, B, C, ax, bx, ay, by) < cut) m |= 1u << q;
+        if (rect_min_exponent(A, B, C, nBC, nBA, ax, bx, ay, by) < cut) m |= 1u << q;
     }
     return m;
 }
@@ -205,20 +212,23 @@ struct Staged {
 // the chi-square and alpha cut-offs) reaches the tile, keeping lane (= list)
 // order, with its strip mask in aux.z and log2 of its opacity in aux.w.
 __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, float chi,
-                                                float alpha_thr, float x0, float y0) {
+                                                float alpha_thr, float log2_alpha_thr, float x0,
+                                                float y0) {
     uint32_t m = 0u;
+    const float log2o = log2_opacity(r.o);
     if (r.id >= 0) {
+        const float chi_eff = effective_chi(log2o, chi, alpha_thr, log2_alpha_thr);
         float ex, ey;
-        ellipse_extent(r.A, r.B, r.C, r.o, chi, alpha_thr, ex, ey);
+        ellipse_extent(r.A, r.B, r.C, chi_eff, ex, ey);
         m = exact_strip_mask(strip_mask(r.u, r.v, ex, ey, x0, y0), r.u, r.v, r.A, r.B, r.C,
-                             effective_chi(r.o, chi, alpha_thr), x0, y0);
+                             chi_eff, x0, y0);
     }
     const uint64_t keep = __ballot(m != 0u);
     const bool bad = m != 0u && !(isfinite(r.r) && isfinite(r.g) && isfinite(r.b));
     if (m != 0u) {
         const int slot = __popcll(keep & lanemask_lt());
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
-        s.aux[slot] = make_float4(r.C, r.o, __uint_as_float(m), log2_opacity(r.o));
+        s.aux[slot] = make_float4(r.C, r.o, __uint_as_float(m), log2o);
         s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
     }
     Staged st;
@@ -262,7 +272,8 @@ struct BatchPipe {
         const int32_t lane = (int32_t)threadIdx.x;
         if (!kRecords) rec = fetch_record(next_id, n, points, conics, opac, colors);
         __syncthreads();  // previous batch fully read before restaging
-        const Staged st = stage_records(s, rec, chi, alpha_thr, x0, y0);
+        const Staged st =
+            stage_records(s, rec, chi, alpha_thr, __builtin_amdgcn_logf(alpha_thr), x0, y0);
         __syncthreads();
         if (kRecords) {
             rec = fetch_record(next_id, n, points, conics, opac, colors);
