@@ -102,23 +102,38 @@ class StageTimer:
     """Opt-in HIP-event timing of entry points on the stream they launch on.
 
     While enabled, each instrumented call records a (start, end) event pair on
-    the device's current stream around the library call; `summary()` returns
-    {stage: (calls, total_ms)} after synchronising.
+    the device's current stream around the library call (only the stages in
+    `only`, when set); `summary()` returns {stage: (calls, total_ms)} after
+    synchronising.  Events come from a pool that reset() rewinds, so timing
+    adds two event records per timed call and no event creation.
     """
 
     def __init__(self):
         self.enabled = False
+        self.only = None
         self.events: dict = {}
+        self._pool: list = []
+        self._used = 0
 
     def reset(self):
         self.events = {}
+        self._used = 0
+
+    def _event(self):
+        import torch
+
+        if self._used == len(self._pool):
+            self._pool.append(torch.cuda.Event(enable_timing=True))
+        ev = self._pool[self._used]
+        self._used += 1
+        return ev
 
     def record(self, stage: str, device):
         import torch
 
-        if not self.enabled:
+        if not self.enabled or (self.only is not None and stage not in self.only):
             return None
-        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev = (self._event(), self._event())
         ev[0].record(torch.cuda.current_stream(device))
         self.events.setdefault(stage, []).append(ev)
         return ev
