@@ -15,10 +15,11 @@ same values with the library's kernels only:
 Values equal the unfused sequence up to floating-point summation order (the
 loss sum and the gradient atomics); tests/test_gpu_fused.py checks both
 against the drop-in path and the CPU oracle.  Only the loss is differentiable;
-the display image, points_img and radii are returned for logging and
-densification (src/strategy.py:47-68 reads dL/d points_img: pass
-`grad2d_norm_accum`, an (N,) fp32 tensor, and the backward adds
-|dL/d points_img| per Gaussian to it).
+the display image, points_img and radii are returned for logging.
+Densification statistics (src/strategy.py:47-68 reads dL/d points_img, which
+this node never materialises as a .grad): pass `densifier`, a
+cuda_rasterizer.train.Densifier, and the backward adds the gradient norms in
+NDC scale and the visibility counts to it (gs_accumulate_grad2d).
 """
 
 from __future__ import annotations
@@ -31,7 +32,7 @@ import cuda_rasterizer as _cr
 class RenderL1Function(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
-                world_to_camera, intrinsic, target, grad2d_norm_accum, width, height, near_plane,
+                world_to_camera, intrinsic, target, densifier, width, height, near_plane,
                 far_plane, min_opacity, min_radius, max_radius, alpha_threshold,
                 transmittance_threshold, chi_squared_threshold):
         scales, quats, opac = _cr.activate(log_scales, quats_raw, opacity_logits)
@@ -47,7 +48,8 @@ class RenderL1Function(torch.autograd.Function):
         ctx.save_for_backward(means, quats_raw, sh_coeffs_dc, sh_coeffs_rest, world_to_camera,
                               intrinsic, target, scales, quats, opac, pts, cov, conic, mask,
                               colors, off, ids, image)
-        ctx.grad2d = grad2d_norm_accum
+        ctx.densifier = densifier
+        ctx.radii = radii if densifier is not None else None
         ctx.params = (width, height, alpha_threshold, transmittance_threshold,
                       chi_squared_threshold)
         ctx.mark_non_differentiable(display, pts, radii)
@@ -64,8 +66,8 @@ class RenderL1Function(torch.autograd.Function):
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_l1_backward(
             target, grad_loss.reshape(1).to(torch.float32), off, ids, pts, conic, opac, colors,
             width, height, image, a_thr, t_thr, chi)
-        if ctx.grad2d is not None:
-            ctx.grad2d.add_(g_pts.norm(dim=1))
+        if ctx.densifier is not None:
+            ctx.densifier.update(g_pts, ctx.radii, width, height)
         g_means, g_scales, g_quats = _cr.project_points_backward(
             g_pts, g_conic, means, scales, quats, opac, w2c, K, width, height, cov, mask)
         _, g_dc, g_rest = _cr.evaluate_spherical_harmonics_render_backward(
@@ -79,7 +81,7 @@ def render_l1(world_to_camera, intrinsic, width, height, means, log_scales, quat
               opacity_logits, sh_coeffs_dc, sh_coeffs_rest, target, near_plane=0.01,
               far_plane=100.0, min_opacity=1 / 255, min_radius=0.5, max_radius=128.0,
               alpha_threshold=1e-4, transmittance_threshold=1e-4, chi_squared_threshold=9.21,
-              grad2d_norm_accum=None):
+              densifier=None):
     """loss = l1_loss(render(...activations of the raw parameters...)[0] / 255, target).
 
     Parameters are the raw training leaves of scripts/train.py:135-143
@@ -89,7 +91,7 @@ def render_l1(world_to_camera, intrinsic, width, height, means, log_scales, quat
     """
     return RenderL1Function.apply(
         means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
-        world_to_camera, intrinsic, target, grad2d_norm_accum, int(width), int(height),
+        world_to_camera, intrinsic, target, densifier, int(width), int(height),
         float(near_plane), float(far_plane), float(min_opacity), float(min_radius),
         float(max_radius), float(alpha_threshold), float(transmittance_threshold),
         float(chi_squared_threshold))

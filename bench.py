@@ -304,7 +304,8 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
               fraction: float = 0.05, jitter: float = 0.01) -> dict:
     """Configuration 5: `steps` training steps (render + L1 + backward + Adam), and
     every `every` steps clone the top `fraction` by accumulated |dL/d points_img|
-    (means jittered by N(0, jitter)) and prune opacity < 0.005.
+    (in NDC scale, over visible steps: src/strategy.py:47-68) (means jittered by
+    N(0, jitter)) and prune opacity < 0.005.
 
     path "fused": render_l1 + FusedAdam + Densifier (library kernels only);
     path "drop-in": the reference's loop -- PyTorch activations and l1_loss
@@ -345,7 +346,7 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
             loss, _, _, _ = render_l1(w2c_all[step], K, W, H, leaves["means"], leaves["log_scales"],
                                       leaves["quats_raw"], leaves["opacity_logits"], leaves["sh_dc"],
                                       leaves["sh_rest"], target, near_plane=cam["near"],
-                                      grad2d_norm_accum=dens.grads)
+                                      densifier=dens)
             loss.backward()
             opt.step()
             opt.zero_grad()
@@ -354,13 +355,18 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
                 sizes.append(leaves["means"].shape[0])
         else:
             scales, quats, opac = activated(leaves)
-            image, pts, _ = render(w2c_all[step], K, W, H, leaves["means"], scales, quats, opac,
-                                   leaves["sh_dc"], leaves["sh_rest"], near_plane=cam["near"])
+            image, pts, radii = render(w2c_all[step], K, W, H, leaves["means"], scales, quats,
+                                       opac, leaves["sh_dc"], leaves["sh_rest"],
+                                       near_plane=cam["near"])
             pts.retain_grad()
             loss = torch.nn.functional.l1_loss(image / 255.0, target)
             loss.backward()
-            with torch.no_grad():
-                grads.add_(pts.grad.norm(dim=1))
+            with torch.no_grad():  # src/strategy.py:47-68
+                g = pts.grad.clone()
+                g[:, 0] *= W / 2.0
+                g[:, 1] *= H / 2.0
+                sel = torch.where((radii > 0.0).all(dim=1))[0]
+                grads.index_add_(0, sel, g[sel].norm(dim=1))
             for o in optims.values():
                 o.step()
                 o.zero_grad(set_to_none=True)

@@ -18,8 +18,10 @@ import torch
 import helpers
 import cuda_rasterizer as cr
 from cuda_rasterizer.fused import render_l1
+from cuda_rasterizer.train import Densifier
 from cuda_rasterizer.wrapper import render
 from oracle import render as orender
+from oracle import train as otrain
 
 pytestmark = pytest.mark.gpu
 
@@ -65,23 +67,29 @@ def test_render_l1_matches_drop_in_path(gpu, scene):
     # drop-in path
     a = _raw_leaves(p, gpu)
     scales, quats, opac = helpers.activated(a)
-    img, pts, _ = render(w2c, K, W, H, a["means"], scales, quats, opac, a["sh_dc"], a["sh_rest"])
+    img, pts, radii = render(w2c, K, W, H, a["means"], scales, quats, opac, a["sh_dc"],
+                             a["sh_rest"])
     pts.retain_grad()
     loss_a = torch.nn.functional.l1_loss(img / 255.0, tgt)
     loss_a.backward()
-    # fused path
+    # fused path, densification statistics through a Densifier
     b = _raw_leaves(p, gpu)
-    accum = torch.zeros(p["means"].shape[0], device=gpu)
+    n = p["means"].shape[0]
+    dens = Densifier(n, gpu)
     loss_b, disp, pts_b, radii_b = render_l1(w2c, K, W, H, b["means"], b["log_scales"],
                                              b["quats_raw"], b["opacity_logits"], b["sh_dc"],
-                                             b["sh_rest"], tgt, grad2d_norm_accum=accum)
+                                             b["sh_rest"], tgt, densifier=dens)
     loss_b.backward()
     assert loss_b.shape == ()
     assert abs(float(loss_b) - float(loss_a)) <= 1e-5 * float(loss_a)
     assert helpers.max_abs(disp / 255.0, img.detach() / 255.0) <= 1e-4
     for k in helpers.PARAMS:
         assert helpers.rel_l2(b[k].grad, a[k].grad) <= 1e-4, k
-    assert helpers.rel_l2(accum, pts.grad.norm(dim=1)) <= 1e-4
+    # src/strategy.py:47-68 applied to the drop-in path's points_img.grad
+    want_g, want_c = otrain.accumulate_grad2d(torch.zeros(n), torch.zeros(n), pts.grad.cpu(),
+                                              radii.detach().cpu(), W, H)
+    assert helpers.rel_l2(dens.grads, want_g) <= 1e-4
+    assert torch.equal(dens.count.cpu(), want_c)
     assert torch.equal(pts_b, pts.detach()) or helpers.max_abs(pts_b, pts.detach()) <= 1e-4
 
 
