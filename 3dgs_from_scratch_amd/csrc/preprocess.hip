@@ -140,6 +140,72 @@ __device__ __forceinline__ void block_copy(float *__restrict__ lds, float *__res
     }
 }
 
+// View direction of a Gaussian at `mean` from the camera centre (cx, cy, cz)
+// and the 15 basis values of degrees 1..3 along it.
+struct ShView {
+    float x, y, z, norm;
+    float b[15];
+};
+
+__device__ __forceinline__ ShView sh_view(const float *__restrict__ mean, float cx, float cy,
+                                          float cz) {
+    ShView v;
+    const float dx = mean[0] - cx;
+    const float dy = mean[1] - cy;
+    const float dz = mean[2] - cz;
+    v.norm = sqrtf(dx * dx + dy * dy + dz * dz);
+    v.x = dx / v.norm;
+    v.y = dy / v.norm;
+    v.z = dz / v.norm;
+    sh_basis_rest(v.x, v.y, v.z, v.b);
+    return v;
+}
+
+// Raw colour channel c: C0 dc + sum_k b_k rest_k (rest: 15 x 3 floats).
+__device__ __forceinline__ float sh_raw_channel(const ShView &v, const float *__restrict__ dc,
+                                                const float *rest, int c) {
+    float acc = kShC0 * dc[c];
+#pragma unroll
+    for (int k = 0; k < 15; ++k) acc += v.b[k] * rest[3 * k + c];
+    return acc;
+}
+
+// render() colour: max(raw + 0.5, 0) keeping NaN (src/cuda/wrapper.py:264-265).
+__device__ __forceinline__ float sh_render_value(float raw) {
+    const float v = raw + 0.5f;
+    return v < 0.0f ? 0.0f : v;
+}
+
+// Gradient of the raw colour g (3 channels) into one Gaussian's SH row: the
+// row `lrest` (15 x 3, read in full first) is overwritten with its gradient,
+// gdc receives the DC gradient and gm the gradient of the mean through the
+// view direction (dir = d / |d| -> (I - dir dir^T) / |d|).
+__device__ __forceinline__ void sh_backward_row(const ShView &v, const float (&g)[3], float *lrest,
+                                                float (&gdc)[3], float (&gm)[3]) {
+    float bx[15], by[15], bz[15];
+    sh_basis_rest_grad(v.x, v.y, v.z, bx, by, bz);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) gdc[c] = kShC0 * g[c];
+    float gdx = 0.f, gdy = 0.f, gdz = 0.f;
+#pragma unroll
+    for (int k = 0; k < 15; ++k) {
+        const float gk = g[0] * lrest[3 * k] + g[1] * lrest[3 * k + 1] + g[2] * lrest[3 * k + 2];
+        gdx += gk * bx[k];
+        gdy += gk * by[k];
+        gdz += gk * bz[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 15; ++k) {
+        lrest[3 * k] = v.b[k] * g[0];
+        lrest[3 * k + 1] = v.b[k] * g[1];
+        lrest[3 * k + 2] = v.b[k] * g[2];
+    }
+    const float dot = v.x * gdx + v.y * gdy + v.z * gdz;
+    gm[0] = (gdx - v.x * dot) / v.norm;
+    gm[1] = (gdy - v.y * dot) / v.norm;
+    gm[2] = (gdz - v.z * dot) / v.norm;
+}
+
 __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(
     int64_t n, const float *__restrict__ cam_pos, const float *__restrict__ w2c,
     const float *__restrict__ means, const float *__restrict__ sh_dc,
@@ -151,29 +217,16 @@ __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(
     if (mask[i]) {
         float cx, cy, cz;
         camera_position(cam_pos, w2c, cx, cy, cz);
-        const float dx = means[3 * i] - cx;
-        const float dy = means[3 * i + 1] - cy;
-        const float dz = means[3 * i + 2] - cz;
-        const float norm = sqrtf(dx * dx + dy * dy + dz * dz);
-        float b[15];
-        sh_basis_rest(dx / norm, dy / norm, dz / norm, b);
+        const ShView v = sh_view(means + 3 * i, cx, cy, cz);
         const float *rest = sh_rest + kRest * i;  // 15 x 12-byte loads per thread
 #pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            float acc = kShC0 * sh_dc[3 * i + c];
-#pragma unroll
-            for (int k = 0; k < 15; ++k) acc += b[k] * rest[3 * k + c];
-            rgb[c] = acc;
-        }
+        for (int c = 0; c < 3; ++c) rgb[c] = sh_raw_channel(v, sh_dc + 3 * i, rest, c);
     }
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         float v = rgb[c];
         if (mode == kShSigmoid && mask[i]) v = 1.0f / (1.0f + expf(-v));
-        if (mode == kShRender) {
-            v = v + 0.5f;
-            v = v < 0.0f ? 0.0f : v;  // clamp_min keeping NaN
-        }
+        if (mode == kShRender) v = sh_render_value(v);
         colors[3 * i + c] = v;
     }
 }
@@ -198,14 +251,7 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(
         if (mask[i]) {
             float cx, cy, cz;
             camera_position(cam_pos, w2c, cx, cy, cz);
-            const float dx = means[3 * i] - cx;
-            const float dy = means[3 * i + 1] - cy;
-            const float dz = means[3 * i + 2] - cz;
-            const float norm = sqrtf(dx * dx + dy * dy + dz * dz);
-            const float x = dx / norm, y = dy / norm, z = dz / norm;
-            float b[15], bx[15], by[15], bz[15];
-            sh_basis_rest(x, y, z, b);
-            sh_basis_rest_grad(x, y, z, bx, by, bz);
+            const ShView v = sh_view(means + 3 * i, cx, cy, cz);
             float g[3];
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
@@ -215,33 +261,11 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(
                     g[c] *= s * (1.0f - s);
                 } else if (mode == kShRender) {
                     // clamp_min(raw + 0.5, 0) passes the gradient where raw + 0.5 >= 0
-                    float raw = kShC0 * sh_dc[3 * i + c];
-#pragma unroll
-                    for (int k = 0; k < 15; ++k) raw += b[k] * lrest[3 * k + c];
+                    const float raw = sh_raw_channel(v, sh_dc + 3 * i, lrest, c);
                     if (!(raw + 0.5f >= 0.0f)) g[c] = 0.0f;
                 }
-                gdc[c] = kShC0 * g[c];
             }
-            float gdx = 0.f, gdy = 0.f, gdz = 0.f;
-#pragma unroll
-            for (int k = 0; k < 15; ++k) {
-                const float gk = g[0] * lrest[3 * k] + g[1] * lrest[3 * k + 1] +
-                                 g[2] * lrest[3 * k + 2];
-                gdx += gk * bx[k];
-                gdy += gk * by[k];
-                gdz += gk * bz[k];
-            }
-#pragma unroll
-            for (int k = 0; k < 15; ++k) {
-                lrest[3 * k] = b[k] * g[0];
-                lrest[3 * k + 1] = b[k] * g[1];
-                lrest[3 * k + 2] = b[k] * g[2];
-            }
-            // dir = d / |d| -> (I - dir dir^T) / |d|
-            const float dot = x * gdx + y * gdy + z * gdz;
-            gm[0] = (gdx - x * dot) / norm;
-            gm[1] = (gdy - y * dot) / norm;
-            gm[2] = (gdz - z * dot) / norm;
+            sh_backward_row(v, g, lrest, gdc, gm);
         } else {
 #pragma unroll
             for (int k = 0; k < kRest; ++k) lrest[k] = 0.0f;
@@ -251,6 +275,220 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(
             grad_means[3 * i + c] = accumulate_means ? grad_means[3 * i + c] + gm[c] : gm[c];
             grad_dc[3 * i + c] = gdc[c];
         }
+    }
+    __syncthreads();
+    block_copy<false>(rest_lds, grad_rest + kRest * first, kRest * nb);
+}
+
+// ------------------------------------------------------------- activations
+// scripts/train.py:135-143: scales = exp(log_scales), quats = q / max(|q|, 1e-12),
+// opacities = sigmoid(logits).
+
+struct Activated {
+    float s[3];
+    float4 qraw;  // the raw quaternion
+    float qn;     // |qraw|
+    float q[4];   // the unit quaternion
+    float o;      // opacity
+};
+
+__device__ __forceinline__ Activated activate_one(const float *__restrict__ log_scales,
+                                                  const float *__restrict__ quats_raw,
+                                                  const float *__restrict__ logits, int64_t i) {
+    Activated a;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) a.s[c] = expf(log_scales[3 * i + c]);
+    const float4 q = reinterpret_cast<const float4 *>(quats_raw)[i];
+    a.qraw = q;
+    a.qn = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+    const float r = a.qn < 1e-12f ? 1e-12f : a.qn;  // clamp_min(1e-12)
+    a.q[0] = q.x / r;
+    a.q[1] = q.y / r;
+    a.q[2] = q.z / r;
+    a.q[3] = q.w / r;
+    a.o = 1.0f / (1.0f + expf(-logits[i]));
+    return a;
+}
+
+// Gradients of (scales, unit quaternion, opacity) mapped to (log-scales, raw
+// quaternion, logit).
+__device__ __forceinline__ void activate_backward_one(const Activated &a, const float (&gs)[3],
+                                                      float4 g, float go, float (&g_ls)[3],
+                                                      float4 &g_qr, float &g_logit) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) g_ls[c] = gs[c] * a.s[c];
+    const float4 q = a.qraw;
+    const float norm = a.qn;
+    if (norm < 1e-12f) {  // the clamp holds the divisor constant
+        g_qr = make_float4(g.x / 1e-12f, g.y / 1e-12f, g.z / 1e-12f, g.w / 1e-12f);
+    } else {  // d(q/|q|) = (g - qhat (qhat . g)) / |q|
+        const float hx = q.x / norm, hy = q.y / norm, hz = q.z / norm, hw = q.w / norm;
+        const float dot = hx * g.x + hy * g.y + hz * g.z + hw * g.w;
+        g_qr = make_float4((g.x - hx * dot) / norm, (g.y - hy * dot) / norm,
+                           (g.z - hz * dot) / norm, (g.w - hw * dot) / norm);
+    }
+    g_logit = go * (a.o * (1.0f - a.o));
+}
+
+__global__ __launch_bounds__(256) void activate_kernel(int64_t n,
+                                                      const float *__restrict__ log_scales,
+                                                      const float *__restrict__ quats_raw,
+                                                      const float *__restrict__ logits,
+                                                      float *__restrict__ scales,
+                                                      float *__restrict__ quats,
+                                                      float *__restrict__ opac) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const Activated a = activate_one(log_scales, quats_raw, logits, i);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) scales[3 * i + c] = a.s[c];
+    reinterpret_cast<float4 *>(quats)[i] = make_float4(a.q[0], a.q[1], a.q[2], a.q[3]);
+    opac[i] = a.o;
+}
+
+// Gradients of activate_kernel's outputs mapped to its inputs; a null gradient
+// input counts as zero.  Scales and opacities are the forward's outputs.
+__global__ __launch_bounds__(256) void activate_backward_kernel(
+    int64_t n, const float *__restrict__ grad_scales, const float *__restrict__ grad_quats,
+    const float *__restrict__ grad_opac, const float *__restrict__ scales,
+    const float *__restrict__ quats_raw, const float *__restrict__ opac,
+    float *__restrict__ grad_log_scales, float *__restrict__ grad_quats_raw,
+    float *__restrict__ grad_logits) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    Activated a;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) a.s[c] = scales[3 * i + c];
+    a.qraw = reinterpret_cast<const float4 *>(quats_raw)[i];
+    a.qn = sqrtf(a.qraw.x * a.qraw.x + a.qraw.y * a.qraw.y + a.qraw.z * a.qraw.z +
+                 a.qraw.w * a.qraw.w);
+    a.o = opac[i];
+    float gs[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) gs[c] = grad_scales ? grad_scales[3 * i + c] : 0.0f;
+    const float4 g = grad_quats ? reinterpret_cast<const float4 *>(grad_quats)[i]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    float g_ls[3], g_logit;
+    float4 g_qr;
+    activate_backward_one(a, gs, g, grad_opac ? grad_opac[i] : 0.0f, g_ls, g_qr, g_logit);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) grad_log_scales[3 * i + c] = grad_scales ? g_ls[c] : 0.0f;
+    reinterpret_cast<float4 *>(grad_quats_raw)[i] = g_qr;
+    grad_logits[i] = grad_opac ? g_logit : 0.0f;
+}
+
+// --------------------------------------------- fused preprocess (training step)
+// For the library's training step: activations, projection and the render()
+// colour of one Gaussian per thread in one pass over its parameters, and the
+// gradients of all three in one pass back.  Values equal the unfused sequence
+// activate -> project_points -> SH (render) and SH backward -> project_points
+// backward -> activate backward (the same device functions in the same order);
+// the forward does not store scales and unit quaternions, the backward
+// recomputes them from the raw parameters.
+
+__global__ __launch_bounds__(kShBlock) void preprocess_forward_kernel(
+    int64_t n, const float *__restrict__ means, const float *__restrict__ log_scales,
+    const float *__restrict__ quats_raw, const float *__restrict__ logits,
+    const float *__restrict__ sh_dc, const float *__restrict__ sh_rest,
+    const float *__restrict__ w2c, const float *__restrict__ K, float near_plane,
+    float far_plane, float min_opacity, float min_radius, float max_radius, int width,
+    int height, float *__restrict__ points_image, float *__restrict__ depths,
+    float *__restrict__ cov_image, float *__restrict__ cov_inv_image,
+    float *__restrict__ radii, uint8_t *__restrict__ mask, float *__restrict__ opacities,
+    float *__restrict__ colors) {
+    const int64_t i = (int64_t)blockIdx.x * kShBlock + threadIdx.x;
+    if (i >= n) return;
+    const Activated a = activate_one(log_scales, quats_raw, logits, i);
+    const Camera cam = load_camera(w2c, K, width, height);
+    const Projection p = project_gaussian(
+        cam, means[3 * i], means[3 * i + 1], means[3 * i + 2], a.s[0], a.s[1], a.s[2], a.q[0],
+        a.q[1], a.q[2], a.q[3], a.o, near_plane, far_plane, min_opacity, min_radius, max_radius,
+        width, height);
+    points_image[2 * i] = p.u;
+    points_image[2 * i + 1] = p.v;
+    depths[i] = p.keep ? p.zc : 0.0f;
+    cov_image[3 * i] = p.a;
+    cov_image[3 * i + 1] = p.b;
+    cov_image[3 * i + 2] = p.c;
+    cov_inv_image[3 * i] = p.A;
+    cov_inv_image[3 * i + 1] = p.B;
+    cov_inv_image[3 * i + 2] = p.C;
+    radii[2 * i] = p.ru;
+    radii[2 * i + 1] = p.rv;
+    mask[i] = p.keep ? 1 : 0;
+    opacities[i] = a.o;
+    float rgb[3] = {0.f, 0.f, 0.f};
+    if (p.keep) {
+        float cx, cy, cz;
+        camera_position(nullptr, w2c, cx, cy, cz);
+        const ShView v = sh_view(means + 3 * i, cx, cy, cz);
+        const float *rest = sh_rest + kRest * i;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) rgb[c] = sh_raw_channel(v, sh_dc + 3 * i, rest, c);
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) colors[3 * i + c] = sh_render_value(rgb[c]);
+}
+
+__global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
+    int64_t n, const float *__restrict__ grad_points_image,
+    const float *__restrict__ grad_cov_inv, const float *__restrict__ grad_opac,
+    const float *__restrict__ grad_colors, const float *__restrict__ means,
+    const float *__restrict__ log_scales, const float *__restrict__ quats_raw,
+    const float *__restrict__ logits, const float *__restrict__ sh_dc,
+    const float *__restrict__ sh_rest, const float *__restrict__ cov_image,
+    const uint8_t *__restrict__ mask, const float *__restrict__ w2c,
+    const float *__restrict__ K, int width, int height, float *__restrict__ grad_means,
+    float *__restrict__ grad_log_scales, float *__restrict__ grad_quats_raw,
+    float *__restrict__ grad_logits, float *__restrict__ grad_dc,
+    float *__restrict__ grad_rest) {
+    __shared__ __align__(16) float rest_lds[kShBlock * kRest];
+    const int64_t first = (int64_t)blockIdx.x * kShBlock;
+    const int nb = (int)min((int64_t)kShBlock, n - first);
+    block_copy<true>(rest_lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb);
+    __syncthreads();
+    const int t = threadIdx.x;
+    float *lrest = rest_lds + kRest * t;
+    if (t < nb) {
+        const int64_t i = first + t;
+        const Activated a = activate_one(log_scales, quats_raw, logits, i);
+        float gp[3] = {0.f, 0.f, 0.f}, gs[3] = {0.f, 0.f, 0.f}, gq[4] = {0.f, 0.f, 0.f, 0.f};
+        float gm[3] = {0.f, 0.f, 0.f}, gdc[3] = {0.f, 0.f, 0.f};
+        if (mask[i]) {
+            const Camera cam = load_camera(w2c, K, width, height);
+            project_gaussian_backward(
+                cam, means[3 * i], means[3 * i + 1], means[3 * i + 2], a.s[0], a.s[1], a.s[2],
+                a.q[0], a.q[1], a.q[2], a.q[3], cov_image[3 * i], cov_image[3 * i + 1],
+                cov_image[3 * i + 2], grad_points_image[2 * i], grad_points_image[2 * i + 1],
+                grad_cov_inv[3 * i], grad_cov_inv[3 * i + 1], grad_cov_inv[3 * i + 2], gp[0],
+                gp[1], gp[2], gs[0], gs[1], gs[2], gq[0], gq[1], gq[2], gq[3]);
+            float cx, cy, cz;
+            camera_position(nullptr, w2c, cx, cy, cz);
+            const ShView v = sh_view(means + 3 * i, cx, cy, cz);
+            float g[3];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                g[c] = grad_colors[3 * i + c];
+                const float raw = sh_raw_channel(v, sh_dc + 3 * i, lrest, c);
+                if (!(raw + 0.5f >= 0.0f)) g[c] = 0.0f;
+            }
+            sh_backward_row(v, g, lrest, gdc, gm);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kRest; ++k) lrest[k] = 0.0f;
+        }
+        float g_ls[3], g_logit;
+        float4 g_qr;
+        activate_backward_one(a, gs, make_float4(gq[0], gq[1], gq[2], gq[3]), grad_opac[i], g_ls,
+                              g_qr, g_logit);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            grad_means[3 * i + c] = gp[c] + gm[c];
+            grad_dc[3 * i + c] = gdc[c];
+            grad_log_scales[3 * i + c] = g_ls[c];
+        }
+        reinterpret_cast<float4 *>(grad_quats_raw)[i] = g_qr;
+        grad_logits[i] = g_logit;
     }
     __syncthreads();
     block_copy<false>(rest_lds, grad_rest + kRest * first, kRest * nb);
@@ -373,59 +611,6 @@ extern "C" int gs_evaluate_sh_render_backward(const float *grad_colors,
                               grad_sh_dc, grad_sh_rest, stream);
 }
 
-// ------------------------------------------------------------- activations
-// scripts/train.py:135-143: scales = exp(log_scales), quats = q / max(|q|, 1e-12),
-// opacities = sigmoid(logits).  One thread per Gaussian.
-
-__global__ __launch_bounds__(256) void activate_kernel(int64_t n,
-                                                      const float *__restrict__ log_scales,
-                                                      const float *__restrict__ quats_raw,
-                                                      const float *__restrict__ logits,
-                                                      float *__restrict__ scales,
-                                                      float *__restrict__ quats,
-                                                      float *__restrict__ opac) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-#pragma unroll
-    for (int c = 0; c < 3; ++c) scales[3 * i + c] = expf(log_scales[3 * i + c]);
-    const float4 q = reinterpret_cast<const float4 *>(quats_raw)[i];
-    const float norm = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
-    const float r = norm < 1e-12f ? 1e-12f : norm;  // clamp_min(1e-12)
-    reinterpret_cast<float4 *>(quats)[i] = make_float4(q.x / r, q.y / r, q.z / r, q.w / r);
-    opac[i] = 1.0f / (1.0f + expf(-logits[i]));
-}
-
-// Gradients of activate_kernel's outputs mapped to its inputs; a null gradient
-// input counts as zero.
-__global__ __launch_bounds__(256) void activate_backward_kernel(
-    int64_t n, const float *__restrict__ grad_scales, const float *__restrict__ grad_quats,
-    const float *__restrict__ grad_opac, const float *__restrict__ scales,
-    const float *__restrict__ quats_raw, const float *__restrict__ opac,
-    float *__restrict__ grad_log_scales, float *__restrict__ grad_quats_raw,
-    float *__restrict__ grad_logits) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-#pragma unroll
-    for (int c = 0; c < 3; ++c)
-        grad_log_scales[3 * i + c] = grad_scales ? grad_scales[3 * i + c] * scales[3 * i + c] : 0.0f;
-    const float4 q = reinterpret_cast<const float4 *>(quats_raw)[i];
-    float4 g = grad_quats ? reinterpret_cast<const float4 *>(grad_quats)[i]
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float norm = sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
-    float4 out;
-    if (norm < 1e-12f) {  // the clamp holds the divisor constant
-        out = make_float4(g.x / 1e-12f, g.y / 1e-12f, g.z / 1e-12f, g.w / 1e-12f);
-    } else {  // d(q/|q|) = (g - qhat (qhat . g)) / |q|
-        const float hx = q.x / norm, hy = q.y / norm, hz = q.z / norm, hw = q.w / norm;
-        const float dot = hx * g.x + hy * g.y + hz * g.z + hw * g.w;
-        out = make_float4((g.x - hx * dot) / norm, (g.y - hy * dot) / norm,
-                          (g.z - hz * dot) / norm, (g.w - hw * dot) / norm);
-    }
-    reinterpret_cast<float4 *>(grad_quats_raw)[i] = out;
-    const float o = opac[i];
-    grad_logits[i] = grad_opac ? grad_opac[i] * (o * (1.0f - o)) : 0.0f;
-}
-
 extern "C" int gs_activate(const float *log_scales, const float *quats_raw,
                            const float *opacity_logits, int64_t n, float *scales, float *quats,
                            float *opacities, hipStream_t stream) {
@@ -454,5 +639,56 @@ extern "C" int gs_activate_backward(const float *grad_scales, const float *grad_
     hipLaunchKernelGGL(activate_backward_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream, n,
                        grad_scales, grad_quats, grad_opacities, scales, quats_raw, opacities,
                        grad_log_scales, grad_quats_raw, grad_opacity_logits);
+    return launch_status();
+}
+
+extern "C" int gs_preprocess_forward(const float *means, const float *log_scales,
+                                     const float *quats_raw, const float *opacity_logits,
+                                     const float *sh_dc, const float *sh_rest,
+                                     const float *world_to_camera, const float *intrinsic,
+                                     int64_t n, float near_plane, float far_plane,
+                                     float min_opacity, float min_radius, float max_radius,
+                                     int32_t width, int32_t height, float *points_image,
+                                     float *depths, float *cov_image, float *cov_inv_image,
+                                     float *radii, uint8_t *mask, float *opacities,
+                                     float *colors, hipStream_t stream) {
+    if (n < 0 || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GS_OK;
+    if (!means || !log_scales || !quats_raw || !opacity_logits || !sh_dc || !sh_rest ||
+        !world_to_camera || !intrinsic || !points_image || !depths || !cov_image ||
+        !cov_inv_image || !radii || !mask || !opacities || !colors ||
+        (reinterpret_cast<uintptr_t>(quats_raw) & 15))
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(preprocess_forward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
+                       stream, n, means, log_scales, quats_raw, opacity_logits, sh_dc, sh_rest,
+                       world_to_camera, intrinsic, near_plane, far_plane, min_opacity,
+                       min_radius, max_radius, width, height, points_image, depths, cov_image,
+                       cov_inv_image, radii, mask, opacities, colors);
+    return launch_status();
+}
+
+extern "C" int gs_preprocess_backward(
+    const float *grad_points_image, const float *grad_cov_inv_image,
+    const float *grad_opacities, const float *grad_colors, const float *means,
+    const float *log_scales, const float *quats_raw, const float *opacity_logits,
+    const float *sh_dc, const float *sh_rest, const float *cov_image, const uint8_t *mask,
+    const float *world_to_camera, const float *intrinsic, int64_t n, int32_t width,
+    int32_t height, float *grad_means, float *grad_log_scales, float *grad_quats_raw,
+    float *grad_opacity_logits, float *grad_sh_dc, float *grad_sh_rest, hipStream_t stream) {
+    if (n < 0 || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GS_OK;
+    if (!grad_points_image || !grad_cov_inv_image || !grad_opacities || !grad_colors || !means ||
+        !log_scales || !quats_raw || !opacity_logits || !sh_dc || !sh_rest || !cov_image ||
+        !mask || !world_to_camera || !intrinsic || !grad_means || !grad_log_scales ||
+        !grad_quats_raw || !grad_opacity_logits || !grad_sh_dc || !grad_sh_rest ||
+        (reinterpret_cast<uintptr_t>(quats_raw) & 15) ||
+        (reinterpret_cast<uintptr_t>(grad_quats_raw) & 15))
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(preprocess_backward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
+                       stream, n, grad_points_image, grad_cov_inv_image, grad_opacities,
+                       grad_colors, means, log_scales, quats_raw, opacity_logits, sh_dc, sh_rest,
+                       cov_image, mask, world_to_camera, intrinsic, width, height, grad_means,
+                       grad_log_scales, grad_quats_raw, grad_opacity_logits, grad_sh_dc,
+                       grad_sh_rest);
     return launch_status();
 }

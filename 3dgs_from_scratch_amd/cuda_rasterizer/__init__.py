@@ -46,6 +46,8 @@ __all__ = [
     "rasterize_display_backward",
     "activate",
     "activate_backward",
+    "preprocess_forward",
+    "preprocess_backward",
     "rasterize_display_l1",
     "rasterize_l1_backward",
     "RasterizerError",
@@ -623,6 +625,77 @@ def activate_backward(grad_scales, grad_quats, grad_opacities, scales, quats_raw
             _ptr(g_ls), _ptr(g_q), _ptr(g_l), _stream(dev)), "activate_backward")
         _lib.timer.stop(ev, dev)
     return g_ls, g_q, g_l
+
+
+def preprocess_forward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
+                       sh_coeffs_rest, world_to_camera, intrinsic, near_plane, far_plane,
+                       min_opacity, min_radius, max_radius, width, height):
+    """activate -> project_points -> evaluate_spherical_harmonics_render in one kernel
+    (gs_preprocess_forward).  Returns (points_image, depths, cov_image, cov_inv_image,
+    radii, mask, opacities, colors)."""
+    dev = _device_of(means)
+    n = means.shape[0]
+    f32 = torch.float32
+    means = _prep(means, "means", f32, (n, 3), dev)
+    log_scales = _prep(log_scales, "log_scales", f32, (n, 3), dev)
+    quats_raw = _prep(quats_raw, "quats_raw", f32, (n, 4), dev)
+    opacity_logits = _prep(opacity_logits, "opacity_logits", f32, (n,), dev)
+    dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+    rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
+    intrinsic = _prep(intrinsic, "intrinsic", f32, (3, 3), dev)
+    out = [torch.empty(shape, dtype=f32, device=dev)
+           for shape in ((n, 2), (n,), (n, 3), (n, 3), (n, 2))]
+    mask = torch.empty((n,), dtype=torch.bool, device=dev)
+    opac = torch.empty((n,), dtype=f32, device=dev)
+    colors = torch.empty((n, 3), dtype=f32, device=dev)
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("preprocess_forward", dev)
+        _lib.check(_lib.load().gs_preprocess_forward(
+            _ptr(means), _ptr(log_scales), _ptr(quats_raw), _ptr(opacity_logits), _ptr(dc),
+            _ptr(rest), _ptr(world_to_camera), _ptr(intrinsic), n, float(near_plane),
+            float(far_plane), float(min_opacity), float(min_radius), float(max_radius), int(width),
+            int(height), *[_ptr(t) for t in out], _ptr(mask), _ptr(opac), _ptr(colors),
+            _stream(dev)), "preprocess_forward")
+        _lib.timer.stop(ev, dev)
+    return (*out, mask, opac, colors)
+
+
+def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors,
+                        means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
+                        sh_coeffs_rest, cov_image, mask, world_to_camera, intrinsic, width,
+                        height):
+    """Gradients of preprocess_forward's points_image, cov_inv_image, opacities and
+    colors w.r.t. the raw parameters (gs_preprocess_backward).  Returns (d means,
+    d log_scales, d quats_raw, d logits, d sh_dc, d sh_rest)."""
+    dev = _device_of(means)
+    n = means.shape[0]
+    f32 = torch.float32
+    g_pts = _prep(grad_points_image, "grad_points_image", f32, (n, 2), dev)
+    g_conic = _prep(grad_cov_inv_image, "grad_cov_inv_image", f32, (n, 3), dev)
+    g_opac = _prep(grad_opacities, "grad_opacities", f32, (n,), dev)
+    g_col = _prep(grad_colors, "grad_colors", f32, (n, 3), dev)
+    means = _prep(means, "means", f32, (n, 3), dev)
+    log_scales = _prep(log_scales, "log_scales", f32, (n, 3), dev)
+    quats_raw = _prep(quats_raw, "quats_raw", f32, (n, 4), dev)
+    opacity_logits = _prep(opacity_logits, "opacity_logits", f32, (n,), dev)
+    dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+    rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    cov_image = _prep(cov_image, "cov_image", f32, (n, 3), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
+    intrinsic = _prep(intrinsic, "intrinsic", f32, (3, 3), dev)
+    outs = [torch.empty(shape, dtype=f32, device=dev)
+            for shape in ((n, 3), (n, 3), (n, 4), (n,), (n, 3), (n, 15, 3))]
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("preprocess_backward", dev)
+        _lib.check(_lib.load().gs_preprocess_backward(
+            _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), _ptr(means), _ptr(log_scales),
+            _ptr(quats_raw), _ptr(opacity_logits), _ptr(dc), _ptr(rest), _ptr(cov_image),
+            _ptr(mask), _ptr(world_to_camera), _ptr(intrinsic), n, int(width), int(height),
+            *[_ptr(t) for t in outs], _stream(dev)), "preprocess_backward")
+        _lib.timer.stop(ev, dev)
+    return tuple(outs)
 
 
 def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,

@@ -6,11 +6,11 @@ and computes an L1 loss on the /255 image (:187-191); autograd then runs
 separate PyTorch kernels for each of those steps.  `render_l1` computes the
 same values with the library's kernels only:
 
-  forward   activate -> project_points -> SH (+0.5, clamp) -> binning ->
-            blend (image, display, per-tile L1 sums) -> loss
-  backward  blend backward seeded by the L1 gradient -> project_points
-            backward -> SH backward (adding into the means gradient) ->
-            activation backward
+  forward   preprocess (activations, projection, SH +0.5 and clamp: one
+            kernel) -> binning -> blend (image, display, per-tile L1 sums) ->
+            loss
+  backward  blend backward seeded by the L1 gradient -> preprocess backward
+            (projection, SH and activation gradients: one kernel)
 
 Values equal the unfused sequence up to floating-point summation order (the
 loss sum and the gradient atomics); tests/test_gpu_fused.py checks both
@@ -35,19 +35,17 @@ class RenderL1Function(torch.autograd.Function):
                 world_to_camera, intrinsic, target, densifier, width, height, near_plane,
                 far_plane, min_opacity, min_radius, max_radius, alpha_threshold,
                 transmittance_threshold, chi_squared_threshold):
-        scales, quats, opac = _cr.activate(log_scales, quats_raw, opacity_logits)
-        pts, depths, cov, conic, radii, mask = _cr.project_points(
-            means, scales, quats, opac, world_to_camera, intrinsic, near_plane, far_plane,
-            min_opacity, min_radius, max_radius, width, height)
-        colors = _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_coeffs_dc,
-                                                         sh_coeffs_rest, mask)
+        pts, depths, cov, conic, radii, mask, opac, colors = _cr.preprocess_forward(
+            means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
+            world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
+            max_radius, width, height)
         off, ids = _cr.compute_tile_intersection(pts, radii, depths, mask, width, height, 16)
         image, display, loss = _cr.rasterize_display_l1(
             off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
             transmittance_threshold, chi_squared_threshold)
-        ctx.save_for_backward(means, quats_raw, sh_coeffs_dc, sh_coeffs_rest, world_to_camera,
-                              intrinsic, target, scales, quats, opac, pts, cov, conic, mask,
-                              colors, off, ids, image)
+        ctx.save_for_backward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
+                              sh_coeffs_rest, world_to_camera, intrinsic, target, opac, pts, cov,
+                              conic, mask, colors, off, ids, image)
         ctx.densifier = densifier
         ctx.radii = radii if densifier is not None else None
         ctx.params = (width, height, alpha_threshold, transmittance_threshold,
@@ -58,8 +56,8 @@ class RenderL1Function(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_loss, grad_display, grad_pts, grad_radii):
-        (means, quats_raw, dc, rest, w2c, K, target, scales, quats, opac, pts, cov, conic, mask,
-         colors, off, ids, image) = ctx.saved_tensors
+        (means, log_scales, quats_raw, logits, dc, rest, w2c, K, target, opac, pts, cov, conic,
+         mask, colors, off, ids, image) = ctx.saved_tensors
         width, height, a_thr, t_thr, chi = ctx.params
         if grad_loss is None:
             return (None,) * 20
@@ -68,12 +66,9 @@ class RenderL1Function(torch.autograd.Function):
             width, height, image, a_thr, t_thr, chi)
         if ctx.densifier is not None:
             ctx.densifier.update(g_pts, ctx.radii, width, height)
-        g_means, g_scales, g_quats = _cr.project_points_backward(
-            g_pts, g_conic, means, scales, quats, opac, w2c, K, width, height, cov, mask)
-        _, g_dc, g_rest = _cr.evaluate_spherical_harmonics_render_backward(
-            g_col, w2c, means, dc, rest, mask, accumulate_means=g_means)
-        g_ls, g_qr, g_logit = _cr.activate_backward(g_scales, g_quats, g_opac, scales, quats_raw,
-                                                    opac)
+        g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(
+            g_pts, g_conic, g_opac, g_col, means, log_scales, quats_raw, logits, dc, rest, cov,
+            mask, w2c, K, width, height)
         return (g_means, g_ls, g_qr, g_logit, g_dc, g_rest) + (None,) * 14
 
 

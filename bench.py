@@ -412,7 +412,8 @@ BLEND_FLOP_PER_PAIR = {"rasterize": 22.0, "rasterize_backward": 70.0, "rasterize
                        "rasterize_l1_backward": 70.0}
 HBM_STAGES = ("activate", "project_points", "evaluate_sh", "evaluate_sh_render", "bin_count",
               "bin_sort", "evaluate_sh_backward", "evaluate_sh_render_backward",
-              "project_points_backward", "activate_backward")
+              "project_points_backward", "activate_backward", "preprocess_forward",
+              "preprocess_backward")
 
 
 def sort_passes(n_tiles: int) -> int:
@@ -456,6 +457,11 @@ def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> floa
         return 12 * hw + k * 76 + 36 * n
     if stage == "rasterize_l1_backward":  # image + target read instead of a gradient image
         return 24 * hw + k * 76 + 36 * n
+    if stage == "preprocess_forward":  # raw parameters + SH -> projection, opacity, colours
+        return n * (12 + 12 + 16 + 4 + 12 + 180) + n * (8 + 4 + 12 + 12 + 8 + 1 + 4 + 12)
+    if stage == "preprocess_backward":  # 4 gradients, raw parameters, SH, cov, mask -> 6 gradients
+        return n * (8 + 12 + 4 + 12 + 12 + 12 + 16 + 4 + 12 + 180 + 12 + 1) + \
+            n * (12 + 12 + 16 + 4 + 12 + 180)
     if stage == "activate":  # log-scales, quaternions, logits -> scales, unit quaternions, opacity
         return n * (12 + 16 + 4) * 2
     if stage == "activate_backward":  # 3 gradients + scales, quaternions, opacity -> 3 gradients
@@ -476,7 +482,9 @@ STAGE_KERNEL = {"rasterize": "blend_forward_kernel", "rasterize_display": "blend
                 "evaluate_sh_render": "sh_forward_kernel",
                 "evaluate_sh_backward": "sh_backward_kernel",
                 "evaluate_sh_render_backward": "sh_backward_kernel",
-                "project_points_backward": "project_points_backward_kernel"}
+                "project_points_backward": "project_points_backward_kernel",
+                "preprocess_forward": "preprocess_forward_kernel",
+                "preprocess_backward": "preprocess_backward_kernel"}
 
 
 def profiled_traffic(stage: str, workload: str):

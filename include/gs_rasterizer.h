@@ -222,6 +222,36 @@ int gs_rasterize_display_backward(const float *grad_display, const float *image,
 /* ----------------------------------------------- fused training step */
 
 /*
+ * Fused preprocess of the library training step: activations
+ * (scripts/train.py:135-143), projection (as gs_project_points) and the
+ * render() colour max(SH + 0.5, 0) (as gs_evaluate_sh_render) in one pass over
+ * each Gaussian's raw parameters; opacities receives sigmoid(logits) for the
+ * blend.  gs_preprocess_backward takes the gradients of points_image,
+ * cov_inv_image, opacities and colors and writes those of the raw parameters
+ * (means, log-scales, raw quaternions, logits, SH dc and rest), recomputing the
+ * activations.  Each equals the unfused sequence of the entries it replaces.
+ * No counterpart in the reference extension (it leaves activations to PyTorch).
+ * quats_raw and grad_quats_raw must be 16-byte aligned.
+ */
+int gs_preprocess_forward(const float *means, const float *log_scales, const float *quats_raw,
+                          const float *opacity_logits, const float *sh_dc, const float *sh_rest,
+                          const float *world_to_camera, const float *intrinsic, int64_t n,
+                          float near_plane, float far_plane, float min_opacity, float min_radius,
+                          float max_radius, int32_t width, int32_t height, float *points_image,
+                          float *depths, float *cov_image, float *cov_inv_image, float *radii,
+                          uint8_t *mask, float *opacities, float *colors, hipStream_t stream);
+int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov_inv_image,
+                           const float *grad_opacities, const float *grad_colors,
+                           const float *means, const float *log_scales, const float *quats_raw,
+                           const float *opacity_logits, const float *sh_dc, const float *sh_rest,
+                           const float *cov_image, const uint8_t *mask,
+                           const float *world_to_camera, const float *intrinsic, int64_t n,
+                           int32_t width, int32_t height, float *grad_means,
+                           float *grad_log_scales, float *grad_quats_raw,
+                           float *grad_opacity_logits, float *grad_sh_dc, float *grad_sh_rest,
+                           hipStream_t stream);
+
+/*
  * The caller-side glue of a training step (scripts/train.py:135-143,187-191),
  * fused: no counterpart in the reference extension.
  *

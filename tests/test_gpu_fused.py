@@ -56,6 +56,41 @@ def test_activate_matches_torch(gpu):
     assert helpers.rel_l2(g_l, leaves[2].grad) <= 1e-5
 
 
+def test_fused_preprocess_equals_unfused_sequence(gpu):
+    """gs_preprocess_forward/backward run the same device functions in the same
+    order as activate -> project -> SH render and their backward: bit-equal."""
+    p, cam, _ = helpers.scene_orbit(6_000, 160, 120, 220.0, seed=31)
+    g = torch.Generator().manual_seed(32)
+    n = p["means"].shape[0]
+    dev = gpu
+    w2c, K = cam["w2c"].to(dev), cam["K"].to(dev)
+    W, H = cam["width"], cam["height"]
+    raw = {k: v.to(dev) for k, v in p.items()}
+    raw["quats_raw"][5] = 0.0  # the clamp_min(1e-12) branch
+    args = (0.01, 100.0, 1 / 255, 0.5, 128.0, W, H)
+    fwd = cr.preprocess_forward(raw["means"], raw["log_scales"], raw["quats_raw"],
+                                raw["opacity_logits"], raw["sh_dc"], raw["sh_rest"], w2c, K, *args)
+    s, q, o = cr.activate(raw["log_scales"], raw["quats_raw"], raw["opacity_logits"])
+    ref = cr.project_points(raw["means"], s, q, o, w2c, K, *args)
+    col = cr.evaluate_spherical_harmonics_render(w2c, raw["means"], raw["sh_dc"], raw["sh_rest"],
+                                                 ref[5])
+    for a, b in zip(fwd[:6], ref):
+        assert torch.equal(a, b)
+    assert torch.equal(fwd[6], o) and torch.equal(fwd[7], col)
+    assert 0 < int(ref[5].sum()) < n
+    ups = [torch.randn(shape, generator=g).to(dev) for shape in ((n, 2), (n, 3), (n,), (n, 3))]
+    got = cr.preprocess_backward(*ups, raw["means"], raw["log_scales"], raw["quats_raw"],
+                                 raw["opacity_logits"], raw["sh_dc"], raw["sh_rest"], ref[2],
+                                 ref[5], w2c, K, W, H)
+    gm, gsc, gq = cr.project_points_backward(ups[0], ups[1], raw["means"], s, q, o, w2c, K, W, H,
+                                             ref[2], ref[5])
+    _, gdc, grest = cr.evaluate_spherical_harmonics_render_backward(
+        ups[3], w2c, raw["means"], raw["sh_dc"], raw["sh_rest"], ref[5], accumulate_means=gm)
+    gls, gqr, glog = cr.activate_backward(gsc, gq, ups[2], s, raw["quats_raw"], o)
+    for a, b in zip(got, (gm, gls, gqr, glog, gdc, grest)):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("scene", ["orbit", "box"])
 def test_render_l1_matches_drop_in_path(gpu, scene):
     if scene == "orbit":
