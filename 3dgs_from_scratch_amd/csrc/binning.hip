@@ -11,9 +11,11 @@
 //   2. gs_bin_sort level 1: one (supertile, Gaussian) entry per touched
 //      supertile, in depth order, stably sorted by supertile id -> for every
 //      supertile, the Gaussians meeting it in depth order (M << K entries).
-//   3. gs_bin_sort level 2: each supertile list is cut into 256-entry chunks;
-//      one ballot per local tile counts, then writes, the chunk's Gaussians
-//      covering that tile straight to their final positions.
+//   3. gs_bin_sort level 2: each supertile list is cut into 512-entry blocks;
+//      per wave, 8 row and 8 column ballots give every local tile's count,
+//      one workgroup per supertile scans the counts over its blocks (and the
+//      tile offsets over the grid), and each block then writes its Gaussians
+//      covering each tile straight to their final positions.
 // Every stage is stable, so each tile's run is in depth order with ties in
 // Gaussian index order.
 //
