@@ -151,13 +151,15 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t key, int shift, uint32_t d
     return (key >> shift) & dmask;
 }
 
-template <int ITEMS>
+// kPayload: each value carries an 8-byte payload (a packed tile rectangle).
+template <int ITEMS, bool kPayload = false>
 struct SortLds {
     uint32_t wave_count[kSortWaves][kRadixMax];
     uint32_t global_start[kRadixMax];
     uint32_t local_start[kRadixMax];
     uint32_t skeys[kSortThreads * ITEMS];
     uint32_t svals[kSortThreads * ITEMS];
+    uint2 spay[kPayload ? kSortThreads * ITEMS : 1];
     uint32_t scan_tmp[kSortThreads / kWave + 1];
 };
 
@@ -213,21 +215,23 @@ __global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
 }
 
 // Stable rank of the block's keys (registers) by digit, staged through LDS in
-// digit order and written to keys_out/vals_out.  `table` holds the position of
-// each (digit, block) among the keys of its digit, `totals` the keys per digit.
-// When counts_out is set,
-// counts_out[dst] = touched[value] is written as well.
-template <typename KeyT, int ITEMS>
+// digit order and written to keys_out/vals_out (and, with kPayload, the
+// payloads to pay_out).  `table` holds the position of each (digit, block)
+// among the keys of its digit, `totals` the keys per digit.  When counts_out
+// is set, counts_out[dst] = touched[value] is written as well.
+template <typename KeyT, int ITEMS, bool kPayload>
 __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               const uint32_t (&v)[ITEMS],
+                                              const uint2 (&pay)[ITEMS],
                                               const bool (&valid)[ITEMS], int shift, int nbits,
                                               int nblocks, const uint32_t *__restrict__ table,
                                               KeyT *__restrict__ keys_out,
-                                              uint32_t *__restrict__ vals_out, int64_t n,
-                                              bool write_keys, SortLds<ITEMS> &s,
+                                              uint32_t *__restrict__ vals_out,
+                                              uint2 *__restrict__ pay_out, int64_t n,
+                                              bool write_keys, SortLds<ITEMS, kPayload> &s,
                                               const uint32_t *__restrict__ totals,
-                                              const uint32_t *__restrict__ touched = nullptr,
-                                              uint64_t *__restrict__ counts_out = nullptr) {
+                                              const uint32_t *__restrict__ touched,
+                                              uint64_t *__restrict__ counts_out) {
     const int radix = 1 << nbits;
     const uint32_t dmask = (uint32_t)radix - 1u;
     const int wave = threadIdx.x / kWave;
@@ -276,6 +280,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
             const uint32_t p = s.local_start[d] + s.wave_count[wave][d] + rank[it];
             s.skeys[p] = k[it];
             s.svals[p] = v[it];
+            if (kPayload) s.spay[p] = pay[it];
         }
     }
     __syncthreads();
@@ -287,6 +292,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
             const uint32_t val = s.svals[p];
             if (write_keys) keys_out[dst] = (KeyT)key;
             vals_out[dst] = val;
+            if (kPayload) pay_out[dst] = s.spay[p];
             if (counts_out) counts_out[dst] = val < (uint64_t)n ? touched[val] : 0u;
         }
     }
@@ -316,16 +322,18 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
         hist[hist_index(d, blockIdx.x, nblocks)] = counts[d];
 }
 
-template <typename KeyT, int ITEMS>
+template <typename KeyT, int ITEMS, bool kPayload>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     const KeyT *__restrict__ keys_in, const uint32_t *__restrict__ vals_in,
-    KeyT *__restrict__ keys_out, uint32_t *__restrict__ vals_out, int64_t n, int shift,
+    const uint2 *__restrict__ pay_in, KeyT *__restrict__ keys_out,
+    uint32_t *__restrict__ vals_out, uint2 *__restrict__ pay_out, int64_t n, int shift,
     int nbits, int nblocks, const uint32_t *__restrict__ table,
     const uint32_t *__restrict__ totals, int write_keys, const uint32_t *__restrict__ touched,
     uint64_t *__restrict__ counts_out) {
-    __shared__ SortLds<ITEMS> s;
+    __shared__ SortLds<ITEMS, kPayload> s;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS], v[ITEMS];
+    uint2 pay[ITEMS];
     bool valid[ITEMS];
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
@@ -333,9 +341,11 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
         valid[it] = i < n;
         k[it] = valid[it] ? (uint32_t)keys_in[i] : 0u;
         v[it] = valid[it] ? vals_in[i] : 0u;
+        pay[it] = (kPayload && valid[it]) ? pay_in[i] : make_uint2(0u, 0u);
     }
-    block_scatter<KeyT, ITEMS>(k, v, valid, shift, nbits, nblocks, table, keys_out, vals_out, n,
-                               write_keys != 0, s, totals, touched, counts_out);
+    block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, shift, nbits, nblocks, table, keys_out,
+                                         vals_out, pay_out, n, write_keys != 0, s, totals,
+                                         touched, counts_out);
 }
 
 struct SortPlan {
@@ -382,11 +392,12 @@ uint32_t *radix_totals(void *ws, int64_t n) {
 // One LSD pass from arrays: histogram (unless the caller already wrote this
 // pass's table: hist_ready), digit scan, scatter.  With counts_out, counts_out[dst] = touched[value] is written next to
 // the values.
-template <typename KeyT, int ITEMS>
+template <typename KeyT, int ITEMS, bool kPayload = false>
 int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout, int64_t n,
                int shift, int nbits, bool write_keys, void *ws, hipStream_t stream,
                bool hist_ready = false, const uint32_t *touched = nullptr,
-               uint64_t *counts_out = nullptr) {
+               uint64_t *counts_out = nullptr, const uint2 *pin = nullptr,
+               uint2 *pout = nullptr) {
     const int nblocks = (int)sort_blocks<ITEMS>(n);
     uint32_t *hist = reinterpret_cast<uint32_t *>(ws);
     uint32_t *totals = radix_totals<ITEMS>(ws, n);
@@ -401,9 +412,10 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
                        nblocks, totals);
     st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS>), dim3(nblocks), dim3(kSortThreads),
-                       0, stream, kin, vin, kout, vout, n, shift, nbits, nblocks, hist,
-                       (const uint32_t *)totals, write_keys ? 1 : 0, touched, counts_out);
+    hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, kPayload>), dim3(nblocks),
+                       dim3(kSortThreads), 0, stream, kin, vin, pin, kout, vout, pout, n, shift,
+                       nbits, nblocks, hist, (const uint32_t *)totals, write_keys ? 1 : 0,
+                       touched, counts_out);
     return launch_status();
 }
 
@@ -543,7 +555,7 @@ struct L2Args {
     const int32_t *super_ids;     // m: Gaussian ids per supertile, depth order
     const uint32_t *chunk_start;  // n_super + 1: first level-2 block of each supertile
     const uint2 *block_map;       // per level-2 block: (supertile, first list position)
-    const uint2 *rects;           // packed tile rectangle per Gaussian (count workspace)
+    const uint2 *super_rects;     // m: packed tile rectangle of each list entry
     int64_t n, m, k;
     int n_super, super_x, tiles_x, tiles_y, width, height, tile_size;
 };
@@ -596,12 +608,14 @@ struct L2Block {
 };
 
 // Bit j (= ly * kSuper + lx) set for every tile of supertile s that Gaussian
-// g's tile rectangle covers; the covered local rectangle goes to x.
-__device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int s, L2Block &x) {
+// g (list entry e, whose tile rectangle is super_rects[e]) covers; the covered
+// local rectangle goes to x.
+__device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int64_t e, int s,
+                                               L2Block &x) {
     x.lx0 = x.ly0 = 1;
     x.lx1 = x.ly1 = 0;
     if (g < 0 || (int64_t)g >= a.n) return 0;
-    const TileRect r = unpack_rect(a.rects[g]);  // Gaussians in the lists have tiles
+    const TileRect r = unpack_rect(a.super_rects[e]);  // Gaussians in the lists have tiles
     const int ox = (s % a.super_x) * kSuper, oy = (s / a.super_x) * kSuper;
     const int x0 = max(r.tx0 - ox, 0), x1 = min(r.tx1 - ox, kSuper - 1);
     const int y0 = max(r.ty0 - oy, 0), y1 = min(r.ty1 - oy, kSuper - 1);
@@ -629,7 +643,7 @@ __device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x) {
     x.mask = 0;
     if (e < end) {
         x.g = a.super_ids[e];
-        x.mask = local_mask(a, x.g, x.s, x);
+        x.mask = local_mask(a, x.g, e, x.s, x);
     } else {
         x.lx0 = x.ly0 = 1;
         x.lx1 = x.ly1 = 0;
@@ -790,7 +804,7 @@ __global__ __launch_bounds__(256) void emit_super_kernel(
     int64_t n, int64_t m, const uint32_t *__restrict__ order,
     const uint64_t *__restrict__ offsets, const uint32_t *__restrict__ super_touched,
     const uint2 *__restrict__ rects, int super_x, KeyT *__restrict__ keys_out,
-    uint32_t *__restrict__ vals_out) {
+    uint32_t *__restrict__ vals_out, uint2 *__restrict__ rects_out) {
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= n) return;
     const uint32_t g = order[r];
@@ -805,10 +819,10 @@ __global__ __launch_bounds__(256) void emit_super_kernel(
             if (o >= m) return;
             keys_out[o] = (KeyT)(y * super_x + x);
             vals_out[o] = g;
+            rects_out[o] = packed;
         }
 }
 
-// Number of level-2 chunks of each supertile list.
 // keys[i] = tile << 32 | depth bits of ids[i], the tile being the last one
 // whose offset is <= i (the reference's sorted 64-bit keys).
 __global__ __launch_bounds__(256) void keys_from_offsets_kernel(
@@ -879,6 +893,7 @@ inline bool use_u16_keys(int tile_bits) { return tile_bits <= 16; }
 struct SortWs {
     void *keys_a, *keys_b;  // supertile keys (u16 or u32)
     uint32_t *vals_tmp;
+    uint2 *rects_tmp;       // packed tile rectangle of each entry (payload of the sort)
     void *pass_ws;  // histogram table + digit totals of each pass
     size_t bytes;
 };
@@ -889,6 +904,7 @@ inline SortWs carve_sort(Carve &c, int64_t m, int super_bits) {
     w.keys_a = c.take<char>(m * kb);
     w.keys_b = c.take<char>(m * kb);
     w.vals_tmp = c.take<uint32_t>(m);
+    w.rects_tmp = c.take<uint2>(m);
     w.pass_ws = c.take<char>((int64_t)radix_workspace_bytes<kTileItems>(m));
     w.bytes = 0;
     return w;
@@ -924,6 +940,7 @@ struct BinWs {
     SortWs lvl1;
     int32_t *super_off;     // n_super (+1 spare)
     int32_t *super_ids;     // m
+    uint2 *super_rects;     // m: packed tile rectangle of each super_ids entry
     uint32_t *chunk_start;  // n_super + 1: first level-2 block of each supertile
     uint2 *block_map;       // level-2 block -> (supertile, first list position)
     uint32_t *table;        // level-2 blocks x 64 local tiles
@@ -938,6 +955,7 @@ inline BinWs carve_bins(void *base, int64_t m, const Grid &g) {
     w.lvl1 = carve_sort(c, m, g.super_bits);
     w.super_off = c.take<int32_t>((int64_t)g.n_super + 1);
     w.super_ids = c.take<int32_t>(m);
+    w.super_rects = c.take<uint2>(m);
     w.chunk_start = c.take<uint32_t>((int64_t)g.n_super + 1);
     w.block_map = c.take<uint2>(l2_blocks_bound(m, g.n_super));
     w.table = c.take<uint32_t>(l2_blocks_bound(m, g.n_super) * kSuperLocal);
@@ -957,24 +975,28 @@ inline int bits_for(int64_t max_value) {
 // supertile id; writes the per-supertile list starts and the sorted ids.
 template <typename KeyT>
 int super_sort(const EmitArgs &a, const SortWs &w, int super_bits, int n_super,
-               int32_t *super_off, int32_t *super_ids, hipStream_t stream) {
+               int32_t *super_off, int32_t *super_ids, uint2 *super_rects, hipStream_t stream) {
     const SortPlan plan = plan_sort(super_bits);
     const int P = plan.passes;
     KeyT *ka = reinterpret_cast<KeyT *>(w.keys_a), *kb = reinterpret_cast<KeyT *>(w.keys_b);
     uint32_t *out = reinterpret_cast<uint32_t *>(super_ids);
-    // pass p writes (kb, out) when P-1-p is even, (ka, vals_tmp) otherwise; the
-    // entries (pass -1) go to the other set than pass 0
+    // pass p writes (kb, out, super_rects) when P-1-p is even, (ka, vals_tmp,
+    // rects_tmp) otherwise; the entries (pass -1) go to the other set than pass 0.
+    // Each entry carries its Gaussian's packed tile rectangle, so that level 2
+    // reads it in list order.
     auto keys_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? kb : ka; };
     auto vals_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? out : w.vals_tmp; };
+    auto rects_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? super_rects : w.rects_tmp; };
     hipLaunchKernelGGL(emit_super_kernel<KeyT>, dim3(ceil_div(a.n, 256)), dim3(256), 0, stream,
                        a.n, a.k, a.order, a.offsets, a.touched, a.rects, a.tiles_x, keys_for(-1),
-                       vals_for(-1));
+                       vals_for(-1), rects_for(-1));
     int st = launch_status();
     if (st) return st;
     for (int p = 0; p < P; ++p) {
-        st = radix_pass<KeyT, kTileItems>(keys_for(p - 1), vals_for(p - 1), keys_for(p),
-                                          vals_for(p), a.k, p * plan.bits_per_pass,
-                                          pass_bits(plan, super_bits, p), true, w.pass_ws, stream);
+        st = radix_pass<KeyT, kTileItems, true>(
+            keys_for(p - 1), vals_for(p - 1), keys_for(p), vals_for(p), a.k,
+            p * plan.bits_per_pass, pass_bits(plan, super_bits, p), true, w.pass_ws, stream,
+            false, nullptr, nullptr, rects_for(p - 1), rects_for(p));
         if (st) return st;
     }
     hipLaunchKernelGGL(tile_ranges_kernel<KeyT>, dim3(ceil_div(n_super, 256)), dim3(256), 0,
@@ -1085,9 +1107,9 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
     a.tiles_x = g.super_x;
     st = use_u16_keys(g.super_bits)
              ? super_sort<uint16_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
-                                    w.super_ids, stream)
+                                    w.super_ids, w.super_rects, stream)
              : super_sort<uint32_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
-                                    w.super_ids, stream);
+                                    w.super_ids, w.super_rects, stream);
     if (st) return st;
 
     // level 2: block plan, per-tile counts, tile offsets and block prefixes, scatter
@@ -1102,7 +1124,7 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
     l2.super_ids = w.super_ids;
     l2.chunk_start = w.chunk_start;
     l2.block_map = w.block_map;
-    l2.rects = cw.rects;
+    l2.super_rects = w.super_rects;
     l2.n = n;
     l2.m = m;
     l2.k = k;
