@@ -765,6 +765,11 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
     }
 }
 
+// Writes each entry's Gaussian id at its final position: lane j of every wave
+// holds the first position of the wave's entries of local tile j, read back
+// with readlane in the loop over tiles.  k32: positions fit 32 bits (K < 2^30),
+// so a store is a 32-bit offset from the uniform base.
+template <bool k32>
 __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
                                                                 const uint32_t *__restrict__ table,
                                                                 int32_t *__restrict__ ids_out) {
@@ -785,14 +790,25 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
         }
     }
     __syncthreads();
-    const uint64_t below = lanemask_lt();
-#pragma unroll 4
+    const uint32_t my_base = base[wave][lane];  // lane j: tile j
+    const uint32_t mlo = (uint32_t)x.mask, mhi = (uint32_t)(x.mask >> 32);
+    const uint32_t k = (uint32_t)(a.k < 0xffffffffLL ? a.k : 0xffffffffLL);
+#pragma unroll
     for (int j = 0; j < kSuperLocal; ++j) {
-        const bool mine = (x.mask >> j) & 1ull;
+        const bool mine = ((j < 32 ? mlo >> j : mhi >> (j - 32)) & 1u) != 0u;
         const uint64_t bal = __ballot(mine);
-        if (mine) {
-            const uint32_t p = base[wave][j] + (uint32_t)__popcll(bal & below);
-            if ((int64_t)p < a.k) ids_out[p] = x.g;
+        const uint32_t b = __builtin_amdgcn_readlane(my_base, j);
+        if (mine) {  // + the lanes below this one that also cover tile j
+            const uint32_t p = b + __builtin_amdgcn_mbcnt_hi(
+                                       (uint32_t)(bal >> 32),
+                                       __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (k32) {  // byte offset p * 4 < 2^32: a 32-bit offset from the uniform base
+                if (p < k)
+                    *reinterpret_cast<int32_t *>(reinterpret_cast<char *>(ids_out) + (p << 2)) =
+                        x.g;
+            } else {
+                if ((int64_t)p < a.k) ids_out[(int64_t)p] = x.g;
+            }
         }
     }
 }
@@ -1149,8 +1165,12 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
                        w.tile_counts, g.n_tiles, fused_scan ? 1 : 0, indexing_offset, w.table);
     st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL(l2_scatter_kernel, dim3((unsigned)nb2), dim3(kL2Threads), 0, stream, l2,
-                       w.table, gaussian_ids_sorted);
+    if (k < (1LL << 30))
+        hipLaunchKernelGGL(l2_scatter_kernel<true>, dim3((unsigned)nb2), dim3(kL2Threads), 0,
+                           stream, l2, w.table, gaussian_ids_sorted);
+    else
+        hipLaunchKernelGGL(l2_scatter_kernel<false>, dim3((unsigned)nb2), dim3(kL2Threads), 0,
+                           stream, l2, w.table, gaussian_ids_sorted);
     st = launch_status();
     if (st) return st;
     if (sorted_keys) {
