@@ -97,7 +97,7 @@ __device__ __forceinline__ float conic_exponent(float A, float B2, float C, floa
 constexpr float kNegHalfLog2e = -0.72134752044448170f;
 struct BatchLds {
     float4 geo[kBatch];  // u, v, A, 2B
-    float4 aux[kBatch];  // C, opacity, strip mask, log2(opacity)
+    float4 aux[kBatch];  // C, 1 / opacity, strip mask, log2(opacity)
     float4 col[kBatch];  // r, g, b, (gaussian id bits)
 };
 
@@ -228,7 +228,7 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
     if (m != 0u) {
         const int slot = __popcll(keep & lanemask_lt());
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
-        s.aux[slot] = make_float4(r.C, r.o, __uint_as_float(m), log2o);
+        s.aux[slot] = make_float4(r.C, __builtin_amdgcn_rcpf(r.o), __uint_as_float(m), log2o);
         s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
     }
     Staged st;
@@ -547,10 +547,10 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
 }
 
 // Destination of the lane's field after wave_sum9:
-// out[stride * g] += value * (inv_o ? 1 / o : fa).
+// out[stride * g] += value * (inv_o ? 1 / o : fa).  stride4 = 4 * stride (bytes).
 struct GradTarget {
     float *base;
-    int stride;
+    uint32_t stride4;
     float fa;
     bool inv_o;
     bool active;
@@ -562,21 +562,22 @@ __device__ __forceinline__ GradTarget grad_target(int lane, float *g_points, flo
     const int f = sum9_field_of_lane(lane);
     t.active = f >= 0;
     t.base = g_points;
-    t.stride = 2;
+    int stride = 2;
     t.fa = 1.0f;
     t.inv_o = false;
     switch (f) {
     case 0: t.base = g_points; break;
     case 1: t.base = g_points + 1; break;
-    case 2: t.base = g_conics; t.stride = 3; t.fa = -0.5f; break;
-    case 3: t.base = g_conics + 1; t.stride = 3; t.fa = -1.0f; break;
-    case 4: t.base = g_conics + 2; t.stride = 3; t.fa = -0.5f; break;
-    case 5: t.base = g_opac; t.stride = 1; t.inv_o = true; break;
-    case 6: t.base = g_colors; t.stride = 3; break;
-    case 7: t.base = g_colors + 1; t.stride = 3; break;
-    case 8: t.base = g_colors + 2; t.stride = 3; break;
+    case 2: t.base = g_conics; stride = 3; t.fa = -0.5f; break;
+    case 3: t.base = g_conics + 1; stride = 3; t.fa = -1.0f; break;
+    case 4: t.base = g_conics + 2; stride = 3; t.fa = -0.5f; break;
+    case 5: t.base = g_opac; stride = 1; t.inv_o = true; break;
+    case 6: t.base = g_colors; stride = 3; break;
+    case 7: t.base = g_colors + 1; stride = 3; break;
+    case 8: t.base = g_colors + 2; stride = 3; break;
     default: break;
     }
+    t.stride4 = 4u * (uint32_t)stride;
     return t;
 }
 
@@ -648,10 +649,14 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
         f[7] = sg;
         f[8] = sb;
         const float total = wave_sum9(f, hi8, f8_lane);
+        // the entry's Gaussian id is uniform (a non-negative int32): one unsigned
+        // 32 x 32 -> 64 multiply-add per field address
+        const uint32_t g = __builtin_amdgcn_readfirstlane(__float_as_uint(col.w));
         if (tgt.active) {
-            const int g = __float_as_int(col.w);
-            const float scale = tgt.inv_o ? __builtin_amdgcn_rcpf(aux.y) : tgt.fa;
-            unsafeAtomicAdd(tgt.base + (int64_t)tgt.stride * g, total * scale);
+            const float scale = tgt.inv_o ? aux.y : tgt.fa;
+            const uint64_t off = (uint64_t)g * (uint64_t)tgt.stride4;
+            unsafeAtomicAdd(reinterpret_cast<float *>(reinterpret_cast<char *>(tgt.base) + off),
+                            total * scale);
         }
     }
 }
