@@ -197,18 +197,33 @@ __device__ __forceinline__ int64_t hist_index(int d, int b, int nblocks) {
 // Block d scans column d of the histogram table over the nblocks blocks in
 // place (first position of (d, block) among the keys with digit d) and writes
 // the column total to totals[d].  The downsweep adds the keys of smaller digits.
+constexpr int kDigitScanItems = 8;  // column entries per thread held in registers
+
 __global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
     uint32_t *__restrict__ table, int nblocks, uint32_t *__restrict__ totals) {
     __shared__ uint32_t tmp[kScanThreads / kWave + 1];
     const int d = blockIdx.x;
     uint32_t run = 0;
     uint32_t *col = table + (int64_t)d * nblocks;
-    for (int b0 = 0; b0 < nblocks; b0 += kScanThreads) {
-        const int b = b0 + threadIdx.x;
-        const uint32_t c = b < nblocks ? col[b] : 0u;
+    // chunks of kScanThreads * kDigitScanItems entries: thread t holds the
+    // consecutive entries [t * items, (t + 1) * items) of the chunk, so that all
+    // of a chunk's loads are issued before its one block scan
+    for (int b0 = 0; b0 < nblocks; b0 += kScanThreads * kDigitScanItems) {
+        const int first = b0 + threadIdx.x * kDigitScanItems;
+        uint32_t c[kDigitScanItems];
+        uint32_t mine = 0;
+#pragma unroll
+        for (int it = 0; it < kDigitScanItems; ++it) {
+            c[it] = first + it < nblocks ? col[first + it] : 0u;
+            mine += c[it];
+        }
         uint32_t chunk;
-        const uint32_t excl = block_exclusive_scan<uint32_t, kScanThreads>(c, tmp, chunk);
-        if (b < nblocks) col[b] = run + excl;
+        uint32_t pos = run + block_exclusive_scan<uint32_t, kScanThreads>(mine, tmp, chunk);
+#pragma unroll
+        for (int it = 0; it < kDigitScanItems; ++it) {
+            if (first + it < nblocks) col[first + it] = pos;
+            pos += c[it];
+        }
         run += chunk;
     }
     if (threadIdx.x == 0) totals[d] = run;
