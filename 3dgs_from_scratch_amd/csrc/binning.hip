@@ -455,8 +455,9 @@ __device__ __forceinline__ TileRect unpack_rect(uint2 p) {
 // tiles_touched and depth sort keys per Gaussian (src/cuda/kernel.cu:784-818),
 // fused with the histogram of the first depth-sort pass.  Also writes the
 // number of supertiles (kSuper x kSuper tiles) each Gaussian touches and adds
-// the block's total of tiles_touched to *total_tiles (K).  Gaussians without
-// tiles get the depth key 0xFFFFFFFF (sorted last; they emit nothing).
+// the block's totals of tiles_touched and of those supertile counts to
+// *total_tiles (K) and *total_entries (M).  Gaussians without tiles get the
+// depth key 0xFFFFFFFF (sorted last; they emit nothing).
 template <int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int64_t n, const float *__restrict__ points_image, const float *__restrict__ radii,
@@ -464,7 +465,7 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int tile_size, uint32_t *__restrict__ touched, uint32_t *__restrict__ super_touched,
     uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys, uint32_t *__restrict__ ids,
     int nbits, int nblocks, uint32_t *__restrict__ hist,
-    unsigned long long *__restrict__ total_tiles) {
+    unsigned long long *__restrict__ total_tiles, unsigned long long *__restrict__ total_entries) {
     __shared__ uint32_t counts[kRadixMax];
     __shared__ uint64_t sum_tmp[kSortThreads / kWave + 1];
     const int radix = 1 << nbits;
@@ -472,7 +473,7 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS];
     bool valid[ITEMS];
-    uint64_t my_tiles = 0;
+    uint64_t my_tiles = 0, my_entries = 0;
     // all loads first (clamped index, no control dependence) so they overlap
     float2 pt[ITEMS], rd[ITEMS];
     float dp[ITEMS];
@@ -507,10 +508,15 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
         depth_keys[i] = k[it];
         ids[i] = (uint32_t)i;
         my_tiles += cnt;
+        my_entries += scnt;
     }
-    uint64_t block_tiles;
+    uint64_t block_tiles, block_entries;
     block_exclusive_scan<uint64_t, kSortThreads>(my_tiles, sum_tmp, block_tiles);
-    if (threadIdx.x == 0 && block_tiles) atomicAdd(total_tiles, (unsigned long long)block_tiles);
+    block_exclusive_scan<uint64_t, kSortThreads>(my_entries, sum_tmp, block_entries);
+    if (threadIdx.x == 0 && block_tiles) {
+        atomicAdd(total_tiles, (unsigned long long)block_tiles);
+        atomicAdd(total_entries, (unsigned long long)block_entries);
+    }
     block_count_digits<ITEMS>(k, valid, 0, nbits, counts);
     __syncthreads();
     for (int d = threadIdx.x; d < radix; d += kSortThreads)
@@ -854,6 +860,124 @@ __global__ __launch_bounds__(256) void emit_super_kernel(
         }
 }
 
+// ---------------------------------------------- level 1 in one radix pass
+// With at most kRadixMax supertiles the supertile id is a single radix digit:
+// block b of kL1Threads handles the depth-ordered Gaussians [b * kL1Threads,
+// ...) and enumerates their (supertile, Gaussian) entries on the fly, without
+// storing them.  A Gaussian meets each supertile once, so in LDS
+// lanes[w][s] has bit L set when lane L of wave w meets supertile s; the
+// block's count of s is the sum of popcounts over its waves, and an entry's
+// rank among the block's entries of s is the popcount of the lanes before it.
+// l1_count_kernel writes the counts to a digit-major table, digit_scan_kernel
+// turns them into positions, and l1_scatter_kernel writes every entry's id and
+// packed tile rectangle at its position in the supertile-sorted list, which is
+// stable: (supertile, depth order).
+
+constexpr int kL1Threads = 512;
+constexpr int kL1Waves = kL1Threads / kWave;
+
+struct L1Args {
+    const uint32_t *order;    // Gaussians in depth order
+    const uint32_t *touched;  // supertiles met per Gaussian (by Gaussian id)
+    const uint2 *rects;       // packed tile rectangle per Gaussian
+    int64_t n, m;             // Gaussians, entries
+    int super_x, nblocks;
+};
+
+// This thread's Gaussian and the supertile range its tile rectangle meets
+// (false: none).
+__device__ __forceinline__ bool l1_gaussian(const L1Args &a, uint32_t &g, uint2 &packed,
+                                            TileRect &sr) {
+    const int64_t r = (int64_t)blockIdx.x * kL1Threads + threadIdx.x;
+    if (r >= a.n) return false;
+    g = a.order[r];
+    if (g >= (uint64_t)a.n || a.touched[g] == 0) return false;
+    packed = a.rects[g];
+    const TileRect t = unpack_rect(packed);
+    sr.tx0 = t.tx0 / kSuper;
+    sr.tx1 = t.tx1 / kSuper;
+    sr.ty0 = t.ty0 / kSuper;
+    sr.ty1 = t.ty1 / kSuper;
+    return true;
+}
+
+// lanes[w][s] for the block (zeroed here); returns whether this lane has entries.
+__device__ __forceinline__ bool l1_lane_masks(const L1Args &a, uint64_t (*lanes)[kRadixMax],
+                                              uint32_t &g, uint2 &packed, TileRect &sr) {
+    for (int i = threadIdx.x; i < kL1Waves * kRadixMax; i += kL1Threads) lanes[0][i] = 0ull;
+    __syncthreads();
+    const int wave = threadIdx.x / kWave;
+    const uint64_t bit = 1ull << (threadIdx.x % kWave);
+    const bool has = l1_gaussian(a, g, packed, sr);
+    if (has)
+        for (int y = sr.ty0; y <= sr.ty1; ++y)
+            for (int x = sr.tx0; x <= sr.tx1; ++x)
+                atomicOr(reinterpret_cast<unsigned long long *>(&lanes[wave][y * a.super_x + x]),
+                         (unsigned long long)bit);
+    __syncthreads();
+    return has;
+}
+
+// hist[s * nblocks + b] = entries of supertile s in block b.
+__global__ __launch_bounds__(kL1Threads) void l1_count_kernel(L1Args a,
+                                                              uint32_t *__restrict__ hist) {
+    __shared__ uint64_t lanes[kL1Waves][kRadixMax];
+    uint32_t g;
+    uint2 packed;
+    TileRect sr;
+    l1_lane_masks(a, lanes, g, packed, sr);
+    if (threadIdx.x < kRadixMax) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < kL1Waves; ++w) c += (uint32_t)__popcll(lanes[w][threadIdx.x]);
+        hist[hist_index(threadIdx.x, blockIdx.x, a.nblocks)] = c;
+    }
+}
+
+// `hist` holds, after digit_scan_kernel, the first position of (s, block)
+// among the entries of s and `totals` the entries of each s.  Writes
+// super_ids / super_rects and, from block 0, super_off[s] = entries with a
+// smaller supertile.
+__global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
+    L1Args a, const uint32_t *__restrict__ hist, const uint32_t *__restrict__ totals,
+    int n_super, int32_t *__restrict__ super_ids, uint2 *__restrict__ super_rects,
+    int32_t *__restrict__ super_off) {
+    __shared__ uint64_t lanes[kL1Waves][kRadixMax];
+    __shared__ uint32_t wave_pos[kL1Waves][kRadixMax];
+    __shared__ uint32_t scan_tmp[kL1Threads / kWave + 1];
+    uint32_t g = 0;
+    uint2 packed = make_uint2(0u, 0u);
+    TileRect sr{0, -1, 0, -1};
+    const bool has = l1_lane_masks(a, lanes, g, packed, sr);
+    const int d = threadIdx.x;
+    const uint32_t tot = d < n_super ? totals[d] : 0u;
+    uint32_t all;
+    const uint32_t smaller = block_exclusive_scan<uint32_t, kL1Threads>(tot, scan_tmp, all);
+    if (d < kRadixMax) {
+        uint32_t pos = smaller + (d < n_super ? hist[hist_index(d, blockIdx.x, a.nblocks)] : 0u);
+#pragma unroll
+        for (int w = 0; w < kL1Waves; ++w) {
+            wave_pos[w][d] = pos;
+            pos += (uint32_t)__popcll(lanes[w][d]);
+        }
+        if (blockIdx.x == 0 && d < n_super) super_off[d] = (int32_t)smaller;
+    }
+    __syncthreads();
+    if (has) {
+        const int wave = threadIdx.x / kWave;
+        const uint64_t below = lanemask_lt();
+        for (int y = sr.ty0; y <= sr.ty1; ++y)
+            for (int x = sr.tx0; x <= sr.tx1; ++x) {
+                const int s = y * a.super_x + x;
+                const uint32_t p = wave_pos[wave][s] + (uint32_t)__popcll(lanes[wave][s] & below);
+                if ((int64_t)p < a.m) {  // always true for consistent counts; guards the store
+                    super_ids[p] = (int32_t)g;
+                    super_rects[p] = packed;
+                }
+            }
+    }
+}
+
 // keys[i] = tile << 32 | depth bits of ids[i], the tile being the last one
 // whose offset is <= i (the reference's sorted 64-bit keys).
 __global__ __launch_bounds__(256) void keys_from_offsets_kernel(
@@ -967,8 +1091,12 @@ inline int64_t l2_blocks_bound(int64_t m, int n_super) {
     return (m + kL2Threads - 1) / kL2Threads + n_super;
 }
 
+inline int64_t l1_blocks(int64_t n) { return (n + kL1Threads - 1) / kL1Threads; }
+
 struct BinWs {
-    SortWs lvl1;
+    SortWs lvl1;            // general level 1 (more than kRadixMax supertiles)
+    uint32_t *l1_hist;      // one-pass level 1: kRadixMax x l1_blocks(n) table
+    uint32_t *l1_totals;    // one-pass level 1: entries per supertile
     int32_t *super_off;     // n_super (+1 spare)
     int32_t *super_ids;     // m
     uint2 *super_rects;     // m: packed tile rectangle of each super_ids entry
@@ -980,10 +1108,15 @@ struct BinWs {
     size_t bytes;
 };
 
-inline BinWs carve_bins(void *base, int64_t m, const Grid &g) {
+inline BinWs carve_bins(void *base, int64_t n, int64_t m, const Grid &g) {
     Carve c{reinterpret_cast<char *>(base)};
-    BinWs w;
-    w.lvl1 = carve_sort(c, m, g.super_bits);
+    BinWs w{};
+    if (g.n_super <= kRadixMax) {
+        w.l1_hist = c.take<uint32_t>(kRadixMax * l1_blocks(n));
+        w.l1_totals = c.take<uint32_t>(kRadixMax);
+    } else {
+        w.lvl1 = carve_sort(c, m, g.super_bits);
+    }
     w.super_off = c.take<int32_t>((int64_t)g.n_super + 1);
     w.super_ids = c.take<int32_t>(m);
     w.super_rects = c.take<uint2>(m);
@@ -1062,38 +1195,44 @@ extern "C" int gs_bin_count(const float *points_image, const float *radii, const
     const int nb0 = pass_bits(plan, kDepthBits, 0);
     uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
     unsigned long long *k_total = reinterpret_cast<unsigned long long *>(totals);
+    unsigned long long *m_total = reinterpret_cast<unsigned long long *>(totals + 1);
     hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
                        stream, n, points_image, radii, depths, mask, width, height, tile_size,
                        w.touched, w.super_touched, w.rects, w.dkeys_a, w.dvals_a, nb0, nblocks,
-                       hist, k_total);
+                       hist, k_total, m_total);
     st = launch_status();
     if (st) return st;
-    // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes no
-    // keys but the supertile counts in depth order
+    // Up to kRadixMax supertiles level 1 enumerates the entries from the depth
+    // order directly (l1_count_kernel); otherwise it places them with the
+    // supertile counts' exclusive scan in depth order, written by the last pass.
+    Grid grid;
+    const bool one_pass_l1 = make_grid(width, height, tile_size, grid) && grid.n_super <= kRadixMax;
+    // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes no keys
     for (int p = 0; p < plan.passes; ++p) {
         const bool from_a = (p % 2) == 0;
         const bool last = p + 1 == plan.passes;
+        const bool counts = last && !one_pass_l1;
         st = radix_pass<uint32_t, kDepthItems>(
             from_a ? w.dkeys_a : w.dkeys_b, from_a ? w.dvals_a : w.dvals_b,
             from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, n,
             p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream,
-            p == 0, last ? w.super_touched : nullptr, last ? w.counts : nullptr);
+            p == 0, counts ? w.super_touched : nullptr, counts ? w.counts : nullptr);
         if (st) return st;
     }
-    // supertile entry offsets in depth order; the total (M) goes to totals[1]
+    if (one_pass_l1) return GS_OK;
+    // supertile entry offsets in depth order (the total equals count_tiles' M)
     return scan_exclusive<uint64_t>(w.counts, w.offsets, n,
                                     reinterpret_cast<uint64_t *>(totals + 1), w.scan_ws, stream);
 }
 
 extern "C" int gs_bin_sort_workspace_size(int64_t n, int64_t k, int64_t m, int32_t width,
                                           int32_t height, int32_t tile_size, size_t *bytes) {
-    (void)n;
     (void)k;
     Grid g;
-    if (m < 0 || width <= 0 || height <= 0 || tile_size <= 0 || !bytes ||
+    if (n < 0 || m < 0 || width <= 0 || height <= 0 || tile_size <= 0 || !bytes ||
         !make_grid(width, height, tile_size, g))
         return GS_ERR_INVALID_ARGUMENT;
-    *bytes = carve_bins(nullptr, m, g).bytes;
+    *bytes = carve_bins(nullptr, n, m, g).bytes;
     return GS_OK;
 }
 
@@ -1113,7 +1252,7 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         return GS_ERR_UNSUPPORTED;  // tile rectangles are staged with 16-bit coordinates
     if ((k == 0) != (m == 0)) return GS_ERR_INVALID_ARGUMENT;
     const CountWs cw = carve_count(const_cast<void *>(count_workspace), n);
-    const BinWs w = carve_bins(workspace, m, g);
+    const BinWs w = carve_bins(workspace, n, m, g);
     if (m > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
     if (n > 0 && !count_workspace) return GS_ERR_INVALID_ARGUMENT;
     int st;
@@ -1128,19 +1267,42 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         return GS_ERR_INVALID_ARGUMENT;
 
     // level 1: (supertile, Gaussian) entries in depth order, stably sorted by supertile
-    EmitArgs a;
-    a.rects = cw.rects;
-    a.order = cw.dvals_a;  // depth order (even number of depth passes)
-    a.offsets = cw.offsets;
-    a.touched = cw.super_touched;
-    a.n = n;
-    a.k = m;
-    a.tiles_x = g.super_x;
-    st = use_u16_keys(g.super_bits)
-             ? super_sort<uint16_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
-                                    w.super_ids, w.super_rects, stream)
-             : super_sort<uint32_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
-                                    w.super_ids, w.super_rects, stream);
+    if (g.n_super <= kRadixMax) {
+        L1Args la;
+        la.order = cw.dvals_a;  // depth order (even number of depth passes)
+        la.touched = cw.super_touched;
+        la.rects = cw.rects;
+        la.n = n;
+        la.m = m;
+        la.super_x = g.super_x;
+        la.nblocks = (int)l1_blocks(n);
+        hipLaunchKernelGGL(l1_count_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
+                           w.l1_hist);
+        st = launch_status();
+        if (st) return st;
+        hipLaunchKernelGGL(digit_scan_kernel, dim3(g.n_super), dim3(kScanThreads), 0, stream,
+                           w.l1_hist, la.nblocks, w.l1_totals);
+        st = launch_status();
+        if (st) return st;
+        hipLaunchKernelGGL(l1_scatter_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
+                           (const uint32_t *)w.l1_hist, (const uint32_t *)w.l1_totals, g.n_super,
+                           w.super_ids, w.super_rects, w.super_off);
+        st = launch_status();
+    } else {  // emitted entries sorted by supertile over several radix passes
+        EmitArgs a;
+        a.rects = cw.rects;
+        a.order = cw.dvals_a;  // depth order (even number of depth passes)
+        a.offsets = cw.offsets;
+        a.touched = cw.super_touched;
+        a.n = n;
+        a.k = m;
+        a.tiles_x = g.super_x;
+        st = use_u16_keys(g.super_bits)
+                 ? super_sort<uint16_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
+                                        w.super_ids, w.super_rects, stream)
+                 : super_sort<uint32_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
+                                        w.super_ids, w.super_rects, stream);
+    }
     if (st) return st;
 
     // level 2: block plan, per-tile counts, tile offsets and block prefixes, scatter

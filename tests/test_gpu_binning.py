@@ -63,6 +63,14 @@ def test_layout_random_bitexact(gpu, n, width, height, tile):
     assert k > 0
 
 
+def test_layout_many_supertiles_bitexact(gpu):
+    """A grid of more than 256 supertiles (40 x 25 at 2560x1600, tile 8): the
+    level-1 sort over several radix passes instead of the one-pass count."""
+    n, width, height, tile = 20000, 2560, 1600, 8
+    pts, radii, depths, mask = _random_splats(n, width, height, seed=7, rmax=24.0)
+    assert _check(gpu, pts, radii, depths, mask, width, height, tile) > 0
+
+
 @pytest.mark.parametrize("name", ["multitile", "truncated"])
 def test_layout_reference_fixtures(gpu, name):
     f = helpers.fixture_tensors(name)
