@@ -151,6 +151,10 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t key, int shift, uint32_t d
     return (key >> shift) & dmask;
 }
 
+// Packed tile rectangle (tx0 | tx1 << 16, ty0 | ty1 << 16) of a Gaussian
+// without tiles: tx0 > tx1.
+constexpr uint2 kEmptyRect = {0xffffu, 0xffffu};
+
 // kPayload: each value carries an 8-byte payload (a packed tile rectangle).
 template <int ITEMS, bool kPayload = false>
 struct SortLds {
@@ -233,7 +237,8 @@ __global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
 // digit order and written to keys_out/vals_out (and, with kPayload, the
 // payloads to pay_out).  `table` holds the position of each (digit, block)
 // among the keys of its digit, `totals` the keys per digit.  When counts_out
-// is set, counts_out[dst] = touched[value] is written as well.
+// is set, counts_out[dst] = touched[value] is written as well, and when
+// rects_out is set, rects_out[dst] = rects[value].
 template <typename KeyT, int ITEMS, bool kPayload>
 __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               const uint32_t (&v)[ITEMS],
@@ -246,7 +251,9 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               bool write_keys, SortLds<ITEMS, kPayload> &s,
                                               const uint32_t *__restrict__ totals,
                                               const uint32_t *__restrict__ touched,
-                                              uint64_t *__restrict__ counts_out) {
+                                              uint64_t *__restrict__ counts_out,
+                                              const uint2 *__restrict__ rects,
+                                              uint2 *__restrict__ rects_out) {
     const int radix = 1 << nbits;
     const uint32_t dmask = (uint32_t)radix - 1u;
     const int wave = threadIdx.x / kWave;
@@ -309,6 +316,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
             vals_out[dst] = val;
             if (kPayload) pay_out[dst] = s.spay[p];
             if (counts_out) counts_out[dst] = val < (uint64_t)n ? touched[val] : 0u;
+            if (rects_out) rects_out[dst] = val < (uint64_t)n ? rects[val] : kEmptyRect;
         }
     }
 }
@@ -344,7 +352,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     uint32_t *__restrict__ vals_out, uint2 *__restrict__ pay_out, int64_t n, int shift,
     int nbits, int nblocks, const uint32_t *__restrict__ table,
     const uint32_t *__restrict__ totals, int write_keys, const uint32_t *__restrict__ touched,
-    uint64_t *__restrict__ counts_out) {
+    uint64_t *__restrict__ counts_out, const uint2 *__restrict__ rects,
+    uint2 *__restrict__ rects_out) {
     __shared__ SortLds<ITEMS, kPayload> s;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS], v[ITEMS];
@@ -360,7 +369,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
     }
     block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, shift, nbits, nblocks, table, keys_out,
                                          vals_out, pay_out, n, write_keys != 0, s, totals,
-                                         touched, counts_out);
+                                         touched, counts_out, rects, rects_out);
 }
 
 struct SortPlan {
@@ -412,7 +421,8 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
                int shift, int nbits, bool write_keys, void *ws, hipStream_t stream,
                bool hist_ready = false, const uint32_t *touched = nullptr,
                uint64_t *counts_out = nullptr, const uint2 *pin = nullptr,
-               uint2 *pout = nullptr) {
+               uint2 *pout = nullptr, const uint2 *rects = nullptr,
+               uint2 *rects_out = nullptr) {
     const int nblocks = (int)sort_blocks<ITEMS>(n);
     uint32_t *hist = reinterpret_cast<uint32_t *>(ws);
     uint32_t *totals = radix_totals<ITEMS>(ws, n);
@@ -430,7 +440,7 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
     hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, kPayload>), dim3(nblocks),
                        dim3(kSortThreads), 0, stream, kin, vin, pin, kout, vout, pout, n, shift,
                        nbits, nblocks, hist, (const uint32_t *)totals, write_keys ? 1 : 0,
-                       touched, counts_out);
+                       touched, counts_out, rects, rects_out);
     return launch_status();
 }
 
@@ -504,7 +514,7 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
         k[it] = cnt ? __float_as_uint(dp[it]) : 0xFFFFFFFFu;
         touched[i] = cnt;
         super_touched[i] = scnt;
-        rects[i] = pack_rect(r);
+        rects[i] = cnt ? pack_rect(r) : kEmptyRect;
         depth_keys[i] = k[it];
         ids[i] = (uint32_t)i;
         my_tiles += cnt;
@@ -877,10 +887,9 @@ constexpr int kL1Threads = 512;
 constexpr int kL1Waves = kL1Threads / kWave;
 
 struct L1Args {
-    const uint32_t *order;    // Gaussians in depth order
-    const uint32_t *touched;  // supertiles met per Gaussian (by Gaussian id)
-    const uint2 *rects;       // packed tile rectangle per Gaussian
-    int64_t n, m;             // Gaussians, entries
+    const uint32_t *order;       // Gaussians in depth order
+    const uint2 *rects_depth;    // their packed tile rectangles, in the same order
+    int64_t n, m;                // Gaussians, entries
     int super_x, nblocks;
 };
 
@@ -891,9 +900,9 @@ __device__ __forceinline__ bool l1_gaussian(const L1Args &a, uint32_t &g, uint2 
     const int64_t r = (int64_t)blockIdx.x * kL1Threads + threadIdx.x;
     if (r >= a.n) return false;
     g = a.order[r];
-    if (g >= (uint64_t)a.n || a.touched[g] == 0) return false;
-    packed = a.rects[g];
+    packed = a.rects_depth[r];
     const TileRect t = unpack_rect(packed);
+    if (g >= (uint64_t)a.n || t.tx0 > t.tx1) return false;
     sr.tx0 = t.tx0 / kSuper;
     sr.tx1 = t.tx1 / kSuper;
     sr.ty0 = t.ty0 / kSuper;
@@ -1016,6 +1025,7 @@ struct Carve {
 struct CountWs {
     uint32_t *touched, *super_touched, *dkeys_a, *dvals_a, *dkeys_b, *dvals_b;
     uint2 *rects;
+    uint2 *rects_depth;  // packed tile rectangles in depth order (one-pass level 1)
     uint64_t *counts, *offsets;
     void *sort_ws, *scan_ws;
     size_t bytes;
@@ -1031,6 +1041,7 @@ inline CountWs carve_count(void *base, int64_t n) {
     w.dvals_a = c.take<uint32_t>(n);
     w.dkeys_b = c.take<uint32_t>(n);
     w.dvals_b = c.take<uint32_t>(n);
+    w.rects_depth = c.take<uint2>(n);
     w.counts = c.take<uint64_t>(n);
     w.offsets = c.take<uint64_t>(n + 1);
     w.sort_ws = c.take<char>((int64_t)radix_workspace_bytes<kDepthItems>(n));
@@ -1203,20 +1214,22 @@ extern "C" int gs_bin_count(const float *points_image, const float *radii, const
     st = launch_status();
     if (st) return st;
     // Up to kRadixMax supertiles level 1 enumerates the entries from the depth
-    // order directly (l1_count_kernel); otherwise it places them with the
-    // supertile counts' exclusive scan in depth order, written by the last pass.
+    // order directly (l1_count_kernel), reading the tile rectangles that the last
+    // pass writes in depth order; otherwise it places them with the supertile
+    // counts' exclusive scan in depth order, also written by the last pass.
     Grid grid;
     const bool one_pass_l1 = make_grid(width, height, tile_size, grid) && grid.n_super <= kRadixMax;
     // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes no keys
     for (int p = 0; p < plan.passes; ++p) {
         const bool from_a = (p % 2) == 0;
         const bool last = p + 1 == plan.passes;
-        const bool counts = last && !one_pass_l1;
+        const bool counts = last && !one_pass_l1, rects = last && one_pass_l1;
         st = radix_pass<uint32_t, kDepthItems>(
             from_a ? w.dkeys_a : w.dkeys_b, from_a ? w.dvals_a : w.dvals_b,
             from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, n,
             p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream,
-            p == 0, counts ? w.super_touched : nullptr, counts ? w.counts : nullptr);
+            p == 0, counts ? w.super_touched : nullptr, counts ? w.counts : nullptr, nullptr,
+            nullptr, rects ? w.rects : nullptr, rects ? w.rects_depth : nullptr);
         if (st) return st;
     }
     if (one_pass_l1) return GS_OK;
@@ -1270,8 +1283,7 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
     if (g.n_super <= kRadixMax) {
         L1Args la;
         la.order = cw.dvals_a;  // depth order (even number of depth passes)
-        la.touched = cw.super_touched;
-        la.rects = cw.rects;
+        la.rects_depth = cw.rects_depth;
         la.n = n;
         la.m = m;
         la.super_x = g.super_x;
