@@ -151,9 +151,42 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t key, int shift, uint32_t d
     return (key >> shift) & dmask;
 }
 
-// Packed tile rectangle (tx0 | tx1 << 16, ty0 | ty1 << 16) of a Gaussian
-// without tiles: tx0 > tx1.
+// Tile rectangle packed as (tx0 | tx1 << 16, ty0 | ty1 << 16); tile coordinates
+// fit 16 bits (gs_bin_sort rejects larger grids).
+__device__ __forceinline__ uint2 pack_rect(const TileRect &r) {
+    return make_uint2((uint32_t)r.tx0 | ((uint32_t)r.tx1 << 16),
+                      (uint32_t)r.ty0 | ((uint32_t)r.ty1 << 16));
+}
+
+__device__ __forceinline__ TileRect unpack_rect(uint2 p) {
+    TileRect r;
+    r.tx0 = (int)(p.x & 0xffffu);
+    r.tx1 = (int)(p.x >> 16);
+    r.ty0 = (int)(p.y & 0xffffu);
+    r.ty1 = (int)(p.y >> 16);
+    return r;
+}
+
+// Packed tile rectangle of a Gaussian without tiles: tx0 > tx1.
 constexpr uint2 kEmptyRect = {0xffffu, 0xffffu};
+
+// Tiles of a packed rectangle (0 for kEmptyRect).
+__device__ __forceinline__ uint32_t rect_tiles(uint2 packed) {
+    const TileRect t = unpack_rect(packed);
+    if (t.tx0 > t.tx1) return 0u;
+    return (uint32_t)((t.tx1 - t.tx0 + 1) * (t.ty1 - t.ty0 + 1));
+}
+
+// Supertiles (kSuper x kSuper tiles) a packed rectangle meets (0 for kEmptyRect).
+__device__ __forceinline__ uint32_t rect_supertiles(uint2 packed) {
+    const TileRect t = unpack_rect(packed);
+    if (t.tx0 > t.tx1) return 0u;
+    return (uint32_t)((t.tx1 / kSuper - t.tx0 / kSuper + 1) *
+                      (t.ty1 / kSuper - t.ty0 / kSuper + 1));
+}
+
+// Depth key of a Gaussian without tiles: the first depth pass drops these keys.
+constexpr uint32_t kNoTilesKey = 0xFFFFFFFFu;
 
 // kPayload: each value carries an 8-byte payload (a packed tile rectangle).
 template <int ITEMS, bool kPayload = false>
@@ -198,15 +231,44 @@ __device__ __forceinline__ int64_t hist_index(int d, int b, int nblocks) {
     return (int64_t)d * nblocks + b;
 }
 
+// Per-block sums of count_tiles (tiles, supertile entries, Gaussians with
+// tiles; three per block) reduced by one workgroup of kScanThreads to
+// sums_out[0] = K, sums_out[1] = M and *live_out.
+__device__ __forceinline__ void reduce_block_sums(const unsigned long long *__restrict__ sums,
+                                                  int nblocks, int64_t *__restrict__ sums_out,
+                                                  int64_t *__restrict__ live_out) {
+    __shared__ unsigned long long tmp[kScanThreads / kWave + 1];
+    unsigned long long acc[3] = {0ull, 0ull, 0ull};
+    for (int b = threadIdx.x; b < nblocks; b += kScanThreads)
+#pragma unroll
+        for (int f = 0; f < 3; ++f) acc[f] += sums[(int64_t)b * 3 + f];
+    unsigned long long total[3];
+#pragma unroll
+    for (int f = 0; f < 3; ++f)
+        block_exclusive_scan<unsigned long long, kScanThreads>(acc[f], tmp, total[f]);
+    if (threadIdx.x == 0) {
+        sums_out[0] = (int64_t)total[0];
+        sums_out[1] = (int64_t)total[1];
+        *live_out = (int64_t)total[2];
+    }
+}
+
 // Block d scans column d of the histogram table over the nblocks blocks in
 // place (first position of (d, block) among the keys with digit d) and writes
 // the column total to totals[d].  The downsweep adds the keys of smaller digits.
+// With block_sums, one more block (the last) runs reduce_block_sums.
 constexpr int kDigitScanItems = 8;  // column entries per thread held in registers
 
 __global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
-    uint32_t *__restrict__ table, int nblocks, uint32_t *__restrict__ totals) {
+    uint32_t *__restrict__ table, int nblocks, uint32_t *__restrict__ totals,
+    const unsigned long long *__restrict__ block_sums, int64_t *__restrict__ sums_out,
+    int64_t *__restrict__ live_out) {
     __shared__ uint32_t tmp[kScanThreads / kWave + 1];
     const int d = blockIdx.x;
+    if (block_sums && d == (int)gridDim.x - 1) {
+        reduce_block_sums(block_sums, nblocks, sums_out, live_out);
+        return;
+    }
     uint32_t run = 0;
     uint32_t *col = table + (int64_t)d * nblocks;
     // chunks of kScanThreads * kDigitScanItems entries: thread t holds the
@@ -237,8 +299,8 @@ __global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
 // digit order and written to keys_out/vals_out (and, with kPayload, the
 // payloads to pay_out).  `table` holds the position of each (digit, block)
 // among the keys of its digit, `totals` the keys per digit.  When counts_out
-// is set, counts_out[dst] = touched[value] is written as well, and when
-// rects_out is set, rects_out[dst] = rects[value].
+// is set, counts_out[dst] = rect_supertiles(rects[value]) is written as well,
+// and when rects_out is set, rects_out[dst] = rects[value].
 template <typename KeyT, int ITEMS, bool kPayload>
 __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               const uint32_t (&v)[ITEMS],
@@ -250,7 +312,6 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               uint2 *__restrict__ pay_out, int64_t n,
                                               bool write_keys, SortLds<ITEMS, kPayload> &s,
                                               const uint32_t *__restrict__ totals,
-                                              const uint32_t *__restrict__ touched,
                                               uint64_t *__restrict__ counts_out,
                                               const uint2 *__restrict__ rects,
                                               uint2 *__restrict__ rects_out) {
@@ -315,20 +376,25 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
             if (write_keys) keys_out[dst] = (KeyT)key;
             vals_out[dst] = val;
             if (kPayload) pay_out[dst] = s.spay[p];
-            if (counts_out) counts_out[dst] = val < (uint64_t)n ? touched[val] : 0u;
-            if (rects_out) rects_out[dst] = val < (uint64_t)n ? rects[val] : kEmptyRect;
+            if (counts_out || rects_out) {
+                const uint2 r = val < (uint64_t)n ? rects[val] : kEmptyRect;
+                if (counts_out) counts_out[dst] = rect_supertiles(r);
+                if (rects_out) rects_out[dst] = r;
+            }
         }
     }
 }
 
-// hist[d * nblocks + block] = number of keys of this block with digit d.
+// hist[d * nblocks + block] = number of keys of this block with digit d.  The
+// keys are the first *n_live (when given, else n) of the array.
 template <typename KeyT, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
-    const KeyT *__restrict__ keys, int64_t n, int shift, int nbits, int nblocks,
-    uint32_t *__restrict__ hist) {
+    const KeyT *__restrict__ keys, int64_t n, const int64_t *__restrict__ n_live, int shift,
+    int nbits, int nblocks, uint32_t *__restrict__ hist) {
     __shared__ uint32_t counts[kRadixMax];
     const int radix = 1 << nbits;
     for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
+    if (n_live) n = *n_live;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS];
     bool valid[ITEMS];
@@ -345,31 +411,71 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
         hist[hist_index(d, blockIdx.x, nblocks)] = counts[d];
 }
 
+// Optional inputs and outputs of a radix pass besides its keys and values.
+struct PassExtras {
+    bool hist_ready = false;            // the caller wrote this pass's histogram table
+    bool drop_no_tiles = false;         // keys equal to kNoTilesKey are not sorted
+    const int64_t *n_live = nullptr;    // device: sort only the first *n_live keys
+    const uint2 *pin = nullptr;         // kPayload: 8-byte payload per key
+    uint2 *pout = nullptr;
+    const uint2 *rects = nullptr;       // gathered by value (last pass):
+    uint64_t *counts_out = nullptr;     //   rect_supertiles(rects[value])
+    uint2 *rects_out = nullptr;         //   rects[value]
+    const unsigned long long *block_sums = nullptr;  // count_tiles' per-block sums,
+    int64_t *sums_out = nullptr;        //   reduced to sums_out[0..1] (K, M)
+    int64_t *live_out = nullptr;        //   and *live_out (keys with tiles)
+};
+
+template <typename KeyT>
+struct DownArgs {
+    const KeyT *keys_in;
+    const uint32_t *vals_in;  // null: the value of key i is i
+    const uint2 *pay_in;
+    KeyT *keys_out;
+    uint32_t *vals_out;
+    uint2 *pay_out;
+    int64_t n;
+    const int64_t *n_live;
+    int shift, nbits, nblocks, write_keys, drop_no_tiles;
+    const uint32_t *table, *totals;
+    uint64_t *counts_out;
+    const uint2 *rects;
+    uint2 *rects_out;
+};
+
+// With n_live, only the first *n_live keys are sorted, and a pass that writes
+// no keys (the last) fills output positions *n_live .. n - 1 of its block's
+// range with a value of 0xFFFFFFFF, a count of 0 and kEmptyRect.
 template <typename KeyT, int ITEMS, bool kPayload>
-__global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(
-    const KeyT *__restrict__ keys_in, const uint32_t *__restrict__ vals_in,
-    const uint2 *__restrict__ pay_in, KeyT *__restrict__ keys_out,
-    uint32_t *__restrict__ vals_out, uint2 *__restrict__ pay_out, int64_t n, int shift,
-    int nbits, int nblocks, const uint32_t *__restrict__ table,
-    const uint32_t *__restrict__ totals, int write_keys, const uint32_t *__restrict__ touched,
-    uint64_t *__restrict__ counts_out, const uint2 *__restrict__ rects,
-    uint2 *__restrict__ rects_out) {
+__global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(DownArgs<KeyT> a) {
     __shared__ SortLds<ITEMS, kPayload> s;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
+    const int64_t live = a.n_live ? *a.n_live : a.n;
     uint32_t k[ITEMS], v[ITEMS];
     uint2 pay[ITEMS];
     bool valid[ITEMS];
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t i = base + slot_index<ITEMS>(it);
-        valid[it] = i < n;
-        k[it] = valid[it] ? (uint32_t)keys_in[i] : 0u;
-        v[it] = valid[it] ? vals_in[i] : 0u;
-        pay[it] = (kPayload && valid[it]) ? pay_in[i] : make_uint2(0u, 0u);
+        const bool in = i < live;
+        k[it] = in ? (uint32_t)a.keys_in[i] : 0u;
+        v[it] = in ? (a.vals_in ? a.vals_in[i] : (uint32_t)i) : 0u;
+        pay[it] = (kPayload && in) ? a.pay_in[i] : make_uint2(0u, 0u);
+        valid[it] = in && !(a.drop_no_tiles && k[it] == kNoTilesKey);
     }
-    block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, shift, nbits, nblocks, table, keys_out,
-                                         vals_out, pay_out, n, write_keys != 0, s, totals,
-                                         touched, counts_out, rects, rects_out);
+    block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, a.shift, a.nbits, a.nblocks, a.table,
+                                         a.keys_out, a.vals_out, a.pay_out, a.n,
+                                         a.write_keys != 0, s, a.totals, a.counts_out, a.rects,
+                                         a.rects_out);
+    if (a.n_live && !a.write_keys) {
+        for (int t = threadIdx.x; t < kSortThreads * ITEMS; t += kSortThreads) {
+            const int64_t j = base + t;
+            if (j < live || j >= a.n) continue;
+            a.vals_out[j] = 0xFFFFFFFFu;
+            if (a.counts_out) a.counts_out[j] = 0u;
+            if (a.rects_out) a.rects_out[j] = kEmptyRect;
+        }
+    }
 }
 
 struct SortPlan {
@@ -414,76 +520,73 @@ uint32_t *radix_totals(void *ws, int64_t n) {
 }
 
 // One LSD pass from arrays: histogram (unless the caller already wrote this
-// pass's table: hist_ready), digit scan, scatter.  With counts_out, counts_out[dst] = touched[value] is written next to
-// the values.
+// pass's table), digit scan, scatter; `x` adds the optional inputs and outputs.
 template <typename KeyT, int ITEMS, bool kPayload = false>
 int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout, int64_t n,
                int shift, int nbits, bool write_keys, void *ws, hipStream_t stream,
-               bool hist_ready = false, const uint32_t *touched = nullptr,
-               uint64_t *counts_out = nullptr, const uint2 *pin = nullptr,
-               uint2 *pout = nullptr, const uint2 *rects = nullptr,
-               uint2 *rects_out = nullptr) {
+               const PassExtras &x = PassExtras()) {
     const int nblocks = (int)sort_blocks<ITEMS>(n);
     uint32_t *hist = reinterpret_cast<uint32_t *>(ws);
     uint32_t *totals = radix_totals<ITEMS>(ws, n);
     int st;
-    if (!hist_ready) {
+    if (!x.hist_ready) {
         hipLaunchKernelGGL((radix_upsweep_kernel<KeyT, ITEMS>), dim3(nblocks), dim3(kSortThreads),
-                           0, stream, kin, n, shift, nbits, nblocks, hist);
+                           0, stream, kin, n, x.n_live, shift, nbits, nblocks, hist);
         st = launch_status();
         if (st) return st;
     }
-    hipLaunchKernelGGL(digit_scan_kernel, dim3(1 << nbits), dim3(kScanThreads), 0, stream, hist,
-                       nblocks, totals);
+    const int sums_block = x.block_sums ? 1 : 0;
+    hipLaunchKernelGGL(digit_scan_kernel, dim3((1 << nbits) + sums_block), dim3(kScanThreads), 0,
+                       stream, hist, nblocks, totals, x.block_sums, x.sums_out, x.live_out);
     st = launch_status();
     if (st) return st;
+    DownArgs<KeyT> a;
+    a.keys_in = kin;
+    a.vals_in = vin;
+    a.pay_in = x.pin;
+    a.keys_out = kout;
+    a.vals_out = vout;
+    a.pay_out = x.pout;
+    a.n = n;
+    a.n_live = x.n_live;
+    a.shift = shift;
+    a.nbits = nbits;
+    a.nblocks = nblocks;
+    a.write_keys = write_keys ? 1 : 0;
+    a.drop_no_tiles = x.drop_no_tiles ? 1 : 0;
+    a.table = hist;
+    a.totals = totals;
+    a.counts_out = x.counts_out;
+    a.rects = x.rects;
+    a.rects_out = x.rects_out;
     hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, kPayload>), dim3(nblocks),
-                       dim3(kSortThreads), 0, stream, kin, vin, pin, kout, vout, pout, n, shift,
-                       nbits, nblocks, hist, (const uint32_t *)totals, write_keys ? 1 : 0,
-                       touched, counts_out, rects, rects_out);
+                       dim3(kSortThreads), 0, stream, a);
     return launch_status();
 }
 
 // ------------------------------------------------------------- binning
 
-// Tile rectangle packed as (tx0 | tx1 << 16, ty0 | ty1 << 16); tile coordinates
-// fit 16 bits (gs_bin_sort rejects larger grids).
-__device__ __forceinline__ uint2 pack_rect(const TileRect &r) {
-    return make_uint2((uint32_t)r.tx0 | ((uint32_t)r.tx1 << 16),
-                      (uint32_t)r.ty0 | ((uint32_t)r.ty1 << 16));
-}
-
-__device__ __forceinline__ TileRect unpack_rect(uint2 p) {
-    TileRect r;
-    r.tx0 = (int)(p.x & 0xffffu);
-    r.tx1 = (int)(p.x >> 16);
-    r.ty0 = (int)(p.y & 0xffffu);
-    r.ty1 = (int)(p.y >> 16);
-    return r;
-}
-
-// tiles_touched and depth sort keys per Gaussian (src/cuda/kernel.cu:784-818),
-// fused with the histogram of the first depth-sort pass.  Also writes the
-// number of supertiles (kSuper x kSuper tiles) each Gaussian touches and adds
-// the block's totals of tiles_touched and of those supertile counts to
-// *total_tiles (K) and *total_entries (M).  Gaussians without tiles get the
-// depth key 0xFFFFFFFF (sorted last; they emit nothing).
+// Tile rectangle and depth sort key per Gaussian (tiles_touched and the keys'
+// depth bits: src/cuda/kernel.cu:784-818), fused with the histogram of the
+// first depth-sort pass.  Gaussians without tiles get the key kNoTilesKey and
+// kEmptyRect and are left out of the histogram (the first pass drops them); so
+// is a Gaussian whose depth bits equal kNoTilesKey (a NaN), which therefore
+// gets no tiles.  block_sums[3 b + f] = the block's tiles (f = 0), supertile
+// entries (f = 1) and Gaussians with tiles (f = 2).
 template <int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int64_t n, const float *__restrict__ points_image, const float *__restrict__ radii,
     const float *__restrict__ depths, const uint8_t *__restrict__ mask, int width, int height,
-    int tile_size, uint32_t *__restrict__ touched, uint32_t *__restrict__ super_touched,
-    uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys, uint32_t *__restrict__ ids,
-    int nbits, int nblocks, uint32_t *__restrict__ hist,
-    unsigned long long *__restrict__ total_tiles, unsigned long long *__restrict__ total_entries) {
+    int tile_size, uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys, int nbits,
+    int nblocks, uint32_t *__restrict__ hist, unsigned long long *__restrict__ block_sums) {
     __shared__ uint32_t counts[kRadixMax];
-    __shared__ uint64_t sum_tmp[kSortThreads / kWave + 1];
+    __shared__ unsigned long long sum_tmp[kSortThreads / kWave + 1];
     const int radix = 1 << nbits;
     for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS];
     bool valid[ITEMS];
-    uint64_t my_tiles = 0, my_entries = 0;
+    unsigned long long my_tiles = 0, my_entries = 0, my_live = 0;
     // all loads first (clamped index, no control dependence) so they overlap
     float2 pt[ITEMS], rd[ITEMS];
     float dp[ITEMS];
@@ -500,32 +603,31 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t i = base + slot_index<ITEMS>(it);
-        valid[it] = i < n;
-        k[it] = 0u;
-        if (!valid[it]) continue;
-        uint32_t cnt = 0, scnt = 0;
+        valid[it] = false;
+        k[it] = kNoTilesKey;
+        if (i >= n) continue;
         TileRect r{0, 0, 0, 0};
-        if (mk[it] && tile_rect(pt[it].x, pt[it].y, rd[it].x, rd[it].y, width, height,
-                                tile_size, r)) {
-            cnt = (uint32_t)((r.tx1 - r.tx0 + 1) * (r.ty1 - r.ty0 + 1));
-            scnt = (uint32_t)((r.tx1 / kSuper - r.tx0 / kSuper + 1) *
-                              (r.ty1 / kSuper - r.ty0 / kSuper + 1));
-        }
-        k[it] = cnt ? __float_as_uint(dp[it]) : 0xFFFFFFFFu;
-        touched[i] = cnt;
-        super_touched[i] = scnt;
-        rects[i] = cnt ? pack_rect(r) : kEmptyRect;
+        const uint32_t bits = __float_as_uint(dp[it]);
+        const bool has = mk[it] && bits != kNoTilesKey &&
+                         tile_rect(pt[it].x, pt[it].y, rd[it].x, rd[it].y, width, height,
+                                   tile_size, r);
+        const uint2 packed = has ? pack_rect(r) : kEmptyRect;
+        valid[it] = has;
+        k[it] = has ? bits : kNoTilesKey;
+        rects[i] = packed;
         depth_keys[i] = k[it];
-        ids[i] = (uint32_t)i;
-        my_tiles += cnt;
-        my_entries += scnt;
+        my_tiles += rect_tiles(packed);
+        my_entries += rect_supertiles(packed);
+        my_live += has ? 1u : 0u;
     }
-    uint64_t block_tiles, block_entries;
-    block_exclusive_scan<uint64_t, kSortThreads>(my_tiles, sum_tmp, block_tiles);
-    block_exclusive_scan<uint64_t, kSortThreads>(my_entries, sum_tmp, block_entries);
-    if (threadIdx.x == 0 && block_tiles) {
-        atomicAdd(total_tiles, (unsigned long long)block_tiles);
-        atomicAdd(total_entries, (unsigned long long)block_entries);
+    unsigned long long block_tiles, block_entries, block_live;
+    block_exclusive_scan<unsigned long long, kSortThreads>(my_tiles, sum_tmp, block_tiles);
+    block_exclusive_scan<unsigned long long, kSortThreads>(my_entries, sum_tmp, block_entries);
+    block_exclusive_scan<unsigned long long, kSortThreads>(my_live, sum_tmp, block_live);
+    if (threadIdx.x == 0) {
+        block_sums[(int64_t)blockIdx.x * 3 + 0] = block_tiles;
+        block_sums[(int64_t)blockIdx.x * 3 + 1] = block_entries;
+        block_sums[(int64_t)blockIdx.x * 3 + 2] = block_live;
     }
     block_count_digits<ITEMS>(k, valid, 0, nbits, counts);
     __syncthreads();
@@ -537,7 +639,6 @@ struct EmitArgs {
     const uint2 *rects;       // packed tile rectangle per Gaussian
     const uint32_t *order;    // Gaussians in depth order
     const uint64_t *offsets;  // first entry of each depth-ordered Gaussian
-    const uint32_t *touched;  // entries per Gaussian (by Gaussian id)
     int64_t n, k;
     int tiles_x;              // width of the grid the entries index
 };
@@ -561,11 +662,12 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(int n_tiles,
     offsets[t] = (int32_t)lo;
 }
 
-__global__ __launch_bounds__(256) void copy_u32_to_i32_kernel(int64_t n,
-                                                              const uint32_t *__restrict__ in,
-                                                              int32_t *__restrict__ out) {
+// tiles_touched per Gaussian from its packed tile rectangle.
+__global__ __launch_bounds__(256) void tiles_from_rects_kernel(int64_t n,
+                                                               const uint2 *__restrict__ rects,
+                                                               int32_t *__restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = (int32_t)in[i];
+    if (i < n) out[i] = (int32_t)rect_tiles(rects[i]);
 }
 
 // ----------------------------------------------------- level 2: tiles
@@ -849,17 +951,16 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
 template <typename KeyT>
 __global__ __launch_bounds__(256) void emit_super_kernel(
     int64_t n, int64_t m, const uint32_t *__restrict__ order,
-    const uint64_t *__restrict__ offsets, const uint32_t *__restrict__ super_touched,
-    const uint2 *__restrict__ rects, int super_x, KeyT *__restrict__ keys_out,
-    uint32_t *__restrict__ vals_out, uint2 *__restrict__ rects_out) {
+    const uint64_t *__restrict__ offsets, const uint2 *__restrict__ rects, int super_x,
+    KeyT *__restrict__ keys_out, uint32_t *__restrict__ vals_out,
+    uint2 *__restrict__ rects_out) {
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= n) return;
     const uint32_t g = order[r];
-    if (g >= (uint64_t)n) return;
-    const uint32_t c = super_touched[g];
+    if (g >= (uint64_t)n) return;  // past the Gaussians with tiles
     const uint2 packed = rects[g];
-    if (c == 0) return;
     const TileRect t = unpack_rect(packed);
+    if (t.tx0 > t.tx1) return;
     int64_t o = (int64_t)offsets[r];
     for (int y = t.ty0 / kSuper; y <= t.ty1 / kSuper; ++y)
         for (int x = t.tx0 / kSuper; x <= t.tx1 / kSuper; ++x, ++o) {
@@ -943,17 +1044,58 @@ __global__ __launch_bounds__(kL1Threads) void l1_count_kernel(L1Args a,
     }
 }
 
+// The level-2 block plan, from block 0 of l1_scatter_kernel (thread d holds
+// supertile d's entry count `tot` and first list position `first`): chunks of
+// kL2Threads list positions per supertile, their exclusive scan chunk_start
+// (chunk_start[n_super] = all chunks) and block_map[b] = (supertile, first
+// list position) of every level-2 block.  Contains __syncthreads().
+__device__ __forceinline__ void l1_block_plan(int n_super, uint32_t tot, uint32_t first,
+                                              uint32_t *scan_tmp, uint32_t *lds_start,
+                                              uint32_t *lds_first,
+                                              uint32_t *__restrict__ chunk_start,
+                                              uint2 *__restrict__ block_map) {
+    const int d = threadIdx.x;
+    const uint32_t c = d < n_super ? (tot + kL2Threads - 1) / kL2Threads : 0u;
+    uint32_t all;
+    const uint32_t b0 = block_exclusive_scan<uint32_t, kL1Threads>(c, scan_tmp, all);
+    if (d < n_super) {
+        lds_start[d] = b0;
+        lds_first[d] = first;
+        chunk_start[d] = b0;
+    }
+    if (d == 0) chunk_start[n_super] = all;
+    __syncthreads();
+    for (uint32_t b = d; b < all; b += kL1Threads) {
+        // the last supertile whose first block is <= b (supertiles without
+        // chunks share their first block with the next one)
+        int lo = 0, hi = n_super - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (lds_start[mid] <= b)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        block_map[b] = make_uint2((uint32_t)lo, lds_first[lo] + (b - lds_start[lo]) * kL2Threads);
+    }
+}
+
 // `hist` holds, after digit_scan_kernel, the first position of (s, block)
 // among the entries of s and `totals` the entries of each s.  Writes
-// super_ids / super_rects and, from block 0, super_off[s] = entries with a
-// smaller supertile.
+// super_ids / super_rects, zeroes the per-tile entry counters of level 2 and,
+// from block 0, super_off[s] = entries with a smaller supertile and the
+// level-2 block plan (l1_block_plan).
 __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
     L1Args a, const uint32_t *__restrict__ hist, const uint32_t *__restrict__ totals,
     int n_super, int32_t *__restrict__ super_ids, uint2 *__restrict__ super_rects,
-    int32_t *__restrict__ super_off) {
+    int32_t *__restrict__ super_off, uint32_t *__restrict__ chunk_start,
+    uint2 *__restrict__ block_map, int n_tiles, uint32_t *__restrict__ tile_counts) {
     __shared__ uint64_t lanes[kL1Waves][kRadixMax];
     __shared__ uint32_t wave_pos[kL1Waves][kRadixMax];
     __shared__ uint32_t scan_tmp[kL1Threads / kWave + 1];
+    for (int64_t t = (int64_t)blockIdx.x * kL1Threads + threadIdx.x; t < n_tiles;
+         t += (int64_t)gridDim.x * kL1Threads)
+        tile_counts[t] = 0u;
     uint32_t g = 0;
     uint2 packed = make_uint2(0u, 0u);
     TileRect sr{0, -1, 0, -1};
@@ -962,6 +1104,12 @@ __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
     const uint32_t tot = d < n_super ? totals[d] : 0u;
     uint32_t all;
     const uint32_t smaller = block_exclusive_scan<uint32_t, kL1Threads>(tot, scan_tmp, all);
+    if (blockIdx.x == 0) {  // uniform per workgroup; wave_pos serves as staging
+        if (d < n_super) super_off[d] = (int32_t)smaller;
+        l1_block_plan(n_super, tot, smaller, scan_tmp, wave_pos[0], wave_pos[1], chunk_start,
+                      block_map);
+        __syncthreads();
+    }
     if (d < kRadixMax) {
         uint32_t pos = smaller + (d < n_super ? hist[hist_index(d, blockIdx.x, a.nblocks)] : 0u);
 #pragma unroll
@@ -969,7 +1117,6 @@ __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
             wave_pos[w][d] = pos;
             pos += (uint32_t)__popcll(lanes[w][d]);
         }
-        if (blockIdx.x == 0 && d < n_super) super_off[d] = (int32_t)smaller;
     }
     __syncthreads();
     if (has) {
@@ -1023,10 +1170,12 @@ struct Carve {
 };
 
 struct CountWs {
-    uint32_t *touched, *super_touched, *dkeys_a, *dvals_a, *dkeys_b, *dvals_b;
-    uint2 *rects;
-    uint2 *rects_depth;  // packed tile rectangles in depth order (one-pass level 1)
+    uint32_t *dkeys_a, *dvals_a, *dkeys_b, *dvals_b;
+    uint2 *rects;        // packed tile rectangle per Gaussian (kEmptyRect: no tiles)
+    uint2 *rects_depth;  // the same in depth order (one-pass level 1)
     uint64_t *counts, *offsets;
+    unsigned long long *block_sums;  // count_tiles: 3 sums per block
+    int64_t *n_live;                 // Gaussians with tiles (keys of depth passes 1..)
     void *sort_ws, *scan_ws;
     size_t bytes;
 };
@@ -1034,8 +1183,6 @@ struct CountWs {
 inline CountWs carve_count(void *base, int64_t n) {
     Carve c{reinterpret_cast<char *>(base)};
     CountWs w;
-    w.touched = c.take<uint32_t>(n);
-    w.super_touched = c.take<uint32_t>(n);
     w.rects = c.take<uint2>(n);
     w.dkeys_a = c.take<uint32_t>(n);
     w.dvals_a = c.take<uint32_t>(n);
@@ -1044,6 +1191,8 @@ inline CountWs carve_count(void *base, int64_t n) {
     w.rects_depth = c.take<uint2>(n);
     w.counts = c.take<uint64_t>(n);
     w.offsets = c.take<uint64_t>(n + 1);
+    w.block_sums = c.take<unsigned long long>(sort_blocks<kDepthItems>(n) * 3);
+    w.n_live = c.take<int64_t>(1);
     w.sort_ws = c.take<char>((int64_t)radix_workspace_bytes<kDepthItems>(n));
     w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint64_t>(n));
     w.bytes = align256(c.off);
@@ -1051,7 +1200,9 @@ inline CountWs carve_count(void *base, int64_t n) {
 }
 
 // The depth sort is 4 passes of 8 bits, so its result ends in the (a) buffers.
+// Its first pass drops keys and its last fills the tail, so they must differ.
 constexpr int kDepthBits = 32;
+static_assert(kDepthBits > kRadixMaxBits, "the depth sort needs at least two passes");
 
 inline bool use_u16_keys(int tile_bits) { return tile_bits <= 16; }
 
@@ -1163,15 +1314,18 @@ int super_sort(const EmitArgs &a, const SortWs &w, int super_bits, int n_super,
     auto vals_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? out : w.vals_tmp; };
     auto rects_for = [&](int p) { return ((P - 1 - p) % 2 == 0) ? super_rects : w.rects_tmp; };
     hipLaunchKernelGGL(emit_super_kernel<KeyT>, dim3(ceil_div(a.n, 256)), dim3(256), 0, stream,
-                       a.n, a.k, a.order, a.offsets, a.touched, a.rects, a.tiles_x, keys_for(-1),
+                       a.n, a.k, a.order, a.offsets, a.rects, a.tiles_x, keys_for(-1),
                        vals_for(-1), rects_for(-1));
     int st = launch_status();
     if (st) return st;
     for (int p = 0; p < P; ++p) {
-        st = radix_pass<KeyT, kTileItems, true>(
-            keys_for(p - 1), vals_for(p - 1), keys_for(p), vals_for(p), a.k,
-            p * plan.bits_per_pass, pass_bits(plan, super_bits, p), true, w.pass_ws, stream,
-            false, nullptr, nullptr, rects_for(p - 1), rects_for(p));
+        PassExtras x;
+        x.pin = rects_for(p - 1);
+        x.pout = rects_for(p);
+        st = radix_pass<KeyT, kTileItems, true>(keys_for(p - 1), vals_for(p - 1), keys_for(p),
+                                                vals_for(p), a.k, p * plan.bits_per_pass,
+                                                pass_bits(plan, super_bits, p), true, w.pass_ws,
+                                                stream, x);
         if (st) return st;
     }
     hipLaunchKernelGGL(tile_ranges_kernel<KeyT>, dim3(ceil_div(n_super, 256)), dim3(256), 0,
@@ -1198,20 +1352,16 @@ extern "C" int gs_bin_count(const float *points_image, const float *radii, const
     if (n > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;  // Gaussian ids are int32
     const CountWs w = carve_count(workspace, n);
     if (n > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
-    int st = zero_bytes(totals, 2 * sizeof(int64_t), stream);
-    if (st || n == 0) return st;
+    if (n == 0) return zero_bytes(totals, 2 * sizeof(int64_t), stream);
     if (!points_image || !radii || !depths || !mask) return GS_ERR_INVALID_ARGUMENT;
     const SortPlan plan = plan_sort(kDepthBits);
     const int nblocks = (int)sort_blocks<kDepthItems>(n);
     const int nb0 = pass_bits(plan, kDepthBits, 0);
     uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
-    unsigned long long *k_total = reinterpret_cast<unsigned long long *>(totals);
-    unsigned long long *m_total = reinterpret_cast<unsigned long long *>(totals + 1);
     hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
                        stream, n, points_image, radii, depths, mask, width, height, tile_size,
-                       w.touched, w.super_touched, w.rects, w.dkeys_a, w.dvals_a, nb0, nblocks,
-                       hist, k_total, m_total);
-    st = launch_status();
+                       w.rects, w.dkeys_a, nb0, nblocks, hist, w.block_sums);
+    int st = launch_status();
     if (st) return st;
     // Up to kRadixMax supertiles level 1 enumerates the entries from the depth
     // order directly (l1_count_kernel), reading the tile rectangles that the last
@@ -1219,17 +1369,34 @@ extern "C" int gs_bin_count(const float *points_image, const float *radii, const
     // counts' exclusive scan in depth order, also written by the last pass.
     Grid grid;
     const bool one_pass_l1 = make_grid(width, height, tile_size, grid) && grid.n_super <= kRadixMax;
-    // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes no keys
+    // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes
+    // no keys.  The first pass takes the histogram count_tiles wrote, numbers the
+    // values itself, drops the Gaussians without tiles and reduces count_tiles'
+    // sums (K, M and the n_live Gaussians with tiles); the others sort n_live keys.
     for (int p = 0; p < plan.passes; ++p) {
         const bool from_a = (p % 2) == 0;
         const bool last = p + 1 == plan.passes;
-        const bool counts = last && !one_pass_l1, rects = last && one_pass_l1;
+        PassExtras x;
+        if (p == 0) {
+            x.hist_ready = true;
+            x.drop_no_tiles = true;
+            x.block_sums = w.block_sums;
+            x.sums_out = totals;
+            x.live_out = w.n_live;
+        } else {
+            x.n_live = w.n_live;
+        }
+        if (last) {
+            x.rects = w.rects;
+            if (one_pass_l1)
+                x.rects_out = w.rects_depth;
+            else
+                x.counts_out = w.counts;
+        }
         st = radix_pass<uint32_t, kDepthItems>(
-            from_a ? w.dkeys_a : w.dkeys_b, from_a ? w.dvals_a : w.dvals_b,
+            from_a ? w.dkeys_a : w.dkeys_b, p == 0 ? nullptr : (from_a ? w.dvals_a : w.dvals_b),
             from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, n,
-            p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream,
-            p == 0, counts ? w.super_touched : nullptr, counts ? w.counts : nullptr, nullptr,
-            nullptr, rects ? w.rects : nullptr, rects ? w.rects_depth : nullptr);
+            p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream, x);
         if (st) return st;
     }
     if (one_pass_l1) return GS_OK;
@@ -1264,14 +1431,15 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
     if (g.tiles_x > 65535 || g.tiles_y > 65535)
         return GS_ERR_UNSUPPORTED;  // tile rectangles are staged with 16-bit coordinates
     if ((k == 0) != (m == 0)) return GS_ERR_INVALID_ARGUMENT;
+    if (l2_blocks_bound(m, g.n_super) > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
     const CountWs cw = carve_count(const_cast<void *>(count_workspace), n);
     const BinWs w = carve_bins(workspace, n, m, g);
     if (m > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
     if (n > 0 && !count_workspace) return GS_ERR_INVALID_ARGUMENT;
     int st;
     if (tiles_touched && n > 0) {
-        hipLaunchKernelGGL(copy_u32_to_i32_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream,
-                           n, cw.touched, tiles_touched);
+        hipLaunchKernelGGL(tiles_from_rects_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream,
+                           n, (const uint2 *)cw.rects, tiles_touched);
         st = launch_status();
         if (st) return st;
     }
@@ -1293,19 +1461,19 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         st = launch_status();
         if (st) return st;
         hipLaunchKernelGGL(digit_scan_kernel, dim3(g.n_super), dim3(kScanThreads), 0, stream,
-                           w.l1_hist, la.nblocks, w.l1_totals);
+                           w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, nullptr);
         st = launch_status();
         if (st) return st;
         hipLaunchKernelGGL(l1_scatter_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
                            (const uint32_t *)w.l1_hist, (const uint32_t *)w.l1_totals, g.n_super,
-                           w.super_ids, w.super_rects, w.super_off);
+                           w.super_ids, w.super_rects, w.super_off, w.chunk_start, w.block_map,
+                           g.n_tiles, w.tile_counts);
         st = launch_status();
     } else {  // emitted entries sorted by supertile over several radix passes
         EmitArgs a;
         a.rects = cw.rects;
         a.order = cw.dvals_a;  // depth order (even number of depth passes)
         a.offsets = cw.offsets;
-        a.touched = cw.super_touched;
         a.n = n;
         a.k = m;
         a.tiles_x = g.super_x;
@@ -1314,16 +1482,16 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
                                         w.super_ids, w.super_rects, stream)
                  : super_sort<uint32_t>(a, w.lvl1, g.super_bits, g.n_super, w.super_off,
                                         w.super_ids, w.super_rects, stream);
+        if (st) return st;
+        // level-2 block plan (the one-pass level 1 writes it itself)
+        hipLaunchKernelGGL(l2_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, g.n_super, m,
+                           w.super_off, w.chunk_start, w.block_map, g.n_tiles, w.tile_counts);
+        st = launch_status();
     }
     if (st) return st;
 
-    // level 2: block plan, per-tile counts, tile offsets and block prefixes, scatter
+    // level 2: per-tile counts, tile offsets and block prefixes, scatter
     const int64_t nb2 = l2_blocks_bound(m, g.n_super);
-    if (nb2 > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
-    hipLaunchKernelGGL(l2_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, g.n_super, m,
-                       w.super_off, w.chunk_start, w.block_map, g.n_tiles, w.tile_counts);
-    st = launch_status();
-    if (st) return st;
     L2Args l2;
     l2.super_off = w.super_off;
     l2.super_ids = w.super_ids;
