@@ -17,7 +17,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "cuda_rasterizer", "libgsraster.so")
-SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "blend.hip", "train.hip"]
+SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "blend.hip", "train.hip", "ssim.hip"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: the preprocess and blend decisions are bit-exact against

@@ -29,6 +29,7 @@ import torch
 
 from . import _lib
 from ._lib import RasterizerError
+from .ssim import fused_ssim
 
 __all__ = [
     "project_points",
@@ -50,6 +51,7 @@ __all__ = [
     "preprocess_backward",
     "rasterize_display_l1",
     "rasterize_l1_backward",
+    "fused_ssim",
     "RasterizerError",
 ]
 

@@ -70,6 +70,9 @@ SIGNATURES.update({
                      ctypes.c_double, _P],
     "gs_accumulate_grad2d": [_P, _P, _I64, _I32, _I32, _P, _P, _P],
     "gs_gather_rows": [_I64, _P, _P, ctypes.POINTER(GsGatherTensor), _I32, _P],
+    "gs_ssim_workspace_size": [_I32, _I32, _I32, _I32, _PSZ],
+    "gs_ssim_forward": [_P] * 4 + [_I32] * 5 + [_P] * 5 + [_SZ, _P],
+    "gs_ssim_backward": [_P] * 5 + [_I32] * 4 + [_P] * 5 + [_P],
 })
 
 _lib = None

@@ -343,6 +343,43 @@ int gs_accumulate_grad2d(const float *grad_points_image, const float *radii, int
 int gs_gather_rows(int64_t n_out, const int32_t *src_rows, const uint8_t *fresh_rows,
                    const GsGatherTensor *tensors, int32_t n_tensors, hipStream_t stream);
 
+/* -------------------------------------------------------------- SSIM loss */
+
+/*
+ * Replace fused_ssim(img1, img2, padding, train) of the third-party package
+ * fused-ssim (fused-ssim==0.0.0, environment.yml:56; not vendored), which the
+ * reference's loss calls at scripts/train.py:193-197 (also
+ * scripts/check_cuda_gradients.py:976-980 and scripts/evaluate.py:57-61).
+ * Images are float32 (batch, channels, height, width) with element strides
+ * strides[0..3] (host arrays of 4; any layout -- the reference passes (H, W, C)
+ * images permuted to (1, C, H, W)).  SSIM per pixel: 11x11 Gaussian window of
+ * standard deviation 1.5 per plane, zero padding, C1 = 0.01^2, C2 = 0.03^2.
+ *
+ * gs_ssim_forward: *ssim_mean (device float) = mean of the SSIM map over every
+ *   pixel (valid_padding = 0) or over the pixels at least 5 from the border
+ *   (valid_padding = 1; NaN when that region is empty).  The three map pointers
+ *   are all NULL or all set; when set, each receives a planar
+ *   (batch * channels, height, width) map -- d mean / d E[x], d mean / d E[x^2]
+ *   and d mean / d E[xy] per pixel, with mu1 = E[x], E[x^2] and E[xy] taken as
+ *   the independent local statistics (zero outside the region) -- for
+ *   gs_ssim_backward.  The mean is reduced in a fixed order (deterministic).
+ * gs_ssim_backward: grad_img1 (element strides grad_strides) = *grad_mean
+ *   (device float) times d(mean SSIM)/d img1.  img2 gets no gradient.
+ * batch * channels must be <= 65535.
+ */
+int gs_ssim_workspace_size(int32_t batch, int32_t channels, int32_t height, int32_t width,
+                           size_t *bytes);
+int gs_ssim_forward(const float *img1, const int64_t *strides1, const float *img2,
+                    const int64_t *strides2, int32_t batch, int32_t channels, int32_t height,
+                    int32_t width, int32_t valid_padding, float *ssim_mean, float *dm_dmu1,
+                    float *dm_dsigma1_sq, float *dm_dsigma12, void *workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+int gs_ssim_backward(const float *grad_mean, const float *img1, const int64_t *strides1,
+                     const float *img2, const int64_t *strides2, int32_t batch, int32_t channels,
+                     int32_t height, int32_t width, const float *dm_dmu1,
+                     const float *dm_dsigma1_sq, const float *dm_dsigma12, float *grad_img1,
+                     const int64_t *grad_strides, hipStream_t stream);
+
 /*
  * Measurement entry (no counterpart in the reference): the work of the
  * reference blend loop (src/cuda/kernel.cu:954-982) for the same inputs as

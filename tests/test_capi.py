@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 6
+    assert lib.gs_abi_version() == 7
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -108,6 +108,20 @@ def test_invalid_arguments_rejected_on_host(lib):
     g = _lib.GsGatherTensor(None, None, None, 0, 0)
     assert lib.gs_gather_rows(10, None, None, ctypes.byref(g), 1, null) == -1
     assert lib.gs_gather_rows(-1, None, None, None, 0, null) == -1
+    # SSIM entries: sizes, plane limit, null buffers, partial map sets
+    assert lib.gs_ssim_workspace_size(1, 3, 64, 64, ctypes.byref(sz)) == 0 and sz.value > 0
+    assert lib.gs_ssim_workspace_size(0, 3, 64, 64, ctypes.byref(sz)) == -1
+    assert lib.gs_ssim_workspace_size(256, 256, 64, 64, ctypes.byref(sz)) == -1  # > 65535 planes
+    st = (ctypes.c_int64 * 4)(3 * 64 * 64, 64 * 64, 64, 1)
+    assert lib.gs_ssim_forward(null, st, null, st, 1, 3, 64, 64, 1, null, null, null, null, null,
+                               0, null) == -1
+    fake = ctypes.c_void_p(256)  # never dereferenced: the host checks fail first
+    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, fake, fake, null, null, fake,
+                               1 << 20, null) == -1  # maps all set or all null
+    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, fake, null, null, null, fake,
+                               0, null) == -2  # workspace too small
+    assert lib.gs_ssim_backward(fake, fake, st, fake, st, 1, 3, 64, 64, fake, fake, null, fake, st,
+                                null) == -1
 
 
 def test_python_layer_refuses_cpu_tensors():
