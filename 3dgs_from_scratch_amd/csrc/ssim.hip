@@ -37,7 +37,9 @@ constexpr int kInY = kTileY + 2 * kRadius;       // staged rows (42)
 constexpr int kPitch = kInX + 1;                 // LDS row pitch of staged values
 constexpr int kQuad = 4;                         // row pass: outputs per thread
 constexpr int kQuadIn = kQuad + 2 * kRadius;     // row pass: inputs per thread (14)
-constexpr int kRowItems = kInY * (kTileX / kQuad);
+constexpr int kQuads = kTileX / kQuad;           // row pass: column groups per row (16)
+constexpr int kRowGroups = (kInY + 3) / 4;       // row pass: groups of 4 rows (one wave each)
+constexpr int kRowItems = kRowGroups * 4 * kQuads;
 constexpr int kStageIters = (kInY * kInX + kThreads - 1) / kThreads;
 constexpr float kC1 = 0.01f * 0.01f;
 constexpr float kC2 = 0.03f * 0.03f;
@@ -65,15 +67,13 @@ Window make_window() {
 
 struct Planes {
     const float *img1, *img2;
-    int64_t s1[4], s2[4];  // element strides (batch, channel, row, column)
+    int64_t s1[2], s2[2];  // element strides of batch and channel
+    int r1, c1, r2, c2;    // element strides of row and column (in-plane offsets fit 31 bits)
     int channels, height, width;
+    int tiles_x, tiles_y, tiles;
     int valid;             // mean over pixels at least kRadius from the border
     float inv_count;       // 1 / pixels in the mean (all planes)
 };
-
-__device__ __forceinline__ int64_t at(const int64_t (&s)[4], int b, int c, int y, int x) {
-    return (int64_t)b * s[0] + (int64_t)c * s[1] + (int64_t)y * s[2] + (int64_t)x * s[3];
-}
 
 __device__ __forceinline__ bool in_region(const Planes &p, int y, int x) {
     if (!p.valid) return true;
@@ -81,13 +81,18 @@ __device__ __forceinline__ bool in_region(const Planes &p, int y, int x) {
 }
 
 // Row pass for NQ quantities: out[q][r][c0 + o] = sum_t w[t] * in_q[r][c0 + o + t],
-// where in_q is produced by `load(k)` for the thread's 14 staged inputs.
-// Items (row, group of 4 columns) are spread over the workgroup.
+// where in_q is produced by `load(r, column)` for the thread's 14 staged inputs.
+// Items (row, group of 4 columns) are spread over the workgroup, 64 per wave:
+// 4 rows x 16 groups, each half-wave taking 8 groups of each of the 4 rows, so
+// that with the odd staging pitch the 32 lanes of a half-wave read 32
+// different banks.
 template <int NQ, typename Load>
 __device__ __forceinline__ void row_pass(const Window &win, float (*out)[kInY][kTileX], Load load) {
     for (int item = threadIdx.x; item < kRowItems; item += kThreads) {
-        const int r = item / (kTileX / kQuad);
-        const int c0 = (item % (kTileX / kQuad)) * kQuad;
+        const int l = item % kWave;
+        const int r = (item / kWave) * 4 + (l % 32) / 8;
+        if (r >= kInY) continue;
+        const int c0 = ((l % 8) + 8 * (l / 32)) * kQuad;
         float acc[NQ][kQuad];
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
@@ -155,84 +160,146 @@ __device__ __forceinline__ double block_sum(double v, double *tmp) {
     return s;
 }
 
+// Tile `t` of the persistent loop: tiles run over (plane, tile row, tile
+// column), column fastest.
+struct Tile {
+    int plane, b, c;
+    int ox, oy;  // first output column / row
+};
+
+__device__ __forceinline__ Tile tile_of(const Planes &p, int t) {
+    Tile r;
+    const int tx = t % p.tiles_x;
+    const int rest = t / p.tiles_x;
+    r.plane = rest / p.tiles_y;
+    r.b = r.plane / p.channels;
+    r.c = r.plane % p.channels;
+    r.ox = tx * kTileX;
+    r.oy = (rest % p.tiles_y) * kTileY;
+    return r;
+}
+
+// Staged window element `it` of this thread: (row, column) in the window and
+// whether it lies in the image.
+__device__ __forceinline__ bool stage_pos(const Planes &p, const Tile &t, int it, int &r,
+                                          int &col, int &gy, int &gx) {
+    const int i = threadIdx.x + it * kThreads;
+    r = i / kInX;
+    col = i % kInX;
+    gy = t.oy - kRadius + r;
+    gx = t.ox - kRadius + col;
+    return i < kInY * kInX && gy >= 0 && gy < p.height && gx >= 0 && gx < p.width;
+}
+
+// Both images' window of tile t (zero outside the image) into registers.
+__device__ __forceinline__ void load_images(const Planes &p, const Tile &t,
+                                            float (&vx)[kStageIters], float (&vy)[kStageIters]) {
+    const float *b1 = p.img1 + ((int64_t)t.b * p.s1[0] + (int64_t)t.c * p.s1[1]);
+    const float *b2 = p.img2 + ((int64_t)t.b * p.s2[0] + (int64_t)t.c * p.s2[1]);
+#pragma unroll
+    for (int it = 0; it < kStageIters; ++it) {
+        int r, col, gy, gx;
+        const bool in = stage_pos(p, t, it, r, col, gy, gx);
+        vx[it] = in ? b1[gy * p.r1 + gx * p.c1] : 0.0f;
+        vy[it] = in ? b2[gy * p.r2 + gx * p.c2] : 0.0f;
+    }
+}
+
+// The three planar derivative maps' window of tile t into registers.
+__device__ __forceinline__ void load_maps(const Planes &p, const Tile &t, const float *m0,
+                                          const float *m1, const float *m2,
+                                          float (&v)[3][kStageIters]) {
+    const int64_t base = (int64_t)t.plane * p.height * p.width;
+#pragma unroll
+    for (int it = 0; it < kStageIters; ++it) {
+        int r, col, gy, gx;
+        const bool in = stage_pos(p, t, it, r, col, gy, gx);
+        const int o = gy * p.width + gx;
+        v[0][it] = in ? m0[base + o] : 0.0f;
+        v[1][it] = in ? m1[base + o] : 0.0f;
+        v[2][it] = in ? m2[base + o] : 0.0f;
+    }
+}
+
+template <int NQ>
+__device__ __forceinline__ void store_stage(float (*dst)[kInY][kPitch],
+                                            const float (&v)[NQ][kStageIters]) {
+#pragma unroll
+    for (int it = 0; it < kStageIters; ++it) {
+        const int i = threadIdx.x + it * kThreads;
+        if (i < kInY * kInX)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) dst[q][i / kInX][i % kInX] = v[q][it];
+    }
+}
+
+// Persistent: workgroup w handles tiles w, w + gridDim.x, ...; the next
+// tile's window is loaded into registers while the current one is filtered.
+// partials[w] = the workgroup's sum of the SSIM map over its region pixels.
 __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window win,
                                                                  float *__restrict__ d_mu,
                                                                  float *__restrict__ d_xx,
                                                                  float *__restrict__ d_xy,
                                                                  double *__restrict__ partials) {
-    __shared__ float sx[kInY][kPitch];
-    __shared__ float sy[kInY][kPitch];
+    __shared__ float stage[2][kInY][kPitch];  // x, y
     __shared__ __align__(16) float rows[5][kInY][kTileX];
     __shared__ double red[kWaves];
-    const int plane = blockIdx.z;
-    const int b = plane / p.channels, c = plane % p.channels;
-    const int x0 = blockIdx.x * kTileX - kRadius, y0 = blockIdx.y * kTileY - kRadius;
-    // stage both images (zero outside), all loads issued before the stores
-    float vx[kStageIters], vy[kStageIters];
-#pragma unroll
-    for (int it = 0; it < kStageIters; ++it) {
-        const int i = threadIdx.x + it * kThreads;
-        const int r = i / kInX, col = i % kInX;
-        const int gy = y0 + r, gx = x0 + col;
-        const bool in = i < kInY * kInX && gy >= 0 && gy < p.height && gx >= 0 && gx < p.width;
-        vx[it] = in ? p.img1[at(p.s1, b, c, gy, gx)] : 0.0f;
-        vy[it] = in ? p.img2[at(p.s2, b, c, gy, gx)] : 0.0f;
-    }
-#pragma unroll
-    for (int it = 0; it < kStageIters; ++it) {
-        const int i = threadIdx.x + it * kThreads;
-        if (i < kInY * kInX) {
-            sx[i / kInX][i % kInX] = vx[it];
-            sy[i / kInX][i % kInX] = vy[it];
-        }
-    }
-    __syncthreads();
-    // row sums of x, y, x^2, y^2, xy
-    row_pass<5>(win, rows, [&](int r, int col, float (&v)[5]) {
-        const float x = sx[r][col], y = sy[r][col];
-        v[0] = x;
-        v[1] = y;
-        v[2] = x * x;
-        v[3] = y * y;
-        v[4] = x * y;
-    });
-    __syncthreads();
-    const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
-    float acc[5][kRowsPerWave];
-    column_pass<5>(win, rows, r0, acc);
-    const int gx = blockIdx.x * kTileX + (int)(threadIdx.x % kWave);
+    float v[2][kStageIters];
+    int t = blockIdx.x;
+    if (t < p.tiles) load_images(p, tile_of(p, t), v[0], v[1]);
     double local = 0.0;
+    const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
+    for (; t < p.tiles; t += gridDim.x) {
+        const Tile tl = tile_of(p, t);
+        __syncthreads();  // the previous tile's row pass is done with `stage`
+        store_stage<2>(stage, v);
+        __syncthreads();
+        if (t + (int)gridDim.x < p.tiles) load_images(p, tile_of(p, t + gridDim.x), v[0], v[1]);
+        // row sums of x, y, x^2, y^2, xy
+        row_pass<5>(win, rows, [&](int r, int col, float (&u)[5]) {
+            const float x = stage[0][r][col], y = stage[1][r][col];
+            u[0] = x;
+            u[1] = y;
+            u[2] = x * x;
+            u[3] = y * y;
+            u[4] = x * y;
+        });
+        __syncthreads();
+        float acc[5][kRowsPerWave];
+        column_pass<5>(win, rows, r0, acc);
+        const int gx = tl.ox + (int)(threadIdx.x % kWave);
+        const int64_t plane_base = (int64_t)tl.plane * p.height * p.width;
 #pragma unroll
-    for (int o = 0; o < kRowsPerWave; ++o) {
-        const int gy = blockIdx.y * kTileY + r0 + o;
-        if (gy >= p.height || gx >= p.width) continue;
-        const float mu1 = acc[0][o], mu2 = acc[1][o];
-        const float s11 = acc[2][o] - mu1 * mu1;
-        const float s22 = acc[3][o] - mu2 * mu2;
-        const float s12 = acc[4][o] - mu1 * mu2;
-        const float C = 2.0f * mu1 * mu2 + kC1;
-        const float D = 2.0f * s12 + kC2;
-        const float A = mu1 * mu1 + mu2 * mu2 + kC1;
-        const float B = s11 + s22 + kC2;
-        const float rA = 1.0f / A, rB = 1.0f / B;
-        const float rAB = rA * rB;
-        const float S = C * D * rAB;
-        const bool in = in_region(p, gy, gx);
-        if (in) local += (double)S;
-        if (d_mu) {
-            // d S / d E[x], d E[x^2], d E[xy] (mu1, E[x^2], E[xy] independent),
-            // times d mean / d S
-            const float g = in ? p.inv_count : 0.0f;
-            const float dm = 2.0f * mu2 * (D - C) * rAB + 2.0f * mu1 * S * (rB - rA);
-            const int64_t o_ = ((int64_t)plane * p.height + gy) * p.width + gx;
-            d_mu[o_] = g * dm;
-            d_xx[o_] = g * (-S * rB);
-            d_xy[o_] = g * (2.0f * C * rAB);
+        for (int o = 0; o < kRowsPerWave; ++o) {
+            const int gy = tl.oy + r0 + o;
+            if (gy >= p.height || gx >= p.width) continue;
+            const float mu1 = acc[0][o], mu2 = acc[1][o];
+            const float s11 = acc[2][o] - mu1 * mu1;
+            const float s22 = acc[3][o] - mu2 * mu2;
+            const float s12 = acc[4][o] - mu1 * mu2;
+            const float C = 2.0f * mu1 * mu2 + kC1;
+            const float D = 2.0f * s12 + kC2;
+            const float A = mu1 * mu1 + mu2 * mu2 + kC1;
+            const float B = s11 + s22 + kC2;
+            const float rA = __builtin_amdgcn_rcpf(A), rB = __builtin_amdgcn_rcpf(B);
+            const float rAB = rA * rB;
+            const float S = C * D * rAB;
+            const bool in = in_region(p, gy, gx);
+            if (in) local += (double)S;
+            if (d_mu) {
+                // d S / d E[x], d E[x^2], d E[xy] (mu1, E[x^2], E[xy] independent),
+                // times d mean / d S
+                const float g = in ? p.inv_count : 0.0f;
+                const float dm = 2.0f * mu2 * (D - C) * rAB + 2.0f * mu1 * S * (rB - rA);
+                const int64_t o_ = plane_base + gy * p.width + gx;
+                d_mu[o_] = g * dm;
+                d_xx[o_] = g * (-S * rB);
+                d_xy[o_] = g * (2.0f * C * rAB);
+            }
         }
     }
     const double s = block_sum(local, red);
-    if (threadIdx.x == 0)
-        partials[((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = s;
+    if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
 // *mean = (sum of partials, fixed order) * inv_count; NaN for an empty region.
@@ -246,89 +313,112 @@ __global__ __launch_bounds__(kThreads) void ssim_mean_kernel(const double *__res
     if (threadIdx.x == 0) *mean = (float)(count > 0.0 ? s / count : __builtin_nan(""));
 }
 
+// Persistent like the forward: the next tile's map window is loaded while the
+// current one is filtered, and a tile's img1 / img2 values at its outputs
+// before its row pass.
 __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     Planes p, Window win, const float *__restrict__ grad_mean, const float *__restrict__ d_mu,
     const float *__restrict__ d_xx, const float *__restrict__ d_xy, float *__restrict__ grad,
-    const int64_t gs0, const int64_t gs1, const int64_t gs2, const int64_t gs3) {
-    __shared__ float sm[3][kInY][kPitch];
+    int64_t gs0, int64_t gs1, int gs2, int gs3) {
+    __shared__ float stage[3][kInY][kPitch];
     __shared__ __align__(16) float rows[3][kInY][kTileX];
-    const int plane = blockIdx.z;
-    const int b = plane / p.channels, c = plane % p.channels;
-    const int x0 = blockIdx.x * kTileX - kRadius, y0 = blockIdx.y * kTileY - kRadius;
-    const float *maps[3] = {d_mu, d_xx, d_xy};
-    const int64_t plane_off = (int64_t)plane * p.height * p.width;
     float v[3][kStageIters];
-#pragma unroll
-    for (int it = 0; it < kStageIters; ++it) {
-        const int i = threadIdx.x + it * kThreads;
-        const int r = i / kInX, col = i % kInX;
-        const int gy = y0 + r, gx = x0 + col;
-        const bool in = i < kInY * kInX && gy >= 0 && gy < p.height && gx >= 0 && gx < p.width;
-        const int64_t o = plane_off + (int64_t)gy * p.width + gx;
-#pragma unroll
-        for (int q = 0; q < 3; ++q) v[q][it] = in ? maps[q][o] : 0.0f;
-    }
-#pragma unroll
-    for (int it = 0; it < kStageIters; ++it) {
-        const int i = threadIdx.x + it * kThreads;
-        if (i < kInY * kInX)
-#pragma unroll
-            for (int q = 0; q < 3; ++q) sm[q][i / kInX][i % kInX] = v[q][it];
-    }
-    __syncthreads();
-    row_pass<3>(win, rows, [&](int r, int col, float (&u)[3]) {
-#pragma unroll
-        for (int q = 0; q < 3; ++q) u[q] = sm[q][r][col];
-    });
-    __syncthreads();
-    const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
-    float acc[3][kRowsPerWave];
-    column_pass<3>(win, rows, r0, acc);
+    int t = blockIdx.x;
+    if (t < p.tiles) load_maps(p, tile_of(p, t), d_mu, d_xx, d_xy, v);
     const float up = *grad_mean;
-    const int gx = blockIdx.x * kTileX + (int)(threadIdx.x % kWave);
-    const int64_t gst[4] = {gs0, gs1, gs2, gs3};
+    const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
+    for (; t < p.tiles; t += gridDim.x) {
+        const Tile tl = tile_of(p, t);
+        const int gx = tl.ox + (int)(threadIdx.x % kWave);
+        const float *b1 = p.img1 + ((int64_t)tl.b * p.s1[0] + (int64_t)tl.c * p.s1[1]);
+        const float *b2 = p.img2 + ((int64_t)tl.b * p.s2[0] + (int64_t)tl.c * p.s2[1]);
+        float xs[kRowsPerWave], ys[kRowsPerWave];
 #pragma unroll
-    for (int o = 0; o < kRowsPerWave; ++o) {
-        const int gy = blockIdx.y * kTileY + r0 + o;
-        if (gy >= p.height || gx >= p.width) continue;
-        const float x = p.img1[at(p.s1, b, c, gy, gx)];
-        const float y = p.img2[at(p.s2, b, c, gy, gx)];
-        const float g = acc[0][o] + 2.0f * x * acc[1][o] + y * acc[2][o];
-        grad[at(gst, b, c, gy, gx)] = up * g;
+        for (int o = 0; o < kRowsPerWave; ++o) {
+            const int gy = tl.oy + r0 + o;
+            const bool in = gy < p.height && gx < p.width;
+            xs[o] = in ? b1[gy * p.r1 + gx * p.c1] : 0.0f;
+            ys[o] = in ? b2[gy * p.r2 + gx * p.c2] : 0.0f;
+        }
+        __syncthreads();
+        store_stage<3>(stage, v);
+        __syncthreads();
+        if (t + (int)gridDim.x < p.tiles)
+            load_maps(p, tile_of(p, t + gridDim.x), d_mu, d_xx, d_xy, v);
+        row_pass<3>(win, rows, [&](int r, int col, float (&u)[3]) {
+#pragma unroll
+            for (int q = 0; q < 3; ++q) u[q] = stage[q][r][col];
+        });
+        __syncthreads();
+        float acc[3][kRowsPerWave];
+        column_pass<3>(win, rows, r0, acc);
+        float *bg = grad + ((int64_t)tl.b * gs0 + (int64_t)tl.c * gs1);
+#pragma unroll
+        for (int o = 0; o < kRowsPerWave; ++o) {
+            const int gy = tl.oy + r0 + o;
+            if (gy >= p.height || gx >= p.width) continue;
+            const float g = acc[0][o] + 2.0f * xs[o] * acc[1][o] + ys[o] * acc[2][o];
+            bg[gy * gs2 + gx * gs3] = up * g;
+        }
     }
 }
 
+// Persistent workgroups: two per CU of a 256-CU MI355X (the LDS use allows
+// two), a fixed count so that the per-workgroup partial sums, and so the mean,
+// do not depend on the device.
+constexpr int kPersistentBlocks = 512;
+
 struct Geometry {
-    dim3 grid;
-    int64_t blocks;
+    int tiles_x, tiles_y, tiles;
+    int blocks;
 };
 
 bool geometry(int32_t batch, int32_t channels, int32_t height, int32_t width, Geometry &g) {
     if (batch <= 0 || channels <= 0 || height <= 0 || width <= 0) return false;
     const int64_t planes = (int64_t)batch * channels;
     if (planes > 65535) return false;
-    g.grid = dim3((unsigned)ceil_div(width, kTileX), (unsigned)ceil_div(height, kTileY),
-                  (unsigned)planes);
-    g.blocks = (int64_t)g.grid.x * g.grid.y * g.grid.z;
+    g.tiles_x = ceil_div(width, kTileX);
+    g.tiles_y = ceil_div(height, kTileY);
+    const int64_t tiles = planes * g.tiles_x * g.tiles_y;
+    if (tiles > 0x7fffffffLL) return false;
+    g.tiles = (int)tiles;
+    g.blocks = g.tiles < kPersistentBlocks ? g.tiles : kPersistentBlocks;
     return true;
 }
 
-bool fill_planes(Planes &p, const float *img1, const int64_t *s1, const float *img2,
-                 const int64_t *s2, int32_t channels, int32_t height, int32_t width,
-                 int32_t valid) {
-    if (!img1 || !img2 || !s1 || !s2) return false;
+// In-plane offsets are 32-bit: strides must be >= 0 and a plane's last element
+// offset below 2^31.
+bool plane_fits(const int64_t *s, int32_t height, int32_t width) {
+    if (s[0] < 0 || s[1] < 0 || s[2] < 0 || s[3] < 0) return false;
+    return s[2] * (int64_t)(height - 1) + s[3] * (int64_t)(width - 1) < 0x7fffffffLL;
+}
+
+int fill_planes(Planes &p, const Geometry &g, const float *img1, const int64_t *s1,
+                const float *img2, const int64_t *s2, int32_t channels, int32_t height,
+                int32_t width, int32_t valid) {
+    if (!img1 || !img2 || !s1 || !s2) return GS_ERR_INVALID_ARGUMENT;
+    if (!plane_fits(s1, height, width) || !plane_fits(s2, height, width) ||
+        (int64_t)height * width >= 0x7fffffffLL)
+        return GS_ERR_UNSUPPORTED;
     p.img1 = img1;
     p.img2 = img2;
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
         p.s1[i] = s1[i];
         p.s2[i] = s2[i];
     }
+    p.r1 = (int)s1[2];
+    p.c1 = (int)s1[3];
+    p.r2 = (int)s2[2];
+    p.c2 = (int)s2[3];
     p.channels = channels;
     p.height = height;
     p.width = width;
+    p.tiles_x = g.tiles_x;
+    p.tiles_y = g.tiles_y;
+    p.tiles = g.tiles;
     p.valid = valid ? 1 : 0;
     p.inv_count = 0.0f;
-    return true;
+    return GS_OK;
 }
 
 double region_pixels(int32_t batch, int32_t channels, int32_t height, int32_t width,
@@ -360,9 +450,11 @@ extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const
                                hipStream_t stream) {
     Geometry g;
     Planes p;
-    if (!geometry(batch, channels, height, width, g) || !ssim_mean ||
-        !fill_planes(p, img1, strides1, img2, strides2, channels, height, width, valid_padding))
+    if (!geometry(batch, channels, height, width, g) || !ssim_mean)
         return GS_ERR_INVALID_ARGUMENT;
+    int st = fill_planes(p, g, img1, strides1, img2, strides2, channels, height, width,
+                         valid_padding);
+    if (st) return st;
     if ((dm_dmu1 != nullptr) != (dm_dsigma1_sq != nullptr) ||
         (dm_dmu1 != nullptr) != (dm_dsigma12 != nullptr))
         return GS_ERR_INVALID_ARGUMENT;
@@ -371,12 +463,12 @@ extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const
     const double count = region_pixels(batch, channels, height, width, valid_padding != 0);
     p.inv_count = count > 0.0 ? (float)(1.0 / count) : 0.0f;
     double *partials = reinterpret_cast<double *>(workspace);
-    hipLaunchKernelGGL(ssim_forward_kernel, g.grid, dim3(kThreads), 0, stream, p, make_window(),
-                       dm_dmu1, dm_dsigma1_sq, dm_dsigma12, partials);
-    int st = launch_status();
+    hipLaunchKernelGGL(ssim_forward_kernel, dim3(g.blocks), dim3(kThreads), 0, stream, p,
+                       make_window(), dm_dmu1, dm_dsigma1_sq, dm_dsigma12, partials);
+    st = launch_status();
     if (st) return st;
     hipLaunchKernelGGL(ssim_mean_kernel, dim3(1), dim3(kThreads), 0, stream,
-                       (const double *)partials, g.blocks, count, ssim_mean);
+                       (const double *)partials, (int64_t)g.blocks, count, ssim_mean);
     return launch_status();
 }
 
@@ -389,13 +481,15 @@ extern "C" int gs_ssim_backward(const float *grad_mean, const float *img1,
                                 hipStream_t stream) {
     Geometry g;
     Planes p;
-    if (!geometry(batch, channels, height, width, g) ||
-        !fill_planes(p, img1, strides1, img2, strides2, channels, height, width, 0))
-        return GS_ERR_INVALID_ARGUMENT;
+    if (!geometry(batch, channels, height, width, g)) return GS_ERR_INVALID_ARGUMENT;
+    int st = fill_planes(p, g, img1, strides1, img2, strides2, channels, height, width, 0);
+    if (st) return st;
     if (!grad_mean || !dm_dmu1 || !dm_dsigma1_sq || !dm_dsigma12 || !grad_img1 || !grad_strides)
         return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(ssim_backward_kernel, g.grid, dim3(kThreads), 0, stream, p, make_window(),
-                       grad_mean, dm_dmu1, dm_dsigma1_sq, dm_dsigma12, grad_img1,
-                       grad_strides[0], grad_strides[1], grad_strides[2], grad_strides[3]);
+    if (!plane_fits(grad_strides, height, width)) return GS_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(ssim_backward_kernel, dim3(g.blocks), dim3(kThreads), 0, stream, p,
+                       make_window(), grad_mean, dm_dmu1, dm_dsigma1_sq, dm_dsigma12, grad_img1,
+                       grad_strides[0], grad_strides[1], (int)grad_strides[2],
+                       (int)grad_strides[3]);
     return launch_status();
 }
