@@ -12,7 +12,9 @@ training loop does it (PyTorch activations and l1_loss around the drop-in
 render()) is timed beside it ("drop_in").  The configuration-5 training
 stress run (2000 steps of render + L1 + backward + Adam with clone / prune
 every 100 steps, through the library and through the reference's loop) is
-reported in the same line as "train_stress".  Prints ONE JSON line.
+reported in the same line as "train_stress", and the SSIM loss term of the
+reference's training loss (fused_ssim at 1920x1080, forward and backward) as
+"ssim".  Prints ONE JSON line.
 
 Scene generators for BASELINE configurations 1-5 live here too (tests import
 them).  Every tensor is drawn on the CPU with torch.Generator().manual_seed(seed)
@@ -272,6 +274,51 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused") -> dict:
                 n=scene["params"]["means"].shape[0], n_visible=int(mask.sum()), keys=int(ids.numel()),
                 n_tiles=int(off.numel()), visited=visited, composited=composited,
                 loss=float(loss.detach()), width=cam["width"], height=cam["height"])
+
+
+def run_ssim(scene: dict, steps: int, warmup: int) -> dict:
+    """The reference's SSIM loss term (scripts/train.py:193-197) at the scene's
+    resolution: fused_ssim(img.permute(2, 0, 1)[None], target.permute(2, 0, 1)[None],
+    padding="valid") forward and backward on (H, W, 3) float32 images resident
+    in HBM, timed with HIP events around each entry point.  Algorithmic HBM
+    bytes: forward reads both images and writes three derivative maps (5 images'
+    worth), backward reads the maps and both images and writes the gradient (6)."""
+    from cuda_rasterizer import _lib
+    from cuda_rasterizer import fused_ssim
+
+    dev = torch.device("cuda:0")
+    W, H = scene["camera"]["width"], scene["camera"]["height"]
+    g = torch.Generator().manual_seed(5)
+    target = scene["target"].to(dev)
+    img = (scene["target"] + 0.1 * torch.randn(scene["target"].shape, generator=g)).clamp(0, 1).to(dev)
+    img.requires_grad_(True)
+
+    def step():
+        img.grad = None
+        v = 1.0 - fused_ssim(img.permute(2, 0, 1).unsqueeze(0), target.permute(2, 0, 1).unsqueeze(0),
+                             padding="valid")
+        v.backward()
+        return v
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.timer.reset()
+    _lib.timer.only = None
+    _lib.timer.enabled = True
+    for _ in range(steps):
+        v = step()
+    _lib.timer.enabled = False
+    st = _lib.timer.summary()
+    image_bytes = H * W * 3 * 4
+    out = {"workload": f"{W}x{H}x3 (H, W, C) permuted to (1, 3, H, W), padding valid",
+           "ssim": round(1.0 - float(v.detach()), 6)}
+    for name, mult in (("ssim_forward", 5), ("ssim_backward", 6)):
+        ms = st[name][1] / steps
+        gbs = mult * image_bytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 4), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "bytes": mult * image_bytes}
+    return out
 
 
 # ------------------------------------------------- configuration 5 (training)
@@ -648,6 +695,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the configuration-5 training stress run beside the headline")
+    ap.add_argument("--no-ssim", action="store_true",
+                    help="skip timing the SSIM loss term at the headline resolution")
     ap.add_argument("--train-steps", type=int, default=2000)
     ap.add_argument("--train-path", choices=["both", "fused", "drop-in"], default="both",
                     help="which loops the training stress run times")
@@ -680,6 +729,7 @@ def main(argv=None):
         d = run_gpu(scene, args.steps, args.warmup, "drop-in")
         drop_in = {"ms_per_step": round(d["ms"], 3), "loss": d["loss"],
                    "stages": roofline(d, scene["name"])["per_stage"]}
+    ssim = None if args.no_ssim else run_ssim(scene, args.steps, args.warmup)
     train = None
     if not args.no_train and args.path == "fused":
         train = train_stress(args.train_steps, args.train_path)
@@ -710,6 +760,7 @@ def main(argv=None):
         "stages": rl["per_stage"],
         "loss": res["loss"],
         "drop_in": drop_in,
+        "ssim": ssim,
         "train_stress": train,
         "cpu_baseline": cpu,
     }
