@@ -9,12 +9,14 @@
 // with zero padding, C1 = 0.01^2, C2 = 0.03^2, averaged over all pixels or
 // over the pixels at least 5 from the border.
 //
-// Layout.  A workgroup of 256 threads (4 waves) owns a 64 x 32 output tile of
-// one plane.  It stages the 74 x 42 input window of both images in LDS (any
-// element strides: the reference hands (H, W, C) images permuted to
-// (1, C, H, W)), filters rows (each thread 4 consecutive outputs of a row, so
-// every staged value is loaded and squared once per thread), stores the five
-// row sums, then filters columns (lane = column, each wave 8 output rows).
+// Layout.  Work is cut into 64 x 32 output tiles of one plane; a fixed number
+// of persistent workgroups of 256 threads (4 waves) each walk a contiguous run
+// of tiles, channel index fastest.  Per tile a workgroup stages the 74 x 42
+// input window of both images in LDS (any element strides: the reference hands
+// (H, W, C) images permuted to (1, C, H, W)), filters rows (each thread 4
+// consecutive outputs of a row, so every staged value is loaded and squared
+// once per thread), stores the five row sums, then filters columns (lane =
+// column, each wave 8 output rows); the next tile's window is loaded meanwhile.
 // The forward writes per-pixel derivative maps (planar, coalesced) for the
 // backward, which filters them back the same way.  The mean is reduced
 // deterministically: per-workgroup double partials, then one workgroup.
@@ -160,8 +162,11 @@ __device__ __forceinline__ double block_sum(double v, double *tmp) {
     return s;
 }
 
-// Tile `t` of the persistent loop: tiles run over (plane, tile row, tile
-// column), column fastest.
+// Tile `t`: tiles run over (batch, tile row, tile column, channel), channel
+// fastest, and each workgroup takes a contiguous run of them (tile_range), so
+// the channels of one region -- interleaved in memory for (H, W, C) images --
+// and the halo shared with the next region are read back to back by one
+// workgroup and come from its XCD's L2 after the first read.
 struct Tile {
     int plane, b, c;
     int ox, oy;  // first output column / row
@@ -169,14 +174,22 @@ struct Tile {
 
 __device__ __forceinline__ Tile tile_of(const Planes &p, int t) {
     Tile r;
-    const int tx = t % p.tiles_x;
-    const int rest = t / p.tiles_x;
-    r.plane = rest / p.tiles_y;
-    r.b = r.plane / p.channels;
-    r.c = r.plane % p.channels;
+    r.c = t % p.channels;
+    const int rest = t / p.channels;
+    const int tx = rest % p.tiles_x;
+    const int rest2 = rest / p.tiles_x;
+    r.b = rest2 / p.tiles_y;
+    r.plane = r.b * p.channels + r.c;
     r.ox = tx * kTileX;
-    r.oy = (rest % p.tiles_y) * kTileY;
+    r.oy = (rest2 % p.tiles_y) * kTileY;
     return r;
+}
+
+// This workgroup's tiles [t0, t1).
+__device__ __forceinline__ void tile_range(const Planes &p, int &t0, int &t1) {
+    const int per = (p.tiles + (int)gridDim.x - 1) / (int)gridDim.x;
+    t0 = min((int)blockIdx.x * per, p.tiles);
+    t1 = min(t0 + per, p.tiles);
 }
 
 // Staged window element `it` of this thread: (row, column) in the window and
@@ -233,9 +246,9 @@ __device__ __forceinline__ void store_stage(float (*dst)[kInY][kPitch],
     }
 }
 
-// Persistent: workgroup w handles tiles w, w + gridDim.x, ...; the next
-// tile's window is loaded into registers while the current one is filtered.
-// partials[w] = the workgroup's sum of the SSIM map over its region pixels.
+// Persistent: workgroup w handles its tile_range; the next tile's window is
+// loaded into registers while the current one is filtered.  partials[w] = the
+// workgroup's sum of the SSIM map over its region pixels.
 __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window win,
                                                                  float *__restrict__ d_mu,
                                                                  float *__restrict__ d_xx,
@@ -245,16 +258,17 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
     __shared__ __align__(16) float rows[5][kInY][kTileX];
     __shared__ double red[kWaves];
     float v[2][kStageIters];
-    int t = blockIdx.x;
-    if (t < p.tiles) load_images(p, tile_of(p, t), v[0], v[1]);
+    int t0, t1;
+    tile_range(p, t0, t1);
+    if (t0 < t1) load_images(p, tile_of(p, t0), v[0], v[1]);
     double local = 0.0;
     const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
-    for (; t < p.tiles; t += gridDim.x) {
+    for (int t = t0; t < t1; ++t) {
         const Tile tl = tile_of(p, t);
         __syncthreads();  // the previous tile's row pass is done with `stage`
         store_stage<2>(stage, v);
         __syncthreads();
-        if (t + (int)gridDim.x < p.tiles) load_images(p, tile_of(p, t + gridDim.x), v[0], v[1]);
+        if (t + 1 < t1) load_images(p, tile_of(p, t + 1), v[0], v[1]);
         // row sums of x, y, x^2, y^2, xy
         row_pass<5>(win, rows, [&](int r, int col, float (&u)[5]) {
             const float x = stage[0][r][col], y = stage[1][r][col];
@@ -323,11 +337,12 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     __shared__ float stage[3][kInY][kPitch];
     __shared__ __align__(16) float rows[3][kInY][kTileX];
     float v[3][kStageIters];
-    int t = blockIdx.x;
-    if (t < p.tiles) load_maps(p, tile_of(p, t), d_mu, d_xx, d_xy, v);
+    int t0, t1;
+    tile_range(p, t0, t1);
+    if (t0 < t1) load_maps(p, tile_of(p, t0), d_mu, d_xx, d_xy, v);
     const float up = *grad_mean;
     const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
-    for (; t < p.tiles; t += gridDim.x) {
+    for (int t = t0; t < t1; ++t) {
         const Tile tl = tile_of(p, t);
         const int gx = tl.ox + (int)(threadIdx.x % kWave);
         const float *b1 = p.img1 + ((int64_t)tl.b * p.s1[0] + (int64_t)tl.c * p.s1[1]);
@@ -343,8 +358,7 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
         __syncthreads();
         store_stage<3>(stage, v);
         __syncthreads();
-        if (t + (int)gridDim.x < p.tiles)
-            load_maps(p, tile_of(p, t + gridDim.x), d_mu, d_xx, d_xy, v);
+        if (t + 1 < t1) load_maps(p, tile_of(p, t + 1), d_mu, d_xx, d_xy, v);
         row_pass<3>(win, rows, [&](int r, int col, float (&u)[3]) {
 #pragma unroll
             for (int q = 0; q < 3; ++q) u[q] = stage[q][r][col];
