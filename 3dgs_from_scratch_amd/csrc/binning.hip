@@ -1169,6 +1169,8 @@ struct Carve {
     }
 };
 
+inline int64_t l1_blocks(int64_t n) { return (n + kL1Threads - 1) / kL1Threads; }
+
 struct CountWs {
     uint32_t *dkeys_a, *dvals_a, *dkeys_b, *dvals_b;
     uint2 *rects;        // packed tile rectangle per Gaussian (kEmptyRect: no tiles)
@@ -1176,6 +1178,8 @@ struct CountWs {
     uint64_t *counts, *offsets;
     unsigned long long *block_sums;  // count_tiles: 3 sums per block
     int64_t *n_live;                 // Gaussians with tiles (keys of depth passes 1..)
+    uint32_t *l1_hist;               // one-pass level 1: kRadixMax x l1_blocks(n) table
+    uint32_t *l1_totals;             // one-pass level 1: entries per supertile
     void *sort_ws, *scan_ws;
     size_t bytes;
 };
@@ -1193,10 +1197,25 @@ inline CountWs carve_count(void *base, int64_t n) {
     w.offsets = c.take<uint64_t>(n + 1);
     w.block_sums = c.take<unsigned long long>(sort_blocks<kDepthItems>(n) * 3);
     w.n_live = c.take<int64_t>(1);
+    w.l1_hist = c.take<uint32_t>(kRadixMax * l1_blocks(n));
+    w.l1_totals = c.take<uint32_t>(kRadixMax);
     w.sort_ws = c.take<char>((int64_t)radix_workspace_bytes<kDepthItems>(n));
     w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint64_t>(n));
     w.bytes = align256(c.off);
     return w;
+}
+
+// One-pass level-1 arguments over the depth order the count workspace holds
+// (the last depth pass writes into the (a) buffers); m bounds the scatter.
+inline L1Args l1_args(const CountWs &cw, int64_t n, int64_t m, int super_x) {
+    L1Args la;
+    la.order = cw.dvals_a;
+    la.rects_depth = cw.rects_depth;
+    la.n = n;
+    la.m = m;
+    la.super_x = super_x;
+    la.nblocks = (int)l1_blocks(n);
+    return la;
 }
 
 // The depth sort is 4 passes of 8 bits, so its result ends in the (a) buffers.
@@ -1253,12 +1272,9 @@ inline int64_t l2_blocks_bound(int64_t m, int n_super) {
     return (m + kL2Threads - 1) / kL2Threads + n_super;
 }
 
-inline int64_t l1_blocks(int64_t n) { return (n + kL1Threads - 1) / kL1Threads; }
 
 struct BinWs {
     SortWs lvl1;            // general level 1 (more than kRadixMax supertiles)
-    uint32_t *l1_hist;      // one-pass level 1: kRadixMax x l1_blocks(n) table
-    uint32_t *l1_totals;    // one-pass level 1: entries per supertile
     int32_t *super_off;     // n_super (+1 spare)
     int32_t *super_ids;     // m
     uint2 *super_rects;     // m: packed tile rectangle of each super_ids entry
@@ -1273,12 +1289,8 @@ struct BinWs {
 inline BinWs carve_bins(void *base, int64_t n, int64_t m, const Grid &g) {
     Carve c{reinterpret_cast<char *>(base)};
     BinWs w{};
-    if (g.n_super <= kRadixMax) {
-        w.l1_hist = c.take<uint32_t>(kRadixMax * l1_blocks(n));
-        w.l1_totals = c.take<uint32_t>(kRadixMax);
-    } else {
-        w.lvl1 = carve_sort(c, m, g.super_bits);
-    }
+    (void)n;
+    if (g.n_super > kRadixMax) w.lvl1 = carve_sort(c, m, g.super_bits);
     w.super_off = c.take<int32_t>((int64_t)g.n_super + 1);
     w.super_ids = c.take<int32_t>(m);
     w.super_rects = c.take<uint2>(m);
@@ -1343,66 +1355,150 @@ extern "C" int gs_bin_count_workspace_size(int64_t n, size_t *bytes) {
     return GS_OK;
 }
 
+namespace gs {
+
+// Arguments shared by the two phases of gs_bin_count.
+struct CountCall {
+    const float *points_image, *radii, *depths;
+    const uint8_t *mask;
+    int64_t n;
+    int32_t width, height, tile_size;
+    void *workspace;
+    size_t workspace_bytes;
+    int64_t *totals;
+};
+
+int check_count_call(const CountCall &c, CountWs &w) {
+    if (c.n < 0 || c.width <= 0 || c.height <= 0 || c.tile_size <= 0 || !c.totals)
+        return GS_ERR_INVALID_ARGUMENT;
+    if (c.n > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;  // Gaussian ids are int32
+    w = carve_count(c.workspace, c.n);
+    if (c.n > 0 && (!c.workspace || c.workspace_bytes < w.bytes))
+        return GS_ERR_WORKSPACE_TOO_SMALL;
+    if (c.n > 0 && (!c.points_image || !c.radii || !c.depths || !c.mask))
+        return GS_ERR_INVALID_ARGUMENT;
+    return GS_OK;
+}
+
+// Up to kRadixMax supertiles level 1 enumerates the entries from the depth
+// order directly (l1_count_kernel), reading the tile rectangles that the last
+// pass writes in depth order; otherwise it places them with the supertile
+// counts' exclusive scan in depth order, also written by the last pass.
+bool one_pass_level1(const CountCall &c, Grid &grid) {
+    return make_grid(c.width, c.height, c.tile_size, grid) && grid.n_super <= kRadixMax;
+}
+
+// Depth pass p of 4 (8 bits each): (a) -> (b) -> (a) -> (b) -> (a); the last
+// pass writes no keys.  The first pass takes the histogram count_tiles wrote,
+// numbers the values itself, drops the Gaussians without tiles and reduces
+// count_tiles' sums (K, M and the n_live Gaussians with tiles); the others sort
+// n_live keys.
+int depth_pass(const CountCall &c, const CountWs &w, int p, bool one_pass_l1,
+               hipStream_t stream) {
+    const SortPlan plan = plan_sort(kDepthBits);
+    const bool from_a = (p % 2) == 0;
+    const bool last = p + 1 == plan.passes;
+    PassExtras x;
+    if (p == 0) {
+        x.hist_ready = true;
+        x.drop_no_tiles = true;
+        x.block_sums = w.block_sums;
+        x.sums_out = c.totals;
+        x.live_out = w.n_live;
+    } else {
+        x.n_live = w.n_live;
+    }
+    if (last) {
+        x.rects = w.rects;
+        if (one_pass_l1)
+            x.rects_out = w.rects_depth;
+        else
+            x.counts_out = w.counts;
+    }
+    return radix_pass<uint32_t, kDepthItems>(
+        from_a ? w.dkeys_a : w.dkeys_b, p == 0 ? nullptr : (from_a ? w.dvals_a : w.dvals_b),
+        from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, c.n,
+        p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream, x);
+}
+
+// Phase 1: tile rectangles, depth keys, the first depth pass; totals are final.
+int bin_count_begin(const CountCall &c, hipStream_t stream) {
+    CountWs w;
+    int st = check_count_call(c, w);
+    if (st) return st;
+    if (c.n == 0) return zero_bytes(c.totals, 2 * sizeof(int64_t), stream);
+    const SortPlan plan = plan_sort(kDepthBits);
+    const int nblocks = (int)sort_blocks<kDepthItems>(c.n);
+    const int nb0 = pass_bits(plan, kDepthBits, 0);
+    uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
+    hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
+                       stream, c.n, c.points_image, c.radii, c.depths, c.mask, c.width, c.height,
+                       c.tile_size, w.rects, w.dkeys_a, nb0, nblocks, hist, w.block_sums);
+    st = launch_status();
+    if (st) return st;
+    Grid grid;
+    return depth_pass(c, w, 0, one_pass_level1(c, grid), stream);
+}
+
+// Phase 2: the other depth passes, then the one-pass level 1's counts and
+// positions (they need neither K nor M) or the general level 1's entry offsets.
+int bin_count_finish(const CountCall &c, hipStream_t stream) {
+    CountWs w;
+    int st = check_count_call(c, w);
+    if (st || c.n == 0) return st;
+    Grid grid;
+    const bool one_pass_l1 = one_pass_level1(c, grid);
+    const SortPlan plan = plan_sort(kDepthBits);
+    for (int p = 1; p < plan.passes; ++p) {
+        st = depth_pass(c, w, p, one_pass_l1, stream);
+        if (st) return st;
+    }
+    if (one_pass_l1) {
+        const L1Args la = l1_args(w, c.n, 0, grid.super_x);
+        hipLaunchKernelGGL(l1_count_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
+                           w.l1_hist);
+        st = launch_status();
+        if (st) return st;
+        hipLaunchKernelGGL(digit_scan_kernel, dim3(grid.n_super), dim3(kScanThreads), 0, stream,
+                           w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, nullptr);
+        return launch_status();
+    }
+    // supertile entry offsets in depth order (the total equals count_tiles' M)
+    return scan_exclusive<uint64_t>(w.counts, w.offsets, c.n,
+                                    reinterpret_cast<uint64_t *>(c.totals + 1), w.scan_ws, stream);
+}
+
+}  // namespace gs
+
+
 extern "C" int gs_bin_count(const float *points_image, const float *radii, const float *depths,
                             const uint8_t *mask, int64_t n, int32_t width, int32_t height,
                             int32_t tile_size, void *workspace, size_t workspace_bytes,
                             int64_t *totals, hipStream_t stream) {
-    if (n < 0 || width <= 0 || height <= 0 || tile_size <= 0 || !totals)
-        return GS_ERR_INVALID_ARGUMENT;
-    if (n > 0x7fffffffLL) return GS_ERR_INVALID_ARGUMENT;  // Gaussian ids are int32
-    const CountWs w = carve_count(workspace, n);
-    if (n > 0 && (!workspace || workspace_bytes < w.bytes)) return GS_ERR_WORKSPACE_TOO_SMALL;
-    if (n == 0) return zero_bytes(totals, 2 * sizeof(int64_t), stream);
-    if (!points_image || !radii || !depths || !mask) return GS_ERR_INVALID_ARGUMENT;
-    const SortPlan plan = plan_sort(kDepthBits);
-    const int nblocks = (int)sort_blocks<kDepthItems>(n);
-    const int nb0 = pass_bits(plan, kDepthBits, 0);
-    uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
-    hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
-                       stream, n, points_image, radii, depths, mask, width, height, tile_size,
-                       w.rects, w.dkeys_a, nb0, nblocks, hist, w.block_sums);
-    int st = launch_status();
-    if (st) return st;
-    // Up to kRadixMax supertiles level 1 enumerates the entries from the depth
-    // order directly (l1_count_kernel), reading the tile rectangles that the last
-    // pass writes in depth order; otherwise it places them with the supertile
-    // counts' exclusive scan in depth order, also written by the last pass.
-    Grid grid;
-    const bool one_pass_l1 = make_grid(width, height, tile_size, grid) && grid.n_super <= kRadixMax;
-    // 4 passes of 8 bits: (a) -> (b) -> (a) -> (b) -> (a); the last pass writes
-    // no keys.  The first pass takes the histogram count_tiles wrote, numbers the
-    // values itself, drops the Gaussians without tiles and reduces count_tiles'
-    // sums (K, M and the n_live Gaussians with tiles); the others sort n_live keys.
-    for (int p = 0; p < plan.passes; ++p) {
-        const bool from_a = (p % 2) == 0;
-        const bool last = p + 1 == plan.passes;
-        PassExtras x;
-        if (p == 0) {
-            x.hist_ready = true;
-            x.drop_no_tiles = true;
-            x.block_sums = w.block_sums;
-            x.sums_out = totals;
-            x.live_out = w.n_live;
-        } else {
-            x.n_live = w.n_live;
-        }
-        if (last) {
-            x.rects = w.rects;
-            if (one_pass_l1)
-                x.rects_out = w.rects_depth;
-            else
-                x.counts_out = w.counts;
-        }
-        st = radix_pass<uint32_t, kDepthItems>(
-            from_a ? w.dkeys_a : w.dkeys_b, p == 0 ? nullptr : (from_a ? w.dvals_a : w.dvals_b),
-            from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, n,
-            p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream, x);
-        if (st) return st;
-    }
-    if (one_pass_l1) return GS_OK;
-    // supertile entry offsets in depth order (the total equals count_tiles' M)
-    return scan_exclusive<uint64_t>(w.counts, w.offsets, n,
-                                    reinterpret_cast<uint64_t *>(totals + 1), w.scan_ws, stream);
+    const CountCall c{points_image, radii, depths, mask, n, width, height, tile_size, workspace,
+                      workspace_bytes, totals};
+    const int st = bin_count_begin(c, stream);
+    return st ? st : bin_count_finish(c, stream);
+}
+
+extern "C" int gs_bin_count_begin(const float *points_image, const float *radii,
+                                  const float *depths, const uint8_t *mask, int64_t n,
+                                  int32_t width, int32_t height, int32_t tile_size,
+                                  void *workspace, size_t workspace_bytes, int64_t *totals,
+                                  hipStream_t stream) {
+    const CountCall c{points_image, radii, depths, mask, n, width, height, tile_size, workspace,
+                      workspace_bytes, totals};
+    return bin_count_begin(c, stream);
+}
+
+extern "C" int gs_bin_count_finish(const float *points_image, const float *radii,
+                                   const float *depths, const uint8_t *mask, int64_t n,
+                                   int32_t width, int32_t height, int32_t tile_size,
+                                   void *workspace, size_t workspace_bytes, int64_t *totals,
+                                   hipStream_t stream) {
+    const CountCall c{points_image, radii, depths, mask, n, width, height, tile_size, workspace,
+                      workspace_bytes, totals};
+    return bin_count_finish(c, stream);
 }
 
 extern "C" int gs_bin_sort_workspace_size(int64_t n, int64_t k, int64_t m, int32_t width,
@@ -1448,26 +1544,12 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         return GS_ERR_INVALID_ARGUMENT;
 
     // level 1: (supertile, Gaussian) entries in depth order, stably sorted by supertile
-    if (g.n_super <= kRadixMax) {
-        L1Args la;
-        la.order = cw.dvals_a;  // depth order (even number of depth passes)
-        la.rects_depth = cw.rects_depth;
-        la.n = n;
-        la.m = m;
-        la.super_x = g.super_x;
-        la.nblocks = (int)l1_blocks(n);
-        hipLaunchKernelGGL(l1_count_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
-                           w.l1_hist);
-        st = launch_status();
-        if (st) return st;
-        hipLaunchKernelGGL(digit_scan_kernel, dim3(g.n_super), dim3(kScanThreads), 0, stream,
-                           w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, nullptr);
-        st = launch_status();
-        if (st) return st;
+    if (g.n_super <= kRadixMax) {  // counts and positions came from gs_bin_count
+        const L1Args la = l1_args(cw, n, m, g.super_x);
         hipLaunchKernelGGL(l1_scatter_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
-                           (const uint32_t *)w.l1_hist, (const uint32_t *)w.l1_totals, g.n_super,
-                           w.super_ids, w.super_rects, w.super_off, w.chunk_start, w.block_map,
-                           g.n_tiles, w.tile_counts);
+                           (const uint32_t *)cw.l1_hist, (const uint32_t *)cw.l1_totals,
+                           g.n_super, w.super_ids, w.super_rects, w.super_off, w.chunk_start,
+                           w.block_map, g.n_tiles, w.tile_counts);
         st = launch_status();
     } else {  // emitted entries sorted by supertile over several radix passes
         EmitArgs a;

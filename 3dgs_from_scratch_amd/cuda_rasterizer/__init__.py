@@ -273,17 +273,21 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         _lib.check(lib.gs_bin_count_workspace_size(n, ctypes.byref(sz)), "workspace query")
         ws_count = torch.empty((max(sz.value, 1),), dtype=torch.uint8, device=dev)
         totals = torch.empty((2,), dtype=torch.int64, device=dev)
+        args = (_ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
+                tile_size, _ptr(ws_count), sz.value, _ptr(totals), stream)
         ev = _lib.timer.record("bin_count", dev)
-        _lib.check(
-            lib.gs_bin_count(
-                _ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
-                tile_size, _ptr(ws_count), sz.value, _ptr(totals), stream,
-            ),
-            "compute_tile_intersection (count)",
-        )
+        _lib.check(lib.gs_bin_count_begin(*args), "compute_tile_intersection (count)")
+        # the one host read (src/cuda/rasterizer.cpp:322): K keys and M supertile
+        # entries are final after the first phase; their copy is queued there and
+        # waited for after the second phase is queued, so the GPU keeps working
+        host_totals = torch.empty((2,), dtype=torch.int64, pin_memory=True)
+        host_totals.copy_(totals, non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(dev))
+        _lib.check(lib.gs_bin_count_finish(*args), "compute_tile_intersection (count)")
         _lib.timer.stop(ev, dev)
-        # the one host synchronisation (src/cuda/rasterizer.cpp:322): K keys, M supertile entries
-        k, m = (int(v) for v in totals.tolist())
+        ready.synchronize()
+        k, m = (int(v) for v in host_totals.tolist())
         if k > 2**31 - 1:
             raise RasterizerError(f"compute_tile_intersection: {k} keys exceed the int32 range")
         sz2 = ctypes.c_size_t(0)

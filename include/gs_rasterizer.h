@@ -120,12 +120,27 @@ int gs_evaluate_sh_backward(const float *grad_colors, const float *camera_pos,
  *     (one int32 per tile).  Optional outputs (may be NULL): sorted_keys (K
  *     uint64, the 64-bit keys in sorted order) and tiles_touched (N int32).
  *     The workspace size depends on M and the image/tile geometry only.
+ *
+ * gs_bin_count = gs_bin_count_begin followed by gs_bin_count_finish (same
+ * arguments).  totals is final once the work gs_bin_count_begin launched has
+ * run, so a caller can queue its copy of totals between the two calls and wait
+ * for that copy after queueing gs_bin_count_finish: the host read of K and M
+ * then overlaps the second phase instead of idling the GPU (the reference reads
+ * num_rendered with .item() after all of its counting, rasterizer.cpp:322).
  */
 int gs_bin_count_workspace_size(int64_t n, size_t *bytes);
 int gs_bin_count(const float *points_image, const float *radii, const float *depths,
                  const uint8_t *mask, int64_t n, int32_t width, int32_t height,
                  int32_t tile_size, void *workspace, size_t workspace_bytes, int64_t *totals,
                  hipStream_t stream);
+int gs_bin_count_begin(const float *points_image, const float *radii, const float *depths,
+                       const uint8_t *mask, int64_t n, int32_t width, int32_t height,
+                       int32_t tile_size, void *workspace, size_t workspace_bytes,
+                       int64_t *totals, hipStream_t stream);
+int gs_bin_count_finish(const float *points_image, const float *radii, const float *depths,
+                        const uint8_t *mask, int64_t n, int32_t width, int32_t height,
+                        int32_t tile_size, void *workspace, size_t workspace_bytes,
+                        int64_t *totals, hipStream_t stream);
 int gs_bin_sort_workspace_size(int64_t n, int64_t k, int64_t m, int32_t width, int32_t height,
                                int32_t tile_size, size_t *bytes);
 int gs_bin_sort(const float *points_image, const float *radii, const float *depths, int64_t n,
