@@ -128,3 +128,39 @@ def test_layout_headline_size_bitexact(gpu):
     pts, radii, depths, mask = (t.cpu().numpy() for t in (g_pts, g_radii, g_depths, g_mask))
     k = _check(gpu, pts, radii, depths, mask, cam["width"], cam["height"], 16)
     assert k > 5_000_000
+
+
+@pytest.mark.parametrize("width,height", [(640, 480), (2560, 1600)])
+def test_single_call_count_equals_two_phases(gpu, width, height):
+    """gs_bin_count (one call) leaves the same workspace state and totals as
+    gs_bin_count_begin + gs_bin_count_finish, which compute_tile_intersection
+    uses: gs_bin_sort after it gives the identical layout (one-pass and general
+    level 1)."""
+    import ctypes
+
+    from cuda_rasterizer import _lib
+
+    pts, radii, depths, mask = (torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+                                for a in _random_splats(20000, width, height, seed=9))
+    off2, ids2 = cr.compute_tile_intersection(pts, radii, depths, mask, width, height, 16)
+    lib = _lib.load()
+    n = pts.shape[0]
+    sz = ctypes.c_size_t(0)
+    assert lib.gs_bin_count_workspace_size(n, ctypes.byref(sz)) == 0
+    ws = torch.empty(sz.value, dtype=torch.uint8, device=gpu)
+    totals = torch.empty(2, dtype=torch.int64, device=gpu)
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    assert lib.gs_bin_count(pts.data_ptr(), radii.data_ptr(), depths.data_ptr(), mask.data_ptr(),
+                            n, width, height, 16, ws.data_ptr(), sz.value, totals.data_ptr(),
+                            stream) == 0
+    k, m = (int(v) for v in totals.tolist())
+    assert k == ids2.numel()
+    sz2 = ctypes.c_size_t(0)
+    assert lib.gs_bin_sort_workspace_size(n, k, m, width, height, 16, ctypes.byref(sz2)) == 0
+    ws2 = torch.empty(max(sz2.value, 1), dtype=torch.uint8, device=gpu)
+    off = torch.empty_like(off2)
+    ids = torch.empty(k, dtype=torch.int32, device=gpu)
+    assert lib.gs_bin_sort(pts.data_ptr(), radii.data_ptr(), depths.data_ptr(), n, width, height,
+                           16, k, m, ws.data_ptr(), ws2.data_ptr(), sz2.value, off.data_ptr(),
+                           ids.data_ptr(), None, None, stream) == 0
+    assert torch.equal(off, off2) and torch.equal(ids, ids2)
