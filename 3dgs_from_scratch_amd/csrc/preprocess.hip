@@ -110,10 +110,12 @@ __device__ __forceinline__ void camera_position(const float *__restrict__ cam_po
 // Copies `count` (<= kShBlock * kRest) floats between global memory and LDS with
 // the block's threads: every thread issues all its loads before its stores (a
 // fully unrolled register stage), 16 bytes per access when the global side is
-// 16-byte aligned.
+// 16-byte aligned.  With `rows` (LDS, one flag per kRest-float row), a float4
+// whose rows all have flag 0 is not read (its LDS slots get zeros): culled
+// Gaussians' SH rows never reach the GPU's caches.
 template <bool kToLds>
 __device__ __forceinline__ void block_copy(float *__restrict__ lds, float *__restrict__ glob,
-                                           int count) {
+                                           int count, const uint8_t *rows = nullptr) {
     constexpr int kMax4 = kShBlock * kRest / 4;
     constexpr int kIters = (kMax4 + kShBlock - 1) / kShBlock;
     static_assert(kShBlock * kRest % 4 == 0, "rows of a block must fill whole float4s");
@@ -126,8 +128,10 @@ __device__ __forceinline__ void block_copy(float *__restrict__ lds, float *__res
         float4 *d4 = reinterpret_cast<float4 *>(dst);
         float4 v[kIters];
 #pragma unroll
-        for (int it = 0; it < kIters; ++it) {  // unconditional (clamped) loads stay in registers
-            v[it] = s4[min(tid + it * kShBlock, n4 - 1)];
+        for (int it = 0; it < kIters; ++it) {  // clamped loads stay in registers
+            const int e = min(tid + it * kShBlock, n4 - 1);
+            const bool need = !rows || (rows[(4 * e) / kRest] | rows[(4 * e + 3) / kRest]);
+            v[it] = need ? s4[e] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int it = 0; it < kIters; ++it) {
@@ -239,9 +243,12 @@ __global__ __launch_bounds__(kShBlock) void sh_backward_kernel(
     int accumulate_means, float *__restrict__ grad_means, float *__restrict__ grad_dc,
     float *__restrict__ grad_rest) {
     __shared__ __align__(16) float rest_lds[kShBlock * kRest];
+    __shared__ uint8_t keep[kShBlock];
     const int64_t first = (int64_t)blockIdx.x * kShBlock;
     const int nb = (int)min((int64_t)kShBlock, n - first);
-    block_copy<true>(rest_lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb);
+    keep[threadIdx.x] = threadIdx.x < nb ? mask[first + threadIdx.x] : 0;
+    __syncthreads();
+    block_copy<true>(rest_lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb, keep);
     __syncthreads();
     const int t = threadIdx.x;
     float *lrest = rest_lds + kRest * t;  // row read in full below, then overwritten by its gradient
@@ -443,9 +450,12 @@ __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
     float *__restrict__ grad_logits, float *__restrict__ grad_dc,
     float *__restrict__ grad_rest) {
     __shared__ __align__(16) float rest_lds[kShBlock * kRest];
+    __shared__ uint8_t keep[kShBlock];
     const int64_t first = (int64_t)blockIdx.x * kShBlock;
     const int nb = (int)min((int64_t)kShBlock, n - first);
-    block_copy<true>(rest_lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb);
+    keep[threadIdx.x] = threadIdx.x < nb ? mask[first + threadIdx.x] : 0;
+    __syncthreads();
+    block_copy<true>(rest_lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb, keep);
     __syncthreads();
     const int t = threadIdx.x;
     float *lrest = rest_lds + kRest * t;
