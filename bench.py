@@ -321,6 +321,56 @@ def run_ssim(scene: dict, steps: int, warmup: int) -> dict:
     return out
 
 
+def run_forward(scene: dict, steps: int, warmup: int) -> dict:
+    """Configuration 4: forward-only render() (no autograd) of the scene, with
+    HIP events around every entry point.  Reports the binning's keys per second
+    (K over the count + sort time) and the blend's pixels per second."""
+    from cuda_rasterizer import _lib
+    from cuda_rasterizer.wrapper import render
+
+    dev = torch.device("cuda:0")
+    p = {k: v.to(dev) for k, v in scene["params"].items()}
+    cam = scene["camera"]
+    w2c, K = cam["w2c"].to(dev), cam["K"].to(dev)
+    W, H = cam["width"], cam["height"]
+    with torch.no_grad():
+        scales, quats, opac = activated(p)
+
+        def step():
+            return render(w2c, K, W, H, p["means"], scales, quats, opac, p["sh_dc"],
+                          p["sh_rest"], near_plane=cam["near"])
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        _lib.timer.reset()
+        _lib.timer.only = None
+        _lib.timer.enabled = True
+        for _ in range(steps):
+            step()
+        _lib.timer.enabled = False
+        st = {k: t / steps for k, (c, t) in _lib.timer.summary().items()}
+        from cuda_rasterizer import compute_tile_intersection, project_points
+        pts, depths, _, _, radii, mask = project_points(
+            p["means"], scales, quats, opac, w2c, K, cam["near"], 100.0, 1 / 255, 0.5, 128.0, W, H)
+        _, ids = compute_tile_intersection(pts, radii, depths, mask, W, H, 16)
+    keys = int(ids.numel())
+    bin_ms = st["bin_count"] + st["bin_sort"]
+    blend_ms = st["rasterize_display"]
+    return {"metric": "forward ms/iter; binning keys/s; blend pixels/s",
+            "workload": f"{scene['name']}: {scene['params']['means'].shape[0]} Gaussians SH3 "
+                        f"{W}x{H} forward-only render()",
+            "ms_per_step": round(ms, 4), "keys": keys,
+            "binning_keys_per_s": round(keys / (bin_ms * 1e-3), 1),
+            "blend_pixels_per_s": round(W * H / (blend_ms * 1e-3), 1),
+            "stages_ms": {k: round(v, 4) for k, v in st.items()}}
+
+
 # ------------------------------------------------- configuration 5 (training)
 
 def _torch_clone_top_and_prune(leaves: dict, optims: dict, grads: torch.Tensor, fraction: float,
@@ -687,7 +737,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=[1, 3, 4, 5],
-                    help="3 (headline, default), 1 or 4; 5 prints only the training stress run")
+                    help="3 (headline, default) or 1; 4 prints only the forward-only sort and "
+                         "blend rates, 5 only the training stress run")
     ap.add_argument("--path", choices=["fused", "drop-in"], default="fused",
                     help="the timed step: fused render_l1 (default) or PyTorch glue around render()")
     ap.add_argument("--no-drop-in", action="store_true",
@@ -719,6 +770,9 @@ def main(argv=None):
 
     if args.config == 5:
         print(json.dumps(train_stress(args.train_steps, args.train_path)), flush=True)
+        return 0
+    if args.config == 4:
+        print(json.dumps(run_forward(CONFIGS[4](), args.steps, args.warmup)), flush=True)
         return 0
 
     scene = CONFIGS[args.config]()
