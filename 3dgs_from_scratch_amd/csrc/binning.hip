@@ -5,12 +5,16 @@
 // in Gaussian order and stably sorts all 64 bits.  The same order -- (tile,
 // depth bits, Gaussian index) -- is produced here without ever storing or
 // sorting the K (tile, Gaussian) keys:
-//   1. gs_bin_count: tiles_touched, a packed tile rectangle and the number of
-//      touched supertiles (8 x 8 tiles) per Gaussian; a stable LSD sort of the
-//      N depth keys (32 bits); a scan of the supertile counts in depth order.
+//   1. gs_bin_count: a packed tile rectangle and a depth key per Gaussian and
+//      the totals K and M; a stable LSD sort of the depth keys of the Gaussians
+//      with tiles (32 bits); then, with at most 256 supertiles (8 x 8 tiles),
+//      the per-block supertile counts of level 1 and their positions, else a
+//      scan of the supertile counts in depth order.
 //   2. gs_bin_sort level 1: one (supertile, Gaussian) entry per touched
 //      supertile, in depth order, stably sorted by supertile id -> for every
-//      supertile, the Gaussians meeting it in depth order (M << K entries).
+//      supertile, the Gaussians meeting it in depth order (M << K entries):
+//      written straight to their places from those positions, or emitted and
+//      radix-sorted by supertile id on larger grids.
 //   3. gs_bin_sort level 2: each supertile list is cut into 512-entry blocks;
 //      per wave, 8 row and 8 column ballots give every local tile's count,
 //      one workgroup per supertile scans the counts over its blocks (and the

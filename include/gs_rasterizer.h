@@ -105,12 +105,14 @@ int gs_evaluate_sh_backward(const float *grad_colors, const float *camera_pos,
  * compute_tile_intersection (src/cuda/rasterizer.cpp:292-359) in two phases
  * around the one host read of the entry counts:
  *
- *   gs_bin_count: tiles_touched per Gaussian (kernel.cu:784-818 semantics), a
- *     stable sort of the visible Gaussians by depth bits, and the scan that
- *     places their supertile entries (a supertile is 8 x 8 tiles).  Writes two
- *     device int64: totals[0] = K, the number of (tile, Gaussian) keys, and
- *     totals[1] = M, the number of (supertile, Gaussian) entries (M <= K).
- *     Keeps its state in `workspace`, which gs_bin_sort reads.
+ *   gs_bin_count: the tile rectangle of every Gaussian (tiles_touched,
+ *     kernel.cu:784-818 semantics), a stable sort of the Gaussians with tiles
+ *     by depth bits, and the placement of their supertile entries (a supertile
+ *     is 8 x 8 tiles): per-supertile counts and positions when the grid has at
+ *     most 256 supertiles, else an exclusive scan.  Writes two device int64:
+ *     totals[0] = K, the number of (tile, Gaussian) keys, and totals[1] = M,
+ *     the number of (supertile, Gaussian) entries (M <= K).  Keeps its state in
+ *     `workspace`, which gs_bin_sort reads.
  *   gs_bin_sort: sorts the M entries by supertile (depth order kept), then
  *     expands every supertile list to its tiles and writes each Gaussian id
  *     once, at its final position.  The result equals a stable sort of the
