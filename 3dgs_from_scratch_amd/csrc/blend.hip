@@ -514,8 +514,15 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image,
     float *__restrict__ display, const float *__restrict__ target,
-    float *__restrict__ tile_loss) {
+    float *__restrict__ tile_loss, float4 *__restrict__ clear4, int64_t clear4_count) {
     __shared__ BatchLds s;
+    if (clear4) {  // this workgroup's share of the buffer to zero (stores overlap the blend)
+        const int64_t per = (clear4_count + gridDim.x - 1) / gridDim.x;
+        const int64_t c0 = (int64_t)blockIdx.x * per;
+        const int64_t c1 = min(c0 + per, clear4_count);
+        for (int64_t c = c0 + threadIdx.x; c < c1; c += kWave)
+            clear4[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     const int tile = tile_of_block(blockIdx.x, n_tiles);
     const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
@@ -952,7 +959,8 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                           int64_t n, int32_t width, int32_t height, int32_t tile_size,
                           float alpha_threshold, float transmittance_threshold,
                           float chi_squared_threshold, float *image, float *display,
-                          const float *target, float *tile_loss, hipStream_t stream) {
+                          const float *target, float *tile_loss, hipStream_t stream,
+                          float *clear = nullptr, int64_t clear_count = 0) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -968,6 +976,16 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
         if (!st && display) st = zero_bytes(display, bytes, stream);
         if (st) return st;
     }
+    if (clear_count < 0 || (clear_count > 0 && !clear)) return GS_ERR_INVALID_ARGUMENT;
+    // the forward kernel zeroes `clear` when it is float4-aligned and has tiles to
+    // spread it over; otherwise a fill kernel does
+    const bool fused_clear = clear_count > 0 && n_tiles > 0 && tile_size == kTile &&
+                             (reinterpret_cast<uintptr_t>(clear) & 15) == 0 &&
+                             clear_count % 4 == 0;
+    if (clear_count > 0 && !fused_clear) {
+        st = zero_bytes(clear, (size_t)clear_count * sizeof(float), stream);
+        if (st) return st;
+    }
     if (n_tiles == 0) return GS_OK;
     if (k > 0 && (!points_image || !cov_inv_image || !opacities || !colors))
         return GS_ERR_INVALID_ARGUMENT;
@@ -976,7 +994,9 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                            indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
-                           image, display, target, tile_loss);
+                           image, display, target, tile_loss,
+                           fused_clear ? reinterpret_cast<float4 *>(clear) : nullptr,
+                           fused_clear ? clear_count / 4 : (int64_t)0);
     } else {
         hipLaunchKernelGGL(blend_forward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, indexing_offset,
@@ -1021,7 +1041,8 @@ extern "C" int gs_rasterize_display_l1(
     const float *points_image, const float *cov_inv_image, const float *opacities,
     const float *colors, int64_t n, int32_t width, int32_t height, int32_t tile_size,
     float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
-    const float *target, float *image, float *display, float *tile_loss, hipStream_t stream) {
+    const float *target, float *image, float *display, float *tile_loss, float *clear,
+    int64_t clear_count, hipStream_t stream) {
     if (!display || !target || !tile_loss || tile_size != kTile) return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     const int tiles_y = (height + tile_size - 1) / tile_size;
@@ -1029,7 +1050,7 @@ extern "C" int gs_rasterize_display_l1(
     return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
                           cov_inv_image, opacities, colors, n, width, height, tile_size,
                           alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
-                          display, target, tile_loss, stream);
+                          display, target, tile_loss, stream, clear, clear_count);
 }
 
 // loss = (sum of the n_tiles partial sums) / count, one workgroup.

@@ -51,6 +51,7 @@ __all__ = [
     "preprocess_backward",
     "rasterize_display_l1",
     "rasterize_l1_backward",
+    "blend_grad_accumulators",
     "fused_ssim",
     "RasterizerError",
 ]
@@ -379,11 +380,22 @@ def rasterize(
     return image
 
 
-def _zeroed_blend_grads(n, dev):
-    """Four zeroed gradient outputs (N,2), (N,3), (N,), (N,3) carved from one buffer."""
-    buf = torch.zeros((9 * n,), dtype=torch.float32, device=dev)
+def _blend_grad_views(buf, n):
+    """The four gradient outputs (N,2), (N,3), (N,), (N,3) carved from one 9N buffer."""
     return (buf[: 2 * n].view(n, 2), buf[2 * n : 5 * n].view(n, 3), buf[5 * n : 6 * n],
             buf[6 * n :].view(n, 3))
+
+
+def _zeroed_blend_grads(n, dev):
+    """Four zeroed gradient outputs (N,2), (N,3), (N,), (N,3) carved from one buffer."""
+    return _blend_grad_views(torch.zeros((9 * n,), dtype=torch.float32, device=dev), n)
+
+
+def blend_grad_accumulators(n, device):
+    """An uninitialised 9N fp32 buffer for the blend gradients: pass it as
+    rasterize_display_l1(clear=...) (which zeroes it) and then as
+    rasterize_l1_backward(accumulators=...)."""
+    return torch.empty((9 * int(n),), dtype=torch.float32, device=device)
 
 
 def rasterize_backward(
@@ -706,9 +718,10 @@ def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, g
 
 def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
                          opacities, colors, width, height, target, alpha_threshold=1e-4,
-                         transmittance_threshold=1e-4, chi_squared_threshold=9.21):
+                         transmittance_threshold=1e-4, chi_squared_threshold=9.21, clear=None):
     """rasterize_display with tile size 16 plus loss = mean(|display / 255 - target|).
-    Returns (image, display, loss[1] fp32)."""
+    Returns (image, display, loss[1] fp32).  `clear` (an fp32 device tensor, e.g.
+    from blend_grad_accumulators) is zeroed by the same launch."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -726,7 +739,8 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
             _ptr(off), _ptr(ids), n_tiles, ids.shape[0], _ptr(pts), _ptr(conic), _ptr(opac),
             _ptr(col), n, width, height, 16, float(alpha_threshold), float(transmittance_threshold),
             float(chi_squared_threshold), _ptr(target), _ptr(image), _ptr(display), _ptr(tile_loss),
-            _stream(dev)), "rasterize_display_l1")
+            _ptr(clear), 0 if clear is None else clear.numel(), _stream(dev)),
+            "rasterize_display_l1")
         _lib.timer.stop(ev, dev)
         _lib.check(lib.gs_l1_finish(_ptr(tile_loss), n_tiles, height * width * 3, _ptr(loss),
                                     _stream(dev)), "l1_finish")
@@ -736,9 +750,11 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
 def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorted, points_image,
                           cov_inv_image, opacities, colors, width, height, rendered_image,
                           alpha_threshold=1e-4, transmittance_threshold=1e-4,
-                          chi_squared_threshold=9.21):
+                          chi_squared_threshold=9.21, accumulators=None):
     """Gradient of rasterize_display_l1's loss (times grad_loss, a 1-element fp32
-    device tensor) w.r.t. the four blend inputs."""
+    device tensor) w.r.t. the four blend inputs.  `accumulators`: a 9N buffer
+    already zeroed (rasterize_display_l1's `clear`) that the gradients are added
+    into; otherwise a zeroed one is allocated."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -746,7 +762,14 @@ def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorte
     target = _prep(target, "target", f32, (height, width, 3), dev)
     img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
     gl = _prep(grad_loss.reshape(1), "grad_loss", f32, (1,), dev)
-    g_pts, g_conic, g_opac, g_col = _zeroed_blend_grads(n, dev)
+    if accumulators is None:
+        g_pts, g_conic, g_opac, g_col = _zeroed_blend_grads(n, dev)
+    else:
+        if (accumulators.dtype != f32 or accumulators.device != dev
+                or accumulators.numel() != 9 * n or not accumulators.is_contiguous()):
+            raise RuntimeError("rasterize_l1_backward: accumulators must be a contiguous fp32 "
+                               f"tensor of {9 * n} elements on {dev}")
+        g_pts, g_conic, g_opac, g_col = _blend_grad_views(accumulators, n)
     with torch.cuda.device(dev):
         ev = _lib.timer.record("rasterize_l1_backward", dev)
         _lib.check(_lib.load().gs_rasterize_l1_backward(

@@ -40,12 +40,14 @@ class RenderL1Function(torch.autograd.Function):
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
             max_radius, width, height)
         off, ids = _cr.compute_tile_intersection(pts, radii, depths, mask, width, height, 16)
+        # the blend gradients' accumulators, zeroed by the forward blend launch
+        acc = _cr.blend_grad_accumulators(means.shape[0], means.device)
         image, display, loss = _cr.rasterize_display_l1(
             off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
-            transmittance_threshold, chi_squared_threshold)
+            transmittance_threshold, chi_squared_threshold, clear=acc)
         ctx.save_for_backward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
                               sh_coeffs_rest, world_to_camera, intrinsic, target, opac, pts, cov,
-                              conic, mask, colors, off, ids, image)
+                              conic, mask, colors, off, ids, image, acc)
         ctx.densifier = densifier
         ctx.radii = radii if densifier is not None else None
         ctx.params = (width, height, alpha_threshold, transmittance_threshold,
@@ -57,13 +59,13 @@ class RenderL1Function(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_loss, grad_display, grad_pts, grad_radii):
         (means, log_scales, quats_raw, logits, dc, rest, w2c, K, target, opac, pts, cov, conic,
-         mask, colors, off, ids, image) = ctx.saved_tensors
+         mask, colors, off, ids, image, acc) = ctx.saved_tensors
         width, height, a_thr, t_thr, chi = ctx.params
         if grad_loss is None:
             return (None,) * 20
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_l1_backward(
             target, grad_loss.reshape(1).to(torch.float32), off, ids, pts, conic, opac, colors,
-            width, height, image, a_thr, t_thr, chi)
+            width, height, image, a_thr, t_thr, chi, accumulators=acc)
         if ctx.densifier is not None:
             ctx.densifier.update(g_pts, ctx.radii, width, height)
         g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(

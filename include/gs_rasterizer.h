@@ -278,7 +278,11 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
  *   zero) to log_scales, raw quaternions and logits.
  * gs_rasterize_display_l1: gs_rasterize_display that also writes, per tile,
  *   the sum over its pixels of |display / 255 - target| (tile_loss, one float
- *   per tile; n_tiles must cover the image; tile_size 16).
+ *   per tile; n_tiles must cover the image; tile_size 16).  When clear is set,
+ *   it also writes clear_count zeros there (in the blend kernel when clear is
+ *   16-byte aligned and clear_count a multiple of 4): the accumulators that
+ *   gs_rasterize_l1_backward then adds into with accumulate = 1, without a
+ *   separate fill.
  * gs_l1_finish: loss = sum(tile_loss) / count (count = H * W * 3), one float.
  * gs_rasterize_l1_backward: gs_rasterize_backward seeded by
  *   loss = mean(|clamp(image, 0, 1) * 255 / 255 - target|) with upstream
@@ -299,7 +303,7 @@ int gs_rasterize_display_l1(const int32_t *indexing_offset, const int32_t *gauss
                             int32_t tile_size, float alpha_threshold,
                             float transmittance_threshold, float chi_squared_threshold,
                             const float *target, float *image, float *display, float *tile_loss,
-                            hipStream_t stream);
+                            float *clear, int64_t clear_count, hipStream_t stream);
 int gs_l1_finish(const float *tile_loss, int32_t n_tiles, int64_t count, float *loss,
                  hipStream_t stream);
 int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const float *image,

@@ -165,3 +165,28 @@ def test_render_l1_repeated_calls_are_stable(gpu):
     assert out[0][0] == out[1][0]
     for k in helpers.PARAMS:
         assert helpers.rel_l2(out[1][1][k], out[0][1][k]) <= 1e-5, k
+
+
+@pytest.mark.parametrize("count", [9 * 8000, 10, 4 * 8000 + 2])
+def test_display_l1_clears_buffer(gpu, count):
+    """rasterize_display_l1(clear=...) zeroes the buffer (in the blend launch when
+    float4-aligned with a multiple of 4 elements, else with a fill), leaving the
+    image, display and loss as without it."""
+    p, cam, target = helpers.scene_box(8_000, 200, 130, 220.0, seed=23, log_scale=(-3.5, 0.6))
+    W, H = cam["width"], cam["height"]
+    a = _raw_leaves(p, gpu)
+    with torch.no_grad():
+        pts, depths, _, conic, radii, mask, opac, colors = cr.preprocess_forward(
+            a["means"], a["log_scales"], a["quats_raw"], a["opacity_logits"], a["sh_dc"],
+            a["sh_rest"], cam["w2c"].to(gpu), cam["K"].to(gpu), 0.01, 100.0, 1 / 255, 0.5, 128.0,
+            W, H)
+        off, ids = cr.compute_tile_intersection(pts, radii, depths, mask, W, H, 16)
+        ref = cr.rasterize_display_l1(off, ids, pts, conic, opac, colors, W, H, target.to(gpu))
+        buf = torch.full((count + 1,), 7.0, device=gpu)
+        view = buf[1:] if count % 4 else buf[:count]  # a misaligned view for the odd counts
+        got = cr.rasterize_display_l1(off, ids, pts, conic, opac, colors, W, H, target.to(gpu),
+                                      clear=view)
+    assert float(view.abs().max()) == 0.0
+    assert float(buf[count if count % 4 == 0 else 0]) == 7.0  # nothing past the buffer
+    for x, y in zip(got, ref):
+        assert torch.equal(x, y)
