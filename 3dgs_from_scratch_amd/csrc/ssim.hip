@@ -337,10 +337,12 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     __shared__ float stage[3][kInY][kPitch];
     __shared__ __align__(16) float rows[3][kInY][kTileX];
     float v[3][kStageIters];
+    float held[2][kRowsPerWave];
     int t0, t1;
     tile_range(p, t0, t1);
     if (t0 < t1) load_maps(p, tile_of(p, t0), d_mu, d_xx, d_xy, v);
     const float up = *grad_mean;
+    const bool interleave3 = p.channels == 3 && gs1 == 1 && gs3 == 3;
     const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
     for (int t = t0; t < t1; ++t) {
         const Tile tl = tile_of(p, t);
@@ -366,13 +368,34 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
         __syncthreads();
         float acc[3][kRowsPerWave];
         column_pass<3>(win, rows, r0, acc);
-        float *bg = grad + ((int64_t)tl.b * gs0 + (int64_t)tl.c * gs1);
+        float g[kRowsPerWave];
+#pragma unroll
+        for (int o = 0; o < kRowsPerWave; ++o)
+            g[o] = up * (acc[0][o] + 2.0f * xs[o] * acc[1][o] + ys[o] * acc[2][o]);
+        // Three interleaved channels (the reference's (H, W, 3) layout): the
+        // gradients of channels 0 and 1 of a region wait in registers while this
+        // workgroup filters the next channel, and channel 2 writes all three, so a
+        // wave's stores cover whole lines (else every channel is its own third).
+        const int first_c = t - tl.c;  // the region's channel-0 tile
+        const bool whole = interleave3 && first_c >= t0 && first_c + 2 < t1;
+        if (whole && tl.c < 2) {
+#pragma unroll
+            for (int o = 0; o < kRowsPerWave; ++o) held[tl.c][o] = g[o];
+            continue;
+        }
+        float *bg = grad + ((int64_t)tl.b * gs0 + (int64_t)(whole ? 0 : tl.c) * gs1);
 #pragma unroll
         for (int o = 0; o < kRowsPerWave; ++o) {
             const int gy = tl.oy + r0 + o;
             if (gy >= p.height || gx >= p.width) continue;
-            const float g = acc[0][o] + 2.0f * xs[o] * acc[1][o] + ys[o] * acc[2][o];
-            bg[gy * gs2 + gx * gs3] = up * g;
+            float *px = bg + (gy * gs2 + gx * gs3);
+            if (whole) {
+                px[0] = held[0][o];
+                px[1] = held[1][o];
+                px[2] = g[o];
+            } else {
+                px[0] = g[o];
+            }
         }
     }
 }
