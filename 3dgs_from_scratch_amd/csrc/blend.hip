@@ -322,12 +322,14 @@ __device__ __forceinline__ float display_grad(float g, float raw) {
 }
 
 // Gradient w.r.t. display of scale * |display / 255 - t| (torch's l1_loss: sign
-// of the difference, 0 at 0; then the division by 255).
-__device__ __forceinline__ float l1_grad(float t, float raw, float scale) {
+// of the difference, 0 at 0), plus `extra`, a further gradient w.r.t.
+// display / 255 (summed there, as autograd sums the two uses of display / 255),
+// then the division by 255.
+__device__ __forceinline__ float l1_grad(float t, float raw, float scale, float extra) {
     const float x = (clamp01(raw) * 255.0f) / 255.0f;
     const float d = x - t;
     const float sgn = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
-    return (sgn * scale) / 255.0f;
+    return (sgn * scale + extra) / 255.0f;
 }
 
 // Some pixel of the wave still composites: !(T < T_thr) (NaN stays active).
@@ -706,7 +708,7 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr_in, float chi, float *__restrict__ g_points,
     float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors,
-    const float *__restrict__ grad_loss, float inv_count) {
+    const float *__restrict__ grad_loss, float inv_count, const float *__restrict__ extra) {
     __shared__ BatchLds s;
     const float T_thr = effective_T_thr(T_thr_in);
     const int tile = tile_of_block(blockIdx.x, n_tiles);
@@ -735,10 +737,11 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
                 cg[q] = image[o + 1];
                 cb[q] = image[o + 2];
             }
-            if (kSeed == kSeedL1) {  // sign(display/255 - t) * g / n, then / 255
-                gr = l1_grad(gr, cr[q], l1_scale);
-                gg = l1_grad(gg, cg[q], l1_scale);
-                gb = l1_grad(gb, cb[q], l1_scale);
+            if (kSeed == kSeedL1) {  // sign(display/255 - t) * g / n (+ extra), then / 255
+                const bool ex = extra != nullptr;
+                gr = l1_grad(gr, cr[q], l1_scale, ex ? extra[o] : 0.0f);
+                gg = l1_grad(gg, cg[q], l1_scale, ex ? extra[o + 1] : 0.0f);
+                gb = l1_grad(gb, cb[q], l1_scale, ex ? extra[o + 2] : 0.0f);
             }
             if (kSeed != kSeedImage) {
                 gr = display_grad(gr, cr[q]);
@@ -1087,7 +1090,8 @@ static int rasterize_backward_impl(
     int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
     float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
     float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
-    int seed, const float *grad_loss, float inv_count, hipStream_t stream) {
+    int seed, const float *grad_loss, float inv_count, hipStream_t stream,
+    const float *extra = nullptr) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -1116,7 +1120,7 @@ static int rasterize_backward_impl(
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
                            grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors,
-                           grad_loss, inv_count);
+                           grad_loss, inv_count, extra);
     } else {
         hipLaunchKernelGGL(blend_backward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, grad_image, image,
@@ -1167,7 +1171,7 @@ extern "C" int gs_rasterize_l1_backward(
     const float *colors, int64_t n, int32_t width, int32_t height, int32_t tile_size,
     float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
     float *grad_points_image, float *grad_cov_inv_image, float *grad_opacities,
-    float *grad_colors, int32_t accumulate, hipStream_t stream) {
+    float *grad_colors, int32_t accumulate, const float *grad_display01, hipStream_t stream) {
     if (!target || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
     const float inv_count = (float)(1.0 / ((double)width * (double)height * 3.0));
     return rasterize_backward_impl(target, image, indexing_offset, gaussian_ids_sorted, n_tiles,
@@ -1175,7 +1179,7 @@ extern "C" int gs_rasterize_l1_backward(
                                    height, tile_size, alpha_threshold, transmittance_threshold,
                                    chi_squared_threshold, grad_points_image, grad_cov_inv_image,
                                    grad_opacities, grad_colors, accumulate, kSeedL1, grad_loss,
-                                   inv_count, stream);
+                                   inv_count, stream, grad_display01);
 }
 
 extern "C" int gs_rasterize_work(const int32_t *indexing_offset,

@@ -750,11 +750,12 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
 def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorted, points_image,
                           cov_inv_image, opacities, colors, width, height, rendered_image,
                           alpha_threshold=1e-4, transmittance_threshold=1e-4,
-                          chi_squared_threshold=9.21, accumulators=None):
+                          chi_squared_threshold=9.21, accumulators=None, grad_display01=None):
     """Gradient of rasterize_display_l1's loss (times grad_loss, a 1-element fp32
     device tensor) w.r.t. the four blend inputs.  `accumulators`: a 9N buffer
     already zeroed (rasterize_display_l1's `clear`) that the gradients are added
-    into; otherwise a zeroed one is allocated."""
+    into; otherwise a zeroed one is allocated.  `grad_display01`: an (H, W, 3)
+    further gradient w.r.t. display / 255 (an SSIM term's), added to the L1 one."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -762,6 +763,8 @@ def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorte
     target = _prep(target, "target", f32, (height, width, 3), dev)
     img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
     gl = _prep(grad_loss.reshape(1), "grad_loss", f32, (1,), dev)
+    extra = (None if grad_display01 is None
+             else _prep(grad_display01, "grad_display01", f32, (height, width, 3), dev))
     if accumulators is None:
         g_pts, g_conic, g_opac, g_col = _zeroed_blend_grads(n, dev)
     else:
@@ -776,7 +779,7 @@ def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorte
             _ptr(target), _ptr(gl), _ptr(img), _ptr(off), _ptr(ids), off.shape[0], ids.shape[0],
             _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, 16,
             float(alpha_threshold), float(transmittance_threshold), float(chi_squared_threshold),
-            _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), 1, _stream(dev)),
+            _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), 1, _ptr(extra), _stream(dev)),
             "rasterize_l1_backward")
         _lib.timer.stop(ev, dev)
     return g_pts, g_conic, g_opac, g_col

@@ -20,6 +20,12 @@ Densification statistics (src/strategy.py:47-68 reads dL/d points_img, which
 this node never materialises as a .grad): pass `densifier`, a
 cuda_rasterizer.train.Densifier, and the backward adds the gradient norms in
 NDC scale and the visibility counts to it (gs_accumulate_grad2d).
+
+With ssim_lambda > 0 the loss is the reference's full training loss,
+(1 - ssim_lambda) * L1 + ssim_lambda * (1 - SSIM(display / 255, target))
+(scripts/train.py:185-205; SSIM by cuda_rasterizer.ssim, padding "valid" as
+there): the SSIM gradient w.r.t. display / 255 joins the L1 seed inside the
+blend backward, as autograd sums the two uses of display / 255.
 """
 
 from __future__ import annotations
@@ -27,6 +33,12 @@ from __future__ import annotations
 import torch
 
 import cuda_rasterizer as _cr
+from cuda_rasterizer import ssim as _ssim
+
+
+def _chw(img: torch.Tensor) -> torch.Tensor:
+    """(H, W, 3) -> the (1, 3, H, W) view the reference hands to fused_ssim."""
+    return img.permute(2, 0, 1).unsqueeze(0)
 
 
 class RenderL1Function(torch.autograd.Function):
@@ -34,7 +46,7 @@ class RenderL1Function(torch.autograd.Function):
     def forward(ctx, means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
                 world_to_camera, intrinsic, target, densifier, width, height, near_plane,
                 far_plane, min_opacity, min_radius, max_radius, alpha_threshold,
-                transmittance_threshold, chi_squared_threshold):
+                transmittance_threshold, chi_squared_threshold, ssim_lambda, ssim_padding):
         pts, depths, cov, conic, radii, mask, opac, colors = _cr.preprocess_forward(
             means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
@@ -45,9 +57,18 @@ class RenderL1Function(torch.autograd.Function):
         image, display, loss = _cr.rasterize_display_l1(
             off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
             transmittance_threshold, chi_squared_threshold, clear=acc)
+        ssim_saved = ()
+        if ssim_lambda > 0.0:
+            # the reference's rendered_image / 255 (its render() returns the display
+            # image) and its permuted (1, 3, H, W) views
+            d01 = display / 255.0
+            s, maps = _ssim.ssim_forward(_chw(d01), _chw(target), ssim_padding, with_maps=True)
+            loss = (1.0 - ssim_lambda) * loss.reshape(()) + ssim_lambda * (1.0 - s)
+            ssim_saved = (d01,) + tuple(maps)
         ctx.save_for_backward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
                               sh_coeffs_rest, world_to_camera, intrinsic, target, opac, pts, cov,
-                              conic, mask, colors, off, ids, image, acc)
+                              conic, mask, colors, off, ids, image, acc, *ssim_saved)
+        ctx.ssim_lambda = ssim_lambda
         ctx.densifier = densifier
         ctx.radii = radii if densifier is not None else None
         ctx.params = (width, height, alpha_threshold, transmittance_threshold,
@@ -58,28 +79,38 @@ class RenderL1Function(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_loss, grad_display, grad_pts, grad_radii):
+        saved = ctx.saved_tensors
         (means, log_scales, quats_raw, logits, dc, rest, w2c, K, target, opac, pts, cov, conic,
-         mask, colors, off, ids, image, acc) = ctx.saved_tensors
+         mask, colors, off, ids, image, acc) = saved[:19]
         width, height, a_thr, t_thr, chi = ctx.params
         if grad_loss is None:
-            return (None,) * 20
+            return (None,) * 22
+        g = grad_loss.reshape(1).to(torch.float32)
+        lam = ctx.ssim_lambda
+        extra = None
+        if lam > 0.0:  # d loss / d SSIM = -lambda g; its gradient w.r.t. display / 255
+            d01, m1, m2, m3 = saved[19:]
+            extra = _ssim.ssim_backward(-lam * g, _chw(d01), _chw(target), (m1, m2, m3))
+            extra = extra[0].permute(1, 2, 0)  # laid out like d01: (H, W, 3) contiguous
+            g = (1.0 - lam) * g
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_l1_backward(
-            target, grad_loss.reshape(1).to(torch.float32), off, ids, pts, conic, opac, colors,
-            width, height, image, a_thr, t_thr, chi, accumulators=acc)
+            target, g, off, ids, pts, conic, opac, colors, width, height, image, a_thr, t_thr,
+            chi, accumulators=acc, grad_display01=extra)
         if ctx.densifier is not None:
             ctx.densifier.update(g_pts, ctx.radii, width, height)
         g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(
             g_pts, g_conic, g_opac, g_col, means, log_scales, quats_raw, logits, dc, rest, cov,
             mask, w2c, K, width, height)
-        return (g_means, g_ls, g_qr, g_logit, g_dc, g_rest) + (None,) * 14
+        return (g_means, g_ls, g_qr, g_logit, g_dc, g_rest) + (None,) * 16
 
 
 def render_l1(world_to_camera, intrinsic, width, height, means, log_scales, quats_raw,
               opacity_logits, sh_coeffs_dc, sh_coeffs_rest, target, near_plane=0.01,
               far_plane=100.0, min_opacity=1 / 255, min_radius=0.5, max_radius=128.0,
               alpha_threshold=1e-4, transmittance_threshold=1e-4, chi_squared_threshold=9.21,
-              densifier=None):
-    """loss = l1_loss(render(...activations of the raw parameters...)[0] / 255, target).
+              densifier=None, ssim_lambda=0.0, ssim_padding="valid"):
+    """loss = l1_loss(render(...activations of the raw parameters...)[0] / 255, target),
+    or with ssim_lambda > 0, (1 - ssim_lambda) * that + ssim_lambda * (1 - SSIM).
 
     Parameters are the raw training leaves of scripts/train.py:135-143
     (log-scales, un-normalised xyzw quaternions, opacity logits); SH colours use
@@ -91,4 +122,4 @@ def render_l1(world_to_camera, intrinsic, width, height, means, log_scales, quat
         world_to_camera, intrinsic, target, densifier, int(width), int(height),
         float(near_plane), float(far_plane), float(min_opacity), float(min_radius),
         float(max_radius), float(alpha_threshold), float(transmittance_threshold),
-        float(chi_squared_threshold))
+        float(chi_squared_threshold), float(ssim_lambda), str(ssim_padding))

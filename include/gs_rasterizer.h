@@ -287,7 +287,10 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
  * gs_rasterize_l1_backward: gs_rasterize_backward seeded by
  *   loss = mean(|clamp(image, 0, 1) * 255 / 255 - target|) with upstream
  *   gradient *grad_loss (device float): the image gradient is computed per
- *   pixel from image and target (image required; tile_size 16).
+ *   pixel from image and target (image required; tile_size 16).  When
+ *   grad_display01 is set (an (H, W, 3) image), it is a further gradient with
+ *   respect to display / 255 (e.g. of an SSIM term on the same image,
+ *   scripts/train.py:185-205), added to the L1 one at that node.
  */
 int gs_activate(const float *log_scales, const float *quats_raw, const float *opacity_logits,
                 int64_t n, float *scales, float *quats, float *opacities, hipStream_t stream);
@@ -315,7 +318,7 @@ int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const 
                              float transmittance_threshold, float chi_squared_threshold,
                              float *grad_points_image, float *grad_cov_inv_image,
                              float *grad_opacities, float *grad_colors, int32_t accumulate,
-                             hipStream_t stream);
+                             const float *grad_display01, hipStream_t stream);
 
 /* ------------------------------------------------------------ training loop */
 

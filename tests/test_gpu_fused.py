@@ -116,7 +116,7 @@ def test_render_l1_matches_drop_in_path(gpu, scene):
                                              b["sh_rest"], tgt, densifier=dens)
     loss_b.backward()
     assert loss_b.shape == ()
-    assert abs(float(loss_b) - float(loss_a)) <= 1e-5 * float(loss_a)
+    assert abs(float(loss_b.detach()) - float(loss_a.detach())) <= 1e-5 * float(loss_a.detach())
     assert helpers.max_abs(disp / 255.0, img.detach() / 255.0) <= 1e-4
     for k in helpers.PARAMS:
         assert helpers.rel_l2(b[k].grad, a[k].grad) <= 1e-4, k
@@ -190,3 +190,33 @@ def test_display_l1_clears_buffer(gpu, count):
     assert float(buf[count if count % 4 == 0 else 0]) == 7.0  # nothing past the buffer
     for x, y in zip(got, ref):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("lam", [0.2, 1.0])
+def test_render_l1_with_ssim_matches_drop_in_path(gpu, lam):
+    """render_l1(ssim_lambda=lam) against the reference's loss written with PyTorch
+    around the drop-in render() and fused_ssim (scripts/train.py:185-205):
+    (1 - lam) * l1(img / 255, t) + lam * (1 - SSIM(img / 255, t), padding valid)."""
+    from cuda_rasterizer import fused_ssim
+
+    p, cam, target = helpers.scene_orbit(20_000, 320, 240, 440.0, seed=24)
+    W, H = cam["width"], cam["height"]
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    a = _raw_leaves(p, gpu)
+    scales, quats, opac = helpers.activated(a)
+    img, _, _ = render(w2c, K, W, H, a["means"], scales, quats, opac, a["sh_dc"], a["sh_rest"])
+    norm = img / 255.0
+    ssim = fused_ssim(norm.permute(2, 0, 1).unsqueeze(0), tgt.permute(2, 0, 1).unsqueeze(0),
+                      padding="valid")
+    loss_a = (1 - lam) * torch.nn.functional.l1_loss(norm, tgt) + lam * (1.0 - ssim)
+    loss_a.backward()
+    b = _raw_leaves(p, gpu)
+    loss_b, disp, _, _ = render_l1(w2c, K, W, H, b["means"], b["log_scales"], b["quats_raw"],
+                                   b["opacity_logits"], b["sh_dc"], b["sh_rest"], tgt,
+                                   ssim_lambda=lam)
+    loss_b.backward()
+    assert loss_b.shape == ()
+    assert abs(float(loss_b.detach()) - float(loss_a.detach())) <= 1e-5 * float(loss_a.detach())
+    assert helpers.max_abs(disp, img.detach()) <= 1e-4 * 255
+    for k in helpers.PARAMS:
+        assert helpers.rel_l2(b[k].grad, a[k].grad) <= 1e-4, k
