@@ -200,9 +200,10 @@ def gpu_step(render, leaves: dict, cam: dict, target: torch.Tensor):
     return loss, image
 
 
-def fused_step(leaves: dict, cam: dict, target: torch.Tensor):
+def fused_step(leaves: dict, cam: dict, target: torch.Tensor, ssim_lambda: float = 0.0):
     """The same step through cuda_rasterizer.fused.render_l1 (activations, render and
-    L1 loss as one autograd node of library kernels)."""
+    L1 loss -- plus the SSIM term with ssim_lambda > 0 -- as one autograd node of
+    library kernels)."""
     from cuda_rasterizer.fused import render_l1
 
     for t in leaves.values():
@@ -210,7 +211,7 @@ def fused_step(leaves: dict, cam: dict, target: torch.Tensor):
     loss, image, _, _ = render_l1(cam["w2c"], cam["K"], cam["width"], cam["height"],
                                   leaves["means"], leaves["log_scales"], leaves["quats_raw"],
                                   leaves["opacity_logits"], leaves["sh_dc"], leaves["sh_rest"],
-                                  target, near_plane=cam["near"])
+                                  target, near_plane=cam["near"], ssim_lambda=ssim_lambda)
     loss.backward()
     return loss, image
 
@@ -274,6 +275,28 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused") -> dict:
                 n=scene["params"]["means"].shape[0], n_visible=int(mask.sum()), keys=int(ids.numel()),
                 n_tiles=int(off.numel()), visited=visited, composited=composited,
                 loss=float(loss.detach()), width=cam["width"], height=cam["height"])
+
+
+def run_full_loss(scene: dict, steps: int, warmup: int, ssim_lambda: float = 0.2) -> dict:
+    """The fused step with the reference's full training loss,
+    (1 - lambda) L1 + lambda (1 - SSIM), lambda = 0.2 (scripts/train.py:185-205 after
+    its warm-up): wall clock over `steps` steps, synchronised on both sides."""
+    dev = torch.device("cuda:0")
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in scene["params"].items()}
+    cam = dict(scene["camera"])
+    cam["w2c"] = cam["w2c"].to(dev)
+    cam["K"] = cam["K"].to(dev)
+    target = scene["target"].to(dev)
+    for _ in range(warmup):
+        fused_step(leaves, cam, target, ssim_lambda)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss, _ = fused_step(leaves, cam, target, ssim_lambda)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"ssim_lambda": ssim_lambda, "ms_per_step": round(ms, 4),
+            "loss": round(float(loss.detach()), 6)}
 
 
 def run_ssim(scene: dict, steps: int, warmup: int) -> dict:
@@ -784,6 +807,8 @@ def main(argv=None):
         drop_in = {"ms_per_step": round(d["ms"], 3), "loss": d["loss"],
                    "stages": roofline(d, scene["name"])["per_stage"]}
     ssim = None if args.no_ssim else run_ssim(scene, args.steps, args.warmup)
+    if ssim is not None and args.path == "fused":
+        ssim["fused_step_l1_ssim"] = run_full_loss(scene, args.steps, args.warmup)
     train = None
     if not args.no_train and args.path == "fused":
         train = train_stress(args.train_steps, args.train_path)
