@@ -1171,9 +1171,12 @@ extern "C" int gs_rasterize_l1_backward(
     const float *colors, int64_t n, int32_t width, int32_t height, int32_t tile_size,
     float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
     float *grad_points_image, float *grad_cov_inv_image, float *grad_opacities,
-    float *grad_colors, int32_t accumulate, const float *grad_display01, hipStream_t stream) {
-    if (!target || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
-    const float inv_count = (float)(1.0 / ((double)width * (double)height * 3.0));
+    float *grad_colors, int32_t accumulate, float loss_scale, const float *grad_display01,
+    hipStream_t stream) {
+    if (!target || width <= 0 || height <= 0 || !(loss_scale == loss_scale))
+        return GS_ERR_INVALID_ARGUMENT;
+    // d loss / d (display / 255) = sign * *grad_loss * loss_scale / (H * W * 3)
+    const float inv_count = (float)((double)loss_scale / ((double)width * (double)height * 3.0));
     return rasterize_backward_impl(target, image, indexing_offset, gaussian_ids_sorted, n_tiles,
                                    k, points_image, cov_inv_image, opacities, colors, n, width,
                                    height, tile_size, alpha_threshold, transmittance_threshold,

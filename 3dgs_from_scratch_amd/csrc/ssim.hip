@@ -75,7 +75,15 @@ struct Planes {
     int tiles_x, tiles_y, tiles;
     int valid;             // mean over pixels at least kRadius from the border
     float inv_count;       // 1 / pixels in the mean (all planes)
+    float inv1;            // img1 values are its elements * inv1 (1: as stored)
 };
+
+// Element of img1 as the SSIM sees it: times inv1 = 1 / divisor rounded to
+// float, which is how PyTorch's GPU kernels compute image / divisor for a
+// scalar divisor (so the values equal the reference's rendered_image / 255).
+__device__ __forceinline__ float img1_value(const Planes &p, float v) {
+    return p.inv1 == 1.0f ? v : v * p.inv1;
+}
 
 __device__ __forceinline__ bool in_region(const Planes &p, int y, int x) {
     if (!p.valid) return true;
@@ -213,7 +221,7 @@ __device__ __forceinline__ void load_images(const Planes &p, const Tile &t,
     for (int it = 0; it < kStageIters; ++it) {
         int r, col, gy, gx;
         const bool in = stage_pos(p, t, it, r, col, gy, gx);
-        vx[it] = in ? b1[gy * p.r1 + gx * p.c1] : 0.0f;
+        vx[it] = in ? img1_value(p, b1[gy * p.r1 + gx * p.c1]) : 0.0f;
         vy[it] = in ? b2[gy * p.r2 + gx * p.c2] : 0.0f;
     }
 }
@@ -317,14 +325,23 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
 }
 
 // *mean = (sum of partials, fixed order) * inv_count; NaN for an empty region.
+// With loss, also *loss = (1 - lambda) * *other + lambda * (1 - *mean), in
+// float as a PyTorch expression of those scalars would round it.
 __global__ __launch_bounds__(kThreads) void ssim_mean_kernel(const double *__restrict__ partials,
                                                               int64_t n, double count,
-                                                              float *__restrict__ mean) {
+                                                              float *__restrict__ mean,
+                                                              const float *__restrict__ other,
+                                                              float lambda,
+                                                              float *__restrict__ loss) {
     __shared__ double red[kWaves];
     double v = 0.0;
     for (int64_t i = threadIdx.x; i < n; i += kThreads) v += partials[i];
     const double s = block_sum(v, red);
-    if (threadIdx.x == 0) *mean = (float)(count > 0.0 ? s / count : __builtin_nan(""));
+    if (threadIdx.x == 0) {
+        const float m = (float)(count > 0.0 ? s / count : __builtin_nan(""));
+        *mean = m;
+        if (loss) *loss = (1.0f - lambda) * *other + lambda * (1.0f - m);
+    }
 }
 
 // Persistent like the forward: the next tile's map window is loaded while the
@@ -333,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void ssim_mean_kernel(const double *__res
 __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     Planes p, Window win, const float *__restrict__ grad_mean, const float *__restrict__ d_mu,
     const float *__restrict__ d_xx, const float *__restrict__ d_xy, float *__restrict__ grad,
-    int64_t gs0, int64_t gs1, int gs2, int gs3) {
+    int64_t gs0, int64_t gs1, int gs2, int gs3, float grad_scale) {
     __shared__ float stage[3][kInY][kPitch];
     __shared__ __align__(16) float rows[3][kInY][kTileX];
     float v[3][kStageIters];
@@ -341,7 +358,7 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     int t0, t1;
     tile_range(p, t0, t1);
     if (t0 < t1) load_maps(p, tile_of(p, t0), d_mu, d_xx, d_xy, v);
-    const float up = *grad_mean;
+    const float up = grad_scale * *grad_mean;
     const bool interleave3 = p.channels == 3 && gs1 == 1 && gs3 == 3;
     const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
     for (int t = t0; t < t1; ++t) {
@@ -354,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
         for (int o = 0; o < kRowsPerWave; ++o) {
             const int gy = tl.oy + r0 + o;
             const bool in = gy < p.height && gx < p.width;
-            xs[o] = in ? b1[gy * p.r1 + gx * p.c1] : 0.0f;
+            xs[o] = in ? img1_value(p, b1[gy * p.r1 + gx * p.c1]) : 0.0f;
             ys[o] = in ? b2[gy * p.r2 + gx * p.c2] : 0.0f;
         }
         __syncthreads();
@@ -455,6 +472,7 @@ int fill_planes(Planes &p, const Geometry &g, const float *img1, const int64_t *
     p.tiles = g.tiles;
     p.valid = valid ? 1 : 0;
     p.inv_count = 0.0f;
+    p.inv1 = 1.0f;
     return GS_OK;
 }
 
@@ -482,16 +500,19 @@ extern "C" int gs_ssim_workspace_size(int32_t batch, int32_t channels, int32_t h
 extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const float *img2,
                                const int64_t *strides2, int32_t batch, int32_t channels,
                                int32_t height, int32_t width, int32_t valid_padding,
-                               float *ssim_mean, float *dm_dmu1, float *dm_dsigma1_sq,
-                               float *dm_dsigma12, void *workspace, size_t workspace_bytes,
-                               hipStream_t stream) {
+                               float img1_divisor, float *ssim_mean, float *dm_dmu1,
+                               float *dm_dsigma1_sq, float *dm_dsigma12, const float *other_loss,
+                               float lambda, float *loss, void *workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
     Geometry g;
     Planes p;
-    if (!geometry(batch, channels, height, width, g) || !ssim_mean)
+    if (!geometry(batch, channels, height, width, g) || !ssim_mean || !(img1_divisor > 0.0f))
         return GS_ERR_INVALID_ARGUMENT;
+    if (loss && !other_loss) return GS_ERR_INVALID_ARGUMENT;
     int st = fill_planes(p, g, img1, strides1, img2, strides2, channels, height, width,
                          valid_padding);
     if (st) return st;
+    p.inv1 = 1.0f / img1_divisor;
     if ((dm_dmu1 != nullptr) != (dm_dsigma1_sq != nullptr) ||
         (dm_dmu1 != nullptr) != (dm_dsigma12 != nullptr))
         return GS_ERR_INVALID_ARGUMENT;
@@ -505,28 +526,31 @@ extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const
     st = launch_status();
     if (st) return st;
     hipLaunchKernelGGL(ssim_mean_kernel, dim3(1), dim3(kThreads), 0, stream,
-                       (const double *)partials, (int64_t)g.blocks, count, ssim_mean);
+                       (const double *)partials, (int64_t)g.blocks, count, ssim_mean, other_loss,
+                       lambda, loss);
     return launch_status();
 }
 
 extern "C" int gs_ssim_backward(const float *grad_mean, const float *img1,
                                 const int64_t *strides1, const float *img2,
                                 const int64_t *strides2, int32_t batch, int32_t channels,
-                                int32_t height, int32_t width, const float *dm_dmu1,
-                                const float *dm_dsigma1_sq, const float *dm_dsigma12,
-                                float *grad_img1, const int64_t *grad_strides,
-                                hipStream_t stream) {
+                                int32_t height, int32_t width, float img1_divisor,
+                                const float *dm_dmu1, const float *dm_dsigma1_sq,
+                                const float *dm_dsigma12, float grad_scale, float *grad_img1,
+                                const int64_t *grad_strides, hipStream_t stream) {
     Geometry g;
     Planes p;
-    if (!geometry(batch, channels, height, width, g)) return GS_ERR_INVALID_ARGUMENT;
+    if (!geometry(batch, channels, height, width, g) || !(img1_divisor > 0.0f))
+        return GS_ERR_INVALID_ARGUMENT;
     int st = fill_planes(p, g, img1, strides1, img2, strides2, channels, height, width, 0);
     if (st) return st;
+    p.inv1 = 1.0f / img1_divisor;
     if (!grad_mean || !dm_dmu1 || !dm_dsigma1_sq || !dm_dsigma12 || !grad_img1 || !grad_strides)
         return GS_ERR_INVALID_ARGUMENT;
     if (!plane_fits(grad_strides, height, width)) return GS_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(ssim_backward_kernel, dim3(g.blocks), dim3(kThreads), 0, stream, p,
                        make_window(), grad_mean, dm_dmu1, dm_dsigma1_sq, dm_dsigma12, grad_img1,
                        grad_strides[0], grad_strides[1], (int)grad_strides[2],
-                       (int)grad_strides[3]);
+                       (int)grad_strides[3], grad_scale);
     return launch_status();
 }

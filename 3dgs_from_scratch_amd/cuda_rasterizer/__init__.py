@@ -750,12 +750,14 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
 def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorted, points_image,
                           cov_inv_image, opacities, colors, width, height, rendered_image,
                           alpha_threshold=1e-4, transmittance_threshold=1e-4,
-                          chi_squared_threshold=9.21, accumulators=None, grad_display01=None):
+                          chi_squared_threshold=9.21, accumulators=None, grad_display01=None,
+                          loss_scale=1.0):
     """Gradient of rasterize_display_l1's loss (times grad_loss, a 1-element fp32
     device tensor) w.r.t. the four blend inputs.  `accumulators`: a 9N buffer
     already zeroed (rasterize_display_l1's `clear`) that the gradients are added
     into; otherwise a zeroed one is allocated.  `grad_display01`: an (H, W, 3)
-    further gradient w.r.t. display / 255 (an SSIM term's), added to the L1 one."""
+    further gradient w.r.t. display / 255 (an SSIM term's), added to the L1 one;
+    `loss_scale` weights the L1 term (1 - lambda in an L1 + SSIM loss)."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -779,7 +781,8 @@ def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorte
             _ptr(target), _ptr(gl), _ptr(img), _ptr(off), _ptr(ids), off.shape[0], ids.shape[0],
             _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, 16,
             float(alpha_threshold), float(transmittance_threshold), float(chi_squared_threshold),
-            _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), 1, _ptr(extra), _stream(dev)),
+            _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), 1, float(loss_scale),
+            _ptr(extra), _stream(dev)),
             "rasterize_l1_backward")
         _lib.timer.stop(ev, dev)
     return g_pts, g_conic, g_opac, g_col

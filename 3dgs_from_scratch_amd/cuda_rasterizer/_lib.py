@@ -41,7 +41,7 @@ SIGNATURES = {
     + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 5 + [_I64, _P],
     "gs_l1_finish": [_P, _I32, _I64, _P, _P],
     "gs_rasterize_l1_backward": [_P] * 5 + [_I32, _I64] + [_P] * 4
-    + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 4 + [_I32, _P, _P],
+    + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 4 + [_I32, _F, _P, _P],
     "gs_rasterize_display": [_P, _P, _I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F, _P, _P, _P],
     "gs_rasterize_display_backward": [_P] * 4 + [_I32, _I64] + [_P] * 4
@@ -73,8 +73,8 @@ SIGNATURES.update({
     "gs_accumulate_grad2d": [_P, _P, _I64, _I32, _I32, _P, _P, _P],
     "gs_gather_rows": [_I64, _P, _P, ctypes.POINTER(GsGatherTensor), _I32, _P],
     "gs_ssim_workspace_size": [_I32, _I32, _I32, _I32, _PSZ],
-    "gs_ssim_forward": [_P] * 4 + [_I32] * 5 + [_P] * 5 + [_SZ, _P],
-    "gs_ssim_backward": [_P] * 5 + [_I32] * 4 + [_P] * 5 + [_P],
+    "gs_ssim_forward": [_P] * 4 + [_I32] * 5 + [_F] + [_P] * 5 + [_F, _P, _P, _SZ, _P],
+    "gs_ssim_backward": [_P] * 5 + [_I32] * 4 + [_F] + [_P] * 3 + [_F, _P, _P, _P],
 })
 
 _lib = None

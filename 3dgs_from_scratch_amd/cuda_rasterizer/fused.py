@@ -59,12 +59,13 @@ class RenderL1Function(torch.autograd.Function):
             transmittance_threshold, chi_squared_threshold, clear=acc)
         ssim_saved = ()
         if ssim_lambda > 0.0:
-            # the reference's rendered_image / 255 (its render() returns the display
-            # image) and its permuted (1, 3, H, W) views
-            d01 = display / 255.0
-            s, maps = _ssim.ssim_forward(_chw(d01), _chw(target), ssim_padding, with_maps=True)
-            loss = (1.0 - ssim_lambda) * loss.reshape(()) + ssim_lambda * (1.0 - s)
-            ssim_saved = (d01,) + tuple(maps)
+            # SSIM of the reference's rendered_image / 255 (its render() returns the
+            # display image; the kernels divide on load) on the permuted (1, 3, H, W)
+            # views, and the combined loss from the same launches
+            _, maps, loss = _ssim.ssim_forward(_chw(display), _chw(target), ssim_padding,
+                                               with_maps=True, img1_divisor=255.0,
+                                               other_loss=loss, lam=ssim_lambda)
+            ssim_saved = (display,) + tuple(maps)
         ctx.save_for_backward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
                               sh_coeffs_rest, world_to_camera, intrinsic, target, opac, pts, cov,
                               conic, mask, colors, off, ids, image, acc, *ssim_saved)
@@ -89,13 +90,13 @@ class RenderL1Function(torch.autograd.Function):
         lam = ctx.ssim_lambda
         extra = None
         if lam > 0.0:  # d loss / d SSIM = -lambda g; its gradient w.r.t. display / 255
-            d01, m1, m2, m3 = saved[19:]
-            extra = _ssim.ssim_backward(-lam * g, _chw(d01), _chw(target), (m1, m2, m3))
-            extra = extra[0].permute(1, 2, 0)  # laid out like d01: (H, W, 3) contiguous
-            g = (1.0 - lam) * g
+            display, m1, m2, m3 = saved[19:]
+            extra = _ssim.ssim_backward(g, _chw(display), _chw(target), (m1, m2, m3),
+                                        img1_divisor=255.0, grad_scale=-lam)
+            extra = extra[0].permute(1, 2, 0)  # laid out like display: (H, W, 3) contiguous
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_l1_backward(
             target, g, off, ids, pts, conic, opac, colors, width, height, image, a_thr, t_thr,
-            chi, accumulators=acc, grad_display01=extra)
+            chi, accumulators=acc, grad_display01=extra, loss_scale=1.0 - lam)
         if ctx.densifier is not None:
             ctx.densifier.update(g_pts, ctx.radii, width, height)
         g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(

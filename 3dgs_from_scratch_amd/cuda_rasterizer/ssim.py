@@ -52,9 +52,14 @@ def _check(img1: torch.Tensor, img2: torch.Tensor):
 
 
 def ssim_forward(img1: torch.Tensor, img2: torch.Tensor, padding: str = "same",
-                 with_maps: bool = True):
-    """Mean SSIM (0-d float32 device tensor) and, with_maps, the three
-    (B*C, H, W) derivative maps that ssim_backward reads."""
+                 with_maps: bool = True, img1_divisor: float = 1.0,
+                 other_loss: torch.Tensor | None = None, lam: float = 0.0):
+    """Mean SSIM (0-d float32 device tensor), with_maps the three (B*C, H, W)
+    derivative maps that ssim_backward reads, and -- with other_loss (a 1-element
+    float32 device tensor) -- the combined loss (1 - lam) * other_loss +
+    lam * (1 - mean) (else None), all from one launch pair.  The SSIM sees
+    img1 / img1_divisor as PyTorch's GPU kernels compute it (times the float
+    reciprocal), so a display image with divisor 255 equals display / 255.0."""
     _check(img1, img2)
     if padding not in ("same", "valid"):
         raise ValueError(f"fused_ssim: padding must be 'same' or 'valid', got {padding!r}")
@@ -65,6 +70,7 @@ def ssim_forward(img1: torch.Tensor, img2: torch.Tensor, padding: str = "same",
     _lib.check(lib.gs_ssim_workspace_size(b, c, h, w, ctypes.byref(sz)), "ssim_workspace_size")
     ws = torch.empty(max(int(sz.value), 8), dtype=torch.uint8, device=dev)
     mean = torch.empty((), dtype=torch.float32, device=dev)
+    loss = None if other_loss is None else torch.empty((), dtype=torch.float32, device=dev)
     maps = (tuple(torch.empty((b * c, h, w), dtype=torch.float32, device=dev) for _ in range(3))
             if with_maps else (None, None, None))
     s1, s2 = _strides(img1), _strides(img2)
@@ -72,16 +78,22 @@ def ssim_forward(img1: torch.Tensor, img2: torch.Tensor, padding: str = "same",
         ev = _lib.timer.record("ssim_forward", dev)
         _lib.check(lib.gs_ssim_forward(
             img1.data_ptr(), _sp(s1), img2.data_ptr(), _sp(s2), b, c, h, w,
-            1 if padding == "valid" else 0, mean.data_ptr(),
-            *(None if m is None else m.data_ptr() for m in maps), ws.data_ptr(), int(sz.value),
+            1 if padding == "valid" else 0, float(img1_divisor), mean.data_ptr(),
+            *(None if m is None else m.data_ptr() for m in maps),
+            None if other_loss is None else other_loss.data_ptr(), float(lam),
+            None if loss is None else loss.data_ptr(), ws.data_ptr(), int(sz.value),
             torch.cuda.current_stream(dev).cuda_stream), "ssim_forward")
         _lib.timer.stop(ev, dev)
+    if other_loss is not None:
+        return mean, maps, loss
     return mean, maps
 
 
-def ssim_backward(grad_mean: torch.Tensor, img1: torch.Tensor, img2: torch.Tensor, maps):
-    """grad_mean (a 1-element float32 device tensor) times d(mean SSIM)/d img1,
-    laid out like img1 when img1 is dense, else contiguous."""
+def ssim_backward(grad_mean: torch.Tensor, img1: torch.Tensor, img2: torch.Tensor, maps,
+                  img1_divisor: float = 1.0, grad_scale: float = 1.0):
+    """grad_scale * grad_mean (a 1-element float32 device tensor) times
+    d(mean SSIM)/d x, x = img1 / img1_divisor; laid out like img1 when img1 is
+    dense, else contiguous."""
     _check(img1, img2)
     dev = img1.device
     b, c, h, w = (int(x) for x in img1.shape)
@@ -92,8 +104,9 @@ def ssim_backward(grad_mean: torch.Tensor, img1: torch.Tensor, img2: torch.Tenso
         ev = _lib.timer.record("ssim_backward", dev)
         _lib.check(_lib.load().gs_ssim_backward(
             g.data_ptr(), img1.data_ptr(), _sp(s1), img2.data_ptr(), _sp(s2), b, c, h, w,
-            *(m.data_ptr() for m in maps), grad.data_ptr(), _sp(sg),
-            torch.cuda.current_stream(dev).cuda_stream), "ssim_backward")
+            float(img1_divisor), *(m.data_ptr() for m in maps), float(grad_scale),
+            grad.data_ptr(), _sp(sg), torch.cuda.current_stream(dev).cuda_stream),
+            "ssim_backward")
         _lib.timer.stop(ev, dev)
     return grad
 

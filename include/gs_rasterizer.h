@@ -287,10 +287,12 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
  * gs_rasterize_l1_backward: gs_rasterize_backward seeded by
  *   loss = mean(|clamp(image, 0, 1) * 255 / 255 - target|) with upstream
  *   gradient *grad_loss (device float): the image gradient is computed per
- *   pixel from image and target (image required; tile_size 16).  When
- *   grad_display01 is set (an (H, W, 3) image), it is a further gradient with
- *   respect to display / 255 (e.g. of an SSIM term on the same image,
- *   scripts/train.py:185-205), added to the L1 one at that node.
+ *   pixel from image and target (image required; tile_size 16), the L1 term
+ *   weighted by loss_scale (1 for the plain L1 loss; 1 - lambda in the
+ *   reference's L1 + SSIM loss).  When grad_display01 is set (an (H, W, 3)
+ *   image), it is a further gradient with respect to display / 255 (e.g. of an
+ *   SSIM term on the same image, scripts/train.py:185-205), added to the L1
+ *   one at that node.
  */
 int gs_activate(const float *log_scales, const float *quats_raw, const float *opacity_logits,
                 int64_t n, float *scales, float *quats, float *opacities, hipStream_t stream);
@@ -318,7 +320,8 @@ int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const 
                              float transmittance_threshold, float chi_squared_threshold,
                              float *grad_points_image, float *grad_cov_inv_image,
                              float *grad_opacities, float *grad_colors, int32_t accumulate,
-                             const float *grad_display01, hipStream_t stream);
+                             float loss_scale, const float *grad_display01,
+                             hipStream_t stream);
 
 /* ------------------------------------------------------------ training loop */
 
@@ -379,6 +382,9 @@ int gs_gather_rows(int64_t n_out, const int32_t *src_rows, const uint8_t *fresh_
  * images permuted to (1, C, H, W)).  SSIM per pixel: 11x11 Gaussian window of
  * standard deviation 1.5 per plane, zero padding, C1 = 0.01^2, C2 = 0.03^2.
  *
+ * The SSIM sees img1's elements times 1 / img1_divisor, the reciprocal rounded
+ *   to float (1: as stored; 255 for a [0, 255] display image: the values equal
+ *   PyTorch's GPU rendered_image / 255.0, which multiplies by that reciprocal).
  * gs_ssim_forward: *ssim_mean (device float) = mean of the SSIM map over every
  *   pixel (valid_padding = 0) or over the pixels at least 5 from the border
  *   (valid_padding = 1; NaN when that region is empty).  The three map pointers
@@ -387,22 +393,26 @@ int gs_gather_rows(int64_t n_out, const int32_t *src_rows, const uint8_t *fresh_
  *   and d mean / d E[xy] per pixel, with mu1 = E[x], E[x^2] and E[xy] taken as
  *   the independent local statistics (zero outside the region) -- for
  *   gs_ssim_backward.  The mean is reduced in a fixed order (deterministic).
- * gs_ssim_backward: grad_img1 (element strides grad_strides) = *grad_mean
- *   (device float) times d(mean SSIM)/d img1.  img2 gets no gradient.
+ *   When loss is set, also *loss = (1 - lambda) * *other_loss + lambda *
+ *   (1 - mean): the reference's training loss (scripts/train.py:205).
+ * gs_ssim_backward: grad_img1 (element strides grad_strides) = grad_scale *
+ *   *grad_mean (device float) times d(mean SSIM)/d x, x = img1 / img1_divisor.
+ *   img2 gets no gradient.
  * batch * channels must be <= 65535.
  */
 int gs_ssim_workspace_size(int32_t batch, int32_t channels, int32_t height, int32_t width,
                            size_t *bytes);
 int gs_ssim_forward(const float *img1, const int64_t *strides1, const float *img2,
                     const int64_t *strides2, int32_t batch, int32_t channels, int32_t height,
-                    int32_t width, int32_t valid_padding, float *ssim_mean, float *dm_dmu1,
-                    float *dm_dsigma1_sq, float *dm_dsigma12, void *workspace,
+                    int32_t width, int32_t valid_padding, float img1_divisor, float *ssim_mean,
+                    float *dm_dmu1, float *dm_dsigma1_sq, float *dm_dsigma12,
+                    const float *other_loss, float lambda, float *loss, void *workspace,
                     size_t workspace_bytes, hipStream_t stream);
 int gs_ssim_backward(const float *grad_mean, const float *img1, const int64_t *strides1,
                      const float *img2, const int64_t *strides2, int32_t batch, int32_t channels,
-                     int32_t height, int32_t width, const float *dm_dmu1,
-                     const float *dm_dsigma1_sq, const float *dm_dsigma12, float *grad_img1,
-                     const int64_t *grad_strides, hipStream_t stream);
+                     int32_t height, int32_t width, float img1_divisor, const float *dm_dmu1,
+                     const float *dm_dsigma1_sq, const float *dm_dsigma12, float grad_scale,
+                     float *grad_img1, const int64_t *grad_strides, hipStream_t stream);
 
 /*
  * Measurement entry (no counterpart in the reference): the work of the

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 9
+    assert lib.gs_abi_version() == 10
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -113,15 +113,19 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.gs_ssim_workspace_size(0, 3, 64, 64, ctypes.byref(sz)) == -1
     assert lib.gs_ssim_workspace_size(256, 256, 64, 64, ctypes.byref(sz)) == -1  # > 65535 planes
     st = (ctypes.c_int64 * 4)(3 * 64 * 64, 64 * 64, 64, 1)
-    assert lib.gs_ssim_forward(null, st, null, st, 1, 3, 64, 64, 1, null, null, null, null, null,
-                               0, null) == -1
+    assert lib.gs_ssim_forward(null, st, null, st, 1, 3, 64, 64, 1, 1.0, null, null, null, null,
+                               null, 0.0, null, null, 0, null) == -1
     fake = ctypes.c_void_p(256)  # never dereferenced: the host checks fail first
-    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, fake, fake, null, null, fake,
-                               1 << 20, null) == -1  # maps all set or all null
-    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, fake, null, null, null, fake,
-                               0, null) == -2  # workspace too small
-    assert lib.gs_ssim_backward(fake, fake, st, fake, st, 1, 3, 64, 64, fake, fake, null, fake, st,
-                                null) == -1
+    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, 1.0, fake, fake, null, null,
+                               null, 0.0, null, fake, 1 << 20, null) == -1  # maps all or none
+    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, 0.0, fake, null, null, null,
+                               null, 0.0, null, fake, 1 << 20, null) == -1  # divisor 0
+    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, 1.0, fake, null, null, null,
+                               null, 0.2, fake, fake, 1 << 20, null) == -1  # loss without other
+    assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, 1.0, fake, null, null, null,
+                               null, 0.0, null, fake, 0, null) == -2  # workspace too small
+    assert lib.gs_ssim_backward(fake, fake, st, fake, st, 1, 3, 64, 64, 1.0, fake, fake, null,
+                                1.0, fake, st, null) == -1
 
 
 def test_python_layer_refuses_cpu_tensors():

@@ -177,3 +177,24 @@ def test_backward_entry_scales_by_grad_mean(gpu):
     torch.testing.assert_close(g3, -3.0 * g1, rtol=1e-6, atol=0)
     want = ossim.ssim_backward(a.double().cpu().numpy(), b.double().cpu().numpy(), "valid")
     assert helpers.rel_l2(g1, torch.from_numpy(want)) <= GRAD_REL
+
+
+def test_divisor_combined_loss_and_grad_scale(gpu):
+    """img1_divisor = 255 on a [0, 255] image equals the plain call on image / 255
+    (the same true division); the combined loss is (1 - lam) * other + lam * (1 - mean);
+    grad_scale multiplies the upstream gradient."""
+    a, b = images((1, 3, 40, 50), seed=9)
+    a255, b = (a * 255.0).to(gpu), b.to(gpu)
+    other = torch.full((1,), 0.3, device=gpu)
+    mean_d, maps_d, loss = ssim_forward(a255, b, "valid", with_maps=True, img1_divisor=255.0,
+                                        other_loss=other, lam=0.2)
+    mean_p, maps_p = ssim_forward(a255 / 255.0, b, "valid", with_maps=True)
+    assert helpers.same(mean_d, mean_p)
+    for x, y in zip(maps_d, maps_p):
+        assert helpers.same(x, y)
+    want = (1.0 - 0.2) * 0.3 + 0.2 * (1.0 - float(mean_p))
+    assert abs(float(loss) - want) <= 1e-6
+    g = torch.full((1,), 1.5, device=gpu)
+    gd = ssim_backward(g, a255, b, maps_d, img1_divisor=255.0, grad_scale=-0.2)
+    gp = ssim_backward(g * -0.2, a255 / 255.0, b, maps_p)
+    torch.testing.assert_close(gd, gp, rtol=1e-6, atol=0)
