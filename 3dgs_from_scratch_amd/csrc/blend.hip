@@ -35,6 +35,14 @@ constexpr int kBatch = kWave;    // records staged per batch (one per lane)
 constexpr int kGradFields = 9;   // du, dv, dA, dB, dC, dopacity, dr, dg, db
 constexpr int kXcds = 8;
 
+// Work units of a tile's walk, counted by the forward and used to launch the
+// backward's tiles heaviest first: per staged batch, per staged record (its
+// staging and, for nearly all of them, the backward's wave sum and atomics) and
+// per evaluated strip, in proportion to the backward's instructions for each.
+constexpr uint32_t kCostBatch = 33;
+constexpr uint32_t kCostStaged = 11;
+constexpr uint32_t kCostStrip = 6;
+
 struct TileSpan {
     int32_t start, end;
 };
@@ -348,7 +356,8 @@ template <bool kSafe>
 __device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const LanePixels &pix,
                                             float alpha_thr, float T_thr, float chi,
                                             float (&T)[kStrips], float (&cr)[kStrips],
-                                            float (&cg)[kStrips], float (&cb)[kStrips]) {
+                                            float (&cg)[kStrips], float (&cb)[kStrips],
+                                            uint32_t &work) {
     const float4 geo = s.geo[j];
     const float4 aux = s.aux[j];
     const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
@@ -363,6 +372,7 @@ __device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const Lane
         const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
         const bool ok = !(T[q] < T_thr) && (E < chi);
         if (!wave_any(ok)) continue;
+        work += kCostStrip;
         const float alpha = alpha_of(E, aux.w);
         const bool inc = ok && !(alpha < alpha_thr);
         if (kSafe) {
@@ -385,9 +395,10 @@ template <bool kSafe>
 __device__ __forceinline__ void blend_batch(const BatchLds &s, int cnt, const LanePixels &pix,
                                             float alpha_thr, float T_thr, float chi,
                                             float (&T)[kStrips], float (&cr)[kStrips],
-                                            float (&cg)[kStrips], float (&cb)[kStrips]) {
+                                            float (&cg)[kStrips], float (&cb)[kStrips],
+                                            uint32_t &work) {
     for (int j = 0; j < cnt; ++j) {
-        blend_entry<kSafe>(s, j, pix, alpha_thr, T_thr, chi, T, cr, cg, cb);
+        blend_entry<kSafe>(s, j, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
         if ((j & 7) == 7 && !any_active(T, T_thr)) break;
     }
 }
@@ -407,7 +418,7 @@ __device__ __forceinline__ void blend_accumulate(
     const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, const LanePixels &pix,
     float alpha_thr, float T_thr_in, float chi, float (&cr)[kStrips], float (&cg)[kStrips],
-    float (&cb)[kStrips]) {
+    float (&cb)[kStrips], uint32_t &work) {
     // a pixel is active while !(T < T_thr)
     const float T_thr = effective_T_thr(T_thr_in);
     float T[kStrips];
@@ -423,10 +434,11 @@ __device__ __forceinline__ void blend_accumulate(
         if (!any_active(T, T_thr)) break;
         const Staged st = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
                                        alpha_thr, pix.x0, pix.y0);
+        work += kCostBatch + kCostStaged * (uint32_t)st.count;
         if (st.nonfinite)
-            blend_batch<true>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb);
+            blend_batch<true>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
         else
-            blend_batch<false>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb);
+            blend_batch<false>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
     }
 }
 
@@ -516,7 +528,8 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image,
     float *__restrict__ display, const float *__restrict__ target,
-    float *__restrict__ tile_loss, float4 *__restrict__ clear4, int64_t clear4_count) {
+    float *__restrict__ tile_loss, float4 *__restrict__ clear4, int64_t clear4_count,
+    uint32_t *__restrict__ tile_cost) {
     __shared__ BatchLds s;
     if (clear4) {  // this workgroup's share of the buffer to zero (stores overlap the blend)
         const int64_t per = (clear4_count + gridDim.x - 1) / gridDim.x;
@@ -529,8 +542,10 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
     float cr[kStrips], cg[kStrips], cb[kStrips];
+    uint32_t work = 0;
     blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr, chi, cr,
-                     cg, cb);
+                     cg, cb, work);
+    if (tile_cost && threadIdx.x == 0) tile_cost[tile] = work;
     float l1 = 0.0f;
 #pragma unroll
     for (int q = 0; q < kStrips; ++q) {
@@ -708,10 +723,13 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr_in, float chi, float *__restrict__ g_points,
     float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors,
-    const float *__restrict__ grad_loss, float inv_count, const float *__restrict__ extra) {
+    const float *__restrict__ grad_loss, float inv_count, const float *__restrict__ extra,
+    const int32_t *__restrict__ tile_order) {
     __shared__ BatchLds s;
     const float T_thr = effective_T_thr(T_thr_in);
-    const int tile = tile_of_block(blockIdx.x, n_tiles);
+    const int slot = tile_of_block(blockIdx.x, n_tiles);
+    const int tile = tile_order ? tile_order[slot] : slot;
+    if ((unsigned)tile >= (unsigned)n_tiles) return;  // uniform across the workgroup
     const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
     if (span.end <= span.start) return;  // uniform across the workgroup
@@ -720,9 +738,10 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
 
     BackwardLane L;
     float cr[kStrips], cg[kStrips], cb[kStrips];
+    uint32_t work = 0;  // unused here
     if (!image)
         blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr_in,
-                         chi, cr, cg, cb);
+                         chi, cr, cg, cb, work);
     bool finite = true;
 #pragma unroll
     for (int q = 0; q < kStrips; ++q) {
@@ -963,7 +982,8 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                           float alpha_threshold, float transmittance_threshold,
                           float chi_squared_threshold, float *image, float *display,
                           const float *target, float *tile_loss, hipStream_t stream,
-                          float *clear = nullptr, int64_t clear_count = 0) {
+                          float *clear = nullptr, int64_t clear_count = 0,
+                          uint32_t *tile_cost = nullptr) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -999,7 +1019,7 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
                            image, display, target, tile_loss,
                            fused_clear ? reinterpret_cast<float4 *>(clear) : nullptr,
-                           fused_clear ? clear_count / 4 : (int64_t)0);
+                           fused_clear ? clear_count / 4 : (int64_t)0, tile_cost);
     } else {
         hipLaunchKernelGGL(blend_forward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, indexing_offset,
@@ -1039,48 +1059,220 @@ extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
                           display, nullptr, nullptr, stream);
 }
 
+static int launch_l1_finish(int32_t n_tiles, const float *tile_loss, float inv_count, float *loss,
+                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream);
+
 extern "C" int gs_rasterize_display_l1(
     const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k,
     const float *points_image, const float *cov_inv_image, const float *opacities,
     const float *colors, int64_t n, int32_t width, int32_t height, int32_t tile_size,
     float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
-    const float *target, float *image, float *display, float *tile_loss, float *clear,
-    int64_t clear_count, hipStream_t stream) {
+    const float *target, float *image, float *display, float *tile_loss, float *loss,
+    int32_t *tile_schedule, float *clear, int64_t clear_count, hipStream_t stream) {
     if (!display || !target || !tile_loss || tile_size != kTile) return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     const int tiles_y = (height + tile_size - 1) / tile_size;
     if (n_tiles != tiles_x * tiles_y) return GS_ERR_INVALID_ARGUMENT;  // every tile's loss
-    return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
-                          cov_inv_image, opacities, colors, n, width, height, tile_size,
-                          alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
-                          display, target, tile_loss, stream, clear, clear_count);
+    uint32_t *cost = tile_schedule ? reinterpret_cast<uint32_t *>(tile_schedule) : nullptr;
+    int st = rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
+                            cov_inv_image, opacities, colors, n, width, height, tile_size,
+                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
+                            image, display, target, tile_loss, stream, clear, clear_count, cost);
+    if (st || n_tiles == 0) return st;
+    // the loss (when asked for) and the backward's tile order, in one launch
+    const double count = (double)width * (double)height * 3.0;
+    return launch_l1_finish(n_tiles, tile_loss, (float)(1.0 / count), loss, cost,
+                            tile_schedule ? tile_schedule + n_tiles : nullptr, stream);
 }
 
-// loss = (sum of the n_tiles partial sums) / count, one workgroup.
-__global__ __launch_bounds__(1024) void l1_finish_kernel(int n_tiles,
-                                                         const float *__restrict__ tile_loss,
-                                                         float inv_count,
-                                                         float *__restrict__ loss) {
-    __shared__ float tmp[1024 / kWave];
+// The backward's launch order from the forward's per-tile work: within each
+// XCD's contiguous tile range (the range tile_of_block gives XCD x), the tiles by
+// descending work, ties by tile, so that an XCD starts its heaviest tiles first
+// and the light ones fill the SIMDs as they free up.  order[p] is the tile that
+// the workgroup at range position p processes.  Work is compared through the
+// top 20 bits of its float value (relative resolution 2^-12); ranges of more
+// than kOrderMax tiles keep their own order.  One workgroup per range: each
+// wave sorts a contiguous chunk in registers, then every key's rank is its
+// position in its chunk plus its lower bound in each other chunk.
+constexpr int kFinishThreads = 512;
+constexpr int kOrderChunks = kFinishThreads / kWave;  // one wave per chunk
+constexpr int kOrderMaxPerLane = 8;
+constexpr int kOrderChunkMax = kWave * kOrderMaxPerLane;
+constexpr int kOrderMax = kOrderChunks * kOrderChunkMax;
+static_assert(kOrderMax <= 4096, "range positions are 12-bit fields of the keys");
+
+// Ascending keys: descending work, then ascending position in the range.
+__device__ __forceinline__ uint32_t order_key(uint32_t work, int local) {
+    const uint32_t q = __float_as_uint((float)work) >> 11;  // exponent + 12 mantissa bits
+    return ((~q & 0xFFFFFu) << 12) | (uint32_t)local;
+}
+
+// One wave sorts the keys v (lane l holds keys l + e * kWave; bitonic network
+// over kWave * EPT keys).  In the merge step of partner distance j within runs
+// of length k, the lower index of a pair keeps the minimum in ascending runs
+// ((index & k) == 0) and the maximum in descending ones; partners in another
+// lane are exchanged by lane permutes, those in another slot in registers.
+template <int EPT>
+__device__ __forceinline__ void wave_sort(uint32_t (&v)[EPT]) {
+    constexpr int P = kWave * EPT;
+    const int lane = threadIdx.x % kWave;
+    for (int k = 2; k <= P; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            if (j >= kWave) {  // partner in slot e ^ (j / kWave); direction by slot
+                const int ej = j / kWave;
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) {
+                    if (e & ej) continue;
+                    const int e2 = e | ej;
+                    const bool asc = ((e * kWave) & k) == 0;
+                    const uint32_t lo = min(v[e], v[e2]), hi = max(v[e], v[e2]);
+                    v[e] = asc ? lo : hi;
+                    v[e2] = asc ? hi : lo;
+                }
+                continue;
+            }
+            const int addr = (lane ^ j) << 2;
+            const bool lower = (lane & j) == 0;
+            const bool keep_min_l = lower == ((lane & k) == 0);  // k < kWave
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v[e]);
+                const bool keep_min = k < kWave ? keep_min_l : (lower == (((e * kWave) & k) == 0));
+                v[e] = keep_min ? min(v[e], w) : max(v[e], w);
+            }
+        }
+    }
+}
+
+template <int EPT>
+__device__ void order_range_sorted(uint32_t (*sorted)[kOrderChunkMax],
+                                   const uint32_t *__restrict__ cost, int start, int len,
+                                   int32_t *__restrict__ order) {
+    const int c = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int q = len / kOrderChunks, r = len % kOrderChunks;
+    const int n = q + (c < r ? 1 : 0), c0 = c * q + min(c, r);
+    uint32_t v[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = e * kWave + lane;
+        v[e] = i < n ? order_key(cost[start + c0 + i], c0 + i) : 0xFFFFFFFFu;
+    }
+    wave_sort<EPT>(v);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = e * kWave + lane;
+        if (i < n) sorted[c][i] = v[e];
+    }
+    __syncthreads();
+    // rank = sum over the chunks of the key's lower bound there (its own chunk
+    // gives its position), all searches stepping together
+    int pos[EPT][kOrderChunks];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e)
+#pragma unroll
+        for (int c2 = 0; c2 < kOrderChunks; ++c2) pos[e][c2] = 0;
+    for (int step = kWave * EPT; step > 0; step >>= 1) {
+        // all of a step's reads first (clamped, unconditional), then the updates;
+        // a probe past a chunk's end is discarded
+        uint32_t probe_key[EPT][kOrderChunks];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+#pragma unroll
+            for (int c2 = 0; c2 < kOrderChunks; ++c2) {
+                const int n2 = q + (c2 < r ? 1 : 0);
+                probe_key[e][c2] = sorted[c2][max(min(pos[e][c2] + step, n2) - 1, 0)];
+            }
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+#pragma unroll
+            for (int c2 = 0; c2 < kOrderChunks; ++c2) {
+                const int n2 = q + (c2 < r ? 1 : 0);
+                const int probe = pos[e][c2] + step;
+                const bool take = (probe <= n2) & (probe_key[e][c2] < v[e]);
+                pos[e][c2] = take ? probe : pos[e][c2];
+            }
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = e * kWave + lane;
+        if (i >= n) continue;
+        int rank = 0;
+#pragma unroll
+        for (int c2 = 0; c2 < kOrderChunks; ++c2) rank += pos[e][c2];
+        if (rank < len) order[start + rank] = start + (int)(v[e] & 0xFFFu);
+    }
+}
+
+__device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tiles,
+                            int32_t *__restrict__ order) {
+    __shared__ uint32_t sorted[kOrderChunks][kOrderChunkMax];
+    const int base = n_tiles / kXcds, rem = n_tiles % kXcds;
+    const int start = x * base + min(x, rem), len = base + (x < rem ? 1 : 0);
+    const int chunk = (len + kOrderChunks - 1) / kOrderChunks;  // largest chunk
+    if (chunk <= kWave) {
+        order_range_sorted<1>(sorted, cost, start, len, order);
+    } else if (chunk <= 2 * kWave) {
+        order_range_sorted<2>(sorted, cost, start, len, order);
+    } else if (chunk <= 4 * kWave) {
+        order_range_sorted<4>(sorted, cost, start, len, order);
+    } else if (chunk <= kOrderChunkMax) {
+        order_range_sorted<kOrderMaxPerLane>(sorted, cost, start, len, order);
+    } else {
+        for (int i = threadIdx.x; i < len; i += kFinishThreads) order[start + i] = start + i;
+    }
+}
+
+// Workgroups 0..kXcds-1 (with tile_order) order the backward's tiles; the last
+// workgroup (with loss) writes loss = (sum of the n_tiles partial sums) * inv_count.
+__global__ __launch_bounds__(kFinishThreads) void l1_finish_kernel(
+    int n_tiles, const float *__restrict__ tile_loss, float inv_count, float *__restrict__ loss,
+    const uint32_t *__restrict__ tile_cost, int32_t *__restrict__ tile_order) {
+    if (tile_order && (int)blockIdx.x < kXcds) {
+        order_range((int)blockIdx.x, tile_cost, n_tiles, tile_order);
+        return;
+    }
+    if (!loss) return;
+    __shared__ float tmp[kFinishThreads / kWave];
+    // kLossLoads independent loads in flight per thread
+    constexpr int kLossLoads = 8;
+    float part[kLossLoads];
+#pragma unroll
+    for (int u = 0; u < kLossLoads; ++u) part[u] = 0.0f;
+    for (int t0 = threadIdx.x; t0 < n_tiles; t0 += kFinishThreads * kLossLoads) {
+#pragma unroll
+        for (int u = 0; u < kLossLoads; ++u) {
+            const int t = t0 + u * kFinishThreads;
+            if (t < n_tiles) part[u] += tile_loss[t];
+        }
+    }
     float acc = 0.0f;
-    for (int t = threadIdx.x; t < n_tiles; t += 1024) acc += tile_loss[t];
+#pragma unroll
+    for (int u = 0; u < kLossLoads; ++u) acc += part[u];
     acc = wave_sum(acc);
     if (threadIdx.x % kWave == 0) tmp[threadIdx.x / kWave] = acc;
     __syncthreads();
     if (threadIdx.x == 0) {
         float total = 0.0f;
-        for (int w = 0; w < 1024 / kWave; ++w) total += tmp[w];
+        for (int w = 0; w < kFinishThreads / kWave; ++w) total += tmp[w];
         *loss = total * inv_count;
     }
+}
+
+static int launch_l1_finish(int32_t n_tiles, const float *tile_loss, float inv_count, float *loss,
+                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream) {
+    const int blocks = (tile_order ? kXcds : 0) + (loss ? 1 : 0);
+    if (blocks == 0) return GS_OK;
+    hipLaunchKernelGGL(l1_finish_kernel, dim3(blocks), dim3(kFinishThreads), 0, stream, n_tiles,
+                       tile_loss, inv_count, loss, tile_cost, tile_order);
+    return launch_status();
 }
 
 extern "C" int gs_l1_finish(const float *tile_loss, int32_t n_tiles, int64_t count, float *loss,
                             hipStream_t stream) {
     if (n_tiles < 0 || count <= 0 || !loss || (n_tiles > 0 && !tile_loss))
         return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(l1_finish_kernel, dim3(1), dim3(1024), 0, stream, n_tiles, tile_loss,
-                       (float)(1.0 / (double)count), loss);
-    return launch_status();
+    return launch_l1_finish(n_tiles, tile_loss, (float)(1.0 / (double)count), loss, nullptr,
+                            nullptr, stream);
 }
 
 static int rasterize_backward_impl(
@@ -1091,7 +1283,7 @@ static int rasterize_backward_impl(
     float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
     float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
     int seed, const float *grad_loss, float inv_count, hipStream_t stream,
-    const float *extra = nullptr) {
+    const float *extra = nullptr, const int32_t *tile_order = nullptr) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -1120,7 +1312,7 @@ static int rasterize_backward_impl(
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
                            grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors,
-                           grad_loss, inv_count, extra);
+                           grad_loss, inv_count, extra, tile_order);
     } else {
         hipLaunchKernelGGL(blend_backward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, grad_image, image,
@@ -1172,7 +1364,7 @@ extern "C" int gs_rasterize_l1_backward(
     float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
     float *grad_points_image, float *grad_cov_inv_image, float *grad_opacities,
     float *grad_colors, int32_t accumulate, float loss_scale, const float *grad_display01,
-    hipStream_t stream) {
+    const int32_t *tile_schedule, hipStream_t stream) {
     if (!target || width <= 0 || height <= 0 || !(loss_scale == loss_scale))
         return GS_ERR_INVALID_ARGUMENT;
     // d loss / d (display / 255) = sign * *grad_loss * loss_scale / (H * W * 3)
@@ -1182,7 +1374,8 @@ extern "C" int gs_rasterize_l1_backward(
                                    height, tile_size, alpha_threshold, transmittance_threshold,
                                    chi_squared_threshold, grad_points_image, grad_cov_inv_image,
                                    grad_opacities, grad_colors, accumulate, kSeedL1, grad_loss,
-                                   inv_count, stream, grad_display01);
+                                   inv_count, stream, grad_display01,
+                                   tile_schedule ? tile_schedule + n_tiles : nullptr);
 }
 
 extern "C" int gs_rasterize_work(const int32_t *indexing_offset,

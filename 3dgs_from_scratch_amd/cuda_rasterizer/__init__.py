@@ -398,6 +398,21 @@ def blend_grad_accumulators(n, device):
     return torch.empty((9 * int(n),), dtype=torch.float32, device=device)
 
 
+def tile_schedule(n_tiles, device):
+    """An uninitialised int32 buffer of 2 * n_tiles: pass it as
+    rasterize_display_l1(schedule=...) (which fills it: the work of each tile,
+    then the backward's launch order) and then as rasterize_l1_backward(schedule=...)."""
+    return torch.empty((2 * max(int(n_tiles), 1),), dtype=torch.int32, device=device)
+
+
+def _check_schedule(schedule, n_tiles, dev, who):
+    if (not isinstance(schedule, torch.Tensor) or schedule.dtype != torch.int32
+            or schedule.device != dev or not schedule.is_contiguous()
+            or schedule.numel() < 2 * n_tiles):
+        raise RuntimeError(f"{who}: schedule must be a contiguous int32 tensor of at least "
+                           f"{2 * n_tiles} elements on {dev}")
+
+
 def rasterize_backward(
     grad_rendered_image,
     indexing_offset,
@@ -718,10 +733,14 @@ def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, g
 
 def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
                          opacities, colors, width, height, target, alpha_threshold=1e-4,
-                         transmittance_threshold=1e-4, chi_squared_threshold=9.21, clear=None):
+                         transmittance_threshold=1e-4, chi_squared_threshold=9.21, clear=None,
+                         schedule=None):
     """rasterize_display with tile size 16 plus loss = mean(|display / 255 - target|).
     Returns (image, display, loss[1] fp32).  `clear` (an fp32 device tensor, e.g.
-    from blend_grad_accumulators) is zeroed by the same launch."""
+    from blend_grad_accumulators) is zeroed by the same launch.  `schedule` (an
+    int32 device tensor of 2 * n_tiles, see tile_schedule) receives the work per
+    tile and the order in which rasterize_l1_backward, given it, launches the
+    tiles (heaviest first)."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -732,6 +751,8 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
     n_tiles = off.shape[0]
     tile_loss = torch.empty((max(n_tiles, 1),), dtype=f32, device=dev)
     loss = torch.empty((1,), dtype=f32, device=dev)
+    if schedule is not None:
+        _check_schedule(schedule, n_tiles, dev, "rasterize_display_l1")
     lib = _lib.load()
     with torch.cuda.device(dev):
         ev = _lib.timer.record("rasterize_display_l1", dev)
@@ -739,11 +760,9 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
             _ptr(off), _ptr(ids), n_tiles, ids.shape[0], _ptr(pts), _ptr(conic), _ptr(opac),
             _ptr(col), n, width, height, 16, float(alpha_threshold), float(transmittance_threshold),
             float(chi_squared_threshold), _ptr(target), _ptr(image), _ptr(display), _ptr(tile_loss),
-            _ptr(clear), 0 if clear is None else clear.numel(), _stream(dev)),
-            "rasterize_display_l1")
+            _ptr(loss), _ptr(schedule), _ptr(clear), 0 if clear is None else clear.numel(),
+            _stream(dev)), "rasterize_display_l1")
         _lib.timer.stop(ev, dev)
-        _lib.check(lib.gs_l1_finish(_ptr(tile_loss), n_tiles, height * width * 3, _ptr(loss),
-                                    _stream(dev)), "l1_finish")
     return image, display, loss
 
 
@@ -751,13 +770,15 @@ def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorte
                           cov_inv_image, opacities, colors, width, height, rendered_image,
                           alpha_threshold=1e-4, transmittance_threshold=1e-4,
                           chi_squared_threshold=9.21, accumulators=None, grad_display01=None,
-                          loss_scale=1.0):
+                          loss_scale=1.0, schedule=None):
     """Gradient of rasterize_display_l1's loss (times grad_loss, a 1-element fp32
     device tensor) w.r.t. the four blend inputs.  `accumulators`: a 9N buffer
     already zeroed (rasterize_display_l1's `clear`) that the gradients are added
     into; otherwise a zeroed one is allocated.  `grad_display01`: an (H, W, 3)
     further gradient w.r.t. display / 255 (an SSIM term's), added to the L1 one;
-    `loss_scale` weights the L1 term (1 - lambda in an L1 + SSIM loss)."""
+    `loss_scale` weights the L1 term (1 - lambda in an L1 + SSIM loss).
+    `schedule`: the tensor rasterize_display_l1 filled for the same layout (the
+    tiles then start heaviest first; the gradients do not depend on it)."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -775,6 +796,8 @@ def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorte
             raise RuntimeError("rasterize_l1_backward: accumulators must be a contiguous fp32 "
                                f"tensor of {9 * n} elements on {dev}")
         g_pts, g_conic, g_opac, g_col = _blend_grad_views(accumulators, n)
+    if schedule is not None:
+        _check_schedule(schedule, off.shape[0], dev, "rasterize_l1_backward")
     with torch.cuda.device(dev):
         ev = _lib.timer.record("rasterize_l1_backward", dev)
         _lib.check(_lib.load().gs_rasterize_l1_backward(
@@ -782,7 +805,7 @@ def rasterize_l1_backward(target, grad_loss, indexing_offset, gaussian_ids_sorte
             _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, 16,
             float(alpha_threshold), float(transmittance_threshold), float(chi_squared_threshold),
             _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), 1, float(loss_scale),
-            _ptr(extra), _stream(dev)),
+            _ptr(extra), _ptr(schedule), _stream(dev)),
             "rasterize_l1_backward")
         _lib.timer.stop(ev, dev)
     return g_pts, g_conic, g_opac, g_col

@@ -54,9 +54,11 @@ class RenderL1Function(torch.autograd.Function):
         off, ids = _cr.compute_tile_intersection(pts, radii, depths, mask, width, height, 16)
         # the blend gradients' accumulators, zeroed by the forward blend launch
         acc = _cr.blend_grad_accumulators(means.shape[0], means.device)
+        # the forward's work per tile orders the backward's tiles (heaviest first)
+        sched = _cr.tile_schedule(off.shape[0], means.device)
         image, display, loss = _cr.rasterize_display_l1(
             off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
-            transmittance_threshold, chi_squared_threshold, clear=acc)
+            transmittance_threshold, chi_squared_threshold, clear=acc, schedule=sched)
         ssim_saved = ()
         if ssim_lambda > 0.0:
             # SSIM of the reference's rendered_image / 255 (its render() returns the
@@ -68,7 +70,7 @@ class RenderL1Function(torch.autograd.Function):
             ssim_saved = (display,) + tuple(maps)
         ctx.save_for_backward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
                               sh_coeffs_rest, world_to_camera, intrinsic, target, opac, pts, cov,
-                              conic, mask, colors, off, ids, image, acc, *ssim_saved)
+                              conic, mask, colors, off, ids, image, acc, sched, *ssim_saved)
         ctx.ssim_lambda = ssim_lambda
         ctx.densifier = densifier
         ctx.radii = radii if densifier is not None else None
@@ -82,7 +84,7 @@ class RenderL1Function(torch.autograd.Function):
     def backward(ctx, grad_loss, grad_display, grad_pts, grad_radii):
         saved = ctx.saved_tensors
         (means, log_scales, quats_raw, logits, dc, rest, w2c, K, target, opac, pts, cov, conic,
-         mask, colors, off, ids, image, acc) = saved[:19]
+         mask, colors, off, ids, image, acc, sched) = saved[:20]
         width, height, a_thr, t_thr, chi = ctx.params
         if grad_loss is None:
             return (None,) * 22
@@ -90,13 +92,13 @@ class RenderL1Function(torch.autograd.Function):
         lam = ctx.ssim_lambda
         extra = None
         if lam > 0.0:  # d loss / d SSIM = -lambda g; its gradient w.r.t. display / 255
-            display, m1, m2, m3 = saved[19:]
+            display, m1, m2, m3 = saved[20:]
             extra = _ssim.ssim_backward(g, _chw(display), _chw(target), (m1, m2, m3),
                                         img1_divisor=255.0, grad_scale=-lam)
             extra = extra[0].permute(1, 2, 0)  # laid out like display: (H, W, 3) contiguous
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_l1_backward(
             target, g, off, ids, pts, conic, opac, colors, width, height, image, a_thr, t_thr,
-            chi, accumulators=acc, grad_display01=extra, loss_scale=1.0 - lam)
+            chi, accumulators=acc, grad_display01=extra, loss_scale=1.0 - lam, schedule=sched)
         if ctx.densifier is not None:
             ctx.densifier.update(g_pts, ctx.radii, width, height)
         g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(

@@ -282,7 +282,12 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
  *   it also writes clear_count zeros there (in the blend kernel when clear is
  *   16-byte aligned and clear_count a multiple of 4): the accumulators that
  *   gs_rasterize_l1_backward then adds into with accumulate = 1, without a
- *   separate fill.
+ *   separate fill.  When loss is set, loss = sum(tile_loss) / (H * W * 3) is
+ *   written as well (the gs_l1_finish result).  When tile_schedule is set
+ *   (2 * n_tiles int32), the forward's work per tile goes to its first half
+ *   and the backward's launch order to its second: per XCD's tile range, the
+ *   tiles by descending work, so that gs_rasterize_l1_backward, given the same
+ *   buffer, starts the heaviest tiles first (the results do not depend on it).
  * gs_l1_finish: loss = sum(tile_loss) / count (count = H * W * 3), one float.
  * gs_rasterize_l1_backward: gs_rasterize_backward seeded by
  *   loss = mean(|clamp(image, 0, 1) * 255 / 255 - target|) with upstream
@@ -292,7 +297,9 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
  *   reference's L1 + SSIM loss).  When grad_display01 is set (an (H, W, 3)
  *   image), it is a further gradient with respect to display / 255 (e.g. of an
  *   SSIM term on the same image, scripts/train.py:185-205), added to the L1
- *   one at that node.
+ *   one at that node.  tile_schedule: null, or the buffer that
+ *   gs_rasterize_display_l1 filled for the same tile layout (its order is a
+ *   permutation of the tiles; other contents give wrong gradients).
  */
 int gs_activate(const float *log_scales, const float *quats_raw, const float *opacity_logits,
                 int64_t n, float *scales, float *quats, float *opacities, hipStream_t stream);
@@ -308,7 +315,8 @@ int gs_rasterize_display_l1(const int32_t *indexing_offset, const int32_t *gauss
                             int32_t tile_size, float alpha_threshold,
                             float transmittance_threshold, float chi_squared_threshold,
                             const float *target, float *image, float *display, float *tile_loss,
-                            float *clear, int64_t clear_count, hipStream_t stream);
+                            float *loss, int32_t *tile_schedule, float *clear,
+                            int64_t clear_count, hipStream_t stream);
 int gs_l1_finish(const float *tile_loss, int32_t n_tiles, int64_t count, float *loss,
                  hipStream_t stream);
 int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const float *image,
@@ -321,7 +329,7 @@ int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const 
                              float *grad_points_image, float *grad_cov_inv_image,
                              float *grad_opacities, float *grad_colors, int32_t accumulate,
                              float loss_scale, const float *grad_display01,
-                             hipStream_t stream);
+                             const int32_t *tile_schedule, hipStream_t stream);
 
 /* ------------------------------------------------------------ training loop */
 

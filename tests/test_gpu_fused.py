@@ -192,6 +192,59 @@ def test_display_l1_clears_buffer(gpu, count):
         assert torch.equal(x, y)
 
 
+def _xcd_ranges(n_tiles):
+    base, rem = divmod(n_tiles, 8)
+    start = 0
+    for x in range(8):
+        size = base + (1 if x < rem else 0)
+        yield start, size
+        start += size
+
+
+@pytest.mark.parametrize("size", [(200, 130), (2560, 1600), (3840, 2160), (4096, 2112)])
+def test_tile_schedule(gpu, size):
+    """rasterize_display_l1(schedule=...) leaves the image, display and loss as
+    without it, writes each tile's work and, per XCD range of at most 4096
+    tiles, the tiles by descending work (ties by tile; larger ranges keep their
+    order); rasterize_l1_backward gives the same gradients with the schedule as
+    without (up to the order of the float atomics)."""
+    W, H = size
+    p, cam, target = helpers.scene_box(8_000, W, H, 220.0 * W / 200, seed=25,
+                                       log_scale=(-3.5, 0.6))
+    a = _raw_leaves(p, gpu)
+    tgt = target.to(gpu)
+    with torch.no_grad():
+        pts, depths, _, conic, radii, mask, opac, colors = cr.preprocess_forward(
+            a["means"], a["log_scales"], a["quats_raw"], a["opacity_logits"], a["sh_dc"],
+            a["sh_rest"], cam["w2c"].to(gpu), cam["K"].to(gpu), 0.01, 100.0, 1 / 255, 0.5, 128.0,
+            W, H)
+        off, ids = cr.compute_tile_intersection(pts, radii, depths, mask, W, H, 16)
+        n_tiles = off.shape[0]
+        ref = cr.rasterize_display_l1(off, ids, pts, conic, opac, colors, W, H, tgt)
+        sched = cr.tile_schedule(n_tiles, gpu)
+        got = cr.rasterize_display_l1(off, ids, pts, conic, opac, colors, W, H, tgt,
+                                      schedule=sched)
+        for x, y in zip(got, ref):
+            assert torch.equal(x, y)
+        cost = sched[:n_tiles].cpu().numpy().view("uint32").astype("int64")
+        order = sched[n_tiles:2 * n_tiles].cpu().numpy()
+        assert cost.max() > 0
+        for start, length in _xcd_ranges(n_tiles):
+            got_order = list(order[start:start + length])
+            if length > 4096:
+                assert got_order == list(range(start, start + length))
+                continue
+            # work compared through the top 20 bits of its float32 value
+            q = (cost[start:start + length].astype("float32").view("uint32") >> 11).astype("int64")
+            want = sorted(range(start, start + length), key=lambda t: (-q[t - start], t))
+            assert got_order == want
+        g = torch.full((1,), 0.7, device=gpu)
+        grads = [cr.rasterize_l1_backward(tgt, g, off, ids, pts, conic, opac, colors, W, H,
+                                          ref[0], schedule=s) for s in (None, sched)]
+    for x, y in zip(*grads):
+        assert helpers.rel_l2(y, x) <= 1e-5
+
+
 @pytest.mark.parametrize("lam", [0.2, 1.0])
 def test_render_l1_with_ssim_matches_drop_in_path(gpu, lam):
     """render_l1(ssim_lambda=lam) against the reference's loss written with PyTorch
