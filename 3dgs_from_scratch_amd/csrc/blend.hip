@@ -1044,6 +1044,9 @@ extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gauss
                           nullptr, nullptr, nullptr, stream);
 }
 
+static int launch_l1_finish(int32_t n_tiles, const float *tile_loss, float inv_count, float *loss,
+                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream);
+
 extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
                                     const int32_t *gaussian_ids_sorted, int32_t n_tiles,
                                     int64_t k, const float *points_image,
@@ -1051,16 +1054,18 @@ extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
                                     const float *colors, int64_t n, int32_t width,
                                     int32_t height, int32_t tile_size, float alpha_threshold,
                                     float transmittance_threshold, float chi_squared_threshold,
-                                    float *image, float *display, hipStream_t stream) {
+                                    float *image, float *display, int32_t *tile_schedule,
+                                    hipStream_t stream) {
     if (!display) return GS_ERR_INVALID_ARGUMENT;
-    return rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
-                          cov_inv_image, opacities, colors, n, width, height, tile_size,
-                          alpha_threshold, transmittance_threshold, chi_squared_threshold, image,
-                          display, nullptr, nullptr, stream);
+    uint32_t *cost = tile_schedule ? reinterpret_cast<uint32_t *>(tile_schedule) : nullptr;
+    const int st = rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
+                                  cov_inv_image, opacities, colors, n, width, height, tile_size,
+                                  alpha_threshold, transmittance_threshold, chi_squared_threshold,
+                                  image, display, nullptr, nullptr, stream, nullptr, 0, cost);
+    if (st || !tile_schedule || n_tiles == 0) return st;
+    return launch_l1_finish(n_tiles, nullptr, 0.0f, nullptr, cost, tile_schedule + n_tiles,
+                            stream);
 }
-
-static int launch_l1_finish(int32_t n_tiles, const float *tile_loss, float inv_count, float *loss,
-                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream);
 
 extern "C" int gs_rasterize_display_l1(
     const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k,
@@ -1347,13 +1352,14 @@ extern "C" int gs_rasterize_display_backward(
     int32_t width, int32_t height, int32_t tile_size, float alpha_threshold,
     float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
     float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
-    hipStream_t stream) {
+    const int32_t *tile_schedule, hipStream_t stream) {
     return rasterize_backward_impl(grad_display, image, indexing_offset, gaussian_ids_sorted,
                                    n_tiles, k, points_image, cov_inv_image, opacities, colors, n,
                                    width, height, tile_size, alpha_threshold,
                                    transmittance_threshold, chi_squared_threshold,
                                    grad_points_image, grad_cov_inv_image, grad_opacities,
-                                   grad_colors, accumulate, kSeedDisplay, nullptr, 0.0f, stream);
+                                   grad_colors, accumulate, kSeedDisplay, nullptr, 0.0f, stream,
+                                   nullptr, tile_schedule ? tile_schedule + n_tiles : nullptr);
 }
 
 extern "C" int gs_rasterize_l1_backward(

@@ -560,12 +560,16 @@ def evaluate_spherical_harmonics_render_backward(grad_colors, world_to_camera, p
 
 def rasterize_display(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
                       opacities, colors, width, height, tile_size, alpha_threshold,
-                      transmittance_threshold, chi_squared_threshold):
+                      transmittance_threshold, chi_squared_threshold, schedule=None):
     """rasterize() that also returns clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294).
-    Returns (image[H,W,3] un-clamped, display[H,W,3])."""
+    Returns (image[H,W,3] un-clamped, display[H,W,3]).  `schedule` (see
+    tile_schedule) receives the work per tile and the order in which
+    rasterize_display_backward, given it, launches the tiles."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
+    if schedule is not None:
+        _check_schedule(schedule, off.shape[0], dev, "rasterize_display")
     image = torch.empty((height, width, 3), dtype=torch.float32, device=dev)
     display = torch.empty((height, width, 3), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
@@ -575,7 +579,7 @@ def rasterize_display(indexing_offset, gaussian_ids_sorted, points_image, cov_in
                 _ptr(off), _ptr(ids), off.shape[0], ids.shape[0], _ptr(pts), _ptr(conic),
                 _ptr(opac), _ptr(col), n, width, height, int(tile_size), float(alpha_threshold),
                 float(transmittance_threshold), float(chi_squared_threshold), _ptr(image),
-                _ptr(display), _stream(dev),
+                _ptr(display), _ptr(schedule), _stream(dev),
             ),
             "rasterize_display",
         )
@@ -586,12 +590,15 @@ def rasterize_display(indexing_offset, gaussian_ids_sorted, points_image, cov_in
 def rasterize_display_backward(grad_display, indexing_offset, gaussian_ids_sorted, points_image,
                                cov_inv_image, opacities, colors, width, height, tile_size,
                                alpha_threshold, transmittance_threshold, chi_squared_threshold,
-                               rendered_image):
+                               rendered_image, schedule=None):
     """Gradient of rasterize_display's display output; `rendered_image` (its
-    un-clamped image) is required.  Returns the four gradients of rasterize_backward."""
+    un-clamped image) is required.  Returns the four gradients of rasterize_backward.
+    `schedule`: the tensor rasterize_display filled for the same layout."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
+    if schedule is not None:
+        _check_schedule(schedule, off.shape[0], dev, "rasterize_display_backward")
     f32 = torch.float32
     grad = _prep(grad_display, "grad_display", f32, (height, width, 3), dev)
     img = _prep(rendered_image, "rendered_image", f32, (height, width, 3), dev)
@@ -604,7 +611,7 @@ def rasterize_display_backward(grad_display, indexing_offset, gaussian_ids_sorte
                 _ptr(pts), _ptr(conic), _ptr(opac), _ptr(col), n, width, height, int(tile_size),
                 float(alpha_threshold), float(transmittance_threshold),
                 float(chi_squared_threshold), _ptr(g_pts), _ptr(g_conic), _ptr(g_opac),
-                _ptr(g_col), 1, _stream(dev),
+                _ptr(g_col), 1, _ptr(schedule), _stream(dev),
             ),
             "rasterize_display_backward",
         )

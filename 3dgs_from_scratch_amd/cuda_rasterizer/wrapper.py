@@ -108,22 +108,25 @@ class RenderRasterizeFunction(torch.autograd.Function):
     def forward(ctx, indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities,
                 colors, width, height, tile_size, alpha_threshold, transmittance_threshold,
                 chi_squared_threshold):
+        # the forward's work per tile orders the backward's tiles (heaviest first)
+        schedule = _cr.tile_schedule(indexing_offset.shape[0], points_img.device)
         image, display = _cr.rasterize_display(
             indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities, colors,
             width, height, tile_size, alpha_threshold, transmittance_threshold,
-            chi_squared_threshold)
+            chi_squared_threshold, schedule=schedule)
         ctx.save_for_backward(indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img,
-                              opacities, colors, image)
+                              opacities, colors, image, schedule)
         ctx.params = (width, height, tile_size, alpha_threshold, transmittance_threshold,
                       chi_squared_threshold)
         return display
 
     @staticmethod
     def backward(ctx, grad_display):
-        offsets, ids, points_img, cov_inv_img, opacities, colors, image = ctx.saved_tensors
+        offsets, ids, points_img, cov_inv_img, opacities, colors, image, schedule = (
+            ctx.saved_tensors)
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_display_backward(
             grad_display, offsets, ids, points_img, cov_inv_img, opacities, colors, *ctx.params,
-            rendered_image=image)
+            rendered_image=image, schedule=schedule)
         return None, None, g_pts, g_conic, g_opac, g_col, None, None, None, None, None, None
 
 

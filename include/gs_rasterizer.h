@@ -206,9 +206,13 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
  *   the means gradient to grad_means instead of overwriting it.
  * gs_rasterize_display: gs_rasterize that also writes
  *   display = clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294); tile_size 16.
+ *   tile_schedule: null, or 2 * n_tiles int32 that receive the work per tile
+ *   and the backward's launch order (as in gs_rasterize_display_l1).
  * gs_rasterize_display_backward: gs_rasterize_backward given the gradient of
  *   display (image required): the image gradient is grad_display * 255 where
- *   0 <= image <= 1, else 0.
+ *   0 <= image <= 1, else 0.  tile_schedule: null, or the buffer that
+ *   gs_rasterize_display filled for the same tile layout (the tiles then start
+ *   heaviest first; the results do not depend on it).
  */
 int gs_evaluate_sh_render(const float *world_to_camera, const float *means, const float *sh_dc,
                           const float *sh_rest, const uint8_t *mask, int64_t n, float *colors,
@@ -224,7 +228,7 @@ int gs_rasterize_display(const int32_t *indexing_offset, const int32_t *gaussian
                          int64_t n, int32_t width, int32_t height, int32_t tile_size,
                          float alpha_threshold, float transmittance_threshold,
                          float chi_squared_threshold, float *image, float *display,
-                         hipStream_t stream);
+                         int32_t *tile_schedule, hipStream_t stream);
 int gs_rasterize_display_backward(const float *grad_display, const float *image,
                                   const int32_t *indexing_offset,
                                   const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k,
@@ -234,7 +238,8 @@ int gs_rasterize_display_backward(const float *grad_display, const float *image,
                                   float alpha_threshold, float transmittance_threshold,
                                   float chi_squared_threshold, float *grad_points_image,
                                   float *grad_cov_inv_image, float *grad_opacities,
-                                  float *grad_colors, int32_t accumulate, hipStream_t stream);
+                                  float *grad_colors, int32_t accumulate,
+                                  const int32_t *tile_schedule, hipStream_t stream);
 
 /* ----------------------------------------------- fused training step */
 

@@ -241,7 +241,21 @@ def test_tile_schedule(gpu, size):
         g = torch.full((1,), 0.7, device=gpu)
         grads = [cr.rasterize_l1_backward(tgt, g, off, ids, pts, conic, opac, colors, W, H,
                                           ref[0], schedule=s) for s in (None, sched)]
+        # the drop-in render path's display entries: same work counts and order
+        thr = (16, 1e-4, 1e-4, 9.21)
+        sched_d = cr.tile_schedule(n_tiles, gpu)
+        img_d, disp_d = cr.rasterize_display(off, ids, pts, conic, opac, colors, W, H, *thr,
+                                             schedule=sched_d)
+        img_r, disp_r = cr.rasterize_display(off, ids, pts, conic, opac, colors, W, H, *thr)
+        assert torch.equal(img_d, img_r) and torch.equal(disp_d, disp_r)
+        assert torch.equal(sched_d[:2 * n_tiles], sched[:2 * n_tiles])
+        up = torch.randn((H, W, 3), generator=torch.Generator().manual_seed(5)).to(gpu)
+        grads_d = [cr.rasterize_display_backward(up, off, ids, pts, conic, opac, colors, W, H,
+                                                 *thr, rendered_image=img_r, schedule=s)
+                   for s in (None, sched_d)]
     for x, y in zip(*grads):
+        assert helpers.rel_l2(y, x) <= 1e-5
+    for x, y in zip(*grads_d):
         assert helpers.rel_l2(y, x) <= 1e-5
 
 
