@@ -12,10 +12,14 @@
 // places workgroup b on XCD b % 8) so that neighbouring tiles, which share
 // Gaussians, run on the same XCD and share its L2.
 //
-// Decision quantities (E, alpha, T) are computed with separately rounded ops in
-// the Torch rasterizer's order (src/torch_rasterizer.py:255-278) -- this file
-// is compiled with -ffp-contract=off -- so inclusion decisions match the CPU
-// oracle for identical inputs; accumulations use explicit fmaf.
+// In the forward, decision quantities (E, alpha, T) are computed with separately
+// rounded ops in the Torch rasterizer's order (src/torch_rasterizer.py:255-278)
+// -- this file is compiled with -ffp-contract=off -- so inclusion decisions,
+// and with them the image, match the CPU oracle for identical inputs;
+// accumulations use explicit fmaf.  The backward evaluates E with two fmas and
+// the alpha test as a cut-off on E, fewer instructions per (entry, strip); its
+// decisions can differ from the forward's only for an E within rounding of a
+// threshold, where the entry's weight is about alpha_thr * T.
 //
 // The backward walks the list in the same front-to-back order.  With
 // S_i = sum_{k>i} w_k (g.c_k) = g.C - sum_{k<=i} w_k (g.c_k), where C is the
@@ -70,8 +74,9 @@ __device__ __forceinline__ int tile_of_block(int b, int n_tiles) {
 
 // Exponent cut-off of a Gaussian with log2 opacity log2o: E < chi and
 // o exp(-E/2) >= alpha_thr, i.e. E <= 2 ln(o / alpha_thr) = 2 ln2 (log2 o -
-// log2 alpha_thr).  Used only for culling, whose tests carry margins well
-// above the error of the hardware log.
+// log2 alpha_thr).  Culling tests it with margins well above the error of the
+// hardware log; the backward's inclusion test uses it as is (an entry within
+// that error of the alpha threshold weighs about alpha_thr * T).
 __device__ __forceinline__ float effective_chi(float log2o, float chi, float alpha_thr,
                                                float log2_alpha_thr) {
     float chi_eff = chi;
@@ -105,7 +110,7 @@ __device__ __forceinline__ float conic_exponent(float A, float B2, float C, floa
 constexpr float kNegHalfLog2e = -0.72134752044448170f;
 struct BatchLds {
     float4 geo[kBatch];  // u, v, A, 2B
-    float4 aux[kBatch];  // C, 1 / opacity, strip mask, log2(opacity)
+    float4 aux[kBatch];  // C, E cut-off (chi_eff), strip mask, log2(opacity)
     float4 col[kBatch];  // r, g, b, (gaussian id bits)
 };
 
@@ -218,14 +223,15 @@ struct Staged {
 
 // Stages the lane's record into the next free LDS slot if its ellipse (with
 // the chi-square and alpha cut-offs) reaches the tile, keeping lane (= list)
-// order, with its strip mask in aux.z and log2 of its opacity in aux.w.
+// order, with its E cut-off (effective_chi) in aux.y, its strip mask in aux.z
+// and log2 of its opacity in aux.w.
 __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, float chi,
                                                 float alpha_thr, float log2_alpha_thr, float x0,
                                                 float y0) {
     uint32_t m = 0u;
     const float log2o = log2_opacity(r.o);
+    const float chi_eff = effective_chi(log2o, chi, alpha_thr, log2_alpha_thr);
     if (r.id >= 0) {
-        const float chi_eff = effective_chi(log2o, chi, alpha_thr, log2_alpha_thr);
         float ex, ey;
         ellipse_extent(r.A, r.B, r.C, chi_eff, ex, ey);
         m = exact_strip_mask(strip_mask(r.u, r.v, ex, ey, x0, y0), r.u, r.v, r.A, r.B, r.C,
@@ -236,7 +242,7 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
     if (m != 0u) {
         const int slot = __popcll(keep & lanemask_lt());
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
-        s.aux[slot] = make_float4(r.C, __builtin_amdgcn_rcpf(r.o), __uint_as_float(m), log2o);
+        s.aux[slot] = make_float4(r.C, chi_eff, __uint_as_float(m), log2o);
         s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
     }
     Staged st;
@@ -627,6 +633,10 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
     const float du = pix.fx - geo.x;
     const float Adudu = (geo.z * du) * du;
     const float B2du = geo.w * du;
+    // the alpha test as a cut-off on E, staged in aux.y: alpha = o exp(-E/2) >=
+    // alpha_thr iff E <= 2 ln(o / alpha_thr) (up to the rounding of the hardware
+    // exp2/log2)
+    const float chi_a = aux.y;
     // -0 is the identity of float addition, so the first strip's sums need no add
     float sH = -0.0f, s1 = -0.0f, s2 = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f;
     bool hit = false;  // some strip was evaluated (otherwise every field is -0)
@@ -634,12 +644,11 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
     for (int q = 0; q < kStrips; ++q) {
         if (!((smask >> q) & 1u)) continue;  // uniform
         const float dv = pix.fy[q] - geo.y;
-        const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
-        const bool ok = !(L.T[q] < T_thr) && (E < chi);
-        if (!wave_any(ok)) continue;
+        const float E = fmaf(fmaf(aux.x, dv, B2du), dv, Adudu);
+        const bool inc = !(L.T[q] < T_thr) && (E < chi_a);
+        if (!wave_any(inc)) continue;
         hit = true;
         const float alpha = alpha_of(E, aux.w);
-        const bool inc = ok && !(alpha < alpha_thr);
         const float a = kSafe ? alpha : (inc ? alpha : 0.0f);
         const float w = a * L.T[q];
         const float gcol = fmaf(L.gr[q], col.x, fmaf(L.gg[q], col.y, L.gb[q] * col.z));
@@ -677,7 +686,8 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
         // 32 x 32 -> 64 multiply-add per field address
         const uint32_t g = __builtin_amdgcn_readfirstlane(__float_as_uint(col.w));
         if (tgt.active) {
-            const float scale = tgt.inv_o ? aux.y : tgt.fa;
+            // 1 / o = 2^-log2(o) (the opacity field's lane)
+            const float scale = tgt.inv_o ? __builtin_amdgcn_exp2f(-aux.w) : tgt.fa;
             const uint64_t off = (uint64_t)g * (uint64_t)tgt.stride4;
             unsafeAtomicAdd(reinterpret_cast<float *>(reinterpret_cast<char *>(tgt.base) + off),
                             total * scale);
