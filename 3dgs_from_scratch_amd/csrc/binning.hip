@@ -904,8 +904,12 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
 
 // Writes each entry's Gaussian id at its final position: lane j of every wave
 // holds the first position of the wave's entries of local tile j, read back
-// with readlane in the loop over tiles.  k32: positions fit 32 bits (K < 2^30),
-// so a store is a 32-bit offset from the uniform base.
+// with readlane in the loop over tiles.  The lanes covering local tile
+// (lx, ly) are those covering row ly and column lx (the rectangles' row and
+// column ballots, uniform masks built once), so a tile's lane mask, its count
+// and the bounds check of its run are scalar work; each covering lane stores at
+// the run's start plus its rank in the mask.  k32: positions fit 32 bits
+// (K < 2^30), so a store is a 32-bit offset from the uniform base.
 template <bool k32>
 __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
                                                                 const uint32_t *__restrict__ table,
@@ -928,24 +932,28 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
     }
     __syncthreads();
     const uint32_t my_base = base[wave][lane];  // lane j: tile j
-    const uint32_t mlo = (uint32_t)x.mask, mhi = (uint32_t)(x.mask >> 32);
-    const uint32_t k = (uint32_t)(a.k < 0xffffffffLL ? a.k : 0xffffffffLL);
+    uint64_t rows[kSuper], cols[kSuper];
+#pragma unroll
+    for (int q = 0; q < kSuper; ++q) {
+        rows[q] = __ballot(x.ly0 <= q && q <= x.ly1);
+        cols[q] = __ballot(x.lx0 <= q && q <= x.lx1);
+    }
+    // k32: K < 2^30, so b + count cannot wrap in 32 bits (a scalar compare)
+    const uint32_t k_lo = (uint32_t)(a.k < 0xffffffffLL ? a.k : 0xffffffffLL);
 #pragma unroll
     for (int j = 0; j < kSuperLocal; ++j) {
-        const bool mine = ((j < 32 ? mlo >> j : mhi >> (j - 32)) & 1u) != 0u;
-        const uint64_t bal = __ballot(mine);
+        const uint64_t bal = rows[j / kSuper] & cols[j % kSuper];
+        if (bal == 0) continue;  // uniform: no lane covers tile j
         const uint32_t b = __builtin_amdgcn_readlane(my_base, j);
-        if (mine) {  // + the lanes below this one that also cover tile j
-            const uint32_t p = b + __builtin_amdgcn_mbcnt_hi(
-                                       (uint32_t)(bal >> 32),
-                                       __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-            if (k32) {  // byte offset p * 4 < 2^32: a 32-bit offset from the uniform base
-                if (p < k)
-                    *reinterpret_cast<int32_t *>(reinterpret_cast<char *>(ids_out) + (p << 2)) =
-                        x.g;
-            } else {
-                if ((int64_t)p < a.k) ids_out[(int64_t)p] = x.g;
-            }
+        const uint32_t cnt = (uint32_t)__popcll(bal);
+        if (k32 ? (b + cnt > k_lo) : ((int64_t)b + cnt > a.k)) continue;  // run inside ids_out
+        if (__builtin_amdgcn_inverse_ballot_w64(bal)) {
+            const uint32_t p = __builtin_amdgcn_mbcnt_hi(
+                (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, b));
+            if (k32)  // byte offset p * 4 < 2^32: a 32-bit offset from the uniform base
+                *reinterpret_cast<int32_t *>(reinterpret_cast<char *>(ids_out) + (p << 2)) = x.g;
+            else
+                ids_out[(int64_t)p] = x.g;
         }
     }
 }
