@@ -1002,9 +1002,16 @@ constexpr int kL1Waves = kL1Threads / kWave;
 struct L1Args {
     const uint32_t *order;       // Gaussians in depth order
     const uint2 *rects_depth;    // their packed tile rectangles, in the same order
+    const int64_t *n_live;       // device: the first *n_live positions hold Gaussians with tiles
     int64_t n, m;                // Gaussians, entries
     int super_x, nblocks;
 };
+
+// Whether this workgroup's positions start before *n_live (the later ones hold
+// only the sentinels of Gaussians without tiles); uniform per workgroup.
+__device__ __forceinline__ bool l1_live_block(const L1Args &a) {
+    return (int64_t)blockIdx.x * kL1Threads < *a.n_live;
+}
 
 // This thread's Gaussian and the supertile range its tile rectangle meets
 // (false: none).
@@ -1044,6 +1051,10 @@ __device__ __forceinline__ bool l1_lane_masks(const L1Args &a, uint64_t (*lanes)
 __global__ __launch_bounds__(kL1Threads) void l1_count_kernel(L1Args a,
                                                               uint32_t *__restrict__ hist) {
     __shared__ uint64_t lanes[kL1Waves][kRadixMax];
+    if (!l1_live_block(a)) {  // no entries: a zero histogram column
+        if (threadIdx.x < kRadixMax) hist[hist_index(threadIdx.x, blockIdx.x, a.nblocks)] = 0u;
+        return;
+    }
     uint32_t g;
     uint2 packed;
     TileRect sr;
@@ -1108,6 +1119,7 @@ __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
     for (int64_t t = (int64_t)blockIdx.x * kL1Threads + threadIdx.x; t < n_tiles;
          t += (int64_t)gridDim.x * kL1Threads)
         tile_counts[t] = 0u;
+    if (blockIdx.x != 0 && !l1_live_block(a)) return;  // no entries (block 0 writes the plan)
     uint32_t g = 0;
     uint2 packed = make_uint2(0u, 0u);
     TileRect sr{0, -1, 0, -1};
@@ -1223,6 +1235,7 @@ inline L1Args l1_args(const CountWs &cw, int64_t n, int64_t m, int super_x) {
     L1Args la;
     la.order = cw.dvals_a;
     la.rects_depth = cw.rects_depth;
+    la.n_live = cw.n_live;
     la.n = n;
     la.m = m;
     la.super_x = super_x;
