@@ -1093,7 +1093,7 @@ extern "C" int gs_rasterize_display_l1(
                             cov_inv_image, opacities, colors, n, width, height, tile_size,
                             alpha_threshold, transmittance_threshold, chi_squared_threshold,
                             image, display, target, tile_loss, stream, clear, clear_count, cost);
-    if (st || n_tiles == 0) return st;
+    if (st) return st;
     // the loss (when asked for) and the backward's tile order, in one launch
     const double count = (double)width * (double)height * 3.0;
     return launch_l1_finish(n_tiles, tile_loss, (float)(1.0 / count), loss, cost,
