@@ -108,14 +108,16 @@ class RenderRasterizeFunction(torch.autograd.Function):
     def forward(ctx, indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities,
                 colors, width, height, tile_size, alpha_threshold, transmittance_threshold,
                 chi_squared_threshold):
-        # the forward's work per tile orders the backward's tiles (heaviest first)
-        schedule = _cr.tile_schedule(indexing_offset.shape[0], points_img.device)
+        # the forward's work per tile orders the backward's tiles (heaviest first);
+        # not computed when no backward can follow
+        grad = torch.is_grad_enabled() and any(ctx.needs_input_grad[2:6])
+        schedule = _cr.tile_schedule(indexing_offset.shape[0], points_img.device) if grad else None
         image, display = _cr.rasterize_display(
             indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities, colors,
             width, height, tile_size, alpha_threshold, transmittance_threshold,
             chi_squared_threshold, schedule=schedule)
         ctx.save_for_backward(indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img,
-                              opacities, colors, image, schedule)
+                              opacities, colors, image, schedule)  # schedule may be None
         ctx.params = (width, height, tile_size, alpha_threshold, transmittance_threshold,
                       chi_squared_threshold)
         return display
