@@ -107,10 +107,11 @@ class RenderRasterizeFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities,
                 colors, width, height, tile_size, alpha_threshold, transmittance_threshold,
-                chi_squared_threshold):
+                chi_squared_threshold, grad_mode=True):
         # the forward's work per tile orders the backward's tiles (heaviest first);
-        # not computed when no backward can follow
-        grad = torch.is_grad_enabled() and any(ctx.needs_input_grad[2:6])
+        # not computed when no backward can follow (grad_mode: the caller's
+        # torch.is_grad_enabled(), which is always False inside forward)
+        grad = grad_mode and any(ctx.needs_input_grad[2:6])
         schedule = _cr.tile_schedule(indexing_offset.shape[0], points_img.device) if grad else None
         image, display = _cr.rasterize_display(
             indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities, colors,
@@ -129,7 +130,7 @@ class RenderRasterizeFunction(torch.autograd.Function):
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_display_backward(
             grad_display, offsets, ids, points_img, cov_inv_img, opacities, colors, *ctx.params,
             rendered_image=image, schedule=schedule)
-        return None, None, g_pts, g_conic, g_opac, g_col, None, None, None, None, None, None
+        return None, None, g_pts, g_conic, g_opac, g_col, None, None, None, None, None, None, None
 
 
 class RasterizeFunction(torch.autograd.Function):
@@ -198,5 +199,5 @@ def render(
     display = RenderRasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img,
                                             cov_inv_img, opacities, colors, width, height,
                                             tile_size, alpha_threshold, transmittance_threshold,
-                                            chi_squared_threshold)
+                                            chi_squared_threshold, torch.is_grad_enabled())
     return display, points_img, radii

@@ -140,3 +140,38 @@ def test_display_blend_equals_clamp_of_image(gpu):
                                  rendered_image=image)
     for a, b in zip(got, want):
         assert helpers.rel_l2(a, b) <= 1e-6
+
+
+def test_render_passes_tile_schedule_only_with_grad(gpu, monkeypatch):
+    """render() gives the blend forward a tile schedule when a backward can follow
+    and hands the same buffer to the blend backward (heaviest tiles first); under
+    torch.no_grad() no schedule is computed."""
+    import cuda_rasterizer as cr
+
+    seen = {}
+    fwd, bwd = cr.rasterize_display, cr.rasterize_display_backward
+
+    def spy_fwd(*args, schedule=None, **kw):
+        seen["fwd"] = schedule
+        return fwd(*args, schedule=schedule, **kw)
+
+    def spy_bwd(*args, schedule=None, **kw):
+        seen["bwd"] = schedule
+        return bwd(*args, schedule=schedule, **kw)
+
+    monkeypatch.setattr(cr, "rasterize_display", spy_fwd)
+    monkeypatch.setattr(cr, "rasterize_display_backward", spy_bwd)
+    p, cam, _ = helpers.scene_box(3000, 96, 80, 110.0, seed=31)
+    leaves = {k: v.to(gpu).clone().requires_grad_(True) for k, v in p.items()}
+
+    def run():
+        scales, quats, opac = helpers.activated(leaves)
+        return render(cam["w2c"].to(gpu), cam["K"].to(gpu), cam["width"], cam["height"],
+                      leaves["means"], scales, quats, opac, leaves["sh_dc"], leaves["sh_rest"])[0]
+
+    run().sum().backward()
+    assert seen["fwd"] is not None and seen["bwd"] is seen["fwd"]
+    seen.clear()
+    with torch.no_grad():
+        run()
+    assert seen["fwd"] is None and "bwd" not in seen
