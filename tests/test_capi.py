@@ -126,6 +126,17 @@ def test_invalid_arguments_rejected_on_host(lib):
                                null, 0.0, null, fake, 0, null) == -2  # workspace too small
     assert lib.gs_ssim_backward(fake, fake, st, fake, st, 1, 3, 64, 64, 1.0, fake, fake, null,
                                 1.0, fake, st, null) == -1
+    # fused blend entries: missing display / target / tile sums, grids not covering the image,
+    # a NaN loss weight
+    blend_args = (null, null, 16, 10, *([null] * 4), 10, 64, 64, 16, 1e-4, 1e-4, 9.21)
+    assert lib.gs_rasterize_display_l1(*blend_args, fake, fake, null, fake, null, null, null, 0,
+                                       null) == -1  # no display
+    assert lib.gs_rasterize_display_l1(null, null, 15, 10, *([null] * 4), 10, 64, 64, 16, 1e-4,
+                                       1e-4, 9.21, fake, fake, fake, fake, null, null, null, 0,
+                                       null) == -1  # 15 offsets for a 16-tile image
+    assert lib.gs_l1_finish(fake, 16, 0, fake, null) == -1
+    assert lib.gs_rasterize_l1_backward(fake, fake, fake, *blend_args, *([fake] * 4), 1,
+                                        float("nan"), null, null, null) == -1
 
 
 def test_python_layer_refuses_cpu_tensors():
@@ -139,6 +150,16 @@ def test_python_layer_refuses_cpu_tensors():
         cuda_rasterizer.compute_tile_intersection(torch.zeros(n, 2), torch.ones(n, 2),
                                                   torch.ones(n), torch.ones(n, dtype=torch.bool),
                                                   16, 16, 16)
+
+
+def test_tile_schedule_buffers_are_checked():
+    """The schedule buffer must be a contiguous int32 tensor of at least 2 * n_tiles."""
+    cpu = torch.device("cpu")
+    cuda_rasterizer._check_schedule(torch.zeros(16, dtype=torch.int32), 8, cpu, "probe")
+    for bad in (torch.zeros(15, dtype=torch.int32), torch.zeros(16, dtype=torch.int64),
+                torch.zeros(32, dtype=torch.int32)[::2], [0] * 16):
+        with pytest.raises(RuntimeError, match="schedule"):
+            cuda_rasterizer._check_schedule(bad, 8, cpu, "probe")
 
 
 def test_status_to_exception():
