@@ -782,7 +782,7 @@ def main(argv=None):
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU design is described in DESIGN.md but not built)", file=sys.stderr)
+              "(the multi-GPU design is documented but not built)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
