@@ -12,14 +12,18 @@
 // places workgroup b on XCD b % 8) so that neighbouring tiles, which share
 // Gaussians, run on the same XCD and share its L2.
 //
-// In the forward, decision quantities (E, alpha, T) are computed with separately
-// rounded ops in the Torch rasterizer's order (src/torch_rasterizer.py:255-278)
-// -- this file is compiled with -ffp-contract=off -- so inclusion decisions,
-// and with them the image, match the CPU oracle for identical inputs;
-// accumulations use explicit fmaf.  The backward evaluates E with two fmas and
-// the alpha test as a cut-off on E, fewer instructions per (entry, strip); its
-// decisions can differ from the forward's only for an E within rounding of a
-// threshold, where the entry's weight is about alpha_thr * T.
+// In the forward, the exponent E and the transmittance T are computed with
+// separately rounded ops in the Torch rasterizer's order
+// (src/torch_rasterizer.py:255-278) -- this file is compiled with
+// -ffp-contract=off -- so the chi-square test (where an entry weighs about
+// 0.01 o T) matches the CPU oracle exactly for identical inputs; accumulations
+// use explicit fmaf.  alpha = o exp(-E/2) is evaluated as exp2 of an fma with
+// the hardware exp2/log2, and the alpha test as the cut-off E < 2 ln(o /
+// alpha_thr) on E; both can differ from the oracle's float results in the last
+// bits, so an entry within rounding of the alpha threshold (weighing about
+// alpha_thr T) may be included differently.  The backward evaluates E with two
+// fmas, fewer instructions per (entry, strip); its decisions can differ from
+// the forward's only for an E within rounding of a threshold.
 //
 // The backward walks the list in the same front-to-back order.  With
 // S_i = sum_{k>i} w_k (g.c_k) = g.C - sum_{k<=i} w_k (g.c_k), where C is the
@@ -75,7 +79,7 @@ __device__ __forceinline__ int tile_of_block(int b, int n_tiles) {
 // Exponent cut-off of a Gaussian with log2 opacity log2o: E < chi and
 // o exp(-E/2) >= alpha_thr, i.e. E <= 2 ln(o / alpha_thr) = 2 ln2 (log2 o -
 // log2 alpha_thr).  Culling tests it with margins well above the error of the
-// hardware log; the backward's inclusion test uses it as is (an entry within
+// hardware log; both blend walks' inclusion tests use it as is (an entry within
 // that error of the alpha threshold weighs about alpha_thr * T).
 __device__ __forceinline__ float effective_chi(float log2o, float chi, float alpha_thr,
                                                float log2_alpha_thr) {
@@ -378,11 +382,11 @@ __device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const Lane
         if (!((smask >> q) & 1u)) continue;  // uniform
         const float dv = pix.fy[q] - geo.y;
         const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
-        const bool ok = !(T[q] < T_thr) && (E < chi);
-        if (!wave_any(ok)) continue;
+        // the chi-square and alpha tests as one cut-off on E (staged in aux.y)
+        const bool inc = !(T[q] < T_thr) && (E < aux.y);
+        if (!wave_any(inc)) continue;
         work += kCostStrip;
         const float alpha = alpha_of(E, aux.w);
-        const bool inc = ok && !(alpha < alpha_thr);
         if (kSafe) {
             const float w = alpha * T[q];
             cr[q] = inc ? fmaf(w, col.x, cr[q]) : cr[q];
