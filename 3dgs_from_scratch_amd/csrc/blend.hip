@@ -116,6 +116,7 @@ struct BatchLds {
     float4 geo[kBatch];  // u, v, A, 2B
     float4 aux[kBatch];  // C, E cut-off (chi_eff), strip mask, log2(opacity)
     float4 col[kBatch];  // r, g, b, (gaussian id bits)
+    float inv_o[kBatch];  // 1 / opacity (staged by the backward for its opacity gradient)
 };
 
 // log2(o) for the exponent form of alpha; -inf when o <= 0 (alpha 0: skipped,
@@ -229,6 +230,7 @@ struct Staged {
 // the chi-square and alpha cut-offs) reaches the tile, keeping lane (= list)
 // order, with its E cut-off (effective_chi) in aux.y, its strip mask in aux.z
 // and log2 of its opacity in aux.w.
+template <bool kInvO>
 __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, float chi,
                                                 float alpha_thr, float log2_alpha_thr, float x0,
                                                 float y0) {
@@ -248,6 +250,7 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
         s.aux[slot] = make_float4(r.C, chi_eff, __uint_as_float(m), log2o);
         s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
+        if (kInvO) s.inv_o[slot] = __builtin_amdgcn_rcpf(r.o);
     }
     Staged st;
     st.count = __popcll(keep);
@@ -260,7 +263,8 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
 // b is processed; without, only the ids of batch b+1 (fewer registers).  Both
 // blend kernels use kRecords: in the backward it costs a wave per SIMD of
 // occupancy (93 VGPRs) and is still 2% faster.
-template <bool kRecords>
+// kInvO: also stage 1 / opacity (the backward).
+template <bool kRecords, bool kInvO>
 struct BatchPipe {
     int32_t next_id;  // this lane's id in the batch after the next one to stage
     Record rec;       // this lane's record of the next batch to stage (kRecords)
@@ -293,7 +297,8 @@ struct BatchPipe {
         if (!kRecords) rec = fetch_record(next_id, n, points, conics, opac, colors);
         __syncthreads();  // previous batch fully read before restaging
         const Staged st =
-            stage_records(s, rec, chi, alpha_thr, __builtin_amdgcn_logf(alpha_thr), x0, y0);
+            stage_records<kInvO>(s, rec, chi, alpha_thr, __builtin_amdgcn_logf(alpha_thr), x0,
+                                 y0);
         __syncthreads();
         if (kRecords) {
             rec = fetch_record(next_id, n, points, conics, opac, colors);
@@ -440,7 +445,7 @@ __device__ __forceinline__ void blend_accumulate(
         cr[q] = cg[q] = cb[q] = 0.0f;
     }
     if (span.end <= span.start) return;
-    BatchPipe<true> pipe;
+    BatchPipe<true, false> pipe;
     pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
         if (!any_active(T, T_thr)) break;
@@ -692,8 +697,7 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
         // 32 x 32 -> 64 multiply-add per field address
         const uint32_t g = __builtin_amdgcn_readfirstlane(__float_as_uint(col.w));
         if (tgt.active) {
-            // 1 / o = 2^-log2(o) (the opacity field's lane)
-            const float scale = tgt.inv_o ? __builtin_amdgcn_exp2f(-aux.w) : tgt.fa;
+            const float scale = tgt.inv_o ? s.inv_o[j] : tgt.fa;
             const uint64_t off = (uint64_t)g * (uint64_t)tgt.stride4;
             unsafeAtomicAdd(reinterpret_cast<float *>(reinterpret_cast<char *>(tgt.base) + off),
                             total * scale);
@@ -805,7 +809,7 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     const bool f8_lane = lane == 4;
     const GradTarget tgt = grad_target(lane, g_points, g_conics, g_opac, g_colors);
 
-    BatchPipe<true> pipe;
+    BatchPipe<true, true> pipe;
     pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
         if (!any_active(L.T, T_thr)) break;
