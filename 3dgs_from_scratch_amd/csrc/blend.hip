@@ -83,9 +83,11 @@ __device__ __forceinline__ int tile_of_block(int b, int n_tiles) {
 // that error of the alpha threshold weighs about alpha_thr * T).
 __device__ __forceinline__ float effective_chi(float log2o, float chi, float alpha_thr,
                                                float log2_alpha_thr) {
+    // o <= 0 (log2 o = -inf) gives -inf: alpha = 0 fails any alpha_thr > 0; a NaN
+    // opacity gives NaN, which fminf drops (alpha NaN passes the test, as in the
+    // reference)
     float chi_eff = chi;
-    if (alpha_thr > 0.0f && log2o > -__builtin_inff())
-        chi_eff = fminf(chi_eff, 1.3862943611198906f * (log2o - log2_alpha_thr));
+    if (alpha_thr > 0.0f) chi_eff = fminf(chi_eff, 1.3862943611198906f * (log2o - log2_alpha_thr));
     return chi_eff;
 }
 
@@ -630,6 +632,56 @@ struct BackwardLane {
     float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips];
 };
 
+// An entry of opacity 0 (log2 o = -inf; included only when alpha_thr <= 0):
+// alpha = 0, so it changes no pixel, no transmittance and no other gradient,
+// and d loss / d o = sum over its pixels of G dalpha with G = exp(-E/2), which
+// the h / o form of the other entries cannot give (0 * inf).  dalpha =
+// T (g.c) - (g.C - acc) / (1 + eps).
+template <bool kSafe>
+__device__ __forceinline__ void backward_zero_opacity_entry(const BatchLds &s, int j,
+                                                            const LanePixels &pix, float T_thr,
+                                                            const BackwardLane &L,
+                                                            const GradTarget &tgt, bool hi8,
+                                                            bool f8_lane) {
+    const float4 geo = s.geo[j];
+    const float4 aux = s.aux[j];
+    const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
+    const float4 col = s.col[j];
+    const float du = pix.fx - geo.x;
+    const float Adudu = (geo.z * du) * du;
+    const float B2du = geo.w * du;
+    const float r_one = __builtin_amdgcn_rcpf(1.0f + kTransmittanceEps);
+    float sO = 0.0f;
+    bool hit = false;
+#pragma unroll
+    for (int q = 0; q < kStrips; ++q) {
+        if (!((smask >> q) & 1u)) continue;  // uniform
+        const float dv = pix.fy[q] - geo.y;
+        const float E = fmaf(fmaf(aux.x, dv, B2du), dv, Adudu);
+        const bool inc = !(L.T[q] < T_thr) && (E < aux.y);
+        if (!wave_any(inc)) continue;
+        hit = true;
+        const float G = __builtin_amdgcn_exp2f(E * kNegHalfLog2e);
+        const float gcol = fmaf(L.gr[q], col.x, fmaf(L.gg[q], col.y, L.gb[q] * col.z));
+        const float dalpha = fmaf(L.acc[q] - L.gC[q], r_one, L.T[q] * gcol);
+        sO += inc ? G * dalpha : 0.0f;
+    }
+    if (hit) {
+        float f[kGradFields];
+#pragma unroll
+        for (int i = 0; i < kGradFields; ++i) f[i] = 0.0f;
+        f[5] = sO;
+        const float total = wave_sum9(f, hi8, f8_lane);
+        const uint32_t g = __builtin_amdgcn_readfirstlane(__float_as_uint(col.w));
+        if (tgt.active && tgt.inv_o) {  // the opacity field's lane; the others add 0
+            const uint64_t off = (uint64_t)g * (uint64_t)tgt.stride4;
+            unsafeAtomicAdd(reinterpret_cast<float *>(reinterpret_cast<char *>(tgt.base) + off),
+                            total);
+        }
+    }
+    (void)kSafe;
+}
+
 // One staged entry j: per-strip gradient terms summed over the lane's pixels,
 // then the nine-field wave sum and one atomic per field (lanes of tgt).
 template <bool kSafe>
@@ -639,6 +691,10 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
                                                bool f8_lane) {
     const float4 geo = s.geo[j];
     const float4 aux = s.aux[j];
+    if (__builtin_amdgcn_readfirstlane(__float_as_uint(aux.w)) == 0xFF800000u) {  // o = 0
+        backward_zero_opacity_entry<kSafe>(s, j, pix, T_thr, L, tgt, hi8, f8_lane);
+        return;
+    }
     const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
     const float4 col = s.col[j];
     const float du = pix.fx - geo.x;

@@ -117,6 +117,37 @@ def test_rasterize_generic_tile_sizes(gpu, tile):
         assert helpers.rel_l2(a, t.grad) <= 1e-3
 
 
+@pytest.mark.parametrize("alpha_thr,chi", [(0.0, 9.21), (1e-4, 9.21), (0.05, 9.21), (1e-4, 4.0)])
+def test_rasterize_thresholds_and_opacity_extremes(gpu, alpha_thr, chi):
+    """The 16x16 kernels' inclusion test (E below min(chi, 2 ln(o / alpha_thr)), staged
+    per record) against the oracle's separate chi-square and alpha tests, with
+    zero, tiny and near-one opacities among the Gaussians and several thresholds:
+    image <= 1e-4, gradients relative L2 <= 1e-3."""
+    p, cam, _ = helpers.scene_box(3_000, 96, 72, 100.0, seed=12, log_scale=(-3.0, 0.5))
+    scales, quats, opac = helpers.activated(p)
+    pts, depths, _, conic, radii, mask = preprocess.project_points(
+        p["means"], scales, quats, opac, cam["w2c"], cam["K"], 0.01, 100.0, 0.0, 0.5, 128.0, 96, 72)
+    opac = opac.detach().clone()
+    opac[::7] = 0.0
+    opac[1::7] = 1e-6
+    opac[2::7] = 0.9999
+    colors = torch.rand(3_000, 3, generator=torch.Generator().manual_seed(3))
+    opac_m = torch.where(mask, opac, torch.zeros_like(opac))
+    d = lambda t: t.detach().to(gpu)  # noqa: E731
+    off, ids = cr.compute_tile_intersection(d(pts), d(radii), d(depths), d(mask), 96, 72, 16)
+    args = (96, 72, 16, alpha_thr, 1e-4, chi)
+    ins = [t.detach().clone().requires_grad_(True) for t in (pts, conic, opac_m, colors)]
+    ref = blend.rasterize(off.cpu(), ids.cpu(), *ins, *args)
+    up = torch.randn(72, 96, 3, generator=torch.Generator().manual_seed(4))
+    (ref * up).sum().backward()
+    image = cr.rasterize(off, ids, *[d(t) for t in ins], *args)
+    assert helpers.max_abs(image.clamp(0, 1), ref.clamp(0, 1)) <= 1e-4
+    grads = cr.rasterize_backward(up.to(gpu), off, ids, *[d(t) for t in ins], *args,
+                                  rendered_image=image)
+    for a, t in zip(grads, ins):
+        assert helpers.rel_l2(a, t.grad) <= 1e-3
+
+
 def test_rasterize_edge_cases(gpu):
     W, H = 40, 24
     off = torch.zeros(6, dtype=torch.int32, device=gpu)
