@@ -246,7 +246,10 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
                              chi_eff, x0, y0);
     }
     const uint64_t keep = __ballot(m != 0u);
-    const bool bad = m != 0u && !(isfinite(r.r) && isfinite(r.g) && isfinite(r.b));
+    // a non-finite colour or log2 opacity (o <= 0 or NaN): the batch takes the
+    // select-based path (where the backward also handles zero opacity)
+    const bool bad = m != 0u && !(isfinite(r.r) && isfinite(r.g) && isfinite(r.b) &&
+                                  isfinite(log2o));
     if (m != 0u) {
         const int slot = __popcll(keep & lanemask_lt());
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
@@ -691,7 +694,7 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
                                                bool f8_lane) {
     const float4 geo = s.geo[j];
     const float4 aux = s.aux[j];
-    if (__builtin_amdgcn_readfirstlane(__float_as_uint(aux.w)) == 0xFF800000u) {  // o = 0
+    if (kSafe && __builtin_amdgcn_readfirstlane(__float_as_uint(aux.w)) == 0xFF800000u) {  // o = 0
         backward_zero_opacity_entry<kSafe>(s, j, pix, T_thr, L, tgt, hi8, f8_lane);
         return;
     }
