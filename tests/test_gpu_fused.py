@@ -201,10 +201,11 @@ def _xcd_ranges(n_tiles):
         start += size
 
 
-# XCD ranges of 14-15, 1020, 2000 and 4050 tiles (one, two, four and eight keys
-# per lane in the per-wave sorts) and of 4224 tiles (kept in band order)
-@pytest.mark.parametrize("size", [(200, 130), (1920, 1080), (2560, 1600), (3840, 2160),
-                                  (4096, 2112)])
+# XCD ranges of 0-1 tiles (a 2x2 and a 1x1 grid), 14-15, 1020, 2000 and 4050
+# tiles (one, two, four and eight keys per lane in the per-wave sorts) and of
+# 4224 tiles (kept in band order)
+@pytest.mark.parametrize("size", [(32, 32), (16, 16), (200, 130), (1920, 1080), (2560, 1600),
+                                  (3840, 2160), (4096, 2112)])
 def test_tile_schedule(gpu, size):
     """rasterize_display_l1(schedule=...) leaves the image, display and loss as
     without it, writes each tile's work and, per XCD range of at most 4096
