@@ -851,6 +851,7 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
     int32_t *__restrict__ indexing_offset, uint32_t *__restrict__ table) {
     __shared__ uint32_t tmp[kL2Waves + 1];
     __shared__ uint32_t thread_base[kL2Threads];
+    __shared__ uint32_t tile_pre[kFusedTileScanMax];  // prefix within the owning thread's run
     __shared__ uint32_t tile_off[kSuperLocal];
     __shared__ uint32_t run_sum[kL2Waves][kSuperLocal];
     const int s = blockIdx.x;
@@ -859,7 +860,11 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
     if (fused_scan) {
         const int t0 = min(tid * per, n_tiles), t1 = min(t0 + per, n_tiles);
         uint32_t mine = 0;
-        for (int t = t0; t < t1; ++t) mine += tile_counts[t];
+#pragma unroll 8
+        for (int t = t0; t < t1; ++t) {
+            tile_pre[t] = mine;
+            mine += tile_counts[t];
+        }
         uint32_t total;
         thread_base[tid] = block_exclusive_scan<uint32_t, kL2Threads>(mine, tmp, total);
         __syncthreads();
@@ -869,9 +874,7 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
         uint32_t off = 0;
         if (t >= 0) {
             if (fused_scan) {
-                const int owner = t / per;
-                off = thread_base[owner];
-                for (int u = owner * per; u < t; ++u) off += tile_counts[u];
+                off = thread_base[t / per] + tile_pre[t];
                 indexing_offset[t] = (int32_t)off;
             } else {
                 off = (uint32_t)indexing_offset[t];
