@@ -56,6 +56,8 @@ def _check(gpu, pts, radii, depths, mask, width, height, tile):
     (3000, 64, 64, 8),
     (3000, 200, 90, 32),
     (50000, 800, 800, 16),
+    (30000, 2048, 2048, 16),  # 16384 tiles: the largest grid the fused tile scan takes
+    (30000, 2048, 2064, 16),  # 16512 tiles: one tile row past it (separate scan)
 ])
 def test_layout_random_bitexact(gpu, n, width, height, tile):
     pts, radii, depths, mask = _random_splats(n, width, height, seed=n + width)
