@@ -119,11 +119,21 @@ struct BatchLds {
     float4 aux[kBatch];  // C, E cut-off (chi_eff), strip mask, log2(opacity)
     float4 col[kBatch];  // r, g, b, (gaussian id bits)
     float inv_o[kBatch];  // 1 / opacity (staged by the backward for its opacity gradient)
+    float o_raw[kBatch];  // the opacity of a record whose log2 is not finite (see below)
 };
 
-// log2(o) for the exponent form of alpha; -inf when o <= 0 (alpha 0: skipped,
-// as o exp(-E/2) <= 0 < alpha_thr), NaN stays NaN (alpha NaN: composited, as
-// in the reference).
+// Records whose log2 opacity is not finite -- opacity <= 0, +inf or NaN -- are
+// composited as alpha = o exp(-E/2) from the staged raw opacity, with the alpha
+// test applied to that value (!(alpha < alpha_thr), so a NaN alpha passes, as in
+// the reference), in the select-based path that their batch takes.  They are
+// staged only when the alpha test can pass them: with alpha_thr > 0 an opacity
+// <= 0 has the cut-off -inf.  Their opacity gradient is sum G dalpha
+// (G = exp(-E/2)); the h / o form of the other records would give 0 * inf at
+// o = 0, so the backward stages 1 for their 1 / o.
+__device__ __forceinline__ bool special_opacity(float log2o) { return !isfinite(log2o); }
+
+// log2(o) for the exponent form of alpha; -inf when o <= 0 and NaN for a NaN
+// opacity: such records are composited from their raw opacity (special_opacity).
 __device__ __forceinline__ float log2_opacity(float o) {
     return o > 0.0f ? __builtin_amdgcn_logf(o) : (o == o ? -__builtin_inff() : o);
 }
@@ -246,8 +256,8 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
                              chi_eff, x0, y0);
     }
     const uint64_t keep = __ballot(m != 0u);
-    // a non-finite colour or log2 opacity (o <= 0 or NaN): the batch takes the
-    // select-based path (where the backward also handles zero opacity)
+    // a non-finite colour or log2 opacity (o <= 0, +inf or NaN): the batch takes
+    // the select-based path (the only one that handles such opacities)
     const bool bad = m != 0u && !(isfinite(r.r) && isfinite(r.g) && isfinite(r.b) &&
                                   isfinite(log2o));
     if (m != 0u) {
@@ -255,7 +265,9 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
         s.aux[slot] = make_float4(r.C, chi_eff, __uint_as_float(m), log2o);
         s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
-        if (kInvO) s.inv_o[slot] = __builtin_amdgcn_rcpf(r.o);
+        const bool special = special_opacity(log2o);
+        if (kInvO) s.inv_o[slot] = special ? 1.0f : __builtin_amdgcn_rcpf(r.o);
+        if (special) s.o_raw[slot] = r.o;
     }
     Staged st;
     st.count = __popcll(keep);
@@ -351,15 +363,22 @@ __device__ __forceinline__ float display_grad(float g, float raw) {
     return (raw >= 0.0f && raw <= 1.0f) ? g * 255.0f : 0.0f;
 }
 
+// x / 255 as PyTorch computes it on the GPU for a tensor x and the Python
+// scalar 255.0: x times the reciprocal of 255 rounded to float (ATen's true
+// division by a CPU scalar multiplies by 1 / b).  The reference's loss divides
+// the display image this way (scripts/train.py:187-197: rendered_image / 255.0),
+// and the backward of that division divides the gradient the same way.
+constexpr float kInv255 = 1.0f / 255.0f;
+
 // Gradient w.r.t. display of scale * |display / 255 - t| (torch's l1_loss: sign
 // of the difference, 0 at 0), plus `extra`, a further gradient w.r.t.
 // display / 255 (summed there, as autograd sums the two uses of display / 255),
 // then the division by 255.
 __device__ __forceinline__ float l1_grad(float t, float raw, float scale, float extra) {
-    const float x = (clamp01(raw) * 255.0f) / 255.0f;
+    const float x = (clamp01(raw) * 255.0f) * kInv255;
     const float d = x - t;
     const float sgn = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
-    return (sgn * scale + extra) / 255.0f;
+    return (sgn * scale + extra) * kInv255;
 }
 
 // Some pixel of the wave still composites: !(T < T_thr) (NaN stays active).
@@ -384,6 +403,10 @@ __device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const Lane
     const float4 aux = s.aux[j];
     const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
     const float4 col = s.col[j];
+    // uniform: a record with a non-finite log2 opacity (only in the select-based path)
+    const bool special =
+        kSafe && special_opacity(__uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(aux.w))));
+    const float o_sp = special ? s.o_raw[j] : 0.0f;
     const float du = pix.fx - geo.x;
     const float Adudu = (geo.z * du) * du;  // (A du) du, as in the oracle's A*du*du
     const float B2du = geo.w * du;
@@ -393,10 +416,15 @@ __device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const Lane
         const float dv = pix.fy[q] - geo.y;
         const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
         // the chi-square and alpha tests as one cut-off on E (staged in aux.y)
-        const bool inc = !(T[q] < T_thr) && (E < aux.y);
+        bool inc = !(T[q] < T_thr) && (E < aux.y);
+        float alpha = 0.0f;
+        if (special) {  // alpha = o exp(-E/2) from the raw opacity, alpha test on its value
+            alpha = o_sp * __builtin_amdgcn_exp2f(E * kNegHalfLog2e);
+            inc = inc && !(alpha < alpha_thr);
+        }
         if (!wave_any(inc)) continue;
         work += kCostStrip;
-        const float alpha = alpha_of(E, aux.w);
+        if (!special) alpha = alpha_of(E, aux.w);
         if (kSafe) {
             const float w = alpha * T[q];
             cr[q] = inc ? fmaf(w, col.x, cr[q]) : cr[q];
@@ -582,7 +610,7 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
                 display[o + c] = d[c];
-                if (target) l1 += fabsf(d[c] / 255.0f - target[o + c]);  // |display/255 - t|
+                if (target) l1 += fabsf(d[c] * kInv255 - target[o + c]);  // |display/255 - t|
             }
         }
     }
@@ -635,56 +663,6 @@ struct BackwardLane {
     float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips];
 };
 
-// An entry of opacity 0 (log2 o = -inf; included only when alpha_thr <= 0):
-// alpha = 0, so it changes no pixel, no transmittance and no other gradient,
-// and d loss / d o = sum over its pixels of G dalpha with G = exp(-E/2), which
-// the h / o form of the other entries cannot give (0 * inf).  dalpha =
-// T (g.c) - (g.C - acc) / (1 + eps).
-template <bool kSafe>
-__device__ __forceinline__ void backward_zero_opacity_entry(const BatchLds &s, int j,
-                                                            const LanePixels &pix, float T_thr,
-                                                            const BackwardLane &L,
-                                                            const GradTarget &tgt, bool hi8,
-                                                            bool f8_lane) {
-    const float4 geo = s.geo[j];
-    const float4 aux = s.aux[j];
-    const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
-    const float4 col = s.col[j];
-    const float du = pix.fx - geo.x;
-    const float Adudu = (geo.z * du) * du;
-    const float B2du = geo.w * du;
-    const float r_one = __builtin_amdgcn_rcpf(1.0f + kTransmittanceEps);
-    float sO = 0.0f;
-    bool hit = false;
-#pragma unroll
-    for (int q = 0; q < kStrips; ++q) {
-        if (!((smask >> q) & 1u)) continue;  // uniform
-        const float dv = pix.fy[q] - geo.y;
-        const float E = fmaf(fmaf(aux.x, dv, B2du), dv, Adudu);
-        const bool inc = !(L.T[q] < T_thr) && (E < aux.y);
-        if (!wave_any(inc)) continue;
-        hit = true;
-        const float G = __builtin_amdgcn_exp2f(E * kNegHalfLog2e);
-        const float gcol = fmaf(L.gr[q], col.x, fmaf(L.gg[q], col.y, L.gb[q] * col.z));
-        const float dalpha = fmaf(L.acc[q] - L.gC[q], r_one, L.T[q] * gcol);
-        sO += inc ? G * dalpha : 0.0f;
-    }
-    if (hit) {
-        float f[kGradFields];
-#pragma unroll
-        for (int i = 0; i < kGradFields; ++i) f[i] = 0.0f;
-        f[5] = sO;
-        const float total = wave_sum9(f, hi8, f8_lane);
-        const uint32_t g = __builtin_amdgcn_readfirstlane(__float_as_uint(col.w));
-        if (tgt.active && tgt.inv_o) {  // the opacity field's lane; the others add 0
-            const uint64_t off = (uint64_t)g * (uint64_t)tgt.stride4;
-            unsafeAtomicAdd(reinterpret_cast<float *>(reinterpret_cast<char *>(tgt.base) + off),
-                            total);
-        }
-    }
-    (void)kSafe;
-}
-
 // One staged entry j: per-strip gradient terms summed over the lane's pixels,
 // then the nine-field wave sum and one atomic per field (lanes of tgt).
 template <bool kSafe>
@@ -694,10 +672,12 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
                                                bool f8_lane) {
     const float4 geo = s.geo[j];
     const float4 aux = s.aux[j];
-    if (kSafe && __builtin_amdgcn_readfirstlane(__float_as_uint(aux.w)) == 0xFF800000u) {  // o = 0
-        backward_zero_opacity_entry<kSafe>(s, j, pix, T_thr, L, tgt, hi8, f8_lane);
-        return;
-    }
+    // uniform: a record with a non-finite log2 opacity (only in the select-based
+    // path); its opacity gradient is summed as G dalpha (its staged 1 / o is 1)
+    const bool special =
+        kSafe && special_opacity(__uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(aux.w))));
+    const float o_sp = special ? s.o_raw[j] : 0.0f;
+    float sGd = -0.0f;
     const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
     const float4 col = s.col[j];
     const float du = pix.fx - geo.x;
@@ -715,10 +695,16 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
         if (!((smask >> q) & 1u)) continue;  // uniform
         const float dv = pix.fy[q] - geo.y;
         const float E = fmaf(fmaf(aux.x, dv, B2du), dv, Adudu);
-        const bool inc = !(L.T[q] < T_thr) && (E < chi_a);
+        bool inc = !(L.T[q] < T_thr) && (E < chi_a);
+        float alpha = 0.0f, G = 0.0f;
+        if (special) {  // alpha = o G from the raw opacity, alpha test on its value
+            G = __builtin_amdgcn_exp2f(E * kNegHalfLog2e);
+            alpha = o_sp * G;
+            inc = inc && !(alpha < alpha_thr);
+        }
         if (!wave_any(inc)) continue;
         hit = true;
-        const float alpha = alpha_of(E, aux.w);
+        if (!special) alpha = alpha_of(E, aux.w);
         const float a = kSafe ? alpha : (inc ? alpha : 0.0f);
         const float w = a * L.T[q];
         const float gcol = fmaf(L.gr[q], col.x, fmaf(L.gg[q], col.y, L.gb[q] * col.z));
@@ -728,6 +714,7 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
         const float dalpha = fmaf(acc_new - L.gC[q], __builtin_amdgcn_rcpf(one_m), L.T[q] * gcol);
         const float h = kSafe ? (inc ? a * dalpha : 0.0f) : a * dalpha;
         const float ws = kSafe ? (inc ? w : 0.0f) : w;
+        if (special) sGd += inc ? G * dalpha : 0.0f;
         sH += h;
         const float t = h * dv;
         s1 += t;
@@ -747,7 +734,7 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
         f[2] = du * ad;                  // d/dA / (-1/2)
         f[3] = du * s1;                  // d/dB / (-1)
         f[4] = s2;                       // d/dC / (-1/2)
-        f[5] = sH;                       // d/dopacity * o
+        f[5] = special ? sGd : sH;       // d/dopacity * o (special: d/dopacity)
         f[6] = sr;
         f[7] = sg;
         f[8] = sb;

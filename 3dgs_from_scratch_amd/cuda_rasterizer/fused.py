@@ -72,6 +72,9 @@ class RenderL1Function(torch.autograd.Function):
                               sh_coeffs_rest, world_to_camera, intrinsic, target, opac, pts, cov,
                               conic, mask, colors, off, ids, image, acc, sched, *ssim_saved)
         ctx.ssim_lambda = ssim_lambda
+        # acc is zeroed once, by the forward launch: only the first backward may add
+        # into it (the gradients it returns are views of it)
+        ctx.acc_fresh = True
         ctx.densifier = densifier
         ctx.radii = radii if densifier is not None else None
         ctx.params = (width, height, alpha_threshold, transmittance_threshold,
@@ -96,9 +99,14 @@ class RenderL1Function(torch.autograd.Function):
             extra = _ssim.ssim_backward(g, _chw(display), _chw(target), (m1, m2, m3),
                                         img1_divisor=255.0, grad_scale=-lam)
             extra = extra[0].permute(1, 2, 0)  # laid out like display: (H, W, 3) contiguous
+        # a later backward over the same graph (retain_graph) gets freshly zeroed
+        # buffers, so it neither adds onto nor overwrites the first one's results
+        accumulators = acc if ctx.acc_fresh else None
+        ctx.acc_fresh = False
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_l1_backward(
             target, g, off, ids, pts, conic, opac, colors, width, height, image, a_thr, t_thr,
-            chi, accumulators=acc, grad_display01=extra, loss_scale=1.0 - lam, schedule=sched)
+            chi, accumulators=accumulators, grad_display01=extra, loss_scale=1.0 - lam,
+            schedule=sched)
         if ctx.densifier is not None:
             ctx.densifier.update(g_pts, ctx.radii, width, height)
         g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(

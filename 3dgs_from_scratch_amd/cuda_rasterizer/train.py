@@ -211,11 +211,10 @@ class Densifier:
             n_rest = int(rest.numel())
             dm = torch.zeros((n_rest + 2 * n_split, 3), device=dev)
             dm[n_rest:] = samples.reshape(2 * n_split, 3)
-            ls = params["log_scales"][x_src[split_sel]]
-            dls = torch.zeros((n_rest + 2 * n_split, 3), device=dev)
-            dls[n_rest:] = (torch.log(s_split / 1.6) - ls).repeat(2, 1)
-            deltas = {"means": dm, "log_scales": dls}
+            deltas = {"means": dm}  # src/strategy.py:191-192: param[selection] + samples
         self._rebuild(params, opt, src_rows, fresh, deltas)
+        if n_split:  # src/strategy.py:193-194 stores log(scale / 1.6) itself (not a delta)
+            params["log_scales"].data[n_rest:] = torch.log(s_split / 1.6).repeat(2, 1)
         return int(is_prune.sum()), n_clone, n_split
 
     @torch.no_grad()

@@ -201,3 +201,32 @@ def render(
                                             tile_size, alpha_threshold, transmittance_threshold,
                                             chi_squared_threshold, torch.is_grad_enabled())
     return display, points_img, radii
+
+
+def render_unfused(world_to_camera, intrinsic, width, height, means, scales, quaternions,
+                   opacities, sh_coeffs_dc, sh_coeffs_rest, near_plane=0.01, far_plane=100.0,
+                   min_opacity=1 / 255, min_radius=0.5, max_radius=128.0, alpha_threshold=1e-4,
+                   transmittance_threshold=1e-4, chi_squared_threshold=9.21, sh_sigmoid=False):
+    """render() composed of the seven extension functions exactly as the reference's
+    own src/cuda/wrapper.py:223-294 composes them: ProjectPointsFunction ->
+    camera position and SphericalHarmonicsFunction -> clamp_min(c + 0.5, 0) in
+    PyTorch -> compute_tile_intersection -> RasterizeFunction -> clamp(0, 1) * 255
+    in PyTorch.  This is the call sequence a caller that keeps the reference's
+    wrapper and swaps in this `cuda_rasterizer` module runs; render() gives the
+    same values with fused kernels."""
+    points_img, depths, cov_inv_img, radii, mask = ProjectPointsFunction.apply(
+        means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
+        far_plane, min_opacity, min_radius, max_radius, width, height)
+    camera_pos = -world_to_camera[:3, :3].t() @ world_to_camera[:3, 3]
+    colors = SphericalHarmonicsFunction.apply(camera_pos, means, sh_coeffs_dc, sh_coeffs_rest,
+                                              mask, sh_sigmoid)
+    if not sh_sigmoid:
+        colors = torch.clamp_min(colors + 0.5, 0.0)
+    tile_size = 16
+    indexing_offset, gaussian_ids_sorted = _cr.compute_tile_intersection(
+        points_img.contiguous(), radii.contiguous(), depths.contiguous(), mask.contiguous(),
+        width, height, tile_size)
+    image = RasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img,
+                                    opacities, colors, width, height, tile_size, alpha_threshold,
+                                    transmittance_threshold, chi_squared_threshold)
+    return image.clamp(0, 1) * 255, points_img, radii

@@ -117,12 +117,18 @@ def test_rasterize_generic_tile_sizes(gpu, tile):
         assert helpers.rel_l2(a, t.grad) <= 1e-3
 
 
-@pytest.mark.parametrize("alpha_thr,chi", [(0.0, 9.21), (1e-4, 9.21), (0.05, 9.21), (1e-4, 4.0)])
-def test_rasterize_thresholds_and_opacity_extremes(gpu, alpha_thr, chi):
+@pytest.mark.parametrize("alpha_thr,chi,t_thr", [(0.0, 9.21, 1e-4), (1e-4, 9.21, 1e-4),
+                                                 (0.05, 9.21, 1e-4), (1e-4, 4.0, 1e-4),
+                                                 (-0.05, 9.21, 0.0)])
+def test_rasterize_thresholds_and_opacity_extremes(gpu, alpha_thr, chi, t_thr):
     """The 16x16 kernels' inclusion test (E below min(chi, 2 ln(o / alpha_thr)), staged
     per record) against the oracle's separate chi-square and alpha tests, with
-    zero, tiny and near-one opacities among the Gaussians and several thresholds:
-    image <= 1e-4, gradients relative L2 <= 1e-3."""
+    zero, tiny, near-one and negative opacities among the Gaussians and several
+    thresholds: image <= 1e-4, gradients relative L2 <= 1e-3.  A negative
+    opacity gives alpha = o exp(-E/2) < 0: skipped (zero gradient) for
+    alpha_thr >= 0, composited where alpha >= alpha_thr < 0 (there with
+    transmittance threshold 0: T can then grow, and the oracle's zeroing of
+    T < T_thr differs from stopping the pixel)."""
     p, cam, _ = helpers.scene_box(3_000, 96, 72, 100.0, seed=12, log_scale=(-3.0, 0.5))
     scales, quats, opac = helpers.activated(p)
     pts, depths, _, conic, radii, mask = preprocess.project_points(
@@ -131,11 +137,12 @@ def test_rasterize_thresholds_and_opacity_extremes(gpu, alpha_thr, chi):
     opac[::7] = 0.0
     opac[1::7] = 1e-6
     opac[2::7] = 0.9999
+    opac[3::7] = -0.3 * opac[3::7]
     colors = torch.rand(3_000, 3, generator=torch.Generator().manual_seed(3))
     opac_m = torch.where(mask, opac, torch.zeros_like(opac))
     d = lambda t: t.detach().to(gpu)  # noqa: E731
     off, ids = cr.compute_tile_intersection(d(pts), d(radii), d(depths), d(mask), 96, 72, 16)
-    args = (96, 72, 16, alpha_thr, 1e-4, chi)
+    args = (96, 72, 16, alpha_thr, t_thr, chi)
     ins = [t.detach().clone().requires_grad_(True) for t in (pts, conic, opac_m, colors)]
     ref = blend.rasterize(off.cpu(), ids.cpu(), *ins, *args)
     up = torch.randn(72, 96, 3, generator=torch.Generator().manual_seed(4))

@@ -167,6 +167,30 @@ def test_render_l1_repeated_calls_are_stable(gpu):
         assert helpers.rel_l2(out[1][1][k], out[0][1][k]) <= 1e-5, k
 
 
+@pytest.mark.parametrize("lam", [0.0, 0.2])
+def test_render_l1_backward_twice_with_retain_graph(gpu, lam):
+    """Two backward passes over one render_l1 graph (retain_graph) accumulate twice
+    the gradients of one pass, as autograd does for any graph; the first pass's
+    gradients are left untouched by the second (its blend accumulators are the
+    forward's zeroed buffer, the second pass's are fresh)."""
+    p, cam, target = helpers.scene_orbit(4_000, 128, 96, 180.0, seed=26)
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    b = _raw_leaves(p, gpu)
+    loss, _, _, _ = render_l1(w2c, K, 128, 96, b["means"], b["log_scales"], b["quats_raw"],
+                              b["opacity_logits"], b["sh_dc"], b["sh_rest"], tgt, ssim_lambda=lam)
+    g1 = torch.autograd.grad(loss, list(b.values()), retain_graph=True)
+    once = [t.clone() for t in g1]
+    g2 = torch.autograd.grad(loss, list(b.values()), retain_graph=True)
+    for k, a, c, d in zip(b, once, g1, g2):
+        assert torch.equal(c, a), k  # the first result is not written into
+        assert helpers.rel_l2(d, a) <= 1e-5, k
+    loss.backward(retain_graph=True)
+    loss.backward()
+    for k, a in zip(b, once):
+        assert float(a.norm()) > 0.0, k
+        assert helpers.rel_l2(b[k].grad, 2.0 * a) <= 1e-5, k
+
+
 @pytest.mark.parametrize("count", [9 * 8000, 10, 4 * 8000 + 2])
 def test_display_l1_clears_buffer(gpu, count):
     """rasterize_display_l1(clear=...) zeroes the buffer (in the blend launch when

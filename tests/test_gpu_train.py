@@ -121,10 +121,15 @@ def test_refine_matches_oracle_row_map(gpu):
     split_rows[len(src) - 2 * n_split:] = True
     _check_rebuild(params, before, opt, st_before, src, fresh, skip_rows=split_rows,
                    skip_keys=("means", "log_scales"))
-    # split copies: log-scale = log(scale / 1.6); means offset by samples of norm ~ scale
+    # split copies: log-scale = log(scale / 1.6), stored as such (src/strategy.py:193-194:
+    # the same torch ops on the same device, so bit-equal); means offset by samples of
+    # norm ~ scale
     got_ls = params["log_scales"].detach().cpu()[split_rows]
-    want_ls = torch.log(torch.exp(before["log_scales"][split_src]) / 1.6).repeat(2, 1)
-    assert torch.allclose(got_ls, want_ls, rtol=0, atol=1e-5)
+    s_dev = torch.exp(before["log_scales"].to(gpu))[split_src.to(gpu)]
+    want_ls = torch.log(s_dev / 1.6).repeat(2, 1).cpu()
+    assert torch.equal(got_ls, want_ls)
+    assert torch.allclose(got_ls, torch.log(torch.exp(before["log_scales"][split_src]) / 1.6)
+                          .repeat(2, 1), rtol=0, atol=1e-5)
     off = params["means"].detach().cpu()[split_rows] - before["means"][split_src].repeat(2, 1)
     scale = torch.exp(before["log_scales"][split_src]).max(dim=1).values.repeat(2)
     assert bool((off.norm(dim=1) <= 6.0 * scale * 3 ** 0.5).all())
