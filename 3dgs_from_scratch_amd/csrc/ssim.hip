@@ -21,6 +21,7 @@
 // backward, which filters them back the same way.  The mean is reduced
 // deterministically: per-workgroup double partials, then one workgroup.
 #include <cmath>
+#include <mutex>
 
 #include "gs_common.h"
 
@@ -497,13 +498,17 @@ extern "C" int gs_ssim_workspace_size(int32_t batch, int32_t channels, int32_t h
     return GS_OK;
 }
 
-extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const float *img2,
-                               const int64_t *strides2, int32_t batch, int32_t channels,
-                               int32_t height, int32_t width, int32_t valid_padding,
-                               float img1_divisor, float *ssim_mean, float *dm_dmu1,
-                               float *dm_dsigma1_sq, float *dm_dsigma12, const float *other_loss,
-                               float lambda, float *loss, void *workspace,
-                               size_t workspace_bytes, hipStream_t stream) {
+namespace gs {
+namespace {
+
+// gs_ssim_forward with the per-workgroup partials in `partials` (room for
+// `capacity` doubles).
+int ssim_forward_impl(const float *img1, const int64_t *strides1, const float *img2,
+                      const int64_t *strides2, int32_t batch, int32_t channels, int32_t height,
+                      int32_t width, int32_t valid_padding, float img1_divisor, float *ssim_mean,
+                      float *dm_dmu1, float *dm_dsigma1_sq, float *dm_dsigma12,
+                      const float *other_loss, float lambda, float *loss, double *partials,
+                      size_t capacity, hipStream_t stream) {
     Geometry g;
     Planes p;
     if (!geometry(batch, channels, height, width, g) || !ssim_mean || !(img1_divisor > 0.0f))
@@ -516,11 +521,9 @@ extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const
     if ((dm_dmu1 != nullptr) != (dm_dsigma1_sq != nullptr) ||
         (dm_dmu1 != nullptr) != (dm_dsigma12 != nullptr))
         return GS_ERR_INVALID_ARGUMENT;
-    if (!workspace || workspace_bytes < (size_t)g.blocks * sizeof(double))
-        return GS_ERR_WORKSPACE_TOO_SMALL;
+    if (!partials || capacity < (size_t)g.blocks) return GS_ERR_WORKSPACE_TOO_SMALL;
     const double count = region_pixels(batch, channels, height, width, valid_padding != 0);
     p.inv_count = count > 0.0 ? (float)(1.0 / count) : 0.0f;
-    double *partials = reinterpret_cast<double *>(workspace);
     hipLaunchKernelGGL(ssim_forward_kernel, dim3(g.blocks), dim3(kThreads), 0, stream, p,
                        make_window(), dm_dmu1, dm_dsigma1_sq, dm_dsigma12, partials);
     st = launch_status();
@@ -529,6 +532,81 @@ extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const
                        (const double *)partials, (int64_t)g.blocks, count, ssim_mean, other_loss,
                        lambda, loss);
     return launch_status();
+}
+
+// Scratch of the allocation-free forward: the per-workgroup partials (one
+// double per persistent workgroup, at most kPersistentBlocks: 4 KiB), in a
+// file-scope device array that every GPU the library runs on holds until the
+// process ends.  Every forward launch writes all the partials its mean kernel
+// reads, so nothing needs clearing between calls; calls that overlap on one GPU
+// (different streams) share the array and race.  In host code the array's name
+// is not a device address: its address on each device comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr int kScratchPartials = kPersistentBlocks;
+__device__ __align__(256) double scratch[kScratchPartials];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex scratch_mutex;
+double *scratch_ptr[kMaxScratchDevices] = {};
+
+// The scratch array's address on the current device, which must be the device
+// of `stream`.
+int scratch_for_stream(hipStream_t stream, double **out) {
+    int dev = -1, stream_dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    e = hipStreamGetDevice(stream, &stream_dev);
+    if (e != hipSuccess) return (int)e;
+    if (stream_dev != dev) return GS_ERR_INVALID_ARGUMENT;
+    if (dev < 0 || dev >= kMaxScratchDevices) return GS_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!ptr) return GS_ERR_UNSUPPORTED;
+        scratch_ptr[dev] = static_cast<double *>(ptr);
+    }
+    *out = scratch_ptr[dev];
+    return GS_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_ssim_forward(const float *img1, const int64_t *strides1, const float *img2,
+                               const int64_t *strides2, int32_t batch, int32_t channels,
+                               int32_t height, int32_t width, int32_t valid_padding,
+                               float img1_divisor, float *ssim_mean, float *dm_dmu1,
+                               float *dm_dsigma1_sq, float *dm_dsigma12, const float *other_loss,
+                               float lambda, float *loss, void *workspace,
+                               size_t workspace_bytes, hipStream_t stream) {
+    return ssim_forward_impl(img1, strides1, img2, strides2, batch, channels, height, width,
+                             valid_padding, img1_divisor, ssim_mean, dm_dmu1, dm_dsigma1_sq,
+                             dm_dsigma12, other_loss, lambda, loss,
+                             reinterpret_cast<double *>(workspace),
+                             workspace ? workspace_bytes / sizeof(double) : 0, stream);
+}
+
+extern "C" int gs_ssim_forward_noalloc(const float *img1, const int64_t *strides1,
+                                       const float *img2, const int64_t *strides2, int32_t batch,
+                                       int32_t channels, int32_t height, int32_t width,
+                                       int32_t valid_padding, float img1_divisor,
+                                       float *ssim_mean, float *dm_dmu1, float *dm_dsigma1_sq,
+                                       float *dm_dsigma12, const float *other_loss, float lambda,
+                                       float *loss, hipStream_t stream) {
+    Geometry g;
+    if (!geometry(batch, channels, height, width, g)) return GS_ERR_INVALID_ARGUMENT;
+    // the partials the launch needs must fit the static array (always true:
+    // geometry() caps the workgroups at kPersistentBlocks)
+    if (g.blocks > kScratchPartials) return GS_ERR_WORKSPACE_TOO_SMALL;
+    double *partials = nullptr;
+    const int st = scratch_for_stream(stream, &partials);
+    if (st) return st;
+    return ssim_forward_impl(img1, strides1, img2, strides2, batch, channels, height, width,
+                             valid_padding, img1_divisor, ssim_mean, dm_dmu1, dm_dsigma1_sq,
+                             dm_dsigma12, other_loss, lambda, loss, partials, kScratchPartials,
+                             stream);
 }
 
 extern "C" int gs_ssim_backward(const float *grad_mean, const float *img1,

@@ -74,6 +74,7 @@ SIGNATURES.update({
     "gs_gather_rows": [_I64, _P, _P, ctypes.POINTER(GsGatherTensor), _I32, _P],
     "gs_ssim_workspace_size": [_I32, _I32, _I32, _I32, _PSZ],
     "gs_ssim_forward": [_P] * 4 + [_I32] * 5 + [_F] + [_P] * 5 + [_F, _P, _P, _SZ, _P],
+    "gs_ssim_forward_noalloc": [_P] * 4 + [_I32] * 5 + [_F] + [_P] * 5 + [_F, _P, _P],
     "gs_ssim_backward": [_P] * 5 + [_I32] * 4 + [_F] + [_P] * 3 + [_F, _P, _P, _P],
 })
 

@@ -7,7 +7,8 @@
  *   > 0          a hipError_t reported by the HIP runtime (launch or API failure)
  *   < 0          one of the GS_ERR_* argument errors below (nothing was launched)
  * No entry point allocates device memory; scratch space is passed in by the
- * caller (query its size with the *_workspace_size functions).  No entry point
+ * caller (query its size with the *_workspace_size functions), except in
+ * gs_ssim_forward_noalloc, which keeps it in a static device array.  No entry point
  * synchronises the stream.  Outputs are written in full (culled / masked
  * entries are written as zero), so callers need not pre-clear them, except
  * where an entry point documents accumulation.
@@ -421,6 +422,23 @@ int gs_ssim_forward(const float *img1, const int64_t *strides1, const float *img
                     float *dm_dmu1, float *dm_dsigma1_sq, float *dm_dsigma12,
                     const float *other_loss, float lambda, float *loss, void *workspace,
                     size_t workspace_bytes, hipStream_t stream);
+/*
+ * gs_ssim_forward_noalloc: gs_ssim_forward without a workspace argument; it
+ *   allocates nothing and keeps its per-workgroup partials in a static device
+ *   array of 512 doubles (4 KiB) that each GPU the library runs on holds until
+ *   the process ends.  No counterpart in the reference: it is for callers that
+ *   cannot allocate (code under HIP graph capture, tight serving loops).  The
+ *   current device must be the device of `stream`.  Every call on one GPU uses
+ *   the same array: calls that overlap on that GPU (on different streams) race.
+ *   Geometries beyond the array are rejected with GS_ERR_WORKSPACE_TOO_SMALL
+ *   (none exist: the forward runs at most 512 workgroups).
+ */
+int gs_ssim_forward_noalloc(const float *img1, const int64_t *strides1, const float *img2,
+                            const int64_t *strides2, int32_t batch, int32_t channels,
+                            int32_t height, int32_t width, int32_t valid_padding,
+                            float img1_divisor, float *ssim_mean, float *dm_dmu1,
+                            float *dm_dsigma1_sq, float *dm_dsigma12, const float *other_loss,
+                            float lambda, float *loss, hipStream_t stream);
 int gs_ssim_backward(const float *grad_mean, const float *img1, const int64_t *strides1,
                      const float *img2, const int64_t *strides2, int32_t batch, int32_t channels,
                      int32_t height, int32_t width, float img1_divisor, const float *dm_dmu1,
