@@ -230,15 +230,16 @@ class Densifier:
     @torch.no_grad()
     def clone_top_and_prune(self, params: dict, opt: FusedAdam | None, fraction: float = 0.05,
                             jitter: float = 0.01, generator=None):
-        """Clone the top `fraction` by accumulated gradient norm (means + N(0, jitter)),
-        prune sigmoid(opacity) < prune_opacity; returns (n_pruned, n_cloned)."""
+        """Clone the top `fraction` by accumulated gradient norm (means + N(0, jitter);
+        ties by index, see top_rows), prune sigmoid(opacity) < prune_opacity; returns
+        (n_pruned, n_cloned)."""
         dev = params["means"].device
         n = params["means"].shape[0]
         opac = torch.sigmoid(params["opacity_logits"])
         is_prune = opac < self.prune_opacity
         keep = torch.where(~is_prune)[0]
         n_top = int(round(fraction * n))
-        top = torch.topk(self.grads, n_top).indices if n_top else keep[:0]
+        top = top_rows(self.grads, n_top)
         src_rows = torch.cat([keep, top])
         fresh = torch.cat([torch.zeros(keep.numel(), dtype=torch.bool, device=dev),
                            torch.ones(n_top, dtype=torch.bool, device=dev)])
@@ -246,6 +247,13 @@ class Densifier:
         dm[keep.numel():] = torch.randn((n_top, 3), device=dev, generator=generator) * jitter
         self._rebuild(params, opt, src_rows, fresh, {"means": dm})
         return int(is_prune.sum()), n_top
+
+
+def top_rows(values: torch.Tensor, count: int) -> torch.Tensor:
+    """Indices of the `count` largest values, largest first, equal values by
+    ascending index (a stable descending sort, so the choice among ties does not
+    depend on the device or the sort implementation)."""
+    return torch.sort(values, descending=True, stable=True).indices[:count]
 
 
 def _rotation(q: torch.Tensor) -> torch.Tensor:

@@ -397,17 +397,22 @@ def run_forward(scene: dict, steps: int, warmup: int) -> dict:
 # ------------------------------------------------- configuration 5 (training)
 
 def _torch_clone_top_and_prune(leaves: dict, optims: dict, grads: torch.Tensor, fraction: float,
-                               jitter: float, prune_opacity: float = 0.005):
+                               jitter: float, prune_opacity: float = 0.005, generator=None):
     """The configuration-5 rule written the way src/strategy.py:71-229 rebuilds
-    parameters and Adam state (index / cat per tensor, state moved to the new leaf)."""
+    parameters and Adam state (index / cat per tensor, state moved to the new leaf).
+    The rows to clone are chosen as cuda_rasterizer.train.top_rows chooses them.
+    The jitter is drawn from `generator` as Densifier.clone_top_and_prune draws it."""
     opac = torch.sigmoid(leaves["opacity_logits"])
     keep = torch.where(~(opac < prune_opacity))[0]
     n_top = int(round(fraction * grads.shape[0]))
-    top = torch.topk(grads, n_top).indices
+    from cuda_rasterizer.train import top_rows
+
+    top = top_rows(grads, n_top)  # the library's rule: largest first, ties by index
     for name, p in list(leaves.items()):
         extra = p[top]
         if name == "means":
-            extra = extra + torch.randn_like(extra) * jitter
+            extra = extra + torch.randn(extra.shape, device=extra.device,
+                                        generator=generator) * jitter
         new = torch.cat([p[keep], extra]).detach().requires_grad_(True)
         opt = optims[name]
         state = opt.state.pop(p)
@@ -493,7 +498,8 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
             sched.step()
             if (step + 1) % every == 0:
                 with torch.no_grad():
-                    _torch_clone_top_and_prune(leaves, optims, grads, fraction, jitter)
+                    _torch_clone_top_and_prune(leaves, optims, grads, fraction, jitter,
+                                               generator=gen)
                 grads = torch.zeros(leaves["means"].shape[0], device=dev)
                 sizes.append(leaves["means"].shape[0])
         if step % 100 == 0 or step == steps - 1:
@@ -518,7 +524,7 @@ def train_stress(steps: int = 2000, which: str = "both") -> dict:
             continue
         r = run_train(scene, path)
         out[path] = {"ms_per_step": round(r["ms"], 4), "peak_hbm_gib": round(r["peak_hbm_bytes"] / 2**30, 3),
-                     "n_end": r["n_end"], "loss_first": round(r["loss_first"], 5),
+                     "n_end": r["n_end"], "sizes": r["sizes"], "loss_first": round(r["loss_first"], 5),
                      "loss_last": round(r["loss_last"], 5)}
     return out
 

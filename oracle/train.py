@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 
@@ -73,11 +74,14 @@ def refine_rows(opacity_logits, log_scales, grads, count, step, prune_opacity=0.
 
 def clone_top_rows(opacity_logits, grads, fraction=0.05, prune_opacity=0.005):
     """Configuration-5 rule: (src_rows, fresh) = kept rows, then the top
-    round(fraction * N) rows by accumulated gradient norm."""
+    round(fraction * N) rows by accumulated gradient norm, largest first and
+    equal norms by ascending index."""
     n = opacity_logits.shape[0]
     keep = torch.where(~(torch.sigmoid(opacity_logits) < prune_opacity))[0]
     n_top = int(round(fraction * n))
-    top = torch.topk(grads, n_top).indices
+    g = grads.detach().cpu().numpy()
+    order = np.lexsort((np.arange(n), -g))  # by -norm, then by index
+    top = torch.from_numpy(order[:n_top].astype(np.int64))
     src_rows = torch.cat([keep, top])
     fresh = torch.cat([torch.zeros(len(keep), dtype=torch.bool), torch.ones(n_top, dtype=torch.bool)])
     return src_rows, fresh

@@ -1,0 +1,200 @@
+"""GPU parity of the blend at the headline sizes (BASELINE configurations 3 and 4).
+
+The blend kernels are checked against the CPU oracle's tile loop
+(src/torch_rasterizer.py:228-284 restated) on the workloads they are timed on:
+the longest tile lists, the multi-batch record prefetch and the heavy-first
+tile order of 8160-tile frames.  Both sides get the GPU's own projected inputs
+(bit-exact with the oracle's projection, tests/test_gpu_preprocess.py) and the
+GPU tile layout (bit-exact, tests/test_gpu_binning.py).  The oracle covers a
+fixed subset -- 200 random non-empty tiles plus the 32 heaviest by the
+forward's work count -- and the upstream gradient is zero outside it, so that
+the GPU backward (which skips pixels with a zero gradient) and the oracle
+cover the same (pixel, entry) pairs.
+
+Bars: image max abs error <= 1e-4 (on [0, 1]); gradients relative L2 <= 1e-3.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import helpers
+import cuda_rasterizer as cr
+from oracle import blend
+
+pytestmark = pytest.mark.gpu
+
+IMG_TOL = 1e-4
+GRAD_TOL = 1e-3
+BLEND_ARGS = (16, 1e-4, 1e-4, 9.21)
+
+
+def _gpu_inputs(scene, gpu):
+    """The fused path's preprocess of the scene on the GPU, then its tile layout."""
+    p, cam = scene["params"], scene["camera"]
+    W, H = cam["width"], cam["height"]
+    d = {k: v.to(gpu) for k, v in p.items()}
+    with torch.no_grad():
+        pts, depths, _, conic, radii, mask, opac, colors = cr.preprocess_forward(
+            d["means"], d["log_scales"], d["quats_raw"], d["opacity_logits"], d["sh_dc"],
+            d["sh_rest"], cam["w2c"].to(gpu), cam["K"].to(gpu), cam["near"], 100.0, 1 / 255, 0.5,
+            128.0, W, H)
+        off, ids = cr.compute_tile_intersection(pts, radii, depths, mask, W, H, 16)
+    return dict(W=W, H=H, off=off, ids=ids, ins=(pts, conic, opac, colors))
+
+
+def _subset(cost, off, k, n_random, n_heavy, seed):
+    """n_random random non-empty tiles plus the n_heavy heaviest by `cost`, sorted."""
+    off = off.cpu().numpy()
+    ends = np.append(off[1:], k)
+    nonempty = np.nonzero(ends > off)[0]
+    rng = np.random.default_rng(seed)
+    heavy = np.argsort(-cost.astype(np.int64), kind="stable")[:n_heavy]
+    return sorted(set(rng.choice(nonempty, n_random, replace=False).tolist()) | set(heavy.tolist()))
+
+
+def _tile_mask(tiles, W, H):
+    tx = (W + 15) // 16
+    m = torch.zeros(H, W, dtype=torch.bool)
+    for t in tiles:
+        y0, x0 = (t // tx) * 16, (t % tx) * 16
+        m[y0:y0 + 16, x0:x0 + 16] = True
+    return m
+
+
+@pytest.fixture(scope="module")
+def config3(gpu):
+    import bench
+
+    s = _gpu_inputs(bench.config3(), gpu)
+    n_tiles = s["off"].shape[0]
+    sched = cr.tile_schedule(n_tiles, gpu)
+    with torch.no_grad():
+        image, display = cr.rasterize_display(s["off"], s["ids"], *s["ins"], s["W"], s["H"],
+                                              *BLEND_ARGS, schedule=sched)
+    cost = sched[:n_tiles].cpu().numpy().view(np.uint32)
+    s.update(image=image, display=display, sched=sched,
+             tiles=_subset(cost, s["off"], s["ids"].numel(), 200, 32, seed=3))
+    return s
+
+
+def test_config3_blend_forward_and_backward_match_oracle(gpu, config3):
+    """Image on the subset tiles, and the blend-input gradients of three seeds: the
+    image gradient (band order), the display gradient with the heavy-first
+    schedule (the drop-in render() path) and the L1 kernel's seed with the
+    schedule (the fused step; L1 weight 0 and an SSIM-style extra gradient, so
+    that its seed is the same subset gradient)."""
+    s = config3
+    W, H = s["W"], s["H"]
+    tiles = s["tiles"]
+    assert len(tiles) >= 220
+    off_c, ids_c = s["off"].cpu(), s["ids"].cpu()
+    leaves = [t.detach().cpu().clone().requires_grad_(True) for t in s["ins"]]
+    ref = blend.rasterize(off_c, ids_c, *leaves, W, H, *BLEND_ARGS, tiles=tiles)
+    m = _tile_mask(tiles, W, H)
+    img = s["image"].cpu()
+    assert helpers.max_abs(img.clamp(0, 1)[m], ref.detach().clamp(0, 1)[m]) <= IMG_TOL
+    assert helpers.max_abs(img[m], ref.detach()[m]) <= IMG_TOL
+    assert torch.equal(s["display"].cpu(), img.clamp(0, 1) * 255)
+    up = torch.randn(H, W, 3, generator=torch.Generator().manual_seed(11)) * m.unsqueeze(-1)
+    want_img = torch.autograd.grad((ref * up).sum(), leaves, retain_graph=True)
+    want_clamped = torch.autograd.grad((ref.clamp(0, 1) * up).sum(), leaves)
+    upg = up.to(gpu)
+    off, ids, ins = s["off"], s["ids"], s["ins"]
+    got_img = cr.rasterize_backward(upg, off, ids, *ins, W, H, *BLEND_ARGS,
+                                    rendered_image=s["image"])
+    got_disp = cr.rasterize_display_backward(upg / 255.0, off, ids, *ins, W, H, *BLEND_ARGS,
+                                             rendered_image=s["image"], schedule=s["sched"])
+    target = torch.rand(H, W, 3, generator=torch.Generator().manual_seed(12)).to(gpu)
+    got_l1 = cr.rasterize_l1_backward(target, torch.ones(1, device=gpu), off, ids, *ins, W, H,
+                                      s["image"], grad_display01=upg, loss_scale=0.0,
+                                      schedule=s["sched"])
+    names = ("points_image", "cov_inv_image", "opacities", "colors")
+    for got, want, seed in ((got_img, want_img, "image"), (got_disp, want_clamped, "display"),
+                            (got_l1, want_clamped, "l1")):
+        for name, a, b in zip(names, got, want):
+            assert float(b.norm()) > 0.0
+            assert helpers.rel_l2(a, b) <= GRAD_TOL, (seed, name)
+
+
+def test_config3_render_l1_matches_drop_in(gpu):
+    """The fused step (render_l1) against the drop-in step at configuration 3.
+    With the library's activations on the drop-in side too (cr.activate, whose
+    backward is cr.activate_backward) only float summation order differs:
+    loss within 1e-6, gradients within 1e-5.  With PyTorch's activations (the
+    reference's loop) the activated values differ in the last bit, which can
+    flip the sign of |display / 255 - target| at near-ties and a few chi-square
+    or alpha decisions: gradients within the 1e-3 north-star bar, and any
+    difference above 1e-5 comes with L1 sign flips between the two images."""
+    import bench
+    from cuda_rasterizer.fused import render_l1
+    from cuda_rasterizer.wrapper import render
+
+    scene = bench.config3()
+    p, cam = scene["params"], scene["camera"]
+    W, H = cam["width"], cam["height"]
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), scene["target"].to(gpu)
+    kw = dict(near_plane=cam["near"])
+    a = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
+    loss_a, disp_a, _, _ = render_l1(w2c, K, W, H, a["means"], a["log_scales"], a["quats_raw"],
+                                     a["opacity_logits"], a["sh_dc"], a["sh_rest"], tgt, **kw)
+    loss_a.backward()
+    ga = {k: t.grad for k, t in a.items()}
+
+    # drop-in with the library's activations: leaves are the activated tensors
+    raw = {k: v.to(gpu) for k, v in p.items()}
+    s, q, o = cr.activate(raw["log_scales"], raw["quats_raw"], raw["opacity_logits"])
+    b = dict(means=raw["means"].clone(), scales=s, quats=q, opac=o, sh_dc=raw["sh_dc"].clone(),
+             sh_rest=raw["sh_rest"].clone())
+    for t in b.values():
+        t.requires_grad_(True)
+    img_b, _, _ = render(w2c, K, W, H, b["means"], b["scales"], b["quats"], b["opac"],
+                         b["sh_dc"], b["sh_rest"], **kw)
+    loss_b = torch.nn.functional.l1_loss(img_b / 255.0, tgt)
+    loss_b.backward()
+    g_ls, g_q, g_l = cr.activate_backward(b["scales"].grad, b["quats"].grad, b["opac"].grad, s,
+                                          raw["quats_raw"], o)
+    gb = dict(means=b["means"].grad, log_scales=g_ls, quats_raw=g_q, opacity_logits=g_l,
+              sh_dc=b["sh_dc"].grad, sh_rest=b["sh_rest"].grad)
+    assert torch.equal(disp_a, img_b.detach())
+    assert abs(float(loss_a) - float(loss_b)) <= 1e-6 * float(loss_b)
+    for k in helpers.PARAMS:
+        assert helpers.rel_l2(ga[k], gb[k]) <= 1e-5, k
+
+    # the reference's loop: PyTorch activations, render(), l1_loss
+    c = {k: v.to(gpu).requires_grad_(True) for k, v in p.items()}
+    loss_c, img_c = bench.gpu_step(render, c, dict(cam, w2c=w2c, K=K), tgt)
+    gc = {k: t.grad for k, t in c.items()}
+    assert abs(float(loss_a) - float(loss_c)) <= 1e-5 * float(loss_c)
+    assert helpers.max_abs(disp_a / 255.0, img_c.detach() / 255.0) <= IMG_TOL
+    worst = max(helpers.rel_l2(ga[k], gc[k]) for k in helpers.PARAMS)
+    assert worst <= GRAD_TOL
+    if worst > 1e-5:
+        x_a = disp_a * (1.0 / 255.0) - tgt
+        x_c = img_c.detach() * (1.0 / 255.0) - tgt
+        assert int((torch.sign(x_a) != torch.sign(x_c)).sum()) > 0
+
+
+def test_config4_blend_forward_matches_oracle(gpu):
+    """Configuration 4 (3M Gaussians, 5% large, 64.6M keys): the forward image on
+    150 random non-empty tiles and the 16 heaviest."""
+    import bench
+
+    s = _gpu_inputs(bench.config4(), gpu)
+    W, H = s["W"], s["H"]
+    n_tiles = s["off"].shape[0]
+    sched = cr.tile_schedule(n_tiles, gpu)
+    with torch.no_grad():
+        image, _ = cr.rasterize_display(s["off"], s["ids"], *s["ins"], W, H, *BLEND_ARGS,
+                                        schedule=sched)
+    assert s["ids"].numel() > 50_000_000
+    cost = sched[:n_tiles].cpu().numpy().view(np.uint32)
+    tiles = _subset(cost, s["off"], s["ids"].numel(), 150, 16, seed=4)
+    with torch.no_grad():
+        ref = blend.rasterize(s["off"].cpu(), s["ids"].cpu(), *[t.cpu() for t in s["ins"]], W, H,
+                              *BLEND_ARGS, tiles=tiles)
+    m = _tile_mask(tiles, W, H)
+    assert helpers.max_abs(image.cpu().clamp(0, 1)[m], ref.clamp(0, 1)[m]) <= IMG_TOL
+    assert float(ref[m].abs().max()) > 0.1

@@ -151,3 +151,68 @@ def test_clone_top_and_prune_matches_oracle(gpu):
     n_pruned, n_top = d.clone_top_and_prune(params, opt, fraction=0.05, jitter=0.0)
     assert n_top == int(fresh.sum()) and n_pruned == int((torch.sigmoid(logits) < 0.005).sum())
     _check_rebuild(params, before, opt, st_before, src, fresh)
+
+
+def test_config5_training_loop_events(gpu):
+    """BASELINE configuration 5 through the library loop (render_l1 + FusedAdam +
+    Densifier, the bench's run_train "fused" path) for 300 steps: three
+    clone / prune events.  At each event every rebuilt parameter and both Adam
+    moments equal the oracle's row map (oracle.train.clone_top_rows on the
+    pre-event opacity logits and accumulated gradient norms) applied to the
+    pre-event tensors, bit for bit; the cloned means add the jitter drawn from
+    the same generator state; the sizes follow N' = kept + round(0.05 N); the
+    loss stays finite and falls."""
+    import bench
+    from cuda_rasterizer.fused import render_l1
+
+    scene = bench.config5(steps=300)
+    w2c_all = scene["w2c_per_step"].to(gpu)
+    targets = scene["targets"].to(gpu)
+    cam = scene["camera"]
+    K, W, H = cam["K"].to(gpu), cam["width"], cam["height"]
+    leaves = {k: v.to(gpu).requires_grad_(True) for k, v in scene["params"].items()}
+    opt = FusedAdam(leaves, means_decay_steps=300)
+    dens = Densifier(leaves["means"].shape[0], gpu)
+    gen = torch.Generator(device=gpu).manual_seed(0)
+    losses, sizes = [], [leaves["means"].shape[0]]
+    for step in range(300):
+        loss, _, _, _ = render_l1(w2c_all[step], K, W, H, leaves["means"], leaves["log_scales"],
+                                  leaves["quats_raw"], leaves["opacity_logits"], leaves["sh_dc"],
+                                  leaves["sh_rest"], targets[step % targets.shape[0]],
+                                  near_plane=cam["near"], densifier=dens)
+        loss.backward()
+        opt.step()
+        opt.zero_grad()
+        losses.append(float(loss.detach()))
+        if (step + 1) % 100:
+            continue
+        n = leaves["means"].shape[0]
+        before = {k: v.detach().clone() for k, v in leaves.items()}
+        m_before = {k: v.clone() for k, v in opt.exp_avg.items()}
+        v_before = {k: v.clone() for k, v in opt.exp_avg_sq.items()}
+        assert float(dens.count.max()) > 0.0
+        src, fresh = otrain.clone_top_rows(before["opacity_logits"].cpu(), dens.grads.cpu(),
+                                           fraction=0.05)
+        gen_state = gen.get_state()
+        n_pruned, n_top = dens.clone_top_and_prune(leaves, opt, 0.05, 0.01, generator=gen)
+        assert n_top == round(0.05 * n) == int(fresh.sum())
+        assert leaves["means"].shape[0] == len(src) == n - n_pruned + n_top
+        src_d, fresh_d = src.to(gpu), fresh.to(gpu)
+        jitter = torch.randn((n_top, 3), device=gpu,
+                             generator=torch.Generator(device=gpu).set_state(gen_state)) * 0.01
+        for k in PARAM_ORDER[1:] + PARAM_ORDER[:1]:  # the row map first, then the jitter
+            want = before[k][src_d]
+            if k == "means":
+                assert torch.equal(leaves[k].detach()[~fresh_d], want[~fresh_d]), k
+                want[fresh_d] = want[fresh_d] + jitter
+            assert torch.equal(leaves[k].detach(), want), k
+            for store, st in ((opt.exp_avg, m_before), (opt.exp_avg_sq, v_before)):
+                w = st[k][src_d]
+                w[fresh_d] = 0.0
+                assert torch.equal(store[k], w), k
+            assert leaves[k].requires_grad and leaves[k].is_leaf
+        assert float(dens.grads.abs().max()) == 0.0 and dens.count.shape[0] == len(src)
+        sizes.append(len(src))
+    assert len(sizes) == 4 and sizes[-1] > sizes[0]
+    assert all(x == x and abs(x) < 1e30 for x in losses)
+    assert sum(losses[-50:]) < sum(losses[:50])

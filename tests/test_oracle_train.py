@@ -66,3 +66,19 @@ def test_clone_top_rows_hand_case():
     src, fresh = otrain.clone_top_rows(logits, grads, fraction=0.5)
     assert src.tolist() == [0, 2, 3, 1, 2]  # kept 0,2,3 then the top-2 rows by gradient
     assert fresh.tolist() == [False, False, False, True, True]
+
+
+def test_clone_top_rows_ties_by_index():
+    """Equal gradient norms are taken largest first, then by ascending index (also
+    across the selection boundary), as cuda_rasterizer.train.top_rows takes them."""
+    from cuda_rasterizer.train import top_rows
+
+    logits = torch.zeros(8)
+    grads = torch.tensor([3.0, 1.0, 3.0, 2.0, 0.0, 2.0, 3.0, 0.0])
+    src, fresh = otrain.clone_top_rows(logits, grads, fraction=0.5)
+    assert src.tolist() == list(range(8)) + [0, 2, 6, 3]
+    assert fresh.tolist() == [False] * 8 + [True] * 4
+    assert top_rows(grads, 4).tolist() == [0, 2, 6, 3]
+    big = torch.randint(0, 50, (5000,), generator=torch.Generator().manual_seed(1)).float()
+    src, _ = otrain.clone_top_rows(torch.zeros(5000), big, fraction=0.05)
+    assert src[5000:].tolist() == top_rows(big, 250).tolist()
