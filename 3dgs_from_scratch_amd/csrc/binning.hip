@@ -394,11 +394,12 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
 template <typename KeyT, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
     const KeyT *__restrict__ keys, int64_t n, const int64_t *__restrict__ n_live, int shift,
-    int nbits, int nblocks, uint32_t *__restrict__ hist) {
+    int nbits, int nblocks, uint32_t *__restrict__ hist, const uint32_t *__restrict__ xform) {
     __shared__ uint32_t counts[kRadixMax];
     const int radix = 1 << nbits;
     for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
     if (n_live) n = *n_live;
+    if (xform) shift += (int)xform[1];  // digits of the bucket bits (see DepthXform)
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS];
     bool valid[ITEMS];
@@ -428,6 +429,8 @@ struct PassExtras {
     const unsigned long long *block_sums = nullptr;  // count_tiles' per-block sums,
     int64_t *sums_out = nullptr;        //   reduced to sums_out[0..1] (K, M)
     int64_t *live_out = nullptr;        //   and *live_out (keys with tiles)
+    const uint32_t *xform = nullptr;    // device DepthXform: digits shifted by its shift
+    bool sub_min = false;               //   and keys minus its minimum (written so)
 };
 
 template <typename KeyT>
@@ -445,6 +448,8 @@ struct DownArgs {
     uint64_t *counts_out;
     const uint2 *rects;
     uint2 *rects_out;
+    const uint32_t *xform;
+    int sub_min;
 };
 
 // With n_live, only the first *n_live keys are sorted, and a pass that writes
@@ -455,6 +460,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(DownArgs<
     __shared__ SortLds<ITEMS, kPayload> s;
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     const int64_t live = a.n_live ? *a.n_live : a.n;
+    const int shift = a.xform ? a.shift + (int)a.xform[1] : a.shift;
+    const uint32_t kmin = a.xform && a.sub_min ? a.xform[0] : 0u;
     uint32_t k[ITEMS], v[ITEMS];
     uint2 pay[ITEMS];
     bool valid[ITEMS];
@@ -466,8 +473,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(DownArgs<
         v[it] = in ? (a.vals_in ? a.vals_in[i] : (uint32_t)i) : 0u;
         pay[it] = (kPayload && in) ? a.pay_in[i] : make_uint2(0u, 0u);
         valid[it] = in && !(a.drop_no_tiles && k[it] == kNoTilesKey);
+        k[it] = valid[it] ? k[it] - kmin : 0u;  // kmin <= every live key
     }
-    block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, a.shift, a.nbits, a.nblocks, a.table,
+    block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, shift, a.nbits, a.nblocks, a.table,
                                          a.keys_out, a.vals_out, a.pay_out, a.n,
                                          a.write_keys != 0, s, a.totals, a.counts_out, a.rects,
                                          a.rects_out);
@@ -535,7 +543,7 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
     int st;
     if (!x.hist_ready) {
         hipLaunchKernelGGL((radix_upsweep_kernel<KeyT, ITEMS>), dim3(nblocks), dim3(kSortThreads),
-                           0, stream, kin, n, x.n_live, shift, nbits, nblocks, hist);
+                           0, stream, kin, n, x.n_live, shift, nbits, nblocks, hist, x.xform);
         st = launch_status();
         if (st) return st;
     }
@@ -563,34 +571,412 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
     a.counts_out = x.counts_out;
     a.rects = x.rects;
     a.rects_out = x.rects_out;
+    a.xform = x.xform;
+    a.sub_min = x.sub_min ? 1 : 0;
     hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, kPayload>), dim3(nblocks),
                        dim3(kSortThreads), 0, stream, a);
     return launch_status();
 }
 
+// ------------------------------------------------------- depth segment sort
+// The depth sort runs on key' = key - kmin (kmin the least key with tiles:
+// the same order and the same ties) and is two stable 8-bit passes over the 16
+// bucket bits of key' (bits shift .. shift + 15, every higher bit being 0: see
+// DepthXform), which leave the keys ordered by (bucket, Gaussian index),
+// followed by segment_sort_kernel: each workgroup takes the buckets that begin
+// in its nominal range of kSegChunk positions and sorts them by the full key,
+// stably, so that the result is ordered by (key, index) as a full 32-bit
+// stable sort is.  A chunk of at most kSegMax keys is sorted in LDS (LSD
+// passes of at most 8 bits over the bits below its highest differing bit); a
+// larger one (a bucket of more than about kSegMax - kSegChunk keys: exact ties,
+// or depths packed far more densely than elsewhere) is sorted by the same
+// workgroup through global memory.
+constexpr int kSegThreads = 256;
+constexpr int kSegWaves = kSegThreads / kWave;
+constexpr int kSegItems = 4;
+constexpr int kSegMax = kSegThreads * kSegItems;  // keys of a chunk sorted in LDS
+constexpr int kSegChunk = 512;                    // nominal positions per workgroup
+static_assert(kSegMax < 65536, "window counts are packed in 16 bits");
+
+struct SegLds {
+    uint32_t keys[2][kSegMax];
+    uint32_t vals[2][kSegMax];
+    uint32_t wave_count[kSegWaves][kRadixMax];
+    uint32_t digit_start[kRadixMax];
+    uint32_t running[kRadixMax];
+    uint32_t scan_tmp[kSegThreads / kWave + 1];
+    uint32_t red[kSegWaves];
+};
+
+// Sum (add) or bitwise OR (!add) of `x` over the workgroup (contains barriers).
+template <bool kAdd>
+__device__ __forceinline__ uint32_t seg_reduce(uint32_t x, SegLds &s) {
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        const uint32_t y = (uint32_t)__shfl_xor((int)x, o, kWave);
+        x = kAdd ? x + y : x | y;
+    }
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) s.red[threadIdx.x / kWave] = x;
+    __syncthreads();
+    uint32_t r = 0;
+#pragma unroll
+    for (int w = 0; w < kSegWaves; ++w) r = kAdd ? r + s.red[w] : r | s.red[w];
+    return r;
+}
+
+// First position q in [lo, live) whose bucket (key >> shift) exceeds b, given
+// that every position in [p0, lo) has a bucket <= b (keys[0 .. live) are
+// ordered by bucket); live when there is none.  Rounds of kSegThreads strided
+// probes, each narrowing the interval by kSegThreads.
+__device__ uint32_t bucket_end_search(const uint32_t *__restrict__ keys, uint32_t lo,
+                                      uint32_t live, int shift, uint32_t b, SegLds &s) {
+    uint32_t hi = live;  // the answer lies in [lo, hi]
+    while (lo < hi) {
+        const uint32_t len = hi - lo;
+        const uint32_t stride = (len + kSegThreads - 1) / kSegThreads;
+        const uint32_t q = lo + threadIdx.x * stride;
+        const uint32_t c = seg_reduce<true>((q < hi && (keys[q] >> shift) <= b) ? 1u : 0u, s);
+        if (c == 0) return lo;
+        if (stride == 1) return lo + c;
+        const uint32_t last_le = lo + (c - 1) * stride;  // a probe <= b
+        const uint32_t first_gt = lo + c * stride;       // a probe > b, or past hi
+        lo = last_le + 1;
+        hi = min(hi, first_gt);
+    }
+    return lo;
+}
+
+// Position of item `it` of this thread in a tile of up to kSegMax keys cut
+// into ipw items per lane: wave-major, then item, then lane, so that one load
+// instruction covers 64 consecutive positions and the order of (wave, item,
+// lane) is the position order.  A tile of `size` keys uses
+// ipw = seg_items(size), spreading it evenly over the waves.
+__device__ __forceinline__ int seg_slot(int it, int ipw) {
+    return (threadIdx.x / kWave) * (kWave * ipw) + it * kWave + (threadIdx.x % kWave);
+}
+
+__device__ __forceinline__ int seg_items(uint32_t size) {
+    return (int)((size + kSegThreads - 1) / kSegThreads);
+}
+
+// Stable LDS rank of a tile of keys -- item it of this thread at position
+// seg_slot(it, ipw), items it < ipw -- by the nbits-bit digit at `shift`
+// (nbits <= kSegDigitBits): pos[it] = the item's rank in digit order;
+// s.digit_start[d] = the first rank of digit d and digit_total (thread d) = the
+// keys of digit d.  Invalid items are ignored.  Contains barriers.
+constexpr int kSegDigitBits = kRadixMaxBits;
+
+__device__ __forceinline__ void seg_rank(const uint32_t (&k)[kSegItems],
+                                         const bool (&valid)[kSegItems], int ipw, int shift,
+                                         int nbits, uint32_t (&pos)[kSegItems], SegLds &s,
+                                         uint32_t &digit_total) {
+    const int wave = threadIdx.x / kWave;
+    const uint32_t dmask = (1u << nbits) - 1u;
+    for (int i = threadIdx.x; i < kSegWaves * kRadixMax; i += kSegThreads)
+        (&s.wave_count[0][0])[i] = 0u;
+    __syncthreads();
+    uint32_t rank[kSegItems];
+#pragma unroll
+    for (int it = 0; it < kSegItems; ++it) {
+        rank[it] = 0u;
+        if (it >= ipw) continue;  // uniform
+        const uint32_t d = digit_of(k[it], shift, dmask);
+        const uint64_t active = __ballot(valid[it]);
+        const uint64_t peers = match_digit(d, nbits, active);
+        const uint32_t before = valid[it] ? s.wave_count[wave][d] : 0u;
+        const uint32_t r = (uint32_t)__popcll(peers & lanemask_lt());
+        if (valid[it] && r == 0) s.wave_count[wave][d] = before + (uint32_t)__popcll(peers);
+        rank[it] = before + r;
+    }
+    __syncthreads();
+    // per digit (thread t = digit): prefix over the waves, then over the digits
+    uint32_t tot = 0;
+    {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int w = 0; w < kSegWaves; ++w) {
+            const uint32_t c = s.wave_count[w][t];
+            s.wave_count[w][t] = tot;
+            tot += c;
+        }
+    }
+    uint32_t all;
+    const uint32_t start = block_exclusive_scan<uint32_t, kSegThreads>(tot, s.scan_tmp, all);
+    s.digit_start[threadIdx.x] = start;
+    digit_total = tot;
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kSegItems; ++it) {
+        const uint32_t d = digit_of(k[it], shift, dmask);
+        pos[it] = s.digit_start[d] + s.wave_count[wave][d] + rank[it];
+    }
+    __syncthreads();
+}
+
+static_assert(kRadixMax == kSegThreads, "one digit per thread in seg_rank");
+static_assert(kRadixMax == kSegThreads, "one digit per thread in seg_rank");
+
+// LSD plan over the bits below the highest set bit of `diff` (the OR of every
+// key XOR the first): passes of at most kSegDigitBits bits, as few as
+// possible, of equal width.
+struct SegPlan {
+    int passes, width, bits;
+};
+
+__device__ __forceinline__ SegPlan seg_plan(uint32_t diff) {
+    SegPlan p;
+    p.bits = diff == 0 ? 0 : 32 - __clz(diff);
+    p.passes = (p.bits + kSegDigitBits - 1) / kSegDigitBits;
+    p.width = p.passes ? (p.bits + p.passes - 1) / p.passes : 0;
+    return p;
+}
+
+struct SegArgs {
+    // (a): ordered by bucket; the values end in full depth order.  The keys of
+    // (a) are never written: other workgroups search bucket boundaries in them.
+    const uint32_t *keys;
+    uint32_t *vals;
+    uint32_t *keys_b, *vals_b, *keys_c;  // scratch of the global-memory path
+    const int64_t *n_live;          // device: live keys
+    const uint32_t *xform;          // device DepthXform (the bucket shift)
+    int64_t n;                      // positions (Gaussians)
+    const uint2 *rects;             // packed tile rectangle per Gaussian
+    uint64_t *counts_out;           // general level 1: supertile count per depth position
+    uint2 *rects_out;               // one-pass level 1: rectangle per depth position
+};
+
+// Per-position outputs of the sorted order: the rectangle or the supertile
+// count of the Gaussian at depth position p (sentinels past the live keys).
+__device__ __forceinline__ void seg_emit(const SegArgs &a, int64_t p, uint32_t val) {
+    const uint2 r = val < (uint64_t)a.n ? a.rects[val] : kEmptyRect;
+    if (a.counts_out) a.counts_out[p] = rect_supertiles(r);
+    if (a.rects_out) a.rects_out[p] = r;
+}
+
+// The chunk [start, end) (more than kSegMax keys) sorted by this workgroup
+// through global memory: LSD passes over the varying digits at the chunk's
+// positions, the keys from (a) into (b) and then between (b) and (c), the
+// values between (a) and (b); the values end in (a).
+__device__ void seg_sort_global(const SegArgs &a, uint32_t start, uint32_t end, SegLds &s) {
+    const uint32_t size = end - start;
+    const uint32_t k0 = a.keys[start];
+    uint32_t diff = 0;
+    for (uint32_t t = threadIdx.x; t < size; t += kSegThreads) diff |= a.keys[start + t] ^ k0;
+    const SegPlan plan = seg_plan(seg_reduce<false>(diff, s));
+    const uint32_t *src_k = a.keys;
+    uint32_t *src_v = a.vals, *dst_k = a.keys_b, *dst_v = a.vals_b;
+    for (int p = 0; p < plan.passes; ++p) {
+        const int shift = p * plan.width;
+        const int nbits = min(plan.width, plan.bits - shift);
+        const uint32_t dmask = (1u << nbits) - 1u;
+        s.running[threadIdx.x] = 0u;
+        __syncthreads();
+        // digit histogram of the chunk
+        for (uint32_t t0 = 0; t0 < size; t0 += kSegMax) {
+            const uint32_t tsize = min((uint32_t)kSegMax, size - t0);
+            const int ipw = seg_items(tsize);
+#pragma unroll
+            for (int it = 0; it < kSegItems; ++it) {
+                if (it >= ipw) continue;  // uniform
+                const uint32_t q = (uint32_t)seg_slot(it, ipw);
+                const bool valid = q < tsize;
+                const uint32_t d = digit_of(valid ? src_k[start + t0 + q] : 0u, shift, dmask);
+                const uint64_t peers = match_digit(d, nbits, __ballot(valid));
+                if (valid && (peers & lanemask_lt()) == 0)
+                    atomicAdd(&s.running[d], (uint32_t)__popcll(peers));
+            }
+        }
+        __syncthreads();
+        uint32_t all;
+        const uint32_t first =
+            block_exclusive_scan<uint32_t, kSegThreads>(s.running[threadIdx.x], s.scan_tmp, all);
+        s.running[threadIdx.x] = first;  // next free offset of each digit
+        __syncthreads();
+        // stable scatter, tile by tile in order
+        for (uint32_t t0 = 0; t0 < size; t0 += kSegMax) {
+            const uint32_t tsize = min((uint32_t)kSegMax, size - t0);
+            const int ipw = seg_items(tsize);
+            uint32_t k[kSegItems], v[kSegItems], pos[kSegItems];
+            bool valid[kSegItems];
+#pragma unroll
+            for (int it = 0; it < kSegItems; ++it) {
+                const uint32_t q = (uint32_t)seg_slot(it, ipw);
+                valid[it] = it < ipw && q < tsize;
+                k[it] = valid[it] ? src_k[start + t0 + q] : 0u;
+                v[it] = valid[it] ? src_v[start + t0 + q] : 0u;
+            }
+            uint32_t tile_total;
+            seg_rank(k, valid, ipw, shift, nbits, pos, s, tile_total);
+            const uint32_t base_d = s.running[threadIdx.x];
+#pragma unroll
+            for (int it = 0; it < kSegItems; ++it) {
+                if (!valid[it]) continue;
+                const uint32_t d = digit_of(k[it], shift, dmask);
+                // rank within the tile's keys of digit d, after the digit's keys
+                // of the earlier tiles
+                const uint32_t dst = s.running[d] + (pos[it] - s.digit_start[d]);
+                if (dst < size) {  // always true for consistent counts; guards the store
+                    dst_k[start + dst] = k[it];
+                    dst_v[start + dst] = v[it];
+                }
+            }
+            __syncthreads();
+            s.running[threadIdx.x] = base_d + tile_total;
+            __syncthreads();
+        }
+        uint32_t *written_k = dst_k, *tv = src_v;
+        dst_k = written_k == a.keys_b ? a.keys_c : a.keys_b;
+        src_k = written_k;
+        src_v = dst_v;
+        dst_v = tv;
+        __syncthreads();
+    }
+    // the values end in (a)
+    if (src_v != a.vals)
+        for (uint32_t t = threadIdx.x; t < size; t += kSegThreads) a.vals[start + t] = src_v[start + t];
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < size; t += kSegThreads) seg_emit(a, start + t, a.vals[start + t]);
+}
+
+__global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(SegArgs a) {
+    __shared__ SegLds s;
+    const int64_t live64 = *a.n_live;
+    const uint32_t live = (uint32_t)(live64 < a.n ? live64 : a.n);
+    const uint32_t lo = (uint32_t)blockIdx.x * kSegChunk;
+    const uint32_t hi = (uint32_t)min((int64_t)lo + kSegChunk, a.n);
+    // positions past the live keys: sentinels
+    for (uint32_t p = max(lo, live) + threadIdx.x; p < hi; p += kSegThreads) {
+        a.vals[p] = 0xFFFFFFFFu;
+        seg_emit(a, p, 0xFFFFFFFFu);
+    }
+    if (lo >= live) return;  // uniform across the workgroup
+    const int shift = (int)a.xform[1];
+    // The chunk [start, end): start = the first bucket beginning at or after lo
+    // (0 for lo = 0), end = the first bucket beginning at or after hi (live
+    // past the live keys).  Both come from the window [lo, lo + wlen) loaded
+    // here, which also holds the chunk's keys unless its last bucket runs past
+    // the window; the buckets <= that of position lo - 1 (resp. hi - 1) form a
+    // prefix of the window.
+    const uint32_t wlen = min((uint32_t)kSegMax, live - lo);
+    const int wipw = seg_items(wlen);
+    const uint32_t b_lo = lo > 0 ? a.keys[lo - 1] >> shift : 0u;
+    const bool end_in = hi < live;  // else end = live
+    const uint32_t b_hi = end_in ? a.keys[hi - 1] >> shift : 0u;
+    uint32_t wk[kSegItems], wv[kSegItems];
+    uint32_t c_lo = 0, c_hi = 0;
+#pragma unroll
+    for (int it = 0; it < kSegItems; ++it) {
+        const uint32_t j = (uint32_t)seg_slot(it, wipw);
+        const bool in = it < wipw && j < wlen;
+        wk[it] = in ? a.keys[lo + j] : 0u;
+        wv[it] = in ? a.vals[lo + j] : 0u;
+        c_lo += (in && lo > 0 && (wk[it] >> shift) <= b_lo) ? 1u : 0u;
+        c_hi += (in && end_in && (wk[it] >> shift) <= b_hi) ? 1u : 0u;
+    }
+    const uint32_t packed = seg_reduce<true>(c_lo | (c_hi << 16), s);
+    c_lo = packed & 0xFFFFu;
+    c_hi = packed >> 16;
+    uint32_t start = lo + c_lo;
+    if (c_lo == wlen && lo + wlen < live)  // the bucket of lo - 1 runs past the window
+        start = bucket_end_search(a.keys, lo + wlen, live, shift, b_lo, s);
+    uint32_t end = live;
+    if (end_in) {
+        end = lo + c_hi;
+        if (c_hi == wlen && lo + wlen < live)
+            end = bucket_end_search(a.keys, lo + wlen, live, shift, b_hi, s);
+    }
+    if (start >= end) return;  // uniform: no bucket begins in this range
+    const uint32_t size = end - start;
+    if (size > (uint32_t)kSegMax) {
+        seg_sort_global(a, start, end, s);
+        return;
+    }
+    // LDS path: the chunk in buffer 0 (from the window, or loaded again when its
+    // last bucket runs past the window), then LSD passes between the buffers
+    if (end <= lo + wlen) {
+        const uint32_t off = start - lo;
+#pragma unroll
+        for (int it = 0; it < kSegItems; ++it) {
+            const uint32_t j = (uint32_t)seg_slot(it, wipw);
+            if (it < wipw && j >= off && j < off + size) {
+                s.keys[0][j - off] = wk[it];
+                s.vals[0][j - off] = wv[it];
+            }
+        }
+    } else {
+        for (uint32_t q = threadIdx.x; q < size; q += kSegThreads) {
+            s.keys[0][q] = a.keys[start + q];
+            s.vals[0][q] = a.vals[start + q];
+        }
+    }
+    __syncthreads();
+    const int ipw = seg_items(size);
+    uint32_t k[kSegItems], v[kSegItems];
+    bool valid[kSegItems];
+    uint32_t diff = 0;
+    const uint32_t k0 = s.keys[0][0];
+#pragma unroll
+    for (int it = 0; it < kSegItems; ++it) {
+        const uint32_t q = (uint32_t)seg_slot(it, ipw);
+        valid[it] = it < ipw && q < size;
+        k[it] = valid[it] ? s.keys[0][q] : 0u;
+        v[it] = valid[it] ? s.vals[0][q] : 0u;
+        diff |= valid[it] ? (k[it] ^ k0) : 0u;
+    }
+    const SegPlan plan = seg_plan(seg_reduce<false>(diff, s));
+    for (int p = 0; p < plan.passes; ++p) {
+        const int sh = p * plan.width;
+        uint32_t pos[kSegItems], total;
+        seg_rank(k, valid, ipw, sh, min(plan.width, plan.bits - sh), pos, s, total);
+        uint32_t *dk = s.keys[(p + 1) & 1], *dv = s.vals[(p + 1) & 1];
+#pragma unroll
+        for (int it = 0; it < kSegItems; ++it) {
+            if (valid[it] && pos[it] < (uint32_t)kSegMax) {
+                dk[pos[it]] = k[it];
+                dv[pos[it]] = v[it];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < kSegItems; ++it) {
+            const int q = seg_slot(it, ipw);
+            if (valid[it]) {
+                k[it] = dk[q];
+                v[it] = dv[q];
+            }
+        }
+    }
+    // sorted: item it of this thread is position seg_slot(it, ipw) of the chunk
+#pragma unroll
+    for (int it = 0; it < kSegItems; ++it) {
+        if (!valid[it]) continue;
+        const uint32_t p = start + (uint32_t)seg_slot(it, ipw);
+        a.vals[p] = v[it];
+        seg_emit(a, p, v[it]);
+    }
+}
+
 // ------------------------------------------------------------- binning
 
 // Tile rectangle and depth sort key per Gaussian (tiles_touched and the keys'
-// depth bits: src/cuda/kernel.cu:784-818), fused with the histogram of the
-// first depth-sort pass.  Gaussians without tiles get the key kNoTilesKey and
-// kEmptyRect and are left out of the histogram (the first pass drops them); so
-// is a Gaussian whose depth bits equal kNoTilesKey (a NaN), which therefore
-// gets no tiles.  block_sums[3 b + f] = the block's tiles (f = 0), supertile
-// entries (f = 1) and Gaussians with tiles (f = 2).
+// depth bits: src/cuda/kernel.cu:784-818).  Gaussians without tiles get the
+// key kNoTilesKey and kEmptyRect (the first depth pass drops them); so does a
+// Gaussian whose depth bits equal kNoTilesKey (a NaN), which therefore gets no
+// tiles.  block_sums[3 b + f] = the block's tiles (f = 0), supertile entries
+// (f = 1) and Gaussians with tiles (f = 2); block_minmax[2 b] and [2 b + 1] =
+// the least and greatest key of the block's Gaussians with tiles (0xFFFFFFFF
+// and 0 when it has none).
 template <int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int64_t n, const float *__restrict__ points_image, const float *__restrict__ radii,
     const float *__restrict__ depths, const uint8_t *__restrict__ mask, int width, int height,
-    int tile_size, uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys, int nbits,
-    int nblocks, uint32_t *__restrict__ hist, unsigned long long *__restrict__ block_sums) {
-    __shared__ uint32_t counts[kRadixMax];
+    int tile_size, uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys,
+    unsigned long long *__restrict__ block_sums, uint32_t *__restrict__ block_minmax) {
     __shared__ unsigned long long sum_tmp[kSortThreads / kWave + 1];
-    const int radix = 1 << nbits;
-    for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
+    __shared__ uint32_t mm[2][kSortThreads / kWave];
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
-    uint32_t k[ITEMS];
-    bool valid[ITEMS];
     unsigned long long my_tiles = 0, my_entries = 0, my_live = 0;
+    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
     // all loads first (clamped index, no control dependence) so they overlap
     float2 pt[ITEMS], rd[ITEMS];
     float dp[ITEMS];
@@ -607,8 +993,6 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t i = base + slot_index<ITEMS>(it);
-        valid[it] = false;
-        k[it] = kNoTilesKey;
         if (i >= n) continue;
         TileRect r{0, 0, 0, 0};
         const uint32_t bits = __float_as_uint(dp[it]);
@@ -616,26 +1000,103 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
                          tile_rect(pt[it].x, pt[it].y, rd[it].x, rd[it].y, width, height,
                                    tile_size, r);
         const uint2 packed = has ? pack_rect(r) : kEmptyRect;
-        valid[it] = has;
-        k[it] = has ? bits : kNoTilesKey;
         rects[i] = packed;
-        depth_keys[i] = k[it];
+        depth_keys[i] = has ? bits : kNoTilesKey;
         my_tiles += rect_tiles(packed);
         my_entries += rect_supertiles(packed);
         my_live += has ? 1u : 0u;
+        kmin = has ? min(kmin, bits) : kmin;
+        kmax = has ? max(kmax, bits) : kmax;
     }
     unsigned long long block_tiles, block_entries, block_live;
     block_exclusive_scan<unsigned long long, kSortThreads>(my_tiles, sum_tmp, block_tiles);
     block_exclusive_scan<unsigned long long, kSortThreads>(my_entries, sum_tmp, block_entries);
     block_exclusive_scan<unsigned long long, kSortThreads>(my_live, sum_tmp, block_live);
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, kWave));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, kWave));
+    }
+    if (threadIdx.x % kWave == 0) {
+        mm[0][threadIdx.x / kWave] = kmin;
+        mm[1][threadIdx.x / kWave] = kmax;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
         block_sums[(int64_t)blockIdx.x * 3 + 0] = block_tiles;
         block_sums[(int64_t)blockIdx.x * 3 + 1] = block_entries;
         block_sums[(int64_t)blockIdx.x * 3 + 2] = block_live;
+        uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+        for (int w = 0; w < kSortThreads / kWave; ++w) {
+            lo = min(lo, mm[0][w]);
+            hi = max(hi, mm[1][w]);
+        }
+        block_minmax[2 * (int64_t)blockIdx.x] = lo;
+        block_minmax[2 * (int64_t)blockIdx.x + 1] = hi;
     }
-    block_count_digits<ITEMS>(k, valid, 0, nbits, counts);
+}
+
+// DepthXform {kmin, shift}: the least key with tiles, and the shift that leaves
+// 16 bits of key - kmin (its bucket: bits shift .. shift + 15, with every
+// higher bit 0).  The depth passes sort by the bucket; the segment sort by the
+// rest.  Subtracting kmin keeps the order and the ties of the keys.
+__device__ __forceinline__ uint2 depth_xform(uint32_t kmin, uint32_t kmax) {
+    if (kmin > kmax) return make_uint2(0u, 0u);  // no Gaussian with tiles
+    const uint32_t range = kmax - kmin;
+    const int hb = range == 0 ? -1 : 31 - __clz(range);
+    return make_uint2(kmin, (uint32_t)max(hb - 15, 0));
+}
+
+// Upsweep of the first depth pass: every workgroup reduces count_tiles' block
+// minima and maxima to the DepthXform (workgroup 0 stores it), then counts the
+// digit (key - kmin) >> shift & 0xFF of its keys with tiles.
+template <int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void depth_upsweep0_kernel(
+    const uint32_t *__restrict__ keys, int64_t n, const uint32_t *__restrict__ block_minmax,
+    int n_count_blocks, int nblocks, uint32_t *__restrict__ hist,
+    uint32_t *__restrict__ xform) {
+    __shared__ uint32_t counts[kRadixMax];
+    __shared__ uint32_t mm[2][kSortThreads / kWave];
+    for (int d = threadIdx.x; d < kRadixMax; d += kSortThreads) counts[d] = 0;
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+    for (int b = threadIdx.x; b < n_count_blocks; b += kSortThreads) {
+        lo = min(lo, block_minmax[2 * (int64_t)b]);
+        hi = max(hi, block_minmax[2 * (int64_t)b + 1]);
+    }
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, kWave));
+        hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, kWave));
+    }
+    if (threadIdx.x % kWave == 0) {
+        mm[0][threadIdx.x / kWave] = lo;
+        mm[1][threadIdx.x / kWave] = hi;
+    }
     __syncthreads();
-    for (int d = threadIdx.x; d < radix; d += kSortThreads)
+    lo = 0xFFFFFFFFu;
+    hi = 0u;
+#pragma unroll
+    for (int w = 0; w < kSortThreads / kWave; ++w) {
+        lo = min(lo, mm[0][w]);
+        hi = max(hi, mm[1][w]);
+    }
+    const uint2 xf = depth_xform(lo, hi);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        xform[0] = xf.x;
+        xform[1] = xf.y;
+    }
+    const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
+    uint32_t k[ITEMS];
+    bool valid[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+        const int64_t i = base + slot_index<ITEMS>(it);
+        const uint32_t key = i < n ? keys[i] : kNoTilesKey;
+        valid[it] = key != kNoTilesKey;
+        k[it] = valid[it] ? key - xf.x : 0u;
+    }
+    block_count_digits<ITEMS>(k, valid, (int)xf.y, kRadixMaxBits, counts);
+    __syncthreads();
+    for (int d = threadIdx.x; d < kRadixMax; d += kSortThreads)
         hist[hist_index(d, blockIdx.x, nblocks)] = counts[d];
 }
 
@@ -1199,11 +1660,13 @@ struct Carve {
 inline int64_t l1_blocks(int64_t n) { return (n + kL1Threads - 1) / kL1Threads; }
 
 struct CountWs {
-    uint32_t *dkeys_a, *dvals_a, *dkeys_b, *dvals_b;
+    uint32_t *dkeys_a, *dvals_a, *dkeys_b, *dvals_b, *dkeys_c;
     uint2 *rects;        // packed tile rectangle per Gaussian (kEmptyRect: no tiles)
     uint2 *rects_depth;  // the same in depth order (one-pass level 1)
     uint64_t *counts, *offsets;
     unsigned long long *block_sums;  // count_tiles: 3 sums per block
+    uint32_t *block_minmax;          // count_tiles: least and greatest key per block
+    uint32_t *xform;                 // DepthXform {kmin, shift}
     int64_t *n_live;                 // Gaussians with tiles (keys of depth passes 1..)
     uint32_t *l1_hist;               // one-pass level 1: kRadixMax x l1_blocks(n) table
     uint32_t *l1_totals;             // one-pass level 1: entries per supertile
@@ -1219,10 +1682,13 @@ inline CountWs carve_count(void *base, int64_t n) {
     w.dvals_a = c.take<uint32_t>(n);
     w.dkeys_b = c.take<uint32_t>(n);
     w.dvals_b = c.take<uint32_t>(n);
+    w.dkeys_c = c.take<uint32_t>(n);
     w.rects_depth = c.take<uint2>(n);
     w.counts = c.take<uint64_t>(n);
     w.offsets = c.take<uint64_t>(n + 1);
     w.block_sums = c.take<unsigned long long>(sort_blocks<kDepthItems>(n) * 3);
+    w.block_minmax = c.take<uint32_t>(sort_blocks<kDepthItems>(n) * 2);
+    w.xform = c.take<uint32_t>(2);
     w.n_live = c.take<int64_t>(1);
     w.l1_hist = c.take<uint32_t>(kRadixMax * l1_blocks(n));
     w.l1_totals = c.take<uint32_t>(kRadixMax);
@@ -1246,10 +1712,11 @@ inline L1Args l1_args(const CountWs &cw, int64_t n, int64_t m, int super_x) {
     return la;
 }
 
-// The depth sort is 4 passes of 8 bits, so its result ends in the (a) buffers.
-// Its first pass drops keys and its last fills the tail, so they must differ.
-constexpr int kDepthBits = 32;
-static_assert(kDepthBits > kRadixMaxBits, "the depth sort needs at least two passes");
+// The depth sort: two radix passes over the bucket bits of key - kmin (bits
+// shift .. shift + 7, then shift + 8 .. shift + 15), (a) -> (b) -> (a), then
+// segment_sort_kernel in place on (a).  The first pass drops the Gaussians
+// without tiles and writes key - kmin; the segment sort fills the tail.
+constexpr int kDepthPassShift[2] = {0, 8};  // added to DepthXform's shift
 
 inline bool use_u16_keys(int tile_bits) { return tile_bits <= 16; }
 
@@ -1416,19 +1883,17 @@ bool one_pass_level1(const CountCall &c, Grid &grid) {
     return make_grid(c.width, c.height, c.tile_size, grid) && grid.n_super <= kRadixMax;
 }
 
-// Depth pass p of 4 (8 bits each): (a) -> (b) -> (a) -> (b) -> (a); the last
-// pass writes no keys.  The first pass takes the histogram count_tiles wrote,
-// numbers the values itself, drops the Gaussians without tiles and reduces
-// count_tiles' sums (K, M and the n_live Gaussians with tiles); the others sort
-// n_live keys.
-int depth_pass(const CountCall &c, const CountWs &w, int p, bool one_pass_l1,
-               hipStream_t stream) {
-    const SortPlan plan = plan_sort(kDepthBits);
-    const bool from_a = (p % 2) == 0;
-    const bool last = p + 1 == plan.passes;
+// Depth pass p of 2 over the bucket bits: (a) -> (b) -> (a).  The first pass
+// takes the histogram depth_upsweep0_kernel wrote, numbers the values itself,
+// drops the Gaussians without tiles, subtracts kmin and reduces count_tiles'
+// sums (K, M and the n_live Gaussians with tiles); the second sorts the n_live
+// keys.
+int depth_pass(const CountCall &c, const CountWs &w, int p, hipStream_t stream) {
     PassExtras x;
+    x.xform = w.xform;
     if (p == 0) {
         x.hist_ready = true;
+        x.sub_min = true;
         x.drop_no_tiles = true;
         x.block_sums = w.block_sums;
         x.sums_out = c.totals;
@@ -1436,17 +1901,11 @@ int depth_pass(const CountCall &c, const CountWs &w, int p, bool one_pass_l1,
     } else {
         x.n_live = w.n_live;
     }
-    if (last) {
-        x.rects = w.rects;
-        if (one_pass_l1)
-            x.rects_out = w.rects_depth;
-        else
-            x.counts_out = w.counts;
-    }
+    const bool from_a = p == 0;
     return radix_pass<uint32_t, kDepthItems>(
-        from_a ? w.dkeys_a : w.dkeys_b, p == 0 ? nullptr : (from_a ? w.dvals_a : w.dvals_b),
-        from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, c.n,
-        p * plan.bits_per_pass, pass_bits(plan, kDepthBits, p), !last, w.sort_ws, stream, x);
+        from_a ? w.dkeys_a : w.dkeys_b, p == 0 ? nullptr : w.dvals_b,
+        from_a ? w.dkeys_b : w.dkeys_a, from_a ? w.dvals_b : w.dvals_a, c.n, kDepthPassShift[p],
+        kRadixMaxBits, true, w.sort_ws, stream, x);
 }
 
 // Phase 1: tile rectangles, depth keys, the first depth pass; totals are final.
@@ -1455,32 +1914,48 @@ int bin_count_begin(const CountCall &c, hipStream_t stream) {
     int st = check_count_call(c, w);
     if (st) return st;
     if (c.n == 0) return zero_bytes(c.totals, 2 * sizeof(int64_t), stream);
-    const SortPlan plan = plan_sort(kDepthBits);
     const int nblocks = (int)sort_blocks<kDepthItems>(c.n);
-    const int nb0 = pass_bits(plan, kDepthBits, 0);
     uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
     hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
                        stream, c.n, c.points_image, c.radii, c.depths, c.mask, c.width, c.height,
-                       c.tile_size, w.rects, w.dkeys_a, nb0, nblocks, hist, w.block_sums);
+                       c.tile_size, w.rects, w.dkeys_a, w.block_sums, w.block_minmax);
     st = launch_status();
     if (st) return st;
-    Grid grid;
-    return depth_pass(c, w, 0, one_pass_level1(c, grid), stream);
+    hipLaunchKernelGGL((depth_upsweep0_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
+                       stream, (const uint32_t *)w.dkeys_a, c.n, (const uint32_t *)w.block_minmax,
+                       nblocks, nblocks, hist, w.xform);
+    st = launch_status();
+    if (st) return st;
+    return depth_pass(c, w, 0, stream);
 }
 
-// Phase 2: the other depth passes, then the one-pass level 1's counts and
-// positions (they need neither K nor M) or the general level 1's entry offsets.
+// Phase 2: the second depth pass and the segment sort, then the one-pass level
+// 1's counts and positions (they need neither K nor M) or the general level 1's
+// entry offsets.
 int bin_count_finish(const CountCall &c, hipStream_t stream) {
     CountWs w;
     int st = check_count_call(c, w);
     if (st || c.n == 0) return st;
     Grid grid;
     const bool one_pass_l1 = one_pass_level1(c, grid);
-    const SortPlan plan = plan_sort(kDepthBits);
-    for (int p = 1; p < plan.passes; ++p) {
-        st = depth_pass(c, w, p, one_pass_l1, stream);
-        if (st) return st;
-    }
+    st = depth_pass(c, w, 1, stream);
+    if (st) return st;
+    SegArgs sa;
+    sa.keys = w.dkeys_a;
+    sa.vals = w.dvals_a;
+    sa.keys_b = w.dkeys_b;
+    sa.vals_b = w.dvals_b;
+    sa.keys_c = w.dkeys_c;
+    sa.n_live = w.n_live;
+    sa.xform = w.xform;
+    sa.n = c.n;
+    sa.rects = w.rects;
+    sa.counts_out = one_pass_l1 ? nullptr : w.counts;
+    sa.rects_out = one_pass_l1 ? w.rects_depth : nullptr;
+    hipLaunchKernelGGL(segment_sort_kernel, dim3(ceil_div(c.n, kSegChunk)), dim3(kSegThreads), 0,
+                       stream, sa);
+    st = launch_status();
+    if (st) return st;
     if (one_pass_l1) {
         const L1Args la = l1_args(w, c.n, 0, grid.super_x);
         hipLaunchKernelGGL(l1_count_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
