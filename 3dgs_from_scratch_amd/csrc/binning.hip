@@ -57,6 +57,27 @@ constexpr int kScanTile = kScanThreads * kScanItems;
 
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
+// Workgroups are dealt to the kBinXcds XCDs round robin (workgroup w runs on
+// XCD w % kBinXcds).  xcd_block maps w to a logical block so that each XCD
+// runs a contiguous range of logical blocks, base + (x < rem) of them from
+// x * base + min(x, rem): kernels whose neighbouring blocks write neighbouring
+// positions of the same lists then fill those cache lines within one L2.  A
+// bijection of [0, nblocks).
+constexpr int kBinXcds = 8;
+
+__device__ __forceinline__ int64_t xcd_block(int64_t w, int64_t nblocks) {
+    const int64_t base = nblocks / kBinXcds, rem = nblocks % kBinXcds;
+    const int64_t x = w % kBinXcds, i = w / kBinXcds;
+    return x * base + (x < rem ? x : rem) + i;
+}
+
+// The same over the first `live` workgroups only (the ones with work: a grid
+// sized by an upper bound leaves the rest idle, and spreading those evenly
+// keeps every XCD's share of the work equal); the others map to themselves.
+__device__ __forceinline__ int64_t xcd_block_live(int64_t w, int64_t live) {
+    return w < live ? xcd_block(w, live) : w;
+}
+
 // ------------------------------------------------------------------ scan
 
 // Per-workgroup sums of kScanTile consecutive elements.
@@ -318,14 +339,14 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               const uint32_t *__restrict__ totals,
                                               uint64_t *__restrict__ counts_out,
                                               const uint2 *__restrict__ rects,
-                                              uint2 *__restrict__ rects_out) {
+                                              uint2 *__restrict__ rects_out, int blk) {
     const int radix = 1 << nbits;
     const uint32_t dmask = (uint32_t)radix - 1u;
     const int wave = threadIdx.x / kWave;
     static_assert(kRadixMax <= kSortThreads, "one digit per thread");
     const int dt = threadIdx.x;
     const uint32_t tot = dt < radix ? totals[dt] : 0u;
-    const uint32_t first = dt < radix ? table[hist_index(dt, blockIdx.x, nblocks)] : 0u;
+    const uint32_t first = dt < radix ? table[hist_index(dt, blk, nblocks)] : 0u;
     uint32_t all_keys;
     const uint32_t smaller = block_exclusive_scan<uint32_t, kSortThreads>(tot, s.scan_tmp, all_keys);
     if (dt < radix) {
@@ -458,8 +479,11 @@ struct DownArgs {
 template <typename KeyT, int ITEMS, bool kPayload>
 __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(DownArgs<KeyT> a) {
     __shared__ SortLds<ITEMS, kPayload> s;
-    const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     const int64_t live = a.n_live ? *a.n_live : a.n;
+    // neighbouring ranges on one XCD (over the workgroups with keys)
+    const int blk = (int)xcd_block_live(blockIdx.x, (live + kSortThreads * ITEMS - 1) /
+                                                        (kSortThreads * ITEMS));
+    const int64_t base = (int64_t)blk * (kSortThreads * ITEMS);
     const int shift = a.xform ? a.shift + (int)a.xform[1] : a.shift;
     const uint32_t kmin = a.xform && a.sub_min ? a.xform[0] : 0u;
     uint32_t k[ITEMS], v[ITEMS];
@@ -478,7 +502,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(DownArgs<
     block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, shift, a.nbits, a.nblocks, a.table,
                                          a.keys_out, a.vals_out, a.pay_out, a.n,
                                          a.write_keys != 0, s, a.totals, a.counts_out, a.rects,
-                                         a.rects_out);
+                                         a.rects_out, blk);
     if (a.n_live && !a.write_keys) {
         for (int t = threadIdx.x; t < kSortThreads * ITEMS; t += kSortThreads) {
             const int64_t j = base + t;
@@ -1231,8 +1255,9 @@ __device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int64
 // Block -> supertile, this lane's Gaussian and mask.  Returns false (uniformly)
 // for the blocks past the last chunk (the grid is sized by an upper bound).
 __device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x) {
-    x.b = blockIdx.x;
-    if (x.b >= a.chunk_start[a.n_super]) return false;
+    const uint32_t chunks = a.chunk_start[a.n_super];
+    x.b = (uint32_t)xcd_block_live(blockIdx.x, chunks);
+    if (x.b >= chunks) return false;
     const uint2 map = a.block_map[x.b];
     x.s = (int)map.x;
     const int64_t end = x.s + 1 < a.n_super ? a.super_off[x.s + 1] : a.m;
@@ -1473,15 +1498,20 @@ struct L1Args {
 
 // Whether this workgroup's positions start before *n_live (the later ones hold
 // only the sentinels of Gaussians without tiles); uniform per workgroup.
-__device__ __forceinline__ bool l1_live_block(const L1Args &a) {
-    return (int64_t)blockIdx.x * kL1Threads < *a.n_live;
+__device__ __forceinline__ bool l1_live_block(const L1Args &a, int64_t blk) {
+    return blk * kL1Threads < *a.n_live;
+}
+
+// Workgroups whose positions start before *n_live.
+__device__ __forceinline__ int64_t l1_live_blocks(const L1Args &a) {
+    return (*a.n_live + kL1Threads - 1) / kL1Threads;
 }
 
 // This thread's Gaussian and the supertile range its tile rectangle meets
 // (false: none).
-__device__ __forceinline__ bool l1_gaussian(const L1Args &a, uint32_t &g, uint2 &packed,
-                                            TileRect &sr) {
-    const int64_t r = (int64_t)blockIdx.x * kL1Threads + threadIdx.x;
+__device__ __forceinline__ bool l1_gaussian(const L1Args &a, int64_t blk, uint32_t &g,
+                                            uint2 &packed, TileRect &sr) {
+    const int64_t r = blk * kL1Threads + threadIdx.x;
     if (r >= a.n) return false;
     g = a.order[r];
     packed = a.rects_depth[r];
@@ -1495,13 +1525,14 @@ __device__ __forceinline__ bool l1_gaussian(const L1Args &a, uint32_t &g, uint2 
 }
 
 // lanes[w][s] for the block (zeroed here); returns whether this lane has entries.
-__device__ __forceinline__ bool l1_lane_masks(const L1Args &a, uint64_t (*lanes)[kRadixMax],
-                                              uint32_t &g, uint2 &packed, TileRect &sr) {
+__device__ __forceinline__ bool l1_lane_masks(const L1Args &a, int64_t blk,
+                                              uint64_t (*lanes)[kRadixMax], uint32_t &g,
+                                              uint2 &packed, TileRect &sr) {
     for (int i = threadIdx.x; i < kL1Waves * kRadixMax; i += kL1Threads) lanes[0][i] = 0ull;
     __syncthreads();
     const int wave = threadIdx.x / kWave;
     const uint64_t bit = 1ull << (threadIdx.x % kWave);
-    const bool has = l1_gaussian(a, g, packed, sr);
+    const bool has = l1_gaussian(a, blk, g, packed, sr);
     if (has)
         for (int y = sr.ty0; y <= sr.ty1; ++y)
             for (int x = sr.tx0; x <= sr.tx1; ++x)
@@ -1515,19 +1546,20 @@ __device__ __forceinline__ bool l1_lane_masks(const L1Args &a, uint64_t (*lanes)
 __global__ __launch_bounds__(kL1Threads) void l1_count_kernel(L1Args a,
                                                               uint32_t *__restrict__ hist) {
     __shared__ uint64_t lanes[kL1Waves][kRadixMax];
-    if (!l1_live_block(a)) {  // no entries: a zero histogram column
-        if (threadIdx.x < kRadixMax) hist[hist_index(threadIdx.x, blockIdx.x, a.nblocks)] = 0u;
+    const int64_t blk = xcd_block_live(blockIdx.x, l1_live_blocks(a));
+    if (!l1_live_block(a, blk)) {  // no entries: a zero histogram column
+        if (threadIdx.x < kRadixMax) hist[hist_index(threadIdx.x, (int)blk, a.nblocks)] = 0u;
         return;
     }
     uint32_t g;
     uint2 packed;
     TileRect sr;
-    l1_lane_masks(a, lanes, g, packed, sr);
+    l1_lane_masks(a, blk, lanes, g, packed, sr);
     if (threadIdx.x < kRadixMax) {
         uint32_t c = 0;
 #pragma unroll
         for (int w = 0; w < kL1Waves; ++w) c += (uint32_t)__popcll(lanes[w][threadIdx.x]);
-        hist[hist_index(threadIdx.x, blockIdx.x, a.nblocks)] = c;
+        hist[hist_index(threadIdx.x, (int)blk, a.nblocks)] = c;
     }
 }
 
@@ -1583,23 +1615,24 @@ __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
     for (int64_t t = (int64_t)blockIdx.x * kL1Threads + threadIdx.x; t < n_tiles;
          t += (int64_t)gridDim.x * kL1Threads)
         tile_counts[t] = 0u;
-    if (blockIdx.x != 0 && !l1_live_block(a)) return;  // no entries (block 0 writes the plan)
+    const int64_t blk = blockIdx.x;  // (round robin over the XCDs measured faster here)
+    if (blk != 0 && !l1_live_block(a, blk)) return;  // no entries (block 0 writes the plan)
     uint32_t g = 0;
     uint2 packed = make_uint2(0u, 0u);
     TileRect sr{0, -1, 0, -1};
-    const bool has = l1_lane_masks(a, lanes, g, packed, sr);
+    const bool has = l1_lane_masks(a, blk, lanes, g, packed, sr);
     const int d = threadIdx.x;
     const uint32_t tot = d < n_super ? totals[d] : 0u;
     uint32_t all;
     const uint32_t smaller = block_exclusive_scan<uint32_t, kL1Threads>(tot, scan_tmp, all);
-    if (blockIdx.x == 0) {  // uniform per workgroup; wave_pos serves as staging
+    if (blk == 0) {  // uniform per workgroup; wave_pos serves as staging
         if (d < n_super) super_off[d] = (int32_t)smaller;
         l1_block_plan(n_super, tot, smaller, scan_tmp, wave_pos[0], wave_pos[1], chunk_start,
                       block_map);
         __syncthreads();
     }
     if (d < kRadixMax) {
-        uint32_t pos = smaller + (d < n_super ? hist[hist_index(d, blockIdx.x, a.nblocks)] : 0u);
+        uint32_t pos = smaller + (d < n_super ? hist[hist_index(d, (int)blk, a.nblocks)] : 0u);
 #pragma unroll
         for (int w = 0; w < kL1Waves; ++w) {
             wave_pos[w][d] = pos;

@@ -344,6 +344,66 @@ def run_ssim(scene: dict, steps: int, warmup: int) -> dict:
     return out
 
 
+def run_cameras(scene: dict, steps: int, warmup: int) -> dict:
+    """Configuration 2: one iteration is the fused step (render_l1) on every one
+    of the scene's cameras against its own target, the loss being the mean of
+    the per-camera L1 terms, so the parameter gradients accumulate over the
+    cameras.  Wall clock over `steps` iterations, synchronised on both sides."""
+    from cuda_rasterizer.fused import render_l1
+
+    dev = torch.device("cuda:0")
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in scene["params"].items()}
+    cams = [dict(c, w2c=c["w2c"].to(dev), K=c["K"].to(dev)) for c in scene["cameras"]]
+    targets = [t.to(dev) for t in scene["targets"]]
+    weight = 1.0 / len(cams)
+
+    def step():
+        for t in leaves.values():
+            t.grad = None
+        total = 0.0
+        for cam, target in zip(cams, targets):
+            loss, _, _, _ = render_l1(cam["w2c"], cam["K"], cam["width"], cam["height"],
+                                      leaves["means"], leaves["log_scales"], leaves["quats_raw"],
+                                      leaves["opacity_logits"], leaves["sh_dc"], leaves["sh_rest"],
+                                      target, near_plane=cam["near"])
+            (loss * weight).backward()
+            total = total + loss.detach() * weight
+        return total
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    n = scene["params"]["means"].shape[0]
+    return {"ms_per_step": round(ms, 4), "cameras": len(cams),
+            "gaussians_per_s": round(n / (ms * 1e-3), 1), "loss": round(float(loss), 6)}
+
+
+def run_small_configs(steps: int, warmup: int, cpu: bool) -> dict:
+    """Configurations 1 and 2 on the GPU (fused fwd+bwd; configuration 2 over its 8
+    cameras) and, with `cpu`, the oracle on the host CPU over the whole of each
+    workload (configuration 2: its first camera)."""
+    out = {}
+    s1 = config1()
+    r = run_gpu(s1, steps, warmup, "fused")
+    out["config1"] = {"workload": f"{r['n']} Gaussians SH0 {r['width']}x{r['height']} fwd+bwd L1",
+                      "ms_per_step": round(r["ms"], 4), "keys": r["keys"],
+                      "gaussians_per_s": round(r["n"] / (r["ms"] * 1e-3), 1)}
+    s2 = config2()
+    c2 = run_cameras(s2, steps, warmup)
+    out["config2"] = dict(workload=f"{s2['params']['means'].shape[0]} Gaussians SH3 800x800 "
+                                   f"fwd+bwd L1 over {c2['cameras']} cameras", **c2)
+    if cpu:
+        out["config1"]["cpu_baseline"] = cpu_baseline(s1, budget_s=float("inf"))
+        out["config2"]["cpu_baseline"] = cpu_baseline(s2, budget_s=float("inf"))
+        out["config2"]["cpu_baseline"]["sample"] += " (first camera only)"
+    return out
+
+
 def run_forward(scene: dict, steps: int, warmup: int) -> dict:
     """Configuration 4: forward-only render() (no autograd) of the scene, with
     HIP events around every entry point.  Reports the binning's keys per second
@@ -675,6 +735,40 @@ def roofline(res: dict, workload: str) -> dict:
     return dict(dominant=dominant, roofline=main, hbm_stages=hbm, per_stage=per_stage)
 
 
+def step_roofline(res: dict, workload: str) -> dict | None:
+    """Speed-of-light fraction of the whole fused step.  Every kernel one step
+    launches -- launches per step and HBM bytes per launch from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE profile of the same step
+    (profiles/hbm_traffic_<workload>.md, lines `step_kernel[<kernel>]:
+    <launches per step> <bytes per launch>`) -- is priced at its bound: its bytes
+    at the HBM peak, and for the two blend kernels the larger of that and their
+    flops (evaluated pairs x flop per pair) at the fp32 peak.  The sum of the
+    bound times over the measured ms per step; None without the profile."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.md")
+    if not os.path.exists(path):
+        return None
+    rows = re.findall(r"^step_kernel\[(.+?)\]:\s*([0-9.eE+]+)\s+([0-9.eE+]+)\s*$",
+                      open(path).read(), re.M)
+    if not rows:
+        return None
+    flop = {"blend_forward_kernel": BLEND_FLOP_PER_PAIR["rasterize_display_l1"],
+            "blend_backward_kernel<2>": BLEND_FLOP_PER_PAIR["rasterize_l1_backward"]}
+    bound_s, hbm_s, valu_s = 0.0, 0.0, 0.0
+    for name, launches, nbytes in rows:
+        t_hbm = float(nbytes) / (HBM_PEAK_GBS * 1e9)
+        t_valu = res["visited"] * flop[name] / (FP32_PEAK_TFLOPS * 1e12) if name in flop else 0.0
+        bound_s += float(launches) * max(t_hbm, t_valu)
+        hbm_s += float(launches) * t_hbm
+        valu_s += float(launches) * t_valu
+    step_s = res["ms"] * 1e-3
+    return dict(frac=round(bound_s / step_s, 4), bound_ms=round(bound_s * 1e3, 4),
+                hbm_ms=round(hbm_s * 1e3, 4), valu_ms=round(valu_s * 1e3, 4),
+                ms_per_step=round(res["ms"], 4), kernels=len(rows),
+                source=os.path.relpath(path, ROOT))
+
+
 # -------------------------------------------------------------- CPU leg
 
 def cpu_baseline(scene: dict, budget_s: float = 12.0, batch_tiles: int = 128, seed: int = 0) -> dict:
@@ -694,7 +788,9 @@ def cpu_baseline(scene: dict, budget_s: float = 12.0, batch_tiles: int = 128, se
     from oracle import blend
     from oracle import render as orender
 
-    torch.set_num_threads(max(1, os.cpu_count() or 1))
+    # the host's CPU share when the environment states it (OMP_NUM_THREADS), else every core
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+                              or os.cpu_count() or 1))
     leaves = {k: v.clone().requires_grad_(True) for k, v in scene["params"].items()}
     cam = scene["camera"]
     W, H = cam["width"], cam["height"]
@@ -748,6 +844,23 @@ def cpu_model() -> str:
 
 # ------------------------------------------------------------------- main
 
+def profile_step(scene: dict, steps: int) -> int:
+    """`steps` fused steps and nothing else on the GPU after the inputs are copied
+    (the copies are the only other dispatches), so that a rocprofv3 run's
+    dispatch counts divided by `steps` are launches per step."""
+    dev = torch.device("cuda:0")
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in scene["params"].items()}
+    cam = dict(scene["camera"], w2c=scene["camera"]["w2c"].to(dev), K=scene["camera"]["K"].to(dev))
+    target = scene["target"].to(dev)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        loss, _ = fused_step(leaves, cam, target)
+    torch.cuda.synchronize()
+    print(json.dumps({"profiled_steps": steps, "workload": scene["name"],
+                      "loss": round(float(loss.detach()), 6)}), flush=True)
+    return 0
+
+
 def copy_calibration(mib: int) -> int:
     """A plain device copy of known size: under rocprofv3 --pmc its FETCH_SIZE and
     WRITE_SIZE per dispatch give the counters' scale (expected: mib * 1024 KiB each)."""
@@ -765,9 +878,14 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=[1, 3, 4, 5],
-                    help="3 (headline, default) or 1; 4 prints only the forward-only sort and "
-                         "blend rates, 5 only the training stress run")
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5],
+                    help="3 (headline, default) or 1; 2 prints only the 8-camera step, 4 only "
+                         "the forward-only sort and blend rates, 5 only the training stress run")
+    ap.add_argument("--profile-step", action="store_true",
+                    help="only run warmup + steps fused steps of the chosen configuration (for "
+                         "rocprofv3: every dispatch then belongs to a step) and print the count")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip configurations 1, 2 and 4 beside the headline")
     ap.add_argument("--path", choices=["fused", "drop-in"], default="fused",
                     help="the timed step: fused render_l1 (default) or PyTorch glue around render()")
     ap.add_argument("--no-drop-in", action="store_true",
@@ -803,8 +921,13 @@ def main(argv=None):
     if args.config == 4:
         print(json.dumps(run_forward(CONFIGS[4](), args.steps, args.warmup)), flush=True)
         return 0
+    if args.config == 2:
+        print(json.dumps(run_cameras(CONFIGS[2](), args.steps, args.warmup)), flush=True)
+        return 0
 
     scene = CONFIGS[args.config]()
+    if args.profile_step:
+        return profile_step(scene, args.steps + args.warmup)
     res = run_gpu(scene, args.steps, args.warmup, args.path)
     rl = roofline(res, scene["name"])
     drop_in = None
@@ -818,6 +941,10 @@ def main(argv=None):
     train = None
     if not args.no_train and args.path == "fused":
         train = train_stress(args.train_steps, args.train_path)
+    configs = None
+    if not args.no_configs and args.config == 3:
+        configs = run_small_configs(args.steps, args.warmup, not args.no_cpu_baseline)
+        configs["config4"] = run_forward(config4(), args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(scene, args.cpu_budget)
@@ -840,6 +967,7 @@ def main(argv=None):
                    "keys": res["keys"], "resolution": [res["width"], res["height"]]},
         "gaussians_per_s": round(res["n"] / (res["ms"] * 1e-3), 1),
         "roofline": rl["roofline"],
+        "step_roofline": step_roofline(res, scene["name"]) if args.path == "fused" else None,
         "hbm_stages": rl["hbm_stages"],
         "blend_pairs": {"visited": res["visited"], "composited": res["composited"]},
         "stages": rl["per_stage"],
@@ -847,6 +975,7 @@ def main(argv=None):
         "drop_in": drop_in,
         "ssim": ssim,
         "train_stress": train,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
