@@ -15,8 +15,9 @@
 // input window of both images in LDS (any element strides: the reference hands
 // (H, W, C) images permuted to (1, C, H, W)), filters rows (each thread 4
 // consecutive outputs of a row, so every staged value is loaded and squared
-// once per thread), stores the five row sums, then filters columns (lane =
-// column, each wave 8 output rows); the next tile's window is loaded meanwhile.
+// once per thread), stores the four row sums (x, y, x^2 + y^2, xy), then
+// filters columns (lane = column, each wave 8 output rows); the next tile's
+// window is loaded meanwhile.
 // The forward writes per-pixel derivative maps (planar, coalesced) for the
 // backward, which filters them back the same way.  The mean is reduced
 // deterministically: per-workgroup double partials, then one workgroup.
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
                                                                  float *__restrict__ d_xy,
                                                                  double *__restrict__ partials) {
     __shared__ float stage[2][kInY][kPitch];  // x, y
-    __shared__ __align__(16) float rows[5][kInY][kTileX];
+    __shared__ __align__(16) float rows[4][kInY][kTileX];
     __shared__ double red[kWaves];
     float v[2][kStageIters];
     int t0, t1;
@@ -278,18 +279,18 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
         store_stage<2>(stage, v);
         __syncthreads();
         if (t + 1 < t1) load_images(p, tile_of(p, t + 1), v[0], v[1]);
-        // row sums of x, y, x^2, y^2, xy
-        row_pass<5>(win, rows, [&](int r, int col, float (&u)[5]) {
+        // row sums of x, y, x^2 + y^2, xy (only the sum of the second moments
+        // enters the SSIM, and its derivative is the same for E[x^2] and E[y^2])
+        row_pass<4>(win, rows, [&](int r, int col, float (&u)[4]) {
             const float x = stage[0][r][col], y = stage[1][r][col];
             u[0] = x;
             u[1] = y;
-            u[2] = x * x;
-            u[3] = y * y;
-            u[4] = x * y;
+            u[2] = x * x + y * y;
+            u[3] = x * y;
         });
         __syncthreads();
-        float acc[5][kRowsPerWave];
-        column_pass<5>(win, rows, r0, acc);
+        float acc[4][kRowsPerWave];
+        column_pass<4>(win, rows, r0, acc);
         const int gx = tl.ox + (int)(threadIdx.x % kWave);
         const int64_t plane_base = (int64_t)tl.plane * p.height * p.width;
 #pragma unroll
@@ -297,13 +298,12 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
             const int gy = tl.oy + r0 + o;
             if (gy >= p.height || gx >= p.width) continue;
             const float mu1 = acc[0][o], mu2 = acc[1][o];
-            const float s11 = acc[2][o] - mu1 * mu1;
-            const float s22 = acc[3][o] - mu2 * mu2;
-            const float s12 = acc[4][o] - mu1 * mu2;
+            const float s_sum = acc[2][o] - mu1 * mu1 - mu2 * mu2;  // sigma1^2 + sigma2^2
+            const float s12 = acc[3][o] - mu1 * mu2;
             const float C = 2.0f * mu1 * mu2 + kC1;
             const float D = 2.0f * s12 + kC2;
             const float A = mu1 * mu1 + mu2 * mu2 + kC1;
-            const float B = s11 + s22 + kC2;
+            const float B = s_sum + kC2;
             const float rA = __builtin_amdgcn_rcpf(A), rB = __builtin_amdgcn_rcpf(B);
             const float rAB = rA * rB;
             const float S = C * D * rAB;
