@@ -579,7 +579,7 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image,
     float *__restrict__ display, const float *__restrict__ target,
     float *__restrict__ tile_loss, float4 *__restrict__ clear4, int64_t clear4_count,
-    uint32_t *__restrict__ tile_cost) {
+    uint32_t *__restrict__ tile_cost, const int32_t *__restrict__ tile_order) {
     __shared__ BatchLds s;
     if (clear4) {  // this workgroup's share of the buffer to zero (stores overlap the blend)
         const int64_t per = (clear4_count + gridDim.x - 1) / gridDim.x;
@@ -588,7 +588,11 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
         for (int64_t c = c0 + threadIdx.x; c < c1; c += kWave)
             clear4[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const int tile = tile_of_block(blockIdx.x, n_tiles);
+    // launch position -> tile: the XCD's contiguous range, in the caller's order
+    // when given (a permutation of every range, e.g. heaviest first)
+    const int slot = tile_of_block(blockIdx.x, n_tiles);
+    const int tile = tile_order ? tile_order[slot] : slot;
+    if ((unsigned)tile >= (unsigned)n_tiles) return;  // uniform across the workgroup
     const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
     float cr[kStrips], cg[kStrips], cb[kStrips];
@@ -1049,7 +1053,7 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                           float chi_squared_threshold, float *image, float *display,
                           const float *target, float *tile_loss, hipStream_t stream,
                           float *clear = nullptr, int64_t clear_count = 0,
-                          uint32_t *tile_cost = nullptr) {
+                          uint32_t *tile_cost = nullptr, const int32_t *tile_order = nullptr) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -1085,7 +1089,7 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
                            image, display, target, tile_loss,
                            fused_clear ? reinterpret_cast<float4 *>(clear) : nullptr,
-                           fused_clear ? clear_count / 4 : (int64_t)0, tile_cost);
+                           fused_clear ? clear_count / 4 : (int64_t)0, tile_cost, tile_order);
     } else {
         hipLaunchKernelGGL(blend_forward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, indexing_offset,
@@ -1139,7 +1143,8 @@ extern "C" int gs_rasterize_display_l1(
     const float *colors, int64_t n, int32_t width, int32_t height, int32_t tile_size,
     float alpha_threshold, float transmittance_threshold, float chi_squared_threshold,
     const float *target, float *image, float *display, float *tile_loss, float *loss,
-    int32_t *tile_schedule, float *clear, int64_t clear_count, hipStream_t stream) {
+    int32_t *tile_schedule, float *clear, int64_t clear_count, const int32_t *forward_order,
+    hipStream_t stream) {
     if (!display || !target || !tile_loss || tile_size != kTile) return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     const int tiles_y = (height + tile_size - 1) / tile_size;
@@ -1148,7 +1153,8 @@ extern "C" int gs_rasterize_display_l1(
     int st = rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
                             cov_inv_image, opacities, colors, n, width, height, tile_size,
                             alpha_threshold, transmittance_threshold, chi_squared_threshold,
-                            image, display, target, tile_loss, stream, clear, clear_count, cost);
+                            image, display, target, tile_loss, stream, clear, clear_count, cost,
+                            forward_order);
     if (st) return st;
     // the loss (when asked for) and the backward's tile order, in one launch
     const double count = (double)width * (double)height * 3.0;

@@ -741,13 +741,15 @@ def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, g
 def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
                          opacities, colors, width, height, target, alpha_threshold=1e-4,
                          transmittance_threshold=1e-4, chi_squared_threshold=9.21, clear=None,
-                         schedule=None):
+                         schedule=None, forward_schedule=None):
     """rasterize_display with tile size 16 plus loss = mean(|display / 255 - target|).
     Returns (image, display, loss[1] fp32).  `clear` (an fp32 device tensor, e.g.
     from blend_grad_accumulators) is zeroed by the same launch.  `schedule` (an
     int32 device tensor of 2 * n_tiles, see tile_schedule) receives the work per
     tile and the order in which rasterize_l1_backward, given it, launches the
-    tiles (heaviest first)."""
+    tiles (heaviest first).  `forward_schedule`: a schedule an earlier call filled
+    for the same image size (not this call's `schedule`); this forward then
+    launches its tiles in that order (results do not depend on it)."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -760,6 +762,13 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
     loss = torch.empty((1,), dtype=f32, device=dev)
     if schedule is not None:
         _check_schedule(schedule, n_tiles, dev, "rasterize_display_l1")
+    fwd_order = None
+    if forward_schedule is not None:
+        _check_schedule(forward_schedule, n_tiles, dev, "rasterize_display_l1")
+        if schedule is not None and forward_schedule.data_ptr() == schedule.data_ptr():
+            raise RasterizerError("rasterize_display_l1: forward_schedule must be an earlier "
+                                  "call's schedule, not the one this call writes")
+        fwd_order = forward_schedule[n_tiles:]
     lib = _lib.load()
     with torch.cuda.device(dev):
         ev = _lib.timer.record("rasterize_display_l1", dev)
@@ -768,7 +777,7 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
             _ptr(col), n, width, height, 16, float(alpha_threshold), float(transmittance_threshold),
             float(chi_squared_threshold), _ptr(target), _ptr(image), _ptr(display), _ptr(tile_loss),
             _ptr(loss), _ptr(schedule), _ptr(clear), 0 if clear is None else clear.numel(),
-            _stream(dev)), "rasterize_display_l1")
+            _ptr(fwd_order), _stream(dev)), "rasterize_display_l1")
         _lib.timer.stop(ev, dev)
     return image, display, loss
 

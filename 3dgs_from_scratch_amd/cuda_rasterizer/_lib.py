@@ -38,7 +38,7 @@ SIGNATURES = {
     "gs_preprocess_backward": [_P] * 14 + [_I64, _I32, _I32] + [_P] * 6 + [_P],
     "gs_activate_backward": [_P] * 6 + [_I64] + [_P] * 3 + [_P],
     "gs_rasterize_display_l1": [_P, _P, _I32, _I64] + [_P] * 4
-    + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 7 + [_I64, _P],
+    + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 7 + [_I64, _P, _P],
     "gs_l1_finish": [_P, _I32, _I64, _P, _P],
     "gs_rasterize_l1_backward": [_P] * 5 + [_I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 4 + [_I32, _F, _P, _P, _P],

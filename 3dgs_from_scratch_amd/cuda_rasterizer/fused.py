@@ -46,7 +46,8 @@ class RenderL1Function(torch.autograd.Function):
     def forward(ctx, means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
                 world_to_camera, intrinsic, target, densifier, width, height, near_plane,
                 far_plane, min_opacity, min_radius, max_radius, alpha_threshold,
-                transmittance_threshold, chi_squared_threshold, ssim_lambda, ssim_padding):
+                transmittance_threshold, chi_squared_threshold, ssim_lambda, ssim_padding,
+                schedule_cache, view_id):
         pts, depths, cov, conic, radii, mask, opac, colors = _cr.preprocess_forward(
             means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
@@ -56,9 +57,19 @@ class RenderL1Function(torch.autograd.Function):
         acc = _cr.blend_grad_accumulators(means.shape[0], means.device)
         # the forward's work per tile orders the backward's tiles (heaviest first)
         sched = _cr.tile_schedule(off.shape[0], means.device)
+        # and, kept per view, the next forward of the same view
+        previous = None
+        if schedule_cache is not None and view_id is not None:
+            previous = schedule_cache.get(view_id)
+            if (previous is not None and (previous.device != means.device
+                                          or previous.numel() != sched.numel())):
+                previous = None
         image, display, loss = _cr.rasterize_display_l1(
             off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
-            transmittance_threshold, chi_squared_threshold, clear=acc, schedule=sched)
+            transmittance_threshold, chi_squared_threshold, clear=acc, schedule=sched,
+            forward_schedule=previous)
+        if schedule_cache is not None and view_id is not None:
+            schedule_cache[view_id] = sched
         ssim_saved = ()
         if ssim_lambda > 0.0:
             # SSIM of the reference's rendered_image / 255 (its render() returns the
@@ -90,7 +101,7 @@ class RenderL1Function(torch.autograd.Function):
          mask, colors, off, ids, image, acc, sched) = saved[:20]
         width, height, a_thr, t_thr, chi = ctx.params
         if grad_loss is None:
-            return (None,) * 22
+            return (None,) * 24
         g = grad_loss.reshape(1).to(torch.float32)
         lam = ctx.ssim_lambda
         extra = None
@@ -112,14 +123,15 @@ class RenderL1Function(torch.autograd.Function):
         g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(
             g_pts, g_conic, g_opac, g_col, means, log_scales, quats_raw, logits, dc, rest, cov,
             mask, w2c, K, width, height)
-        return (g_means, g_ls, g_qr, g_logit, g_dc, g_rest) + (None,) * 16
+        return (g_means, g_ls, g_qr, g_logit, g_dc, g_rest) + (None,) * 18
 
 
 def render_l1(world_to_camera, intrinsic, width, height, means, log_scales, quats_raw,
               opacity_logits, sh_coeffs_dc, sh_coeffs_rest, target, near_plane=0.01,
               far_plane=100.0, min_opacity=1 / 255, min_radius=0.5, max_radius=128.0,
               alpha_threshold=1e-4, transmittance_threshold=1e-4, chi_squared_threshold=9.21,
-              densifier=None, ssim_lambda=0.0, ssim_padding="valid"):
+              densifier=None, ssim_lambda=0.0, ssim_padding="valid", schedule_cache=None,
+              view_id=None):
     """loss = l1_loss(render(...activations of the raw parameters...)[0] / 255, target),
     or with ssim_lambda > 0, (1 - ssim_lambda) * that + ssim_lambda * (1 - SSIM).
 
@@ -127,10 +139,18 @@ def render_l1(world_to_camera, intrinsic, width, height, means, log_scales, quat
     (log-scales, un-normalised xyzw quaternions, opacity logits); SH colours use
     max(c + 0.5, 0) (render's default).  Returns (loss, display[H,W,3] in
     [0,255], points_img[N,2], radii[N,2]).
+
+    schedule_cache / view_id: a training loop over a fixed set of views (the
+    reference's, scripts/train.py:84,146) can pass a dict and the view's key; each
+    step then stores its per-tile work there, and the next step of the same view
+    launches its forward tiles heaviest first by it (the backward always uses the
+    step's own).  Only the launch order changes: the results are the same with
+    or without it.
     """
     return RenderL1Function.apply(
         means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
         world_to_camera, intrinsic, target, densifier, int(width), int(height),
         float(near_plane), float(far_plane), float(min_opacity), float(min_radius),
         float(max_radius), float(alpha_threshold), float(transmittance_threshold),
-        float(chi_squared_threshold), float(ssim_lambda), str(ssim_padding))
+        float(chi_squared_threshold), float(ssim_lambda), str(ssim_padding), schedule_cache,
+        view_id)

@@ -200,10 +200,12 @@ def gpu_step(render, leaves: dict, cam: dict, target: torch.Tensor):
     return loss, image
 
 
-def fused_step(leaves: dict, cam: dict, target: torch.Tensor, ssim_lambda: float = 0.0):
+def fused_step(leaves: dict, cam: dict, target: torch.Tensor, ssim_lambda: float = 0.0,
+               schedule_cache: dict | None = None):
     """The same step through cuda_rasterizer.fused.render_l1 (activations, render and
     L1 loss -- plus the SSIM term with ssim_lambda > 0 -- as one autograd node of
-    library kernels)."""
+    library kernels).  With `schedule_cache`, the step passes it with the scene's
+    one view id (a training loop revisiting the view)."""
     from cuda_rasterizer.fused import render_l1
 
     for t in leaves.values():
@@ -211,14 +213,19 @@ def fused_step(leaves: dict, cam: dict, target: torch.Tensor, ssim_lambda: float
     loss, image, _, _ = render_l1(cam["w2c"], cam["K"], cam["width"], cam["height"],
                                   leaves["means"], leaves["log_scales"], leaves["quats_raw"],
                                   leaves["opacity_logits"], leaves["sh_dc"], leaves["sh_rest"],
-                                  target, near_plane=cam["near"], ssim_lambda=ssim_lambda)
+                                  target, near_plane=cam["near"], ssim_lambda=ssim_lambda,
+                                  schedule_cache=schedule_cache,
+                                  view_id=None if schedule_cache is None else "view0")
     loss.backward()
     return loss, image
 
 
-def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused") -> dict:
+def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
+            schedule_cache: bool = False) -> dict:
     """Times `steps` steps after `warmup`; path "fused" (fused_step) or "drop-in"
-    (gpu_step: PyTorch activations and loss around the drop-in render())."""
+    (gpu_step: PyTorch activations and loss around the drop-in render()).
+    schedule_cache: the fused step with a per-view schedule cache (the view
+    repeats every step, as a training view does every epoch)."""
     from cuda_rasterizer import _lib
     from cuda_rasterizer.wrapper import render
 
@@ -228,8 +235,9 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused") -> dict:
     cam["w2c"] = cam["w2c"].to(dev)
     cam["K"] = cam["K"].to(dev)
     target = scene["target"].to(dev)
+    cache = {} if schedule_cache else None
     if path == "fused":
-        step = lambda: fused_step(leaves, cam, target)  # noqa: E731
+        step = lambda: fused_step(leaves, cam, target, schedule_cache=cache)  # noqa: E731
     else:
         step = lambda: gpu_step(render, leaves, cam, target)  # noqa: E731
     for _ in range(warmup):
@@ -935,6 +943,14 @@ def main(argv=None):
         d = run_gpu(scene, args.steps, args.warmup, "drop-in")
         drop_in = {"ms_per_step": round(d["ms"], 3), "loss": d["loss"],
                    "stages": roofline(d, scene["name"])["per_stage"]}
+    view_cache = None
+    if args.path == "fused":
+        v = run_gpu(scene, args.steps, args.warmup, "fused", schedule_cache=True)
+        view_cache = {"ms_per_step": round(v["ms"], 4),
+                      "rasterize_display_l1_ms": round(v["stages"]["rasterize_display_l1"][1], 4),
+                      "note": "the fused step with a per-view tile schedule cache: the forward "
+                              "launches its tiles heaviest first by the last render of the same "
+                              "view (a training view recurs every epoch; here every step)"}
     ssim = None if args.no_ssim else run_ssim(scene, args.steps, args.warmup)
     if ssim is not None and args.path == "fused":
         ssim["fused_step_l1_ssim"] = run_full_loss(scene, args.steps, args.warmup)
@@ -973,6 +989,7 @@ def main(argv=None):
         "stages": rl["per_stage"],
         "loss": res["loss"],
         "drop_in": drop_in,
+        "view_schedule_cache": view_cache,
         "ssim": ssim,
         "train_stress": train,
         "configs": configs,

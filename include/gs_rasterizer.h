@@ -294,6 +294,12 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
  *   and the backward's launch order to its second: per XCD's tile range, the
  *   tiles by descending work, so that gs_rasterize_l1_backward, given the same
  *   buffer, starts the heaviest tiles first (the results do not depend on it).
+ *   forward_order: null (each XCD's range in tile order), or the second half
+ *   of a tile_schedule buffer that an earlier call filled for the same tile
+ *   grid, e.g. the last render of the same view in a training loop that visits
+ *   a fixed set of views: this forward then also starts its heaviest tiles (as
+ *   they were then) first.  It must be a permutation of every XCD range (such a
+ *   buffer is); the results do not depend on it.
  * gs_l1_finish: loss = sum(tile_loss) / count (count = H * W * 3), one float.
  * gs_rasterize_l1_backward: gs_rasterize_backward seeded by
  *   loss = mean(|clamp(image, 0, 1) * 255 / 255 - target|) with upstream
@@ -322,7 +328,8 @@ int gs_rasterize_display_l1(const int32_t *indexing_offset, const int32_t *gauss
                             float transmittance_threshold, float chi_squared_threshold,
                             const float *target, float *image, float *display, float *tile_loss,
                             float *loss, int32_t *tile_schedule, float *clear,
-                            int64_t clear_count, hipStream_t stream);
+                            int64_t clear_count, const int32_t *forward_order,
+                            hipStream_t stream);
 int gs_l1_finish(const float *tile_loss, int32_t n_tiles, int64_t count, float *loss,
                  hipStream_t stream);
 int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const float *image,

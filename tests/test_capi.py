@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 13
+    assert lib.gs_abi_version() == 14
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -130,10 +130,10 @@ def test_invalid_arguments_rejected_on_host(lib):
     # a NaN loss weight
     blend_args = (null, null, 16, 10, *([null] * 4), 10, 64, 64, 16, 1e-4, 1e-4, 9.21)
     assert lib.gs_rasterize_display_l1(*blend_args, fake, fake, null, fake, null, null, null, 0,
-                                       null) == -1  # no display
+                                       null, null) == -1  # no display
     assert lib.gs_rasterize_display_l1(null, null, 15, 10, *([null] * 4), 10, 64, 64, 16, 1e-4,
                                        1e-4, 9.21, fake, fake, fake, fake, null, null, null, 0,
-                                       null) == -1  # 15 offsets for a 16-tile image
+                                       null, null) == -1  # 15 offsets for a 16-tile image
     assert lib.gs_l1_finish(fake, 16, 0, fake, null) == -1
     assert lib.gs_rasterize_l1_backward(fake, fake, fake, *blend_args, *([fake] * 4), 1,
                                         float("nan"), null, null, null) == -1

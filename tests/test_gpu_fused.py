@@ -91,6 +91,63 @@ def test_fused_preprocess_equals_unfused_sequence(gpu):
         assert torch.equal(a, b)
 
 
+def test_forward_tile_order_changes_nothing_but_the_launch_order(gpu):
+    """rasterize_display_l1 with an earlier call's schedule as forward_schedule (its
+    tiles launched heaviest first): image, display, loss and this call's schedule
+    (work per tile and backward order) are bit-equal to the plain launch; a
+    reversed order (any per-range permutation is allowed) likewise."""
+    p, cam, target = helpers.scene_orbit(20_000, 320, 240, 440.0, seed=23)
+    W, H = cam["width"], cam["height"]
+    raw = {k: v.to(gpu) for k, v in p.items()}
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    pts, depths, _, conic, radii, mask, opac, colors = cr.preprocess_forward(
+        raw["means"], raw["log_scales"], raw["quats_raw"], raw["opacity_logits"], raw["sh_dc"],
+        raw["sh_rest"], w2c, K, 0.01, 100.0, 1 / 255, 0.5, 128.0, W, H)
+    off, ids = cr.compute_tile_intersection(pts, radii, depths, mask, W, H, 16)
+    nt = off.shape[0]
+    args = (off, ids, pts, conic, opac, colors, W, H, tgt)
+    first = cr.tile_schedule(nt, gpu)
+    ref = cr.rasterize_display_l1(*args, schedule=first)
+    reversed_sched = first.clone()
+    base, rem = divmod(nt, 8)
+    for x in range(8):  # each XCD range reversed: another permutation of every range
+        s0 = x * base + min(x, rem)
+        ln = base + (1 if x < rem else 0)
+        reversed_sched[nt + s0:nt + s0 + ln] = torch.arange(s0 + ln - 1, s0 - 1, -1,
+                                                           dtype=torch.int32, device=gpu)
+    for prev in (first, reversed_sched):
+        second = cr.tile_schedule(nt, gpu)
+        got = cr.rasterize_display_l1(*args, schedule=second, forward_schedule=prev)
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b)
+        assert torch.equal(second, first)
+    with pytest.raises(cr.RasterizerError):
+        cr.rasterize_display_l1(*args, schedule=first, forward_schedule=first)
+
+
+def test_render_l1_view_schedule_cache(gpu):
+    """render_l1 with a per-view schedule cache: the first step of a view fills
+    it, the next launches its forward in that order; loss and display are
+    bit-equal to the uncached step, gradients equal up to the float-atomic order."""
+    p, cam, target = helpers.scene_orbit(20_000, 320, 240, 440.0, seed=24)
+    W, H = cam["width"], cam["height"]
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    cache = {}
+    runs = []
+    for use_cache in (False, True, True):
+        a = _raw_leaves(p, gpu)
+        loss, disp, _, _ = render_l1(w2c, K, W, H, a["means"], a["log_scales"], a["quats_raw"],
+                                     a["opacity_logits"], a["sh_dc"], a["sh_rest"], tgt,
+                                     schedule_cache=cache if use_cache else None, view_id="v0")
+        loss.backward()
+        runs.append((loss.detach(), disp, {k: a[k].grad for k in helpers.PARAMS}))
+    assert list(cache) == ["v0"] and cache["v0"].dtype == torch.int32
+    for loss, disp, grads in runs[1:]:
+        assert torch.equal(loss, runs[0][0]) and torch.equal(disp, runs[0][1])
+        for k in helpers.PARAMS:
+            assert helpers.rel_l2(grads[k], runs[0][2][k]) <= 1e-5, k
+
+
 @pytest.mark.parametrize("scene", ["orbit", "box"])
 def test_render_l1_matches_drop_in_path(gpu, scene):
     if scene == "orbit":
