@@ -1254,9 +1254,11 @@ __device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int64
 
 // Block -> supertile, this lane's Gaussian and mask.  Returns false (uniformly)
 // for the blocks past the last chunk (the grid is sized by an upper bound).
-__device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x) {
+// Workgroup w handles block w - skip (the first `skip` workgroups, a multiple of
+// kBinXcds, do other work).
+__device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x, uint32_t skip = 0) {
     const uint32_t chunks = a.chunk_start[a.n_super];
-    x.b = (uint32_t)xcd_block_live(blockIdx.x, chunks);
+    x.b = (uint32_t)xcd_block_live(blockIdx.x - skip, chunks);
     if (x.b >= chunks) return false;
     const uint2 map = a.block_map[x.b];
     x.s = (int)map.x;
@@ -1399,14 +1401,82 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
 // and the bounds check of its run are scalar work; each covering lane stores at
 // the run's start plus its rank in the mask.  k32: positions fit 32 bits
 // (K < 2^30), so a store is a 32-bit offset from the uniform base.
+// Blend launch order of XCD range x of the tile grid (the ranges the blend
+// kernels give the XCDs: x * base + min(x, rem) onwards, base + (x < rem) tiles,
+// base = n_tiles / kBinXcds): the range's tiles by ascending bit length of their
+// list length (0, 1, 2-3, 4-7, ...), in tile order within a bucket.  A stable
+// counting sort over 32 buckets by one workgroup of kL2Threads: a histogram,
+// then the range in chunks of kL2Threads tiles, each tile placed at its
+// bucket's running start plus its rank among the chunk's tiles of that bucket
+// (ballot matching within a wave, per-wave counts across the waves).
+__device__ void tile_launch_order(int x, int n_tiles, int64_t k, const int32_t *__restrict__ offsets,
+                                  int32_t *__restrict__ order) {
+    constexpr int kBuckets = 32;
+    __shared__ uint32_t start_of[kBuckets];
+    __shared__ uint32_t wave_cnt[kL2Waves][kBuckets];
+    const int base = n_tiles / kBinXcds, rem = n_tiles % kBinXcds;
+    const int first = x * base + min(x, rem), len = base + (x < rem ? 1 : 0);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    auto bucket = [&](int t) -> uint32_t {
+        const int64_t end = t + 1 < n_tiles ? (int64_t)offsets[t + 1] : k;
+        const int64_t n_t = end - (int64_t)offsets[t];
+        const uint32_t c = n_t > 0 ? (uint32_t)min(n_t, (int64_t)0x7fffffff) : 0u;
+        return c == 0u ? 0u : 32u - (uint32_t)__clz(c);  // bit length: 0..31
+    };
+    if (threadIdx.x < kBuckets) start_of[threadIdx.x] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < len; i += kL2Threads) atomicAdd(&start_of[bucket(first + i)], 1u);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int d = 0; d < kBuckets; ++d) {
+            const uint32_t c = start_of[d];
+            start_of[d] = run;
+            run += c;
+        }
+    }
+    for (int c0 = 0; c0 < len; c0 += kL2Threads) {
+        if (lane < kBuckets) wave_cnt[wave][lane] = 0u;
+        __syncthreads();
+        const int i = c0 + (int)threadIdx.x;
+        const bool valid = i < len;
+        const uint32_t d = valid ? bucket(first + i) : 0u;
+        const uint64_t peers = match_digit(d, 5, __ballot(valid));
+        if (valid && (peers & lanemask_lt()) == 0) wave_cnt[wave][d] = (uint32_t)__popcll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t pos = start_of[d] + (uint32_t)__popcll(peers & lanemask_lt());
+            for (int w = 0; w < wave; ++w) pos += wave_cnt[w][d];
+            order[first + (int)pos] = first + i;
+        }
+        __syncthreads();
+        if (threadIdx.x < kBuckets) {
+            uint32_t c = 0;
+#pragma unroll
+            for (int w = 0; w < kL2Waves; ++w) c += wave_cnt[w][threadIdx.x];
+            start_of[threadIdx.x] += c;
+        }
+        __syncthreads();  // counts read before the next chunk clears them
+    }
+}
+
+// With launch_order, the grid has kBinXcds more workgroups than the scatter
+// needs (the first ones, one per XCD): each writes the blend launch order of
+// one XCD range while the scatter runs.
 template <bool k32>
 __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
                                                                 const uint32_t *__restrict__ table,
-                                                                int32_t *__restrict__ ids_out) {
+                                                                int32_t *__restrict__ ids_out,
+                                                                const int32_t *__restrict__ offsets,
+                                                                int32_t *__restrict__ launch_order) {
     __shared__ uint32_t base[kL2Waves][kSuperLocal];
     __shared__ uint64_t rowcol[kL2Waves][2 * kSuper];
+    if (launch_order && blockIdx.x < kBinXcds) {
+        tile_launch_order((int)blockIdx.x, a.tiles_x * a.tiles_y, a.k, offsets, launch_order);
+        return;
+    }
     L2Block x;
-    if (!l2_block(a, x)) return;
+    if (!l2_block(a, x, launch_order ? kBinXcds : 0)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     base[wave][lane] = wave_local_counts(x, rowcol[wave]);
     __syncthreads();
@@ -2048,12 +2118,19 @@ extern "C" int gs_bin_sort_workspace_size(int64_t n, int64_t k, int64_t m, int32
     return GS_OK;
 }
 
-extern "C" int gs_bin_sort(const float *points_image, const float *radii, const float *depths,
-                           int64_t n, int32_t width, int32_t height, int32_t tile_size,
-                           int64_t k, int64_t m, const void *count_workspace, void *workspace,
-                           size_t workspace_bytes, int32_t *indexing_offset,
-                           int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
-                           int32_t *tiles_touched, hipStream_t stream) {
+namespace gs {
+
+// Identity order of each range (band order): the launch order when K = 0.
+__global__ __launch_bounds__(256) void iota_kernel(int n, int32_t *__restrict__ out) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = i;
+}
+
+int bin_sort(const float *points_image, const float *radii, const float *depths, int64_t n,
+             int32_t width, int32_t height, int32_t tile_size, int64_t k, int64_t m,
+             const void *count_workspace, void *workspace, size_t workspace_bytes,
+             int32_t *indexing_offset, int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
+             int32_t *tiles_touched, int32_t *launch_order, hipStream_t stream) {
     if (n < 0 || k < 0 || m < 0 || m > k || width <= 0 || height <= 0 || tile_size <= 0)
         return GS_ERR_INVALID_ARGUMENT;
     if (k > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
@@ -2075,7 +2152,15 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         st = launch_status();
         if (st) return st;
     }
-    if (k == 0) return zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)g.n_tiles, stream);
+    if (k == 0) {
+        if (launch_order) {
+            hipLaunchKernelGGL(iota_kernel, dim3(ceil_div(g.n_tiles, 256)), dim3(256), 0, stream,
+                               g.n_tiles, launch_order);
+            st = launch_status();
+            if (st) return st;
+        }
+        return zero_bytes(indexing_offset, sizeof(int32_t) * (size_t)g.n_tiles, stream);
+    }
     if (!points_image || !radii || !gaussian_ids_sorted || (sorted_keys && !depths) || n == 0)
         return GS_ERR_INVALID_ARGUMENT;
 
@@ -2140,12 +2225,13 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
                        w.tile_counts, g.n_tiles, fused_scan ? 1 : 0, indexing_offset, w.table);
     st = launch_status();
     if (st) return st;
+    const unsigned grid2 = (unsigned)nb2 + (launch_order ? kBinXcds : 0);
     if (k < (1LL << 30))
-        hipLaunchKernelGGL(l2_scatter_kernel<true>, dim3((unsigned)nb2), dim3(kL2Threads), 0,
-                           stream, l2, w.table, gaussian_ids_sorted);
+        hipLaunchKernelGGL(l2_scatter_kernel<true>, dim3(grid2), dim3(kL2Threads), 0, stream, l2,
+                           w.table, gaussian_ids_sorted, indexing_offset, launch_order);
     else
-        hipLaunchKernelGGL(l2_scatter_kernel<false>, dim3((unsigned)nb2), dim3(kL2Threads), 0,
-                           stream, l2, w.table, gaussian_ids_sorted);
+        hipLaunchKernelGGL(l2_scatter_kernel<false>, dim3(grid2), dim3(kL2Threads), 0, stream, l2,
+                           w.table, gaussian_ids_sorted, indexing_offset, launch_order);
     st = launch_status();
     if (st) return st;
     if (sorted_keys) {
@@ -2155,4 +2241,31 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
         st = launch_status();
     }
     return st;
+}
+
+}  // namespace gs
+
+extern "C" int gs_bin_sort(const float *points_image, const float *radii, const float *depths,
+                           int64_t n, int32_t width, int32_t height, int32_t tile_size,
+                           int64_t k, int64_t m, const void *count_workspace, void *workspace,
+                           size_t workspace_bytes, int32_t *indexing_offset,
+                           int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
+                           int32_t *tiles_touched, hipStream_t stream) {
+    return gs::bin_sort(points_image, radii, depths, n, width, height, tile_size, k, m,
+                        count_workspace, workspace, workspace_bytes, indexing_offset,
+                        gaussian_ids_sorted, sorted_keys, tiles_touched, nullptr, stream);
+}
+
+extern "C" int gs_bin_sort_ordered(const float *points_image, const float *radii,
+                                   const float *depths, int64_t n, int32_t width, int32_t height,
+                                   int32_t tile_size, int64_t k, int64_t m,
+                                   const void *count_workspace, void *workspace,
+                                   size_t workspace_bytes, int32_t *indexing_offset,
+                                   int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
+                                   int32_t *tiles_touched, int32_t *launch_order,
+                                   hipStream_t stream) {
+    if (!launch_order) return GS_ERR_INVALID_ARGUMENT;
+    return gs::bin_sort(points_image, radii, depths, n, width, height, tile_size, k, m,
+                        count_workspace, workspace, workspace_bytes, indexing_offset,
+                        gaussian_ids_sorted, sorted_keys, tiles_touched, launch_order, stream);
 }

@@ -277,9 +277,9 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
 
 // Software pipeline over a tile's list in batches of kBatch.  With kRecords,
 // the ids of batch b+2 and the records of batch b+1 are in flight while batch
-// b is processed; without, only the ids of batch b+1 (fewer registers).  Both
-// blend kernels use kRecords: in the backward it costs a wave per SIMD of
-// occupancy (93 VGPRs) and is still 2% faster.
+// b is processed; without, only the ids of batch b+1 (fewer registers).  The
+// backward uses kRecords (2% faster although it costs a wave per SIMD at 93
+// VGPRs); the forward does not (4% faster without).
 // kInvO: also stage 1 / opacity (the backward).
 template <bool kRecords, bool kInvO>
 struct BatchPipe {
@@ -478,7 +478,7 @@ __device__ __forceinline__ void blend_accumulate(
         cr[q] = cg[q] = cb[q] = 0.0f;
     }
     if (span.end <= span.start) return;
-    BatchPipe<true, false> pipe;
+    BatchPipe<false, false> pipe;
     pipe.start(span, ids, n, points, conics, opac, colors);
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
         if (!any_active(T, T_thr)) break;

@@ -38,6 +38,7 @@ __all__ = [
     "evaluate_spherical_harmonics_backward",
     "compute_tile_intersection",
     "compute_tile_intersection_debug",
+    "compute_tile_intersection_ordered",
     "rasterize",
     "rasterize_backward",
     "rasterize_work",
@@ -255,7 +256,8 @@ def evaluate_spherical_harmonics_backward(
     return g_means, g_dc, g_rest
 
 
-def _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, debug):
+def _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, debug,
+                       ordered=False):
     dev = _device_of(points_image)
     n = points_image.shape[0]
     f32 = torch.float32
@@ -299,18 +301,21 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         gaussian_ids_sorted = torch.empty((k,), dtype=torch.int32, device=dev)
         sorted_keys = torch.empty((k,), dtype=torch.int64, device=dev) if debug else None
         tiles_touched = torch.empty((n,), dtype=torch.int32, device=dev) if debug else None
+        order = torch.empty((n_tiles,), dtype=torch.int32, device=dev) if ordered else None
+        sort_args = (_ptr(points_image), _ptr(radii), _ptr(depths), n, width, height, tile_size,
+                     k, m, _ptr(ws_count), _ptr(ws_sort), sz2.value, _ptr(indexing_offset),
+                     _ptr(gaussian_ids_sorted), _ptr(sorted_keys), _ptr(tiles_touched))
         ev = _lib.timer.record("bin_sort", dev)
-        _lib.check(
-            lib.gs_bin_sort(
-                _ptr(points_image), _ptr(radii), _ptr(depths), n, width, height, tile_size, k,
-                m, _ptr(ws_count), _ptr(ws_sort), sz2.value, _ptr(indexing_offset),
-                _ptr(gaussian_ids_sorted), _ptr(sorted_keys), _ptr(tiles_touched), stream,
-            ),
-            "compute_tile_intersection (sort)",
-        )
+        if ordered:
+            _lib.check(lib.gs_bin_sort_ordered(*sort_args, _ptr(order), stream),
+                       "compute_tile_intersection (sort)")
+        else:
+            _lib.check(lib.gs_bin_sort(*sort_args, stream), "compute_tile_intersection (sort)")
         _lib.timer.stop(ev, dev)
     if debug:
         return indexing_offset, gaussian_ids_sorted, sorted_keys, tiles_touched
+    if ordered:
+        return indexing_offset, gaussian_ids_sorted, order
     return indexing_offset, gaussian_ids_sorted
 
 
@@ -322,6 +327,16 @@ def compute_tile_intersection(points_image, radii, depths, mask, width, height, 
     index); indexing_offset[t] = number of entries whose tile is < t.
     """
     return _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, False)
+
+
+def compute_tile_intersection_ordered(points_image, radii, depths, mask, width, height,
+                                      tile_size=16):
+    """compute_tile_intersection plus a blend launch order (n_tiles int32) for
+    rasterize_display_l1(forward_order=...): in each XCD's tile range, the tiles by
+    ascending bit length of their list length, tile order within a bucket
+    (gs_bin_sort_ordered).  Returns (indexing_offset, gaussian_ids_sorted, order)."""
+    return _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, False,
+                              ordered=True)
 
 
 def compute_tile_intersection_debug(points_image, radii, depths, mask, width, height, tile_size=16):
@@ -741,7 +756,7 @@ def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, g
 def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
                          opacities, colors, width, height, target, alpha_threshold=1e-4,
                          transmittance_threshold=1e-4, chi_squared_threshold=9.21, clear=None,
-                         schedule=None, forward_schedule=None):
+                         schedule=None, forward_schedule=None, forward_order=None):
     """rasterize_display with tile size 16 plus loss = mean(|display / 255 - target|).
     Returns (image, display, loss[1] fp32).  `clear` (an fp32 device tensor, e.g.
     from blend_grad_accumulators) is zeroed by the same launch.  `schedule` (an
@@ -749,7 +764,9 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
     tile and the order in which rasterize_l1_backward, given it, launches the
     tiles (heaviest first).  `forward_schedule`: a schedule an earlier call filled
     for the same image size (not this call's `schedule`); this forward then
-    launches its tiles in that order (results do not depend on it)."""
+    launches its tiles in that order (results do not depend on it).
+    `forward_order`: instead of forward_schedule, any per-XCD-range launch order
+    of n_tiles int32 (e.g. compute_tile_intersection_ordered's)."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -769,6 +786,21 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
             raise RasterizerError("rasterize_display_l1: forward_schedule must be an earlier "
                                   "call's schedule, not the one this call writes")
         fwd_order = forward_schedule[n_tiles:]
+    if forward_order is not None:
+        if forward_schedule is not None:
+            raise RasterizerError("rasterize_display_l1: pass forward_schedule or forward_order, "
+                                  "not both")
+        if (not isinstance(forward_order, torch.Tensor) or forward_order.dtype != torch.int32
+                or forward_order.device != dev or not forward_order.is_contiguous()
+                or forward_order.numel() < n_tiles):
+            raise RuntimeError("rasterize_display_l1: forward_order must be a contiguous int32 "
+                               f"tensor of at least {n_tiles} elements on {dev}")
+        if schedule is not None and (
+                schedule.data_ptr() <= forward_order.data_ptr()
+                < schedule.data_ptr() + schedule.numel() * 4):
+            raise RasterizerError("rasterize_display_l1: forward_order must not lie in the "
+                                  "schedule this call writes")
+        fwd_order = forward_order
     lib = _lib.load()
     with torch.cuda.device(dev):
         ev = _lib.timer.record("rasterize_display_l1", dev)

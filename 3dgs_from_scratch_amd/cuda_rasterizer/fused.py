@@ -52,7 +52,9 @@ class RenderL1Function(torch.autograd.Function):
             means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
             max_radius, width, height)
-        off, ids = _cr.compute_tile_intersection(pts, radii, depths, mask, width, height, 16)
+        # with a launch order for the forward's tiles from the list lengths
+        off, ids, list_order = _cr.compute_tile_intersection_ordered(pts, radii, depths, mask,
+                                                                     width, height, 16)
         # the blend gradients' accumulators, zeroed by the forward blend launch
         acc = _cr.blend_grad_accumulators(means.shape[0], means.device)
         # the forward's work per tile orders the backward's tiles (heaviest first)
@@ -64,10 +66,12 @@ class RenderL1Function(torch.autograd.Function):
             if (previous is not None and (previous.device != means.device
                                           or previous.numel() != sched.numel())):
                 previous = None
+        # the forward launches heaviest first by the view's last render when there
+        # is one, else in the order from the list lengths
         image, display, loss = _cr.rasterize_display_l1(
             off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
             transmittance_threshold, chi_squared_threshold, clear=acc, schedule=sched,
-            forward_schedule=previous)
+            forward_schedule=previous, forward_order=None if previous is not None else list_order)
         if schedule_cache is not None and view_id is not None:
             schedule_cache[view_id] = sched
         ssim_saved = ()

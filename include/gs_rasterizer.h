@@ -152,6 +152,26 @@ int gs_bin_sort(const float *points_image, const float *radii, const float *dept
                 int32_t *indexing_offset, int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
                 int32_t *tiles_touched, hipStream_t stream);
 
+/*
+ * gs_bin_sort that also writes launch_order (n_tiles int32, required): a launch
+ * order for gs_rasterize_display_l1's forward_order, computed from the tile
+ * lists alone.  Within each XCD's tile range (the ranges the blend kernels use:
+ * with base = n_tiles / 8 and rem = n_tiles % 8, range x starts at
+ * x * base + min(x, rem) and holds base + (x < rem) tiles), the range's tiles by
+ * ascending bit length of their list length (0, 1, 2-3, 4-7, ...), in tile
+ * order within each of those buckets.  Measured at 1920x1080 it shortens the
+ * forward by 10-20 us against tile order (the tiles with the longest lists,
+ * which start after the first wave of tiles, are not the slowest); it changes
+ * no result.  The order comes from extra workgroups of the last binning launch.
+ * No counterpart in the reference extension.
+ */
+int gs_bin_sort_ordered(const float *points_image, const float *radii, const float *depths,
+                        int64_t n, int32_t width, int32_t height, int32_t tile_size, int64_t k,
+                        int64_t m, const void *count_workspace, void *workspace,
+                        size_t workspace_bytes, int32_t *indexing_offset,
+                        int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
+                        int32_t *tiles_touched, int32_t *launch_order, hipStream_t stream);
+
 /* --------------------------------------------------------------------- blend */
 
 /*

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 14
+    assert lib.gs_abi_version() == 15
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -95,6 +95,11 @@ def test_invalid_arguments_rejected_on_host(lib):
                            null, null, null) == -3
     assert lib.gs_bin_sort(null, null, null, 10, 64, 64, 16, 5, 6, null, null, 0, null, null,
                            null, null, null) == -1  # more supertile entries than keys
+    assert lib.gs_bin_sort_ordered(null, null, null, 10, 64, 64, 16, 5, 5, null, null, 0, null,
+                                   null, null, null, null, null) == -1  # launch_order required
+    fake = ctypes.c_void_p(256)  # never dereferenced: the key count is rejected first
+    assert lib.gs_bin_sort_ordered(null, null, null, 10, 64, 64, 16, 2**31, 5, null, null, 0,
+                                   null, null, null, null, fake, null) == -3
     sz = ctypes.c_size_t(0)
     assert lib.gs_bin_count(null, null, null, null, 10, 64, 64, 16, null, 0, null, null) == -1
     # training-loop entries: bad hyper-parameters, missing buffers, bad widths

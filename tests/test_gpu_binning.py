@@ -166,3 +166,47 @@ def test_single_call_count_equals_two_phases(gpu, width, height):
                            16, k, m, ws.data_ptr(), ws2.data_ptr(), sz2.value, off.data_ptr(),
                            ids.data_ptr(), None, None, stream) == 0
     assert torch.equal(off, off2) and torch.equal(ids, ids2)
+
+
+def _launch_order_ref(off, k, n_tiles):
+    """Per XCD range (8 ranges: base + (x < rem) tiles from x * base + min(x, rem)),
+    the tiles by (bit length of the list length, tile)."""
+    lens = np.diff(np.append(off.astype(np.int64), k))
+    bits = np.array([int(v).bit_length() for v in lens], dtype=np.int64)
+    out = np.empty(n_tiles, dtype=np.int64)
+    base, rem = divmod(n_tiles, 8)
+    for x in range(8):
+        st, ln = x * base + min(x, rem), base + (1 if x < rem else 0)
+        t = np.arange(st, st + ln)
+        out[st:st + ln] = t[np.lexsort((t, bits[t]))]
+    return out
+
+
+@pytest.mark.parametrize("n,width,height,tile,culled", [
+    (1, 32, 32, 16, False),        # 4 tiles: ranges of 0 and 1 tiles
+    (3000, 64, 64, 16, False),     # 16 tiles
+    (3000, 64, 64, 8, False),
+    (50000, 800, 800, 16, False),
+    (200000, 1920, 1080, 16, False),  # 1020 tiles per range: two chunks of 512
+    (100000, 3840, 2160, 16, False),  # 4050 tiles per range
+    (5000, 640, 480, 16, True),    # K = 0: tile order
+])
+def test_launch_order(gpu, n, width, height, tile, culled):
+    """gs_bin_sort_ordered: the same layout as gs_bin_sort, and a launch order that
+    sorts each XCD range stably by the bit length of its tiles' list lengths."""
+    pts, radii, depths, mask = _random_splats(n, width, height, seed=n + width)
+    if culled:
+        mask[:] = False
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    off, ids, order = cr.compute_tile_intersection_ordered(d(pts), d(radii), d(depths), d(mask),
+                                                           width, height, tile)
+    off2, ids2 = cr.compute_tile_intersection(d(pts), d(radii), d(depths), d(mask), width, height,
+                                              tile)
+    assert torch.equal(off, off2) and torch.equal(ids, ids2)
+    n_tiles = off.shape[0]
+    ref = _launch_order_ref(off.cpu().numpy(), ids.shape[0], n_tiles)
+    assert np.array_equal(order.cpu().numpy().astype(np.int64), ref)
+    if culled:
+        assert ids.shape[0] == 0 and np.array_equal(ref, np.arange(n_tiles))
+    elif n >= 1000:  # lists of many lengths, so the order is not trivial
+        assert len(set(np.diff(np.append(off.cpu().numpy(), ids.shape[0])).tolist())) > 3
