@@ -1,8 +1,9 @@
 // Tile blending: front-to-back alpha compositing and its gradient.
 //
-// One wave64 per 16x16 tile.  Lane l owns the four pixels
-// (x0 + l%16, y0 + l/16 + 4s), s = 0..3, i.e. one pixel in each 16x4 strip of
-// the tile.  The tile's depth-sorted Gaussian list is walked in batches of 64
+// One wave64 per 16x16 tile (on grids of at most 1024 tiles, 4 waves per tile:
+// see blend_waves).  Lane l owns the four pixels (x0 + l%16, y0 + l/16 + 4s),
+// s = 0..3, i.e. one pixel in each 16x4 strip of the tile (with W waves per
+// tile, wave w's lanes own strips w*4/W .. and the waves share the staging).  The tile's depth-sorted Gaussian list is walked in batches of 64
 // Gaussians (one per lane); at staging each lane computes which strips the
 // Gaussian's chi-square / alpha ellipse reaches, and only Gaussians reaching
 // the tile are written to LDS (ballot compaction, list order kept) with that
@@ -39,7 +40,7 @@ namespace gs {
 
 constexpr int kTile = 16;
 constexpr int kStrips = 4;       // 16x4 strips per tile; one pixel of each per lane
-constexpr int kBatch = kWave;    // records staged per batch (one per lane)
+constexpr int kBatch = kWave;    // records staged per batch and wave (one per lane)
 constexpr int kGradFields = 9;   // du, dv, dA, dB, dC, dopacity, dr, dg, db
 constexpr int kXcds = 8;
 
@@ -114,12 +115,18 @@ __device__ __forceinline__ float conic_exponent(float A, float B2, float C, floa
 // alpha = o exp(-E/2) = exp2(E * kNegHalfLog2e + log2(o)): one fma and one
 // v_exp_f32 per (entry, pixel).
 constexpr float kNegHalfLog2e = -0.72134752044448170f;
+// One batch of staged records of a tile worked by W waves (W * kBatch records).
+template <int W>
 struct BatchLds {
-    float4 geo[kBatch];  // u, v, A, 2B
-    float4 aux[kBatch];  // C, E cut-off (chi_eff), strip mask, log2(opacity)
-    float4 col[kBatch];  // r, g, b, (gaussian id bits)
-    float inv_o[kBatch];  // 1 / opacity (staged by the backward for its opacity gradient)
-    float o_raw[kBatch];  // the opacity of a record whose log2 is not finite (see below)
+    float4 geo[kBatch * W];  // u, v, A, 2B
+    float4 aux[kBatch * W];  // C, E cut-off (chi_eff), strip mask, log2(opacity)
+    float4 col[kBatch * W];  // r, g, b, (gaussian id bits)
+    float inv_o[kBatch * W];  // 1 / opacity (staged by the backward for its opacity gradient)
+    float o_raw[kBatch * W];  // the opacity of a record whose log2 is not finite (see below)
+    int wave_count[W];        // W > 1: records each wave stages, and whether one is
+    int wave_bad[W];          //   non-finite (the batch then takes the select-based path)
+    int wave_flag[W];         // W > 1: per-wave votes of the batch loops (tile_any)
+    int wave_flag_once[W];    // W > 1: the backward's one vote before its loop
 };
 
 // Records whose log2 opacity is not finite -- opacity <= 0, +inf or NaN -- are
@@ -238,12 +245,13 @@ struct Staged {
     bool nonfinite;
 };
 
-// Stages the lane's record into the next free LDS slot if its ellipse (with
-// the chi-square and alpha cut-offs) reaches the tile, keeping lane (= list)
-// order, with its E cut-off (effective_chi) in aux.y, its strip mask in aux.z
-// and log2 of its opacity in aux.w.
-template <bool kInvO>
-__device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, float chi,
+// Stages the thread's record into the next free LDS slot if its ellipse (with
+// the chi-square and alpha cut-offs) reaches the tile, keeping thread (= list)
+// order, with its E cut-off (effective_chi) in aux.y, its strip mask (all four
+// strips of the tile) in aux.z and log2 of its opacity in aux.w.  With W > 1
+// waves, wave w's records follow those of waves 0..w-1 (one more barrier).
+template <bool kInvO, int W>
+__device__ __forceinline__ Staged stage_records(BatchLds<W> &s, const Record &r, float chi,
                                                 float alpha_thr, float log2_alpha_thr, float x0,
                                                 float y0) {
     uint32_t m = 0u;
@@ -260,8 +268,31 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
     // the select-based path (the only one that handles such opacities)
     const bool bad = m != 0u && !(isfinite(r.r) && isfinite(r.g) && isfinite(r.b) &&
                                   isfinite(log2o));
+    Staged st;
+    int first = 0;  // this wave's first slot
+    if constexpr (W == 1) {
+        st.count = __popcll(keep);
+        st.nonfinite = __ballot(bad) != 0;
+    } else {
+        const int wave = threadIdx.x / kWave;
+        const bool wave_bad = __ballot(bad) != 0;
+        if (threadIdx.x % kWave == 0) {
+            s.wave_count[wave] = __popcll(keep);
+            s.wave_bad[wave] = wave_bad ? 1 : 0;
+        }
+        __syncthreads();
+        st.count = 0;
+        st.nonfinite = false;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const int c = s.wave_count[w];
+            first += w < wave ? c : 0;
+            st.count += c;
+            st.nonfinite = st.nonfinite || s.wave_bad[w] != 0;
+        }
+    }
     if (m != 0u) {
-        const int slot = __popcll(keep & lanemask_lt());
+        const int slot = first + __popcll(keep & lanemask_lt());
         s.geo[slot] = make_float4(r.u, r.v, r.A, r.B + r.B);
         s.aux[slot] = make_float4(r.C, chi_eff, __uint_as_float(m), log2o);
         s.col[slot] = make_float4(r.r, r.g, r.b, __int_as_float(r.id));
@@ -269,9 +300,6 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
         if (kInvO) s.inv_o[slot] = special ? 1.0f : __builtin_amdgcn_rcpf(r.o);
         if (special) s.o_raw[slot] = r.o;
     }
-    Staged st;
-    st.count = __popcll(keep);
-    st.nonfinite = __ballot(bad) != 0;
     return st;
 }
 
@@ -280,11 +308,12 @@ __device__ __forceinline__ Staged stage_records(BatchLds &s, const Record &r, fl
 // b is processed; without, only the ids of batch b+1 (fewer registers).  The
 // backward uses kRecords (2% faster although it costs a wave per SIMD at 93
 // VGPRs); the forward does not (4% faster without).
-// kInvO: also stage 1 / opacity (the backward).
-template <bool kRecords, bool kInvO>
+// kInvO: also stage 1 / opacity (the backward).  W waves stage W * kBatch
+// records per batch, one per thread.
+template <bool kRecords, bool kInvO, int W = 1>
 struct BatchPipe {
-    int32_t next_id;  // this lane's id in the batch after the next one to stage
-    Record rec;       // this lane's record of the next batch to stage (kRecords)
+    int32_t next_id;  // this thread's id in the batch after the next one to stage
+    Record rec;       // this thread's record of the next batch to stage (kRecords)
 
     __device__ __forceinline__ void start(TileSpan span, const int32_t *__restrict__ ids,
                                           int64_t n, const float *__restrict__ points,
@@ -294,7 +323,7 @@ struct BatchPipe {
         const int32_t lane = (int32_t)threadIdx.x;
         if (kRecords) {
             const int32_t g0 = fetch_id(span.start + lane, span.end, ids);
-            next_id = fetch_id(span.start + kBatch + lane, span.end, ids);
+            next_id = fetch_id(span.start + kBatch * W + lane, span.end, ids);
             rec = fetch_record(g0, n, points, conics, opac, colors);
         } else {
             next_id = fetch_id(span.start + lane, span.end, ids);
@@ -303,7 +332,7 @@ struct BatchPipe {
 
     // Stages the batch starting at b0 (only records reaching the tile) and
     // fetches ahead.
-    __device__ __forceinline__ Staged advance(BatchLds &s, int32_t b0, TileSpan span,
+    __device__ __forceinline__ Staged advance(BatchLds<W> &s, int32_t b0, TileSpan span,
                                            const int32_t *__restrict__ ids, int64_t n,
                                            const float *__restrict__ points,
                                            const float *__restrict__ conics,
@@ -314,30 +343,41 @@ struct BatchPipe {
         if (!kRecords) rec = fetch_record(next_id, n, points, conics, opac, colors);
         __syncthreads();  // previous batch fully read before restaging
         const Staged st =
-            stage_records<kInvO>(s, rec, chi, alpha_thr, __builtin_amdgcn_logf(alpha_thr), x0,
-                                 y0);
+            stage_records<kInvO, W>(s, rec, chi, alpha_thr, __builtin_amdgcn_logf(alpha_thr), x0,
+                                    y0);
         __syncthreads();
         if (kRecords) {
             rec = fetch_record(next_id, n, points, conics, opac, colors);
-            next_id = fetch_id(b0 + 2 * kBatch + lane, span.end, ids);
+            next_id = fetch_id(b0 + 2 * kBatch * W + lane, span.end, ids);
         } else {
-            next_id = fetch_id(b0 + kBatch + lane, span.end, ids);
+            next_id = fetch_id(b0 + kBatch * W + lane, span.end, ids);
         }
         return st;
     }
 };
 
-// Pixel geometry of one lane.
+// Pixel geometry of one lane: with W waves per tile, wave w's lanes own the
+// S = kStrips / W strips w*S .. w*S + S - 1, one pixel of each per lane.
+template <int S>
 struct LanePixels {
-    float fx;             // pixel x
-    float fy[kStrips];    // pixel y in strip s
-    float x0, y0;         // tile origin
-    bool inside[kStrips];
+    float fx;       // pixel x
+    float fy[S];    // pixel y in the lane's strip s
+    float x0, y0;   // tile origin
+    bool inside[S];
 };
 
-__device__ __forceinline__ LanePixels lane_pixels(int tile, int tiles_x, int width, int height) {
-    LanePixels p;
-    const int lane = threadIdx.x;
+// The wave's index within its tile's workgroup, as a wave-uniform value.
+__device__ __forceinline__ int tile_wave() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+}
+
+template <int W>
+__device__ __forceinline__ LanePixels<kStrips / W> lane_pixels(int tile, int tiles_x, int width,
+                                                               int height) {
+    constexpr int S = kStrips / W;
+    LanePixels<S> p;
+    const int lane = threadIdx.x % kWave;
+    const int q0 = W == 1 ? 0 : tile_wave() * S;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const int px = tx * kTile + (lane & 15);
     const int py = ty * kTile + (lane >> 4);
@@ -345,9 +385,9 @@ __device__ __forceinline__ LanePixels lane_pixels(int tile, int tiles_x, int wid
     p.x0 = (float)(tx * kTile);
     p.y0 = (float)(ty * kTile);
 #pragma unroll
-    for (int s = 0; s < kStrips; ++s) {
-        p.fy[s] = (float)(py + 4 * s);
-        p.inside[s] = px < width && py + 4 * s < height;
+    for (int s = 0; s < S; ++s) {
+        p.fy[s] = (float)(py + 4 * (q0 + s));
+        p.inside[s] = px < width && py + 4 * (q0 + s) < height;
     }
     return p;
 }
@@ -382,8 +422,29 @@ __device__ __forceinline__ float l1_grad(float t, float raw, float scale, float 
 }
 
 // Some pixel of the wave still composites: !(T < T_thr) (NaN stays active).
-__device__ __forceinline__ bool any_active(const float (&T)[kStrips], float T_thr) {
-    return wave_any(!(T[0] < T_thr) || !(T[1] < T_thr) || !(T[2] < T_thr) || !(T[3] < T_thr));
+template <int S>
+__device__ __forceinline__ bool any_active(const float (&T)[S], float T_thr) {
+    bool a = false;
+#pragma unroll
+    for (int q = 0; q < S; ++q) a = a || !(T[q] < T_thr);
+    return wave_any(a);
+}
+
+// OR of a wave-uniform value over the tile's W waves (one barrier when W > 1).
+// Every wave of the workgroup must call it; `flag` must not be written again
+// before the next barrier.
+template <int W>
+__device__ __forceinline__ bool tile_any(bool v, int *flag) {
+    if constexpr (W == 1) {
+        return v;
+    } else {
+        if (threadIdx.x % kWave == 0) flag[threadIdx.x / kWave] = v ? 1 : 0;
+        __syncthreads();
+        bool any = false;
+#pragma unroll
+        for (int w = 0; w < W; ++w) any = any || flag[w] != 0;
+        return any;
+    }
 }
 
 // One staged entry j applied to the lane's four pixels.  Branch-free per
@@ -393,15 +454,22 @@ __device__ __forceinline__ bool any_active(const float (&T)[kStrips], float T_th
 // T_{i+1} = T_i - alpha T_i, i.e. T_i (1 - alpha): the 1e-10 of the
 // reference's 1 - alpha + 1e-10 is below the float resolution of that factor
 // unless alpha is within 1e-7 of 1, where T drops below any threshold either way.
-template <bool kSafe>
-__device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const LanePixels &pix,
-                                            float alpha_thr, float T_thr, float chi,
-                                            float (&T)[kStrips], float (&cr)[kStrips],
-                                            float (&cg)[kStrips], float (&cb)[kStrips],
-                                            uint32_t &work) {
-    const float4 geo = s.geo[j];
+// With W waves per tile, the entry is applied to the wave's own S strips only
+// (and skipped when its strip mask misses them).
+template <bool kSafe, int W>
+__device__ __forceinline__ void blend_entry(const BatchLds<W> &s, int j,
+                                            const LanePixels<kStrips / W> &pix, float alpha_thr,
+                                            float T_thr, float chi, float (&T)[kStrips / W],
+                                            float (&cr)[kStrips / W], float (&cg)[kStrips / W],
+                                            float (&cb)[kStrips / W], uint32_t &work) {
+    constexpr int S = kStrips / W;
     const float4 aux = s.aux[j];
-    const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
+    uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
+    if constexpr (W > 1) {
+        smask = (smask >> (tile_wave() * S)) & ((1u << S) - 1u);
+        if (smask == 0u) return;  // uniform: none of this wave's strips
+    }
+    const float4 geo = s.geo[j];
     const float4 col = s.col[j];
     // uniform: a record with a non-finite log2 opacity (only in the select-based path)
     const bool special =
@@ -411,7 +479,7 @@ __device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const Lane
     const float Adudu = (geo.z * du) * du;  // (A du) du, as in the oracle's A*du*du
     const float B2du = geo.w * du;
 #pragma unroll
-    for (int q = 0; q < kStrips; ++q) {
+    for (int q = 0; q < S; ++q) {
         if (!((smask >> q) & 1u)) continue;  // uniform
         const float dv = pix.fy[q] - geo.y;
         const float E = (Adudu + B2du * dv) + (aux.x * dv) * dv;
@@ -441,14 +509,15 @@ __device__ __forceinline__ void blend_entry(const BatchLds &s, int j, const Lane
     }
 }
 
-template <bool kSafe>
-__device__ __forceinline__ void blend_batch(const BatchLds &s, int cnt, const LanePixels &pix,
-                                            float alpha_thr, float T_thr, float chi,
-                                            float (&T)[kStrips], float (&cr)[kStrips],
-                                            float (&cg)[kStrips], float (&cb)[kStrips],
-                                            uint32_t &work) {
+template <bool kSafe, int W>
+__device__ __forceinline__ void blend_batch(const BatchLds<W> &s, int cnt,
+                                            const LanePixels<kStrips / W> &pix, float alpha_thr,
+                                            float T_thr, float chi, float (&T)[kStrips / W],
+                                            float (&cr)[kStrips / W], float (&cg)[kStrips / W],
+                                            float (&cb)[kStrips / W], uint32_t &work) {
+    if (W > 1 && !any_active(T, T_thr)) return;  // this wave's pixels are done
     for (int j = 0; j < cnt; ++j) {
-        blend_entry<kSafe>(s, j, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
+        blend_entry<kSafe, W>(s, j, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
         if ((j & 7) == 7 && !any_active(T, T_thr)) break;
     }
 }
@@ -461,34 +530,40 @@ constexpr float kInactiveT = -3.0e38f;
 
 __device__ __forceinline__ float effective_T_thr(float T_thr) { return fmaxf(T_thr, -1e30f); }
 
-// Front-to-back accumulation of the lane's four pixels over the tile's list.
-// All 64 lanes must call it (it contains barriers).
+// Front-to-back accumulation of the lane's pixels over the tile's list, the
+// tile's W waves sharing each staged batch of W * kBatch records.  Every thread
+// of the workgroup must call it (it contains barriers).  `work` counts the
+// wave's own strips and, in wave 0 only, the batches and staged records.
+template <int W>
 __device__ __forceinline__ void blend_accumulate(
-    BatchLds &s, TileSpan span, const int32_t *__restrict__ ids, int64_t n,
+    BatchLds<W> &s, TileSpan span, const int32_t *__restrict__ ids, int64_t n,
     const float *__restrict__ points, const float *__restrict__ conics,
-    const float *__restrict__ opac, const float *__restrict__ colors, const LanePixels &pix,
-    float alpha_thr, float T_thr_in, float chi, float (&cr)[kStrips], float (&cg)[kStrips],
-    float (&cb)[kStrips], uint32_t &work) {
+    const float *__restrict__ opac, const float *__restrict__ colors,
+    const LanePixels<kStrips / W> &pix, float alpha_thr, float T_thr_in, float chi,
+    float (&cr)[kStrips / W], float (&cg)[kStrips / W], float (&cb)[kStrips / W],
+    uint32_t &work) {
+    constexpr int S = kStrips / W;
     // a pixel is active while !(T < T_thr)
     const float T_thr = effective_T_thr(T_thr_in);
-    float T[kStrips];
+    float T[S];
 #pragma unroll
-    for (int q = 0; q < kStrips; ++q) {
+    for (int q = 0; q < S; ++q) {
         T[q] = pix.inside[q] ? 1.0f : kInactiveT;
         cr[q] = cg[q] = cb[q] = 0.0f;
     }
     if (span.end <= span.start) return;
-    BatchPipe<false, false> pipe;
+    BatchPipe<false, false, W> pipe;
     pipe.start(span, ids, n, points, conics, opac, colors);
-    for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
-        if (!any_active(T, T_thr)) break;
+    const bool counter = W == 1 || tile_wave() == 0;
+    for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch * W) {
+        if (!tile_any<W>(any_active(T, T_thr), s.wave_flag)) break;
         const Staged st = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
                                        alpha_thr, pix.x0, pix.y0);
-        work += kCostBatch + kCostStaged * (uint32_t)st.count;
+        if (counter) work += kCostBatch + kCostStaged * (uint32_t)st.count;
         if (st.nonfinite)
-            blend_batch<true>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
+            blend_batch<true, W>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
         else
-            blend_batch<false>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
+            blend_batch<false, W>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
     }
 }
 
@@ -572,7 +647,9 @@ __device__ __forceinline__ float wave_sum9(const float (&f)[kGradFields], bool h
     return f8_lane ? q2 : r;
 }
 
-__global__ __launch_bounds__(kWave) void blend_forward_kernel(
+// One tile per workgroup of W waves (64 W threads).
+template <int W>
+__global__ __launch_bounds__(kWave * W) void blend_forward_kernel(
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
@@ -580,12 +657,15 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     float *__restrict__ display, const float *__restrict__ target,
     float *__restrict__ tile_loss, float4 *__restrict__ clear4, int64_t clear4_count,
     uint32_t *__restrict__ tile_cost, const int32_t *__restrict__ tile_order) {
-    __shared__ BatchLds s;
+    constexpr int S = kStrips / W;
+    __shared__ BatchLds<W> s;
+    __shared__ float wave_l1[W];
+    __shared__ uint32_t wave_work[W];
     if (clear4) {  // this workgroup's share of the buffer to zero (stores overlap the blend)
         const int64_t per = (clear4_count + gridDim.x - 1) / gridDim.x;
         const int64_t c0 = (int64_t)blockIdx.x * per;
         const int64_t c1 = min(c0 + per, clear4_count);
-        for (int64_t c = c0 + threadIdx.x; c < c1; c += kWave)
+        for (int64_t c = c0 + threadIdx.x; c < c1; c += kWave * W)
             clear4[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     // launch position -> tile: the XCD's contiguous range, in the caller's order
@@ -593,16 +673,15 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
     const int slot = tile_of_block(blockIdx.x, n_tiles);
     const int tile = tile_order ? tile_order[slot] : slot;
     if ((unsigned)tile >= (unsigned)n_tiles) return;  // uniform across the workgroup
-    const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
+    const LanePixels<S> pix = lane_pixels<W>(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
-    float cr[kStrips], cg[kStrips], cb[kStrips];
+    float cr[S], cg[S], cb[S];
     uint32_t work = 0;
-    blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr, chi, cr,
-                     cg, cb, work);
-    if (tile_cost && threadIdx.x == 0) tile_cost[tile] = work;
+    blend_accumulate<W>(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr, chi,
+                        cr, cg, cb, work);
     float l1 = 0.0f;
 #pragma unroll
-    for (int q = 0; q < kStrips; ++q) {
+    for (int q = 0; q < S; ++q) {
         if (!pix.inside[q]) continue;
         const int64_t o = ((int64_t)pix.fy[q] * width + (int64_t)pix.fx) * 3;
         image[o] = cr[q];
@@ -618,9 +697,27 @@ __global__ __launch_bounds__(kWave) void blend_forward_kernel(
             }
         }
     }
-    if (tile_loss) {  // per-tile sum of the L1 terms (reduced by gs_l1_finish)
-        l1 = wave_sum(l1);
-        if (threadIdx.x == 0) tile_loss[tile] = l1;
+    if (tile_loss) l1 = wave_sum(l1);  // per-tile sum of the L1 terms (reduced by gs_l1_finish)
+    if constexpr (W == 1) {
+        if (tile_cost && threadIdx.x == 0) tile_cost[tile] = work;
+        if (tile_loss && threadIdx.x == 0) tile_loss[tile] = l1;
+    } else {  // the waves' sums in wave order
+        if (threadIdx.x % kWave == 0) {
+            wave_l1[threadIdx.x / kWave] = l1;
+            wave_work[threadIdx.x / kWave] = work;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float sum = 0.0f;
+            uint32_t wsum = 0;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                sum += wave_l1[w];
+                wsum += wave_work[w];
+            }
+            if (tile_cost) tile_cost[tile] = wsum;
+            if (tile_loss) tile_loss[tile] = sum;
+        }
     }
 }
 
@@ -662,27 +759,35 @@ __device__ __forceinline__ GradTarget grad_target(int lane, float *g_points, flo
 // Per-lane state of the backward walk: transmittance and the running sum
 // acc = sum_{k<=i} w_k (g.c_k) of the lane's four pixels, their colour
 // gradients g and gC = g.C.
+template <int S>
 struct BackwardLane {
-    float T[kStrips], acc[kStrips];
-    float gr[kStrips], gg[kStrips], gb[kStrips], gC[kStrips];
+    float T[S], acc[S];
+    float gr[S], gg[S], gb[S], gC[S];
 };
 
 // One staged entry j: per-strip gradient terms summed over the lane's pixels,
-// then the nine-field wave sum and one atomic per field (lanes of tgt).
-template <bool kSafe>
-__device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const LanePixels &pix,
+// then the nine-field wave sum and one atomic per field (lanes of tgt).  With
+// W waves per tile each wave sums and adds its own S strips' share.
+template <bool kSafe, int W>
+__device__ __forceinline__ void backward_entry(const BatchLds<W> &s, int j,
+                                               const LanePixels<kStrips / W> &pix,
                                                float alpha_thr, float T_thr, float chi,
-                                               BackwardLane &L, const GradTarget &tgt, bool hi8,
-                                               bool f8_lane) {
-    const float4 geo = s.geo[j];
+                                               BackwardLane<kStrips / W> &L,
+                                               const GradTarget &tgt, bool hi8, bool f8_lane) {
+    constexpr int S = kStrips / W;
     const float4 aux = s.aux[j];
+    uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
+    if constexpr (W > 1) {
+        smask = (smask >> (tile_wave() * S)) & ((1u << S) - 1u);
+        if (smask == 0u) return;  // uniform: none of this wave's strips
+    }
+    const float4 geo = s.geo[j];
     // uniform: a record with a non-finite log2 opacity (only in the select-based
     // path); its opacity gradient is summed as G dalpha (its staged 1 / o is 1)
     const bool special =
         kSafe && special_opacity(__uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(aux.w))));
     const float o_sp = special ? s.o_raw[j] : 0.0f;
     float sGd = -0.0f;
-    const uint32_t smask = __builtin_amdgcn_readfirstlane(__float_as_uint(aux.z));
     const float4 col = s.col[j];
     const float du = pix.fx - geo.x;
     const float Adudu = (geo.z * du) * du;
@@ -695,7 +800,7 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
     float sH = -0.0f, s1 = -0.0f, s2 = -0.0f, sr = -0.0f, sg = -0.0f, sb = -0.0f;
     bool hit = false;  // some strip was evaluated (otherwise every field is -0)
 #pragma unroll
-    for (int q = 0; q < kStrips; ++q) {
+    for (int q = 0; q < S; ++q) {
         if (!((smask >> q) & 1u)) continue;  // uniform
         const float dv = pix.fy[q] - geo.y;
         const float E = fmaf(fmaf(aux.x, dv, B2du), dv, Adudu);
@@ -755,13 +860,15 @@ __device__ __forceinline__ void backward_entry(const BatchLds &s, int j, const L
     }
 }
 
-template <bool kSafe>
-__device__ __forceinline__ void backward_batch(const BatchLds &s, int cnt, const LanePixels &pix,
+template <bool kSafe, int W>
+__device__ __forceinline__ void backward_batch(const BatchLds<W> &s, int cnt,
+                                               const LanePixels<kStrips / W> &pix,
                                                float alpha_thr, float T_thr, float chi,
-                                               BackwardLane &L, const GradTarget &tgt, bool hi8,
-                                               bool f8_lane) {
+                                               BackwardLane<kStrips / W> &L,
+                                               const GradTarget &tgt, bool hi8, bool f8_lane) {
+    if (W > 1 && !any_active(L.T, T_thr)) return;  // this wave's pixels are done
     for (int j = 0; j < cnt; ++j) {
-        backward_entry<kSafe>(s, j, pix, alpha_thr, T_thr, chi, L, tgt, hi8, f8_lane);
+        backward_entry<kSafe, W>(s, j, pix, alpha_thr, T_thr, chi, L, tgt, hi8, f8_lane);
         if ((j & 7) == 7 && !any_active(L.T, T_thr)) break;
     }
 }
@@ -785,8 +892,8 @@ __device__ __forceinline__ void backward_batch(const BatchLds &s, int cnt, const
 //                     times *grad_loss: grad_image holds the target (image required).
 enum { kSeedImage = 0, kSeedDisplay = 1, kSeedL1 = 2 };
 
-template <int kSeed>
-__global__ __launch_bounds__(kWave) void blend_backward_kernel(
+template <int kSeed, int W>
+__global__ __launch_bounds__(kWave * W) void blend_backward_kernel(
     const float *__restrict__ grad_image, const float *__restrict__ image,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
@@ -795,26 +902,27 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
     float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors,
     const float *__restrict__ grad_loss, float inv_count, const float *__restrict__ extra,
     const int32_t *__restrict__ tile_order) {
-    __shared__ BatchLds s;
+    constexpr int S = kStrips / W;
+    __shared__ BatchLds<W> s;
     const float T_thr = effective_T_thr(T_thr_in);
     const int slot = tile_of_block(blockIdx.x, n_tiles);
     const int tile = tile_order ? tile_order[slot] : slot;
     if ((unsigned)tile >= (unsigned)n_tiles) return;  // uniform across the workgroup
-    const LanePixels pix = lane_pixels(tile, tiles_x, width, height);
+    const LanePixels<S> pix = lane_pixels<W>(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
     if (span.end <= span.start) return;  // uniform across the workgroup
     // d loss / d (display / 255) per element, for kSeedL1
     const float l1_scale = kSeed == kSeedL1 ? *grad_loss * inv_count : 0.0f;
 
-    BackwardLane L;
-    float cr[kStrips], cg[kStrips], cb[kStrips];
+    BackwardLane<S> L;
+    float cr[S], cg[S], cb[S];
     uint32_t work = 0;  // unused here
     if (!image)
-        blend_accumulate(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr_in,
-                         chi, cr, cg, cb, work);
+        blend_accumulate<W>(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr,
+                            T_thr_in, chi, cr, cg, cb, work);
     bool finite = true;
 #pragma unroll
-    for (int q = 0; q < kStrips; ++q) {
+    for (int q = 0; q < S; ++q) {
         float gr = 0.0f, gg = 0.0f, gb = 0.0f;
         if (pix.inside[q]) {
             const int64_t o = ((int64_t)pix.fy[q] * width + (int64_t)pix.fx) * 3;
@@ -852,23 +960,25 @@ __global__ __launch_bounds__(kWave) void blend_backward_kernel(
         L.T[q] = live ? 1.0f : kInactiveT;
     }
     // the zero-weight update needs finite gradients and image values in the tile
-    const bool tile_nonfinite = __ballot(!finite) != 0;
+    const bool tile_nonfinite = tile_any<W>(__ballot(!finite) != 0, s.wave_flag_once);
 
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x % kWave;
     const bool hi8 = (lane & 8) != 0;
     const bool f8_lane = lane == 4;
     const GradTarget tgt = grad_target(lane, g_points, g_conics, g_opac, g_colors);
 
-    BatchPipe<true, true> pipe;
+    BatchPipe<true, true, W> pipe;
     pipe.start(span, ids, n, points, conics, opac, colors);
-    for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch) {
-        if (!any_active(L.T, T_thr)) break;
+    for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch * W) {
+        if (!tile_any<W>(any_active(L.T, T_thr), s.wave_flag)) break;
         const Staged st = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
                                        alpha_thr, pix.x0, pix.y0);
         if (st.nonfinite || tile_nonfinite)
-            backward_batch<true>(s, st.count, pix, alpha_thr, T_thr, chi, L, tgt, hi8, f8_lane);
+            backward_batch<true, W>(s, st.count, pix, alpha_thr, T_thr, chi, L, tgt, hi8,
+                                    f8_lane);
         else
-            backward_batch<false>(s, st.count, pix, alpha_thr, T_thr, chi, L, tgt, hi8, f8_lane);
+            backward_batch<false, W>(s, st.count, pix, alpha_thr, T_thr, chi, L, tgt, hi8,
+                                     f8_lane);
     }
 }
 
@@ -1045,6 +1155,25 @@ static int check_blend_args(const int32_t *indexing_offset, const int32_t *ids, 
     return GS_OK;
 }
 
+// Waves per tile of the 16x16 blend kernels.  A grid with few tiles leaves most
+// SIMDs idle, and a kernel then lasts as long as its slowest tile takes on its
+// waves: splitting each tile's strips over 2 or 4 waves (which share the staged
+// batches) shortens that, at the price of each wave reading the entries that
+// reach its strips, and in the backward of a wave sum and atomics per wave and
+// entry.  Measured (blend forward / backward, us, 1 -> 2 -> 4 waves):
+// 256 tiles 101/155 -> 86/118 -> 73/88; 2500 tiles 140/193 -> 138/247 ->
+// 149/352; 3600 tiles 160/210 -> 146/229 -> 152/329; 8160 tiles 159/238 ->
+// 173/396 -> 202/712.
+// Two waves gain only in the 3600-tile forward and lose in every backward, so
+// the default is 4 waves up to kFourWaveTiles tiles and 1 above.
+constexpr int kFourWaveTiles = 1024;
+static int g_blend_waves = 0;  // gs_set_blend_waves: 0 = by tile count
+
+static int blend_waves(int32_t n_tiles) {
+    if (g_blend_waves) return g_blend_waves;
+    return n_tiles <= kFourWaveTiles ? 4 : 1;
+}
+
 static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
                           int32_t n_tiles, int64_t k, const float *points_image,
                           const float *cov_inv_image, const float *opacities, const float *colors,
@@ -1083,7 +1212,11 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
     if (k > 0 && (!points_image || !cov_inv_image || !opacities || !colors))
         return GS_ERR_INVALID_ARGUMENT;
     if (tile_size == kTile) {
-        hipLaunchKernelGGL(blend_forward_kernel, dim3(n_tiles), dim3(kWave), 0, stream,
+        const int W = blend_waves(n_tiles);
+        auto kern = W == 4 ? blend_forward_kernel<4>
+                    : W == 2 ? blend_forward_kernel<2>
+                             : blend_forward_kernel<1>;
+        hipLaunchKernelGGL(kern, dim3(n_tiles), dim3(kWave * W), 0, stream,
                            indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
@@ -1099,6 +1232,12 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                            image);
     }
     return launch_status();
+}
+
+extern "C" int gs_set_blend_waves(int32_t waves) {
+    if (waves != 0 && waves != 1 && waves != 2 && waves != 4) return GS_ERR_INVALID_ARGUMENT;
+    g_blend_waves = waves;
+    return GS_OK;
 }
 
 extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
@@ -1381,10 +1520,20 @@ static int rasterize_backward_impl(
         return GS_ERR_INVALID_ARGUMENT;
     const int tiles_x = (width + tile_size - 1) / tile_size;
     if (tile_size == kTile) {
-        auto kern = seed == kSeedL1       ? blend_backward_kernel<kSeedL1>
-                    : seed == kSeedDisplay ? blend_backward_kernel<kSeedDisplay>
-                                           : blend_backward_kernel<kSeedImage>;
-        hipLaunchKernelGGL(kern, dim3(n_tiles), dim3(kWave), 0, stream, grad_image, image,
+        const int W = blend_waves(n_tiles);
+        auto pick = [&](auto l1, auto disp, auto img) {
+            return seed == kSeedL1 ? l1 : (seed == kSeedDisplay ? disp : img);
+        };
+        auto kern = W == 4 ? pick(blend_backward_kernel<kSeedL1, 4>,
+                                  blend_backward_kernel<kSeedDisplay, 4>,
+                                  blend_backward_kernel<kSeedImage, 4>)
+                    : W == 2 ? pick(blend_backward_kernel<kSeedL1, 2>,
+                                    blend_backward_kernel<kSeedDisplay, 2>,
+                                    blend_backward_kernel<kSeedImage, 2>)
+                             : pick(blend_backward_kernel<kSeedL1, 1>,
+                                    blend_backward_kernel<kSeedDisplay, 1>,
+                                    blend_backward_kernel<kSeedImage, 1>);
+        hipLaunchKernelGGL(kern, dim3(n_tiles), dim3(kWave * W), 0, stream, grad_image, image,
                            indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
                            cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,

@@ -53,6 +53,7 @@ __all__ = [
     "rasterize_display_l1",
     "rasterize_l1_backward",
     "blend_grad_accumulators",
+    "set_blend_waves",
     "fused_ssim",
     "RasterizerError",
 ]
@@ -411,6 +412,12 @@ def blend_grad_accumulators(n, device):
     rasterize_display_l1(clear=...) (which zeroes it) and then as
     rasterize_l1_backward(accumulators=...)."""
     return torch.empty((9 * int(n),), dtype=torch.float32, device=device)
+
+
+def set_blend_waves(waves: int = 0) -> None:
+    """Waves per 16x16 tile of the blend kernels (gs_set_blend_waves): 0 = by the
+    tile count (the default), or 1, 2, 4.  Process-wide."""
+    _lib.check(_lib.load().gs_set_blend_waves(int(waves)), "set_blend_waves")
 
 
 def tile_schedule(n_tiles, device):

@@ -42,6 +42,7 @@ SIGNATURES = {
     "gs_rasterize_display_l1": [_P, _P, _I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 7 + [_I64, _P, _P],
     "gs_l1_finish": [_P, _I32, _I64, _P, _P],
+    "gs_set_blend_waves": [_I32],
     "gs_rasterize_l1_backward": [_P] * 5 + [_I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 4 + [_I32, _F, _P, _P, _P],
     "gs_rasterize_display": [_P, _P, _I32, _I64] + [_P] * 4

@@ -175,6 +175,18 @@ int gs_bin_sort_ordered(const float *points_image, const float *radii, const flo
 /* --------------------------------------------------------------------- blend */
 
 /*
+ * Waves per 16x16 tile of the blend kernels (every gs_rasterize* entry with
+ * tile_size 16): 0, the default, picks by the tile count (4 waves for grids of
+ * at most 1024 tiles, else 1); 1, 2 or 4 force that count.  With
+ * W waves, wave w composites strips w * 4/W .. of the tile's four 16x4 strips
+ * and the waves share each staged batch.  Images are bit-equal for every
+ * setting; gradients and the per-tile loss sums differ only in float summation
+ * order.  Process-wide; not synchronised with launches in flight.  No
+ * counterpart in the reference extension.
+ */
+int gs_set_blend_waves(int32_t waves);
+
+/*
  * Front-to-back alpha compositing of each tile's sorted Gaussian list.
  * Replaces cuda_rasterizer.rasterize (src/cuda/rasterizer.cpp:361-395, kernel
  * src/cuda/kernel.cu:916-987) with the Torch rasterizer's inclusion rules

@@ -22,13 +22,21 @@ pytestmark = pytest.mark.gpu
 INPUTS = ("points_image", "cov_inv_image", "opacities", "colors")
 
 
+@pytest.fixture(params=[1, 2, 4])
+def waves(request):
+    """The blend kernels run each tile on 1, 2 or 4 waves (gs_set_blend_waves)."""
+    cr.set_blend_waves(request.param)
+    yield request.param
+    cr.set_blend_waves(0)
+
+
 def _thresholds(f):
     return (f["width"], f["height"], f["tile_size"], f["alpha_threshold"],
             f["transmittance_threshold"], f["chi_squared_threshold"])
 
 
 @pytest.mark.parametrize("name", ["multitile", "truncated"])
-def test_reference_fixtures(gpu, name):
+def test_reference_fixtures(gpu, name, waves):
     f = helpers.fixture_tensors(name)
     off, ids = cr.compute_tile_intersection(f["points_image"].to(gpu), f["radii"].to(gpu),
                                             f["depths"].to(gpu), f["mask"].to(gpu), f["width"],
@@ -75,7 +83,7 @@ SCENES = {
 
 
 @pytest.mark.parametrize("name", list(SCENES))
-def test_rasterize_shared_inputs(gpu, name):
+def test_rasterize_shared_inputs(gpu, name, waves):
     leaves, off, ids, cam, target = _shared_inputs(SCENES[name]())
     W, H = cam["width"], cam["height"]
     args = (W, H, 16, 1e-4, 1e-4, 9.21)
@@ -120,7 +128,7 @@ def test_rasterize_generic_tile_sizes(gpu, tile):
 @pytest.mark.parametrize("alpha_thr,chi,t_thr", [(0.0, 9.21, 1e-4), (1e-4, 9.21, 1e-4),
                                                  (0.05, 9.21, 1e-4), (1e-4, 4.0, 1e-4),
                                                  (-0.05, 9.21, 0.0)])
-def test_rasterize_thresholds_and_opacity_extremes(gpu, alpha_thr, chi, t_thr):
+def test_rasterize_thresholds_and_opacity_extremes(gpu, alpha_thr, chi, t_thr, waves):
     """The 16x16 kernels' inclusion test (E below min(chi, 2 ln(o / alpha_thr)), staged
     per record) against the oracle's separate chi-square and alpha tests, with
     zero, tiny, near-one and negative opacities among the Gaussians and several

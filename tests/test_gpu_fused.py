@@ -125,6 +125,38 @@ def test_forward_tile_order_changes_nothing_but_the_launch_order(gpu):
         cr.rasterize_display_l1(*args, schedule=first, forward_schedule=first)
 
 
+def test_render_l1_waves_per_tile(gpu):
+    """The fused step with each tile on 1, 2 or 4 waves: display bit-equal, the loss
+    within 1e-6 (summation order of the per-tile sums) and the gradients within
+    1e-5 of one wave.  (The per-tile work counts differ: a batch is 64 records per
+    wave, so the tiles' batch counts differ.)"""
+    p, cam, target = helpers.scene_orbit(20_000, 320, 240, 440.0, seed=27)
+    W, H = cam["width"], cam["height"]
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    runs = {}
+    try:
+        for waves in (1, 2, 4):
+            cr.set_blend_waves(waves)
+            a = _raw_leaves(p, gpu)
+            cache = {}
+            loss, disp, _, _ = render_l1(w2c, K, W, H, a["means"], a["log_scales"],
+                                         a["quats_raw"], a["opacity_logits"], a["sh_dc"],
+                                         a["sh_rest"], tgt, schedule_cache=cache, view_id="v")
+            loss.backward()
+            runs[waves] = (loss.detach(), disp, {k: a[k].grad for k in helpers.PARAMS},
+                           cache["v"][:cache["v"].numel() // 2].clone())
+    finally:
+        cr.set_blend_waves(0)
+    l1, d1, g1, w1 = runs[1]
+    for waves in (2, 4):
+        loss, disp, grads, work = runs[waves]
+        assert torch.equal(disp, d1)
+        assert work.shape == w1.shape and bool((work > 0).any())
+        assert abs(float(loss) - float(l1)) <= 1e-6 * abs(float(l1))
+        for k in helpers.PARAMS:
+            assert helpers.rel_l2(grads[k], g1[k]) <= 1e-5, (waves, k)
+
+
 def test_render_l1_view_schedule_cache(gpu):
     """render_l1 with a per-view schedule cache: the first step of a view fills
     it, the next launches its forward in that order; loss and display are
