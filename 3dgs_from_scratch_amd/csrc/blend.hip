@@ -1264,13 +1264,14 @@ extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
                                     int32_t height, int32_t tile_size, float alpha_threshold,
                                     float transmittance_threshold, float chi_squared_threshold,
                                     float *image, float *display, int32_t *tile_schedule,
-                                    hipStream_t stream) {
+                                    const int32_t *forward_order, hipStream_t stream) {
     if (!display) return GS_ERR_INVALID_ARGUMENT;
     uint32_t *cost = tile_schedule ? reinterpret_cast<uint32_t *>(tile_schedule) : nullptr;
     const int st = rasterize_impl(indexing_offset, gaussian_ids_sorted, n_tiles, k, points_image,
                                   cov_inv_image, opacities, colors, n, width, height, tile_size,
                                   alpha_threshold, transmittance_threshold, chi_squared_threshold,
-                                  image, display, nullptr, nullptr, stream, nullptr, 0, cost);
+                                  image, display, nullptr, nullptr, stream, nullptr, 0, cost,
+                                  forward_order);
     if (st || !tile_schedule || n_tiles == 0) return st;
     return launch_l1_finish(n_tiles, nullptr, 0.0f, nullptr, cost, tile_schedule + n_tiles,
                             stream);

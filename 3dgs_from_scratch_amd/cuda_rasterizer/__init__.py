@@ -435,6 +435,20 @@ def _check_schedule(schedule, n_tiles, dev, who):
                            f"{2 * n_tiles} elements on {dev}")
 
 
+def _check_order(order, schedule, n_tiles, dev, who):
+    """A forward launch order: n_tiles int32 on the device, not inside `schedule`."""
+    if order is None:
+        return
+    if (not isinstance(order, torch.Tensor) or order.dtype != torch.int32
+            or order.device != dev or not order.is_contiguous() or order.numel() < n_tiles):
+        raise RuntimeError(f"{who}: forward_order must be a contiguous int32 tensor of at "
+                           f"least {n_tiles} elements on {dev}")
+    if schedule is not None and (
+            schedule.data_ptr() <= order.data_ptr() < schedule.data_ptr() + schedule.numel() * 4):
+        raise RasterizerError(f"{who}: forward_order must not lie in the schedule this call "
+                              "writes")
+
+
 def rasterize_backward(
     grad_rendered_image,
     indexing_offset,
@@ -582,16 +596,19 @@ def evaluate_spherical_harmonics_render_backward(grad_colors, world_to_camera, p
 
 def rasterize_display(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image,
                       opacities, colors, width, height, tile_size, alpha_threshold,
-                      transmittance_threshold, chi_squared_threshold, schedule=None):
+                      transmittance_threshold, chi_squared_threshold, schedule=None,
+                      forward_order=None):
     """rasterize() that also returns clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294).
     Returns (image[H,W,3] un-clamped, display[H,W,3]).  `schedule` (see
     tile_schedule) receives the work per tile and the order in which
-    rasterize_display_backward, given it, launches the tiles."""
+    rasterize_display_backward, given it, launches the tiles.  `forward_order`:
+    a launch order for this forward (compute_tile_intersection_ordered's)."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
     if schedule is not None:
         _check_schedule(schedule, off.shape[0], dev, "rasterize_display")
+    _check_order(forward_order, schedule, off.shape[0], dev, "rasterize_display")
     image = torch.empty((height, width, 3), dtype=torch.float32, device=dev)
     display = torch.empty((height, width, 3), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
@@ -601,7 +618,7 @@ def rasterize_display(indexing_offset, gaussian_ids_sorted, points_image, cov_in
                 _ptr(off), _ptr(ids), off.shape[0], ids.shape[0], _ptr(pts), _ptr(conic),
                 _ptr(opac), _ptr(col), n, width, height, int(tile_size), float(alpha_threshold),
                 float(transmittance_threshold), float(chi_squared_threshold), _ptr(image),
-                _ptr(display), _ptr(schedule), _stream(dev),
+                _ptr(display), _ptr(schedule), _ptr(forward_order), _stream(dev),
             ),
             "rasterize_display",
         )
@@ -797,16 +814,7 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
         if forward_schedule is not None:
             raise RasterizerError("rasterize_display_l1: pass forward_schedule or forward_order, "
                                   "not both")
-        if (not isinstance(forward_order, torch.Tensor) or forward_order.dtype != torch.int32
-                or forward_order.device != dev or not forward_order.is_contiguous()
-                or forward_order.numel() < n_tiles):
-            raise RuntimeError("rasterize_display_l1: forward_order must be a contiguous int32 "
-                               f"tensor of at least {n_tiles} elements on {dev}")
-        if schedule is not None and (
-                schedule.data_ptr() <= forward_order.data_ptr()
-                < schedule.data_ptr() + schedule.numel() * 4):
-            raise RasterizerError("rasterize_display_l1: forward_order must not lie in the "
-                                  "schedule this call writes")
+        _check_order(forward_order, schedule, n_tiles, dev, "rasterize_display_l1")
         fwd_order = forward_order
     lib = _lib.load()
     with torch.cuda.device(dev):

@@ -46,7 +46,7 @@ SIGNATURES = {
     "gs_rasterize_l1_backward": [_P] * 5 + [_I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 4 + [_I32, _F, _P, _P, _P],
     "gs_rasterize_display": [_P, _P, _I32, _I64] + [_P] * 4
-    + [_I64, _I32, _I32, _I32, _F, _F, _F, _P, _P, _P, _P],
+    + [_I64, _I32, _I32, _I32, _F, _F, _F, _P, _P, _P, _P, _P],
     "gs_rasterize_display_backward": [_P] * 4 + [_I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F]
     + [_P] * 4

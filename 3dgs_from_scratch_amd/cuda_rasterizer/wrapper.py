@@ -107,7 +107,7 @@ class RenderRasterizeFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities,
                 colors, width, height, tile_size, alpha_threshold, transmittance_threshold,
-                chi_squared_threshold, grad_mode=True):
+                chi_squared_threshold, grad_mode=True, forward_order=None):
         # the forward's work per tile orders the backward's tiles (heaviest first);
         # not computed when no backward can follow (grad_mode: the caller's
         # torch.is_grad_enabled(), which is always False inside forward)
@@ -116,7 +116,7 @@ class RenderRasterizeFunction(torch.autograd.Function):
         image, display = _cr.rasterize_display(
             indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities, colors,
             width, height, tile_size, alpha_threshold, transmittance_threshold,
-            chi_squared_threshold, schedule=schedule)
+            chi_squared_threshold, schedule=schedule, forward_order=forward_order)
         ctx.save_for_backward(indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img,
                               opacities, colors, image, schedule)  # schedule may be None
         ctx.params = (width, height, tile_size, alpha_threshold, transmittance_threshold,
@@ -130,7 +130,8 @@ class RenderRasterizeFunction(torch.autograd.Function):
         g_pts, g_conic, g_opac, g_col = _cr.rasterize_display_backward(
             grad_display, offsets, ids, points_img, cov_inv_img, opacities, colors, *ctx.params,
             rendered_image=image, schedule=schedule)
-        return None, None, g_pts, g_conic, g_opac, g_col, None, None, None, None, None, None, None
+        return (None, None, g_pts, g_conic, g_opac, g_col, None, None, None, None, None, None,
+                None, None)
 
 
 class RasterizeFunction(torch.autograd.Function):
@@ -193,13 +194,14 @@ def render(
                                             mask)
 
     tile_size = 16
-    indexing_offset, gaussian_ids_sorted = _cr.compute_tile_intersection(
+    # the tile lists, and a launch order for the blend forward from their lengths
+    indexing_offset, gaussian_ids_sorted, order = _cr.compute_tile_intersection_ordered(
         points_img.detach(), radii, depths, mask, width, height, tile_size)
 
     display = RenderRasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img,
                                             cov_inv_img, opacities, colors, width, height,
                                             tile_size, alpha_threshold, transmittance_threshold,
-                                            chi_squared_threshold, torch.is_grad_enabled())
+                                            chi_squared_threshold, torch.is_grad_enabled(), order)
     return display, points_img, radii
 
 

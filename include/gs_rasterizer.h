@@ -241,6 +241,8 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
  *   display = clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294); tile_size 16.
  *   tile_schedule: null, or 2 * n_tiles int32 that receive the work per tile
  *   and the backward's launch order (as in gs_rasterize_display_l1).
+ *   forward_order: null or a launch order of the tiles, as in
+ *   gs_rasterize_display_l1 (e.g. gs_bin_sort_ordered's).
  * gs_rasterize_display_backward: gs_rasterize_backward given the gradient of
  *   display (image required): the image gradient is grad_display * 255 where
  *   0 <= image <= 1, else 0.  tile_schedule: null, or the buffer that
@@ -261,7 +263,8 @@ int gs_rasterize_display(const int32_t *indexing_offset, const int32_t *gaussian
                          int64_t n, int32_t width, int32_t height, int32_t tile_size,
                          float alpha_threshold, float transmittance_threshold,
                          float chi_squared_threshold, float *image, float *display,
-                         int32_t *tile_schedule, hipStream_t stream);
+                         int32_t *tile_schedule, const int32_t *forward_order,
+                         hipStream_t stream);
 int gs_rasterize_display_backward(const float *grad_display, const float *image,
                                   const int32_t *indexing_offset,
                                   const int32_t *gaussian_ids_sorted, int32_t n_tiles, int64_t k,
