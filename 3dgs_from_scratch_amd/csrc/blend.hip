@@ -1306,136 +1306,73 @@ extern "C" int gs_rasterize_display_l1(
 // XCD's contiguous tile range (the range tile_of_block gives XCD x), the tiles by
 // descending work, ties by tile, so that an XCD starts its heaviest tiles first
 // and the light ones fill the SIMDs as they free up.  order[p] is the tile that
-// the workgroup at range position p processes.  Work is compared through the
-// top 20 bits of its float value (relative resolution 2^-12); ranges of more
-// than kOrderMax tiles keep their own order.  One workgroup per range: each
-// wave sorts a contiguous chunk in registers, then every key's rank is its
-// position in its chunk plus its lower bound in each other chunk.
+// the workgroup at range position p processes.  Work is compared through a
+// 9-bit code, its bit length and the 4 bits below its leading one (16 steps per
+// octave, 4% apart), with tiles of equal code in tile order: a stable counting
+// sort by one workgroup per range (a histogram, then the range in chunks of
+// kFinishThreads tiles, each placed at its code's running start plus its rank
+// among the chunk's tiles of that code, by ballot matching and per-wave counts).
 constexpr int kFinishThreads = 512;
-constexpr int kOrderChunks = kFinishThreads / kWave;  // one wave per chunk
-constexpr int kOrderMaxPerLane = 8;
-constexpr int kOrderChunkMax = kWave * kOrderMaxPerLane;
-constexpr int kOrderMax = kOrderChunks * kOrderChunkMax;
-static_assert(kOrderMax <= 4096, "range positions are 12-bit fields of the keys");
+constexpr int kFinishWaves = kFinishThreads / kWave;
+constexpr int kOrderCodes = 512;
 
-// Ascending keys: descending work, then ascending position in the range.
-__device__ __forceinline__ uint32_t order_key(uint32_t work, int local) {
-    const uint32_t q = __float_as_uint((float)work) >> 11;  // exponent + 12 mantissa bits
-    return ((~q & 0xFFFFFu) << 12) | (uint32_t)local;
-}
-
-// One wave sorts the keys v (lane l holds keys l + e * kWave; bitonic network
-// over kWave * EPT keys).  In the merge step of partner distance j within runs
-// of length k, the lower index of a pair keeps the minimum in ascending runs
-// ((index & k) == 0) and the maximum in descending ones; partners in another
-// lane are exchanged by lane permutes, those in another slot in registers.
-template <int EPT>
-__device__ __forceinline__ void wave_sort(uint32_t (&v)[EPT]) {
-    constexpr int P = kWave * EPT;
-    const int lane = threadIdx.x % kWave;
-    for (int k = 2; k <= P; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            if (j >= kWave) {  // partner in slot e ^ (j / kWave); direction by slot
-                const int ej = j / kWave;
-#pragma unroll
-                for (int e = 0; e < EPT; ++e) {
-                    if (e & ej) continue;
-                    const int e2 = e | ej;
-                    const bool asc = ((e * kWave) & k) == 0;
-                    const uint32_t lo = min(v[e], v[e2]), hi = max(v[e], v[e2]);
-                    v[e] = asc ? lo : hi;
-                    v[e2] = asc ? hi : lo;
-                }
-                continue;
-            }
-            const int addr = (lane ^ j) << 2;
-            const bool lower = (lane & j) == 0;
-            const bool keep_min_l = lower == ((lane & k) == 0);  // k < kWave
-#pragma unroll
-            for (int e = 0; e < EPT; ++e) {
-                const uint32_t w = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v[e]);
-                const bool keep_min = k < kWave ? keep_min_l : (lower == (((e * kWave) & k) == 0));
-                v[e] = keep_min ? min(v[e], w) : max(v[e], w);
-            }
-        }
-    }
-}
-
-template <int EPT>
-__device__ void order_range_sorted(uint32_t (*sorted)[kOrderChunkMax],
-                                   const uint32_t *__restrict__ cost, int start, int len,
-                                   int32_t *__restrict__ order) {
-    const int c = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int q = len / kOrderChunks, r = len % kOrderChunks;
-    const int n = q + (c < r ? 1 : 0), c0 = c * q + min(c, r);
-    uint32_t v[EPT];
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        const int i = e * kWave + lane;
-        v[e] = i < n ? order_key(cost[start + c0 + i], c0 + i) : 0xFFFFFFFFu;
-    }
-    wave_sort<EPT>(v);
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        const int i = e * kWave + lane;
-        if (i < n) sorted[c][i] = v[e];
-    }
-    __syncthreads();
-    // rank = sum over the chunks of the key's lower bound there (its own chunk
-    // gives its position), all searches stepping together
-    int pos[EPT][kOrderChunks];
-#pragma unroll
-    for (int e = 0; e < EPT; ++e)
-#pragma unroll
-        for (int c2 = 0; c2 < kOrderChunks; ++c2) pos[e][c2] = 0;
-    for (int step = kWave * EPT; step > 0; step >>= 1) {
-        // all of a step's reads first (clamped, unconditional), then the updates;
-        // a probe past a chunk's end is discarded
-        uint32_t probe_key[EPT][kOrderChunks];
-#pragma unroll
-        for (int e = 0; e < EPT; ++e)
-#pragma unroll
-            for (int c2 = 0; c2 < kOrderChunks; ++c2) {
-                const int n2 = q + (c2 < r ? 1 : 0);
-                probe_key[e][c2] = sorted[c2][max(min(pos[e][c2] + step, n2) - 1, 0)];
-            }
-#pragma unroll
-        for (int e = 0; e < EPT; ++e)
-#pragma unroll
-            for (int c2 = 0; c2 < kOrderChunks; ++c2) {
-                const int n2 = q + (c2 < r ? 1 : 0);
-                const int probe = pos[e][c2] + step;
-                const bool take = (probe <= n2) & (probe_key[e][c2] < v[e]);
-                pos[e][c2] = take ? probe : pos[e][c2];
-            }
-    }
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        const int i = e * kWave + lane;
-        if (i >= n) continue;
-        int rank = 0;
-#pragma unroll
-        for (int c2 = 0; c2 < kOrderChunks; ++c2) rank += pos[e][c2];
-        if (rank < len) order[start + rank] = start + (int)(v[e] & 0xFFFu);
-    }
+// Ascending codes: descending work (0 for the heaviest class, 511 for no work).
+__device__ __forceinline__ uint32_t order_code(uint32_t work) {
+    if (work == 0u) return kOrderCodes - 1;
+    const uint32_t e = 31u - (uint32_t)__clz(work);  // leading one
+    const uint32_t m = e >= 4u ? (work >> (e - 4u)) & 15u : (work << (4u - e)) & 15u;
+    return (uint32_t)(kOrderCodes - 2) - min(e * 16u + m, (uint32_t)(kOrderCodes - 2));
 }
 
 __device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tiles,
                             int32_t *__restrict__ order) {
-    __shared__ uint32_t sorted[kOrderChunks][kOrderChunkMax];
+    __shared__ uint32_t start_of[kOrderCodes];
+    __shared__ uint32_t wave_cnt[kFinishWaves][kOrderCodes];
     const int base = n_tiles / kXcds, rem = n_tiles % kXcds;
-    const int start = x * base + min(x, rem), len = base + (x < rem ? 1 : 0);
-    const int chunk = (len + kOrderChunks - 1) / kOrderChunks;  // largest chunk
-    if (chunk <= kWave) {
-        order_range_sorted<1>(sorted, cost, start, len, order);
-    } else if (chunk <= 2 * kWave) {
-        order_range_sorted<2>(sorted, cost, start, len, order);
-    } else if (chunk <= 4 * kWave) {
-        order_range_sorted<4>(sorted, cost, start, len, order);
-    } else if (chunk <= kOrderChunkMax) {
-        order_range_sorted<kOrderMaxPerLane>(sorted, cost, start, len, order);
-    } else {
-        for (int i = threadIdx.x; i < len; i += kFinishThreads) order[start + i] = start + i;
+    const int first = x * base + min(x, rem), len = base + (x < rem ? 1 : 0);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    for (int d = threadIdx.x; d < kOrderCodes; d += kFinishThreads) start_of[d] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < len; i += kFinishThreads)
+        atomicAdd(&start_of[order_code(cost[first + i])], 1u);
+    __syncthreads();
+    if (threadIdx.x < kWave) {  // exclusive scan of the 256 counts by one wave
+        uint32_t c[kOrderCodes / kWave], run = 0;
+#pragma unroll
+        for (int e = 0; e < kOrderCodes / kWave; ++e) {
+            c[e] = start_of[lane * (kOrderCodes / kWave) + e];
+            run += c[e];
+        }
+        const uint32_t incl = wave_inclusive_scan(run);
+        uint32_t at = incl - run;
+#pragma unroll
+        for (int e = 0; e < kOrderCodes / kWave; ++e) {
+            start_of[lane * (kOrderCodes / kWave) + e] = at;
+            at += c[e];
+        }
+    }
+    for (int c0 = 0; c0 < len; c0 += kFinishThreads) {
+        for (int d = lane; d < kOrderCodes; d += kWave) wave_cnt[wave][d] = 0u;
+        __syncthreads();
+        const int i = c0 + (int)threadIdx.x;
+        const bool valid = i < len;
+        const uint32_t d = valid ? order_code(cost[first + i]) : 0u;
+        const uint64_t peers = match_digit(d, 9, __ballot(valid));
+        if (valid && (peers & lanemask_lt()) == 0) wave_cnt[wave][d] = (uint32_t)__popcll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t pos = start_of[d] + (uint32_t)__popcll(peers & lanemask_lt());
+            for (int w = 0; w < wave; ++w) pos += wave_cnt[w][d];
+            order[first + (int)pos] = first + i;
+        }
+        __syncthreads();
+        for (int dd = threadIdx.x; dd < kOrderCodes; dd += kFinishThreads) {
+            uint32_t c = 0;
+#pragma unroll
+            for (int w = 0; w < kFinishWaves; ++w) c += wave_cnt[w][dd];
+            start_of[dd] += c;
+        }
+        __syncthreads();  // counts read before the next chunk clears them
     }
 }
 

@@ -314,17 +314,25 @@ def _xcd_ranges(n_tiles):
         start += size
 
 
-# XCD ranges of 0-1 tiles (a 2x2 and a 1x1 grid), 14-15, 1020, 2000 and 4050
-# tiles (one, two, four and eight keys per lane in the per-wave sorts) and of
-# 4224 tiles (kept in band order)
+def _order_code(w):
+    """Work class of the backward's order: 16 steps per octave, heaviest first."""
+    if w == 0:
+        return 511
+    e = int(w).bit_length() - 1
+    m = (w >> (e - 4)) & 15 if e >= 4 else (w << (4 - e)) & 15
+    return 510 - min(e * 16 + m, 510)
+
+
+# XCD ranges of 0-1 tiles (a 2x2 and a 1x1 grid), 14-15, 1020, 2000, 4050 and
+# 4224 tiles (one to nine chunks of 512 in the counting sort)
 @pytest.mark.parametrize("size", [(32, 32), (16, 16), (200, 130), (1920, 1080), (2560, 1600),
                                   (3840, 2160), (4096, 2112)])
 def test_tile_schedule(gpu, size):
     """rasterize_display_l1(schedule=...) leaves the image, display and loss as
-    without it, writes each tile's work and, per XCD range of at most 4096
-    tiles, the tiles by descending work (ties by tile; larger ranges keep their
-    order); rasterize_l1_backward gives the same gradients with the schedule as
-    without (up to the order of the float atomics)."""
+    without it, writes each tile's work and, per XCD range, the tiles by
+    descending work class (_order_code; ties by tile); rasterize_l1_backward
+    gives the same gradients with the schedule as without (up to the order of
+    the float atomics)."""
     W, H = size
     p, cam, target = helpers.scene_box(8_000, W, H, 220.0 * W / 200, seed=25,
                                        log_scale=(-3.5, 0.6))
@@ -348,12 +356,8 @@ def test_tile_schedule(gpu, size):
         assert cost.max() > 0
         for start, length in _xcd_ranges(n_tiles):
             got_order = list(order[start:start + length])
-            if length > 4096:
-                assert got_order == list(range(start, start + length))
-                continue
-            # work compared through the top 20 bits of its float32 value
-            q = (cost[start:start + length].astype("float32").view("uint32") >> 11).astype("int64")
-            want = sorted(range(start, start + length), key=lambda t: (-q[t - start], t))
+            want = sorted(range(start, start + length),
+                          key=lambda t: (_order_code(int(cost[t])), t))
             assert got_order == want
         g = torch.full((1,), 0.7, device=gpu)
         grads = [cr.rasterize_l1_backward(tgt, g, off, ids, pts, conic, opac, colors, W, H,
