@@ -9,15 +9,17 @@
 // with zero padding, C1 = 0.01^2, C2 = 0.03^2, averaged over all pixels or
 // over the pixels at least 5 from the border.
 //
-// Layout.  Work is cut into 64 x 32 output tiles of one plane; a fixed number
-// of persistent workgroups of 256 threads (4 waves) each walk a contiguous run
-// of tiles, channel index fastest.  Per tile a workgroup stages the 74 x 42
-// input window of both images in LDS (any element strides: the reference hands
-// (H, W, C) images permuted to (1, C, H, W)), filters rows (each thread 4
-// consecutive outputs of a row, so every staged value is loaded and squared
-// once per thread), stores the four row sums (x, y, x^2 + y^2, xy), then
-// filters columns (lane = column, each wave 8 output rows); the next tile's
-// window is loaded meanwhile.
+// Layout.  Work is cut into units of 64 columns x 34 (forward) or 56
+// (backward) rows of outputs of one plane, one per wave (lane = output
+// column); a fixed number of workgroups of 4 waves (set by the image geometry
+// alone) walk them.  A wave streams its unit's input rows (10 more than its
+// output rows) top to bottom: each row's 74 staged values (and products x^2 + y^2, xy) go
+// to a wave-private LDS line, each lane filters its 11 neighbours, and the
+// column filter accumulates into an 11-row ring of registers, so an output row
+// is complete (and its SSIM and derivatives formed) 10 rows after its first
+// contribution.  No workgroup barrier inside the walk; input rows are loaded
+// a few rows ahead.  Both passes sum their 11 taps in ascending order, as a
+// separable 2D filter evaluated row pass first does.
 // The forward writes per-pixel derivative maps (planar, coalesced) for the
 // backward, which filters them back the same way.  The mean is reduced
 // deterministically: per-workgroup double partials, then one workgroup.
@@ -32,24 +34,31 @@ namespace {
 constexpr int kRadius = 5;
 constexpr int kTaps = 2 * kRadius + 1;
 constexpr int kTileX = 64;                       // output columns per workgroup (lane = column)
-constexpr int kTileY = 32;                       // output rows per workgroup
-constexpr int kThreads = 256;
+constexpr int kUnitWaves = 4;                    // units (waves) per workgroup
+constexpr int kThreads = kUnitWaves * kWave;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kRowsPerWave = kTileY / kWaves;    // column pass: output rows per thread
-constexpr int kInX = kTileX + 2 * kRadius;       // staged columns (74)
-constexpr int kInY = kTileY + 2 * kRadius;       // staged rows (42)
-constexpr int kPitch = kInX + 1;                 // LDS row pitch of staged values
-constexpr int kQuad = 4;                         // row pass: outputs per thread
-constexpr int kQuadIn = kQuad + 2 * kRadius;     // row pass: inputs per thread (14)
-constexpr int kQuads = kTileX / kQuad;           // row pass: column groups per row (16)
-constexpr int kRowGroups = (kInY + 3) / 4;       // row pass: groups of 4 rows (one wave each)
-constexpr int kRowItems = kRowGroups * 4 * kQuads;
-constexpr int kStageIters = (kInY * kInX + kThreads - 1) / kThreads;
+constexpr int kInX = kTileX + 2 * kRadius;       // staged columns of an input row (74)
+constexpr int kRing = kTaps;                     // output rows accumulating at once
 constexpr float kC1 = 0.01f * 0.01f;
 constexpr float kC2 = 0.03f * 0.03f;
 
-static_assert(kTileX == kWave, "one lane per output column in the column pass");
-static_assert(kTileY % kWaves == 0, "whole rows per wave");
+static_assert(kTileX == kWave, "one lane per output column");
+
+// Unit shape of a pass: kRows output rows per unit (kRows + 2 kRadius input
+// rows, walked in whole ring turns: the rows past them complete output rows
+// past the unit, which are not written), input rows loaded kAheadRows ahead of
+// the filtered one.  Taller units re-read fewer halo rows; the forward, with
+// twice the live registers of the backward, keeps them shorter.
+template <int kRows, int kAheadRows>
+struct Shape {
+    static constexpr int rows = kRows;
+    static constexpr int ahead = kAheadRows;
+    static constexpr int in_rows = kRows + 2 * kRadius;
+    static constexpr int walk = (in_rows + kRing - 1) / kRing * kRing;
+    static_assert(kAheadRows > 0 && kAheadRows < kRing, "prefetch within the ring");
+};
+using FwdShape = Shape<34, 5>;
+using BwdShape = Shape<56, 4>;
 
 struct Window {
     float w[kTaps];
@@ -92,68 +101,6 @@ __device__ __forceinline__ bool in_region(const Planes &p, int y, int x) {
     return y >= kRadius && y < p.height - kRadius && x >= kRadius && x < p.width - kRadius;
 }
 
-// Row pass for NQ quantities: out[q][r][c0 + o] = sum_t w[t] * in_q[r][c0 + o + t],
-// where in_q is produced by `load(r, column)` for the thread's 14 staged inputs.
-// Items (row, group of 4 columns) are spread over the workgroup, 64 per wave:
-// 4 rows x 16 groups, each half-wave taking 8 groups of each of the 4 rows, so
-// that with the odd staging pitch the 32 lanes of a half-wave read 32
-// different banks.
-template <int NQ, typename Load>
-__device__ __forceinline__ void row_pass(const Window &win, float (*out)[kInY][kTileX], Load load) {
-    for (int item = threadIdx.x; item < kRowItems; item += kThreads) {
-        const int l = item % kWave;
-        const int r = (item / kWave) * 4 + (l % 32) / 8;
-        if (r >= kInY) continue;
-        const int c0 = ((l % 8) + 8 * (l / 32)) * kQuad;
-        float acc[NQ][kQuad];
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-#pragma unroll
-            for (int o = 0; o < kQuad; ++o) acc[q][o] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kQuadIn; ++k) {
-            float v[NQ];
-            load(r, c0 + k, v);
-#pragma unroll
-            for (int o = 0; o < kQuad; ++o) {
-                const int t = k - o;
-                if (t < 0 || t >= kTaps) continue;
-#pragma unroll
-                for (int q = 0; q < NQ; ++q) acc[q][o] = fmaf(win.w[t], v[q], acc[q][o]);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-            *reinterpret_cast<float4 *>(&out[q][r][c0]) =
-                make_float4(acc[q][0], acc[q][1], acc[q][2], acc[q][3]);
-    }
-}
-
-// Column pass: acc[q][o] = sum_t w[t] * rows_q[r0 + o + t][lane] for the wave's
-// kRowsPerWave output rows r0 + o.
-template <int NQ>
-__device__ __forceinline__ void column_pass(const Window &win, const float (*rows)[kInY][kTileX],
-                                            int r0, float (&acc)[NQ][kRowsPerWave]) {
-    const int col = threadIdx.x % kWave;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q)
-#pragma unroll
-        for (int o = 0; o < kRowsPerWave; ++o) acc[q][o] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRowsPerWave + 2 * kRadius; ++j) {
-        float h[NQ];
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) h[q] = rows[q][r0 + j][col];
-#pragma unroll
-        for (int o = 0; o < kRowsPerWave; ++o) {
-            const int t = j - o;
-            if (t < 0 || t >= kTaps) continue;
-#pragma unroll
-            for (int q = 0; q < NQ; ++q) acc[q][o] = fmaf(win.w[t], h[q], acc[q][o]);
-        }
-    }
-}
-
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
     for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
@@ -172,16 +119,16 @@ __device__ __forceinline__ double block_sum(double v, double *tmp) {
     return s;
 }
 
-// Tile `t`: tiles run over (batch, tile row, tile column, channel), channel
-// fastest, and each workgroup takes a contiguous run of them (tile_range), so
-// the channels of one region -- interleaved in memory for (H, W, C) images --
-// and the halo shared with the next region are read back to back by one
-// workgroup and come from its XCD's L2 after the first read.
+// Unit `t`: units run over (batch, unit row, unit column, channel), channel
+// fastest, so the channels of one region -- interleaved in memory for (H, W, C)
+// images -- are walked by neighbouring waves at the same time and their rows
+// come from one L2.
 struct Tile {
     int plane, b, c;
     int ox, oy;  // first output column / row
 };
 
+template <int kRows>
 __device__ __forceinline__ Tile tile_of(const Planes &p, int t) {
     Tile r;
     r.c = t % p.channels;
@@ -191,135 +138,254 @@ __device__ __forceinline__ Tile tile_of(const Planes &p, int t) {
     r.b = rest2 / p.tiles_y;
     r.plane = r.b * p.channels + r.c;
     r.ox = tx * kTileX;
-    r.oy = (rest2 % p.tiles_y) * kTileY;
+    r.oy = (rest2 % p.tiles_y) * kRows;
     return r;
 }
 
-// This workgroup's tiles [t0, t1).
-__device__ __forceinline__ void tile_range(const Planes &p, int &t0, int &t1) {
-    const int per = (p.tiles + (int)gridDim.x - 1) / (int)gridDim.x;
-    t0 = min((int)blockIdx.x * per, p.tiles);
-    t1 = min(t0 + per, p.tiles);
+// This lane's staged columns of a unit: ox - kRadius + lane and, for the first
+// 2 kRadius lanes, ox - kRadius + kWave + lane (the right halo).
+struct Cols {
+    int a, b;
+    bool has_b;
+};
+
+__device__ __forceinline__ Cols cols_of(const Tile &t) {
+    const int lane = threadIdx.x % kWave;
+    Cols c;
+    c.a = t.ox - kRadius + lane;
+    c.b = t.ox - kRadius + kWave + lane;
+    c.has_b = lane < 2 * kRadius;
+    return c;
 }
 
-// Staged window element `it` of this thread: (row, column) in the window and
-// whether it lies in the image.
-__device__ __forceinline__ bool stage_pos(const Planes &p, const Tile &t, int it, int &r,
-                                          int &col, int &gy, int &gx) {
-    const int i = threadIdx.x + it * kThreads;
-    r = i / kInX;
-    col = i % kInX;
-    gy = t.oy - kRadius + r;
-    gx = t.ox - kRadius + col;
-    return i < kInY * kInX && gy >= 0 && gy < p.height && gx >= 0 && gx < p.width;
+// Image row gy of both images at the lane's staged columns, as stored (loads
+// at clamped, in-image positions; image_value zeroes the positions outside the
+// image and applies the divisor when the values are used, some rows later, so
+// that no load has to complete before then).
+__device__ __forceinline__ void load_image_row(const Planes &p, const float *b1, const float *b2,
+                                               int gy, const Cols &c, float &xa, float &ya,
+                                               float &xb, float &yb) {
+    int y = min(max(gy, 0), p.height - 1);
+    asm volatile("" : "+v"(y));  // the loads stay at their row (not hoisted ahead)
+    const int ca = min(max(c.a, 0), p.width - 1), cb = min(c.b, p.width - 1);
+    xa = b1[y * p.r1 + ca * p.c1];
+    ya = b2[y * p.r2 + ca * p.c2];
+    xb = b1[y * p.r1 + cb * p.c1];
+    yb = b2[y * p.r2 + cb * p.c2];
 }
 
-// Both images' window of tile t (zero outside the image) into registers.
-__device__ __forceinline__ void load_images(const Planes &p, const Tile &t,
-                                            float (&vx)[kStageIters], float (&vy)[kStageIters]) {
-    const float *b1 = p.img1 + ((int64_t)t.b * p.s1[0] + (int64_t)t.c * p.s1[1]);
-    const float *b2 = p.img2 + ((int64_t)t.b * p.s2[0] + (int64_t)t.c * p.s2[1]);
-#pragma unroll
-    for (int it = 0; it < kStageIters; ++it) {
-        int r, col, gy, gx;
-        const bool in = stage_pos(p, t, it, r, col, gy, gx);
-        vx[it] = in ? img1_value(p, b1[gy * p.r1 + gx * p.c1]) : 0.0f;
-        vy[it] = in ? b2[gy * p.r2 + gx * p.c2] : 0.0f;
-    }
+// Whether image row gy's staged columns a and b lie in the image.
+__device__ __forceinline__ void row_inside(const Planes &p, int gy, const Cols &c, bool &ina,
+                                           bool &inb) {
+    const bool row_in = gy >= 0 && gy < p.height;
+    ina = row_in && c.a >= 0 && c.a < p.width;
+    inb = row_in && c.has_b && c.b < p.width;
 }
 
-// The three planar derivative maps' window of tile t into registers.
-__device__ __forceinline__ void load_maps(const Planes &p, const Tile &t, const float *m0,
-                                          const float *m1, const float *m2,
-                                          float (&v)[3][kStageIters]) {
-    const int64_t base = (int64_t)t.plane * p.height * p.width;
-#pragma unroll
-    for (int it = 0; it < kStageIters; ++it) {
-        int r, col, gy, gx;
-        const bool in = stage_pos(p, t, it, r, col, gy, gx);
-        const int o = gy * p.width + gx;
-        v[0][it] = in ? m0[base + o] : 0.0f;
-        v[1][it] = in ? m1[base + o] : 0.0f;
-        v[2][it] = in ? m2[base + o] : 0.0f;
-    }
+// Row gy of the three planar maps at the lane's staged columns, as stored
+// (clamped loads; zeroed outside the image when used).
+__device__ __forceinline__ void load_map_row(const Planes &p, const float *m0, const float *m1,
+                                             const float *m2, int64_t base, int gy, const Cols &c,
+                                             float (&va)[3], float (&vb)[3]) {
+    int y = min(max(gy, 0), p.height - 1);
+    asm volatile("" : "+v"(y));  // the loads stay at their row (not hoisted ahead)
+    const int ca = min(max(c.a, 0), p.width - 1), cb = min(c.b, p.width - 1);
+    const int64_t o = base + (int64_t)y * p.width;
+    va[0] = m0[o + ca];
+    va[1] = m1[o + ca];
+    va[2] = m2[o + ca];
+    vb[0] = m0[o + cb];
+    vb[1] = m1[o + cb];
+    vb[2] = m2[o + cb];
 }
 
+// img1 / img2 at pixel (gy, gx) as stored (clamped load; zeroed and divided
+// when used).
+__device__ __forceinline__ void load_pixel(const Planes &p, const float *b1, const float *b2,
+                                           int gy, int gx, float &x, float &y) {
+    int yy = min(max(gy, 0), p.height - 1);
+    asm volatile("" : "+v"(yy));  // the loads stay at their row
+    const int xx = min(gx, p.width - 1);
+    x = b1[yy * p.r1 + xx * p.c1];
+    y = b2[yy * p.r2 + xx * p.c2];
+}
+
+// Horizontal filter of the wave's LDS line at this lane's output column:
+// h[q] = sum_k w[k] line[lane + k].q, k ascending.
 template <int NQ>
-__device__ __forceinline__ void store_stage(float (*dst)[kInY][kPitch],
-                                            const float (&v)[NQ][kStageIters]) {
+__device__ __forceinline__ void filter_line(const Window &win, const float4 *line,
+                                            float (&h)[NQ]) {
+    const int lane = threadIdx.x % kWave;
 #pragma unroll
-    for (int it = 0; it < kStageIters; ++it) {
-        const int i = threadIdx.x + it * kThreads;
-        if (i < kInY * kInX)
+    for (int q = 0; q < NQ; ++q) h[q] = 0.0f;
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) dst[q][i / kInX][i % kInX] = v[q][it];
+    for (int k = 0; k < kTaps; ++k) {
+        const float4 v = line[lane + k];
+        const float u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) h[q] = fmaf(win.w[k], u[q], h[q]);
     }
 }
 
-// Persistent: workgroup w handles its tile_range; the next tile's window is
-// loaded into registers while the current one is filtered.  partials[w] = the
-// workgroup's sum of the SSIM map over its region pixels.
+// Makes the wave's LDS line stores visible to the wave's loads that follow
+// (and keeps the next row's stores after this row's loads).
+__device__ __forceinline__ void line_sync() {
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// One input row ri of a unit in the column filter: the row's filtered values h
+// add tap k to output row ri - k (ring slot (ri - k) mod kRing, written as
+// (s - k) mod kRing with s = ri mod kRing), rows above the unit (ri - k < 0)
+// excluded.  kFirst: ri = s (the first kRing rows; the exclusion is then
+// resolved at compile time).
+template <int NQ, bool kFirst, int S>
+__device__ __forceinline__ void ring_add(const Window &win, int ri, const float (&h)[NQ],
+                                         float (&acc)[kRing][NQ]) {
+#pragma unroll
+    for (int k = 0; k < kTaps; ++k) {
+        if (kFirst && S < k) continue;
+        (void)ri;
+        float(&a)[NQ] = acc[(S - k + kRing) % kRing];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) a[q] = fmaf(win.w[k], h[q], a[q]);
+    }
+    // the ring as it stands after this row, in registers: otherwise the
+    // compiler sinks these FMAs to the rows that complete the sums, keeping up
+    // to 10 rows of LDS loads live (hundreds of registers)
+#pragma unroll
+    for (int r = 0; r < kRing; ++r)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(acc[r][q]));
+}
+
+// SSIM of one output (statistics mu1, mu2, E[x^2] + E[y^2], E[xy] of its
+// window) and its derivatives: S and, with the maps, d mean / d (E[x], E[x^2],
+// E[xy]) scaled by g (1 / pixels in the mean, 0 outside the region).
+struct SsimOut {
+    float S, dm, dxx, dxy;
+};
+
+__device__ __forceinline__ SsimOut ssim_point(const float (&a)[4]) {
+    const float mu1 = a[0], mu2 = a[1];
+    const float s_sum = a[2] - mu1 * mu1 - mu2 * mu2;  // sigma1^2 + sigma2^2
+    const float s12 = a[3] - mu1 * mu2;
+    const float C = 2.0f * mu1 * mu2 + kC1;
+    const float D = 2.0f * s12 + kC2;
+    const float A = mu1 * mu1 + mu2 * mu2 + kC1;
+    const float B = s_sum + kC2;
+    const float rA = __builtin_amdgcn_rcpf(A), rB = __builtin_amdgcn_rcpf(B);
+    const float rAB = rA * rB;
+    SsimOut o;
+    o.S = C * D * rAB;
+    // d S / d E[x], d E[x^2], d E[xy] (mu1, E[x^2], E[xy] independent)
+    o.dm = 2.0f * mu2 * (D - C) * rAB + 2.0f * mu1 * o.S * (rB - rA);
+    o.dxx = -o.S * rB;
+    o.dxy = 2.0f * C * rAB;
+    return o;
+}
+
+// Forward of one unit: per input row, x, y, x^2 + y^2 and xy into the LDS line,
+// the horizontal filter, the ring; each completed output row gives its SSIM
+// (summed into `local` over the region) and, with d_mu, the derivative maps.
+template <bool kFirst, int S>
+__device__ __forceinline__ void forward_row(const Planes &p, const Window &win, const Tile &tl,
+                                            const Cols &c, const float *b1, const float *b2,
+                                            float4 *line, int ri, float (&xa)[kRing],
+                                            float (&ya)[kRing], float (&xb)[kRing],
+                                            float (&yb)[kRing], float (&acc)[kRing][4],
+                                            double &local, float *d_mu, float *d_xx,
+                                            float *d_xy) {
+    const int lane = threadIdx.x % kWave;
+    constexpr int kNext = (S + FwdShape::ahead) % kRing;
+    // (rows past the walk load in-image values that are never used)
+    load_image_row(p, b1, b2, tl.oy - kRadius + ri + FwdShape::ahead, c, xa[kNext], ya[kNext],
+                   xb[kNext], yb[kNext]);
+    bool ina, inb;
+    row_inside(p, tl.oy - kRadius + ri, c, ina, inb);
+    const float x = ina ? img1_value(p, xa[S]) : 0.0f, y = ina ? ya[S] : 0.0f;
+    line[lane] = make_float4(x, y, x * x + y * y, x * y);
+    if (c.has_b) {
+        const float x2 = inb ? img1_value(p, xb[S]) : 0.0f, y2 = inb ? yb[S] : 0.0f;
+        line[kWave + lane] = make_float4(x2, y2, x2 * x2 + y2 * y2, x2 * y2);
+    }
+    line_sync();
+    float h[4];
+    filter_line<4>(win, line, h);
+    line_sync();
+    ring_add<4, kFirst, S>(win, ri, h, acc);
+    if (kFirst && S < 2 * kRadius) return;  // no output row complete yet
+    float(&a)[4] = acc[(S + 1) % kRing];   // output row ri - 2 kRadius
+    const int j = ri - 2 * kRadius;
+    const int gy = tl.oy + j;
+    const int gx = tl.ox + lane;
+    if (j < FwdShape::rows && gy < p.height && gx < p.width) {
+        const SsimOut o = ssim_point(a);
+        const bool in = in_region(p, gy, gx);
+        if (in) local += (double)o.S;
+        if (d_mu) {
+            const float g = in ? p.inv_count : 0.0f;
+            int row = gy;
+            asm volatile("" : "+v"(row));  // the addresses are formed here, not ahead
+            const int64_t at = (int64_t)tl.plane * p.height * p.width + (int64_t)row * p.width + gx;
+            d_mu[at] = g * o.dm;
+            d_xx[at] = g * o.dxx;
+            d_xy[at] = g * o.dxy;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = 0.0f;
+}
+
+template <bool kFirst, int S = 0>
+__device__ __forceinline__ void forward_rows(const Planes &p, const Window &win, const Tile &tl,
+                                             const Cols &c, const float *b1, const float *b2,
+                                             float4 *line, int base, float (&xa)[kRing],
+                                             float (&ya)[kRing], float (&xb)[kRing],
+                                             float (&yb)[kRing], float (&acc)[kRing][4],
+                                             double &local, float *d_mu, float *d_xx,
+                                             float *d_xy) {
+    if constexpr (S < kRing) {
+        forward_row<kFirst, S>(p, win, tl, c, b1, b2, line, base + S, xa, ya, xb, yb, acc, local,
+                               d_mu, d_xx, d_xy);
+        forward_rows<kFirst, S + 1>(p, win, tl, c, b1, b2, line, base, xa, ya, xb, yb, acc,
+                                    local, d_mu, d_xx, d_xy);
+    }
+}
+
+// Workgroup w's waves take units w * kUnitWaves + wave, then every
+// gridDim.x * kUnitWaves further; partials[w] = the workgroup's sum of the SSIM
+// map over its region pixels (waves in order).
 __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window win,
                                                                  float *__restrict__ d_mu,
                                                                  float *__restrict__ d_xx,
                                                                  float *__restrict__ d_xy,
                                                                  double *__restrict__ partials) {
-    __shared__ float stage[2][kInY][kPitch];  // x, y
-    __shared__ __align__(16) float rows[4][kInY][kTileX];
+    __shared__ float4 lines[kUnitWaves][kInX];
     __shared__ double red[kWaves];
-    float v[2][kStageIters];
-    int t0, t1;
-    tile_range(p, t0, t1);
-    if (t0 < t1) load_images(p, tile_of(p, t0), v[0], v[1]);
+    const int wave = threadIdx.x / kWave;
+    float4 *line = lines[wave];
     double local = 0.0;
-    const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
-    for (int t = t0; t < t1; ++t) {
-        const Tile tl = tile_of(p, t);
-        __syncthreads();  // the previous tile's row pass is done with `stage`
-        store_stage<2>(stage, v);
-        __syncthreads();
-        if (t + 1 < t1) load_images(p, tile_of(p, t + 1), v[0], v[1]);
-        // row sums of x, y, x^2 + y^2, xy (only the sum of the second moments
-        // enters the SSIM, and its derivative is the same for E[x^2] and E[y^2])
-        row_pass<4>(win, rows, [&](int r, int col, float (&u)[4]) {
-            const float x = stage[0][r][col], y = stage[1][r][col];
-            u[0] = x;
-            u[1] = y;
-            u[2] = x * x + y * y;
-            u[3] = x * y;
-        });
-        __syncthreads();
-        float acc[4][kRowsPerWave];
-        column_pass<4>(win, rows, r0, acc);
-        const int gx = tl.ox + (int)(threadIdx.x % kWave);
-        const int64_t plane_base = (int64_t)tl.plane * p.height * p.width;
+    for (int t = (int)blockIdx.x * kUnitWaves + wave; t < p.tiles;
+         t += (int)gridDim.x * kUnitWaves) {
+        const Tile tl = tile_of<FwdShape::rows>(p, t);
+        const Cols c = cols_of(tl);
+        const float *b1 = p.img1 + ((int64_t)tl.b * p.s1[0] + (int64_t)tl.c * p.s1[1]);
+        const float *b2 = p.img2 + ((int64_t)tl.b * p.s2[0] + (int64_t)tl.c * p.s2[1]);
+        float xa[kRing], ya[kRing], xb[kRing], yb[kRing];
+        float acc[kRing][4];
 #pragma unroll
-        for (int o = 0; o < kRowsPerWave; ++o) {
-            const int gy = tl.oy + r0 + o;
-            if (gy >= p.height || gx >= p.width) continue;
-            const float mu1 = acc[0][o], mu2 = acc[1][o];
-            const float s_sum = acc[2][o] - mu1 * mu1 - mu2 * mu2;  // sigma1^2 + sigma2^2
-            const float s12 = acc[3][o] - mu1 * mu2;
-            const float C = 2.0f * mu1 * mu2 + kC1;
-            const float D = 2.0f * s12 + kC2;
-            const float A = mu1 * mu1 + mu2 * mu2 + kC1;
-            const float B = s_sum + kC2;
-            const float rA = __builtin_amdgcn_rcpf(A), rB = __builtin_amdgcn_rcpf(B);
-            const float rAB = rA * rB;
-            const float S = C * D * rAB;
-            const bool in = in_region(p, gy, gx);
-            if (in) local += (double)S;
-            if (d_mu) {
-                // d S / d E[x], d E[x^2], d E[xy] (mu1, E[x^2], E[xy] independent),
-                // times d mean / d S
-                const float g = in ? p.inv_count : 0.0f;
-                const float dm = 2.0f * mu2 * (D - C) * rAB + 2.0f * mu1 * S * (rB - rA);
-                const int64_t o_ = plane_base + gy * p.width + gx;
-                d_mu[o_] = g * dm;
-                d_xx[o_] = g * (-S * rB);
-                d_xy[o_] = g * (2.0f * C * rAB);
-            }
-        }
+        for (int r = 0; r < kRing; ++r)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[r][q] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < FwdShape::ahead; ++d)
+            load_image_row(p, b1, b2, tl.oy - kRadius + d, c, xa[d], ya[d], xb[d], yb[d]);
+        forward_rows<true>(p, win, tl, c, b1, b2, line, 0, xa, ya, xb, yb, acc, local, d_mu,
+                           d_xx, d_xy);
+        for (int base = kRing; base < FwdShape::walk; base += kRing)
+            forward_rows<false>(p, win, tl, c, b1, b2, line, base, xa, ya, xb, yb, acc, local,
+                                d_mu, d_xx, d_xy);
     }
     const double s = block_sum(local, red);
     if (threadIdx.x == 0) partials[blockIdx.x] = s;
@@ -345,99 +411,134 @@ __global__ __launch_bounds__(kThreads) void ssim_mean_kernel(const double *__res
     }
 }
 
-// Persistent like the forward: the next tile's map window is loaded while the
-// current one is filtered, and a tile's img1 / img2 values at its outputs
-// before its row pass.
+// Backward of one unit: the three maps filtered back the same way; output row
+// j's gradient is up * (F[d_mu] + 2 x F[d_xx] + y F[d_xy]) with x, y its pixel
+// (loaded BwdShape::ahead rows ahead as well).
+struct BwdRows {
+    float ma[kRing][3], mb[kRing][3];  // map rows in flight
+    float xo[kRing], yo[kRing];        // img1 / img2 at the output row completed `ahead` rows on
+};
+
+template <bool kFirst, int S>
+__device__ __forceinline__ void backward_row(const Planes &p, const Window &win, const Tile &tl,
+                                             const Cols &c, const float *m0, const float *m1,
+                                             const float *m2, const float *b1, const float *b2,
+                                             float4 *line, int ri, BwdRows &r,
+                                             float (&acc)[kRing][3], float up, float *bg,
+                                             int gs2, int gs3) {
+    const int lane = threadIdx.x % kWave;
+    const int gx = tl.ox + lane;
+    const int64_t base = (int64_t)tl.plane * p.height * p.width;
+    constexpr int kNext = (S + BwdShape::ahead) % kRing;
+    {  // (rows past the walk load in-image values that are never used)
+        load_map_row(p, m0, m1, m2, base, tl.oy - kRadius + ri + BwdShape::ahead, c,
+                     r.ma[kNext], r.mb[kNext]);
+        // the pixel of the output row that row ri + ahead completes
+        load_pixel(p, b1, b2, tl.oy + ri + BwdShape::ahead - 2 * kRadius, gx, r.xo[kNext],
+                   r.yo[kNext]);
+    }
+    bool ina, inb;
+    row_inside(p, tl.oy - kRadius + ri, c, ina, inb);
+    line[lane] = ina ? make_float4(r.ma[S][0], r.ma[S][1], r.ma[S][2], 0.0f)
+                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (c.has_b)
+        line[kWave + lane] = inb ? make_float4(r.mb[S][0], r.mb[S][1], r.mb[S][2], 0.0f)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    line_sync();
+    float h[3];
+    filter_line<3>(win, line, h);
+    line_sync();
+    ring_add<3, kFirst, S>(win, ri, h, acc);
+    if (kFirst && S < 2 * kRadius) return;
+    float(&a)[3] = acc[(S + 1) % kRing];
+    const int j = ri - 2 * kRadius;
+    const int gy = tl.oy + j;
+    if (j < BwdShape::rows && gy < p.height && gx < p.width) {
+        int row = gy;
+        asm volatile("" : "+v"(row));  // the address is formed here, not ahead
+        const float x = img1_value(p, r.xo[S]), y = r.yo[S];  // an in-image pixel
+        bg[row * gs2 + gx * gs3] = up * (a[0] + 2.0f * x * a[1] + y * a[2]);
+    }
+#pragma unroll
+    for (int q = 0; q < 3; ++q) a[q] = 0.0f;
+}
+
+template <bool kFirst, int S = 0>
+__device__ __forceinline__ void backward_rows(const Planes &p, const Window &win, const Tile &tl,
+                                              const Cols &c, const float *m0, const float *m1,
+                                              const float *m2, const float *b1, const float *b2,
+                                              float4 *line, int base, BwdRows &r,
+                                              float (&acc)[kRing][3], float up, float *bg,
+                                              int gs2, int gs3) {
+    if constexpr (S < kRing) {
+        backward_row<kFirst, S>(p, win, tl, c, m0, m1, m2, b1, b2, line, base + S, r, acc, up,
+                                bg, gs2, gs3);
+        backward_rows<kFirst, S + 1>(p, win, tl, c, m0, m1, m2, b1, b2, line, base, r, acc, up,
+                                     bg, gs2, gs3);
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     Planes p, Window win, const float *__restrict__ grad_mean, const float *__restrict__ d_mu,
     const float *__restrict__ d_xx, const float *__restrict__ d_xy, float *__restrict__ grad,
     int64_t gs0, int64_t gs1, int gs2, int gs3, float grad_scale) {
-    __shared__ float stage[3][kInY][kPitch];
-    __shared__ __align__(16) float rows[3][kInY][kTileX];
-    float v[3][kStageIters];
-    float held[2][kRowsPerWave];
-    int t0, t1;
-    tile_range(p, t0, t1);
-    if (t0 < t1) load_maps(p, tile_of(p, t0), d_mu, d_xx, d_xy, v);
+    __shared__ float4 lines[kUnitWaves][kInX];
+    const int wave = threadIdx.x / kWave;
+    float4 *line = lines[wave];
     const float up = grad_scale * *grad_mean;
-    const bool interleave3 = p.channels == 3 && gs1 == 1 && gs3 == 3;
-    const int r0 = (threadIdx.x / kWave) * kRowsPerWave;
-    for (int t = t0; t < t1; ++t) {
-        const Tile tl = tile_of(p, t);
-        const int gx = tl.ox + (int)(threadIdx.x % kWave);
+    const int lane = threadIdx.x % kWave;
+    for (int t = (int)blockIdx.x * kUnitWaves + wave; t < p.tiles;
+         t += (int)gridDim.x * kUnitWaves) {
+        const Tile tl = tile_of<BwdShape::rows>(p, t);
+        const Cols c = cols_of(tl);
         const float *b1 = p.img1 + ((int64_t)tl.b * p.s1[0] + (int64_t)tl.c * p.s1[1]);
         const float *b2 = p.img2 + ((int64_t)tl.b * p.s2[0] + (int64_t)tl.c * p.s2[1]);
-        float xs[kRowsPerWave], ys[kRowsPerWave];
+        float *bg = grad + ((int64_t)tl.b * gs0 + (int64_t)tl.c * gs1);
+        const int64_t base = (int64_t)tl.plane * p.height * p.width;
+        BwdRows r;
+        float acc[kRing][3];
 #pragma unroll
-        for (int o = 0; o < kRowsPerWave; ++o) {
-            const int gy = tl.oy + r0 + o;
-            const bool in = gy < p.height && gx < p.width;
-            xs[o] = in ? img1_value(p, b1[gy * p.r1 + gx * p.c1]) : 0.0f;
-            ys[o] = in ? b2[gy * p.r2 + gx * p.c2] : 0.0f;
+        for (int k = 0; k < kRing; ++k)
+#pragma unroll
+            for (int q = 0; q < 3; ++q) acc[k][q] = 0.0f;
+        const int gx = tl.ox + lane;
+#pragma unroll
+        for (int d = 0; d < BwdShape::ahead; ++d) {
+            load_map_row(p, d_mu, d_xx, d_xy, base, tl.oy - kRadius + d, c, r.ma[d], r.mb[d]);
+            // (row d completes no output row: d < 2 kRadius)
+            load_pixel(p, b1, b2, tl.oy + d - 2 * kRadius, gx, r.xo[d], r.yo[d]);
         }
-        __syncthreads();
-        store_stage<3>(stage, v);
-        __syncthreads();
-        if (t + 1 < t1) load_maps(p, tile_of(p, t + 1), d_mu, d_xx, d_xy, v);
-        row_pass<3>(win, rows, [&](int r, int col, float (&u)[3]) {
-#pragma unroll
-            for (int q = 0; q < 3; ++q) u[q] = stage[q][r][col];
-        });
-        __syncthreads();
-        float acc[3][kRowsPerWave];
-        column_pass<3>(win, rows, r0, acc);
-        float g[kRowsPerWave];
-#pragma unroll
-        for (int o = 0; o < kRowsPerWave; ++o)
-            g[o] = up * (acc[0][o] + 2.0f * xs[o] * acc[1][o] + ys[o] * acc[2][o]);
-        // Three interleaved channels (the reference's (H, W, 3) layout): the
-        // gradients of channels 0 and 1 of a region wait in registers while this
-        // workgroup filters the next channel, and channel 2 writes all three, so a
-        // wave's stores cover whole lines (else every channel is its own third).
-        const int first_c = t - tl.c;  // the region's channel-0 tile
-        const bool whole = interleave3 && first_c >= t0 && first_c + 2 < t1;
-        if (whole && tl.c < 2) {
-#pragma unroll
-            for (int o = 0; o < kRowsPerWave; ++o) held[tl.c][o] = g[o];
-            continue;
-        }
-        float *bg = grad + ((int64_t)tl.b * gs0 + (int64_t)(whole ? 0 : tl.c) * gs1);
-#pragma unroll
-        for (int o = 0; o < kRowsPerWave; ++o) {
-            const int gy = tl.oy + r0 + o;
-            if (gy >= p.height || gx >= p.width) continue;
-            float *px = bg + (gy * gs2 + gx * gs3);
-            if (whole) {
-                px[0] = held[0][o];
-                px[1] = held[1][o];
-                px[2] = g[o];
-            } else {
-                px[0] = g[o];
-            }
-        }
+        backward_rows<true>(p, win, tl, c, d_mu, d_xx, d_xy, b1, b2, line, 0, r, acc, up, bg,
+                            gs2, gs3);
+        for (int rb = kRing; rb < BwdShape::walk; rb += kRing)
+            backward_rows<false>(p, win, tl, c, d_mu, d_xx, d_xy, b1, b2, line, rb, r, acc, up,
+                                 bg, gs2, gs3);
     }
 }
 
-// Persistent workgroups: two per CU of a 256-CU MI355X (the LDS use allows
-// two), a fixed count so that the per-workgroup partial sums, and so the mean,
-// do not depend on the device.
-constexpr int kPersistentBlocks = 512;
+// Workgroups: one per kUnitWaves units, at most kMaxBlocks (their waves then
+// take several units each).  The count depends on the image geometry alone, so
+// the per-workgroup partial sums, and so the mean, do not depend on the device.
+constexpr int kMaxBlocks = 1024;
 
 struct Geometry {
     int tiles_x, tiles_y, tiles;
     int blocks;
 };
 
+// Units of kRows output rows.
+template <int kRows>
 bool geometry(int32_t batch, int32_t channels, int32_t height, int32_t width, Geometry &g) {
     if (batch <= 0 || channels <= 0 || height <= 0 || width <= 0) return false;
     const int64_t planes = (int64_t)batch * channels;
     if (planes > 65535) return false;
     g.tiles_x = ceil_div(width, kTileX);
-    g.tiles_y = ceil_div(height, kTileY);
+    g.tiles_y = ceil_div(height, kRows);
     const int64_t tiles = planes * g.tiles_x * g.tiles_y;
     if (tiles > 0x7fffffffLL) return false;
     g.tiles = (int)tiles;
-    g.blocks = g.tiles < kPersistentBlocks ? g.tiles : kPersistentBlocks;
+    const int per = ceil_div(g.tiles, kUnitWaves);
+    g.blocks = per < kMaxBlocks ? per : kMaxBlocks;
     return true;
 }
 
@@ -493,7 +594,8 @@ using namespace gs;
 extern "C" int gs_ssim_workspace_size(int32_t batch, int32_t channels, int32_t height,
                                       int32_t width, size_t *bytes) {
     Geometry g;
-    if (!bytes || !geometry(batch, channels, height, width, g)) return GS_ERR_INVALID_ARGUMENT;
+    if (!bytes || !geometry<FwdShape::rows>(batch, channels, height, width, g))
+        return GS_ERR_INVALID_ARGUMENT;
     *bytes = (size_t)g.blocks * sizeof(double);
     return GS_OK;
 }
@@ -511,7 +613,8 @@ int ssim_forward_impl(const float *img1, const int64_t *strides1, const float *i
                       size_t capacity, hipStream_t stream) {
     Geometry g;
     Planes p;
-    if (!geometry(batch, channels, height, width, g) || !ssim_mean || !(img1_divisor > 0.0f))
+    if (!geometry<FwdShape::rows>(batch, channels, height, width, g) || !ssim_mean ||
+        !(img1_divisor > 0.0f))
         return GS_ERR_INVALID_ARGUMENT;
     if (loss && !other_loss) return GS_ERR_INVALID_ARGUMENT;
     int st = fill_planes(p, g, img1, strides1, img2, strides2, channels, height, width,
@@ -535,14 +638,14 @@ int ssim_forward_impl(const float *img1, const int64_t *strides1, const float *i
 }
 
 // Scratch of the allocation-free forward: the per-workgroup partials (one
-// double per persistent workgroup, at most kPersistentBlocks: 4 KiB), in a
+// double per workgroup, at most kMaxBlocks: 8 KiB), in a
 // file-scope device array that every GPU the library runs on holds until the
 // process ends.  Every forward launch writes all the partials its mean kernel
 // reads, so nothing needs clearing between calls; calls that overlap on one GPU
 // (different streams) share the array and race.  In host code the array's name
 // is not a device address: its address on each device comes from
 // hipGetSymbolAddress, taken once per device with that device current.
-constexpr int kScratchPartials = kPersistentBlocks;
+constexpr int kScratchPartials = kMaxBlocks;
 __device__ __align__(256) double scratch[kScratchPartials];
 
 constexpr int kMaxScratchDevices = 64;
@@ -596,9 +699,10 @@ extern "C" int gs_ssim_forward_noalloc(const float *img1, const int64_t *strides
                                        float *dm_dsigma12, const float *other_loss, float lambda,
                                        float *loss, hipStream_t stream) {
     Geometry g;
-    if (!geometry(batch, channels, height, width, g)) return GS_ERR_INVALID_ARGUMENT;
+    if (!geometry<FwdShape::rows>(batch, channels, height, width, g))
+        return GS_ERR_INVALID_ARGUMENT;
     // the partials the launch needs must fit the static array (always true:
-    // geometry() caps the workgroups at kPersistentBlocks)
+    // geometry() caps the workgroups at kMaxBlocks)
     if (g.blocks > kScratchPartials) return GS_ERR_WORKSPACE_TOO_SMALL;
     double *partials = nullptr;
     const int st = scratch_for_stream(stream, &partials);
@@ -618,7 +722,7 @@ extern "C" int gs_ssim_backward(const float *grad_mean, const float *img1,
                                 const int64_t *grad_strides, hipStream_t stream) {
     Geometry g;
     Planes p;
-    if (!geometry(batch, channels, height, width, g) || !(img1_divisor > 0.0f))
+    if (!geometry<BwdShape::rows>(batch, channels, height, width, g) || !(img1_divisor > 0.0f))
         return GS_ERR_INVALID_ARGUMENT;
     int st = fill_planes(p, g, img1, strides1, img2, strides2, channels, height, width, 0);
     if (st) return st;
