@@ -13,13 +13,15 @@
 // (backward) rows of outputs of one plane, one per wave (lane = output
 // column); a fixed number of workgroups of 4 waves (set by the image geometry
 // alone) walk them.  A wave streams its unit's input rows (10 more than its
-// output rows) top to bottom: each row's 74 staged values (and products x^2 + y^2, xy) go
-// to a wave-private LDS line, each lane filters its 11 neighbours, and the
-// column filter accumulates into an 11-row ring of registers, so an output row
-// is complete (and its SSIM and derivatives formed) 10 rows after its first
-// contribution.  No workgroup barrier inside the walk; input rows are loaded
-// a few rows ahead.  Both passes sum their 11 taps in ascending order, as a
-// separable 2D filter evaluated row pass first does.
+// output rows) top to bottom: each row's 74 staged values (and the products
+// x^2 + y^2, xy) go to a wave-private LDS line, each lane filters its 11
+// neighbours, and the column filter accumulates into an 11-row ring of
+// registers, so an output row is complete 10 rows after its first
+// contribution; its SSIM and derivatives are formed during the next row's LDS
+// reads.  No workgroup barrier inside the walk; input rows are loaded a few
+// rows ahead, at wave-uniform row addresses plus per-lane column offsets.
+// Both passes sum their 11 taps in ascending order, as a separable 2D filter
+// evaluated row pass first does.
 // The forward writes per-pixel derivative maps (planar, coalesced) for the
 // backward, which filters them back the same way.  The mean is reduced
 // deterministically: per-workgroup double partials, then one workgroup.
@@ -143,35 +145,71 @@ __device__ __forceinline__ Tile tile_of(const Planes &p, int t) {
 }
 
 // This lane's staged columns of a unit: ox - kRadius + lane and, for the first
-// 2 kRadius lanes, ox - kRadius + kWave + lane (the right halo).
+// 2 kRadius lanes, ox - kRadius + kWave + lane (the right halo); with their
+// byte offsets, clamped into the image, in a row of img1, of img2 and of a
+// planar map, and the byte offsets of the lane's output column (clamped) in a
+// row of img1 and img2.  Row starts are wave-uniform pointers (scalar
+// registers), so a load adds only these per-lane offsets.
 struct Cols {
     int a, b;
     bool has_b;
+    uint32_t a1, b1, a2, b2, am, bm;
+    uint32_t o1, o2;
 };
 
-__device__ __forceinline__ Cols cols_of(const Tile &t) {
+__device__ __forceinline__ Cols cols_of(const Planes &p, const Tile &t) {
     const int lane = threadIdx.x % kWave;
     Cols c;
     c.a = t.ox - kRadius + lane;
     c.b = t.ox - kRadius + kWave + lane;
     c.has_b = lane < 2 * kRadius;
+    const uint32_t ca = (uint32_t)min(max(c.a, 0), p.width - 1);
+    const uint32_t cb = (uint32_t)min(c.b, p.width - 1);
+    const uint32_t co = (uint32_t)min(t.ox + lane, p.width - 1);
+    c.a1 = ca * (uint32_t)p.c1 * 4u;
+    c.b1 = cb * (uint32_t)p.c1 * 4u;
+    c.a2 = ca * (uint32_t)p.c2 * 4u;
+    c.b2 = cb * (uint32_t)p.c2 * 4u;
+    c.am = ca * 4u;
+    c.bm = cb * 4u;
+    c.o1 = co * (uint32_t)p.c1 * 4u;
+    c.o2 = co * (uint32_t)p.c2 * 4u;
     return c;
 }
 
+// The float `byte_offset` bytes past `row`, a wave-uniform pointer: a raw
+// buffer access over the bytes from `row` on, whose base and row offset live in
+// scalar registers and whose per-lane offset is the 32-bit value itself (a
+// plain access would add a 64-bit vector address per load or store).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_of(const float *row) {
+    // stride 0, 2^32 - 1 bytes (no range check in practice), gfx9 data format
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row), (short)0, -1, 0x00020000);
+}
+
+__device__ __forceinline__ float load_at(const float *row, uint32_t byte_offset) {
+    return __uint_as_float(
+        __builtin_amdgcn_raw_buffer_load_b32(span_of(row), (int)byte_offset, 0, 0));
+}
+
+__device__ __forceinline__ void store_at(float *row, uint32_t byte_offset, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), span_of(row), (int)byte_offset, 0,
+                                          0);
+}
+
 // Image row gy of both images at the lane's staged columns, as stored (loads
-// at clamped, in-image positions; image_value zeroes the positions outside the
-// image and applies the divisor when the values are used, some rows later, so
-// that no load has to complete before then).
+// at clamped, in-image positions; the positions outside the image are zeroed
+// and the divisor applied when the values are used, some rows later, so that
+// no load has to complete before then).
 __device__ __forceinline__ void load_image_row(const Planes &p, const float *b1, const float *b2,
                                                int gy, const Cols &c, float &xa, float &ya,
                                                float &xb, float &yb) {
     int y = min(max(gy, 0), p.height - 1);
-    asm volatile("" : "+v"(y));  // the loads stay at their row (not hoisted ahead)
-    const int ca = min(max(c.a, 0), p.width - 1), cb = min(c.b, p.width - 1);
-    xa = b1[y * p.r1 + ca * p.c1];
-    ya = b2[y * p.r2 + ca * p.c2];
-    xb = b1[y * p.r1 + cb * p.c1];
-    yb = b2[y * p.r2 + cb * p.c2];
+    asm volatile("" : "+s"(y));  // the loads stay at their row (not hoisted ahead)
+    const float *r1 = b1 + y * p.r1, *r2 = b2 + y * p.r2;
+    xa = load_at(r1, c.a1);
+    ya = load_at(r2, c.a2);
+    xb = load_at(r1, c.b1);
+    yb = load_at(r2, c.b2);
 }
 
 // Whether image row gy's staged columns a and b lie in the image.
@@ -188,43 +226,57 @@ __device__ __forceinline__ void load_map_row(const Planes &p, const float *m0, c
                                              const float *m2, int64_t base, int gy, const Cols &c,
                                              float (&va)[3], float (&vb)[3]) {
     int y = min(max(gy, 0), p.height - 1);
-    asm volatile("" : "+v"(y));  // the loads stay at their row (not hoisted ahead)
-    const int ca = min(max(c.a, 0), p.width - 1), cb = min(c.b, p.width - 1);
+    asm volatile("" : "+s"(y));  // the loads stay at their row (not hoisted ahead)
     const int64_t o = base + (int64_t)y * p.width;
-    va[0] = m0[o + ca];
-    va[1] = m1[o + ca];
-    va[2] = m2[o + ca];
-    vb[0] = m0[o + cb];
-    vb[1] = m1[o + cb];
-    vb[2] = m2[o + cb];
+    va[0] = load_at(m0 + o, c.am);
+    va[1] = load_at(m1 + o, c.am);
+    va[2] = load_at(m2 + o, c.am);
+    vb[0] = load_at(m0 + o, c.bm);
+    vb[1] = load_at(m1 + o, c.bm);
+    vb[2] = load_at(m2 + o, c.bm);
 }
 
-// img1 / img2 at pixel (gy, gx) as stored (clamped load; zeroed and divided
-// when used).
+// img1 / img2 at row gy of the lane's output column as stored (clamped load;
+// zeroed and divided when used).
 __device__ __forceinline__ void load_pixel(const Planes &p, const float *b1, const float *b2,
-                                           int gy, int gx, float &x, float &y) {
+                                           int gy, const Cols &c, float &x, float &y) {
     int yy = min(max(gy, 0), p.height - 1);
-    asm volatile("" : "+v"(yy));  // the loads stay at their row
-    const int xx = min(gx, p.width - 1);
-    x = b1[yy * p.r1 + xx * p.c1];
-    y = b2[yy * p.r2 + xx * p.c2];
+    asm volatile("" : "+s"(yy));  // the loads stay at their row
+    x = load_at(b1 + yy * p.r1, c.o1);
+    y = load_at(b2 + yy * p.r2, c.o2);
 }
 
-// Horizontal filter of the wave's LDS line at this lane's output column:
-// h[q] = sum_k w[k] line[lane + k].q, k ascending.
-template <int NQ>
-__device__ __forceinline__ void filter_line(const Window &win, const float4 *line,
-                                            float (&h)[NQ]) {
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// The wave's LDS line at this lane's 11 taps (line[lane + k], k = 0..10), the
+// reads issued together.
+__device__ __forceinline__ void read_taps(const float4 *line, f4v (&v)[kTaps]) {
     const int lane = threadIdx.x % kWave;
+    const f4v *src = reinterpret_cast<const f4v *>(line) + lane;
+#pragma unroll
+    for (int k = 0; k < kTaps; ++k) v[k] = src[k];
+}
+
+// Waits for all the taps at once, here: left alone, the compiler keeps two
+// reads in flight and waits on each pair in turn (and work placed between
+// read_taps and this point runs while the reads are in flight).
+__device__ __forceinline__ void taps_ready(f4v (&v)[kTaps]) {
+    static_assert(kTaps == 11, "one operand per tap");
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                 "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]));
+}
+
+// Horizontal filter at this lane's output column: h[q] = sum_k w[k] v[k].q,
+// k ascending.
+template <int NQ>
+__device__ __forceinline__ void filter_taps(const Window &win, const f4v (&v)[kTaps],
+                                            float (&h)[NQ]) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) h[q] = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kTaps; ++k) {
-        const float4 v = line[lane + k];
-        const float u[4] = {v.x, v.y, v.z, v.w};
+    for (int k = 0; k < kTaps; ++k)
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) h[q] = fmaf(win.w[k], u[q], h[q]);
-    }
+        for (int q = 0; q < NQ; ++q) h[q] = fmaf(win.w[k], v[k][q], h[q]);
 }
 
 // Makes the wave's LDS line stores visible to the wave's loads that follow
@@ -285,9 +337,40 @@ __device__ __forceinline__ SsimOut ssim_point(const float (&a)[4]) {
     return o;
 }
 
-// Forward of one unit: per input row, x, y, x^2 + y^2 and xy into the LDS line,
-// the horizontal filter, the ring; each completed output row gives its SSIM
-// (summed into `local` over the region) and, with d_mu, the derivative maps.
+// Output row j of a forward unit, complete in ring slot kSlot: its SSIM
+// (summed into `local` over the region) and, with d_mu, the derivative maps;
+// the slot is then cleared for the output row that starts in it.
+template <int kSlot>
+__device__ __forceinline__ void forward_out(const Planes &p, const Tile &tl, int j,
+                                            float (&acc)[kRing][4], double &local, float *d_mu,
+                                            float *d_xx, float *d_xy) {
+    const int lane = threadIdx.x % kWave;
+    float(&a)[4] = acc[kSlot];
+    const int gy = tl.oy + j;
+    const int gx = tl.ox + lane;
+    if (j < FwdShape::rows && gy < p.height && gx < p.width) {
+        const SsimOut o = ssim_point(a);
+        const bool in = in_region(p, gy, gx);
+        if (in) local += (double)o.S;
+        if (d_mu) {
+            const float g = in ? p.inv_count : 0.0f;
+            int row = gy;
+            asm volatile("" : "+s"(row));  // the addresses are formed here, not ahead
+            const int64_t at = (int64_t)tl.plane * p.height * p.width + (int64_t)row * p.width;
+            const uint32_t col = (uint32_t)gx * 4u;
+            store_at(d_mu + at, col, g * o.dm);
+            store_at(d_xx + at, col, g * o.dxx);
+            store_at(d_xy + at, col, g * o.dxy);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = 0.0f;
+}
+
+// Forward of one unit: per input row ri, x, y, x^2 + y^2 and xy into the LDS
+// line, the horizontal filter, the ring.  Input row ri - 1 completed output row
+// ri - 1 - 2 kRadius in slot S (= ri mod kRing); it is emitted while this row's
+// taps are read, before tap 0 of this row starts the slot again.
 template <bool kFirst, int S>
 __device__ __forceinline__ void forward_row(const Planes &p, const Window &win, const Tile &tl,
                                             const Cols &c, const float *b1, const float *b2,
@@ -310,31 +393,15 @@ __device__ __forceinline__ void forward_row(const Planes &p, const Window &win, 
         line[kWave + lane] = make_float4(x2, y2, x2 * x2 + y2 * y2, x2 * y2);
     }
     line_sync();
+    f4v v[kTaps];
+    read_taps(line, v);
+    // (the first kRing input rows complete no output row before this one)
+    if constexpr (!kFirst) forward_out<S>(p, tl, ri - kRing, acc, local, d_mu, d_xx, d_xy);
+    taps_ready(v);
     float h[4];
-    filter_line<4>(win, line, h);
+    filter_taps<4>(win, v, h);
     line_sync();
     ring_add<4, kFirst, S>(win, ri, h, acc);
-    if (kFirst && S < 2 * kRadius) return;  // no output row complete yet
-    float(&a)[4] = acc[(S + 1) % kRing];   // output row ri - 2 kRadius
-    const int j = ri - 2 * kRadius;
-    const int gy = tl.oy + j;
-    const int gx = tl.ox + lane;
-    if (j < FwdShape::rows && gy < p.height && gx < p.width) {
-        const SsimOut o = ssim_point(a);
-        const bool in = in_region(p, gy, gx);
-        if (in) local += (double)o.S;
-        if (d_mu) {
-            const float g = in ? p.inv_count : 0.0f;
-            int row = gy;
-            asm volatile("" : "+v"(row));  // the addresses are formed here, not ahead
-            const int64_t at = (int64_t)tl.plane * p.height * p.width + (int64_t)row * p.width + gx;
-            d_mu[at] = g * o.dm;
-            d_xx[at] = g * o.dxx;
-            d_xy[at] = g * o.dxy;
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) a[q] = 0.0f;
 }
 
 template <bool kFirst, int S = 0>
@@ -363,13 +430,13 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
                                                                  double *__restrict__ partials) {
     __shared__ float4 lines[kUnitWaves][kInX];
     __shared__ double red[kWaves];
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     float4 *line = lines[wave];
     double local = 0.0;
     for (int t = (int)blockIdx.x * kUnitWaves + wave; t < p.tiles;
          t += (int)gridDim.x * kUnitWaves) {
         const Tile tl = tile_of<FwdShape::rows>(p, t);
-        const Cols c = cols_of(tl);
+        const Cols c = cols_of(p, tl);
         const float *b1 = p.img1 + ((int64_t)tl.b * p.s1[0] + (int64_t)tl.c * p.s1[1]);
         const float *b2 = p.img2 + ((int64_t)tl.b * p.s2[0] + (int64_t)tl.c * p.s2[1]);
         float xa[kRing], ya[kRing], xb[kRing], yb[kRing];
@@ -386,6 +453,9 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
         for (int base = kRing; base < FwdShape::walk; base += kRing)
             forward_rows<false>(p, win, tl, c, b1, b2, line, base, xa, ya, xb, yb, acc, local,
                                 d_mu, d_xx, d_xy);
+        // the output row the last input row completed
+        forward_out<FwdShape::walk % kRing>(p, tl, FwdShape::walk - kRing, acc, local, d_mu,
+                                            d_xx, d_xy);
     }
     const double s = block_sum(local, red);
     if (threadIdx.x == 0) partials[blockIdx.x] = s;
@@ -419,6 +489,29 @@ struct BwdRows {
     float xo[kRing], yo[kRing];        // img1 / img2 at the output row completed `ahead` rows on
 };
 
+// Output row j of a backward unit, complete in ring slot kSlot, with its pixel
+// in xo / yo slot kPix: its gradient; the slot is then cleared.
+template <int kSlot, int kPix>
+__device__ __forceinline__ void backward_out(const Planes &p, const Tile &tl, int j,
+                                             const BwdRows &r, float (&acc)[kRing][3], float up,
+                                             float *bg, int gs2, int gs3) {
+    const int gx = tl.ox + (int)(threadIdx.x % kWave);
+    float(&a)[3] = acc[kSlot];
+    const int gy = tl.oy + j;
+    if (j < BwdShape::rows && gy < p.height && gx < p.width) {
+        int row = gy;
+        asm volatile("" : "+s"(row));  // the address is formed here, not ahead
+        const float x = img1_value(p, r.xo[kPix]), y = r.yo[kPix];  // an in-image pixel
+        store_at(bg + row * gs2, (uint32_t)gx * (uint32_t)gs3 * 4u,
+                 up * (a[0] + 2.0f * x * a[1] + y * a[2]));
+    }
+#pragma unroll
+    for (int q = 0; q < 3; ++q) a[q] = 0.0f;
+}
+
+// One input row ri of a backward unit; as in the forward, output row
+// ri - 1 - 2 kRadius (complete in slot S, its pixel loaded into slot S - 1) is
+// emitted while this row's taps are read.
 template <bool kFirst, int S>
 __device__ __forceinline__ void backward_row(const Planes &p, const Window &win, const Tile &tl,
                                              const Cols &c, const float *m0, const float *m1,
@@ -427,14 +520,13 @@ __device__ __forceinline__ void backward_row(const Planes &p, const Window &win,
                                              float (&acc)[kRing][3], float up, float *bg,
                                              int gs2, int gs3) {
     const int lane = threadIdx.x % kWave;
-    const int gx = tl.ox + lane;
     const int64_t base = (int64_t)tl.plane * p.height * p.width;
     constexpr int kNext = (S + BwdShape::ahead) % kRing;
     {  // (rows past the walk load in-image values that are never used)
         load_map_row(p, m0, m1, m2, base, tl.oy - kRadius + ri + BwdShape::ahead, c,
                      r.ma[kNext], r.mb[kNext]);
         // the pixel of the output row that row ri + ahead completes
-        load_pixel(p, b1, b2, tl.oy + ri + BwdShape::ahead - 2 * kRadius, gx, r.xo[kNext],
+        load_pixel(p, b1, b2, tl.oy + ri + BwdShape::ahead - 2 * kRadius, c, r.xo[kNext],
                    r.yo[kNext]);
     }
     bool ina, inb;
@@ -445,22 +537,15 @@ __device__ __forceinline__ void backward_row(const Planes &p, const Window &win,
         line[kWave + lane] = inb ? make_float4(r.mb[S][0], r.mb[S][1], r.mb[S][2], 0.0f)
                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     line_sync();
+    f4v v[kTaps];
+    read_taps(line, v);
+    if constexpr (!kFirst)
+        backward_out<S, (S + kRing - 1) % kRing>(p, tl, ri - kRing, r, acc, up, bg, gs2, gs3);
+    taps_ready(v);
     float h[3];
-    filter_line<3>(win, line, h);
+    filter_taps<3>(win, v, h);
     line_sync();
     ring_add<3, kFirst, S>(win, ri, h, acc);
-    if (kFirst && S < 2 * kRadius) return;
-    float(&a)[3] = acc[(S + 1) % kRing];
-    const int j = ri - 2 * kRadius;
-    const int gy = tl.oy + j;
-    if (j < BwdShape::rows && gy < p.height && gx < p.width) {
-        int row = gy;
-        asm volatile("" : "+v"(row));  // the address is formed here, not ahead
-        const float x = img1_value(p, r.xo[S]), y = r.yo[S];  // an in-image pixel
-        bg[row * gs2 + gx * gs3] = up * (a[0] + 2.0f * x * a[1] + y * a[2]);
-    }
-#pragma unroll
-    for (int q = 0; q < 3; ++q) a[q] = 0.0f;
 }
 
 template <bool kFirst, int S = 0>
@@ -483,14 +568,13 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     const float *__restrict__ d_xx, const float *__restrict__ d_xy, float *__restrict__ grad,
     int64_t gs0, int64_t gs1, int gs2, int gs3, float grad_scale) {
     __shared__ float4 lines[kUnitWaves][kInX];
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     float4 *line = lines[wave];
     const float up = grad_scale * *grad_mean;
-    const int lane = threadIdx.x % kWave;
     for (int t = (int)blockIdx.x * kUnitWaves + wave; t < p.tiles;
          t += (int)gridDim.x * kUnitWaves) {
         const Tile tl = tile_of<BwdShape::rows>(p, t);
-        const Cols c = cols_of(tl);
+        const Cols c = cols_of(p, tl);
         const float *b1 = p.img1 + ((int64_t)tl.b * p.s1[0] + (int64_t)tl.c * p.s1[1]);
         const float *b2 = p.img2 + ((int64_t)tl.b * p.s2[0] + (int64_t)tl.c * p.s2[1]);
         float *bg = grad + ((int64_t)tl.b * gs0 + (int64_t)tl.c * gs1);
@@ -501,18 +585,20 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
         for (int k = 0; k < kRing; ++k)
 #pragma unroll
             for (int q = 0; q < 3; ++q) acc[k][q] = 0.0f;
-        const int gx = tl.ox + lane;
 #pragma unroll
         for (int d = 0; d < BwdShape::ahead; ++d) {
             load_map_row(p, d_mu, d_xx, d_xy, base, tl.oy - kRadius + d, c, r.ma[d], r.mb[d]);
             // (row d completes no output row: d < 2 kRadius)
-            load_pixel(p, b1, b2, tl.oy + d - 2 * kRadius, gx, r.xo[d], r.yo[d]);
+            load_pixel(p, b1, b2, tl.oy + d - 2 * kRadius, c, r.xo[d], r.yo[d]);
         }
         backward_rows<true>(p, win, tl, c, d_mu, d_xx, d_xy, b1, b2, line, 0, r, acc, up, bg,
                             gs2, gs3);
         for (int rb = kRing; rb < BwdShape::walk; rb += kRing)
             backward_rows<false>(p, win, tl, c, d_mu, d_xx, d_xy, b1, b2, line, rb, r, acc, up,
                                  bg, gs2, gs3);
+        constexpr int kLast = BwdShape::walk % kRing;  // the last input row's output
+        backward_out<kLast, (kLast + kRing - 1) % kRing>(p, tl, BwdShape::walk - kRing, r, acc,
+                                                         up, bg, gs2, gs3);
     }
 }
 
@@ -542,10 +628,12 @@ bool geometry(int32_t batch, int32_t channels, int32_t height, int32_t width, Ge
     return true;
 }
 
-// In-plane offsets are 32-bit: strides must be >= 0 and a plane's last element
-// offset below 2^31.
+// In-plane offsets are 32-bit: strides must be >= 0, a plane's last element
+// offset below 2^31 and a row's last element offset below 2^30 (its byte
+// offset, added to a row start, fits 32 bits).
 bool plane_fits(const int64_t *s, int32_t height, int32_t width) {
     if (s[0] < 0 || s[1] < 0 || s[2] < 0 || s[3] < 0) return false;
+    if (s[3] * (int64_t)(width - 1) >= (1LL << 30)) return false;
     return s[2] * (int64_t)(height - 1) + s[3] * (int64_t)(width - 1) < 0x7fffffffLL;
 }
 

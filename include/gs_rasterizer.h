@@ -454,7 +454,9 @@ int gs_gather_rows(int64_t n_out, const int32_t *src_rows, const uint8_t *fresh_
  * gs_ssim_backward: grad_img1 (element strides grad_strides) = grad_scale *
  *   *grad_mean (device float) times d(mean SSIM)/d x, x = img1 / img1_divisor.
  *   img2 gets no gradient.
- * batch * channels must be <= 65535.
+ * batch * channels must be <= 65535.  Strides must be >= 0, a plane's last
+ * element lie less than 2^31 elements past its first and a row's last less
+ * than 2^30 past its first (GS_ERR_UNSUPPORTED otherwise).
  */
 int gs_ssim_workspace_size(int32_t batch, int32_t channels, int32_t height, int32_t width,
                            size_t *bytes);
@@ -467,13 +469,13 @@ int gs_ssim_forward(const float *img1, const int64_t *strides1, const float *img
 /*
  * gs_ssim_forward_noalloc: gs_ssim_forward without a workspace argument; it
  *   allocates nothing and keeps its per-workgroup partials in a static device
- *   array of 512 doubles (4 KiB) that each GPU the library runs on holds until
+ *   array of 1024 doubles (8 KiB) that each GPU the library runs on holds until
  *   the process ends.  No counterpart in the reference: it is for callers that
  *   cannot allocate (code under HIP graph capture, tight serving loops).  The
  *   current device must be the device of `stream`.  Every call on one GPU uses
  *   the same array: calls that overlap on that GPU (on different streams) race.
  *   Geometries beyond the array are rejected with GS_ERR_WORKSPACE_TOO_SMALL
- *   (none exist: the forward runs at most 512 workgroups).
+ *   (none exist: the forward runs at most 1024 workgroups).
  */
 int gs_ssim_forward_noalloc(const float *img1, const int64_t *strides1, const float *img2,
                             const int64_t *strides2, int32_t batch, int32_t channels,

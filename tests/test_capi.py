@@ -129,6 +129,11 @@ def test_invalid_arguments_rejected_on_host(lib):
                                null, 0.2, fake, fake, 1 << 20, null) == -1  # loss without other
     assert lib.gs_ssim_forward(fake, st, fake, st, 1, 3, 64, 64, 1, 1.0, fake, null, null, null,
                                null, 0.0, null, fake, 0, null) == -2  # workspace too small
+    # a row whose last element lies 2^30 or more elements past its first: unsupported (-4)
+    # (a 33-column row with column stride 2^25, within the 2^31 plane limit)
+    wide = (ctypes.c_int64 * 4)(3 * 64 * 64, 64 * 64, 64, 1 << 25)
+    assert lib.gs_ssim_forward(fake, wide, fake, st, 1, 3, 64, 33, 1, 1.0, fake, null, null, null,
+                               null, 0.0, null, fake, 1 << 20, null) == -4
     assert lib.gs_ssim_backward(fake, fake, st, fake, st, 1, 3, 64, 64, 1.0, fake, fake, null,
                                 1.0, fake, st, null) == -1
     # fused blend entries: missing display / target / tile sums, grids not covering the image,
