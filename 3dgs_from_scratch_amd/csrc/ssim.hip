@@ -9,10 +9,10 @@
 // with zero padding, C1 = 0.01^2, C2 = 0.03^2, averaged over all pixels or
 // over the pixels at least 5 from the border.
 //
-// Layout.  Work is cut into units of 64 columns x 34 (forward) or 56
-// (backward) rows of outputs of one plane, one per wave (lane = output
-// column); a fixed number of workgroups of 4 waves (set by the image geometry
-// alone) walk them.  A wave streams its unit's input rows (10 more than its
+// Layout.  Work is cut into units of 64 columns x 34 rows of outputs of one
+// plane, one per wave (lane = output column); a fixed number of workgroups of
+// 4 waves (set by the image geometry alone) walk them, each XCD a contiguous
+// range.  A wave streams its unit's input rows (10 more than its
 // output rows) top to bottom: each row's 74 staged values (and the products
 // x^2 + y^2, xy) go to a wave-private LDS line, each lane filters its 11
 // neighbours, and the column filter accumulates into an 11-row ring of
@@ -49,8 +49,9 @@ static_assert(kTileX == kWave, "one lane per output column");
 // Unit shape of a pass: kRows output rows per unit (kRows + 2 kRadius input
 // rows, walked in whole ring turns: the rows past them complete output rows
 // past the unit, which are not written), input rows loaded kAheadRows ahead of
-// the filtered one.  Taller units re-read fewer halo rows; the forward, with
-// twice the live registers of the backward, keeps them shorter.
+// the filtered one.  kRows + 2 kRadius a multiple of kRing walks no rows past
+// the unit; taller units re-read fewer halo rows (from L2) but leave fewer
+// waves to fill the GPU.
 template <int kRows, int kAheadRows>
 struct Shape {
     static constexpr int rows = kRows;
@@ -60,7 +61,7 @@ struct Shape {
     static_assert(kAheadRows > 0 && kAheadRows < kRing, "prefetch within the ring");
 };
 using FwdShape = Shape<34, 5>;
-using BwdShape = Shape<56, 4>;
+using BwdShape = Shape<34, 4>;
 
 struct Window {
     float w[kTaps];
@@ -119,6 +120,20 @@ __device__ __forceinline__ double block_sum(double v, double *tmp) {
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) s += tmp[w];
     return s;
+}
+
+// Workgroups are dealt to the kXcds XCDs round robin (workgroup w runs on XCD
+// w % kXcds), each XCD with its own L2.  xcd_block(w) is the logical workgroup
+// whose units w walks: each XCD takes a contiguous range of logical
+// workgroups, so the channels of a region, the neighbouring strips whose halo
+// columns overlap and the unit rows above and below are read through one L2.
+// A bijection of [0, blocks).
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int xcd_block(int w, int blocks) {
+    const int base = blocks / kXcds, rem = blocks % kXcds;
+    const int x = w % kXcds, i = w / kXcds;
+    return x * base + (x < rem ? x : rem) + i;
 }
 
 // Unit `t`: units run over (batch, unit row, unit column, channel), channel
@@ -420,7 +435,7 @@ __device__ __forceinline__ void forward_rows(const Planes &p, const Window &win,
     }
 }
 
-// Workgroup w's waves take units w * kUnitWaves + wave, then every
+// Logical workgroup w's waves take units w * kUnitWaves + wave, then every
 // gridDim.x * kUnitWaves further; partials[w] = the workgroup's sum of the SSIM
 // map over its region pixels (waves in order).
 __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window win,
@@ -432,8 +447,9 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
     __shared__ double red[kWaves];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     float4 *line = lines[wave];
+    const int blk = xcd_block((int)blockIdx.x, (int)gridDim.x);
     double local = 0.0;
-    for (int t = (int)blockIdx.x * kUnitWaves + wave; t < p.tiles;
+    for (int t = blk * kUnitWaves + wave; t < p.tiles;
          t += (int)gridDim.x * kUnitWaves) {
         const Tile tl = tile_of<FwdShape::rows>(p, t);
         const Cols c = cols_of(p, tl);
@@ -458,7 +474,7 @@ __global__ __launch_bounds__(kThreads) void ssim_forward_kernel(Planes p, Window
                                             d_xx, d_xy);
     }
     const double s = block_sum(local, red);
-    if (threadIdx.x == 0) partials[blockIdx.x] = s;
+    if (threadIdx.x == 0) partials[blk] = s;
 }
 
 // *mean = (sum of partials, fixed order) * inv_count; NaN for an empty region.
@@ -571,7 +587,8 @@ __global__ __launch_bounds__(kThreads) void ssim_backward_kernel(
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     float4 *line = lines[wave];
     const float up = grad_scale * *grad_mean;
-    for (int t = (int)blockIdx.x * kUnitWaves + wave; t < p.tiles;
+    const int blk = xcd_block((int)blockIdx.x, (int)gridDim.x);
+    for (int t = blk * kUnitWaves + wave; t < p.tiles;
          t += (int)gridDim.x * kUnitWaves) {
         const Tile tl = tile_of<BwdShape::rows>(p, t);
         const Cols c = cols_of(p, tl);

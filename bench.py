@@ -869,6 +869,30 @@ def profile_step(scene: dict, steps: int) -> int:
     return 0
 
 
+def profile_ssim(scene: dict, steps: int) -> int:
+    """`steps` SSIM loss terms (forward and backward, as run_ssim times them) and
+    nothing else on the GPU after the inputs are copied, for rocprofv3 counter
+    runs over the SSIM kernels alone."""
+    from cuda_rasterizer import fused_ssim
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(5)
+    target = scene["target"].to(dev)
+    img = (scene["target"] + 0.1 * torch.randn(scene["target"].shape, generator=g)).clamp(0, 1).to(dev)
+    img.requires_grad_(True)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        img.grad = None
+        v = 1.0 - fused_ssim(img.permute(2, 0, 1).unsqueeze(0), target.permute(2, 0, 1).unsqueeze(0),
+                             padding="valid")
+        v.backward()
+    torch.cuda.synchronize()
+    W, H = scene["camera"]["width"], scene["camera"]["height"]
+    print(json.dumps({"profiled_ssim_steps": steps, "workload": f"{W}x{H}x3 padding valid",
+                      "ssim": round(1.0 - float(v.detach()), 6)}), flush=True)
+    return 0
+
+
 def copy_calibration(mib: int) -> int:
     """A plain device copy of known size: under rocprofv3 --pmc its FETCH_SIZE and
     WRITE_SIZE per dispatch give the counters' scale (expected: mib * 1024 KiB each)."""
@@ -892,6 +916,9 @@ def main(argv=None):
     ap.add_argument("--profile-step", action="store_true",
                     help="only run warmup + steps fused steps of the chosen configuration (for "
                          "rocprofv3: every dispatch then belongs to a step) and print the count")
+    ap.add_argument("--profile-ssim", action="store_true",
+                    help="only run warmup + steps SSIM loss terms (forward and backward) at the "
+                         "chosen configuration's resolution (for rocprofv3 counter runs)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip configurations 1, 2 and 4 beside the headline")
     ap.add_argument("--path", choices=["fused", "drop-in"], default="fused",
@@ -936,6 +963,8 @@ def main(argv=None):
     scene = CONFIGS[args.config]()
     if args.profile_step:
         return profile_step(scene, args.steps + args.warmup)
+    if args.profile_ssim:
+        return profile_ssim(scene, args.steps + args.warmup)
     res = run_gpu(scene, args.steps, args.warmup, args.path)
     rl = roofline(res, scene["name"])
     drop_in = None
