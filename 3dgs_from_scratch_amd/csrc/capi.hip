@@ -58,4 +58,4 @@ extern "C" const char *gs_status_string(int status) {
     }
 }
 
-extern "C" int gs_abi_version(void) { return 15; }
+extern "C" int gs_abi_version(void) { return 16; }

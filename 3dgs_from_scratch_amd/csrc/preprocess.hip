@@ -215,23 +215,25 @@ __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(
     const float *__restrict__ means, const float *__restrict__ sh_dc,
     const float *__restrict__ sh_rest, const uint8_t *__restrict__ mask, int mode,
     float *__restrict__ colors) {
-    const int64_t i = (int64_t)blockIdx.x * kShBlock + threadIdx.x;
-    if (i >= n) return;
-    float rgb[3] = {0.f, 0.f, 0.f};
-    if (mask[i]) {
-        float cx, cy, cz;
-        camera_position(cam_pos, w2c, cx, cy, cz);
-        const ShView v = sh_view(means + 3 * i, cx, cy, cz);
-        const float *rest = sh_rest + kRest * i;  // 15 x 12-byte loads per thread
+    // one Gaussian per thread; a grid smaller than that walks the rest in strides
+    for (int64_t i = (int64_t)blockIdx.x * kShBlock + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kShBlock) {
+        float rgb[3] = {0.f, 0.f, 0.f};
+        if (mask[i]) {
+            float cx, cy, cz;
+            camera_position(cam_pos, w2c, cx, cy, cz);
+            const ShView v = sh_view(means + 3 * i, cx, cy, cz);
+            const float *rest = sh_rest + kRest * i;  // 15 x 12-byte loads per thread
 #pragma unroll
-        for (int c = 0; c < 3; ++c) rgb[c] = sh_raw_channel(v, sh_dc + 3 * i, rest, c);
-    }
+            for (int c = 0; c < 3; ++c) rgb[c] = sh_raw_channel(v, sh_dc + 3 * i, rest, c);
+        }
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
-        float v = rgb[c];
-        if (mode == kShSigmoid && mask[i]) v = 1.0f / (1.0f + expf(-v));
-        if (mode == kShRender) v = sh_render_value(v);
-        colors[3 * i + c] = v;
+        for (int c = 0; c < 3; ++c) {
+            float v = rgb[c];
+            if (mode == kShSigmoid && mask[i]) v = 1.0f / (1.0f + expf(-v));
+            if (mode == kShRender) v = sh_render_value(v);
+            colors[3 * i + c] = v;
+        }
     }
 }
 
@@ -424,6 +426,7 @@ __global__ __launch_bounds__(kShBlock) void preprocess_forward_kernel(
     radii[2 * i + 1] = p.rv;
     mask[i] = p.keep ? 1 : 0;
     opacities[i] = a.o;
+    if (!colors) return;  // the colours come from another launch
     float rgb[3] = {0.f, 0.f, 0.f};
     if (p.keep) {
         float cx, cy, cz;
@@ -550,14 +553,18 @@ extern "C" int gs_project_points_backward(
     return launch_status();
 }
 
+// max_blocks > 0 caps the grid (its workgroups then take several Gaussians each).
 static int launch_sh_forward(const float *camera_pos, const float *w2c, const float *means,
                              const float *sh_dc, const float *sh_rest, const uint8_t *mask,
-                             int64_t n, int mode, float *colors, hipStream_t stream) {
-    if (n < 0) return GS_ERR_INVALID_ARGUMENT;
+                             int64_t n, int mode, float *colors, hipStream_t stream,
+                             int64_t max_blocks = 0) {
+    if (n < 0 || max_blocks < 0) return GS_ERR_INVALID_ARGUMENT;
     if (n == 0) return GS_OK;
     if ((!camera_pos && !w2c) || !means || !sh_dc || !sh_rest || !mask || !colors)
         return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(sh_forward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
+    int64_t blocks = ceil_div(n, kShBlock);
+    if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
+    hipLaunchKernelGGL(sh_forward_kernel, dim3((unsigned)blocks), dim3(kShBlock), 0,
                        stream, n, camera_pos, w2c, means, sh_dc, sh_rest, mask, mode, colors);
     return launch_status();
 }
@@ -606,6 +613,36 @@ extern "C" int gs_evaluate_sh_render(const float *world_to_camera, const float *
     if (!world_to_camera && n > 0) return GS_ERR_INVALID_ARGUMENT;
     return launch_sh_forward(nullptr, world_to_camera, means, sh_dc, sh_rest, mask, n,
                              kShRender, colors, stream);
+}
+
+// Compute units of the current device (cached per device; 0 if unknown).
+static int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cus[dev] = v;
+    }
+    return cus[dev];
+}
+
+extern "C" int gs_evaluate_sh_render_beside(const float *world_to_camera, const float *means,
+                                            const float *sh_dc, const float *sh_rest,
+                                            const uint8_t *mask, int64_t n, float *colors,
+                                            hipStream_t stream) {
+    if (!world_to_camera && n > 0) return GS_ERR_INVALID_ARGUMENT;
+    // one workgroup per compute unit (measured at config 3 beside binning: 256
+    // workgroups 0.693 ms per fused step, 192 0.698, 320 0.704, 512 0.697, one
+    // per 128 Gaussians 0.714), more when a thread would take over 32 Gaussians
+    const int cus = device_cus();
+    int64_t blocks = cus > 0 ? cus : 256;
+    const int64_t per32 = (n + 32 * kShBlock - 1) / (32 * kShBlock);
+    if (per32 > blocks) blocks = per32;
+    return launch_sh_forward(nullptr, world_to_camera, means, sh_dc, sh_rest, mask, n,
+                             kShRender, colors, stream, blocks);
 }
 
 extern "C" int gs_evaluate_sh_render_backward(const float *grad_colors,
@@ -664,9 +701,9 @@ extern "C" int gs_preprocess_forward(const float *means, const float *log_scales
                                      float *colors, hipStream_t stream) {
     if (n < 0 || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
     if (n == 0) return GS_OK;
-    if (!means || !log_scales || !quats_raw || !opacity_logits || !sh_dc || !sh_rest ||
-        !world_to_camera || !intrinsic || !points_image || !depths || !cov_image ||
-        !cov_inv_image || !radii || !mask || !opacities || !colors ||
+    if (!means || !log_scales || !quats_raw || !opacity_logits ||
+        (colors && (!sh_dc || !sh_rest)) || !world_to_camera || !intrinsic || !points_image ||
+        !depths || !cov_image || !cov_inv_image || !radii || !mask || !opacities ||
         (reinterpret_cast<uintptr_t>(quats_raw) & 15))
         return GS_ERR_INVALID_ARGUMENT;
     hipLaunchKernelGGL(preprocess_forward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,

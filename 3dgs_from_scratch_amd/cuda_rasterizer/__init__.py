@@ -529,9 +529,12 @@ def rasterize_work(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_i
 
 
 def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs_dc,
-                                        sh_coeffs_rest, mask):
+                                        sh_coeffs_rest, mask, out=None, beside=False):
     """max(evaluate_spherical_harmonics(-R^T t, ...) + 0.5, 0) in one kernel
-    (src/cuda/wrapper.py:260-265).  Masked rows are 0.5."""
+    (src/cuda/wrapper.py:260-265).  Masked rows are 0.5.  out: a contiguous
+    (N, 3) float32 tensor to write instead of a new one.  beside: launch it for a
+    stream that runs beside other work (gs_evaluate_sh_render_beside: one
+    workgroup per compute unit; the same values)."""
     dev = _device_of(points_world)
     n = points_world.shape[0]
     f32 = torch.float32
@@ -540,11 +543,20 @@ def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs
     sh_coeffs_dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
     sh_coeffs_rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
     mask = _prep(mask, "mask", torch.bool, (n,), dev)
-    colors = torch.empty((n, 3), dtype=f32, device=dev)
+    if out is None:
+        colors = torch.empty((n, 3), dtype=f32, device=dev)
+    else:
+        if (not isinstance(out, torch.Tensor) or out.dtype != f32 or out.shape != (n, 3)
+                or out.device != dev or not out.is_contiguous()):
+            raise RuntimeError("evaluate_spherical_harmonics_render: out must be a contiguous "
+                               f"({n}, 3) float32 tensor on {dev}")
+        colors = out
     with torch.cuda.device(dev):
         ev = _lib.timer.record("evaluate_sh_render", dev)
+        lib = _lib.load()
+        fn = lib.gs_evaluate_sh_render_beside if beside else lib.gs_evaluate_sh_render
         _lib.check(
-            _lib.load().gs_evaluate_sh_render(
+            fn(
                 _ptr(world_to_camera), _ptr(points_world), _ptr(sh_coeffs_dc),
                 _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(colors), _stream(dev),
             ),
@@ -708,10 +720,11 @@ def activate_backward(grad_scales, grad_quats, grad_opacities, scales, quats_raw
 
 def preprocess_forward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
                        sh_coeffs_rest, world_to_camera, intrinsic, near_plane, far_plane,
-                       min_opacity, min_radius, max_radius, width, height):
+                       min_opacity, min_radius, max_radius, width, height, with_colors=True):
     """activate -> project_points -> evaluate_spherical_harmonics_render in one kernel
     (gs_preprocess_forward).  Returns (points_image, depths, cov_image, cov_inv_image,
-    radii, mask, opacities, colors)."""
+    radii, mask, opacities, colors); with_colors=False skips the colours (None;
+    evaluate_spherical_harmonics_render gives the same values)."""
     dev = _device_of(means)
     n = means.shape[0]
     f32 = torch.float32
@@ -719,17 +732,19 @@ def preprocess_forward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_d
     log_scales = _prep(log_scales, "log_scales", f32, (n, 3), dev)
     quats_raw = _prep(quats_raw, "quats_raw", f32, (n, 4), dev)
     opacity_logits = _prep(opacity_logits, "opacity_logits", f32, (n,), dev)
-    dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
-    rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    dc = rest = colors = None
+    if with_colors:
+        dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+        rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+        colors = torch.empty((n, 3), dtype=f32, device=dev)
     world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
     intrinsic = _prep(intrinsic, "intrinsic", f32, (3, 3), dev)
     out = [torch.empty(shape, dtype=f32, device=dev)
            for shape in ((n, 2), (n,), (n, 3), (n, 3), (n, 2))]
     mask = torch.empty((n,), dtype=torch.bool, device=dev)
     opac = torch.empty((n,), dtype=f32, device=dev)
-    colors = torch.empty((n, 3), dtype=f32, device=dev)
     with torch.cuda.device(dev):
-        ev = _lib.timer.record("preprocess_forward", dev)
+        ev = _lib.timer.record("preprocess_forward" if with_colors else "preprocess_project", dev)
         _lib.check(_lib.load().gs_preprocess_forward(
             _ptr(means), _ptr(log_scales), _ptr(quats_raw), _ptr(opacity_logits), _ptr(dc),
             _ptr(rest), _ptr(world_to_camera), _ptr(intrinsic), n, float(near_plane),

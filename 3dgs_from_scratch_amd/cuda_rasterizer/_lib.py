@@ -34,6 +34,7 @@ SIGNATURES = {
     "gs_rasterize_work": [_P, _P, _I32, _I64] + [_P] * 3 + [_I64, _I32, _I32, _I32, _F, _F, _F]
     + [_P, _P, _P],
     "gs_evaluate_sh_render": [_P] * 5 + [_I64, _P, _P],
+    "gs_evaluate_sh_render_beside": [_P] * 5 + [_I64, _P, _P],
     "gs_evaluate_sh_render_backward": [_P] * 6 + [_I64, _I32] + [_P] * 3 + [_P],
     "gs_activate": [_P] * 3 + [_I64] + [_P] * 3 + [_P],
     "gs_preprocess_forward": [_P] * 8 + [_I64, _F, _F, _F, _F, _F, _I32, _I32] + [_P] * 8 + [_P],

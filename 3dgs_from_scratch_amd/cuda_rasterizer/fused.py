@@ -6,9 +6,10 @@ and computes an L1 loss on the /255 image (:187-191); autograd then runs
 separate PyTorch kernels for each of those steps.  `render_l1` computes the
 same values with the library's kernels only:
 
-  forward   preprocess (activations, projection, SH +0.5 and clamp: one
-            kernel) -> binning -> blend (image, display, per-tile L1 sums) ->
-            loss
+  forward   preprocess (activations and projection: one kernel) -> binning
+            -> blend (image, display, per-tile L1 sums) -> loss; the colours
+            (SH +0.5 and clamp) run on a second stream beside binning, whose
+            chain of small launches leaves most of the GPU idle
   backward  blend backward seeded by the L1 gradient -> preprocess backward
             (projection, SH and activation gradients: one kernel)
 
@@ -36,6 +37,36 @@ import cuda_rasterizer as _cr
 from cuda_rasterizer import ssim as _ssim
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """This device's second stream (default priority), created once."""
+    s = _SIDE_STREAMS.get(dev.index)
+    if s is None:
+        s = _SIDE_STREAMS[dev.index] = torch.cuda.Stream(device=dev)
+    return s
+
+
+def _colors_beside(world_to_camera, means, sh_dc, sh_rest, mask):
+    """The render colours max(SH + 0.5, 0) of the Gaussians in `mask`, computed on
+    the device's second stream once the current stream has produced `mask`.
+    The tensor is allocated on the current stream, and the caller makes that
+    stream wait for the returned event before reading it; every input stays
+    alive until then (saved for the backward or a parameter)."""
+    dev = means.device
+    main = torch.cuda.current_stream(dev)
+    colors = torch.empty((means.shape[0], 3), dtype=torch.float32, device=dev)
+    side = _side_stream(dev)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_dc, sh_rest, mask,
+                                                out=colors, beside=True)
+        done = torch.cuda.Event()
+        done.record(side)
+    return colors, done
+
+
 def _chw(img: torch.Tensor) -> torch.Tensor:
     """(H, W, 3) -> the (1, 3, H, W) view the reference hands to fused_ssim."""
     return img.permute(2, 0, 1).unsqueeze(0)
@@ -48,10 +79,12 @@ class RenderL1Function(torch.autograd.Function):
                 far_plane, min_opacity, min_radius, max_radius, alpha_threshold,
                 transmittance_threshold, chi_squared_threshold, ssim_lambda, ssim_padding,
                 schedule_cache, view_id):
-        pts, depths, cov, conic, radii, mask, opac, colors = _cr.preprocess_forward(
+        pts, depths, cov, conic, radii, mask, opac, _ = _cr.preprocess_forward(
             means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
-            max_radius, width, height)
+            max_radius, width, height, with_colors=False)
+        colors, colors_ready = _colors_beside(world_to_camera, means, sh_coeffs_dc,
+                                              sh_coeffs_rest, mask)
         # with a launch order for the forward's tiles from the list lengths
         off, ids, list_order = _cr.compute_tile_intersection_ordered(pts, radii, depths, mask,
                                                                      width, height, 16)
@@ -66,6 +99,7 @@ class RenderL1Function(torch.autograd.Function):
             if (previous is not None and (previous.device != means.device
                                           or previous.numel() != sched.numel())):
                 previous = None
+        torch.cuda.current_stream(means.device).wait_event(colors_ready)
         # the forward launches heaviest first by the view's last render when there
         # is one, else in the order from the list lengths
         image, display, loss = _cr.rasterize_display_l1(

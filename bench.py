@@ -614,7 +614,10 @@ BLEND_FLOP_PER_PAIR = {"rasterize": 22.0, "rasterize_backward": 70.0, "rasterize
 HBM_STAGES = ("activate", "project_points", "evaluate_sh", "evaluate_sh_render", "bin_count",
               "bin_sort", "evaluate_sh_backward", "evaluate_sh_render_backward",
               "project_points_backward", "activate_backward", "preprocess_forward",
-              "preprocess_backward")
+              "preprocess_project", "preprocess_backward")
+# stages of the fused step that run on a second stream beside binning: their bytes
+# count in the HBM stages, their time does not (it overlaps bin_count and bin_sort)
+SIDE_STAGES = {"preprocess_project": ("evaluate_sh_render",)}
 
 
 def sort_passes(n_tiles: int) -> int:
@@ -660,6 +663,8 @@ def algorithmic_bytes(stage: str, n: int, k: int, n_tiles: int, hw: int) -> floa
         return 24 * hw + k * 76 + 36 * n
     if stage == "preprocess_forward":  # raw parameters + SH -> projection, opacity, colours
         return n * (12 + 12 + 16 + 4 + 12 + 180) + n * (8 + 4 + 12 + 12 + 8 + 1 + 4 + 12)
+    if stage == "preprocess_project":  # raw parameters -> projection, opacity (no colours)
+        return n * (12 + 12 + 16 + 4) + n * (8 + 4 + 12 + 12 + 8 + 1 + 4)
     if stage == "preprocess_backward":  # 4 gradients, raw parameters, SH, cov, mask -> 6 gradients
         return n * (8 + 12 + 4 + 12 + 12 + 12 + 16 + 4 + 12 + 180 + 12 + 1) + \
             n * (12 + 12 + 16 + 4 + 12 + 180)
@@ -685,6 +690,7 @@ STAGE_KERNEL = {"rasterize": "blend_forward_kernel", "rasterize_display": "blend
                 "evaluate_sh_render_backward": "sh_backward_kernel",
                 "project_points_backward": "project_points_backward_kernel",
                 "preprocess_forward": "preprocess_forward_kernel",
+                "preprocess_project": "preprocess_forward_kernel",
                 "preprocess_backward": "preprocess_backward_kernel"}
 
 
@@ -754,10 +760,14 @@ def roofline(res: dict, workload: str) -> dict:
     # HBM-bound stages together (preprocess fwd/bwd, binning and sort)
     hb = sum(algorithmic_bytes(s, n, k, nt, hw) * res["stages"][s][0] / steps
              for s in HBM_STAGES if s in res["stages"])
-    ht = sum(res["stages"][s][1] for s in HBM_STAGES if s in res["stages"]) * 1e-3
+    beside = {b for s, bs in SIDE_STAGES.items() if s in res["stages"] for b in bs}
+    ht = sum(res["stages"][s][1] for s in HBM_STAGES
+             if s in res["stages"] and s not in beside) * 1e-3
     hbm = dict(achieved=round(hb / ht / 1e9, 1) if ht else None, peak=HBM_PEAK_GBS, unit="GB/s",
                frac=round(hb / ht / 1e9 / HBM_PEAK_GBS, 4) if ht else None, bytes=int(hb),
                ms=round(ht * 1e3, 4))
+    if beside:
+        hbm["beside_binning"] = sorted(beside)
     # the reference binning algorithm's bytes per second of this build's binning
     bt = sum(res["stages"][s][1] for s in ("bin_count", "bin_sort") if s in res["stages"]) * 1e-3
     if bt:

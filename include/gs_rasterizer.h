@@ -234,6 +234,11 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
  * gs_evaluate_sh_render: colors = max(gs_evaluate_sh(camera_pos, ...) + 0.5, 0)
  *   with camera_pos = -R^T t taken from world_to_camera
  *   (src/cuda/wrapper.py:260-265); masked rows are 0.5.
+ * gs_evaluate_sh_render_beside: gs_evaluate_sh_render (the same values) for a
+ *   stream that runs beside other work, such as binning's chain of small
+ *   launches: one workgroup per compute unit (more beyond 32 Gaussians per
+ *   thread) walks the Gaussians, leaving the rest of each unit's slots to the
+ *   other stream.
  * gs_evaluate_sh_render_backward: its gradient (the clamp passes the gradient
  *   where raw + 0.5 >= 0, as torch.clamp_min does); accumulate_means != 0 adds
  *   the means gradient to grad_means instead of overwriting it.
@@ -252,6 +257,9 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
 int gs_evaluate_sh_render(const float *world_to_camera, const float *means, const float *sh_dc,
                           const float *sh_rest, const uint8_t *mask, int64_t n, float *colors,
                           hipStream_t stream);
+int gs_evaluate_sh_render_beside(const float *world_to_camera, const float *means,
+                                 const float *sh_dc, const float *sh_rest, const uint8_t *mask,
+                                 int64_t n, float *colors, hipStream_t stream);
 int gs_evaluate_sh_render_backward(const float *grad_colors, const float *world_to_camera,
                                    const float *means, const float *sh_dc, const float *sh_rest,
                                    const uint8_t *mask, int64_t n, int32_t accumulate_means,
@@ -289,7 +297,10 @@ int gs_rasterize_display_backward(const float *grad_display, const float *image,
  * (means, log-scales, raw quaternions, logits, SH dc and rest), recomputing the
  * activations.  Each equals the unfused sequence of the entries it replaces.
  * No counterpart in the reference extension (it leaves activations to PyTorch).
- * quats_raw and grad_quats_raw must be 16-byte aligned.
+ * quats_raw and grad_quats_raw must be 16-byte aligned.  With colors NULL the
+ * forward skips the colours (sh_dc and sh_rest may then be NULL): a caller can
+ * compute them with gs_evaluate_sh_render_beside on another stream, beside
+ * binning.
  */
 int gs_preprocess_forward(const float *means, const float *log_scales, const float *quats_raw,
                           const float *opacity_logits, const float *sh_dc, const float *sh_rest,

@@ -78,6 +78,18 @@ def test_fused_preprocess_equals_unfused_sequence(gpu):
         assert torch.equal(a, b)
     assert torch.equal(fwd[6], o) and torch.equal(fwd[7], col)
     assert 0 < int(ref[5].sum()) < n
+    # without colours (the fused step's launch): the same projection; the colours
+    # from the grid-capped launch meant for a second stream are bit-equal too
+    proj = cr.preprocess_forward(raw["means"], raw["log_scales"], raw["quats_raw"],
+                                 raw["opacity_logits"], raw["sh_dc"], raw["sh_rest"], w2c, K,
+                                 *args, with_colors=False)
+    assert proj[7] is None
+    for a, b in zip(proj[:7], fwd[:7]):
+        assert torch.equal(a, b)
+    out = torch.full((n, 3), float("nan"), device=dev)
+    beside = cr.evaluate_spherical_harmonics_render(w2c, raw["means"], raw["sh_dc"],
+                                                    raw["sh_rest"], ref[5], out=out, beside=True)
+    assert beside is out and torch.equal(beside, col)
     ups = [torch.randn(shape, generator=g).to(dev) for shape in ((n, 2), (n, 3), (n,), (n, 3))]
     got = cr.preprocess_backward(*ups, raw["means"], raw["log_scales"], raw["quats_raw"],
                                  raw["opacity_logits"], raw["sh_dc"], raw["sh_rest"], ref[2],
