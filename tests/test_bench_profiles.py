@@ -31,7 +31,7 @@ def test_committed_profile_feeds_the_bench_line():
     b = load_bench()
     traffic = b.profiled_traffic("rasterize_l1_backward", "config3")
     assert traffic is not None and traffic > 1e8
-    assert b.profiled_traffic("preprocess_forward", "config3") > 1e8
+    assert b.profiled_traffic("preprocess_forward", "config3") > 5e7
     res = {"visited": 261_421_531, "ms": 0.73}
     sr = b.step_roofline(res, "config3")
     assert sr is not None and sr["kernels"] >= 10
