@@ -529,12 +529,15 @@ def rasterize_work(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_i
 
 
 def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs_dc,
-                                        sh_coeffs_rest, mask, out=None, beside=False):
+                                        sh_coeffs_rest, mask, out=None, beside=False,
+                                        stream=None):
     """max(evaluate_spherical_harmonics(-R^T t, ...) + 0.5, 0) in one kernel
     (src/cuda/wrapper.py:260-265).  Masked rows are 0.5.  out: a contiguous
     (N, 3) float32 tensor to write instead of a new one.  beside: launch it for a
     stream that runs beside other work (gs_evaluate_sh_render_beside: one
-    workgroup per compute unit; the same values)."""
+    workgroup per compute unit; the same values).  stream: a torch.cuda.Stream
+    of the tensors' device to launch on (default: the current stream); the
+    caller orders it against the producers and consumers of the tensors."""
     dev = _device_of(points_world)
     n = points_world.shape[0]
     f32 = torch.float32
@@ -552,17 +555,18 @@ def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs
                                f"({n}, 3) float32 tensor on {dev}")
         colors = out
     with torch.cuda.device(dev):
-        ev = _lib.timer.record("evaluate_sh_render", dev)
+        ev = _lib.timer.record("evaluate_sh_render", dev, stream)
         lib = _lib.load()
         fn = lib.gs_evaluate_sh_render_beside if beside else lib.gs_evaluate_sh_render
         _lib.check(
             fn(
                 _ptr(world_to_camera), _ptr(points_world), _ptr(sh_coeffs_dc),
-                _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(colors), _stream(dev),
+                _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(colors),
+                _stream(dev) if stream is None else stream.cuda_stream,
             ),
             "evaluate_spherical_harmonics_render",
         )
-        _lib.timer.stop(ev, dev)
+        _lib.timer.stop(ev, dev, stream)
     return colors
 
 

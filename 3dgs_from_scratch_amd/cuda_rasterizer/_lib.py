@@ -140,21 +140,21 @@ class StageTimer:
         self._used += 1
         return ev
 
-    def record(self, stage: str, device):
+    def record(self, stage: str, device, stream=None):
         import torch
 
         if not self.enabled or (self.only is not None and stage not in self.only):
             return None
         ev = (self._event(), self._event())
-        ev[0].record(torch.cuda.current_stream(device))
+        ev[0].record(stream if stream is not None else torch.cuda.current_stream(device))
         self.events.setdefault(stage, []).append(ev)
         return ev
 
-    def stop(self, ev, device):
+    def stop(self, ev, device, stream=None):
         import torch
 
         if ev is not None:
-            ev[1].record(torch.cuda.current_stream(device))
+            ev[1].record(stream if stream is not None else torch.cuda.current_stream(device))
 
     def summary(self) -> dict:
         import torch

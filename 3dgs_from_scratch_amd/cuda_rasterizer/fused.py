@@ -37,14 +37,16 @@ import cuda_rasterizer as _cr
 from cuda_rasterizer import ssim as _ssim
 
 
-_SIDE_STREAMS: dict = {}
+_SIDE: dict = {}
 
 
-def _side_stream(dev: torch.device) -> torch.cuda.Stream:
-    """This device's second stream (default priority), created once."""
-    s = _SIDE_STREAMS.get(dev.index)
+def _side_stream(dev: torch.device):
+    """This device's second stream (default priority) and the two events that
+    order it against the current stream, created once."""
+    s = _SIDE.get(dev.index)
     if s is None:
-        s = _SIDE_STREAMS[dev.index] = torch.cuda.Stream(device=dev)
+        s = _SIDE[dev.index] = (torch.cuda.Stream(device=dev), torch.cuda.Event(),
+                                torch.cuda.Event())
     return s
 
 
@@ -53,18 +55,18 @@ def _colors_beside(world_to_camera, means, sh_dc, sh_rest, mask):
     the device's second stream once the current stream has produced `mask`.
     The tensor is allocated on the current stream, and the caller makes that
     stream wait for the returned event before reading it; every input stays
-    alive until then (saved for the backward or a parameter)."""
+    alive until then (saved for the backward or a parameter).  The events are
+    reused: each record comes after the previous one's wait was queued."""
     dev = means.device
     main = torch.cuda.current_stream(dev)
     colors = torch.empty((means.shape[0], 3), dtype=torch.float32, device=dev)
-    side = _side_stream(dev)
-    side.wait_stream(main)
-    with torch.cuda.stream(side):
-        _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_dc, sh_rest, mask,
-                                                out=colors, beside=True)
-        done = torch.cuda.Event()
-        done.record(side)
-    return colors, done
+    side, fork, join = _side_stream(dev)
+    fork.record(main)
+    side.wait_event(fork)
+    _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_dc, sh_rest, mask,
+                                            out=colors, beside=True, stream=side)
+    join.record(side)
+    return colors, join
 
 
 def _chw(img: torch.Tensor) -> torch.Tensor:
