@@ -73,6 +73,25 @@ def test_points_img_grad_and_radii(gpu):
     assert helpers.rel_l2(pts_g.grad.cpu() * keep.unsqueeze(1), ref) <= GRAD_TOL
 
 
+def test_render_colours_beside_binning_equal_the_plain_launch(gpu):
+    """With grad enabled render() computes its colours on a second stream while
+    binning runs; without grad on the current stream: the same display, and
+    repeated calls (reused fork/join events) stay bit-equal."""
+    p, cam, _ = helpers.scene_orbit(30_000, 320, 240, 440.0, seed=41)
+    dev = gpu
+    w2c, K = cam["w2c"].to(dev), cam["K"].to(dev)
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in p.items()}
+    scales, quats, opac = helpers.activated(leaves)
+    args = (w2c, K, cam["width"], cam["height"], leaves["means"], scales, quats, opac,
+            leaves["sh_dc"], leaves["sh_rest"])
+    with torch.no_grad():
+        plain, _, _ = render(*args)
+    for _ in range(3):
+        beside, _, _ = render(*args)
+        assert beside.requires_grad
+        assert torch.equal(beside.detach(), plain)
+
+
 def test_render_empty_frame(gpu):
     """Everything behind the camera: black image, zero gradients, no failure."""
     p, cam, target = helpers.scene_box(500, 64, 64, 75.0, seed=4)
