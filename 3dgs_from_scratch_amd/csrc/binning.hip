@@ -1771,6 +1771,7 @@ struct CountWs {
     uint32_t *block_minmax;          // count_tiles: least and greatest key per block
     uint32_t *xform;                 // DepthXform {kmin, shift}
     int64_t *n_live;                 // Gaussians with tiles (keys of depth passes 1..)
+    uint64_t *m_scan;                // the general level 1's entry total (equals M)
     uint32_t *l1_hist;               // one-pass level 1: kRadixMax x l1_blocks(n) table
     uint32_t *l1_totals;             // one-pass level 1: entries per supertile
     void *sort_ws, *scan_ws;
@@ -1793,6 +1794,7 @@ inline CountWs carve_count(void *base, int64_t n) {
     w.block_minmax = c.take<uint32_t>(sort_blocks<kDepthItems>(n) * 2);
     w.xform = c.take<uint32_t>(2);
     w.n_live = c.take<int64_t>(1);
+    w.m_scan = c.take<uint64_t>(1);
     w.l1_hist = c.take<uint32_t>(kRadixMax * l1_blocks(n));
     w.l1_totals = c.take<uint32_t>(kRadixMax);
     w.sort_ws = c.take<char>((int64_t)radix_workspace_bytes<kDepthItems>(n));
@@ -2069,9 +2071,10 @@ int bin_count_finish(const CountCall &c, hipStream_t stream) {
                            w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, nullptr);
         return launch_status();
     }
-    // supertile entry offsets in depth order (the total equals count_tiles' M)
-    return scan_exclusive<uint64_t>(w.counts, w.offsets, c.n,
-                                    reinterpret_cast<uint64_t *>(c.totals + 1), w.scan_ws, stream);
+    // supertile entry offsets in depth order (the total equals count_tiles' M; it
+    // goes to the workspace: totals is not written after the first phase, so a
+    // caller may keep it in host memory and read it once that phase has run)
+    return scan_exclusive<uint64_t>(w.counts, w.offsets, c.n, w.m_scan, w.scan_ws, stream);
 }
 
 }  // namespace gs

@@ -58,4 +58,15 @@ extern "C" const char *gs_status_string(int status) {
     }
 }
 
-extern "C" int gs_abi_version(void) { return 16; }
+extern "C" int gs_abi_version(void) { return 17; }
+
+extern "C" int gs_host_device_pointer(void *host, void **device) {
+    if (!host || !device) return GS_ERR_INVALID_ARGUMENT;
+    *device = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(device, host, 0);
+    if (e != hipSuccess) {
+        *device = nullptr;
+        return (int)e;
+    }
+    return *device ? GS_OK : GS_ERR_UNSUPPORTED;
+}

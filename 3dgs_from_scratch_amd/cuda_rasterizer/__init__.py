@@ -257,6 +257,15 @@ def evaluate_spherical_harmonics_backward(
     return g_means, g_dc, g_rest
 
 
+def _pinned_device_pointer(t: torch.Tensor):
+    """The device address of a pinned host tensor (gs_host_device_pointer), or
+    None when the memory is not mapped for the current device."""
+    out = ctypes.c_void_p(0)
+    if _lib.load().gs_host_device_pointer(_ptr(t), ctypes.byref(out)) != 0 or not out.value:
+        return None
+    return out.value
+
+
 def _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, debug,
                        ordered=False):
     dev = _device_of(points_image)
@@ -276,22 +285,30 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         sz = ctypes.c_size_t(0)
         _lib.check(lib.gs_bin_count_workspace_size(n, ctypes.byref(sz)), "workspace query")
         ws_count = torch.empty((max(sz.value, 1),), dtype=torch.uint8, device=dev)
-        totals = torch.empty((2,), dtype=torch.int64, device=dev)
+        # the one host read (src/cuda/rasterizer.cpp:322): K keys and M supertile
+        # entries, final after the first phase and written by the device straight
+        # into pinned host memory (no copy); waited for after the second phase is
+        # queued, so the GPU keeps working.  Device memory and a copy instead when
+        # the pinned memory is not mapped for the device, and for n = 0 (the
+        # library then zeroes them with a memset)
+        host_totals = torch.empty((2,), dtype=torch.int64, pin_memory=n > 0)
+        totals_ptr = _pinned_device_pointer(host_totals) if n > 0 else None
+        totals = None
+        if totals_ptr is None:  # device memory and a copy
+            totals = torch.empty((2,), dtype=torch.int64, device=dev)
+            totals_ptr = _ptr(totals)
         args = (_ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
-                tile_size, _ptr(ws_count), sz.value, _ptr(totals), stream)
+                tile_size, _ptr(ws_count), sz.value, totals_ptr, stream)
         ev = _lib.timer.record("bin_count", dev)
         _lib.check(lib.gs_bin_count_begin(*args), "compute_tile_intersection (count)")
-        # the one host read (src/cuda/rasterizer.cpp:322): K keys and M supertile
-        # entries are final after the first phase; their copy is queued there and
-        # waited for after the second phase is queued, so the GPU keeps working
-        host_totals = torch.empty((2,), dtype=torch.int64, pin_memory=True)
-        host_totals.copy_(totals, non_blocking=True)
+        if totals is not None and n > 0:
+            host_totals.copy_(totals, non_blocking=True)
         ready = torch.cuda.Event()
         ready.record(torch.cuda.current_stream(dev))
         _lib.check(lib.gs_bin_count_finish(*args), "compute_tile_intersection (count)")
         _lib.timer.stop(ev, dev)
         ready.synchronize()
-        k, m = (int(v) for v in host_totals.tolist())
+        k, m = (int(v) for v in (host_totals if n > 0 else totals.cpu()).tolist())
         if k > 2**31 - 1:
             raise RasterizerError(f"compute_tile_intersection: {k} keys exceed the int32 range")
         sz2 = ctypes.c_size_t(0)

@@ -18,6 +18,7 @@ _PSZ = ctypes.POINTER(ctypes.c_size_t)
 # name -> argtypes (all functions return int status)
 SIGNATURES = {
     "gs_abi_version": [],
+    "gs_host_device_pointer": [_P, ctypes.POINTER(ctypes.c_void_p)],
     "gs_project_points": [_P] * 6 + [_I64, _F, _F, _F, _F, _F, _I32, _I32] + [_P] * 6 + [_P],
     "gs_project_points_backward": [_P] * 8 + [_I64, _I32, _I32] + [_P] * 5 + [_P],
     "gs_evaluate_sh": [_P] * 5 + [_I64, _I32, _P, _P],

@@ -44,6 +44,12 @@ const char *gs_status_string(int status);
 /* Version of this ABI (incremented on any signature change). */
 int gs_abi_version(void);
 
+/* The device address of pinned host memory (hipHostMalloc) for the current
+ * device, for entries that write a few values straight to the host (e.g. the
+ * totals of gs_bin_count).  Non-zero status (and *device = NULL) when the
+ * memory is not mapped for the device.  No counterpart in the reference. */
+int gs_host_device_pointer(void *host, void **device);
+
 /* ---------------------------------------------------------------- preprocess */
 
 /*
@@ -110,7 +116,7 @@ int gs_evaluate_sh_backward(const float *grad_colors, const float *camera_pos,
  *     kernel.cu:784-818 semantics), a stable sort of the Gaussians with tiles
  *     by depth bits, and the placement of their supertile entries (a supertile
  *     is 8 x 8 tiles): per-supertile counts and positions when the grid has at
- *     most 256 supertiles, else an exclusive scan.  Writes two device int64:
+ *     most 256 supertiles, else an exclusive scan.  Writes two int64:
  *     totals[0] = K, the number of (tile, Gaussian) keys, and totals[1] = M,
  *     the number of (supertile, Gaussian) entries (M <= K).  Keeps its state in
  *     `workspace`, which gs_bin_sort reads.
@@ -126,10 +132,13 @@ int gs_evaluate_sh_backward(const float *grad_colors, const float *camera_pos,
  *
  * gs_bin_count = gs_bin_count_begin followed by gs_bin_count_finish (same
  * arguments).  totals is final once the work gs_bin_count_begin launched has
- * run, so a caller can queue its copy of totals between the two calls and wait
- * for that copy after queueing gs_bin_count_finish: the host read of K and M
- * then overlaps the second phase instead of idling the GPU (the reference reads
- * num_rendered with .item() after all of its counting, rasterizer.cpp:322).
+ * run, and nothing writes it after that, so a caller can queue its copy of
+ * totals between the two calls and wait for that copy after queueing
+ * gs_bin_count_finish: the host read of K and M then overlaps the second phase
+ * instead of idling the GPU (the reference reads num_rendered with .item()
+ * after all of its counting, rasterizer.cpp:322).  totals may also be pinned
+ * host memory the device can write (hipHostMalloc): the host then reads it
+ * directly after an event recorded between the two calls, with no copy.
  */
 int gs_bin_count_workspace_size(int64_t n, size_t *bytes);
 int gs_bin_count(const float *points_image, const float *radii, const float *depths,

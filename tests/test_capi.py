@@ -46,11 +46,17 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 16
+    assert lib.gs_abi_version() == 17
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
     assert lib.gs_status_string(-99) == b"unknown status"
+
+
+def test_host_device_pointer_rejects_null(lib):
+    out = ctypes.c_void_p(123)
+    assert lib.gs_host_device_pointer(None, ctypes.byref(out)) == -1
+    assert lib.gs_host_device_pointer(ctypes.c_void_p(256), None) == -1
 
 
 def test_workspace_queries(lib):
