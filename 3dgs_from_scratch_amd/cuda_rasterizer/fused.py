@@ -42,7 +42,8 @@ _SIDE: dict = {}
 
 def _side_stream(dev: torch.device):
     """This device's second stream (default priority) and the two events that
-    order it against the current stream, created once."""
+    order it against the current stream, created once (shared by every step on
+    the device: steps are queued from one host thread at a time)."""
     s = _SIDE.get(dev.index)
     if s is None:
         s = _SIDE[dev.index] = (torch.cuda.Stream(device=dev), torch.cuda.Event(),
