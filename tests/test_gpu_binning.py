@@ -65,6 +65,17 @@ def test_layout_random_bitexact(gpu, n, width, height, tile):
     assert k > 0
 
 
+@pytest.mark.parametrize("width,height,tile", [(256, 256, 16), (2560, 1600, 8)])
+def test_totals_copy_fallback_bitexact(gpu, monkeypatch, width, height, tile):
+    """The host layer reads K and M from pinned host memory the device writes;
+    where that memory is not mapped for the device it keeps them in device
+    memory and copies them.  Both give the same layouts (one-pass and general
+    level 1)."""
+    pts, radii, depths, mask = _random_splats(20000, width, height, seed=width + tile)
+    monkeypatch.setattr(cr, "_pinned_device_pointer", lambda t: None)
+    assert _check(gpu, pts, radii, depths, mask, width, height, tile) > 0
+
+
 def test_layout_many_supertiles_bitexact(gpu):
     """A grid of more than 256 supertiles (40 x 25 at 2560x1600, tile 8): the
     level-1 sort over several radix passes instead of the one-pass count."""
