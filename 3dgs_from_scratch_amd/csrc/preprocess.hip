@@ -634,6 +634,7 @@ extern "C" int gs_evaluate_sh_render_beside(const float *world_to_camera, const 
                                             const uint8_t *mask, int64_t n, float *colors,
                                             hipStream_t stream) {
     if (!world_to_camera && n > 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n <= 0) return n < 0 ? GS_ERR_INVALID_ARGUMENT : GS_OK;  // no device query
     // one workgroup per compute unit (measured at config 3 beside binning: 256
     // workgroups 0.693 ms per fused step, 192 0.698, 320 0.704, 512 0.697, one
     // per 128 Gaussians 0.714), more when a thread would take over 32 Gaussians

@@ -86,6 +86,10 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.gs_project_points(*([null] * 6), 10, 0.01, 100.0, 0.0, 0.5, 128.0, 64, 64,
                                  *([null] * 6), null) == -1  # null buffers
     assert lib.gs_evaluate_sh(*([null] * 5), -3, 0, null, null) == -1
+    # the colour launch for a second stream: the same checks as gs_evaluate_sh_render
+    assert lib.gs_evaluate_sh_render_beside(*([null] * 5), 10, null, null) == -1
+    assert lib.gs_evaluate_sh_render_beside(*([null] * 5), -1, null, null) == -1
+    assert lib.gs_evaluate_sh_render_beside(*([null] * 5), 0, null, null) == 0  # nothing to do
     assert lib.gs_rasterize(null, null, 4, 10, *([null] * 4), 10, 32, 32, 16, 1e-4, 1e-4, 9.21,
                             null, null) == -1
     assert lib.gs_rasterize(null, null, 4, 2**31, *([null] * 4), 10, 32, 32, 16, 1e-4, 1e-4,
