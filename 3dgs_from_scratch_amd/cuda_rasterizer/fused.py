@@ -37,6 +37,12 @@ import cuda_rasterizer as _cr
 from cuda_rasterizer import ssim as _ssim
 
 
+# Gaussians from which the colours run on a second stream beside binning.  Measured
+# in one process, fused step: 1M Gaussians (config 3) 0.707 -> 0.689 ms beside
+# binning; 200k (config 5) 0.526 -> 0.539 ms and 10k (config 1) 0.417 -> 0.454 ms,
+# where the fork and join cost more than the short colour pass saves.
+BESIDE_MIN_GAUSSIANS = 600_000
+
 _SIDE: dict = {}
 
 
@@ -82,12 +88,15 @@ class RenderL1Function(torch.autograd.Function):
                 far_plane, min_opacity, min_radius, max_radius, alpha_threshold,
                 transmittance_threshold, chi_squared_threshold, ssim_lambda, ssim_padding,
                 schedule_cache, view_id):
-        pts, depths, cov, conic, radii, mask, opac, _ = _cr.preprocess_forward(
+        beside = means.shape[0] >= BESIDE_MIN_GAUSSIANS
+        pts, depths, cov, conic, radii, mask, opac, colors = _cr.preprocess_forward(
             means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
-            max_radius, width, height, with_colors=False)
-        colors, colors_ready = _colors_beside(world_to_camera, means, sh_coeffs_dc,
-                                              sh_coeffs_rest, mask)
+            max_radius, width, height, with_colors=not beside)
+        colors_ready = None
+        if beside:
+            colors, colors_ready = _colors_beside(world_to_camera, means, sh_coeffs_dc,
+                                                  sh_coeffs_rest, mask)
         # with a launch order for the forward's tiles from the list lengths
         off, ids, list_order = _cr.compute_tile_intersection_ordered(pts, radii, depths, mask,
                                                                      width, height, 16)
@@ -102,7 +111,8 @@ class RenderL1Function(torch.autograd.Function):
             if (previous is not None and (previous.device != means.device
                                           or previous.numel() != sched.numel())):
                 previous = None
-        torch.cuda.current_stream(means.device).wait_event(colors_ready)
+        if colors_ready is not None:
+            torch.cuda.current_stream(means.device).wait_event(colors_ready)
         # the forward launches heaviest first by the view's last render when there
         # is one, else in the order from the list lengths
         image, display, loss = _cr.rasterize_display_l1(

@@ -119,13 +119,15 @@ class RenderColorsFunction(torch.autograd.Function):
 
 def _render_colors(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask):
     """render()'s colours and the event to wait for before reading them (None:
-    computed on the current stream).  In a training step (grad enabled) they are
-    computed on the device's second stream while binning runs (config 3 loop
-    0.988 -> 0.969 ms); a forward-only render keeps them on the current stream
-    (config 4, 3M Gaussians: 0.70 ms against 0.72 beside binning)."""
-    from cuda_rasterizer.fused import _side_stream
+    computed on the current stream).  In a training step (grad enabled) with at
+    least BESIDE_MIN_GAUSSIANS Gaussians they are computed on the device's second
+    stream while binning runs (config 3 loop 0.988 -> 0.969 ms); a forward-only
+    render keeps them on the current stream (config 4, 3M Gaussians: 0.70 ms
+    against 0.72 beside binning), as do small scenes (the fork and join cost more
+    than they save)."""
+    from cuda_rasterizer.fused import BESIDE_MIN_GAUSSIANS, _side_stream
 
-    beside = torch.is_grad_enabled()
+    beside = torch.is_grad_enabled() and means.shape[0] >= BESIDE_MIN_GAUSSIANS
     colors = RenderColorsFunction.apply(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest,
                                         mask, beside)
     return colors, (_side_stream(means.device)[2] if beside else None)

@@ -250,6 +250,31 @@ def test_render_l1_config1_matches_oracle(gpu):
             assert helpers.rel_l2(b[k].grad, grads_c[k]) <= 1e-3, k
 
 
+def test_render_l1_colours_beside_binning_equal_joint(gpu, monkeypatch):
+    """The colours on a second stream beside binning (scenes of at least
+    BESIDE_MIN_GAUSSIANS) or inside the preprocess launch: the same loss, and the
+    gradients up to the float atomics' order, over repeated steps."""
+    import cuda_rasterizer.fused as fused
+
+    p, cam, target = helpers.scene_orbit(20_000, 256, 192, 300.0, seed=29)
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    b = _raw_leaves(p, gpu)
+    out = {}
+    for mode, threshold in (("joint", 10**9), ("beside", 0), ("beside again", 0)):
+        monkeypatch.setattr(fused, "BESIDE_MIN_GAUSSIANS", threshold)
+        for t in b.values():
+            t.grad = None
+        loss, _, _, _ = render_l1(w2c, K, 256, 192, b["means"], b["log_scales"],
+                                  b["quats_raw"], b["opacity_logits"], b["sh_dc"], b["sh_rest"],
+                                  tgt)
+        loss.backward()
+        out[mode] = (float(loss), {k: t.grad.clone() for k, t in b.items()})
+    for mode in ("beside", "beside again"):
+        assert out[mode][0] == out["joint"][0]
+        for k in helpers.PARAMS:
+            assert helpers.rel_l2(out[mode][1][k], out["joint"][1][k]) <= 1e-5, (mode, k)
+
+
 def test_render_l1_repeated_calls_are_stable(gpu):
     """Two steps in a row on the same leaves give the same loss and gradients."""
     p, cam, target = helpers.scene_orbit(3_000, 96, 80, 140.0, seed=23)

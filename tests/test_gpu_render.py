@@ -73,10 +73,14 @@ def test_points_img_grad_and_radii(gpu):
     assert helpers.rel_l2(pts_g.grad.cpu() * keep.unsqueeze(1), ref) <= GRAD_TOL
 
 
-def test_render_colours_beside_binning_equal_the_plain_launch(gpu):
-    """With grad enabled render() computes its colours on a second stream while
-    binning runs; without grad on the current stream: the same display, and
-    repeated calls (reused fork/join events) stay bit-equal."""
+def test_render_colours_beside_binning_equal_the_plain_launch(gpu, monkeypatch):
+    """With grad enabled (and, here, any scene size) render() computes its
+    colours on a second stream while binning runs; without grad on the current
+    stream: the same display, and repeated calls (reused fork/join events) stay
+    bit-equal."""
+    import cuda_rasterizer.fused as fused
+
+    monkeypatch.setattr(fused, "BESIDE_MIN_GAUSSIANS", 0)
     p, cam, _ = helpers.scene_orbit(30_000, 320, 240, 440.0, seed=41)
     dev = gpu
     w2c, K = cam["w2c"].to(dev), cam["K"].to(dev)
