@@ -54,6 +54,7 @@ __all__ = [
     "rasterize_l1_backward",
     "blend_grad_accumulators",
     "set_blend_waves",
+    "check_forward_order",
     "fused_ssim",
     "RasterizerError",
 ]
@@ -300,14 +301,23 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         args = (_ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
                 tile_size, _ptr(ws_count), sz.value, totals_ptr, stream)
         ev = _lib.timer.record("bin_count", dev)
-        _lib.check(lib.gs_bin_count_begin(*args), "compute_tile_intersection (count)")
-        if totals is not None and n > 0:
-            host_totals.copy_(totals, non_blocking=True)
-        ready = torch.cuda.Event()
-        ready.record(torch.cuda.current_stream(dev))
-        _lib.check(lib.gs_bin_count_finish(*args), "compute_tile_intersection (count)")
-        _lib.timer.stop(ev, dev)
-        ready.synchronize()
+        ready = None
+        try:
+            _lib.check(lib.gs_bin_count_begin(*args), "compute_tile_intersection (count)")
+            if totals is not None and n > 0:
+                host_totals.copy_(totals, non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record(torch.cuda.current_stream(dev))
+            _lib.check(lib.gs_bin_count_finish(*args), "compute_tile_intersection (count)")
+            _lib.timer.stop(ev, dev)
+        finally:
+            # the pinned block is the caching host allocator's, which does not know
+            # that the device writes it: it is released only once those writes are
+            # done, also when a call above raised
+            if ready is not None:
+                ready.synchronize()
+            else:
+                torch.cuda.current_stream(dev).synchronize()
         k, m = (int(v) for v in (host_totals if n > 0 else totals.cpu()).tolist())
         if k > 2**31 - 1:
             raise RasterizerError(f"compute_tile_intersection: {k} keys exceed the int32 range")
@@ -452,8 +462,43 @@ def _check_schedule(schedule, n_tiles, dev, who):
                            f"{2 * n_tiles} elements on {dev}")
 
 
+# Set True (tests do) to verify every forward launch order as a permutation of
+# each XCD range before the launch: a device sort and one host read per call.
+CHECK_FORWARD_ORDERS = False
+
+_XCDS = 8  # the blend kernels' tile ranges: launch slot p of XCD x is in range x
+
+
+def check_forward_order(order, n_tiles):
+    """Raise RasterizerError unless order[:n_tiles] permutes every XCD range.
+
+    The blend forward launches the tiles of each XCD's contiguous range
+    [x*b + min(x, r), (x+1)*b + min(x+1, r)), b, r = divmod(n_tiles, 8), in the
+    order's sequence: slot p launches tile order[p], which must lie in p's range,
+    and every tile must appear once.  An order that breaks this leaves some tiles'
+    image, display and loss entries unwritten (nothing faults: the kernel skips
+    tiles out of range)."""
+    n_tiles = int(n_tiles)
+    if n_tiles == 0:
+        return
+    o = order[:n_tiles].to(torch.int64)
+    b, r = divmod(n_tiles, _XCDS)
+
+    def range_of(t):
+        big = r * (b + 1)  # the first r ranges hold b + 1 tiles
+        return torch.where(t < big, t // (b + 1), r + (t - big) // max(b, 1))
+
+    slots = torch.arange(n_tiles, device=o.device)
+    in_range = bool(((o >= 0) & (o < n_tiles)).all())
+    if not in_range or not bool((range_of(o) == range_of(slots)).all()) or not torch.equal(
+            torch.sort(o).values, slots):
+        raise RasterizerError("forward_order is not a permutation of every XCD tile range")
+
+
 def _check_order(order, schedule, n_tiles, dev, who):
-    """A forward launch order: n_tiles int32 on the device, not inside `schedule`."""
+    """A forward launch order: n_tiles int32 on the device, not inside `schedule`
+    (a permutation of every XCD range, see check_forward_order; verified only
+    with CHECK_FORWARD_ORDERS)."""
     if order is None:
         return
     if (not isinstance(order, torch.Tensor) or order.dtype != torch.int32
@@ -464,6 +509,8 @@ def _check_order(order, schedule, n_tiles, dev, who):
             schedule.data_ptr() <= order.data_ptr() < schedule.data_ptr() + schedule.numel() * 4):
         raise RasterizerError(f"{who}: forward_order must not lie in the schedule this call "
                               "writes")
+    if CHECK_FORWARD_ORDERS:
+        check_forward_order(order, n_tiles)
 
 
 def rasterize_backward(
@@ -545,6 +592,21 @@ def rasterize_work(indexing_offset, gaussian_ids_sorted, points_image, cov_inv_i
 # cuda_rasterizer.wrapper.render.
 
 
+def sh_render_inputs(world_to_camera, points_world, sh_coeffs_dc, sh_coeffs_rest, mask):
+    """evaluate_spherical_harmonics_render's inputs validated (dtype, device, shape)
+    and made contiguous, on the current stream.  A caller that launches the
+    colours on another stream calls this first, so that any copy is queued
+    before its fork."""
+    dev = _device_of(points_world)
+    n = points_world.shape[0]
+    f32 = torch.float32
+    return (_prep(world_to_camera, "world_to_camera", f32, (4, 4), dev),
+            _prep(points_world, "points_world", f32, (n, 3), dev),
+            _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev),
+            _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev),
+            _prep(mask, "mask", torch.bool, (n,), dev))
+
+
 def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs_dc,
                                         sh_coeffs_rest, mask, out=None, beside=False,
                                         stream=None):
@@ -558,11 +620,8 @@ def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs
     dev = _device_of(points_world)
     n = points_world.shape[0]
     f32 = torch.float32
-    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
-    points_world = _prep(points_world, "points_world", f32, (n, 3), dev)
-    sh_coeffs_dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
-    sh_coeffs_rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
-    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    world_to_camera, points_world, sh_coeffs_dc, sh_coeffs_rest, mask = sh_render_inputs(
+        world_to_camera, points_world, sh_coeffs_dc, sh_coeffs_rest, mask)
     if out is None:
         colors = torch.empty((n, 3), dtype=f32, device=dev)
     else:
@@ -635,7 +694,9 @@ def rasterize_display(indexing_offset, gaussian_ids_sorted, points_image, cov_in
     Returns (image[H,W,3] un-clamped, display[H,W,3]).  `schedule` (see
     tile_schedule) receives the work per tile and the order in which
     rasterize_display_backward, given it, launches the tiles.  `forward_order`:
-    a launch order for this forward (compute_tile_intersection_ordered's)."""
+    a launch order for this forward (compute_tile_intersection_ordered's).  It
+    must permute every XCD tile range (check_forward_order states the ranges):
+    tiles it leaves out are not written."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -826,7 +887,9 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
     for the same image size (not this call's `schedule`); this forward then
     launches its tiles in that order (results do not depend on it).
     `forward_order`: instead of forward_schedule, any per-XCD-range launch order
-    of n_tiles int32 (e.g. compute_tile_intersection_ordered's)."""
+    of n_tiles int32 (e.g. compute_tile_intersection_ordered's).  Either order must
+    permute every XCD tile range (check_forward_order states the ranges): tiles
+    it leaves out are not written, and the loss then sums unwritten entries."""
     dev, n, off, ids, pts, conic, opac, col = _blend_inputs(
         indexing_offset, gaussian_ids_sorted, points_image, cov_inv_image, opacities, colors)
     width, height = int(width), int(height)
@@ -846,6 +909,8 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
             raise RasterizerError("rasterize_display_l1: forward_schedule must be an earlier "
                                   "call's schedule, not the one this call writes")
         fwd_order = forward_schedule[n_tiles:]
+        if CHECK_FORWARD_ORDERS:
+            check_forward_order(fwd_order, n_tiles)
     if forward_order is not None:
         if forward_schedule is not None:
             raise RasterizerError("rasterize_display_l1: pass forward_schedule or forward_order, "

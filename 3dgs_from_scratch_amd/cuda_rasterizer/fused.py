@@ -31,6 +31,8 @@ blend backward, as autograd sums the two uses of display / 255.
 
 from __future__ import annotations
 
+import threading
+
 import torch
 
 import cuda_rasterizer as _cr
@@ -47,33 +49,60 @@ _SIDE: dict = {}
 
 
 def _side_stream(dev: torch.device):
-    """This device's second stream (default priority) and the two events that
-    order it against the current stream, created once (shared by every step on
-    the device: steps are queued from one host thread at a time)."""
-    s = _SIDE.get(dev.index)
+    """The calling thread's second stream on this device (default priority) and
+    the two events that order it against the current stream, created once per
+    (thread, device): two host threads rendering on one device never re-record
+    each other's events."""
+    key = (threading.get_ident(), dev.index)
+    s = _SIDE.get(key)
     if s is None:
-        s = _SIDE[dev.index] = (torch.cuda.Stream(device=dev), torch.cuda.Event(),
-                                torch.cuda.Event())
+        s = _SIDE[key] = (torch.cuda.Stream(device=dev), torch.cuda.Event(), torch.cuda.Event())
     return s
 
 
-def _colors_beside(world_to_camera, means, sh_dc, sh_rest, mask):
+class ColorsBeside:
+    """Colours being computed on the second stream.  `wait()` queues the current
+    stream's wait for them (once; later calls do nothing) and then releases the
+    tensors the second stream reads and writes.  Until then they stay referenced
+    here, so the caching allocator (whose blocks serve only the stream that
+    allocated them, the current one) cannot hand them out again before the
+    current stream is ordered after the colour kernel.  Call it before the
+    colours are read, and in a `finally` so that an exception between the fork
+    and the join leaves no kernel writing into freed memory."""
+
+    __slots__ = ("colors", "_main", "_join", "_held")
+
+    def __init__(self, colors, main, join, held):
+        self.colors, self._main, self._join, self._held = colors, main, join, held
+
+    def wait(self):
+        if self._held is not None:
+            self._main.wait_event(self._join)
+            self._held = None
+
+
+def colors_beside(world_to_camera, means, sh_dc, sh_rest, mask) -> ColorsBeside:
     """The render colours max(SH + 0.5, 0) of the Gaussians in `mask`, computed on
-    the device's second stream once the current stream has produced `mask`.
-    The tensor is allocated on the current stream, and the caller makes that
-    stream wait for the returned event before reading it; every input stays
-    alive until then (saved for the backward or a parameter).  The events are
-    reused: each record comes after the previous one's wait was queued."""
+    the calling thread's second stream once the current stream has produced
+    `mask`.  Every input is validated and made contiguous on the current stream
+    before the fork, so a copy is ordered before the colour kernel reads it.
+    The events are reused: each record comes after the previous wait was queued
+    (the returned object's wait())."""
     dev = means.device
     main = torch.cuda.current_stream(dev)
+    w2c, means, sh_dc, sh_rest, mask = _cr.sh_render_inputs(world_to_camera, means, sh_dc,
+                                                            sh_rest, mask)
     colors = torch.empty((means.shape[0], 3), dtype=torch.float32, device=dev)
     side, fork, join = _side_stream(dev)
     fork.record(main)
     side.wait_event(fork)
-    _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_dc, sh_rest, mask,
-                                            out=colors, beside=True, stream=side)
-    join.record(side)
-    return colors, join
+    pending = ColorsBeside(colors, main, join, (w2c, means, sh_dc, sh_rest, mask))
+    try:
+        _cr.evaluate_spherical_harmonics_render(w2c, means, sh_dc, sh_rest, mask, out=colors,
+                                                beside=True, stream=side)
+    finally:
+        join.record(side)
+    return pending
 
 
 def _chw(img: torch.Tensor) -> torch.Tensor:
@@ -93,17 +122,20 @@ class RenderL1Function(torch.autograd.Function):
             means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
             max_radius, width, height, with_colors=not beside)
-        colors_ready = None
-        if beside:
-            colors, colors_ready = _colors_beside(world_to_camera, means, sh_coeffs_dc,
-                                                  sh_coeffs_rest, mask)
-        # with a launch order for the forward's tiles from the list lengths
-        off, ids, list_order = _cr.compute_tile_intersection_ordered(pts, radii, depths, mask,
-                                                                     width, height, 16)
-        # the blend gradients' accumulators, zeroed by the forward blend launch
-        acc = _cr.blend_grad_accumulators(means.shape[0], means.device)
-        # the forward's work per tile orders the backward's tiles (heaviest first)
-        sched = _cr.tile_schedule(off.shape[0], means.device)
+        pending = colors_beside(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest,
+                                mask) if beside else None
+        try:
+            # with a launch order for the forward's tiles from the list lengths
+            off, ids, list_order = _cr.compute_tile_intersection_ordered(
+                pts, radii, depths, mask, width, height, 16)
+            # the blend gradients' accumulators, zeroed by the forward blend launch
+            acc = _cr.blend_grad_accumulators(means.shape[0], means.device)
+            # the forward's work per tile orders the backward's tiles (heaviest first)
+            sched = _cr.tile_schedule(off.shape[0], means.device)
+        finally:
+            if pending is not None:
+                pending.wait()
+                colors = pending.colors
         # and, kept per view, the next forward of the same view
         previous = None
         if schedule_cache is not None and view_id is not None:
@@ -111,8 +143,6 @@ class RenderL1Function(torch.autograd.Function):
             if (previous is not None and (previous.device != means.device
                                           or previous.numel() != sched.numel())):
                 previous = None
-        if colors_ready is not None:
-            torch.cuda.current_stream(means.device).wait_event(colors_ready)
         # the forward launches heaviest first by the view's last render when there
         # is one, else in the order from the list lengths
         image, display, loss = _cr.rasterize_display_l1(

@@ -86,23 +86,16 @@ class RenderColorsFunction(torch.autograd.Function):
     as one kernel each way."""
 
     @staticmethod
-    def forward(ctx, world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask, beside=False):
-        if beside:
-            # on the device's second stream, beside binning: the caller makes the
-            # current stream wait for the second stream's join event before it
-            # reads the colours (the backward stays on the current stream)
-            from cuda_rasterizer.fused import _side_stream
+    def forward(ctx, world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask, beside=None):
+        if beside is not None:
+            # on the calling thread's second stream, beside binning: `beside` (a
+            # list) receives the fused.ColorsBeside whose wait() the caller queues
+            # before it reads the colours (the backward stays on the current stream)
+            from cuda_rasterizer.fused import colors_beside
 
-            dev = means.device
-            main = torch.cuda.current_stream(dev)
-            side, fork, join = _side_stream(dev)
-            colors = torch.empty((means.shape[0], 3), dtype=torch.float32, device=dev)
-            fork.record(main)
-            side.wait_event(fork)
-            _cr.evaluate_spherical_harmonics_render(world_to_camera, means, sh_coeffs_dc,
-                                                    sh_coeffs_rest, mask, out=colors,
-                                                    beside=True, stream=side)
-            join.record(side)
+            pending = colors_beside(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask)
+            beside.append(pending)
+            colors = pending.colors
         else:
             colors = _cr.evaluate_spherical_harmonics_render(world_to_camera, means,
                                                              sh_coeffs_dc, sh_coeffs_rest, mask)
@@ -118,19 +111,19 @@ class RenderColorsFunction(torch.autograd.Function):
 
 
 def _render_colors(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask):
-    """render()'s colours and the event to wait for before reading them (None:
-    computed on the current stream).  In a training step (grad enabled) with at
-    least BESIDE_MIN_GAUSSIANS Gaussians they are computed on the device's second
-    stream while binning runs (config 3 loop 0.988 -> 0.969 ms); a forward-only
-    render keeps them on the current stream (config 4, 3M Gaussians: 0.70 ms
-    against 0.72 beside binning), as do small scenes (the fork and join cost more
-    than they save)."""
-    from cuda_rasterizer.fused import BESIDE_MIN_GAUSSIANS, _side_stream
+    """render()'s colours and the fused.ColorsBeside to wait on before reading
+    them (None: computed on the current stream).  In a training step (grad
+    enabled) with at least BESIDE_MIN_GAUSSIANS Gaussians they are computed on
+    the calling thread's second stream while binning runs (config 3 loop 0.988
+    -> 0.969 ms); a forward-only render keeps them on the current stream (config
+    4, 3M Gaussians: 0.70 ms against 0.72 beside binning), as do small scenes
+    (the fork and join cost more than they save)."""
+    from cuda_rasterizer.fused import BESIDE_MIN_GAUSSIANS
 
-    beside = torch.is_grad_enabled() and means.shape[0] >= BESIDE_MIN_GAUSSIANS
+    sink = [] if torch.is_grad_enabled() and means.shape[0] >= BESIDE_MIN_GAUSSIANS else None
     colors = RenderColorsFunction.apply(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest,
-                                        mask, beside)
-    return colors, (_side_stream(means.device)[2] if beside else None)
+                                        mask, sink)
+    return colors, (sink[0] if sink else None)
 
 
 class RenderRasterizeFunction(torch.autograd.Function):
@@ -228,12 +221,13 @@ def render(
                                               sh_coeffs_rest, mask)
 
     tile_size = 16
-    # the tile lists, and a launch order for the blend forward from their lengths
-    indexing_offset, gaussian_ids_sorted, order = _cr.compute_tile_intersection_ordered(
-        points_img.detach(), radii, depths, mask, width, height, tile_size)
-
-    if colors_ready is not None:
-        torch.cuda.current_stream(means.device).wait_event(colors_ready)
+    try:
+        # the tile lists, and a launch order for the blend forward from their lengths
+        indexing_offset, gaussian_ids_sorted, order = _cr.compute_tile_intersection_ordered(
+            points_img.detach(), radii, depths, mask, width, height, tile_size)
+    finally:
+        if colors_ready is not None:
+            colors_ready.wait()
     display = RenderRasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img,
                                             cov_inv_img, opacities, colors, width, height,
                                             tile_size, alpha_threshold, transmittance_threshold,

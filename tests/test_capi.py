@@ -185,3 +185,35 @@ def test_tile_schedule_buffers_are_checked():
 def test_status_to_exception():
     with pytest.raises(_lib.RasterizerError, match="invalid argument"):
         _lib.check(-1, "probe")
+
+
+@pytest.mark.parametrize("n_tiles", [1, 7, 8, 256, 2500, 8160, 8163])
+def test_check_forward_order_accepts_range_permutations(n_tiles):
+    """Each XCD range [x*b + min(x, r), ...) of b, r = divmod(n_tiles, 8), shuffled
+    within itself, is a valid launch order; the identity too."""
+    g = torch.Generator().manual_seed(n_tiles)
+    b, r = divmod(n_tiles, 8)
+    starts = [x * b + min(x, r) for x in range(9)]
+    parts = [starts[x] + torch.randperm(starts[x + 1] - starts[x], generator=g)
+             for x in range(8)]
+    order = torch.cat(parts).to(torch.int32)
+    cuda_rasterizer.check_forward_order(order, n_tiles)
+    cuda_rasterizer.check_forward_order(torch.arange(n_tiles, dtype=torch.int32), n_tiles)
+
+
+@pytest.mark.parametrize("n_tiles", [16, 2500, 8160])
+def test_check_forward_order_rejects_broken_orders(n_tiles):
+    ident = torch.arange(n_tiles, dtype=torch.int32)
+    dup = ident.clone()
+    dup[1] = dup[0]  # a tile twice, another never
+    across = ident.clone()
+    b, r = divmod(n_tiles, 8)
+    first_end = b + (1 if r else 0)
+    across[0], across[first_end] = across[first_end].item(), across[0].item()  # swaps two ranges
+    out = ident.clone()
+    out[-1] = n_tiles  # past the grid
+    neg = ident.clone()
+    neg[0] = -1
+    for bad in (dup, across, out, neg):
+        with pytest.raises(cuda_rasterizer.RasterizerError):
+            cuda_rasterizer.check_forward_order(bad, n_tiles)

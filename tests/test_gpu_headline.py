@@ -119,6 +119,26 @@ def test_config3_blend_forward_and_backward_match_oracle(gpu, config3):
             assert helpers.rel_l2(a, b) <= GRAD_TOL, (seed, name)
 
 
+def test_config3_full_frame_forward_matches_oracle(gpu, config3):
+    """The whole config-3 frame: every one of the 8160 tiles of the forward image
+    against the oracle's tile loop under no_grad (about 15 s of CPU), so the
+    partial bottom tile row (1080 = 67.5 tiles) and every heavy tile are covered
+    deterministically, not by the subset's seed."""
+    s = config3
+    W, H = s["W"], s["H"]
+    assert H % 16 != 0  # the bottom tile row is partial
+    with torch.no_grad():
+        ref = blend.rasterize(s["off"].cpu(), s["ids"].cpu(), *[t.cpu() for t in s["ins"]], W, H,
+                              *BLEND_ARGS)
+    img = s["image"].cpu()
+    assert helpers.max_abs(img, ref) <= IMG_TOL
+    assert helpers.max_abs(img.clamp(0, 1), ref.clamp(0, 1)) <= IMG_TOL
+    bottom = slice(H - H % 16, H)
+    assert float(ref[bottom].abs().max()) > 0.1  # the partial row holds rendered pixels
+    assert helpers.max_abs(img[bottom], ref[bottom]) <= IMG_TOL
+    assert torch.equal(s["display"].cpu(), img.clamp(0, 1) * 255)
+
+
 def test_config3_render_l1_matches_drop_in(gpu):
     """The fused step (render_l1) against the drop-in step at configuration 3.
     With the library's activations on the drop-in side too (cr.activate, whose

@@ -198,3 +198,80 @@ def test_render_passes_tile_schedule_only_with_grad(gpu, monkeypatch):
     with torch.no_grad():
         run()
     assert seen["fwd"] is None and "bwd" not in seen
+
+
+def test_colours_beside_binning_with_non_contiguous_inputs(gpu, monkeypatch):
+    """The colour pass on the second stream reads contiguous copies that are made
+    on the current stream before the fork and held until the join: a transposed
+    world_to_camera, means sliced from a wider array and sh_rest sliced from a
+    16-coefficient array give the display and gradients of contiguous inputs,
+    in render() and in render_l1, over repeated calls; a failure between the
+    fork and the join propagates and the next call is unaffected."""
+    import cuda_rasterizer as cr
+    import cuda_rasterizer.fused as fused
+    from cuda_rasterizer.fused import render_l1
+
+    monkeypatch.setattr(fused, "BESIDE_MIN_GAUSSIANS", 0)
+    n, W, H = 30_000, 320, 240
+    p, cam, target = helpers.scene_orbit(n, W, H, 440.0, seed=43)
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    w2c_t = w2c.t().contiguous().t()  # the same values, column-major
+    assert not w2c_t.is_contiguous()
+
+    def leaves(contiguous):
+        out = {k: v.to(gpu).clone().requires_grad_(True) for k, v in p.items()}
+        if contiguous:
+            return out, out
+        wide_means = torch.zeros(n, 5, device=gpu)
+        wide_means[:, 1:4] = out["means"].detach()
+        wide_means.requires_grad_(True)
+        wide_rest = torch.zeros(n, 16, 3, device=gpu)
+        wide_rest[:, 1:] = out["sh_rest"].detach()
+        wide_rest.requires_grad_(True)
+        views = dict(out, means=wide_means[:, 1:4], sh_rest=wide_rest[:, 1:])
+        assert not views["means"].is_contiguous() and not views["sh_rest"].is_contiguous()
+        return views, dict(out, means=wide_means, sh_rest=wide_rest)
+
+    def grads(roots, contiguous):
+        g = {k: t.grad for k, t in roots.items()}
+        if not contiguous:  # the wide arrays' gradients, cut to the views
+            g["means"], g["sh_rest"] = g["means"][:, 1:4], g["sh_rest"][:, 1:]
+        return g
+
+    ref, ref_roots = leaves(True)
+    sc, qq, op = helpers.activated(ref)
+    disp_ref, _, _ = render(w2c, K, W, H, ref["means"], sc, qq, op, ref["sh_dc"], ref["sh_rest"])
+    loss_ref, _, _, _ = render_l1(w2c, K, W, H, ref["means"], ref["log_scales"], ref["quats_raw"],
+                                  ref["opacity_logits"], ref["sh_dc"], ref["sh_rest"], tgt)
+    loss_ref.backward()
+    g_ref = grads(ref_roots, True)
+    for _ in range(2):
+        v, roots = leaves(False)
+        sc, qq, op = helpers.activated(v)
+        disp, _, _ = render(w2c_t, K, W, H, v["means"], sc, qq, op, v["sh_dc"], v["sh_rest"])
+        assert torch.equal(disp.detach(), disp_ref.detach())
+        loss, _, _, _ = render_l1(w2c_t, K, W, H, v["means"], v["log_scales"], v["quats_raw"],
+                                  v["opacity_logits"], v["sh_dc"], v["sh_rest"], tgt)
+        assert float(loss) == float(loss_ref)
+        loss.backward()
+        g = grads(roots, False)
+        for k in g_ref:
+            assert helpers.rel_l2(g[k], g_ref[k]) <= 1e-5, k
+
+    # binning fails after the fork: the error reaches the caller and the wait
+    # for the colours is still queued, so the next call is unaffected
+    real = cr.compute_tile_intersection_ordered
+
+    def failing(*a, **k):
+        raise cr.RasterizerError("planted binning failure")
+
+    monkeypatch.setattr(cr, "compute_tile_intersection_ordered", failing)
+    v, _ = leaves(False)
+    with pytest.raises(cr.RasterizerError, match="planted"):
+        render_l1(w2c_t, K, W, H, v["means"], v["log_scales"], v["quats_raw"],
+                  v["opacity_logits"], v["sh_dc"], v["sh_rest"], tgt)
+    monkeypatch.setattr(cr, "compute_tile_intersection_ordered", real)
+    v, _ = leaves(False)
+    loss, _, _, _ = render_l1(w2c_t, K, W, H, v["means"], v["log_scales"], v["quats_raw"],
+                              v["opacity_logits"], v["sh_dc"], v["sh_rest"], tgt)
+    assert float(loss) == float(loss_ref)

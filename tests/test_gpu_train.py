@@ -155,8 +155,8 @@ def test_clone_top_and_prune_matches_oracle(gpu):
 
 def test_config5_training_loop_events(gpu):
     """BASELINE configuration 5 through the library loop (render_l1 + FusedAdam +
-    Densifier, the bench's run_train "fused" path) for 300 steps: three
-    clone / prune events.  At each event every rebuilt parameter and both Adam
+    Densifier, the bench's run_train "fused" path) for 1600 steps: 16
+    clone / prune events, the last ones above 400k Gaussians.  At each event every rebuilt parameter and both Adam
     moments equal the oracle's row map (oracle.train.clone_top_rows on the
     pre-event opacity logits and accumulated gradient norms) applied to the
     pre-event tensors, bit for bit; the cloned means add the jitter drawn from
@@ -165,17 +165,18 @@ def test_config5_training_loop_events(gpu):
     import bench
     from cuda_rasterizer.fused import render_l1
 
-    scene = bench.config5(steps=300)
+    steps = 1600
+    scene = bench.config5(steps=steps)
     w2c_all = scene["w2c_per_step"].to(gpu)
     targets = scene["targets"].to(gpu)
     cam = scene["camera"]
     K, W, H = cam["K"].to(gpu), cam["width"], cam["height"]
     leaves = {k: v.to(gpu).requires_grad_(True) for k, v in scene["params"].items()}
-    opt = FusedAdam(leaves, means_decay_steps=300)
+    opt = FusedAdam(leaves, means_decay_steps=steps)
     dens = Densifier(leaves["means"].shape[0], gpu)
     gen = torch.Generator(device=gpu).manual_seed(0)
     losses, sizes = [], [leaves["means"].shape[0]]
-    for step in range(300):
+    for step in range(steps):
         loss, _, _, _ = render_l1(w2c_all[step], K, W, H, leaves["means"], leaves["log_scales"],
                                   leaves["quats_raw"], leaves["opacity_logits"], leaves["sh_dc"],
                                   leaves["sh_rest"], targets[step % targets.shape[0]],
@@ -213,6 +214,121 @@ def test_config5_training_loop_events(gpu):
             assert leaves[k].requires_grad and leaves[k].is_leaf
         assert float(dens.grads.abs().max()) == 0.0 and dens.count.shape[0] == len(src)
         sizes.append(len(src))
-    assert len(sizes) == 4 and sizes[-1] > sizes[0]
+    assert len(sizes) == 17 and sizes[-1] > sizes[0]
+    assert sizes[-2] >= 400_000  # the events from step 1500 on run above 400k Gaussians
     assert all(x == x and abs(x) < 1e30 for x in losses)
     assert sum(losses[-50:]) < sum(losses[:50])
+
+
+def _refine_with_cap(gpu, n, cap_from_keep, seed, max_gaussians=None):
+    """Densifier.refine where the growth budget binds, against the oracle's row
+    map given the same randperm draw (the generator's first draw in refine)."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(n, generator=g) * 3.0
+    log_scales = torch.randn(n, 3, generator=g) * 0.8 - 4.5
+    params = _params(n, g, gpu, logits=logits, log_scales=log_scales)
+    opt = _opt_with_state(params, g, gpu)
+    before = {k: v.detach().cpu().clone() for k, v in params.items()}
+    st_before = {"m": {k: v.cpu().clone() for k, v in opt.exp_avg.items()},
+                 "v": {k: v.cpu().clone() for k, v in opt.exp_avg_sq.items()}}
+    d = Densifier(n, gpu)
+    d.grads = (torch.rand(n, generator=g) * 4e-4).to(gpu)
+    d.count = torch.ones(n).to(gpu)
+    n_keep = int((torch.sigmoid(logits) >= d.prune_opacity).sum())
+    free = otrain.refine_rows(logits, log_scales, d.grads.cpu(), d.count.cpu(), step=600,
+                              max_gaussians=10**12)
+    n_cand = int(free[1].sum()) - 2 * free[2]
+    cap = max_gaussians if max_gaussians is not None else n_keep + cap_from_keep
+    d.max_gaussians = cap
+    budget = cap - n_keep
+    assert 0 < budget < n_cand  # the cap binds
+    seed_dev = 1234 + seed
+    perm = torch.randperm(n_cand, device=gpu,
+                          generator=torch.Generator(device=gpu).manual_seed(seed_dev)).cpu()
+    src, fresh, n_split, split_src = otrain.refine_rows(
+        logits, log_scales, d.grads.cpu(), d.count.cpu(), step=600, max_gaussians=cap,
+        budget_perm=perm)
+    n_pruned, n_cloned, n_split2 = d.refine(
+        params, opt, step=600, generator=torch.Generator(device=gpu).manual_seed(seed_dev))
+    assert (n_pruned, n_cloned, n_split2) == (n - n_keep, budget, n_split)
+    assert len(src) == cap + n_split
+    split_rows = torch.zeros(len(src), dtype=torch.bool)
+    split_rows[len(src) - 2 * n_split:] = True
+    _check_rebuild(params, before, opt, st_before, src, fresh, skip_rows=split_rows,
+                   skip_keys=("means", "log_scales"))
+    got_ls = params["log_scales"].detach().cpu()[split_rows]
+    s_dev = torch.exp(before["log_scales"].to(gpu))[split_src.to(gpu)]
+    assert torch.equal(got_ls, torch.log(s_dev / 1.6).repeat(2, 1).cpu())
+
+
+def test_refine_growth_budget_matches_oracle(gpu):
+    """src/strategy.py:116-137: more clone candidates than max_gaussians leaves
+    room for (the cap set on the instance to 100 above the rows kept): the
+    library clones the candidates its generator's randperm picks, in row order,
+    and splits uncapped -- bit for bit the oracle's row map given that draw."""
+    _refine_with_cap(gpu, 6000, 100, seed=5)
+
+
+def test_refine_growth_budget_at_the_default_cap(gpu):
+    """The same at the reference's own cap, max_gaussians = 1,000,000: of
+    1,003,000 Gaussians 38,694 fall to the prune, so the budget is 35,694 rows
+    for 43,424 clone candidates (and 439,691 uncapped splits)."""
+    _refine_with_cap(gpu, 1_003_000, None, seed=6, max_gaussians=1_000_000)
+
+
+def test_refine_at_the_cap_grows_nothing(gpu):
+    """With as many rows kept as max_gaussians, refine prunes only: no clone, no
+    split (src/strategy.py:119-124), as the oracle."""
+    g = torch.Generator().manual_seed(8)
+    n = 3000
+    logits = torch.randn(n, generator=g) * 3.0
+    log_scales = torch.randn(n, 3, generator=g) * 0.8 - 4.5
+    params = _params(n, g, gpu, logits=logits, log_scales=log_scales)
+    opt = _opt_with_state(params, g, gpu)
+    before = {k: v.detach().cpu().clone() for k, v in params.items()}
+    st_before = {"m": {k: v.cpu().clone() for k, v in opt.exp_avg.items()},
+                 "v": {k: v.cpu().clone() for k, v in opt.exp_avg_sq.items()}}
+    d = Densifier(n, gpu)
+    d.grads = (torch.rand(n, generator=g) * 4e-4).to(gpu)
+    d.count = torch.ones(n).to(gpu)
+    n_keep = int((torch.sigmoid(logits) >= d.prune_opacity).sum())
+    d.max_gaussians = n_keep
+    src, fresh, n_split, _ = otrain.refine_rows(logits, log_scales, d.grads.cpu(),
+                                                d.count.cpu(), step=600, max_gaussians=n_keep)
+    assert d.refine(params, opt, step=600) == (n - n_keep, 0, 0)
+    assert n_split == 0 and not bool(fresh.any())
+    _check_rebuild(params, before, opt, st_before, src, fresh)
+
+
+def test_reset_opacities_matches_oracle(gpu):
+    """src/strategy.py:231-253: logits clamped from above at logit(0.01) computed
+    on the device, the opacities' Adam moments zeroed, every other tensor
+    untouched; the device threshold is within one float32 ulp of the oracle's."""
+    import math
+
+    g = torch.Generator().manual_seed(9)
+    n = 50_000
+    logits = torch.randn(n, generator=g) * 4.0
+    params = _params(n, g, gpu, logits=logits)
+    opt = _opt_with_state(params, g, gpu)
+    before = {k: v.detach().cpu().clone() for k, v in params.items()}
+    m_before = {k: v.cpu().clone() for k, v in opt.exp_avg.items()}
+    v_before = {k: v.cpu().clone() for k, v in opt.exp_avg_sq.items()}
+    d = Densifier(n, gpu)
+    d.reset_opacities(params, opt)
+    thr_dev = torch.logit(torch.tensor(0.01, device=gpu)).cpu()
+    want, m0, v0 = otrain.reset_opacities(logits, m_before["opacity_logits"],
+                                          v_before["opacity_logits"], threshold=thr_dev)
+    assert torch.equal(params["opacity_logits"].detach().cpu(), want)
+    assert int((want == thr_dev).sum()) > n // 10  # the clamp is exercised
+    thr_cpu = otrain.reset_opacities(torch.tensor([0.0]), torch.zeros(1), torch.zeros(1))[0]
+    assert abs(float(thr_dev) - float(thr_cpu)) <= 2.0 ** (math.floor(math.log2(4.6)) - 23)
+    assert torch.equal(opt.exp_avg["opacity_logits"].cpu(), m0)
+    assert torch.equal(opt.exp_avg_sq["opacity_logits"].cpu(), v0)
+    for k in PARAM_ORDER:
+        if k == "opacity_logits":
+            continue
+        assert torch.equal(params[k].detach().cpu(), before[k]), k
+        assert torch.equal(opt.exp_avg[k].cpu(), m_before[k]), k
+        assert torch.equal(opt.exp_avg_sq[k].cpu(), v_before[k]), k
+    assert params["opacity_logits"].requires_grad

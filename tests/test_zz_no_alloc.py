@@ -5,9 +5,10 @@ It runs gs_ssim_forward's kernels with the per-workgroup partials in a static
 device array instead of a caller workspace, so its outputs -- the mean, the
 three derivative maps and the combined loss -- must equal gs_ssim_forward's bit
 for bit (the mean is reduced in a fixed order).  Checked on two calls in a row,
-the second with a smaller input (the array then still holds the first call's
-partials past the second call's workgroup count), in both orders of the two
-entry points, and its argument checks.
+each with a smaller input than the one before (the array then still holds
+the earlier call's partials past the later call's workgroup count; the first
+fills all 1024), in both orders of the two entry points, and its argument
+checks.
 """
 
 from __future__ import annotations
@@ -65,10 +66,14 @@ def _inputs(shape_hwc, seed, permuted, gpu):
             y.permute(2, 0, 1).contiguous().unsqueeze(0).to(gpu))
 
 
-# 64 x 32 output tiles per plane: the first call has 1380 tiles, so 512 workgroups
-# (the maximum), the second 6 (every partial after the sixth still holds the
-# first call's value)
-CALLS = [((720, 1280, 3), 1, True, 1, 255.0), ((32, 96, 3), 2, False, 0, 255.0)]
+# Units of 64 columns x 34 output rows per plane, 4 per workgroup, at most 1024
+# workgroups (the static array's size).  2160x3840x3: 60 x 64 x 3 = 11520 units,
+# 2880 workgroups capped at 1024, so the array is filled to capacity; then
+# 720x1280x3: 20 x 22 x 3 = 1320 units, 330 workgroups; then 32x96x3: 2 x 1 x 3 =
+# 6 units, 2 workgroups (every partial past the second still holds an earlier
+# call's value)
+CALLS = [((2160, 3840, 3), 4, True, 0, 255.0), ((720, 1280, 3), 1, True, 1, 255.0),
+         ((32, 96, 3), 2, False, 0, 255.0)]
 
 
 @pytest.mark.parametrize("noalloc_first", [True, False])
@@ -104,6 +109,10 @@ def test_noalloc_argument_checks(gpu):
         assert lib.gs_ssim_forward_noalloc(img1.data_ptr(), s1, img2.data_ptr(), s2, 1, 3, 32,
                                            48, 0, 1.0, None, None, None, None, None, 0.0, None,
                                            stream) == -1
+        # past the limits: more than 65535 planes
+        assert lib.gs_ssim_forward_noalloc(img1.data_ptr(), s1, img2.data_ptr(), s2, 65536, 1,
+                                           32, 48, 0, 1.0, mean.data_ptr(), None, None, None,
+                                           None, 0.0, None, stream) == -1
         # only some of the three maps
         maps = torch.empty((3, 32, 48), device=gpu)
         assert lib.gs_ssim_forward_noalloc(img1.data_ptr(), s1, img2.data_ptr(), s2, 1, 3, 32,
