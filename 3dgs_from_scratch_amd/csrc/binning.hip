@@ -176,6 +176,34 @@ __device__ __forceinline__ uint32_t digit_of(uint32_t key, int shift, uint32_t d
     return (key >> shift) & dmask;
 }
 
+// Depth bucket of a key (the depth sort's DepthXform {kmin, shift}): bits
+// shift .. shift + 15 of key - kmin, clamped to [0, 0xFFFF] -- keys at or below
+// kmin in bucket 0, keys past the 16 bits in bucket 0xFFFF.  Non-decreasing in
+// the key, so ordering by bucket and then by the full key is ordering by key,
+// whatever the transform; with the least and greatest key of the sort it never
+// clamps.  `on` false: the identity (the passes that are not depth passes).
+struct BucketFn {
+    uint32_t kmin = 0;
+    int shift = 0;
+    bool on = false;
+    __device__ __forceinline__ uint32_t operator()(uint32_t key) const {
+        if (!on) return key;
+        if (key <= kmin) return 0u;
+        const uint32_t b = (key - kmin) >> shift;
+        return b < 0xFFFFu ? b : 0xFFFFu;
+    }
+};
+
+__device__ __forceinline__ BucketFn bucket_fn(const uint32_t *xform) {
+    BucketFn f;
+    if (xform) {
+        f.kmin = xform[0];
+        f.shift = (int)xform[1];
+        f.on = true;
+    }
+    return f;
+}
+
 // Tile rectangle packed as (tx0 | tx1 << 16, ty0 | ty1 << 16); tile coordinates
 // fit 16 bits (gs_bin_sort rejects larger grids).
 __device__ __forceinline__ uint2 pack_rect(const TileRect &r) {
@@ -237,11 +265,12 @@ __device__ __forceinline__ int slot_index(int it) {
 template <int ITEMS>
 __device__ __forceinline__ void block_count_digits(const uint32_t (&k)[ITEMS],
                                                    const bool (&valid)[ITEMS], int shift,
-                                                   int nbits, uint32_t *counts) {
+                                                   int nbits, uint32_t *counts,
+                                                   BucketFn bf = BucketFn()) {
     const uint32_t dmask = (1u << nbits) - 1u;
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
-        const uint32_t d = digit_of(k[it], shift, dmask);
+        const uint32_t d = digit_of(bf(k[it]), shift, dmask);
         const uint64_t active = __ballot(valid[it]);
         const uint64_t peers = match_digit(d, nbits, active);
         if (valid[it] && (peers & lanemask_lt()) == 0)
@@ -258,40 +287,74 @@ __device__ __forceinline__ int64_t hist_index(int d, int b, int nblocks) {
 
 // Per-block sums of count_tiles (tiles, supertile entries, Gaussians with
 // tiles; three per block) reduced by one workgroup of kScanThreads to
-// sums_out[0] = K, sums_out[1] = M and *live_out.
+// sums_out[0] = K, sums_out[1] = M and *live_out; with minmax (count_tiles'
+// per-block least and greatest key with tiles) also sums_out[2] and
+// sums_out[3] = the least and greatest key with tiles over all blocks
+// (0xFFFFFFFF and 0 when there is none).
 __device__ __forceinline__ void reduce_block_sums(const unsigned long long *__restrict__ sums,
+                                                  const uint32_t *__restrict__ minmax,
                                                   int nblocks, int64_t *__restrict__ sums_out,
                                                   int64_t *__restrict__ live_out) {
     __shared__ unsigned long long tmp[kScanThreads / kWave + 1];
+    __shared__ uint32_t mm[2][kScanThreads / kWave];
     unsigned long long acc[3] = {0ull, 0ull, 0ull};
-    for (int b = threadIdx.x; b < nblocks; b += kScanThreads)
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+    for (int b = threadIdx.x; b < nblocks; b += kScanThreads) {
 #pragma unroll
         for (int f = 0; f < 3; ++f) acc[f] += sums[(int64_t)b * 3 + f];
+        if (minmax) {
+            lo = min(lo, minmax[2 * (int64_t)b]);
+            hi = max(hi, minmax[2 * (int64_t)b + 1]);
+        }
+    }
     unsigned long long total[3];
 #pragma unroll
     for (int f = 0; f < 3; ++f)
         block_exclusive_scan<unsigned long long, kScanThreads>(acc[f], tmp, total[f]);
+    if (minmax) {
+        for (int o = kWave / 2; o > 0; o >>= 1) {
+            lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, kWave));
+            hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, kWave));
+        }
+        if (threadIdx.x % kWave == 0) {
+            mm[0][threadIdx.x / kWave] = lo;
+            mm[1][threadIdx.x / kWave] = hi;
+        }
+        __syncthreads();
+    }
     if (threadIdx.x == 0) {
         sums_out[0] = (int64_t)total[0];
         sums_out[1] = (int64_t)total[1];
         *live_out = (int64_t)total[2];
+        if (minmax) {
+            lo = 0xFFFFFFFFu;
+            hi = 0u;
+#pragma unroll
+            for (int w = 0; w < kScanThreads / kWave; ++w) {
+                lo = min(lo, mm[0][w]);
+                hi = max(hi, mm[1][w]);
+            }
+            sums_out[2] = (int64_t)lo;
+            sums_out[3] = (int64_t)hi;
+        }
     }
 }
 
 // Block d scans column d of the histogram table over the nblocks blocks in
 // place (first position of (d, block) among the keys with digit d) and writes
 // the column total to totals[d].  The downsweep adds the keys of smaller digits.
-// With block_sums, one more block (the last) runs reduce_block_sums.
+// With block_sums, one more block (the last) runs reduce_block_sums (with
+// block_minmax when it is set).
 constexpr int kDigitScanItems = 8;  // column entries per thread held in registers
 
 __global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
     uint32_t *__restrict__ table, int nblocks, uint32_t *__restrict__ totals,
-    const unsigned long long *__restrict__ block_sums, int64_t *__restrict__ sums_out,
-    int64_t *__restrict__ live_out) {
+    const unsigned long long *__restrict__ block_sums, const uint32_t *__restrict__ block_minmax,
+    int nsum_blocks, int64_t *__restrict__ sums_out, int64_t *__restrict__ live_out) {
     __shared__ uint32_t tmp[kScanThreads / kWave + 1];
     const int d = blockIdx.x;
     if (block_sums && d == (int)gridDim.x - 1) {
-        reduce_block_sums(block_sums, nblocks, sums_out, live_out);
+        reduce_block_sums(block_sums, block_minmax, nsum_blocks, sums_out, live_out);
         return;
     }
     uint32_t run = 0;
@@ -339,7 +402,8 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
                                               const uint32_t *__restrict__ totals,
                                               uint64_t *__restrict__ counts_out,
                                               const uint2 *__restrict__ rects,
-                                              uint2 *__restrict__ rects_out, int blk) {
+                                              uint2 *__restrict__ rects_out, int blk,
+                                              BucketFn bf) {
     const int radix = 1 << nbits;
     const uint32_t dmask = (uint32_t)radix - 1u;
     const int wave = threadIdx.x / kWave;
@@ -358,7 +422,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
     uint32_t rank[ITEMS];
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
-        const uint32_t d = digit_of(k[it], shift, dmask);
+        const uint32_t d = digit_of(bf(k[it]), shift, dmask);
         const uint64_t active = __ballot(valid[it]);
         const uint64_t peers = match_digit(d, nbits, active);
         const uint32_t before = valid[it] ? s.wave_count[wave][d] : 0u;
@@ -384,7 +448,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         if (valid[it]) {
-            const uint32_t d = digit_of(k[it], shift, dmask);
+            const uint32_t d = digit_of(bf(k[it]), shift, dmask);
             const uint32_t p = s.local_start[d] + s.wave_count[wave][d] + rank[it];
             s.skeys[p] = k[it];
             s.svals[p] = v[it];
@@ -394,7 +458,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
     __syncthreads();
     for (uint32_t p = threadIdx.x; p < block_count; p += kSortThreads) {
         const uint32_t key = s.skeys[p];
-        const uint32_t d = digit_of(key, shift, dmask);
+        const uint32_t d = digit_of(bf(key), shift, dmask);
         const uint32_t dst = s.global_start[d] + (p - s.local_start[d]);
         if (dst < (uint64_t)n) {  // always true for a consistent histogram; guards the store
             const uint32_t val = s.svals[p];
@@ -420,7 +484,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
     const int radix = 1 << nbits;
     for (int d = threadIdx.x; d < radix; d += kSortThreads) counts[d] = 0;
     if (n_live) n = *n_live;
-    if (xform) shift += (int)xform[1];  // digits of the bucket bits (see DepthXform)
+    const BucketFn bf = bucket_fn(xform);  // digits of the depth buckets (see BucketFn)
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     uint32_t k[ITEMS];
     bool valid[ITEMS];
@@ -431,7 +495,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_upsweep_kernel(
         k[it] = valid[it] ? (uint32_t)keys[i] : 0u;
     }
     __syncthreads();
-    block_count_digits<ITEMS>(k, valid, shift, nbits, counts);
+    block_count_digits<ITEMS>(k, valid, shift, nbits, counts, bf);
     __syncthreads();
     for (int d = threadIdx.x; d < radix; d += kSortThreads)
         hist[hist_index(d, blockIdx.x, nblocks)] = counts[d];
@@ -449,9 +513,10 @@ struct PassExtras {
     uint2 *rects_out = nullptr;         //   rects[value]
     const unsigned long long *block_sums = nullptr;  // count_tiles' per-block sums,
     int64_t *sums_out = nullptr;        //   reduced to sums_out[0..1] (K, M)
-    int64_t *live_out = nullptr;        //   and *live_out (keys with tiles)
-    const uint32_t *xform = nullptr;    // device DepthXform: digits shifted by its shift
-    bool sub_min = false;               //   and keys minus its minimum (written so)
+    int64_t *live_out = nullptr;        //   and *live_out (keys with tiles);
+    const uint32_t *block_minmax = nullptr;  // with it, sums_out[2..3] = least and
+                                             //   greatest key with tiles
+    const uint32_t *xform = nullptr;    // device DepthXform: digits of the keys' depth buckets
 };
 
 template <typename KeyT>
@@ -470,7 +535,6 @@ struct DownArgs {
     const uint2 *rects;
     uint2 *rects_out;
     const uint32_t *xform;
-    int sub_min;
 };
 
 // With n_live, only the first *n_live keys are sorted, and a pass that writes
@@ -484,8 +548,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(DownArgs<
     const int blk = (int)xcd_block_live(blockIdx.x, (live + kSortThreads * ITEMS - 1) /
                                                         (kSortThreads * ITEMS));
     const int64_t base = (int64_t)blk * (kSortThreads * ITEMS);
-    const int shift = a.xform ? a.shift + (int)a.xform[1] : a.shift;
-    const uint32_t kmin = a.xform && a.sub_min ? a.xform[0] : 0u;
+    const int shift = a.shift;
+    const BucketFn bf = bucket_fn(a.xform);
     uint32_t k[ITEMS], v[ITEMS];
     uint2 pay[ITEMS];
     bool valid[ITEMS];
@@ -497,12 +561,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_downsweep_kernel(DownArgs<
         v[it] = in ? (a.vals_in ? a.vals_in[i] : (uint32_t)i) : 0u;
         pay[it] = (kPayload && in) ? a.pay_in[i] : make_uint2(0u, 0u);
         valid[it] = in && !(a.drop_no_tiles && k[it] == kNoTilesKey);
-        k[it] = valid[it] ? k[it] - kmin : 0u;  // kmin <= every live key
+        k[it] = valid[it] ? k[it] : 0u;
     }
     block_scatter<KeyT, ITEMS, kPayload>(k, v, pay, valid, shift, a.nbits, a.nblocks, a.table,
                                          a.keys_out, a.vals_out, a.pay_out, a.n,
                                          a.write_keys != 0, s, a.totals, a.counts_out, a.rects,
-                                         a.rects_out, blk);
+                                         a.rects_out, blk, bf);
     if (a.n_live && !a.write_keys) {
         for (int t = threadIdx.x; t < kSortThreads * ITEMS; t += kSortThreads) {
             const int64_t j = base + t;
@@ -573,7 +637,8 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
     }
     const int sums_block = x.block_sums ? 1 : 0;
     hipLaunchKernelGGL(digit_scan_kernel, dim3((1 << nbits) + sums_block), dim3(kScanThreads), 0,
-                       stream, hist, nblocks, totals, x.block_sums, x.sums_out, x.live_out);
+                       stream, hist, nblocks, totals, x.block_sums, x.block_minmax, nblocks,
+                       x.sums_out, x.live_out);
     st = launch_status();
     if (st) return st;
     DownArgs<KeyT> a;
@@ -596,7 +661,6 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
     a.rects = x.rects;
     a.rects_out = x.rects_out;
     a.xform = x.xform;
-    a.sub_min = x.sub_min ? 1 : 0;
     hipLaunchKernelGGL((radix_downsweep_kernel<KeyT, ITEMS, kPayload>), dim3(nblocks),
                        dim3(kSortThreads), 0, stream, a);
     return launch_status();
@@ -648,18 +712,18 @@ __device__ __forceinline__ uint32_t seg_reduce(uint32_t x, SegLds &s) {
     return r;
 }
 
-// First position q in [lo, live) whose bucket (key >> shift) exceeds b, given
+// First position q in [lo, live) whose bucket bf(key) exceeds b, given
 // that every position in [p0, lo) has a bucket <= b (keys[0 .. live) are
 // ordered by bucket); live when there is none.  Rounds of kSegThreads strided
 // probes, each narrowing the interval by kSegThreads.
 __device__ uint32_t bucket_end_search(const uint32_t *__restrict__ keys, uint32_t lo,
-                                      uint32_t live, int shift, uint32_t b, SegLds &s) {
+                                      uint32_t live, BucketFn bf, uint32_t b, SegLds &s) {
     uint32_t hi = live;  // the answer lies in [lo, hi]
     while (lo < hi) {
         const uint32_t len = hi - lo;
         const uint32_t stride = (len + kSegThreads - 1) / kSegThreads;
         const uint32_t q = lo + threadIdx.x * stride;
-        const uint32_t c = seg_reduce<true>((q < hi && (keys[q] >> shift) <= b) ? 1u : 0u, s);
+        const uint32_t c = seg_reduce<true>((q < hi && bf(keys[q]) <= b) ? 1u : 0u, s);
         if (c == 0) return lo;
         if (stride == 1) return lo + c;
         const uint32_t last_le = lo + (c - 1) * stride;  // a probe <= b
@@ -874,7 +938,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(SegArgs a) {
         seg_emit(a, p, 0xFFFFFFFFu);
     }
     if (lo >= live) return;  // uniform across the workgroup
-    const int shift = (int)a.xform[1];
+    const BucketFn bf = bucket_fn(a.xform);
     // The chunk [start, end): start = the first bucket beginning at or after lo
     // (0 for lo = 0), end = the first bucket beginning at or after hi (live
     // past the live keys).  Both come from the window [lo, lo + wlen) loaded
@@ -883,9 +947,9 @@ __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(SegArgs a) {
     // prefix of the window.
     const uint32_t wlen = min((uint32_t)kSegMax, live - lo);
     const int wipw = seg_items(wlen);
-    const uint32_t b_lo = lo > 0 ? a.keys[lo - 1] >> shift : 0u;
+    const uint32_t b_lo = lo > 0 ? bf(a.keys[lo - 1]) : 0u;
     const bool end_in = hi < live;  // else end = live
-    const uint32_t b_hi = end_in ? a.keys[hi - 1] >> shift : 0u;
+    const uint32_t b_hi = end_in ? bf(a.keys[hi - 1]) : 0u;
     uint32_t wk[kSegItems], wv[kSegItems];
     uint32_t c_lo = 0, c_hi = 0;
 #pragma unroll
@@ -894,20 +958,20 @@ __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(SegArgs a) {
         const bool in = it < wipw && j < wlen;
         wk[it] = in ? a.keys[lo + j] : 0u;
         wv[it] = in ? a.vals[lo + j] : 0u;
-        c_lo += (in && lo > 0 && (wk[it] >> shift) <= b_lo) ? 1u : 0u;
-        c_hi += (in && end_in && (wk[it] >> shift) <= b_hi) ? 1u : 0u;
+        c_lo += (in && lo > 0 && bf(wk[it]) <= b_lo) ? 1u : 0u;
+        c_hi += (in && end_in && bf(wk[it]) <= b_hi) ? 1u : 0u;
     }
     const uint32_t packed = seg_reduce<true>(c_lo | (c_hi << 16), s);
     c_lo = packed & 0xFFFFu;
     c_hi = packed >> 16;
     uint32_t start = lo + c_lo;
     if (c_lo == wlen && lo + wlen < live)  // the bucket of lo - 1 runs past the window
-        start = bucket_end_search(a.keys, lo + wlen, live, shift, b_lo, s);
+        start = bucket_end_search(a.keys, lo + wlen, live, bf, b_lo, s);
     uint32_t end = live;
     if (end_in) {
         end = lo + c_hi;
         if (c_hi == wlen && lo + wlen < live)
-            end = bucket_end_search(a.keys, lo + wlen, live, shift, b_hi, s);
+            end = bucket_end_search(a.keys, lo + wlen, live, bf, b_hi, s);
     }
     if (start >= end) return;  // uniform: no bucket begins in this range
     const uint32_t size = end - start;
@@ -995,12 +1059,24 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int64_t n, const float *__restrict__ points_image, const float *__restrict__ radii,
     const float *__restrict__ depths, const uint8_t *__restrict__ mask, int width, int height,
     int tile_size, uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys,
-    unsigned long long *__restrict__ block_sums, uint32_t *__restrict__ block_minmax) {
+    unsigned long long *__restrict__ block_sums, uint32_t *__restrict__ block_minmax,
+    uint32_t hint_kmin, int hint_shift, uint32_t *__restrict__ hist,
+    uint32_t *__restrict__ xform) {
     __shared__ unsigned long long sum_tmp[kSortThreads / kWave + 1];
     __shared__ uint32_t mm[2][kSortThreads / kWave];
+    __shared__ uint32_t counts[kRadixMax];
+    if (hist) {  // with a depth hint: the first depth pass's histogram, zeroed here
+        for (int d = threadIdx.x; d < kRadixMax; d += kSortThreads) counts[d] = 0;
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            xform[0] = hint_kmin;
+            xform[1] = (uint32_t)hint_shift;
+        }
+    }
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
     unsigned long long my_tiles = 0, my_entries = 0, my_live = 0;
     uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+    uint32_t keys[ITEMS];
+    bool live[ITEMS];
     // all loads first (clamped index, no control dependence) so they overlap
     float2 pt[ITEMS], rd[ITEMS];
     float dp[ITEMS];
@@ -1017,6 +1093,8 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t i = base + slot_index<ITEMS>(it);
+        keys[it] = 0u;
+        live[it] = false;
         if (i >= n) continue;
         TileRect r{0, 0, 0, 0};
         const uint32_t bits = __float_as_uint(dp[it]);
@@ -1031,6 +1109,20 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
         my_live += has ? 1u : 0u;
         kmin = has ? min(kmin, bits) : kmin;
         kmax = has ? max(kmax, bits) : kmax;
+        keys[it] = bits;
+        live[it] = has;
+    }
+    if (hist) {
+        BucketFn bf;
+        bf.kmin = hint_kmin;
+        bf.shift = hint_shift;
+        bf.on = true;
+        __syncthreads();  // counts zeroed
+        // the first depth pass's digit: the bucket's low byte
+        block_count_digits<ITEMS>(keys, live, 0, kRadixMaxBits, counts, bf);
+        __syncthreads();
+        for (int d = threadIdx.x; d < kRadixMax; d += kSortThreads)
+            hist[hist_index(d, blockIdx.x, gridDim.x)] = counts[d];
     }
     unsigned long long block_tiles, block_entries, block_live;
     block_exclusive_scan<unsigned long long, kSortThreads>(my_tiles, sum_tmp, block_tiles);
@@ -1062,8 +1154,10 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
 
 // DepthXform {kmin, shift}: the least key with tiles, and the shift that leaves
 // 16 bits of key - kmin (its bucket: bits shift .. shift + 15, with every
-// higher bit 0).  The depth passes sort by the bucket; the segment sort by the
-// rest.  Subtracting kmin keeps the order and the ties of the keys.
+// higher bit 0).  The depth passes sort by the bucket (BucketFn); the segment
+// sort by the whole key.  A caller's depth hint replaces it by a transform
+// chosen before the keys are known (count_tiles_kernel writes it); BucketFn's
+// clamp keeps the order correct for keys outside its range.
 __device__ __forceinline__ uint2 depth_xform(uint32_t kmin, uint32_t kmax) {
     if (kmin > kmax) return make_uint2(0u, 0u);  // no Gaussian with tiles
     const uint32_t range = kmax - kmin;
@@ -1073,7 +1167,7 @@ __device__ __forceinline__ uint2 depth_xform(uint32_t kmin, uint32_t kmax) {
 
 // Upsweep of the first depth pass: every workgroup reduces count_tiles' block
 // minima and maxima to the DepthXform (workgroup 0 stores it), then counts the
-// digit (key - kmin) >> shift & 0xFF of its keys with tiles.
+// low byte of the depth bucket (BucketFn) of its keys with tiles.
 template <int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void depth_upsweep0_kernel(
     const uint32_t *__restrict__ keys, int64_t n, const uint32_t *__restrict__ block_minmax,
@@ -1116,9 +1210,13 @@ __global__ __launch_bounds__(kSortThreads) void depth_upsweep0_kernel(
         const int64_t i = base + slot_index<ITEMS>(it);
         const uint32_t key = i < n ? keys[i] : kNoTilesKey;
         valid[it] = key != kNoTilesKey;
-        k[it] = valid[it] ? key - xf.x : 0u;
+        k[it] = valid[it] ? key : 0u;
     }
-    block_count_digits<ITEMS>(k, valid, (int)xf.y, kRadixMaxBits, counts);
+    BucketFn bf;
+    bf.kmin = xf.x;
+    bf.shift = (int)xf.y;
+    bf.on = true;
+    block_count_digits<ITEMS>(k, valid, 0, kRadixMaxBits, counts, bf);
     __syncthreads();
     for (int d = threadIdx.x; d < kRadixMax; d += kSortThreads)
         hist[hist_index(d, blockIdx.x, nblocks)] = counts[d];
@@ -1176,11 +1274,16 @@ struct L2Args {
     const int32_t *super_off;     // n_super: first list position of each supertile
     const int32_t *super_ids;     // m: Gaussian ids per supertile, depth order
     const uint32_t *chunk_start;  // n_super + 1: first level-2 block of each supertile
-    const uint2 *block_map;       // per level-2 block: (supertile, first list position)
+    const uint4 *block_map;       // per level-2 block: (supertile, first and end list
+                                  // position, 0); supertile kNoBlock past the last block
     const uint2 *super_rects;     // m: packed tile rectangle of each list entry
     int64_t n, m, k;
     int n_super, super_x, tiles_x, tiles_y, width, height, tile_size;
+    int64_t nblocks;              // level-2 blocks the grid covers (a bound on the chunks)
 };
+
+// block_map entry of the blocks past the last chunk (the grid is sized by a bound).
+constexpr uint32_t kNoBlock = 0xFFFFFFFFu;
 
 // One workgroup: chunks of every supertile's list (kL2Threads entries each),
 // their exclusive scan chunk_start (chunk_start[n_super] = all chunks), the
@@ -1191,8 +1294,8 @@ constexpr int kPlanThreads = 1024;
 
 __global__ __launch_bounds__(kPlanThreads) void l2_plan_kernel(
     int n_super, int64_t m, const int32_t *__restrict__ super_off,
-    uint32_t *__restrict__ chunk_start, uint2 *__restrict__ block_map, int n_tiles,
-    uint32_t *__restrict__ tile_counts) {
+    uint32_t *__restrict__ chunk_start, uint4 *__restrict__ block_map, int64_t nblocks,
+    int n_tiles, uint32_t *__restrict__ tile_counts) {
     __shared__ uint32_t tmp[kPlanThreads / kWave + 1];
     for (int t = threadIdx.x; t < n_tiles; t += kPlanThreads) tile_counts[t] = 0u;
     const int per = (n_super + kPlanThreads - 1) / kPlanThreads;
@@ -1208,10 +1311,16 @@ __global__ __launch_bounds__(kPlanThreads) void l2_plan_kernel(
     for (int s = s0; s < s1; ++s) {
         chunk_start[s] = b;
         const uint32_t first = (uint32_t)super_off[s], c = chunks_of(s);
-        for (uint32_t i = 0; i < c; ++i) block_map[b + i] = make_uint2((uint32_t)s, first + i * kL2Threads);
+        const uint32_t end = (uint32_t)(s + 1 < n_super ? super_off[s + 1] : m);
+        for (uint32_t i = 0; i < c; ++i) {
+            const uint32_t e0 = first + i * kL2Threads;
+            block_map[b + i] = make_uint4((uint32_t)s, e0, min(e0 + kL2Threads, end), 0u);
+        }
         b += c;
     }
     if (threadIdx.x == 0) chunk_start[n_super] = total;
+    for (int64_t q = (int64_t)total + threadIdx.x; q < nblocks; q += kPlanThreads)
+        block_map[q] = make_uint4(kNoBlock, 0u, 0u, 0u);
 }
 
 // Tile id of local tile j of supertile s, or -1 outside the tile grid.
@@ -1224,6 +1333,7 @@ __device__ __forceinline__ int tile_of_local(const L2Args &a, int s, int j) {
 struct L2Block {
     int s;
     uint32_t b;
+    uint32_t trow;  // table[b * kSuperLocal + thread] for the first kSuperLocal threads
     int32_t g;
     uint64_t mask;
     int lx0, lx1, ly0, ly1;  // the mask as a rectangle of local tiles (empty: lx0 > lx1)
@@ -1256,13 +1366,18 @@ __device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int64
 // for the blocks past the last chunk (the grid is sized by an upper bound).
 // Workgroup w handles block w - skip (the first `skip` workgroups, a multiple of
 // kBinXcds, do other work).
-__device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x, uint32_t skip = 0) {
-    const uint32_t chunks = a.chunk_start[a.n_super];
-    x.b = (uint32_t)xcd_block_live(blockIdx.x - skip, chunks);
-    if (x.b >= chunks) return false;
-    const uint2 map = a.block_map[x.b];
+__device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x, uint32_t skip = 0,
+                                         const uint32_t *__restrict__ table = nullptr) {
+    // the chunks fill all but the last few of the nblocks logical blocks, so the
+    // spread is over the grid (no dependent read of the chunk count)
+    x.b = (uint32_t)xcd_block(blockIdx.x - skip, a.nblocks);
+    const uint4 map = a.block_map[x.b];
+    if (map.x == kNoBlock) return false;
+    // this block's row of the table, loaded beside the list entries
+    x.trow = table && threadIdx.x < kSuperLocal ? table[(int64_t)x.b * kSuperLocal + threadIdx.x]
+                                                : 0u;
     x.s = (int)map.x;
-    const int64_t end = x.s + 1 < a.n_super ? a.super_off[x.s + 1] : a.m;
+    const int64_t end = (int64_t)map.z;
     const int64_t e = (int64_t)map.y + threadIdx.x;
     x.g = -1;
     x.mask = 0;
@@ -1276,27 +1391,22 @@ __device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x, uint32_t s
     return true;
 }
 
-// Per local tile j = (ly, lx), the number of lanes of this wave whose rectangle
-// covers it, returned in lane j: the lanes covering row ly and those covering
-// column lx are one ballot each (kSuper + kSuper ballots), and lane j counts
-// their intersection.  `rc` is this wave's 2 * kSuper words of LDS.
-__device__ __forceinline__ uint32_t wave_local_counts(const L2Block &x, uint64_t *rc) {
+// The lanes of this wave covering local row q (rows[q]) and local column q
+// (cols[q]) of the supertile, one ballot each (uniform masks); returns, in lane
+// j = (ly, lx), the number of lanes covering local tile j: the lanes covering
+// both its row and its column.
+__device__ __forceinline__ uint32_t wave_masks(const L2Block &x, uint64_t (&rows)[kSuper],
+                                               uint64_t (&cols)[kSuper]) {
     const int lane = threadIdx.x % kWave;
     uint64_t mine_row = 0, mine_col = 0;
 #pragma unroll
     for (int q = 0; q < kSuper; ++q) {
-        const uint64_t r = __ballot(x.ly0 <= q && q <= x.ly1);
-        const uint64_t c = __ballot(x.lx0 <= q && q <= x.lx1);
-        mine_row = lane == q ? r : mine_row;
-        mine_col = lane == q ? c : mine_col;
+        rows[q] = __ballot(x.ly0 <= q && q <= x.ly1);
+        cols[q] = __ballot(x.lx0 <= q && q <= x.lx1);
+        mine_row = lane / kSuper == q ? rows[q] : mine_row;
+        mine_col = lane % kSuper == q ? cols[q] : mine_col;
     }
-    if (lane < kSuper) {
-        rc[lane] = mine_row;
-        rc[kSuper + lane] = mine_col;
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    return (uint32_t)__popcll(rc[lane / kSuper] & rc[kSuper + lane % kSuper]);
+    return (uint32_t)__popcll(mine_row & mine_col);
 }
 
 // table[b * kSuperLocal + j] = entries of local tile j in level-2 block b;
@@ -1305,11 +1415,11 @@ __global__ __launch_bounds__(kL2Threads) void l2_count_kernel(L2Args a,
                                                               uint32_t *__restrict__ table,
                                                               uint32_t *__restrict__ tile_counts) {
     __shared__ uint32_t wave_cnt[kL2Waves][kSuperLocal];
-    __shared__ uint64_t rowcol[kL2Waves][2 * kSuper];
     L2Block x;
     if (!l2_block(a, x)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    wave_cnt[wave][lane] = wave_local_counts(x, rowcol[wave]);
+    uint64_t rows[kSuper], cols[kSuper];
+    wave_cnt[wave][lane] = wave_masks(x, rows, cols);
     __syncthreads();
     if (threadIdx.x < kSuperLocal) {
         const int j = threadIdx.x;
@@ -1470,18 +1580,18 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
                                                                 const int32_t *__restrict__ offsets,
                                                                 int32_t *__restrict__ launch_order) {
     __shared__ uint32_t base[kL2Waves][kSuperLocal];
-    __shared__ uint64_t rowcol[kL2Waves][2 * kSuper];
     if (launch_order && blockIdx.x < kBinXcds) {
         tile_launch_order((int)blockIdx.x, a.tiles_x * a.tiles_y, a.k, offsets, launch_order);
         return;
     }
     L2Block x;
-    if (!l2_block(a, x, launch_order ? kBinXcds : 0)) return;
+    if (!l2_block(a, x, launch_order ? kBinXcds : 0, table)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    base[wave][lane] = wave_local_counts(x, rowcol[wave]);
+    uint64_t rows[kSuper], cols[kSuper];
+    base[wave][lane] = wave_masks(x, rows, cols);
     __syncthreads();
     if (threadIdx.x < kSuperLocal) {  // first position of each wave's entries of tile j
-        uint32_t pos = table[(int64_t)x.b * kSuperLocal + threadIdx.x];  // from l2_prefix_kernel
+        uint32_t pos = x.trow;  // from l2_prefix_kernel
 #pragma unroll
         for (int w = 0; w < kL2Waves; ++w) {
             const uint32_t c = base[w][threadIdx.x];
@@ -1491,12 +1601,6 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
     }
     __syncthreads();
     const uint32_t my_base = base[wave][lane];  // lane j: tile j
-    uint64_t rows[kSuper], cols[kSuper];
-#pragma unroll
-    for (int q = 0; q < kSuper; ++q) {
-        rows[q] = __ballot(x.ly0 <= q && q <= x.ly1);
-        cols[q] = __ballot(x.lx0 <= q && q <= x.lx1);
-    }
     // k32: K < 2^30, so b + count cannot wrap in 32 bits (a scalar compare)
     const uint32_t k_lo = (uint32_t)(a.k < 0xffffffffLL ? a.k : 0xffffffffLL);
 #pragma unroll
@@ -1637,12 +1741,13 @@ __global__ __launch_bounds__(kL1Threads) void l1_count_kernel(L1Args a,
 // supertile d's entry count `tot` and first list position `first`): chunks of
 // kL2Threads list positions per supertile, their exclusive scan chunk_start
 // (chunk_start[n_super] = all chunks) and block_map[b] = (supertile, first
-// list position) of every level-2 block.  Contains __syncthreads().
+// and end list position, 0) of every level-2 block, kNoBlock for the blocks
+// past the last chunk up to nblocks.  Contains __syncthreads().
 __device__ __forceinline__ void l1_block_plan(int n_super, uint32_t tot, uint32_t first,
                                               uint32_t *scan_tmp, uint32_t *lds_start,
-                                              uint32_t *lds_first,
+                                              uint32_t *lds_first, uint32_t *lds_end,
                                               uint32_t *__restrict__ chunk_start,
-                                              uint2 *__restrict__ block_map) {
+                                              uint4 *__restrict__ block_map, int64_t nblocks) {
     const int d = threadIdx.x;
     const uint32_t c = d < n_super ? (tot + kL2Threads - 1) / kL2Threads : 0u;
     uint32_t all;
@@ -1650,6 +1755,7 @@ __device__ __forceinline__ void l1_block_plan(int n_super, uint32_t tot, uint32_
     if (d < n_super) {
         lds_start[d] = b0;
         lds_first[d] = first;
+        lds_end[d] = first + tot;
         chunk_start[d] = b0;
     }
     if (d == 0) chunk_start[n_super] = all;
@@ -1665,8 +1771,11 @@ __device__ __forceinline__ void l1_block_plan(int n_super, uint32_t tot, uint32_
             else
                 hi = mid - 1;
         }
-        block_map[b] = make_uint2((uint32_t)lo, lds_first[lo] + (b - lds_start[lo]) * kL2Threads);
+        const uint32_t e0 = lds_first[lo] + (b - lds_start[lo]) * kL2Threads;
+        block_map[b] = make_uint4((uint32_t)lo, e0, min(e0 + kL2Threads, lds_end[lo]), 0u);
     }
+    for (int64_t q = (int64_t)all + d; q < nblocks; q += kL1Threads)
+        block_map[q] = make_uint4(kNoBlock, 0u, 0u, 0u);
 }
 
 // `hist` holds, after digit_scan_kernel, the first position of (s, block)
@@ -1678,7 +1787,8 @@ __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
     L1Args a, const uint32_t *__restrict__ hist, const uint32_t *__restrict__ totals,
     int n_super, int32_t *__restrict__ super_ids, uint2 *__restrict__ super_rects,
     int32_t *__restrict__ super_off, uint32_t *__restrict__ chunk_start,
-    uint2 *__restrict__ block_map, int n_tiles, uint32_t *__restrict__ tile_counts) {
+    uint4 *__restrict__ block_map, int64_t l2_nblocks, int n_tiles,
+    uint32_t *__restrict__ tile_counts) {
     __shared__ uint64_t lanes[kL1Waves][kRadixMax];
     __shared__ uint32_t wave_pos[kL1Waves][kRadixMax];
     __shared__ uint32_t scan_tmp[kL1Threads / kWave + 1];
@@ -1697,8 +1807,8 @@ __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
     const uint32_t smaller = block_exclusive_scan<uint32_t, kL1Threads>(tot, scan_tmp, all);
     if (blk == 0) {  // uniform per workgroup; wave_pos serves as staging
         if (d < n_super) super_off[d] = (int32_t)smaller;
-        l1_block_plan(n_super, tot, smaller, scan_tmp, wave_pos[0], wave_pos[1], chunk_start,
-                      block_map);
+        l1_block_plan(n_super, tot, smaller, scan_tmp, wave_pos[0], wave_pos[1], wave_pos[2],
+                      chunk_start, block_map, l2_nblocks);
         __syncthreads();
     }
     if (d < kRadixMax) {
@@ -1821,7 +1931,7 @@ inline L1Args l1_args(const CountWs &cw, int64_t n, int64_t m, int super_x) {
 // shift .. shift + 7, then shift + 8 .. shift + 15), (a) -> (b) -> (a), then
 // segment_sort_kernel in place on (a).  The first pass drops the Gaussians
 // without tiles and writes key - kmin; the segment sort fills the tail.
-constexpr int kDepthPassShift[2] = {0, 8};  // added to DepthXform's shift
+constexpr int kDepthPassShift[2] = {0, 8};  // digit p: bits 8p .. 8p + 7 of the depth bucket
 
 inline bool use_u16_keys(int tile_bits) { return tile_bits <= 16; }
 
@@ -1879,7 +1989,7 @@ struct BinWs {
     int32_t *super_ids;     // m
     uint2 *super_rects;     // m: packed tile rectangle of each super_ids entry
     uint32_t *chunk_start;  // n_super + 1: first level-2 block of each supertile
-    uint2 *block_map;       // level-2 block -> (supertile, first list position)
+    uint4 *block_map;       // level-2 block -> (supertile, first and end list position, 0)
     uint32_t *table;        // level-2 blocks x 64 local tiles
     uint32_t *tile_counts;  // entries per tile
     void *scan_ws;          // tile-count scan of grids above kFusedTileScanMax tiles
@@ -1895,7 +2005,7 @@ inline BinWs carve_bins(void *base, int64_t n, int64_t m, const Grid &g) {
     w.super_ids = c.take<int32_t>(m);
     w.super_rects = c.take<uint2>(m);
     w.chunk_start = c.take<uint32_t>((int64_t)g.n_super + 1);
-    w.block_map = c.take<uint2>(l2_blocks_bound(m, g.n_super));
+    w.block_map = c.take<uint4>(l2_blocks_bound(m, g.n_super));
     w.table = c.take<uint32_t>(l2_blocks_bound(m, g.n_super) * kSuperLocal);
     w.tile_counts = c.take<uint32_t>(g.n_tiles);
     w.scan_ws = c.take<char>((int64_t)scan_workspace_bytes<uint32_t>(g.n_tiles));
@@ -1966,6 +2076,12 @@ struct CountCall {
     void *workspace;
     size_t workspace_bytes;
     int64_t *totals;
+    // depth hint {kmin, shift} for the bucket transform (hint_shift < 0: none,
+    // the transform comes from the keys' least and greatest value); with
+    // totals4, totals has 4 entries: K, M, least and greatest key with tiles
+    uint32_t hint_kmin = 0;
+    int hint_shift = -1;
+    bool totals4 = false;
 };
 
 int check_count_call(const CountCall &c, CountWs &w) {
@@ -1977,6 +2093,7 @@ int check_count_call(const CountCall &c, CountWs &w) {
         return GS_ERR_WORKSPACE_TOO_SMALL;
     if (c.n > 0 && (!c.points_image || !c.radii || !c.depths || !c.mask))
         return GS_ERR_INVALID_ARGUMENT;
+    if (c.hint_shift > 16) return GS_ERR_INVALID_ARGUMENT;  // 16 bucket bits of 32
     return GS_OK;
 }
 
@@ -1989,18 +2106,19 @@ bool one_pass_level1(const CountCall &c, Grid &grid) {
 }
 
 // Depth pass p of 2 over the bucket bits: (a) -> (b) -> (a).  The first pass
-// takes the histogram depth_upsweep0_kernel wrote, numbers the values itself,
-// drops the Gaussians without tiles, subtracts kmin and reduces count_tiles'
-// sums (K, M and the n_live Gaussians with tiles); the second sorts the n_live
-// keys.
+// takes the histogram depth_upsweep0_kernel (or, with a depth hint,
+// count_tiles_kernel) wrote, numbers the values itself, drops the Gaussians
+// without tiles and reduces count_tiles' sums (K, M, the n_live Gaussians with
+// tiles and, for a caller's four totals, the least and greatest key); the
+// second sorts the n_live keys.
 int depth_pass(const CountCall &c, const CountWs &w, int p, hipStream_t stream) {
     PassExtras x;
     x.xform = w.xform;
     if (p == 0) {
         x.hist_ready = true;
-        x.sub_min = true;
         x.drop_no_tiles = true;
         x.block_sums = w.block_sums;
+        x.block_minmax = c.totals4 ? w.block_minmax : nullptr;
         x.sums_out = c.totals;
         x.live_out = w.n_live;
     } else {
@@ -2013,24 +2131,40 @@ int depth_pass(const CountCall &c, const CountWs &w, int p, hipStream_t stream) 
         kRadixMaxBits, true, w.sort_ws, stream, x);
 }
 
+// The four totals of no Gaussians: no keys, no entries, no least or greatest key.
+__global__ __launch_bounds__(kWave) void empty_totals_kernel(int64_t *__restrict__ totals) {
+    if (threadIdx.x < 4) totals[threadIdx.x] = threadIdx.x == 2 ? 0xFFFFFFFFLL : 0;
+}
+
 // Phase 1: tile rectangles, depth keys, the first depth pass; totals are final.
 int bin_count_begin(const CountCall &c, hipStream_t stream) {
     CountWs w;
     int st = check_count_call(c, w);
     if (st) return st;
-    if (c.n == 0) return zero_bytes(c.totals, 2 * sizeof(int64_t), stream);
+    if (c.n == 0) {
+        if (!c.totals4) return zero_bytes(c.totals, 2 * sizeof(int64_t), stream);
+        hipLaunchKernelGGL(empty_totals_kernel, dim3(1), dim3(kWave), 0, stream, c.totals);
+        return launch_status();
+    }
     const int nblocks = (int)sort_blocks<kDepthItems>(c.n);
     uint32_t *hist = reinterpret_cast<uint32_t *>(w.sort_ws);
+    const bool hinted = c.hint_shift >= 0;
+    // with a depth hint the count kernel writes the transform and the first
+    // pass's histogram itself; otherwise the upsweep derives the transform from
+    // the keys' least and greatest value
     hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
                        stream, c.n, c.points_image, c.radii, c.depths, c.mask, c.width, c.height,
-                       c.tile_size, w.rects, w.dkeys_a, w.block_sums, w.block_minmax);
+                       c.tile_size, w.rects, w.dkeys_a, w.block_sums, w.block_minmax,
+                       c.hint_kmin, hinted ? c.hint_shift : 0, hinted ? hist : nullptr, w.xform);
     st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL((depth_upsweep0_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
-                       stream, (const uint32_t *)w.dkeys_a, c.n, (const uint32_t *)w.block_minmax,
-                       nblocks, nblocks, hist, w.xform);
-    st = launch_status();
-    if (st) return st;
+    if (!hinted) {
+        hipLaunchKernelGGL((depth_upsweep0_kernel<kDepthItems>), dim3(nblocks),
+                           dim3(kSortThreads), 0, stream, (const uint32_t *)w.dkeys_a, c.n,
+                           (const uint32_t *)w.block_minmax, nblocks, nblocks, hist, w.xform);
+        st = launch_status();
+        if (st) return st;
+    }
     return depth_pass(c, w, 0, stream);
 }
 
@@ -2068,7 +2202,8 @@ int bin_count_finish(const CountCall &c, hipStream_t stream) {
         st = launch_status();
         if (st) return st;
         hipLaunchKernelGGL(digit_scan_kernel, dim3(grid.n_super), dim3(kScanThreads), 0, stream,
-                           w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, nullptr);
+                           w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, 0, nullptr,
+                           nullptr);
         return launch_status();
     }
     // supertile entry offsets in depth order (the total equals count_tiles' M; it
@@ -2097,6 +2232,20 @@ extern "C" int gs_bin_count_begin(const float *points_image, const float *radii,
                                   hipStream_t stream) {
     const CountCall c{points_image, radii, depths, mask, n, width, height, tile_size, workspace,
                       workspace_bytes, totals};
+    return bin_count_begin(c, stream);
+}
+
+extern "C" int gs_bin_count_begin_hinted(const float *points_image, const float *radii,
+                                         const float *depths, const uint8_t *mask, int64_t n,
+                                         int32_t width, int32_t height, int32_t tile_size,
+                                         void *workspace, size_t workspace_bytes,
+                                         uint32_t hint_kmin, int32_t hint_shift,
+                                         int64_t *totals, hipStream_t stream) {
+    CountCall c{points_image, radii, depths, mask, n, width, height, tile_size, workspace,
+                workspace_bytes, totals};
+    c.hint_kmin = hint_kmin;
+    c.hint_shift = hint_shift < 0 ? -1 : hint_shift;
+    c.totals4 = true;
     return bin_count_begin(c, stream);
 }
 
@@ -2167,13 +2316,15 @@ int bin_sort(const float *points_image, const float *radii, const float *depths,
     if (!points_image || !radii || !gaussian_ids_sorted || (sorted_keys && !depths) || n == 0)
         return GS_ERR_INVALID_ARGUMENT;
 
+    // level-2 blocks the grids cover: a bound on the chunks of the supertile lists
+    const int64_t nb2 = l2_blocks_bound(m, g.n_super);
     // level 1: (supertile, Gaussian) entries in depth order, stably sorted by supertile
     if (g.n_super <= kRadixMax) {  // counts and positions came from gs_bin_count
         const L1Args la = l1_args(cw, n, m, g.super_x);
         hipLaunchKernelGGL(l1_scatter_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
                            (const uint32_t *)cw.l1_hist, (const uint32_t *)cw.l1_totals,
                            g.n_super, w.super_ids, w.super_rects, w.super_off, w.chunk_start,
-                           w.block_map, g.n_tiles, w.tile_counts);
+                           w.block_map, nb2, g.n_tiles, w.tile_counts);
         st = launch_status();
     } else {  // emitted entries sorted by supertile over several radix passes
         EmitArgs a;
@@ -2191,13 +2342,13 @@ int bin_sort(const float *points_image, const float *radii, const float *depths,
         if (st) return st;
         // level-2 block plan (the one-pass level 1 writes it itself)
         hipLaunchKernelGGL(l2_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, g.n_super, m,
-                           w.super_off, w.chunk_start, w.block_map, g.n_tiles, w.tile_counts);
+                           w.super_off, w.chunk_start, w.block_map, nb2, g.n_tiles,
+                           w.tile_counts);
         st = launch_status();
     }
     if (st) return st;
 
     // level 2: per-tile counts, tile offsets and block prefixes, scatter
-    const int64_t nb2 = l2_blocks_bound(m, g.n_super);
     L2Args l2;
     l2.super_off = w.super_off;
     l2.super_ids = w.super_ids;
@@ -2214,6 +2365,7 @@ int bin_sort(const float *points_image, const float *radii, const float *depths,
     l2.width = width;
     l2.height = height;
     l2.tile_size = tile_size;
+    l2.nblocks = nb2;
     hipLaunchKernelGGL(l2_count_kernel, dim3((unsigned)nb2), dim3(kL2Threads), 0, stream, l2,
                        w.table, w.tile_counts);
     st = launch_status();

@@ -24,6 +24,7 @@ Behavioural notes relative to the reference:
 from __future__ import annotations
 
 import ctypes
+import time
 
 import torch
 
@@ -267,6 +268,45 @@ def _pinned_device_pointer(t: torch.Tensor):
     return out.value
 
 
+# The host waits for K and M by polling the event (hipEventQuery) for up to
+# SPIN_WAIT_S seconds, then blocks: the count's second phase runs on the GPU
+# meanwhile and the sort is queued behind it, so a wake-up later than that phase
+# leaves the GPU idle.
+SPIN_WAIT_S = 500e-6
+
+
+def _wait(event) -> None:
+    t_end = time.perf_counter() + SPIN_WAIT_S
+    while not event.query():
+        if time.perf_counter() > t_end:
+            event.synchronize()
+            return
+
+
+# The depth sort's bucket transform is taken from the previous call's least and
+# greatest depth key on the same device (gs_bin_count_begin_hinted), widened by
+# an eighth of the span on each side: consecutive renders of a scene (training
+# steps, camera paths) cover nearly the same depths.  The outputs never depend
+# on it; a poor hint only crowds keys into few buckets.  DEPTH_HINTS = False
+# derives the transform on the device instead (one more launch).
+DEPTH_HINTS = True
+_DEPTH_RANGE: dict = {}
+_FORCED_DEPTH_HINT = None  # (kmin, shift): tests force a hint
+
+
+def _depth_hint(dev) -> tuple:
+    """(hint_kmin, hint_shift) for gs_bin_count_begin_hinted; shift -1: none."""
+    if _FORCED_DEPTH_HINT is not None:
+        return _FORCED_DEPTH_HINT
+    r = _DEPTH_RANGE.get(dev.index) if DEPTH_HINTS else None
+    if r is None or r[0] > r[1]:
+        return 0, -1
+    lo, hi = r
+    span = hi - lo
+    lo, hi = max(lo - span // 8, 0), min(hi + span // 8, 0xFFFFFFFE)
+    return lo, max((hi - lo).bit_length() - 16, 0)  # 16 bucket bits cover hi - lo
+
+
 def _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, debug,
                        ordered=False):
     dev = _device_of(points_image)
@@ -292,18 +332,26 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         # queued, so the GPU keeps working.  Device memory and a copy instead when
         # the pinned memory is not mapped for the device, and for n = 0 (the
         # library then zeroes them with a memset)
-        host_totals = torch.empty((2,), dtype=torch.int64, pin_memory=n > 0)
+        # four totals: K, M and the least and greatest depth key (the next call's hint)
+        host_totals = torch.empty((4,), dtype=torch.int64, pin_memory=n > 0)
         totals_ptr = _pinned_device_pointer(host_totals) if n > 0 else None
         totals = None
         if totals_ptr is None:  # device memory and a copy
-            totals = torch.empty((2,), dtype=torch.int64, device=dev)
+            totals = torch.empty((4,), dtype=torch.int64, device=dev)
             totals_ptr = _ptr(totals)
         args = (_ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
                 tile_size, _ptr(ws_count), sz.value, totals_ptr, stream)
+        hint_kmin, hint_shift = _depth_hint(dev)
+        # the outputs whose size does not depend on K or M, allocated before the wait
+        indexing_offset = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
+        tiles_touched = torch.empty((n,), dtype=torch.int32, device=dev) if debug else None
+        order = torch.empty((n_tiles,), dtype=torch.int32, device=dev) if ordered else None
         ev = _lib.timer.record("bin_count", dev)
         ready = None
         try:
-            _lib.check(lib.gs_bin_count_begin(*args), "compute_tile_intersection (count)")
+            _lib.check(lib.gs_bin_count_begin_hinted(*args[:10], hint_kmin, hint_shift,
+                                                     *args[10:]),
+                       "compute_tile_intersection (count)")
             if totals is not None and n > 0:
                 host_totals.copy_(totals, non_blocking=True)
             ready = torch.cuda.Event()
@@ -315,21 +363,20 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
             # that the device writes it: it is released only once those writes are
             # done, also when a call above raised
             if ready is not None:
-                ready.synchronize()
+                _wait(ready)
             else:
                 torch.cuda.current_stream(dev).synchronize()
-        k, m = (int(v) for v in (host_totals if n > 0 else totals.cpu()).tolist())
+        k, m, kmin, kmax = (int(v) for v in (host_totals if n > 0 else totals.cpu()).tolist())
+        if n > 0:
+            _DEPTH_RANGE[dev.index] = (kmin, kmax)
         if k > 2**31 - 1:
             raise RasterizerError(f"compute_tile_intersection: {k} keys exceed the int32 range")
         sz2 = ctypes.c_size_t(0)
         _lib.check(lib.gs_bin_sort_workspace_size(n, k, m, width, height, tile_size,
                                                   ctypes.byref(sz2)), "workspace query")
         ws_sort = torch.empty((max(sz2.value, 1),), dtype=torch.uint8, device=dev)
-        indexing_offset = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
         gaussian_ids_sorted = torch.empty((k,), dtype=torch.int32, device=dev)
         sorted_keys = torch.empty((k,), dtype=torch.int64, device=dev) if debug else None
-        tiles_touched = torch.empty((n,), dtype=torch.int32, device=dev) if debug else None
-        order = torch.empty((n_tiles,), dtype=torch.int32, device=dev) if ordered else None
         sort_args = (_ptr(points_image), _ptr(radii), _ptr(depths), n, width, height, tile_size,
                      k, m, _ptr(ws_count), _ptr(ws_sort), sz2.value, _ptr(indexing_offset),
                      _ptr(gaussian_ids_sorted), _ptr(sorted_keys), _ptr(tiles_touched))

@@ -27,6 +27,8 @@ SIGNATURES = {
     "gs_bin_count": [_P] * 4 + [_I64, _I32, _I32, _I32, _P, _SZ, _P, _P],
     "gs_bin_count_begin": [_P] * 4 + [_I64, _I32, _I32, _I32, _P, _SZ, _P, _P],
     "gs_bin_count_finish": [_P] * 4 + [_I64, _I32, _I32, _I32, _P, _SZ, _P, _P],
+    "gs_bin_count_begin_hinted": [_P] * 4 + [_I64, _I32, _I32, _I32, _P, _SZ, ctypes.c_uint32,
+                                            _I32, _P, _P],
     "gs_bin_sort_workspace_size": [_I64, _I64, _I64, _I32, _I32, _I32, _PSZ],
     "gs_bin_sort": [_P] * 3 + [_I64, _I32, _I32, _I32, _I64, _I64, _P, _P, _SZ] + [_P] * 4 + [_P],
     "gs_bin_sort_ordered": [_P] * 3 + [_I64, _I32, _I32, _I32, _I64, _I64, _P, _P, _SZ]

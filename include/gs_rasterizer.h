@@ -153,6 +153,28 @@ int gs_bin_count_finish(const float *points_image, const float *radii, const flo
                         const uint8_t *mask, int64_t n, int32_t width, int32_t height,
                         int32_t tile_size, void *workspace, size_t workspace_bytes,
                         int64_t *totals, hipStream_t stream);
+
+/*
+ * gs_bin_count_begin with a depth hint and four totals.  The depth sort orders
+ * the keys (depth bits) by a 16-bit bucket and then by the whole key; its
+ * transform {kmin, shift} maps key -> (key - kmin) >> shift clamped to
+ * [0, 0xFFFF], which keeps the order of any keys.  gs_bin_count_begin derives
+ * it from the least and greatest key with tiles, which costs a launch; here the
+ * caller supplies it (hint_kmin, hint_shift in 0..16; hint_shift < 0: derived
+ * as in gs_bin_count_begin), e.g. from the previous call's totals, and the count
+ * kernel histograms the first depth pass itself.  The outputs are the same
+ * for every hint; a hint far from the keys' range only puts many keys in one
+ * bucket, which the segment sort then sorts more slowly.  totals: 4 entries --
+ * K, M, the least and the greatest depth key (bits) of the Gaussians with
+ * tiles (0xFFFFFFFF and 0 when there is none).  Follow it with
+ * gs_bin_count_finish as after gs_bin_count_begin.  No counterpart in the
+ * reference extension (which sorts 64-bit keys and needs no transform).
+ */
+int gs_bin_count_begin_hinted(const float *points_image, const float *radii,
+                              const float *depths, const uint8_t *mask, int64_t n,
+                              int32_t width, int32_t height, int32_t tile_size,
+                              void *workspace, size_t workspace_bytes, uint32_t hint_kmin,
+                              int32_t hint_shift, int64_t *totals, hipStream_t stream);
 int gs_bin_sort_workspace_size(int64_t n, int64_t k, int64_t m, int32_t width, int32_t height,
                                int32_t tile_size, size_t *bytes);
 int gs_bin_sort(const float *points_image, const float *radii, const float *depths, int64_t n,

@@ -221,3 +221,50 @@ def test_launch_order(gpu, n, width, height, tile, culled):
         assert ids.shape[0] == 0 and np.array_equal(ref, np.arange(n_tiles))
     elif n >= 1000:  # lists of many lengths, so the order is not trivial
         assert len(set(np.diff(np.append(off.cpu().numpy(), ids.shape[0])).tolist())) > 3
+
+
+def _key_range(depths, mask):
+    bits = depths.view(np.uint32)
+    live = bits[mask]
+    return int(live.min()), int(live.max())
+
+
+@pytest.mark.parametrize("case", ["derived", "previous", "below", "above", "narrow", "shift0",
+                                  "top"])
+@pytest.mark.parametrize("width,height,tile", [(256, 256, 16), (2560, 1600, 8)])
+def test_depth_hint_layouts_bitexact(gpu, monkeypatch, case, width, height, tile):
+    """The depth sort's bucket transform (gs_bin_count_begin_hinted): derived on
+    the device, taken from the previous call's key range, or forced far from the
+    keys -- a range below every key (all in the last bucket), above every key
+    (all in bucket 0), one covering a tenth of the span (both clamps), shift 0
+    (a 16-bit window of single key values) and the top of the key space.  Every
+    transform gives the oracle's layout bit for bit; the crowded buckets run the
+    segment sort's global-memory path.  Both level-1 paths (one pass and, at
+    2560x1600 with 8-pixel tiles, general)."""
+    pts, radii, depths, mask = _random_splats(30000, width, height, seed=7 + width)
+    kmin, kmax = _key_range(depths, mask)
+    span = kmax - kmin
+    forced = {"below": (max(kmin - 2 * span - 100, 0), 0),
+              "above": (kmax + 1, 4),
+              "narrow": (kmin + span // 2, max((span // 10).bit_length() - 16, 0)),
+              "shift0": (kmin + span // 3, 0),
+              "top": (0xFFFFFF00, 16)}
+    if case == "derived":
+        monkeypatch.setattr(cr, "DEPTH_HINTS", False)
+    elif case == "previous":
+        _check(gpu, pts, radii, depths, mask, width, height, tile)  # leaves this range as hint
+        assert cr._DEPTH_RANGE[gpu.index] == (kmin, kmax)
+    else:
+        monkeypatch.setattr(cr, "_FORCED_DEPTH_HINT", forced[case])
+    assert _check(gpu, pts, radii, depths, mask, width, height, tile) > 0
+    if case != "derived":
+        assert cr._DEPTH_RANGE[gpu.index] == (kmin, kmax)  # the totals report the key range
+
+
+def test_depth_hint_rejects_wide_shift(gpu, monkeypatch):
+    """A hint shift above 16 is rejected before any launch."""
+    pts, radii, depths, mask = _random_splats(100, 64, 64, seed=3)
+    monkeypatch.setattr(cr, "_FORCED_DEPTH_HINT", (0, 17))
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    with pytest.raises(cr.RasterizerError):
+        cr.compute_tile_intersection(d(pts), d(radii), d(depths), d(mask), 64, 64, 16)
