@@ -71,6 +71,16 @@ __device__ __forceinline__ int64_t xcd_block(int64_t w, int64_t nblocks) {
     return x * base + (x < rem ? x : rem) + i;
 }
 
+// The inverse of xcd_block: the workgroup index that xcd_block maps to logical
+// block b.
+__device__ __forceinline__ int64_t xcd_block_inverse(int64_t b, int64_t nblocks) {
+    const int64_t base = nblocks / kBinXcds, rem = nblocks % kBinXcds;
+    const int64_t big = rem * (base + 1);  // the first rem ranges hold base + 1 blocks
+    const int64_t x = b < big ? b / (base + 1) : rem + (b - big) / base;
+    const int64_t i = b - (x * base + (x < rem ? x : rem));
+    return i * kBinXcds + x;
+}
+
 // The same over the first `live` workgroups only (the ones with work: a grid
 // sized by an upper bound leaves the rest idle, and spreading those evenly
 // keeps every XCD's share of the work equal); the others map to themselves.
@@ -287,14 +297,15 @@ __device__ __forceinline__ int64_t hist_index(int d, int b, int nblocks) {
 
 // Per-block sums of count_tiles (tiles, supertile entries, Gaussians with
 // tiles; three per block) reduced by one workgroup of kScanThreads to
-// sums_out[0] = K, sums_out[1] = M and *live_out; with minmax (count_tiles'
-// per-block least and greatest key with tiles) also sums_out[2] and
-// sums_out[3] = the least and greatest key with tiles over all blocks
-// (0xFFFFFFFF and 0 when there is none).
+// sums_out[0] = K, sums_out[1] = M and *live_out (K and M also to sums_dev, a
+// device copy, when set); with minmax (count_tiles' per-block least and
+// greatest key with tiles) also sums_out[2] and sums_out[3] = the least and
+// greatest key with tiles over all blocks (0xFFFFFFFF and 0 when there is none).
 __device__ __forceinline__ void reduce_block_sums(const unsigned long long *__restrict__ sums,
                                                   const uint32_t *__restrict__ minmax,
                                                   int nblocks, int64_t *__restrict__ sums_out,
-                                                  int64_t *__restrict__ live_out) {
+                                                  int64_t *__restrict__ live_out,
+                                                  int64_t *__restrict__ sums_dev) {
     __shared__ unsigned long long tmp[kScanThreads / kWave + 1];
     __shared__ uint32_t mm[2][kScanThreads / kWave];
     unsigned long long acc[3] = {0ull, 0ull, 0ull};
@@ -326,6 +337,10 @@ __device__ __forceinline__ void reduce_block_sums(const unsigned long long *__re
         sums_out[0] = (int64_t)total[0];
         sums_out[1] = (int64_t)total[1];
         *live_out = (int64_t)total[2];
+        if (sums_dev) {
+            sums_dev[0] = (int64_t)total[0];
+            sums_dev[1] = (int64_t)total[1];
+        }
         if (minmax) {
             lo = 0xFFFFFFFFu;
             hi = 0u;
@@ -350,11 +365,12 @@ constexpr int kDigitScanItems = 8;  // column entries per thread held in registe
 __global__ __launch_bounds__(kScanThreads) void digit_scan_kernel(
     uint32_t *__restrict__ table, int nblocks, uint32_t *__restrict__ totals,
     const unsigned long long *__restrict__ block_sums, const uint32_t *__restrict__ block_minmax,
-    int nsum_blocks, int64_t *__restrict__ sums_out, int64_t *__restrict__ live_out) {
+    int nsum_blocks, int64_t *__restrict__ sums_out, int64_t *__restrict__ live_out,
+    int64_t *__restrict__ sums_dev) {
     __shared__ uint32_t tmp[kScanThreads / kWave + 1];
     const int d = blockIdx.x;
     if (block_sums && d == (int)gridDim.x - 1) {
-        reduce_block_sums(block_sums, block_minmax, nsum_blocks, sums_out, live_out);
+        reduce_block_sums(block_sums, block_minmax, nsum_blocks, sums_out, live_out, sums_dev);
         return;
     }
     uint32_t run = 0;
@@ -516,6 +532,7 @@ struct PassExtras {
     int64_t *live_out = nullptr;        //   and *live_out (keys with tiles);
     const uint32_t *block_minmax = nullptr;  // with it, sums_out[2..3] = least and
                                              //   greatest key with tiles
+    int64_t *sums_dev = nullptr;        // device copy of K and M
     const uint32_t *xform = nullptr;    // device DepthXform: digits of the keys' depth buckets
 };
 
@@ -638,7 +655,7 @@ int radix_pass(const KeyT *kin, const uint32_t *vin, KeyT *kout, uint32_t *vout,
     const int sums_block = x.block_sums ? 1 : 0;
     hipLaunchKernelGGL(digit_scan_kernel, dim3((1 << nbits) + sums_block), dim3(kScanThreads), 0,
                        stream, hist, nblocks, totals, x.block_sums, x.block_minmax, nblocks,
-                       x.sums_out, x.live_out);
+                       x.sums_out, x.live_out, x.sums_dev);
     st = launch_status();
     if (st) return st;
     DownArgs<KeyT> a;
@@ -1274,22 +1291,34 @@ struct L2Args {
     const int32_t *super_off;     // n_super: first list position of each supertile
     const int32_t *super_ids;     // m: Gaussian ids per supertile, depth order
     const uint32_t *chunk_start;  // n_super + 1: first level-2 block of each supertile
-    const uint4 *block_map;       // per level-2 block: (supertile, first and end list
-                                  // position, 0); supertile kNoBlock past the last block
+    const uint4 *block_map;       // per level-2 workgroup w: (supertile, first and end list
+                                  // position, logical block xcd_block(w, chunks)), laid out
+                                  // so that each XCD takes a contiguous range of the
+                                  // chunks; supertile kNoBlock past the last chunk
     const uint2 *super_rects;     // m: packed tile rectangle of each list entry
     int64_t n, m, k;
     int n_super, super_x, tiles_x, tiles_y, width, height, tile_size;
     int64_t nblocks;              // level-2 blocks the grid covers (a bound on the chunks)
+    // capped sort (gs_bin_sort_capped): device K and M; k and m above are then the
+    // capacities.  K > k or M > m: no output (every tile empty at offset k).
+    // Otherwise the positions are shifted by k - K, so that the last tile's list
+    // ends at k, the capacity (ids[0 .. k - K) are not part of any list).
+    const int64_t *cap_totals;
 };
+
+__device__ __forceinline__ bool capped_overflow(const L2Args &a) {
+    return a.cap_totals && (a.cap_totals[0] > a.k || a.cap_totals[1] > a.m);
+}
 
 // block_map entry of the blocks past the last chunk (the grid is sized by a bound).
 constexpr uint32_t kNoBlock = 0xFFFFFFFFu;
 
 // One workgroup: chunks of every supertile's list (kL2Threads entries each),
 // their exclusive scan chunk_start (chunk_start[n_super] = all chunks), the
-// block map block_map[b] = (supertile, first list position) of every level-2
-// block, and zeroed per-tile entry counters.  Thread i handles a contiguous
-// run of supertiles.
+// block map (entry xcd_block_inverse(b, chunks) = (supertile, first and end
+// list position, b) for every logical level-2 block b, kNoBlock past the last
+// chunk) and zeroed per-tile entry counters.  Thread i handles a contiguous run
+// of supertiles.
 constexpr int kPlanThreads = 1024;
 
 __global__ __launch_bounds__(kPlanThreads) void l2_plan_kernel(
@@ -1314,7 +1343,8 @@ __global__ __launch_bounds__(kPlanThreads) void l2_plan_kernel(
         const uint32_t end = (uint32_t)(s + 1 < n_super ? super_off[s + 1] : m);
         for (uint32_t i = 0; i < c; ++i) {
             const uint32_t e0 = first + i * kL2Threads;
-            block_map[b + i] = make_uint4((uint32_t)s, e0, min(e0 + kL2Threads, end), 0u);
+            block_map[xcd_block_inverse(b + i, total)] =
+                make_uint4((uint32_t)s, e0, min(e0 + kL2Threads, end), b + i);
         }
         b += c;
     }
@@ -1368,11 +1398,11 @@ __device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int64
 // kBinXcds, do other work).
 __device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x, uint32_t skip = 0,
                                          const uint32_t *__restrict__ table = nullptr) {
-    // the chunks fill all but the last few of the nblocks logical blocks, so the
-    // spread is over the grid (no dependent read of the chunk count)
-    x.b = (uint32_t)xcd_block(blockIdx.x - skip, a.nblocks);
-    const uint4 map = a.block_map[x.b];
-    if (map.x == kNoBlock) return false;
+    // workgroup -> logical block through the map (no dependent read of the chunk
+    // count): the live chunks are spread over the XCDs whatever the grid's bound
+    const uint4 map = a.block_map[blockIdx.x - skip];
+    if (map.x == kNoBlock || capped_overflow(a)) return false;
+    x.b = map.w;  // the logical block: its row of the table
     // this block's row of the table, loaded beside the list entries
     x.trow = table && threadIdx.x < kSuperLocal ? table[(int64_t)x.b * kSuperLocal + threadIdx.x]
                                                 : 0u;
@@ -1454,6 +1484,15 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
     __shared__ uint32_t run_sum[kL2Waves][kSuperLocal];
     const int s = blockIdx.x;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    if (capped_overflow(a)) {  // no lists: every tile empty at the capacity
+        if (tid < kSuperLocal) {
+            const int t = tile_of_local(a, s, tid);
+            if (t >= 0) indexing_offset[t] = (int32_t)a.k;
+        }
+        return;
+    }
+    // capped sort: lists end at the capacity k (see L2Args)
+    const uint32_t shift = a.cap_totals ? (uint32_t)(a.k - a.cap_totals[0]) : 0u;
     const int per = (n_tiles + kL2Threads - 1) / kL2Threads;
     if (fused_scan) {
         const int t0 = min(tid * per, n_tiles), t1 = min(t0 + per, n_tiles);
@@ -1472,7 +1511,7 @@ __global__ __launch_bounds__(kL2Threads) void l2_prefix_kernel(
         uint32_t off = 0;
         if (t >= 0) {
             if (fused_scan) {
-                off = thread_base[t / per] + tile_pre[t];
+                off = thread_base[t / per] + tile_pre[t] + shift;
                 indexing_offset[t] = (int32_t)off;
             } else {
                 off = (uint32_t)indexing_offset[t];
@@ -1666,8 +1705,9 @@ struct L1Args {
     const uint32_t *order;       // Gaussians in depth order
     const uint2 *rects_depth;    // their packed tile rectangles, in the same order
     const int64_t *n_live;       // device: the first *n_live positions hold Gaussians with tiles
-    int64_t n, m;                // Gaussians, entries
+    int64_t n, m;                // Gaussians, entries (capped sort: the entry capacity)
     int super_x, nblocks;
+    const int64_t *cap_totals = nullptr;  // capped sort: device K and M (see L2Args)
 };
 
 // Whether this workgroup's positions start before *n_live (the later ones hold
@@ -1740,9 +1780,11 @@ __global__ __launch_bounds__(kL1Threads) void l1_count_kernel(L1Args a,
 // The level-2 block plan, from block 0 of l1_scatter_kernel (thread d holds
 // supertile d's entry count `tot` and first list position `first`): chunks of
 // kL2Threads list positions per supertile, their exclusive scan chunk_start
-// (chunk_start[n_super] = all chunks) and block_map[b] = (supertile, first
-// and end list position, 0) of every level-2 block, kNoBlock for the blocks
-// past the last chunk up to nblocks.  Contains __syncthreads().
+// (chunk_start[n_super] = all chunks) and the block map: entry w = (supertile,
+// first and end list position, b) of logical block b = xcd_block(w, chunks), so
+// that each XCD's workgroups take a contiguous range of chunks, and kNoBlock
+// for the workgroups past the last chunk up to nblocks.  Contains
+// __syncthreads().
 __device__ __forceinline__ void l1_block_plan(int n_super, uint32_t tot, uint32_t first,
                                               uint32_t *scan_tmp, uint32_t *lds_start,
                                               uint32_t *lds_first, uint32_t *lds_end,
@@ -1760,7 +1802,8 @@ __device__ __forceinline__ void l1_block_plan(int n_super, uint32_t tot, uint32_
     }
     if (d == 0) chunk_start[n_super] = all;
     __syncthreads();
-    for (uint32_t b = d; b < all; b += kL1Threads) {
+    for (uint32_t w = d; w < all; w += kL1Threads) {
+        const uint32_t b = (uint32_t)xcd_block(w, all);  // workgroup w's logical block
         // the last supertile whose first block is <= b (supertiles without
         // chunks share their first block with the next one)
         int lo = 0, hi = n_super - 1;
@@ -1772,7 +1815,7 @@ __device__ __forceinline__ void l1_block_plan(int n_super, uint32_t tot, uint32_
                 hi = mid - 1;
         }
         const uint32_t e0 = lds_first[lo] + (b - lds_start[lo]) * kL2Threads;
-        block_map[b] = make_uint4((uint32_t)lo, e0, min(e0 + kL2Threads, lds_end[lo]), 0u);
+        block_map[w] = make_uint4((uint32_t)lo, e0, min(e0 + kL2Threads, lds_end[lo]), b);
     }
     for (int64_t q = (int64_t)all + d; q < nblocks; q += kL1Threads)
         block_map[q] = make_uint4(kNoBlock, 0u, 0u, 0u);
@@ -1795,6 +1838,7 @@ __global__ __launch_bounds__(kL1Threads) void l1_scatter_kernel(
     for (int64_t t = (int64_t)blockIdx.x * kL1Threads + threadIdx.x; t < n_tiles;
          t += (int64_t)gridDim.x * kL1Threads)
         tile_counts[t] = 0u;
+    if (a.cap_totals && a.cap_totals[1] > a.m) return;  // past the entry capacity: no output
     const int64_t blk = blockIdx.x;  // (round robin over the XCDs measured faster here)
     if (blk != 0 && !l1_live_block(a, blk)) return;  // no entries (block 0 writes the plan)
     uint32_t g = 0;
@@ -1881,6 +1925,7 @@ struct CountWs {
     uint32_t *block_minmax;          // count_tiles: least and greatest key per block
     uint32_t *xform;                 // DepthXform {kmin, shift}
     int64_t *n_live;                 // Gaussians with tiles (keys of depth passes 1..)
+    int64_t *dev_totals;             // K and M in device memory (read by gs_bin_sort_capped)
     uint64_t *m_scan;                // the general level 1's entry total (equals M)
     uint32_t *l1_hist;               // one-pass level 1: kRadixMax x l1_blocks(n) table
     uint32_t *l1_totals;             // one-pass level 1: entries per supertile
@@ -1903,6 +1948,7 @@ inline CountWs carve_count(void *base, int64_t n) {
     w.block_sums = c.take<unsigned long long>(sort_blocks<kDepthItems>(n) * 3);
     w.block_minmax = c.take<uint32_t>(sort_blocks<kDepthItems>(n) * 2);
     w.xform = c.take<uint32_t>(2);
+    w.dev_totals = c.take<int64_t>(2);
     w.n_live = c.take<int64_t>(1);
     w.m_scan = c.take<uint64_t>(1);
     w.l1_hist = c.take<uint32_t>(kRadixMax * l1_blocks(n));
@@ -2120,6 +2166,7 @@ int depth_pass(const CountCall &c, const CountWs &w, int p, hipStream_t stream) 
         x.block_sums = w.block_sums;
         x.block_minmax = c.totals4 ? w.block_minmax : nullptr;
         x.sums_out = c.totals;
+        x.sums_dev = w.dev_totals;
         x.live_out = w.n_live;
     } else {
         x.n_live = w.n_live;
@@ -2203,7 +2250,7 @@ int bin_count_finish(const CountCall &c, hipStream_t stream) {
         if (st) return st;
         hipLaunchKernelGGL(digit_scan_kernel, dim3(grid.n_super), dim3(kScanThreads), 0, stream,
                            w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, 0, nullptr,
-                           nullptr);
+                           nullptr, nullptr);
         return launch_status();
     }
     // supertile entry offsets in depth order (the total equals count_tiles' M; it
@@ -2282,8 +2329,10 @@ int bin_sort(const float *points_image, const float *radii, const float *depths,
              int32_t width, int32_t height, int32_t tile_size, int64_t k, int64_t m,
              const void *count_workspace, void *workspace, size_t workspace_bytes,
              int32_t *indexing_offset, int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
-             int32_t *tiles_touched, int32_t *launch_order, hipStream_t stream) {
-    if (n < 0 || k < 0 || m < 0 || m > k || width <= 0 || height <= 0 || tile_size <= 0)
+             int32_t *tiles_touched, int32_t *launch_order, hipStream_t stream,
+             bool capped = false) {
+    if (n < 0 || k < 0 || m < 0 || (!capped && m > k) || width <= 0 || height <= 0 ||
+        tile_size <= 0)
         return GS_ERR_INVALID_ARGUMENT;
     if (k > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
     Grid g;
@@ -2292,6 +2341,12 @@ int bin_sort(const float *points_image, const float *radii, const float *depths,
     if (g.tiles_x > 65535 || g.tiles_y > 65535)
         return GS_ERR_UNSUPPORTED;  // tile rectangles are staged with 16-bit coordinates
     if ((k == 0) != (m == 0)) return GS_ERR_INVALID_ARGUMENT;
+    // the capped sort takes K and M from the count workspace on the device: one-pass
+    // level 1 and the tile scan inside l2_prefix_kernel only (grids of at most 256
+    // supertiles), no debug outputs
+    if (capped && (g.n_super > kRadixMax || g.n_tiles > kFusedTileScanMax || k == 0 ||
+                   sorted_keys || tiles_touched))
+        return GS_ERR_UNSUPPORTED;
     if (l2_blocks_bound(m, g.n_super) > 0x7fffffffLL) return GS_ERR_TOO_MANY_KEYS;
     const CountWs cw = carve_count(const_cast<void *>(count_workspace), n);
     const BinWs w = carve_bins(workspace, n, m, g);
@@ -2320,7 +2375,8 @@ int bin_sort(const float *points_image, const float *radii, const float *depths,
     const int64_t nb2 = l2_blocks_bound(m, g.n_super);
     // level 1: (supertile, Gaussian) entries in depth order, stably sorted by supertile
     if (g.n_super <= kRadixMax) {  // counts and positions came from gs_bin_count
-        const L1Args la = l1_args(cw, n, m, g.super_x);
+        L1Args la = l1_args(cw, n, m, g.super_x);
+        la.cap_totals = capped ? cw.dev_totals : nullptr;
         hipLaunchKernelGGL(l1_scatter_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
                            (const uint32_t *)cw.l1_hist, (const uint32_t *)cw.l1_totals,
                            g.n_super, w.super_ids, w.super_rects, w.super_off, w.chunk_start,
@@ -2366,6 +2422,7 @@ int bin_sort(const float *points_image, const float *radii, const float *depths,
     l2.height = height;
     l2.tile_size = tile_size;
     l2.nblocks = nb2;
+    l2.cap_totals = capped ? cw.dev_totals : nullptr;
     hipLaunchKernelGGL(l2_count_kernel, dim3((unsigned)nb2), dim3(kL2Threads), 0, stream, l2,
                        w.table, w.tile_counts);
     st = launch_status();
@@ -2409,6 +2466,19 @@ extern "C" int gs_bin_sort(const float *points_image, const float *radii, const 
     return gs::bin_sort(points_image, radii, depths, n, width, height, tile_size, k, m,
                         count_workspace, workspace, workspace_bytes, indexing_offset,
                         gaussian_ids_sorted, sorted_keys, tiles_touched, nullptr, stream);
+}
+
+extern "C" int gs_bin_sort_capped(const float *points_image, const float *radii,
+                                  const float *depths, int64_t n, int32_t width, int32_t height,
+                                  int32_t tile_size, int64_t k_capacity, int64_t m_capacity,
+                                  const void *count_workspace, void *workspace,
+                                  size_t workspace_bytes, int32_t *indexing_offset,
+                                  int32_t *gaussian_ids_sorted, int32_t *launch_order,
+                                  hipStream_t stream) {
+    if (!launch_order || !count_workspace) return GS_ERR_INVALID_ARGUMENT;
+    return gs::bin_sort(points_image, radii, depths, n, width, height, tile_size, k_capacity,
+                        m_capacity, count_workspace, workspace, workspace_bytes, indexing_offset,
+                        gaussian_ids_sorted, nullptr, nullptr, launch_order, stream, true);
 }
 
 extern "C" int gs_bin_sort_ordered(const float *points_image, const float *radii,

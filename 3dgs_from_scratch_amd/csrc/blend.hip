@@ -757,8 +757,9 @@ __device__ __forceinline__ GradTarget grad_target(int lane, float *g_points, flo
 }
 
 // Per-lane state of the backward walk: transmittance and the running sum
-// acc = sum_{k<=i} w_k (g.c_k) of the lane's four pixels, their colour
-// gradients g and gC = g.C.
+// acc = sum_{k<=i} w_k (g.c_k) - g.C of the lane's four pixels (minus the
+// remaining colour gradient S_i, starting at -g.C), their colour gradients g
+// and gC = g.C.
 template <int S>
 struct BackwardLane {
     float T[S], acc[S];
@@ -817,10 +818,10 @@ __device__ __forceinline__ void backward_entry(const BatchLds<W> &s, int j,
         const float a = kSafe ? alpha : (inc ? alpha : 0.0f);
         const float w = a * L.T[q];
         const float gcol = fmaf(L.gr[q], col.x, fmaf(L.gg[q], col.y, L.gb[q] * col.z));
-        const float acc_new = fmaf(w, gcol, L.acc[q]);
+        const float acc_new = fmaf(w, gcol, L.acc[q]);  // -S_i
         const float one_m = (1.0f - a) + kTransmittanceEps;
-        // dalpha = T gcol - (gC - acc_new) / (1 - alpha + eps)
-        const float dalpha = fmaf(acc_new - L.gC[q], __builtin_amdgcn_rcpf(one_m), L.T[q] * gcol);
+        // dalpha = T gcol - S_i / (1 - alpha + eps)
+        const float dalpha = fmaf(acc_new, __builtin_amdgcn_rcpf(one_m), L.T[q] * gcol);
         const float h = kSafe ? (inc ? a * dalpha : 0.0f) : a * dalpha;
         const float ws = kSafe ? (inc ? w : 0.0f) : w;
         if (special) sGd += inc ? G * dalpha : 0.0f;
@@ -952,7 +953,7 @@ __global__ __launch_bounds__(kWave * W) void blend_backward_kernel(
         L.gg[q] = gg;
         L.gb[q] = gb;
         L.gC[q] = gr * cr[q] + gg * cg[q] + gb * cb[q];
-        L.acc[q] = 0.0f;
+        L.acc[q] = -L.gC[q];
         finite = finite && isfinite(gr) && isfinite(gg) && isfinite(gb) && isfinite(L.gC[q]);
         // active while !(T < T_thr); pixels outside the image or with a zero
         // gradient (skipped as in src/cuda/kernel.cu:1028-1030) start inactive

@@ -40,6 +40,7 @@ __all__ = [
     "compute_tile_intersection",
     "compute_tile_intersection_debug",
     "compute_tile_intersection_ordered",
+    "tile_intersection_capped",
     "rasterize",
     "rasterize_backward",
     "rasterize_work",
@@ -369,6 +370,7 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         k, m, kmin, kmax = (int(v) for v in (host_totals if n > 0 else totals.cpu()).tolist())
         if n > 0:
             _DEPTH_RANGE[dev.index] = (kmin, kmax)
+            _grow_capacity(dev, k, m)
         if k > 2**31 - 1:
             raise RasterizerError(f"compute_tile_intersection: {k} keys exceed the int32 range")
         sz2 = ctypes.c_size_t(0)
@@ -412,6 +414,131 @@ def compute_tile_intersection_ordered(points_image, radii, depths, mask, width, 
     (gs_bin_sort_ordered).  Returns (indexing_offset, gaussian_ids_sorted, order)."""
     return _tile_intersection(points_image, radii, depths, mask, width, height, tile_size, False,
                               ordered=True)
+
+
+# Capacities of the capped sort per device: K and M of the largest lists seen,
+# plus a quarter and a constant (a scene's K varies from view to view).
+# CAPPED_BINNING = False makes tile_intersection_capped bin with exact sizes.
+CAPPED_BINNING = True
+_CAPACITY: dict = {}
+
+
+def _grow_capacity(dev, k: int, m: int) -> None:
+    cap = _CAPACITY.get(dev.index, (0, 0))
+    want = (k + k // 4 + 4096, m + m // 4 + 1024)
+    _CAPACITY[dev.index] = (max(cap[0], want[0]), max(cap[1], want[1]))
+
+
+class CappedCheck:
+    """The pending check of a capped sort (tile_intersection_capped): ok() waits
+    for the count's totals (K, M and the depth key range), which the GPU has
+    usually written long before, records them for the next call's depth hint
+    and capacities, and returns whether the lists fit the capacities -- if not,
+    no list was written and the caller bins again with exact sizes.  The pinned
+    totals are released only after that wait."""
+
+    __slots__ = ("_ready", "_host", "_dev_totals", "_caps", "_device", "_result")
+
+    def __init__(self, ready, host_totals, dev_totals, caps, device):
+        self._ready, self._host, self._dev_totals = ready, host_totals, dev_totals
+        self._caps, self._device, self._result = caps, device, None
+
+    def ok(self) -> bool:
+        if self._result is None:
+            _wait(self._ready)
+            src = self._host if self._dev_totals is None else self._dev_totals.cpu()
+            k, m, kmin, kmax = (int(v) for v in src.tolist())
+            _DEPTH_RANGE[self._device.index] = (kmin, kmax)
+            _grow_capacity(self._device, k, m)
+            self._result = k <= self._caps[0] and m <= self._caps[1]
+            self._host = self._dev_totals = None
+        return self._result
+
+    def __del__(self):
+        if self._result is None and self._ready is not None:
+            self._ready.synchronize()
+
+
+def tile_intersection_capped(points_image, radii, depths, mask, width, height, tile_size=16):
+    """compute_tile_intersection_ordered without the host read between the
+    count and the sort (gs_bin_sort_capped): the lists are sized by this
+    device's capacities, K and M stay on the device, and the lists end at the
+    capacity (indexing_offset shifted by capacity - K; the result is a valid
+    blend input with k = gaussian_ids_sorted.numel()).  Returns (indexing_offset,
+    gaussian_ids_sorted, launch_order, check): call check.ok() after queueing
+    the work that reads the lists; False means they did not fit (every tile is
+    then empty) and must be binned again, e.g. by
+    compute_tile_intersection_ordered, which also grows the capacities.  check is
+    None when the lists were binned with exact sizes: the first call on a device,
+    grids of more than 256 supertiles (16384 tiles), or no Gaussians."""
+    dev = _device_of(points_image)
+    n = points_image.shape[0]
+    f32 = torch.float32
+    width, height, tile_size = int(width), int(height), int(tile_size)
+    if tile_size <= 0 or width <= 0 or height <= 0:
+        raise RuntimeError("compute_tile_intersection: width, height and tile_size must be > 0")
+    tiles_x = (width + tile_size - 1) // tile_size
+    tiles_y = (height + tile_size - 1) // tile_size
+    n_tiles = tiles_x * tiles_y
+    n_super = ((tiles_x + 7) // 8) * ((tiles_y + 7) // 8)
+    caps = _CAPACITY.get(dev.index)
+    if not CAPPED_BINNING or caps is None or n == 0 or n_super > 256 or n_tiles > 16384:
+        off, ids, order = _tile_intersection(points_image, radii, depths, mask, width, height,
+                                             tile_size, False, ordered=True)
+        return off, ids, order, None
+    points_image = _prep(points_image, "points_image", f32, (n, 2), dev)
+    radii = _prep(radii, "radii", f32, (n, 2), dev)
+    depths = _prep(depths, "depths", f32, (n,), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    lib = _lib.load()
+    k_cap, m_cap = caps
+    with torch.cuda.device(dev):
+        stream = _stream(dev)
+        sz = ctypes.c_size_t(0)
+        _lib.check(lib.gs_bin_count_workspace_size(n, ctypes.byref(sz)), "workspace query")
+        ws_count = torch.empty((max(sz.value, 1),), dtype=torch.uint8, device=dev)
+        sz2 = ctypes.c_size_t(0)
+        _lib.check(lib.gs_bin_sort_workspace_size(n, k_cap, m_cap, width, height, tile_size,
+                                                  ctypes.byref(sz2)), "workspace query")
+        ws_sort = torch.empty((max(sz2.value, 1),), dtype=torch.uint8, device=dev)
+        indexing_offset = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
+        order = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
+        ids = torch.empty((k_cap,), dtype=torch.int32, device=dev)
+        host_totals = torch.empty((4,), dtype=torch.int64, pin_memory=True)
+        totals_ptr = _pinned_device_pointer(host_totals)
+        dev_totals = None
+        if totals_ptr is None:  # device memory, read with a copy in check.ok()
+            dev_totals = torch.empty((4,), dtype=torch.int64, device=dev)
+            totals_ptr = _ptr(dev_totals)
+        args = (_ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
+                tile_size, _ptr(ws_count), sz.value, totals_ptr, stream)
+        hint_kmin, hint_shift = _depth_hint(dev)
+        ev = _lib.timer.record("bin_count", dev)
+        ready = None
+        check = None
+        try:
+            _lib.check(lib.gs_bin_count_begin_hinted(*args[:10], hint_kmin, hint_shift,
+                                                     *args[10:]),
+                       "compute_tile_intersection (count)")
+            ready = torch.cuda.Event()
+            ready.record(torch.cuda.current_stream(dev))
+            check = CappedCheck(ready, host_totals, dev_totals, caps, dev)
+            _lib.check(lib.gs_bin_count_finish(*args), "compute_tile_intersection (count)")
+            _lib.timer.stop(ev, dev)
+            ev = _lib.timer.record("bin_sort", dev)
+            _lib.check(lib.gs_bin_sort_capped(
+                _ptr(points_image), _ptr(radii), _ptr(depths), n, width, height, tile_size,
+                k_cap, m_cap, _ptr(ws_count), _ptr(ws_sort), sz2.value, _ptr(indexing_offset),
+                _ptr(ids), _ptr(order), stream), "compute_tile_intersection (sort)")
+            _lib.timer.stop(ev, dev)
+        except BaseException:
+            # the device may still write the pinned totals: wait before releasing them
+            if check is not None:
+                check.ok()
+            else:
+                torch.cuda.current_stream(dev).synchronize()
+            raise
+    return indexing_offset, ids, order, check
 
 
 def compute_tile_intersection_debug(points_image, radii, depths, mask, width, height, tile_size=16):

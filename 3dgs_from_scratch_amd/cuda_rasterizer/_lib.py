@@ -33,6 +33,8 @@ SIGNATURES = {
     "gs_bin_sort": [_P] * 3 + [_I64, _I32, _I32, _I32, _I64, _I64, _P, _P, _SZ] + [_P] * 4 + [_P],
     "gs_bin_sort_ordered": [_P] * 3 + [_I64, _I32, _I32, _I32, _I64, _I64, _P, _P, _SZ]
     + [_P] * 5 + [_P],
+    "gs_bin_sort_capped": [_P] * 3 + [_I64, _I32, _I32, _I32, _I64, _I64, _P, _P, _SZ]
+    + [_P] * 3 + [_P],
     "gs_rasterize": [_P, _P, _I32, _I64] + [_P] * 4 + [_I64, _I32, _I32, _I32, _F, _F, _F, _P, _P],
     "gs_rasterize_work": [_P, _P, _I32, _I64] + [_P] * 3 + [_I64, _I32, _I32, _I32, _F, _F, _F]
     + [_P, _P, _P],

@@ -124,9 +124,11 @@ class RenderL1Function(torch.autograd.Function):
             max_radius, width, height, with_colors=not beside)
         pending = colors_beside(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest,
                                 mask) if beside else None
+        check = None
         try:
-            # with a launch order for the forward's tiles from the list lengths
-            off, ids, list_order = _cr.compute_tile_intersection_ordered(
+            # with a launch order for the forward's tiles from the list lengths; sized
+            # by capacities, so no host read of K and M before the blend is queued
+            off, ids, list_order, check = _cr.tile_intersection_capped(
                 pts, radii, depths, mask, width, height, 16)
             # the blend gradients' accumulators, zeroed by the forward blend launch
             acc = _cr.blend_grad_accumulators(means.shape[0], means.device)
@@ -145,10 +147,21 @@ class RenderL1Function(torch.autograd.Function):
                 previous = None
         # the forward launches heaviest first by the view's last render when there
         # is one, else in the order from the list lengths
-        image, display, loss = _cr.rasterize_display_l1(
-            off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
-            transmittance_threshold, chi_squared_threshold, clear=acc, schedule=sched,
-            forward_schedule=previous, forward_order=None if previous is not None else list_order)
+        def blend_forward():
+            return _cr.rasterize_display_l1(
+                off, ids, pts, conic, opac, colors, width, height, target, alpha_threshold,
+                transmittance_threshold, chi_squared_threshold, clear=acc, schedule=sched,
+                forward_schedule=previous,
+                forward_order=None if previous is not None else list_order)
+
+        try:
+            image, display, loss = blend_forward()
+        finally:
+            fits = check is None or check.ok()
+        if not fits:  # the lists outgrew the capacities: bin with exact sizes, blend again
+            off, ids, list_order = _cr.compute_tile_intersection_ordered(
+                pts, radii, depths, mask, width, height, 16)
+            image, display, loss = blend_forward()
         if schedule_cache is not None and view_id is not None:
             schedule_cache[view_id] = sched
         ssim_saved = ()

@@ -221,17 +221,30 @@ def render(
                                               sh_coeffs_rest, mask)
 
     tile_size = 16
+    check = None
     try:
-        # the tile lists, and a launch order for the blend forward from their lengths
-        indexing_offset, gaussian_ids_sorted, order = _cr.compute_tile_intersection_ordered(
+        # the tile lists, and a launch order for the blend forward from their lengths;
+        # sized by capacities, so no host read of K and M before the blend is queued
+        indexing_offset, gaussian_ids_sorted, order, check = _cr.tile_intersection_capped(
             points_img.detach(), radii, depths, mask, width, height, tile_size)
     finally:
         if colors_ready is not None:
             colors_ready.wait()
-    display = RenderRasterizeFunction.apply(indexing_offset, gaussian_ids_sorted, points_img,
-                                            cov_inv_img, opacities, colors, width, height,
-                                            tile_size, alpha_threshold, transmittance_threshold,
-                                            chi_squared_threshold, torch.is_grad_enabled(), order)
+
+    def blend():
+        return RenderRasterizeFunction.apply(
+            indexing_offset, gaussian_ids_sorted, points_img, cov_inv_img, opacities, colors,
+            width, height, tile_size, alpha_threshold, transmittance_threshold,
+            chi_squared_threshold, torch.is_grad_enabled(), order)
+
+    try:
+        display = blend()
+    finally:
+        fits = check is None or check.ok()
+    if not fits:  # the lists outgrew the capacities: bin with exact sizes, blend again
+        indexing_offset, gaussian_ids_sorted, order = _cr.compute_tile_intersection_ordered(
+            points_img.detach(), radii, depths, mask, width, height, tile_size)
+        display = blend()
     return display, points_img, radii
 
 

@@ -203,6 +203,30 @@ int gs_bin_sort_ordered(const float *points_image, const float *radii, const flo
                         int32_t *gaussian_ids_sorted, uint64_t *sorted_keys,
                         int32_t *tiles_touched, int32_t *launch_order, hipStream_t stream);
 
+/*
+ * gs_bin_sort_ordered sized by capacities instead of K and M, so that it can be
+ * queued before the host has read them: K and M come from count_workspace on
+ * the device (written by the gs_bin_count_begin* call that filled it).  The
+ * workspace is sized by gs_bin_sort_workspace_size(n, k_capacity, m_capacity,
+ * ...); gaussian_ids_sorted holds k_capacity ids.  With K <= k_capacity and
+ * M <= m_capacity the lists are the exact ones, shifted by k_capacity - K:
+ * indexing_offset[t] is K's offset plus that shift, so the lists end at
+ * k_capacity and (indexing_offset, gaussian_ids_sorted, k_capacity) is a valid
+ * input of every blend entry (ids[0 .. k_capacity - K) belong to no tile).
+ * Otherwise nothing is written but indexing_offset, all k_capacity (every tile
+ * empty), and launch_order; the caller reads K and M (the totals of the count)
+ * and redoes the binning with exact sizes.  Grids of at most 256 supertiles of
+ * 8x8 tiles (16384 tiles; e.g. up to 2048x2048 at tile size 16), else
+ * GS_ERR_UNSUPPORTED.  No counterpart in the reference extension (its
+ * rasterizer.cpp:322 reads num_rendered with .item() before sizing the sort).
+ */
+int gs_bin_sort_capped(const float *points_image, const float *radii, const float *depths,
+                       int64_t n, int32_t width, int32_t height, int32_t tile_size,
+                       int64_t k_capacity, int64_t m_capacity, const void *count_workspace,
+                       void *workspace, size_t workspace_bytes, int32_t *indexing_offset,
+                       int32_t *gaussian_ids_sorted, int32_t *launch_order,
+                       hipStream_t stream);
+
 /* --------------------------------------------------------------------- blend */
 
 /*

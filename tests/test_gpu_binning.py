@@ -268,3 +268,69 @@ def test_depth_hint_rejects_wide_shift(gpu, monkeypatch):
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
     with pytest.raises(cr.RasterizerError):
         cr.compute_tile_intersection(d(pts), d(radii), d(depths), d(mask), 64, 64, 16)
+
+
+def _capped(gpu, pts, radii, depths, mask, width, height, caps):
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    cr._CAPACITY[gpu.index] = caps
+    out = cr.tile_intersection_capped(d(pts), d(radii), d(depths), d(mask), width, height, 16)
+    ok = out[3].ok() if out[3] is not None else None
+    return out[:3], ok
+
+
+@pytest.mark.parametrize("width,height", [(256, 256), (800, 600), (2048, 2048)])
+def test_capped_sort_equals_exact_lists_shifted(gpu, monkeypatch, width, height):
+    """gs_bin_sort_capped, queued before the host reads K and M: with room to
+    spare, each tile's list is the exact one and the offsets are the exact ones
+    shifted by capacity - K, so the lists end at the capacity; the launch order
+    is the same.  Also with capacities exactly K and M (no spare room)."""
+    monkeypatch.setattr(cr, "_CAPACITY", dict(cr._CAPACITY))
+    pts, radii, depths, mask = _random_splats(40000, width, height, seed=width + 1)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    off, ids, order = cr.compute_tile_intersection_ordered(d(pts), d(radii), d(depths), d(mask),
+                                                           width, height, 16)
+    k = ids.numel()
+    ref_off, ref_ids, _, _ = binning.tile_layout(pts, radii, depths, mask, width, height, 16)
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    for caps in [(k + 12345, 10**7), (k, None)]:
+        if caps[1] is None:  # the exact M: the smallest capacity that fits
+            lo, hi = 1, 10**7
+            while lo < hi:  # M from the capped call's own check
+                mid = (lo + hi) // 2
+                _, fits = _capped(gpu, pts, radii, depths, mask, width, height, (k, mid))
+                lo, hi = (lo, mid) if fits else (mid + 1, hi)
+            caps = (k, lo)
+            _, fits = _capped(gpu, pts, radii, depths, mask, width, height, (k, lo - 1))
+            assert not fits
+        (c_off, c_ids, c_order), fits = _capped(gpu, pts, radii, depths, mask, width, height,
+                                                caps)
+        assert fits
+        shift = caps[0] - k
+        assert c_ids.numel() == caps[0]
+        assert torch.equal(c_off.cpu() - shift, off.cpu())
+        assert torch.equal(c_ids[shift:].cpu(), ids.cpu())
+        assert torch.equal(c_order, order)
+
+
+def test_capped_sort_overflow_leaves_empty_lists(gpu, monkeypatch):
+    """Capacities below K (or M): check.ok() is False and every tile is empty at
+    the capacity, so a blend over the result reads nothing; the next exact call
+    grows the capacities so that a capped call fits again."""
+    monkeypatch.setattr(cr, "_CAPACITY", dict(cr._CAPACITY))
+    pts, radii, depths, mask = _random_splats(20000, 320, 240, seed=5)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    off, ids, _ = cr.compute_tile_intersection_ordered(d(pts), d(radii), d(depths), d(mask), 320,
+                                                       240, 16)
+    k = ids.numel()
+    for caps in [(k - 1, 10**7), (k + 10, 1)]:
+        (c_off, c_ids, c_order), fits = _capped(gpu, pts, radii, depths, mask, 320, 240, caps)
+        assert fits is False
+        assert bool((c_off == caps[0]).all())
+        cr.check_forward_order(c_order, c_off.numel())
+    cr._CAPACITY.pop(gpu.index)
+    out = cr.tile_intersection_capped(d(pts), d(radii), d(depths), d(mask), 320, 240, 16)
+    assert out[3] is None and torch.equal(out[1], ids)  # first call: exact sizes
+    out = cr.tile_intersection_capped(d(pts), d(radii), d(depths), d(mask), 320, 240, 16)
+    assert out[3] is not None and out[3].ok()
+    shift = out[1].numel() - k
+    assert shift > 0 and torch.equal(out[1][shift:], ids) and torch.equal(out[0] - shift, off)

@@ -445,3 +445,39 @@ def test_render_l1_with_ssim_matches_drop_in_path(gpu, lam):
     assert helpers.max_abs(disp, img.detach()) <= 1e-4 * 255
     for k in helpers.PARAMS:
         assert helpers.rel_l2(b[k].grad, a[k].grad) <= 1e-4, k
+
+
+def test_render_l1_and_render_with_outgrown_capacities(gpu, monkeypatch):
+    """The fused step and render() bin with capacity-sized lists and check K and M
+    only after the blend is queued; when the lists outgrow the capacities they bin
+    again with exact sizes.  Forced small capacities give the loss, display and
+    gradients of roomy ones."""
+    import cuda_rasterizer as cr
+    from cuda_rasterizer.wrapper import render
+
+    monkeypatch.setattr(cr, "_CAPACITY", {})
+    p, cam, target = helpers.scene_orbit(20_000, 256, 192, 300.0, seed=31)
+    w2c, K, tgt = cam["w2c"].to(gpu), cam["K"].to(gpu), target.to(gpu)
+    out = {}
+    for mode in ("first", "roomy", "small", "roomy again"):
+        if mode == "small":
+            cr._CAPACITY[gpu.index] = (1000, 100)
+        b = _raw_leaves(p, gpu)
+        loss, display, _, _ = render_l1(w2c, K, 256, 192, b["means"], b["log_scales"],
+                                        b["quats_raw"], b["opacity_logits"], b["sh_dc"],
+                                        b["sh_rest"], tgt)
+        loss.backward()
+        sc, qq, op = helpers.activated(b)
+        if mode == "small":
+            cr._CAPACITY[gpu.index] = (1000, 100)
+        disp, _, _ = render(w2c, K, 256, 192, b["means"].detach(), sc.detach(), qq.detach(),
+                            op.detach(), b["sh_dc"].detach(), b["sh_rest"].detach())
+        out[mode] = (float(loss), display.clone(), disp.clone(),
+                     {k: t.grad.clone() for k, t in b.items()})
+    assert cr._CAPACITY[gpu.index][0] > 1000  # grown again by the exact binning
+    for mode in ("roomy", "small", "roomy again"):
+        assert out[mode][0] == out["first"][0], mode
+        assert torch.equal(out[mode][1], out["first"][1]), mode
+        assert torch.equal(out[mode][2], out["first"][2]), mode
+        for k in helpers.PARAMS:
+            assert helpers.rel_l2(out[mode][3][k], out["first"][3][k]) <= 1e-5, (mode, k)

@@ -260,17 +260,17 @@ def test_colours_beside_binning_with_non_contiguous_inputs(gpu, monkeypatch):
 
     # binning fails after the fork: the error reaches the caller and the wait
     # for the colours is still queued, so the next call is unaffected
-    real = cr.compute_tile_intersection_ordered
+    real = cr.tile_intersection_capped
 
     def failing(*a, **k):
         raise cr.RasterizerError("planted binning failure")
 
-    monkeypatch.setattr(cr, "compute_tile_intersection_ordered", failing)
+    monkeypatch.setattr(cr, "tile_intersection_capped", failing)
     v, _ = leaves(False)
     with pytest.raises(cr.RasterizerError, match="planted"):
         render_l1(w2c_t, K, W, H, v["means"], v["log_scales"], v["quats_raw"],
                   v["opacity_logits"], v["sh_dc"], v["sh_rest"], tgt)
-    monkeypatch.setattr(cr, "compute_tile_intersection_ordered", real)
+    monkeypatch.setattr(cr, "tile_intersection_capped", real)
     v, _ = leaves(False)
     loss, _, _, _ = render_l1(w2c_t, K, W, H, v["means"], v["log_scales"], v["quats_raw"],
                               v["opacity_logits"], v["sh_dc"], v["sh_rest"], tgt)
