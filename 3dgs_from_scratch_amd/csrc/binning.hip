@@ -1372,12 +1372,12 @@ struct L2Block {
 // Bit j (= ly * kSuper + lx) set for every tile of supertile s that Gaussian
 // g (list entry e, whose tile rectangle is super_rects[e]) covers; the covered
 // local rectangle goes to x.
-__device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, int64_t e, int s,
+__device__ __forceinline__ uint64_t local_mask(const L2Args &a, int32_t g, uint2 packed, int s,
                                                L2Block &x) {
     x.lx0 = x.ly0 = 1;
     x.lx1 = x.ly1 = 0;
     if (g < 0 || (int64_t)g >= a.n) return 0;
-    const TileRect r = unpack_rect(a.super_rects[e]);  // Gaussians in the lists have tiles
+    const TileRect r = unpack_rect(packed);  // Gaussians in the lists have tiles
     const int ox = (s % a.super_x) * kSuper, oy = (s / a.super_x) * kSuper;
     const int x0 = max(r.tx0 - ox, 0), x1 = min(r.tx1 - ox, kSuper - 1);
     const int y0 = max(r.ty0 - oy, 0), y1 = min(r.ty1 - oy, kSuper - 1);
@@ -1409,15 +1409,15 @@ __device__ __forceinline__ bool l2_block(const L2Args &a, L2Block &x, uint32_t s
     x.s = (int)map.x;
     const int64_t end = (int64_t)map.z;
     const int64_t e = (int64_t)map.y + threadIdx.x;
-    x.g = -1;
-    x.mask = 0;
-    if (e < end) {
-        x.g = a.super_ids[e];
-        x.mask = local_mask(a, x.g, e, x.s, x);
-    } else {
-        x.lx0 = x.ly0 = 1;
-        x.lx1 = x.ly1 = 0;
-    }
+    // every lane loads (a block holds at least one entry, so the clamped position
+    // is in its list): no load on a conditional path, which would make the
+    // compiler wait for all memory operations, stores included, before each of the
+    // scatter's stores of x.g
+    const int64_t ec = e < end ? e : end - 1;
+    const int32_t g = a.super_ids[ec];
+    const uint2 packed = a.super_rects[ec];
+    x.g = e < end ? g : -1;
+    x.mask = local_mask(a, x.g, packed, x.s, x);
     return true;
 }
 

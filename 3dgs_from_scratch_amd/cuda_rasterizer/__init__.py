@@ -370,7 +370,7 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
         k, m, kmin, kmax = (int(v) for v in (host_totals if n > 0 else totals.cpu()).tolist())
         if n > 0:
             _DEPTH_RANGE[dev.index] = (kmin, kmax)
-            _grow_capacity(dev, k, m)
+            _set_capacity((dev.index, width, height, tile_size), k, m)
         if k > 2**31 - 1:
             raise RasterizerError(f"compute_tile_intersection: {k} keys exceed the int32 range")
         sz2 = ctypes.c_size_t(0)
@@ -416,17 +416,18 @@ def compute_tile_intersection_ordered(points_image, radii, depths, mask, width, 
                               ordered=True)
 
 
-# Capacities of the capped sort per device: K and M of the largest lists seen,
-# plus a quarter and a constant (a scene's K varies from view to view).
-# CAPPED_BINNING = False makes tile_intersection_capped bin with exact sizes.
+# Capacities of the capped sort per (device, image and tile size): K and M of
+# the last lists binned there, plus a quarter and a constant (a scene's K varies
+# from view to view and grows with densification).  Taken from the last call,
+# not the largest, so that a smaller scene at the same resolution does not keep
+# an oversized sort.  CAPPED_BINNING = False makes tile_intersection_capped bin
+# with exact sizes.
 CAPPED_BINNING = True
 _CAPACITY: dict = {}
 
 
-def _grow_capacity(dev, k: int, m: int) -> None:
-    cap = _CAPACITY.get(dev.index, (0, 0))
-    want = (k + k // 4 + 4096, m + m // 4 + 1024)
-    _CAPACITY[dev.index] = (max(cap[0], want[0]), max(cap[1], want[1]))
+def _set_capacity(key, k: int, m: int) -> None:
+    _CAPACITY[key] = (k + k // 4 + 4096, m + m // 4 + 1024)
 
 
 class CappedCheck:
@@ -437,19 +438,19 @@ class CappedCheck:
     no list was written and the caller bins again with exact sizes.  The pinned
     totals are released only after that wait."""
 
-    __slots__ = ("_ready", "_host", "_dev_totals", "_caps", "_device", "_result")
+    __slots__ = ("_ready", "_host", "_dev_totals", "_caps", "_key", "_result")
 
-    def __init__(self, ready, host_totals, dev_totals, caps, device):
+    def __init__(self, ready, host_totals, dev_totals, caps, key):
         self._ready, self._host, self._dev_totals = ready, host_totals, dev_totals
-        self._caps, self._device, self._result = caps, device, None
+        self._caps, self._key, self._result = caps, key, None
 
     def ok(self) -> bool:
         if self._result is None:
             _wait(self._ready)
             src = self._host if self._dev_totals is None else self._dev_totals.cpu()
             k, m, kmin, kmax = (int(v) for v in src.tolist())
-            _DEPTH_RANGE[self._device.index] = (kmin, kmax)
-            _grow_capacity(self._device, k, m)
+            _DEPTH_RANGE[self._key[0]] = (kmin, kmax)
+            _set_capacity(self._key, k, m)
             self._result = k <= self._caps[0] and m <= self._caps[1]
             self._host = self._dev_totals = None
         return self._result
@@ -481,7 +482,8 @@ def tile_intersection_capped(points_image, radii, depths, mask, width, height, t
     tiles_y = (height + tile_size - 1) // tile_size
     n_tiles = tiles_x * tiles_y
     n_super = ((tiles_x + 7) // 8) * ((tiles_y + 7) // 8)
-    caps = _CAPACITY.get(dev.index)
+    key = (dev.index, width, height, tile_size)
+    caps = _CAPACITY.get(key)
     if not CAPPED_BINNING or caps is None or n == 0 or n_super > 256 or n_tiles > 16384:
         off, ids, order = _tile_intersection(points_image, radii, depths, mask, width, height,
                                              tile_size, False, ordered=True)
@@ -522,7 +524,7 @@ def tile_intersection_capped(points_image, radii, depths, mask, width, height, t
                        "compute_tile_intersection (count)")
             ready = torch.cuda.Event()
             ready.record(torch.cuda.current_stream(dev))
-            check = CappedCheck(ready, host_totals, dev_totals, caps, dev)
+            check = CappedCheck(ready, host_totals, dev_totals, caps, key)
             _lib.check(lib.gs_bin_count_finish(*args), "compute_tile_intersection (count)")
             _lib.timer.stop(ev, dev)
             ev = _lib.timer.record("bin_sort", dev)

@@ -272,7 +272,7 @@ def test_depth_hint_rejects_wide_shift(gpu, monkeypatch):
 
 def _capped(gpu, pts, radii, depths, mask, width, height, caps):
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
-    cr._CAPACITY[gpu.index] = caps
+    cr._CAPACITY[(gpu.index, width, height, 16)] = caps
     out = cr.tile_intersection_capped(d(pts), d(radii), d(depths), d(mask), width, height, 16)
     ok = out[3].ok() if out[3] is not None else None
     return out[:3], ok
@@ -327,7 +327,7 @@ def test_capped_sort_overflow_leaves_empty_lists(gpu, monkeypatch):
         assert fits is False
         assert bool((c_off == caps[0]).all())
         cr.check_forward_order(c_order, c_off.numel())
-    cr._CAPACITY.pop(gpu.index)
+    cr._CAPACITY.pop((gpu.index, 320, 240, 16))
     out = cr.tile_intersection_capped(d(pts), d(radii), d(depths), d(mask), 320, 240, 16)
     assert out[3] is None and torch.equal(out[1], ids)  # first call: exact sizes
     out = cr.tile_intersection_capped(d(pts), d(radii), d(depths), d(mask), 320, 240, 16)

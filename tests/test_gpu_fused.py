@@ -461,7 +461,7 @@ def test_render_l1_and_render_with_outgrown_capacities(gpu, monkeypatch):
     out = {}
     for mode in ("first", "roomy", "small", "roomy again"):
         if mode == "small":
-            cr._CAPACITY[gpu.index] = (1000, 100)
+            cr._CAPACITY[(gpu.index, 256, 192, 16)] = (1000, 100)
         b = _raw_leaves(p, gpu)
         loss, display, _, _ = render_l1(w2c, K, 256, 192, b["means"], b["log_scales"],
                                         b["quats_raw"], b["opacity_logits"], b["sh_dc"],
@@ -469,12 +469,12 @@ def test_render_l1_and_render_with_outgrown_capacities(gpu, monkeypatch):
         loss.backward()
         sc, qq, op = helpers.activated(b)
         if mode == "small":
-            cr._CAPACITY[gpu.index] = (1000, 100)
+            cr._CAPACITY[(gpu.index, 256, 192, 16)] = (1000, 100)
         disp, _, _ = render(w2c, K, 256, 192, b["means"].detach(), sc.detach(), qq.detach(),
                             op.detach(), b["sh_dc"].detach(), b["sh_rest"].detach())
         out[mode] = (float(loss), display.clone(), disp.clone(),
                      {k: t.grad.clone() for k, t in b.items()})
-    assert cr._CAPACITY[gpu.index][0] > 1000  # grown again by the exact binning
+    assert cr._CAPACITY[(gpu.index, 256, 192, 16)][0] > 1000  # grown again by exact binning
     for mode in ("roomy", "small", "roomy again"):
         assert out[mode][0] == out["first"][0], mode
         assert torch.equal(out[mode][1], out["first"][1]), mode
