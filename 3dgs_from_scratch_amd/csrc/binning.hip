@@ -233,6 +233,17 @@ __device__ __forceinline__ TileRect unpack_rect(uint2 p) {
 // Packed tile rectangle of a Gaussian without tiles: tx0 > tx1.
 constexpr uint2 kEmptyRect = {0xffffu, 0xffffu};
 
+// rects[val] for a Gaussian index val < n, else kEmptyRect.  The load is from a
+// clamped index (a global load of the rectangle array in every case, then a
+// select): a choice between two addresses, one of them the constant, compiles
+// to a flat load, which makes every later store wait for it and all before it.
+__device__ __forceinline__ uint2 rect_or_empty(const uint2 *__restrict__ rects, uint32_t val,
+                                               int64_t n) {
+    const bool in = val < (uint64_t)n;
+    const uint2 r = rects[in ? val : 0u];
+    return in ? r : kEmptyRect;
+}
+
 // Tiles of a packed rectangle (0 for kEmptyRect).
 __device__ __forceinline__ uint32_t rect_tiles(uint2 packed) {
     const TileRect t = unpack_rect(packed);
@@ -482,7 +493,7 @@ __device__ __forceinline__ void block_scatter(const uint32_t (&k)[ITEMS],
             vals_out[dst] = val;
             if (kPayload) pay_out[dst] = s.spay[p];
             if (counts_out || rects_out) {
-                const uint2 r = val < (uint64_t)n ? rects[val] : kEmptyRect;
+                const uint2 r = rect_or_empty(rects, val, n);
                 if (counts_out) counts_out[dst] = rect_supertiles(r);
                 if (rects_out) rects_out[dst] = r;
             }
@@ -852,10 +863,13 @@ struct SegArgs {
 
 // Per-position outputs of the sorted order: the rectangle or the supertile
 // count of the Gaussian at depth position p (sentinels past the live keys).
-__device__ __forceinline__ void seg_emit(const SegArgs &a, int64_t p, uint32_t val) {
-    const uint2 r = val < (uint64_t)a.n ? a.rects[val] : kEmptyRect;
+__device__ __forceinline__ void seg_store(const SegArgs &a, int64_t p, uint2 r) {
     if (a.counts_out) a.counts_out[p] = rect_supertiles(r);
     if (a.rects_out) a.rects_out[p] = r;
+}
+
+__device__ __forceinline__ void seg_emit(const SegArgs &a, int64_t p, uint32_t val) {
+    seg_store(a, p, rect_or_empty(a.rects, val, a.n));
 }
 
 // The chunk [start, end) (more than kSegMax keys) sorted by this workgroup
@@ -1051,13 +1065,18 @@ __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(SegArgs a) {
             }
         }
     }
-    // sorted: item it of this thread is position seg_slot(it, ipw) of the chunk
+    // sorted: item it of this thread is position seg_slot(it, ipw) of the chunk;
+    // every rectangle is loaded before the first store, so the loads overlap
+    uint2 r[kSegItems];
+#pragma unroll
+    for (int it = 0; it < kSegItems; ++it)
+        r[it] = rect_or_empty(a.rects, valid[it] ? v[it] : 0xFFFFFFFFu, a.n);
 #pragma unroll
     for (int it = 0; it < kSegItems; ++it) {
         if (!valid[it]) continue;
         const uint32_t p = start + (uint32_t)seg_slot(it, ipw);
         a.vals[p] = v[it];
-        seg_emit(a, p, v[it]);
+        seg_store(a, p, r[it]);
     }
 }
 
