@@ -1098,8 +1098,10 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     unsigned long long *__restrict__ block_sums, uint32_t *__restrict__ block_minmax,
     uint32_t hint_kmin, int hint_shift, uint32_t *__restrict__ hist,
     uint32_t *__restrict__ xform) {
-    __shared__ unsigned long long sum_tmp[kSortThreads / kWave + 1];
-    __shared__ uint32_t mm[2][kSortThreads / kWave];
+    // per-wave tiles and supertile entries; Gaussians with tiles, least and
+    // greatest key
+    __shared__ unsigned long long wave_sum[2][kSortThreads / kWave];
+    __shared__ uint32_t wave_red[3][kSortThreads / kWave];
     __shared__ uint32_t counts[kRadixMax];
     if (hist) {  // with a depth hint: the first depth pass's histogram, zeroed here
         for (int d = threadIdx.x; d < kRadixMax; d += kSortThreads) counts[d] = 0;
@@ -1109,7 +1111,8 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
         }
     }
     const int64_t base = (int64_t)blockIdx.x * (kSortThreads * ITEMS);
-    unsigned long long my_tiles = 0, my_entries = 0, my_live = 0;
+    unsigned long long my_tiles = 0, my_entries = 0;
+    uint32_t my_live = 0;
     uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
     uint32_t keys[ITEMS];
     bool live[ITEMS];
@@ -1148,43 +1151,53 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
         keys[it] = bits;
         live[it] = has;
     }
+    // the block's totals: wave reductions, then one barrier (which also orders
+    // the zeroing of the histogram before its use)
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        my_tiles += (unsigned long long)__shfl_xor((long long)my_tiles, o, kWave);
+        my_entries += (unsigned long long)__shfl_xor((long long)my_entries, o, kWave);
+        my_live += (uint32_t)__shfl_xor((int)my_live, o, kWave);
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, kWave));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, kWave));
+    }
+    const int wave = threadIdx.x / kWave;
+    if (threadIdx.x % kWave == 0) {
+        wave_sum[0][wave] = my_tiles;
+        wave_sum[1][wave] = my_entries;
+        wave_red[0][wave] = my_live;
+        wave_red[1][wave] = kmin;
+        wave_red[2][wave] = kmax;
+    }
+    __syncthreads();
     if (hist) {
         BucketFn bf;
         bf.kmin = hint_kmin;
         bf.shift = hint_shift;
         bf.on = true;
-        __syncthreads();  // counts zeroed
         // the first depth pass's digit: the bucket's low byte
         block_count_digits<ITEMS>(keys, live, 0, kRadixMaxBits, counts, bf);
+    }
+    if (threadIdx.x == 0) {
+        unsigned long long t = 0, e = 0;
+        uint32_t l = 0, lo = 0xFFFFFFFFu, hi = 0u;
+#pragma unroll
+        for (int w = 0; w < kSortThreads / kWave; ++w) {
+            t += wave_sum[0][w];
+            e += wave_sum[1][w];
+            l += wave_red[0][w];
+            lo = min(lo, wave_red[1][w]);
+            hi = max(hi, wave_red[2][w]);
+        }
+        block_sums[(int64_t)blockIdx.x * 3 + 0] = t;
+        block_sums[(int64_t)blockIdx.x * 3 + 1] = e;
+        block_sums[(int64_t)blockIdx.x * 3 + 2] = l;
+        block_minmax[2 * (int64_t)blockIdx.x] = lo;
+        block_minmax[2 * (int64_t)blockIdx.x + 1] = hi;
+    }
+    if (hist) {
         __syncthreads();
         for (int d = threadIdx.x; d < kRadixMax; d += kSortThreads)
             hist[hist_index(d, blockIdx.x, gridDim.x)] = counts[d];
-    }
-    unsigned long long block_tiles, block_entries, block_live;
-    block_exclusive_scan<unsigned long long, kSortThreads>(my_tiles, sum_tmp, block_tiles);
-    block_exclusive_scan<unsigned long long, kSortThreads>(my_entries, sum_tmp, block_entries);
-    block_exclusive_scan<unsigned long long, kSortThreads>(my_live, sum_tmp, block_live);
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o, kWave));
-        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o, kWave));
-    }
-    if (threadIdx.x % kWave == 0) {
-        mm[0][threadIdx.x / kWave] = kmin;
-        mm[1][threadIdx.x / kWave] = kmax;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        block_sums[(int64_t)blockIdx.x * 3 + 0] = block_tiles;
-        block_sums[(int64_t)blockIdx.x * 3 + 1] = block_entries;
-        block_sums[(int64_t)blockIdx.x * 3 + 2] = block_live;
-        uint32_t lo = 0xFFFFFFFFu, hi = 0u;
-#pragma unroll
-        for (int w = 0; w < kSortThreads / kWave; ++w) {
-            lo = min(lo, mm[0][w]);
-            hi = max(hi, mm[1][w]);
-        }
-        block_minmax[2 * (int64_t)blockIdx.x] = lo;
-        block_minmax[2 * (int64_t)blockIdx.x + 1] = hi;
     }
 }
 

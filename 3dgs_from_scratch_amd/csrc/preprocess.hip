@@ -440,6 +440,13 @@ __global__ __launch_bounds__(kShBlock) void preprocess_forward_kernel(
     for (int c = 0; c < 3; ++c) colors[3 * i + c] = sh_render_value(rgb[c]);
 }
 
+// kRaw: gradients w.r.t. the raw training parameters (log-scales, raw
+// quaternions, opacity logits: the activations' backward included).  !kRaw: the
+// render() inputs -- scales, quaternions as given (log_scales and quats_raw then
+// hold those; logits, grad_opac and grad_logits are unused) -- and the
+// gradients of project_points_backward plus evaluate_sh_render_backward, the
+// means' two terms summed.
+template <bool kRaw>
 __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
     int64_t n, const float *__restrict__ grad_points_image,
     const float *__restrict__ grad_cov_inv, const float *__restrict__ grad_opac,
@@ -464,7 +471,15 @@ __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
     float *lrest = rest_lds + kRest * t;
     if (t < nb) {
         const int64_t i = first + t;
-        const Activated a = activate_one(log_scales, quats_raw, logits, i);
+        Activated a;
+        if constexpr (kRaw) {
+            a = activate_one(log_scales, quats_raw, logits, i);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 3; ++c) a.s[c] = log_scales[3 * i + c];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a.q[c] = quats_raw[4 * i + c];
+        }
         float gp[3] = {0.f, 0.f, 0.f}, gs[3] = {0.f, 0.f, 0.f}, gq[4] = {0.f, 0.f, 0.f, 0.f};
         float gm[3] = {0.f, 0.f, 0.f}, gdc[3] = {0.f, 0.f, 0.f};
         if (mask[i]) {
@@ -490,18 +505,31 @@ __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
 #pragma unroll
             for (int k = 0; k < kRest; ++k) lrest[k] = 0.0f;
         }
-        float g_ls[3], g_logit;
+        float g_ls[3], g_logit = 0.0f;
         float4 g_qr;
-        activate_backward_one(a, gs, make_float4(gq[0], gq[1], gq[2], gq[3]), grad_opac[i], g_ls,
-                              g_qr, g_logit);
+        if constexpr (kRaw) {
+            activate_backward_one(a, gs, make_float4(gq[0], gq[1], gq[2], gq[3]), grad_opac[i],
+                                  g_ls, g_qr, g_logit);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 3; ++c) g_ls[c] = gs[c];
+            g_qr = make_float4(gq[0], gq[1], gq[2], gq[3]);
+        }
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             grad_means[3 * i + c] = gp[c] + gm[c];
             grad_dc[3 * i + c] = gdc[c];
             grad_log_scales[3 * i + c] = g_ls[c];
         }
-        reinterpret_cast<float4 *>(grad_quats_raw)[i] = g_qr;
-        grad_logits[i] = g_logit;
+        if constexpr (kRaw) {
+            reinterpret_cast<float4 *>(grad_quats_raw)[i] = g_qr;
+            grad_logits[i] = g_logit;
+        } else {  // the caller's quaternion gradient need not be 16-byte aligned
+            grad_quats_raw[4 * i] = g_qr.x;
+            grad_quats_raw[4 * i + 1] = g_qr.y;
+            grad_quats_raw[4 * i + 2] = g_qr.z;
+            grad_quats_raw[4 * i + 3] = g_qr.w;
+        }
     }
     __syncthreads();
     block_copy<false>(rest_lds, grad_rest + kRest * first, kRest * nb);
@@ -732,11 +760,33 @@ extern "C" int gs_preprocess_backward(
         (reinterpret_cast<uintptr_t>(quats_raw) & 15) ||
         (reinterpret_cast<uintptr_t>(grad_quats_raw) & 15))
         return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(preprocess_backward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
-                       stream, n, grad_points_image, grad_cov_inv_image, grad_opacities,
-                       grad_colors, means, log_scales, quats_raw, opacity_logits, sh_dc, sh_rest,
+    hipLaunchKernelGGL(preprocess_backward_kernel<true>, dim3(ceil_div(n, kShBlock)),
+                       dim3(kShBlock), 0, stream, n, grad_points_image, grad_cov_inv_image,
+                       grad_opacities, grad_colors, means, log_scales, quats_raw, opacity_logits,
+                       sh_dc, sh_rest, cov_image, mask, world_to_camera, intrinsic, width, height,
+                       grad_means, grad_log_scales, grad_quats_raw, grad_opacity_logits,
+                       grad_sh_dc, grad_sh_rest);
+    return launch_status();
+}
+
+extern "C" int gs_render_preprocess_backward(
+    const float *grad_points_image, const float *grad_cov_inv_image, const float *grad_colors,
+    const float *means, const float *scales, const float *quaternions, const float *sh_dc,
+    const float *sh_rest, const float *cov_image, const uint8_t *mask,
+    const float *world_to_camera, const float *intrinsic, int64_t n, int32_t width,
+    int32_t height, float *grad_means, float *grad_scales, float *grad_quaternions,
+    float *grad_sh_dc, float *grad_sh_rest, hipStream_t stream) {
+    if (n < 0 || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n == 0) return GS_OK;
+    if (!grad_points_image || !grad_cov_inv_image || !grad_colors || !means || !scales ||
+        !quaternions || !sh_dc || !sh_rest || !cov_image || !mask || !world_to_camera ||
+        !intrinsic || !grad_means || !grad_scales || !grad_quaternions || !grad_sh_dc ||
+        !grad_sh_rest)
+        return GS_ERR_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(preprocess_backward_kernel<false>, dim3(ceil_div(n, kShBlock)),
+                       dim3(kShBlock), 0, stream, n, grad_points_image, grad_cov_inv_image,
+                       nullptr, grad_colors, means, scales, quaternions, nullptr, sh_dc, sh_rest,
                        cov_image, mask, world_to_camera, intrinsic, width, height, grad_means,
-                       grad_log_scales, grad_quats_raw, grad_opacity_logits, grad_sh_dc,
-                       grad_sh_rest);
+                       grad_scales, grad_quaternions, nullptr, grad_sh_dc, grad_sh_rest);
     return launch_status();
 }

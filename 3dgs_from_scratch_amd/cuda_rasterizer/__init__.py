@@ -52,6 +52,7 @@ __all__ = [
     "activate_backward",
     "preprocess_forward",
     "preprocess_backward",
+    "render_preprocess_backward",
     "rasterize_display_l1",
     "rasterize_l1_backward",
     "blend_grad_accumulators",
@@ -1046,6 +1047,41 @@ def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, g
             _ptr(quats_raw), _ptr(opacity_logits), _ptr(dc), _ptr(rest), _ptr(cov_image),
             _ptr(mask), _ptr(world_to_camera), _ptr(intrinsic), n, int(width), int(height),
             *[_ptr(t) for t in outs], _stream(dev)), "preprocess_backward")
+        _lib.timer.stop(ev, dev)
+    return tuple(outs)
+
+
+def render_preprocess_backward(grad_points_image, grad_cov_inv_image, grad_colors, means, scales,
+                               quaternions, sh_coeffs_dc, sh_coeffs_rest, cov_image, mask,
+                               world_to_camera, intrinsic, width, height):
+    """project_points_backward and evaluate_sh_render_backward in one kernel
+    (gs_render_preprocess_backward): gradients of render()'s points_image,
+    cov_inv_image and colours w.r.t. (means, scales, quaternions, sh_dc,
+    sh_rest), the means' two terms summed.  Returns those five tensors."""
+    dev = _device_of(means)
+    n = means.shape[0]
+    f32 = torch.float32
+    g_pts = _prep(grad_points_image, "grad_points_image", f32, (n, 2), dev)
+    g_conic = _prep(grad_cov_inv_image, "grad_cov_inv_image", f32, (n, 3), dev)
+    g_col = _prep(grad_colors, "grad_colors", f32, (n, 3), dev)
+    means = _prep(means, "means", f32, (n, 3), dev)
+    scales = _prep(scales, "scales", f32, (n, 3), dev)
+    quaternions = _prep(quaternions, "quaternions", f32, (n, 4), dev)
+    dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
+    rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    cov_image = _prep(cov_image, "cov_image", f32, (n, 3), dev)
+    mask = _prep(mask, "mask", torch.bool, (n,), dev)
+    world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
+    intrinsic = _prep(intrinsic, "intrinsic", f32, (3, 3), dev)
+    outs = [torch.empty(shape, dtype=f32, device=dev)
+            for shape in ((n, 3), (n, 3), (n, 4), (n, 3), (n, 15, 3))]
+    with torch.cuda.device(dev):
+        ev = _lib.timer.record("render_preprocess_backward", dev)
+        _lib.check(_lib.load().gs_render_preprocess_backward(
+            _ptr(g_pts), _ptr(g_conic), _ptr(g_col), _ptr(means), _ptr(scales),
+            _ptr(quaternions), _ptr(dc), _ptr(rest), _ptr(cov_image), _ptr(mask),
+            _ptr(world_to_camera), _ptr(intrinsic), n, int(width), int(height),
+            *[_ptr(t) for t in outs], _stream(dev)), "render_preprocess_backward")
         _lib.timer.stop(ev, dev)
     return tuple(outs)
 

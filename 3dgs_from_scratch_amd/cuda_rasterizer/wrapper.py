@@ -12,9 +12,11 @@ Differences from the reference glue (same values and gradients):
   kernel, so the backward does not recompute each pixel's colour
   (src/cuda/kernel.cu:1032-1060 replays the whole forward pass).
 - render() uses fused kernels for the glue around the seven functions: the
-  camera position, SH and max(c + 0.5, 0) in one kernel (RenderColorsFunction),
-  and the blend writing clamp(image, 0, 1) * 255 itself, with the clamp's
-  gradient applied inside the blend backward (RenderRasterizeFunction).
+  camera position, SH and max(c + 0.5, 0) in one kernel, which with the
+  projection forms one autograd node whose backward is one kernel
+  (RenderPreprocessFunction), and the blend writing clamp(image, 0, 1) * 255
+  itself, with the clamp's gradient applied inside the blend backward
+  (RenderRasterizeFunction).
 - ProjectPointsFunction marks depths, radii and mask non-differentiable, so
   autograd allocates no zero gradients for them.
 """
@@ -81,16 +83,23 @@ class SphericalHarmonicsFunction(torch.autograd.Function):
         return None, g_means, g_dc, g_rest, None, None
 
 
-class RenderColorsFunction(torch.autograd.Function):
-    """Camera position, SH and max(c + 0.5, 0) of render() (src/cuda/wrapper.py:260-265)
-    as one kernel each way."""
+class RenderPreprocessFunction(torch.autograd.Function):
+    """ProjectPointsFunction and the render() colours (camera position, SH and
+    max(c + 0.5, 0); src/cuda/wrapper.py:223-265) as one autograd node: the
+    forward runs project_points and the colour kernel (on the calling thread's
+    second stream, beside binning, when `beside` is a list: it receives the
+    fused.ColorsBeside to wait on), the backward one kernel for both
+    (render_preprocess_backward), so the means' two gradient terms are summed in
+    it rather than by autograd."""
 
     @staticmethod
-    def forward(ctx, world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask, beside=None):
+    def forward(ctx, means, scales, quaternions, opacities, world_to_camera, intrinsic,
+                sh_coeffs_dc, sh_coeffs_rest, near_plane, far_plane, min_opacity, min_radius,
+                max_radius, width, height, beside=None):
+        points_img, depths, cov_img, cov_inv_img, radii, mask = _cr.project_points(
+            means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
+            far_plane, min_opacity, min_radius, max_radius, width, height)
         if beside is not None:
-            # on the calling thread's second stream, beside binning: `beside` (a
-            # list) receives the fused.ColorsBeside whose wait() the caller queues
-            # before it reads the colours (the backward stays on the current stream)
             from cuda_rasterizer.fused import colors_beside
 
             pending = colors_beside(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask)
@@ -99,31 +108,31 @@ class RenderColorsFunction(torch.autograd.Function):
         else:
             colors = _cr.evaluate_spherical_harmonics_render(world_to_camera, means,
                                                              sh_coeffs_dc, sh_coeffs_rest, mask)
-        ctx.save_for_backward(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask)
-        return colors
+        ctx.save_for_backward(means, scales, quaternions, world_to_camera, intrinsic,
+                              sh_coeffs_dc, sh_coeffs_rest, cov_img, mask)
+        ctx.width = width
+        ctx.height = height
+        ctx.mark_non_differentiable(depths, radii, mask)
+        ctx.set_materialize_grads(False)
+        return points_img, depths, cov_inv_img, radii, mask, colors
 
     @staticmethod
-    def backward(ctx, grad_colors):
-        world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask = ctx.saved_tensors
-        g_means, g_dc, g_rest = _cr.evaluate_spherical_harmonics_render_backward(
-            grad_colors, world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask)
-        return None, g_means, g_dc, g_rest, None, None
+    def backward(ctx, grad_points_img, grad_depths, grad_cov_inv_img, grad_radii, grad_mask,
+                 grad_colors):
+        means, scales, quaternions, w2c, K, dc, rest, cov_img, mask = ctx.saved_tensors
+        if grad_points_img is None and grad_cov_inv_img is None and grad_colors is None:
+            return (None,) * 16
+        n = means.shape[0]
 
+        def zeros(w):
+            return torch.zeros((n, w), dtype=means.dtype, device=means.device)
 
-def _render_colors(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask):
-    """render()'s colours and the fused.ColorsBeside to wait on before reading
-    them (None: computed on the current stream).  In a training step (grad
-    enabled) with at least BESIDE_MIN_GAUSSIANS Gaussians they are computed on
-    the calling thread's second stream while binning runs (config 3 loop 0.988
-    -> 0.969 ms); a forward-only render keeps them on the current stream (config
-    4, 3M Gaussians: 0.70 ms against 0.72 beside binning), as do small scenes
-    (the fork and join cost more than they save)."""
-    from cuda_rasterizer.fused import BESIDE_MIN_GAUSSIANS
-
-    sink = [] if torch.is_grad_enabled() and means.shape[0] >= BESIDE_MIN_GAUSSIANS else None
-    colors = RenderColorsFunction.apply(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest,
-                                        mask, sink)
-    return colors, (sink[0] if sink else None)
+        g_means, g_scales, g_quats, g_dc, g_rest = _cr.render_preprocess_backward(
+            zeros(2) if grad_points_img is None else grad_points_img,
+            zeros(3) if grad_cov_inv_img is None else grad_cov_inv_img,
+            zeros(3) if grad_colors is None else grad_colors, means, scales, quaternions, dc,
+            rest, cov_img, mask, w2c, K, ctx.width, ctx.height)
+        return (g_means, g_scales, g_quats, None, None, None, g_dc, g_rest) + (None,) * 8
 
 
 class RenderRasterizeFunction(torch.autograd.Function):
@@ -207,18 +216,23 @@ def render(
     sh_sigmoid=False,
 ):
     """src/cuda/wrapper.py:223-294.  Returns (image*255 clamped, points_img, radii)."""
-    points_img, depths, cov_inv_img, radii, mask = ProjectPointsFunction.apply(
-        means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
-        far_plane, min_opacity, min_radius, max_radius, width, height)
-
     if sh_sigmoid:
+        points_img, depths, cov_inv_img, radii, mask = ProjectPointsFunction.apply(
+            means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
+            far_plane, min_opacity, min_radius, max_radius, width, height)
         camera_pos = -world_to_camera[:3, :3].t() @ world_to_camera[:3, 3]
         colors = SphericalHarmonicsFunction.apply(camera_pos, means, sh_coeffs_dc,
                                                   sh_coeffs_rest, mask, True)
         colors_ready = None
-    else:  # max(sh + 0.5, 0), fused (beside binning in a training step)
-        colors, colors_ready = _render_colors(world_to_camera, means, sh_coeffs_dc,
-                                              sh_coeffs_rest, mask)
+    else:  # projection and max(sh + 0.5, 0) as one node (colours beside binning in training)
+        from cuda_rasterizer.fused import BESIDE_MIN_GAUSSIANS
+
+        sink = [] if torch.is_grad_enabled() and means.shape[0] >= BESIDE_MIN_GAUSSIANS else None
+        points_img, depths, cov_inv_img, radii, mask, colors = RenderPreprocessFunction.apply(
+            means, scales, quaternions, opacities, world_to_camera, intrinsic, sh_coeffs_dc,
+            sh_coeffs_rest, near_plane, far_plane, min_opacity, min_radius, max_radius, width,
+            height, sink)
+        colors_ready = sink[0] if sink else None
 
     tile_size = 16
     check = None

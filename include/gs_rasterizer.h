@@ -376,6 +376,29 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
                            hipStream_t stream);
 
 /*
+ * The drop-in render()'s backward of projection and colours in one pass:
+ * gs_project_points_backward (src/cuda/rasterizer.cpp:193-232) and
+ * gs_evaluate_sh_render_backward (the colour max(SH + 0.5, 0) of
+ * src/cuda/wrapper.py:260-265, backward of rasterizer.cpp:259-290), with
+ * grad_means the sum of the two means gradients.  Inputs as those entries take
+ * them: scales and quaternions as rendered (no activation), cov_image and mask
+ * from gs_project_points, sh_rest (N, 15, 3).  Each output equals the
+ * corresponding output of the two entries (the means: their sum).  No
+ * counterpart in the reference extension, whose wrapper runs the two
+ * backwards as separate autograd nodes.
+ */
+int gs_render_preprocess_backward(const float *grad_points_image,
+                                  const float *grad_cov_inv_image, const float *grad_colors,
+                                  const float *means, const float *scales,
+                                  const float *quaternions, const float *sh_dc,
+                                  const float *sh_rest, const float *cov_image,
+                                  const uint8_t *mask, const float *world_to_camera,
+                                  const float *intrinsic, int64_t n, int32_t width,
+                                  int32_t height, float *grad_means, float *grad_scales,
+                                  float *grad_quaternions, float *grad_sh_dc, float *grad_sh_rest,
+                                  hipStream_t stream);
+
+/*
  * The caller-side glue of a training step (scripts/train.py:135-143,187-191),
  * fused: no counterpart in the reference extension.
  *

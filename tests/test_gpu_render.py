@@ -275,3 +275,45 @@ def test_colours_beside_binning_with_non_contiguous_inputs(gpu, monkeypatch):
     loss, _, _, _ = render_l1(w2c_t, K, W, H, v["means"], v["log_scales"], v["quats_raw"],
                               v["opacity_logits"], v["sh_dc"], v["sh_rest"], tgt)
     assert float(loss) == float(loss_ref)
+
+
+def test_render_preprocess_backward_equals_the_two_entries(gpu):
+    """gs_render_preprocess_backward (render()'s projection + colour node backward,
+    one kernel) equals project_points_backward and
+    evaluate_spherical_harmonics_render_backward bit for bit, the means gradient
+    being their sum (as autograd adds the two nodes' gradients)."""
+    import cuda_rasterizer as cr
+
+    n = 9_000
+    p, cam, _ = helpers.scene_orbit(n, 200, 150, 260.0, seed=17, log_scale=(-3.5, 0.5))
+    scales, quats, opac = helpers.activated(p)
+    g = torch.Generator().manual_seed(23)
+    d = lambda t: t.to(gpu)  # noqa: E731
+    w2c, K = d(cam["w2c"]), d(cam["K"])
+    means, scales, quats, opac = d(p["means"]), d(scales), d(quats), d(opac)
+    dc = d(torch.randn(n, 3, generator=g) * 0.8)  # some colours clamped at 0
+    rest = d(p["sh_rest"])
+    pts, depths, cov, conic, radii, mask = cr.project_points(means, scales, quats, opac, w2c, K,
+                                                             0.01, 100.0, 1 / 255, 0.5, 128.0,
+                                                             200, 150)
+    assert 0 < int(mask.sum()) < n
+    gp = d(torch.randn(n, 2, generator=g))
+    gc = d(torch.randn(n, 3, generator=g))
+    gcol = d(torch.randn(n, 3, generator=g))
+    fm, fs, fq, fdc, frest = cr.render_preprocess_backward(gp, gc, gcol, means, scales, quats, dc,
+                                                            rest, cov, mask, w2c, K, 200, 150)
+    pm, ps, pq = cr.project_points_backward(gp, gc, means, scales, quats, opac, w2c, K, 200, 150,
+                                            cov, mask)
+    sm, sdc, srest = cr.evaluate_spherical_harmonics_render_backward(gcol, w2c, means, dc, rest,
+                                                                     mask)
+    assert torch.equal(fm, pm + sm)
+    assert torch.equal(fs, ps) and torch.equal(fq, pq)
+    assert torch.equal(fdc, sdc) and torch.equal(frest, srest)
+    # a quaternion view that is not 16-byte aligned (the entry takes any row start)
+    wide = torch.zeros(n * 4 + 1, device=gpu)
+    wide[1:] = quats.flatten()
+    quats_odd = wide[1:].view(n, 4)
+    assert quats_odd.data_ptr() % 16 != 0
+    om, os_, oq, odc, orest = cr.render_preprocess_backward(gp, gc, gcol, means, scales, quats_odd,
+                                                            dc, rest, cov, mask, w2c, K, 200, 150)
+    assert torch.equal(oq, fq) and torch.equal(om, fm)
