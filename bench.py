@@ -220,6 +220,32 @@ def fused_step(leaves: dict, cam: dict, target: torch.Tensor, ssim_lambda: float
     return loss, image
 
 
+def device_time(step, steps: int):
+    """Kernel time per step in ms over `steps` calls of `step`, summed over every
+    stream (the fused step's colours run beside binning on a second stream), from
+    torch.profiler's device activity; None when the profiler reports none."""
+    try:
+        from torch.profiler import ProfilerActivity, profile
+
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+        total_us = sum(e.self_device_time_total for e in prof.key_averages())
+    except Exception:  # noqa: BLE001 -- the profiler is optional here
+        return None
+    return total_us / steps / 1e3 if total_us > 0 else None
+
+
+def busy(device_ms, wall_ms: float):
+    """{"device_ms", "busy"}: kernel time per step and its share of the wall time
+    per step (above 1 where streams overlap); None without a device time."""
+    if device_ms is None:
+        return None
+    return {"device_ms": round(device_ms, 4), "busy": round(device_ms / wall_ms, 3)}
+
+
 def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
             schedule_cache: bool = False) -> dict:
     """Times `steps` steps after `warmup`; path "fused" (fused_step) or "drop-in"
@@ -267,6 +293,7 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
         step()
     _lib.timer.enabled = False
     stages = _lib.timer.summary()
+    device_ms = device_time(step, steps)
 
     # workload statistics of one step
     from cuda_rasterizer import compute_tile_intersection, project_points, rasterize_work
@@ -282,7 +309,8 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
                 main_stages={k: (c, t / steps) for k, (c, t) in main_stages.items()}, steps=steps,
                 n=scene["params"]["means"].shape[0], n_visible=int(mask.sum()), keys=int(ids.numel()),
                 n_tiles=int(off.numel()), visited=visited, composited=composited,
-                loss=float(loss.detach()), width=cam["width"], height=cam["height"])
+                loss=float(loss.detach()), width=cam["width"], height=cam["height"],
+                device_busy=busy(device_ms, ms))
 
 
 def run_full_loss(scene: dict, steps: int, warmup: int, ssim_lambda: float = 0.2) -> dict:
@@ -395,7 +423,8 @@ def run_cameras(scene: dict, steps: int, warmup: int) -> dict:
     ms = (time.perf_counter() - t0) * 1e3 / steps
     n = scene["params"]["means"].shape[0]
     return {"ms_per_step": round(ms, 4), "cameras": len(cams),
-            "gaussians_per_s": round(n / (ms * 1e-3), 1), "loss": round(float(loss), 6)}
+            "gaussians_per_s": round(n / (ms * 1e-3), 1), "loss": round(float(loss), 6),
+            "device_busy": busy(device_time(step, steps), ms)}
 
 
 def run_small_configs(steps: int, warmup: int, cpu: bool) -> dict:
@@ -407,7 +436,8 @@ def run_small_configs(steps: int, warmup: int, cpu: bool) -> dict:
     r = run_gpu(s1, steps, warmup, "fused")
     out["config1"] = {"workload": f"{r['n']} Gaussians SH0 {r['width']}x{r['height']} fwd+bwd L1",
                       "ms_per_step": round(r["ms"], 4), "keys": r["keys"],
-                      "gaussians_per_s": round(r["n"] / (r["ms"] * 1e-3), 1)}
+                      "gaussians_per_s": round(r["n"] / (r["ms"] * 1e-3), 1),
+                      "device_busy": r["device_busy"]}
     s2 = config2()
     c2 = run_cameras(s2, steps, warmup)
     out["config2"] = dict(workload=f"{s2['params']['means'].shape[0]} Gaussians SH3 800x800 "
@@ -536,11 +566,9 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
         sched = torch.optim.lr_scheduler.ExponentialLR(optims["means"], gamma=0.01 ** (1 / steps))
         grads = torch.zeros(leaves["means"].shape[0], device=dev)
     losses, sizes = [], []
-    torch.cuda.synchronize()
-    torch.cuda.reset_peak_memory_stats(dev)
-    base = torch.cuda.memory_allocated(dev)
-    t0 = time.perf_counter()
-    for step in range(steps):
+    state = {"grads": None if path == "fused" else grads}
+
+    def one_step(step, densify=True):
         target = targets[step % targets.shape[0]]
         if path == "fused":
             loss, _, _, _ = render_l1(w2c_all[step], K, W, H, leaves["means"], leaves["log_scales"],
@@ -550,10 +578,11 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
             loss.backward()
             opt.step()
             opt.zero_grad()
-            if (step + 1) % every == 0:
+            if densify and (step + 1) % every == 0:
                 dens.clone_top_and_prune(leaves, opt, fraction, jitter, generator=gen)
                 sizes.append(leaves["means"].shape[0])
         else:
+            grads = state["grads"]
             scales, quats, opac = activated(leaves)
             image, pts, radii = render(w2c_all[step], K, W, H, leaves["means"], scales, quats,
                                        opac, leaves["sh_dc"], leaves["sh_rest"],
@@ -571,21 +600,41 @@ def run_train(scene: dict, path: str = "fused", steps: int | None = None, every:
                 o.step()
                 o.zero_grad(set_to_none=True)
             sched.step()
-            if (step + 1) % every == 0:
+            if densify and (step + 1) % every == 0:
                 with torch.no_grad():
                     _torch_clone_top_and_prune(leaves, optims, grads, fraction, jitter,
                                                generator=gen)
-                grads = torch.zeros(leaves["means"].shape[0], device=dev)
+                state["grads"] = torch.zeros(leaves["means"].shape[0], device=dev)
                 sizes.append(leaves["means"].shape[0])
+        return loss
+
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    t0 = time.perf_counter()
+    for step in range(steps):
+        loss = one_step(step)
         if step % 100 == 0 or step == steps - 1:
             losses.append(loss.detach())
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     peak = torch.cuda.max_memory_allocated(dev)
+    # device busy over a window of steps at the final size (no densification):
+    # wall clock, then the same steps under the profiler
+    window = 20
+    cams = iter(range(window * 2))
+    t2 = time.perf_counter()
+    for _ in range(window):
+        one_step(next(cams) % steps, densify=False)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t2) * 1e3 / window
+    dev_ms = device_time(lambda: one_step(next(cams) % steps, densify=False), window)
     return dict(ms=(t1 - t0) * 1e3 / steps, steps=steps, peak_hbm_bytes=int(peak),
                 peak_hbm_above_inputs_bytes=int(peak - base), n_start=scene["params"]["means"].shape[0],
                 n_end=leaves["means"].shape[0], sizes=sizes,
-                loss_first=float(losses[0]), loss_last=float(losses[-1]), width=W, height=H)
+                loss_first=float(losses[0]), loss_last=float(losses[-1]), width=W, height=H,
+                device_busy=dict(busy(dev_ms, wall) or {}, window_ms_per_step=round(wall, 4),
+                                 window=f"{window} steps at the final size, no densification"))
 
 
 def train_stress(steps: int = 2000, which: str = "both") -> dict:
@@ -600,7 +649,7 @@ def train_stress(steps: int = 2000, which: str = "both") -> dict:
         r = run_train(scene, path)
         out[path] = {"ms_per_step": round(r["ms"], 4), "peak_hbm_gib": round(r["peak_hbm_bytes"] / 2**30, 3),
                      "n_end": r["n_end"], "sizes": r["sizes"], "loss_first": round(r["loss_first"], 5),
-                     "loss_last": round(r["loss_last"], 5)}
+                     "loss_last": round(r["loss_last"], 5), "device_busy": r["device_busy"]}
     return out
 
 
@@ -1004,6 +1053,7 @@ def main(argv=None):
     if args.path == "fused" and not args.no_drop_in:
         d = run_gpu(scene, args.steps, args.warmup, "drop-in")
         drop_in = {"ms_per_step": round(d["ms"], 3), "loss": d["loss"],
+                   "device_busy": d["device_busy"],
                    "stages": roofline(d, scene["name"])["per_stage"]}
     view_cache = None
     if args.path == "fused":
@@ -1044,6 +1094,7 @@ def main(argv=None):
                    "path": args.path, "gaussians": res["n"], "visible": res["n_visible"],
                    "keys": res["keys"], "resolution": [res["width"], res["height"]]},
         "gaussians_per_s": round(res["n"] / (res["ms"] * 1e-3), 1),
+        "device_busy": res["device_busy"],
         "roofline": rl["roofline"],
         "step_roofline": step_roofline(res, scene["name"]) if args.path == "fused" else None,
         "hbm_stages": rl["hbm_stages"],
