@@ -24,6 +24,7 @@ Behavioural notes relative to the reference:
 from __future__ import annotations
 
 import ctypes
+import threading
 import time
 
 import torch
@@ -41,6 +42,8 @@ __all__ = [
     "compute_tile_intersection_debug",
     "compute_tile_intersection_ordered",
     "tile_intersection_capped",
+    "CappedCheck",
+    "CapturedChecks",
     "rasterize",
     "rasterize_backward",
     "rasterize_work",
@@ -322,6 +325,10 @@ def _tile_intersection(points_image, radii, depths, mask, width, height, tile_si
     if tile_size <= 0 or width <= 0 or height <= 0:
         raise RuntimeError("compute_tile_intersection: width, height and tile_size must be > 0")
     n_tiles = ((width + tile_size - 1) // tile_size) * ((height + tile_size - 1) // tile_size)
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("compute_tile_intersection: the list sizes are read on the host, "
+                           "which a graph capture cannot wait for (render through "
+                           "render_l1 or render(), whose capped sort needs no host read)")
     lib = _lib.load()
     with torch.cuda.device(dev):
         stream = _stream(dev)
@@ -431,13 +438,40 @@ def _set_capacity(key, k: int, m: int) -> None:
     _CAPACITY[key] = (k + k // 4 + 4096, m + m // 4 + 1024)
 
 
+# Checks of capped sorts queued while the calling thread captures a HIP graph:
+# CapturedChecks collects them so that the graph's owner can test every replay.
+_CAPTURE = threading.local()
+
+
+class CapturedChecks:
+    """Context manager that collects the capped-sort checks queued by the calling
+    thread inside it (while it captures a graph): `.checks` afterwards."""
+
+    def __init__(self):
+        self.checks = []
+
+    def __enter__(self):
+        self._outer = getattr(_CAPTURE, "sink", None)
+        _CAPTURE.sink = self.checks
+        return self
+
+    def __exit__(self, *exc):
+        _CAPTURE.sink = self._outer
+        return False
+
+
 class CappedCheck:
     """The pending check of a capped sort (tile_intersection_capped): ok() waits
     for the count's totals (K, M and the depth key range), which the GPU has
     usually written long before, records them for the next call's depth hint
     and capacities, and returns whether the lists fit the capacities -- if not,
     no list was written and the caller bins again with exact sizes.  The pinned
-    totals are released only after that wait."""
+    totals are released only after that wait.
+
+    A check queued during a graph capture (no `ready` event; the totals in
+    device memory of the graph's pool) cannot wait: ok() returns True and hands
+    the check to the enclosing CapturedChecks, and replayed_ok() tells, once a
+    replay has completed, whether that replay's lists fit."""
 
     __slots__ = ("_ready", "_host", "_dev_totals", "_caps", "_key", "_result")
 
@@ -445,16 +479,36 @@ class CappedCheck:
         self._ready, self._host, self._dev_totals = ready, host_totals, dev_totals
         self._caps, self._key, self._result = caps, key, None
 
+    @property
+    def captured(self) -> bool:
+        return self._ready is None
+
     def ok(self) -> bool:
+        if self.captured:
+            sink = getattr(_CAPTURE, "sink", None)
+            if sink is not None and not any(c is self for c in sink):
+                sink.append(self)
+            return True
         if self._result is None:
             _wait(self._ready)
             src = self._host if self._dev_totals is None else self._dev_totals.cpu()
-            k, m, kmin, kmax = (int(v) for v in src.tolist())
-            _DEPTH_RANGE[self._key[0]] = (kmin, kmax)
-            _set_capacity(self._key, k, m)
-            self._result = k <= self._caps[0] and m <= self._caps[1]
+            self._result = self._record(src)
             self._host = self._dev_totals = None
         return self._result
+
+    def _record(self, src) -> bool:
+        k, m, kmin, kmax = (int(v) for v in src.tolist())
+        _DEPTH_RANGE[self._key[0]] = (kmin, kmax)
+        _set_capacity(self._key, k, m)
+        return k <= self._caps[0] and m <= self._caps[1]
+
+    def replayed_ok(self) -> bool:
+        """A captured check, after a replay of its graph has completed (the caller
+        synchronised): whether that replay's lists fit the capacities fixed at
+        capture.  Also records the replay's totals for later eager calls."""
+        if not self.captured:
+            raise RuntimeError("replayed_ok: the check was not queued during a graph capture")
+        return self._record(self._dev_totals.cpu())
 
     def __del__(self):
         if self._result is None and self._ready is not None:
@@ -485,7 +539,15 @@ def tile_intersection_capped(points_image, radii, depths, mask, width, height, t
     n_super = ((tiles_x + 7) // 8) * ((tiles_y + 7) // 8)
     key = (dev.index, width, height, tile_size)
     caps = _CAPACITY.get(key)
+    capturing = torch.cuda.is_current_stream_capturing()
     if not CAPPED_BINNING or caps is None or n == 0 or n_super > 256 or n_tiles > 16384:
+        if capturing:  # the exact sizes need a host read, which a capture cannot wait for
+            raise RuntimeError(
+                "compute_tile_intersection: a graph capture needs the capped sort: render "
+                "once at this resolution before capturing (the capacities come from that "
+                f"call), with at least one visible Gaussian and at most 16384 tiles "
+                f"(n={n}, {n_tiles} tiles, capacities {'set' if caps else 'unset'}, "
+                f"CAPPED_BINNING={CAPPED_BINNING})")
         off, ids, order = _tile_intersection(points_image, radii, depths, mask, width, height,
                                              tile_size, False, ordered=True)
         return off, ids, order, None
@@ -507,10 +569,15 @@ def tile_intersection_capped(points_image, radii, depths, mask, width, height, t
         indexing_offset = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
         order = torch.empty((n_tiles,), dtype=torch.int32, device=dev)
         ids = torch.empty((k_cap,), dtype=torch.int32, device=dev)
-        host_totals = torch.empty((4,), dtype=torch.int64, pin_memory=True)
-        totals_ptr = _pinned_device_pointer(host_totals)
-        dev_totals = None
-        if totals_ptr is None:  # device memory, read with a copy in check.ok()
+        # the totals go to mapped pinned memory, or (when it is not mapped, and in a
+        # graph capture, where the graph's pool holds them for every replay) to
+        # device memory read with a copy
+        host_totals = dev_totals = totals_ptr = None
+        if not capturing:
+            host_totals = torch.empty((4,), dtype=torch.int64, pin_memory=True)
+            totals_ptr = _pinned_device_pointer(host_totals)
+        if totals_ptr is None:
+            host_totals = None
             dev_totals = torch.empty((4,), dtype=torch.int64, device=dev)
             totals_ptr = _ptr(dev_totals)
         args = (_ptr(points_image), _ptr(radii), _ptr(depths), _ptr(mask), n, width, height,
@@ -523,8 +590,9 @@ def tile_intersection_capped(points_image, radii, depths, mask, width, height, t
             _lib.check(lib.gs_bin_count_begin_hinted(*args[:10], hint_kmin, hint_shift,
                                                      *args[10:]),
                        "compute_tile_intersection (count)")
-            ready = torch.cuda.Event()
-            ready.record(torch.cuda.current_stream(dev))
+            if not capturing:
+                ready = torch.cuda.Event()
+                ready.record(torch.cuda.current_stream(dev))
             check = CappedCheck(ready, host_totals, dev_totals, caps, key)
             _lib.check(lib.gs_bin_count_finish(*args), "compute_tile_intersection (count)")
             _lib.timer.stop(ev, dev)
@@ -536,7 +604,9 @@ def tile_intersection_capped(points_image, radii, depths, mask, width, height, t
             _lib.timer.stop(ev, dev)
         except BaseException:
             # the device may still write the pinned totals: wait before releasing them
-            if check is not None:
+            if capturing:
+                pass  # nothing ran yet; the capture itself is invalid now
+            elif check is not None:
                 check.ok()
             else:
                 torch.cuda.current_stream(dev).synchronize()
@@ -675,7 +745,8 @@ def check_forward_order(order, n_tiles):
 def _check_order(order, schedule, n_tiles, dev, who):
     """A forward launch order: n_tiles int32 on the device, not inside `schedule`
     (a permutation of every XCD range, see check_forward_order; verified only
-    with CHECK_FORWARD_ORDERS)."""
+    with CHECK_FORWARD_ORDERS, and not during a graph capture, which cannot read
+    it on the host)."""
     if order is None:
         return
     if (not isinstance(order, torch.Tensor) or order.dtype != torch.int32
@@ -686,7 +757,7 @@ def _check_order(order, schedule, n_tiles, dev, who):
             schedule.data_ptr() <= order.data_ptr() < schedule.data_ptr() + schedule.numel() * 4):
         raise RasterizerError(f"{who}: forward_order must not lie in the schedule this call "
                               "writes")
-    if CHECK_FORWARD_ORDERS:
+    if CHECK_FORWARD_ORDERS and not torch.cuda.is_current_stream_capturing():
         check_forward_order(order, n_tiles)
 
 
@@ -1121,7 +1192,7 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
             raise RasterizerError("rasterize_display_l1: forward_schedule must be an earlier "
                                   "call's schedule, not the one this call writes")
         fwd_order = forward_schedule[n_tiles:]
-        if CHECK_FORWARD_ORDERS:
+        if CHECK_FORWARD_ORDERS and not torch.cuda.is_current_stream_capturing():
             check_forward_order(fwd_order, n_tiles)
     if forward_order is not None:
         if forward_schedule is not None:

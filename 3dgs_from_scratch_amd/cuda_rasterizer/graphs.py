@@ -1,0 +1,75 @@
+"""Training steps captured into HIP graphs.
+
+A step of a small scene is bound by the host: each of its ~30 library and
+PyTorch launches costs a few microseconds of Python, ctypes and HIP runtime
+time, more than the GPU spends on many of them.  CapturedStep records a step
+(any callable that renders through `render_l1` or the drop-in `render()` and
+calls backward, e.g. the body of scripts/train.py:133-227's loop without the
+optimizer's host logic) into one HIP graph (torch.cuda.CUDAGraph) and replays it
+with one launch.
+
+What the capture fixes, and what each replay must therefore keep:
+  * tensor addresses: the inputs the step reads (parameters, camera, target)
+    are the same tensors on every replay -- update them in place (copy_), and
+    read outputs (loss, .grad) from the tensors the capture produced;
+  * list capacities: the tile lists are sized by the capacities of the capped
+    sort, taken from the warm-up calls.  A replay whose lists would outgrow them
+    writes no list entries (its image and gradients are then incomplete) and is
+    reported by ok(); run the step eagerly once (it rebins with exact sizes and
+    raises the capacities) and recapture();
+  * the depth hint of the sort (any hint gives the same lists; a stale one only
+    slows the sort).
+No library launch in the step uses hipMemsetAsync (buffers are cleared by
+kernels), and none waits on the host once the capacities are set.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import cuda_rasterizer as _cr
+
+
+class CapturedStep:
+    """`fn()` captured into a HIP graph on the current device after `warmup`
+    eager calls (on a side stream, as torch.cuda.graphs requires; they also set
+    the capacities).  replay() relaunches it on the current stream; `output` is
+    what the captured call returned (its tensors are rewritten by every replay).
+    ok() synchronises and returns whether every capped sort of the last replay
+    fit its capacities."""
+
+    def __init__(self, fn, warmup: int = 2):
+        if warmup < 1:
+            raise ValueError("CapturedStep: at least one warm-up call sets the capacities")
+        self._fn = fn
+        self.graph = None
+        self.output = None
+        self.checks: list = []
+        self.capture(warmup)
+
+    def capture(self, warmup: int = 1) -> None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+        main = torch.cuda.current_stream(dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self._fn()
+        main.wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = None  # release the previous graph's pool before capturing again
+        self.output = None
+        graph = torch.cuda.CUDAGraph()
+        with _cr.CapturedChecks() as sink:
+            with torch.cuda.graph(graph):
+                out = self._fn()
+        self.graph, self.output, self.checks = graph, out, sink.checks
+
+    recapture = capture
+
+    def replay(self) -> None:
+        self.graph.replay()
+
+    def ok(self) -> bool:
+        torch.cuda.current_stream().synchronize()
+        return all(c.replayed_ok() for c in self.checks)

@@ -424,7 +424,35 @@ def run_cameras(scene: dict, steps: int, warmup: int) -> dict:
     n = scene["params"]["means"].shape[0]
     return {"ms_per_step": round(ms, 4), "cameras": len(cams),
             "gaussians_per_s": round(n / (ms * 1e-3), 1), "loss": round(float(loss), 6),
-            "device_busy": busy(device_time(step, steps), ms)}
+            "device_busy": busy(device_time(step, steps), ms),
+            "graph": run_graph(step, steps, warmup, float(loss))}
+
+
+def run_graph(step, steps: int, warmup: int, eager_loss: float) -> dict:
+    """The same step captured into a HIP graph (cuda_rasterizer.graphs.CapturedStep)
+    and replayed: wall clock over `steps` replays after `warmup`, synchronised on
+    both sides; every capped sort of the last replay is checked against its
+    capacities afterwards, and its loss against the eager step's (the parameters
+    do not change between steps, so the two agree up to float summation order)."""
+    from cuda_rasterizer.graphs import CapturedStep
+
+    captured = CapturedStep(step, warmup=max(warmup, 1))
+    for _ in range(warmup):
+        captured.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        captured.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    if not captured.ok():
+        raise RuntimeError("bench: a replay's tile lists outgrew the captured capacities")
+    out = captured.output
+    loss = float((out[0] if isinstance(out, tuple) else out).detach())
+    if abs(loss - eager_loss) > 1e-5 * abs(eager_loss):
+        raise RuntimeError(f"bench: graph replay loss {loss} != eager loss {eager_loss}")
+    return {"ms_per_step": round(ms, 4), "loss": round(loss, 6),
+            "device_busy": busy(device_time(captured.replay, steps), ms)}
 
 
 def run_small_configs(steps: int, warmup: int, cpu: bool) -> dict:
@@ -434,10 +462,16 @@ def run_small_configs(steps: int, warmup: int, cpu: bool) -> dict:
     out = {}
     s1 = config1()
     r = run_gpu(s1, steps, warmup, "fused")
+    dev = torch.device("cuda:0")
+    leaves = {k: v.to(dev).requires_grad_(True) for k, v in s1["params"].items()}
+    cam = dict(s1["camera"], w2c=s1["camera"]["w2c"].to(dev), K=s1["camera"]["K"].to(dev))
+    target = s1["target"].to(dev)
     out["config1"] = {"workload": f"{r['n']} Gaussians SH0 {r['width']}x{r['height']} fwd+bwd L1",
                       "ms_per_step": round(r["ms"], 4), "keys": r["keys"],
                       "gaussians_per_s": round(r["n"] / (r["ms"] * 1e-3), 1),
-                      "device_busy": r["device_busy"]}
+                      "device_busy": r["device_busy"],
+                      "graph": run_graph(lambda: fused_step(leaves, cam, target), steps, warmup,
+                                         r["loss"])}
     s2 = config2()
     c2 = run_cameras(s2, steps, warmup)
     out["config2"] = dict(workload=f"{s2['params']['means'].shape[0]} Gaussians SH3 800x800 "
