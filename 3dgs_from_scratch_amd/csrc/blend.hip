@@ -69,6 +69,72 @@ __device__ __forceinline__ TileSpan tile_span(const int32_t *__restrict__ offset
     return s;
 }
 
+// Checkpoints of the forward walk, which let the backward walk a long tile list
+// in up to kCheckpoints + 1 segments on as many workgroups.  Every
+// checkpoint_spacing<W>() batches (at most kCheckpoints times) the forward
+// saves each pixel's transmittance and accumulated colour before the batch at
+// list position pos, where the next segment starts.  A segment's backward walk
+// starts from that state: T from the checkpoint and the running colour-gradient
+// sum from the accumulated colour (sum_{k<pos} w_k (g.c_k) = g . C_prefix), so
+// the segments together make the same front-to-back walk (up to the rounding of
+// that one dot product and of the backward's own alpha).  They live in the
+// schedule buffer after the per-tile work and launch order (schedule_layout).
+constexpr int kCheckpoints = 3;
+constexpr int kSegments = kCheckpoints + 1;
+// Grids of more tiles keep more workgroups waiting than the GPU holds at once,
+// and the dispatcher's start of each as a slot frees already balances the
+// walks: there the forward saves no checkpoints (its stores cost more than the
+// segments gain: 1M Gaussians at 1920x1080, 8160 tiles, forward 138 -> 153 us,
+// backward unchanged) and the schedule is 2 n_tiles int32 (work, order).
+// Measured in one process against one workgroup per tile: 200k Gaussians at
+// 1280x720 (3600 tiles) backward 227 -> 150 us, 100k at 800x800 (2500 tiles)
+// 192 -> 147 us, 10k at 256x256 (256 tiles, 4 waves each) 92 -> 74 us.
+constexpr int kCheckpointMaxTiles = 6144;
+constexpr int kTilePixels = 256;  // 16 x 16
+
+template <int W>
+__device__ __forceinline__ constexpr int checkpoint_spacing() {
+    return W == 1 ? 2 : 1;  // batches of W * kBatch records: 128 records with one wave
+}
+
+struct Checkpoints {
+    float *data;      // [n_tiles * kCheckpoints][4][kTilePixels]: T, r, g, b planes
+    int32_t *pos;     // [n_tiles * kCheckpoints] list position where segment i + 1 starts
+    uint32_t *work;   // [n_tiles * kCheckpoints] the walk's work units before checkpoint i
+    int32_t *count;   // [n_tiles] checkpoints saved by the forward
+    int32_t *items;   // [4 n_tiles] per XCD range (at 4 * its first tile): the backward's
+                      // segments tile * kSegments + segment, by descending work
+    int32_t *n_items; // [kXcds] segments listed per range
+};
+
+// Schedule buffer (int32 elements): [0, n) work per tile, [n, 2n) the backward's
+// launch order, [2n, 3n) checkpoint counts, [3n, 6n) checkpoint positions,
+// [6n, 9n) work before each checkpoint, [9n, 13n) segment lists, [13n, 13n + 8)
+// their lengths, then (16-byte aligned) the checkpoint pixels.
+__host__ __device__ inline size_t schedule_head_elems(int64_t n_tiles) {
+    return (size_t)((13 * n_tiles + 8 + 3) / 4 * 4);
+}
+__host__ __device__ inline size_t schedule_elems(int64_t n_tiles) {
+    return schedule_head_elems(n_tiles) + (size_t)n_tiles * kCheckpoints * kTilePixels * 4;
+}
+inline Checkpoints schedule_checkpoints(int32_t *schedule, int64_t n_tiles) {
+    Checkpoints c;
+    c.count = schedule + 2 * n_tiles;
+    c.pos = schedule + 3 * n_tiles;
+    c.work = reinterpret_cast<uint32_t *>(schedule + 6 * n_tiles);
+    c.items = schedule + 9 * n_tiles;
+    c.n_items = schedule + 13 * n_tiles;
+    c.data = reinterpret_cast<float *>(schedule + schedule_head_elems(n_tiles));
+    return c;
+}
+constexpr Checkpoints kNoCheckpoints{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+// The checkpoints of a schedule buffer, or none (without one, or on grids of
+// more than kCheckpointMaxTiles tiles).
+inline Checkpoints schedule_ck(const int32_t *schedule, int64_t n_tiles) {
+    if (!schedule || n_tiles <= 0 || n_tiles > kCheckpointMaxTiles) return kNoCheckpoints;
+    return schedule_checkpoints(const_cast<int32_t *>(schedule), n_tiles);
+}
+
 // Bijection workgroup -> tile giving XCD x the contiguous tile range
 // [x*base + min(x, rem), ...) of length base + (x < rem).
 __device__ __forceinline__ int tile_of_block(int b, int n_tiles) {
@@ -534,6 +600,37 @@ __device__ __forceinline__ float effective_T_thr(float T_thr) { return fmaxf(T_t
 // tile's W waves sharing each staged batch of W * kBatch records.  Every thread
 // of the workgroup must call it (it contains barriers).  `work` counts the
 // wave's own strips and, in wave 0 only, the batches and staged records.
+// The lane's pixels of checkpoint i of `tile` (local pixel lane + 64 * strip):
+// each strip's 64 lanes store 1 KB contiguously.
+template <int W>
+__device__ __forceinline__ void save_checkpoint(const Checkpoints &ck, int tile, int i,
+                                                int32_t pos, uint32_t work,
+                                                const float (&T)[kStrips / W],
+                                                const float (&cr)[kStrips / W],
+                                                const float (&cg)[kStrips / W],
+                                                const float (&cb)[kStrips / W]) {
+    constexpr int S = kStrips / W;
+    // the slot is uniform: a scalar base plus the lane's 32-bit offset
+    const int slot = __builtin_amdgcn_readfirstlane(tile * kCheckpoints + i);
+    const int q0 = W == 1 ? 0 : tile_wave() * S;
+    float *dst = ck.data + (int64_t)slot * (4 * kTilePixels);
+    const uint32_t lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int q = 0; q < S; ++q) {  // four planes: no packing of the values into quads
+        const uint32_t p = lane + (uint32_t)(kWave * (q0 + q));
+        dst[p] = T[q];
+        dst[kTilePixels + p] = cr[q];
+        dst[2 * kTilePixels + p] = cg[q];
+        dst[3 * kTilePixels + p] = cb[q];
+    }
+    if (threadIdx.x == 0) {  // thread 0 holds the batch and record work (wave 0)
+        ck.pos[slot] = pos;
+        ck.work[slot] = work;
+    }
+}
+
+// With ck.data (the forward of a tile in [0, n_tiles)), saves up to kCheckpoints
+// checkpoints and returns their number in n_ck (uniform across the workgroup).
 template <int W>
 __device__ __forceinline__ void blend_accumulate(
     BatchLds<W> &s, TileSpan span, const int32_t *__restrict__ ids, int64_t n,
@@ -541,7 +638,8 @@ __device__ __forceinline__ void blend_accumulate(
     const float *__restrict__ opac, const float *__restrict__ colors,
     const LanePixels<kStrips / W> &pix, float alpha_thr, float T_thr_in, float chi,
     float (&cr)[kStrips / W], float (&cg)[kStrips / W], float (&cb)[kStrips / W],
-    uint32_t &work) {
+    uint32_t &work, const Checkpoints &ck = kNoCheckpoints,
+    int tile = 0, int *n_ck = nullptr) {
     constexpr int S = kStrips / W;
     // a pixel is active while !(T < T_thr)
     const float T_thr = effective_T_thr(T_thr_in);
@@ -551,12 +649,19 @@ __device__ __forceinline__ void blend_accumulate(
         T[q] = pix.inside[q] ? 1.0f : kInactiveT;
         cr[q] = cg[q] = cb[q] = 0.0f;
     }
+    if (n_ck) *n_ck = 0;
     if (span.end <= span.start) return;
     BatchPipe<false, false, W> pipe;
     pipe.start(span, ids, n, points, conics, opac, colors);
     const bool counter = W == 1 || tile_wave() == 0;
-    for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch * W) {
+    int batch = 0, saved = 0;
+    for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch * W, ++batch) {
         if (!tile_any<W>(any_active(T, T_thr), s.wave_flag)) break;
+        if (ck.data && batch > 0 && batch % checkpoint_spacing<W>() == 0 &&
+            saved < kCheckpoints) {
+            save_checkpoint<W>(ck, tile, saved, b0, work, T, cr, cg, cb);
+            ++saved;
+        }
         const Staged st = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
                                        alpha_thr, pix.x0, pix.y0);
         if (counter) work += kCostBatch + kCostStaged * (uint32_t)st.count;
@@ -565,6 +670,7 @@ __device__ __forceinline__ void blend_accumulate(
         else
             blend_batch<false, W>(s, st.count, pix, alpha_thr, T_thr, chi, T, cr, cg, cb, work);
     }
+    if (n_ck) *n_ck = saved;
 }
 
 // ------------------------------------------------- wave reductions (gfx950)
@@ -647,16 +753,19 @@ __device__ __forceinline__ float wave_sum9(const float (&f)[kGradFields], bool h
     return f8_lane ? q2 : r;
 }
 
-// One tile per workgroup of W waves (64 W threads).
+// One tile per workgroup of W waves (64 W threads).  Held to 64 VGPRs (8 waves
+// per SIMD), which the compiler meets without spilling; the checkpoint stores
+// would otherwise take it to 72 (7 waves).
 template <int W>
-__global__ __launch_bounds__(kWave * W) void blend_forward_kernel(
+__global__ __launch_bounds__(kWave * W) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void blend_forward_kernel(
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
     int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
     const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
     int height, float alpha_thr, float T_thr, float chi, float *__restrict__ image,
     float *__restrict__ display, const float *__restrict__ target,
     float *__restrict__ tile_loss, float4 *__restrict__ clear4, int64_t clear4_count,
-    uint32_t *__restrict__ tile_cost, const int32_t *__restrict__ tile_order) {
+    uint32_t *__restrict__ tile_cost, const int32_t *__restrict__ tile_order, Checkpoints ck) {
     constexpr int S = kStrips / W;
     __shared__ BatchLds<W> s;
     __shared__ float wave_l1[W];
@@ -677,8 +786,10 @@ __global__ __launch_bounds__(kWave * W) void blend_forward_kernel(
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
     float cr[S], cg[S], cb[S];
     uint32_t work = 0;
+    int n_ck = 0;
     blend_accumulate<W>(s, span, ids, n, points, conics, opac, colors, pix, alpha_thr, T_thr, chi,
-                        cr, cg, cb, work);
+                        cr, cg, cb, work, ck, tile, &n_ck);
+    if (ck.count && threadIdx.x == 0) ck.count[tile] = n_ck;
     float l1 = 0.0f;
 #pragma unroll
     for (int q = 0; q < S; ++q) {
@@ -893,24 +1004,41 @@ __device__ __forceinline__ void backward_batch(const BatchLds<W> &s, int cnt,
 //                     times *grad_loss: grad_image holds the target (image required).
 enum { kSeedImage = 0, kSeedDisplay = 1, kSeedL1 = 2 };
 
+#define GS_BACKWARD_PARAMS                                                                   \
+    const float *__restrict__ grad_image, const float *__restrict__ image,                   \
+        const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,    \
+        int64_t k, int64_t n, const float *__restrict__ points,                               \
+        const float *__restrict__ conics, const float *__restrict__ opac,                     \
+        const float *__restrict__ colors, int tiles_x, int width, int height, float alpha_thr, \
+        float T_thr_in, float chi, float *__restrict__ g_points, float *__restrict__ g_conics, \
+        float *__restrict__ g_opac, float *__restrict__ g_colors,                             \
+        const float *__restrict__ grad_loss, float inv_count, const float *__restrict__ extra
+
+// The backward walk of `tile`'s list, or (seg >= 0) of its segment seg: from the
+// start to checkpoint 0, between checkpoints seg - 1 and seg, or from the last
+// checkpoint to the end.  Every thread of the workgroup calls it with the same
+// tile and segment (it contains barriers).
 template <int kSeed, int W>
-__global__ __launch_bounds__(kWave * W) void blend_backward_kernel(
-    const float *__restrict__ grad_image, const float *__restrict__ image,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ ids, int n_tiles,
-    int64_t k, int64_t n, const float *__restrict__ points, const float *__restrict__ conics,
-    const float *__restrict__ opac, const float *__restrict__ colors, int tiles_x, int width,
-    int height, float alpha_thr, float T_thr_in, float chi, float *__restrict__ g_points,
-    float *__restrict__ g_conics, float *__restrict__ g_opac, float *__restrict__ g_colors,
-    const float *__restrict__ grad_loss, float inv_count, const float *__restrict__ extra,
-    const int32_t *__restrict__ tile_order) {
+__device__ __forceinline__ void backward_tile(BatchLds<W> &s, int tile, int seg,
+                                              const Checkpoints &ck, GS_BACKWARD_PARAMS) {
     constexpr int S = kStrips / W;
-    __shared__ BatchLds<W> s;
     const float T_thr = effective_T_thr(T_thr_in);
-    const int slot = tile_of_block(blockIdx.x, n_tiles);
-    const int tile = tile_order ? tile_order[slot] : slot;
     if ((unsigned)tile >= (unsigned)n_tiles) return;  // uniform across the workgroup
     const LanePixels<S> pix = lane_pixels<W>(tile, tiles_x, width, height);
-    const TileSpan span = tile_span(offsets, n_tiles, k, tile);
+    TileSpan span = tile_span(offsets, n_tiles, k, tile);
+    int32_t ck_slot = -1;  // the checkpoint this segment starts from (seg > 0)
+    if (seg >= 0) {
+        // positions clamped into the tile's list: a stale count or position can
+        // only make the segments wrong, never reach outside the list
+        const int c = min(max(ck.count[tile], 0), kCheckpoints);
+        if (seg > c) return;
+        const int32_t *pos = ck.pos + (int64_t)tile * kCheckpoints;
+        const int32_t a = seg == 0 ? span.start : min(max(pos[seg - 1], span.start), span.end);
+        const int32_t b = seg < c ? min(max(pos[seg], a), span.end) : span.end;
+        span.start = a;
+        span.end = b;
+        if (seg > 0) ck_slot = tile * kCheckpoints + seg - 1;
+    }
     if (span.end <= span.start) return;  // uniform across the workgroup
     // d loss / d (display / 255) per element, for kSeedL1
     const float l1_scale = kSeed == kSeedL1 ? *grad_loss * inv_count : 0.0f;
@@ -958,7 +1086,17 @@ __global__ __launch_bounds__(kWave * W) void blend_backward_kernel(
         // active while !(T < T_thr); pixels outside the image or with a zero
         // gradient (skipped as in src/cuda/kernel.cu:1028-1030) start inactive
         const bool live = pix.inside[q] && !(gr == 0.0f && gg == 0.0f && gb == 0.0f);
-        L.T[q] = live ? 1.0f : kInactiveT;
+        float T0 = 1.0f;
+        if (ck_slot >= 0) {  // a later segment: the forward's state at its first entry
+            const int q0 = W == 1 ? 0 : tile_wave() * S;
+            const float *c = ck.data + (int64_t)ck_slot * (4 * kTilePixels) +
+                             (threadIdx.x % kWave) + kWave * (q0 + q);
+            T0 = c[0];
+            L.acc[q] = fmaf(gr, c[kTilePixels], fmaf(gg, c[2 * kTilePixels],
+                                                    gb * c[3 * kTilePixels])) - L.gC[q];
+            finite = finite && isfinite(L.acc[q]);
+        }
+        L.T[q] = live ? T0 : kInactiveT;
     }
     // the zero-weight update needs finite gradients and image values in the tile
     const bool tile_nonfinite = tile_any<W>(__ballot(!finite) != 0, s.wave_flag_once);
@@ -981,6 +1119,36 @@ __global__ __launch_bounds__(kWave * W) void blend_backward_kernel(
             backward_batch<false, W>(s, st.count, pix, alpha_thr, T_thr, chi, L, tgt, hi8,
                                      f8_lane);
     }
+}
+
+// Without segment lists: one workgroup of W waves per tile slot.  With them:
+// kSegments workgroups per tile slot of the largest XCD range, workgroup b
+// taking entry b / kXcds of range b % kXcds's list (the dispatcher places
+// workgroup b on XCD b % kXcds and launches in order: each XCD works through its
+// list heaviest tiles first, a tile's segments side by side); workgroups past
+// their range's list end at once.
+template <int kSeed, int W>
+__global__ __launch_bounds__(kWave * W) void blend_backward_kernel(
+    GS_BACKWARD_PARAMS, const int32_t *__restrict__ tile_order, Checkpoints ck) {
+    __shared__ BatchLds<W> s;
+    int tile, seg = -1;
+    if (!ck.items) {
+        const int slot = tile_of_block(blockIdx.x, n_tiles);
+        tile = tile_order ? tile_order[slot] : slot;
+    } else {
+        const int base = n_tiles / kXcds, rem = n_tiles % kXcds;
+        const int x = (int)blockIdx.x % kXcds, j = (int)blockIdx.x / kXcds;
+        const int first = x * base + min(x, rem), len = base + (x < rem ? 1 : 0);
+        const int listed = min(ck.n_items[x], kSegments * len);
+        if (j >= listed) return;  // uniform across the workgroup
+        const int item = ck.items[4 * (int64_t)first + j];
+        tile = item / kSegments;
+        seg = item % kSegments;
+    }
+    backward_tile<kSeed, W>(s, tile, seg, ck, grad_image, image, offsets, ids, n_tiles, k, n,
+                            points, conics, opac, colors, tiles_x, width, height, alpha_thr,
+                            T_thr_in, chi, g_points, g_conics, g_opac, g_colors, grad_loss,
+                            inv_count, extra);
 }
 
 // ------------------------------------------------ generic tile size path
@@ -1183,7 +1351,8 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                           float chi_squared_threshold, float *image, float *display,
                           const float *target, float *tile_loss, hipStream_t stream,
                           float *clear = nullptr, int64_t clear_count = 0,
-                          uint32_t *tile_cost = nullptr, const int32_t *tile_order = nullptr) {
+                          uint32_t *tile_cost = nullptr, const int32_t *tile_order = nullptr,
+                          Checkpoints ck = kNoCheckpoints) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -1223,7 +1392,7 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
                            image, display, target, tile_loss,
                            fused_clear ? reinterpret_cast<float4 *>(clear) : nullptr,
-                           fused_clear ? clear_count / 4 : (int64_t)0, tile_cost, tile_order);
+                           fused_clear ? clear_count / 4 : (int64_t)0, tile_cost, tile_order, ck);
     } else {
         hipLaunchKernelGGL(blend_forward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, indexing_offset,
@@ -1255,7 +1424,8 @@ extern "C" int gs_rasterize(const int32_t *indexing_offset, const int32_t *gauss
 }
 
 static int launch_l1_finish(int32_t n_tiles, const float *tile_loss, float inv_count, float *loss,
-                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream);
+                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream,
+                            Checkpoints ck = kNoCheckpoints);
 
 extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
                                     const int32_t *gaussian_ids_sorted, int32_t n_tiles,
@@ -1272,10 +1442,10 @@ extern "C" int gs_rasterize_display(const int32_t *indexing_offset,
                                   cov_inv_image, opacities, colors, n, width, height, tile_size,
                                   alpha_threshold, transmittance_threshold, chi_squared_threshold,
                                   image, display, nullptr, nullptr, stream, nullptr, 0, cost,
-                                  forward_order);
+                                  forward_order, schedule_ck(tile_schedule, n_tiles));
     if (st || !tile_schedule || n_tiles == 0) return st;
     return launch_l1_finish(n_tiles, nullptr, 0.0f, nullptr, cost, tile_schedule + n_tiles,
-                            stream);
+                            stream, schedule_ck(tile_schedule, n_tiles));
 }
 
 extern "C" int gs_rasterize_display_l1(
@@ -1295,12 +1465,13 @@ extern "C" int gs_rasterize_display_l1(
                             cov_inv_image, opacities, colors, n, width, height, tile_size,
                             alpha_threshold, transmittance_threshold, chi_squared_threshold,
                             image, display, target, tile_loss, stream, clear, clear_count, cost,
-                            forward_order);
+                            forward_order, schedule_ck(tile_schedule, n_tiles));
     if (st) return st;
     // the loss (when asked for) and the backward's tile order, in one launch
     const double count = (double)width * (double)height * 3.0;
     return launch_l1_finish(n_tiles, tile_loss, (float)(1.0 / count), loss, cost,
-                            tile_schedule ? tile_schedule + n_tiles : nullptr, stream);
+                            tile_schedule ? tile_schedule + n_tiles : nullptr, stream,
+                            schedule_ck(tile_schedule, n_tiles));
 }
 
 // The backward's launch order from the forward's per-tile work: within each
@@ -1325,46 +1496,45 @@ __device__ __forceinline__ uint32_t order_code(uint32_t work) {
     return (uint32_t)(kOrderCodes - 2) - min(e * 16u + m, (uint32_t)(kOrderCodes - 2));
 }
 
+
 __device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tiles,
-                            int32_t *__restrict__ order) {
+                            int32_t *__restrict__ order, const Checkpoints &ck) {
     __shared__ uint32_t start_of[kOrderCodes];
     __shared__ uint32_t wave_cnt[kFinishWaves][kOrderCodes];
     const int base = n_tiles / kXcds, rem = n_tiles % kXcds;
     const int first = x * base + min(x, rem), len = base + (x < rem ? 1 : 0);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    for (int d = threadIdx.x; d < kOrderCodes; d += kFinishThreads) start_of[d] = 0u;
-    __syncthreads();
-    for (int i = threadIdx.x; i < len; i += kFinishThreads)
-        atomicAdd(&start_of[order_code(cost[first + i])], 1u);
-    __syncthreads();
-    if (threadIdx.x < kWave) {  // exclusive scan of the 256 counts by one wave
-        uint32_t c[kOrderCodes / kWave], run = 0;
+    // one stable counting sort pass: the code of each element, then the elements
+    // in chunks of kFinishThreads (one per thread), each placed at its code's
+    // running start plus its rank among the chunk's elements of that code
+    auto scan_codes = [&]() {
+        if (threadIdx.x < kWave) {  // exclusive scan of the counts by one wave
+            uint32_t c[kOrderCodes / kWave], run = 0;
 #pragma unroll
-        for (int e = 0; e < kOrderCodes / kWave; ++e) {
-            c[e] = start_of[lane * (kOrderCodes / kWave) + e];
-            run += c[e];
-        }
-        const uint32_t incl = wave_inclusive_scan(run);
-        uint32_t at = incl - run;
+            for (int e = 0; e < kOrderCodes / kWave; ++e) {
+                c[e] = start_of[lane * (kOrderCodes / kWave) + e];
+                run += c[e];
+            }
+            const uint32_t incl = wave_inclusive_scan(run);
+            uint32_t at = incl - run;
 #pragma unroll
-        for (int e = 0; e < kOrderCodes / kWave; ++e) {
-            start_of[lane * (kOrderCodes / kWave) + e] = at;
-            at += c[e];
+            for (int e = 0; e < kOrderCodes / kWave; ++e) {
+                start_of[lane * (kOrderCodes / kWave) + e] = at;
+                at += c[e];
+            }
         }
-    }
-    for (int c0 = 0; c0 < len; c0 += kFinishThreads) {
-        for (int d = lane; d < kOrderCodes; d += kWave) wave_cnt[wave][d] = 0u;
+    };
+    // places one element per thread (valid ones), returns its position (or 0)
+    auto place = [&](bool valid, uint32_t d) -> uint32_t {
+        for (int dd = lane; dd < kOrderCodes; dd += kWave) wave_cnt[wave][dd] = 0u;
         __syncthreads();
-        const int i = c0 + (int)threadIdx.x;
-        const bool valid = i < len;
-        const uint32_t d = valid ? order_code(cost[first + i]) : 0u;
         const uint64_t peers = match_digit(d, 9, __ballot(valid));
         if (valid && (peers & lanemask_lt()) == 0) wave_cnt[wave][d] = (uint32_t)__popcll(peers);
         __syncthreads();
+        uint32_t pos = 0;
         if (valid) {
-            uint32_t pos = start_of[d] + (uint32_t)__popcll(peers & lanemask_lt());
+            pos = start_of[d] + (uint32_t)__popcll(peers & lanemask_lt());
             for (int w = 0; w < wave; ++w) pos += wave_cnt[w][d];
-            order[first + (int)pos] = first + i;
         }
         __syncthreads();
         for (int dd = threadIdx.x; dd < kOrderCodes; dd += kFinishThreads) {
@@ -1374,16 +1544,71 @@ __device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tile
             start_of[dd] += c;
         }
         __syncthreads();  // counts read before the next chunk clears them
+        return pos;
+    };
+
+    // the tiles by descending work
+    for (int d = threadIdx.x; d < kOrderCodes; d += kFinishThreads) start_of[d] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < len; i += kFinishThreads)
+        atomicAdd(&start_of[order_code(cost[first + i])], 1u);
+    __syncthreads();
+    scan_codes();
+    for (int c0 = 0; c0 < len; c0 += kFinishThreads) {
+        const int i = c0 + (int)threadIdx.x;
+        const bool valid = i < len;
+        const uint32_t d = valid ? order_code(cost[first + i]) : 0u;
+        const uint32_t pos = place(valid, d);
+        if (valid) order[first + (int)pos] = first + i;
     }
+    if (!ck.count) return;
+
+    // the segments by descending work: segment q of tile t is worked from
+    // checkpoint q - 1 (or the start) to checkpoint q (or the end)
+    auto segment_work = [&](int t, int q, int c) -> uint32_t {
+        const uint32_t before = q > 0 ? ck.work[t * kCheckpoints + q - 1] : 0u;
+        const uint32_t upto = q < c ? ck.work[t * kCheckpoints + q] : cost[t];
+        return upto > before ? upto - before : 1u;
+    };
+    __syncthreads();
+    for (int d = threadIdx.x; d < kOrderCodes; d += kFinishThreads) start_of[d] = 0u;
+    __syncthreads();
+    uint32_t mine = 0;
+    for (int i = threadIdx.x; i < len; i += kFinishThreads) {
+        const int t = first + i;
+        const int c = min(max(ck.count[t], 0), kCheckpoints);
+        for (int q = 0; q <= c; ++q) atomicAdd(&start_of[order_code(segment_work(t, q, c))], 1u);
+        mine += (uint32_t)c + 1u;
+    }
+    __syncthreads();
+    scan_codes();
+    int32_t *items = ck.items + 4 * (int64_t)first;
+    for (int c0 = 0; c0 < len; c0 += kFinishThreads) {
+        const int i = c0 + (int)threadIdx.x;
+        const int t = first + i;
+        const int c = i < len ? min(max(ck.count[t], 0), kCheckpoints) : -1;
+        for (int q = 0; q < kSegments; ++q) {  // the chunk's q-th segments, one per tile
+            const bool valid = q <= c;
+            const uint32_t d = valid ? order_code(segment_work(t, q, c)) : 0u;
+            const uint32_t pos = place(valid, d);
+            if (valid) items[pos] = t * kSegments + q;
+        }
+    }
+    // the list's length: the sum of the tiles' segment counts
+    uint32_t total;
+    __shared__ uint32_t scan_tmp[kFinishWaves + 1];
+    block_exclusive_scan<uint32_t, kFinishThreads>(mine, scan_tmp, total);
+    if (threadIdx.x == 0) ck.n_items[x] = (int32_t)total;
 }
 
-// Workgroups 0..kXcds-1 (with tile_order) order the backward's tiles; the last
-// workgroup (with loss) writes loss = (sum of the n_tiles partial sums) * inv_count.
+// Workgroups 0..kXcds-1 (with tile_order) order the backward's tiles (and, with
+// checkpoints, list their segments); the last workgroup (with loss) writes
+// loss = (sum of the n_tiles partial sums) * inv_count.
 __global__ __launch_bounds__(kFinishThreads) void l1_finish_kernel(
     int n_tiles, const float *__restrict__ tile_loss, float inv_count, float *__restrict__ loss,
-    const uint32_t *__restrict__ tile_cost, int32_t *__restrict__ tile_order) {
+    const uint32_t *__restrict__ tile_cost, int32_t *__restrict__ tile_order, Checkpoints ck) {
     if (tile_order && (int)blockIdx.x < kXcds) {
-        order_range((int)blockIdx.x, tile_cost, n_tiles, tile_order);
+        order_range((int)blockIdx.x, tile_cost, n_tiles, tile_order, ck);
         return;
     }
     if (!loss) return;
@@ -1414,11 +1639,13 @@ __global__ __launch_bounds__(kFinishThreads) void l1_finish_kernel(
 }
 
 static int launch_l1_finish(int32_t n_tiles, const float *tile_loss, float inv_count, float *loss,
-                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream) {
+                            const uint32_t *tile_cost, int32_t *tile_order, hipStream_t stream,
+                            Checkpoints ck) {
     const int blocks = (tile_order ? kXcds : 0) + (loss ? 1 : 0);
     if (blocks == 0) return GS_OK;
     hipLaunchKernelGGL(l1_finish_kernel, dim3(blocks), dim3(kFinishThreads), 0, stream, n_tiles,
-                       tile_loss, inv_count, loss, tile_cost, tile_order);
+                       tile_loss, inv_count, loss, tile_cost, tile_order,
+                       tile_order ? ck : kNoCheckpoints);
     return launch_status();
 }
 
@@ -1438,7 +1665,8 @@ static int rasterize_backward_impl(
     float transmittance_threshold, float chi_squared_threshold, float *grad_points_image,
     float *grad_cov_inv_image, float *grad_opacities, float *grad_colors, int32_t accumulate,
     int seed, const float *grad_loss, float inv_count, hipStream_t stream,
-    const float *extra = nullptr, const int32_t *tile_order = nullptr) {
+    const float *extra = nullptr, const int32_t *tile_order = nullptr,
+    Checkpoints ck = kNoCheckpoints) {
     int st = check_blend_args(indexing_offset, gaussian_ids_sorted, n_tiles, k, n, width, height,
                               tile_size, alpha_threshold, transmittance_threshold,
                               chi_squared_threshold);
@@ -1472,12 +1700,18 @@ static int rasterize_backward_impl(
                              : pick(blend_backward_kernel<kSeedL1, 1>,
                                     blend_backward_kernel<kSeedDisplay, 1>,
                                     blend_backward_kernel<kSeedImage, 1>);
-        hipLaunchKernelGGL(kern, dim3(n_tiles), dim3(kWave * W), 0, stream, grad_image, image,
-                           indexing_offset, gaussian_ids_sorted, n_tiles, k, n, points_image,
-                           cov_inv_image, opacities, colors, tiles_x, width, height,
+        // segments from the forward's checkpoints need the image (a recomputed
+        // forward has none) and the order they came with
+        if (!image || !tile_order) ck = kNoCheckpoints;
+        // with lists: kSegments workgroups per slot of the largest range, on each XCD
+        const int64_t grid =
+            ck.items ? (int64_t)kXcds * kSegments * ((n_tiles + kXcds - 1) / kXcds) : n_tiles;
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kWave * W), 0, stream, grad_image,
+                           image, indexing_offset, gaussian_ids_sorted, n_tiles, k, n,
+                           points_image, cov_inv_image, opacities, colors, tiles_x, width, height,
                            alpha_threshold, transmittance_threshold, chi_squared_threshold,
                            grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors,
-                           grad_loss, inv_count, extra, tile_order);
+                           grad_loss, inv_count, extra, tile_order, ck);
     } else {
         hipLaunchKernelGGL(blend_backward_generic_kernel, dim3(n_tiles),
                            dim3(tile_size * tile_size), 0, stream, grad_image, image,
@@ -1519,7 +1753,8 @@ extern "C" int gs_rasterize_display_backward(
                                    transmittance_threshold, chi_squared_threshold,
                                    grad_points_image, grad_cov_inv_image, grad_opacities,
                                    grad_colors, accumulate, kSeedDisplay, nullptr, 0.0f, stream,
-                                   nullptr, tile_schedule ? tile_schedule + n_tiles : nullptr);
+                                   nullptr, tile_schedule ? tile_schedule + n_tiles : nullptr,
+                                   schedule_ck(tile_schedule, n_tiles));
 }
 
 extern "C" int gs_rasterize_l1_backward(
@@ -1541,7 +1776,8 @@ extern "C" int gs_rasterize_l1_backward(
                                    chi_squared_threshold, grad_points_image, grad_cov_inv_image,
                                    grad_opacities, grad_colors, accumulate, kSeedL1, grad_loss,
                                    inv_count, stream, grad_display01,
-                                   tile_schedule ? tile_schedule + n_tiles : nullptr);
+                                   tile_schedule ? tile_schedule + n_tiles : nullptr,
+                                   schedule_ck(tile_schedule, n_tiles));
 }
 
 extern "C" int gs_rasterize_work(const int32_t *indexing_offset,
@@ -1568,4 +1804,12 @@ extern "C" int gs_rasterize_work(const int32_t *indexing_offset,
                        reinterpret_cast<unsigned long long *>(visited),
                        reinterpret_cast<unsigned long long *>(composited));
     return launch_status();
+}
+
+extern "C" int gs_tile_schedule_size(int32_t n_tiles, size_t *elements) {
+    if (n_tiles < 0 || !elements) return GS_ERR_INVALID_ARGUMENT;
+    *elements = n_tiles <= 0                              ? 2
+                : n_tiles > gs::kCheckpointMaxTiles ? 2 * (size_t)n_tiles
+                                                    : gs::schedule_elems(n_tiles);
+    return GS_OK;
 }

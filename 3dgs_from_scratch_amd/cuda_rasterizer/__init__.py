@@ -59,6 +59,8 @@ __all__ = [
     "rasterize_display_l1",
     "rasterize_l1_backward",
     "blend_grad_accumulators",
+    "tile_schedule",
+    "schedule_size",
     "set_blend_waves",
     "check_forward_order",
     "fused_ssim",
@@ -694,19 +696,30 @@ def set_blend_waves(waves: int = 0) -> None:
     _lib.check(_lib.load().gs_set_blend_waves(int(waves)), "set_blend_waves")
 
 
+def schedule_size(n_tiles) -> int:
+    """int32 elements of a tile schedule for n_tiles tiles (gs_tile_schedule_size)."""
+    out = ctypes.c_size_t(0)
+    _lib.check(_lib.load().gs_tile_schedule_size(int(n_tiles), ctypes.byref(out)),
+               "tile_schedule_size")
+    return int(out.value)
+
+
 def tile_schedule(n_tiles, device):
-    """An uninitialised int32 buffer of 2 * n_tiles: pass it as
-    rasterize_display_l1(schedule=...) (which fills it: the work of each tile,
-    then the backward's launch order) and then as rasterize_l1_backward(schedule=...)."""
-    return torch.empty((2 * max(int(n_tiles), 1),), dtype=torch.int32, device=device)
+    """An uninitialised int32 buffer of schedule_size(n_tiles) elements: pass it as
+    rasterize_display_l1(schedule=...) or rasterize_display(schedule=...), which
+    fill it (the work of each tile, the backward's launch order, and the
+    transmittance and colour checkpoints of the long tiles' walks), and then as
+    the backward's schedule, which launches those tiles in segments."""
+    return torch.empty((max(schedule_size(n_tiles), 2),), dtype=torch.int32, device=device)
 
 
 def _check_schedule(schedule, n_tiles, dev, who):
+    need = schedule_size(n_tiles)
     if (not isinstance(schedule, torch.Tensor) or schedule.dtype != torch.int32
             or schedule.device != dev or not schedule.is_contiguous()
-            or schedule.numel() < 2 * n_tiles):
+            or schedule.numel() < need):
         raise RuntimeError(f"{who}: schedule must be a contiguous int32 tensor of at least "
-                           f"{2 * n_tiles} elements on {dev}")
+                           f"{need} elements on {dev} (tile_schedule)")
 
 
 # Set True (tests do) to verify every forward launch order as a permutation of
@@ -1164,9 +1177,9 @@ def rasterize_display_l1(indexing_offset, gaussian_ids_sorted, points_image, cov
     """rasterize_display with tile size 16 plus loss = mean(|display / 255 - target|).
     Returns (image, display, loss[1] fp32).  `clear` (an fp32 device tensor, e.g.
     from blend_grad_accumulators) is zeroed by the same launch.  `schedule` (an
-    int32 device tensor of 2 * n_tiles, see tile_schedule) receives the work per
-    tile and the order in which rasterize_l1_backward, given it, launches the
-    tiles (heaviest first).  `forward_schedule`: a schedule an earlier call filled
+    int32 device tensor from tile_schedule) receives the work per tile, the order
+    in which rasterize_l1_backward, given it, launches the tiles (heaviest first)
+    and the checkpoints that let it walk long tiles in segments.  `forward_schedule`: a schedule an earlier call filled
     for the same image size (not this call's `schedule`); this forward then
     launches its tiles in that order (results do not depend on it).
     `forward_order`: instead of forward_schedule, any per-XCD-range launch order

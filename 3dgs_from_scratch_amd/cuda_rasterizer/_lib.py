@@ -17,6 +17,7 @@ _PSZ = ctypes.POINTER(ctypes.c_size_t)
 
 # name -> argtypes (all functions return int status)
 SIGNATURES = {
+    "gs_tile_schedule_size": [_I32, _P],
     "gs_abi_version": [],
     "gs_host_device_pointer": [_P, ctypes.POINTER(ctypes.c_void_p)],
     "gs_project_points": [_P] * 6 + [_I64, _F, _F, _F, _F, _F, _I32, _I32] + [_P] * 6 + [_P],

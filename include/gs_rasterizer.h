@@ -299,8 +299,9 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
  *   the means gradient to grad_means instead of overwriting it.
  * gs_rasterize_display: gs_rasterize that also writes
  *   display = clamp(image, 0, 1) * 255 (src/cuda/wrapper.py:294); tile_size 16.
- *   tile_schedule: null, or 2 * n_tiles int32 that receive the work per tile
- *   and the backward's launch order (as in gs_rasterize_display_l1).
+ *   tile_schedule: null, or gs_tile_schedule_size(n_tiles) int32 that receive
+ *   the work per tile, the backward's launch order and the walk's checkpoints
+ *   (as in gs_rasterize_display_l1).
  *   forward_order: null or a launch order of the tiles, as in
  *   gs_rasterize_display_l1 (e.g. gs_bin_sort_ordered's).
  * gs_rasterize_display_backward: gs_rasterize_backward given the gradient of
@@ -414,13 +415,19 @@ int gs_render_preprocess_backward(const float *grad_points_image,
  *   gs_rasterize_l1_backward then adds into with accumulate = 1, without a
  *   separate fill.  When loss is set, loss = sum(tile_loss) / (H * W * 3) is
  *   written as well (the gs_l1_finish result).  When tile_schedule is set
- *   (2 * n_tiles int32), the forward's work per tile goes to its first half
- *   and the backward's launch order to its second: per XCD's tile range, the
- *   tiles by descending work, so that gs_rasterize_l1_backward, given the same
- *   buffer, starts the heaviest tiles first (the results do not depend on it).
- *   forward_order: null (each XCD's range in tile order), or the second half
- *   of a tile_schedule buffer that an earlier call filled for the same tile
- *   grid, e.g. the last render of the same view in a training loop that visits
+ *   (gs_tile_schedule_size(n_tiles) int32), the forward's work per tile goes to
+ *   elements [0, n_tiles) and the backward's launch order to [n_tiles,
+ *   2 n_tiles): per XCD's tile range, the tiles by descending work, so that
+ *   gs_rasterize_l1_backward, given the same buffer, starts the heaviest tiles
+ *   first.  The rest receives checkpoints of each tile's walk: every 128 list
+ *   entries (every batch of 256 with 4 waves per tile), at most 3 times, each
+ *   pixel's transmittance and accumulated colour, from which the backward walks
+ *   the tile in up to 4 segments on as many workgroups (the results do not
+ *   depend on either, up to float rounding).
+ *   forward_order: null (each XCD's range in tile order), or elements
+ *   [n_tiles, 2 n_tiles) of a tile_schedule buffer that an earlier call filled
+ *   for the same tile grid, e.g. the last render of the same view in a training
+ *   loop that visits
  *   a fixed set of views: this forward then also starts its heaviest tiles (as
  *   they were then) first.  It must be a permutation of every XCD range (such a
  *   buffer is); the results do not depend on it.
@@ -434,8 +441,22 @@ int gs_render_preprocess_backward(const float *grad_points_image,
  *   image), it is a further gradient with respect to display / 255 (e.g. of an
  *   SSIM term on the same image, scripts/train.py:185-205), added to the L1
  *   one at that node.  tile_schedule: null, or the buffer that
- *   gs_rasterize_display_l1 filled for the same tile layout (its order is a
- *   permutation of the tiles; other contents give wrong gradients).
+ *   gs_rasterize_display_l1 filled for the same tile layout and image (its
+ *   order is a permutation of the tiles and its checkpoints belong to that
+ *   forward; other contents give wrong gradients, never an access outside the
+ *   lists: segment bounds are clamped into each tile's list).  With it the
+ *   tiles that have checkpoints run in segments.
+ * gs_tile_schedule_size: the int32 elements of a tile_schedule buffer for
+ *   n_tiles tiles: 2 n_tiles (work, order), n_tiles checkpoint counts,
+ *   3 n_tiles checkpoint positions, 3 n_tiles work counts, 4 n_tiles
+ *   segment-list entries, 8 list lengths (the forward's launch of the order
+ *   writes the lists: per XCD tile range, the segments of its tiles by
+ *   descending work), padded to 16 bytes, then
+ *   3 * 256 * 4 floats per tile (2 for n_tiles = 0).  Grids of more than 6144
+ *   tiles take no checkpoints (the backward starts one workgroup per tile, more
+ *   than the GPU holds at once, which balances them already): 2 n_tiles.  No counterpart in the reference (its
+ *   backward is one thread per pixel over the whole list,
+ *   src/cuda/kernel.cu:989-1111).
  */
 int gs_activate(const float *log_scales, const float *quats_raw, const float *opacity_logits,
                 int64_t n, float *scales, float *quats, float *opacities, hipStream_t stream);
@@ -467,6 +488,7 @@ int gs_rasterize_l1_backward(const float *target, const float *grad_loss, const 
                              float *grad_opacities, float *grad_colors, int32_t accumulate,
                              float loss_scale, const float *grad_display01,
                              const int32_t *tile_schedule, hipStream_t stream);
+int gs_tile_schedule_size(int32_t n_tiles, size_t *elements);
 
 /* ------------------------------------------------------------ training loop */
 

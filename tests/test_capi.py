@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 18
+    assert lib.gs_abi_version() == 19
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -173,11 +173,24 @@ def test_python_layer_refuses_cpu_tensors():
 
 
 def test_tile_schedule_buffers_are_checked():
-    """The schedule buffer must be a contiguous int32 tensor of at least 2 * n_tiles."""
+    """The schedule buffer must be a contiguous int32 tensor of at least
+    gs_tile_schedule_size(n_tiles) elements: per tile its work, launch slot,
+    checkpoint count, 3 checkpoint positions, 3 work counts and 4 segment-list
+    entries, 8 list lengths (padded to 16 bytes), then 3 checkpoints of 256
+    (T, r, g, b) pixels per tile."""
+    need = cuda_rasterizer.schedule_size(8)
+    assert need == 112 + 8 * 3 * 256 * 4
+    assert cuda_rasterizer.schedule_size(7) == 100 + 7 * 3 * 256 * 4  # 99 padded to 100
+    assert cuda_rasterizer.schedule_size(0) == 2
+    assert cuda_rasterizer.schedule_size(6144) == (13 * 6144 + 8 + 3) // 4 * 4 + 6144 * 3072
+    assert cuda_rasterizer.schedule_size(6145) == 2 * 6145  # no checkpoints on larger grids
+    out = ctypes.c_size_t(0)
+    assert _lib.load().gs_tile_schedule_size(-1, ctypes.byref(out)) != 0
+    assert _lib.load().gs_tile_schedule_size(8, None) != 0
     cpu = torch.device("cpu")
-    cuda_rasterizer._check_schedule(torch.zeros(16, dtype=torch.int32), 8, cpu, "probe")
-    for bad in (torch.zeros(15, dtype=torch.int32), torch.zeros(16, dtype=torch.int64),
-                torch.zeros(32, dtype=torch.int32)[::2], [0] * 16):
+    cuda_rasterizer._check_schedule(torch.zeros(need, dtype=torch.int32), 8, cpu, "probe")
+    for bad in (torch.zeros(need - 1, dtype=torch.int32), torch.zeros(need, dtype=torch.int64),
+                torch.zeros(2 * need, dtype=torch.int32)[::2], [0] * need):
         with pytest.raises(RuntimeError, match="schedule"):
             cuda_rasterizer._check_schedule(bad, 8, cpu, "probe")
 

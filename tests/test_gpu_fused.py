@@ -103,6 +103,36 @@ def test_fused_preprocess_equals_unfused_sequence(gpu):
         assert torch.equal(a, b)
 
 
+def _written_schedule(sched, n_tiles):
+    """The parts of a schedule a forward writes: work, backward order and
+    checkpoint counts of every tile, the position, work and pixels of each saved
+    checkpoint (the slots past a tile's count keep whatever they held), and each
+    XCD range's segment list; on grids of more than 6144 tiles, which take no
+    checkpoints, the work and order."""
+    s = sched.cpu()
+    n = n_tiles
+    if n > 6144:  # larger grids: work and order only
+        assert s.numel() == 2 * n
+        return s.tolist()
+    counts = s[2 * n:3 * n].long()
+    assert int(counts.min()) >= 0 and int(counts.max()) <= 3
+    used = torch.arange(3).unsqueeze(0) < counts.unsqueeze(1)  # (n_tiles, 3)
+    pos = s[3 * n:6 * n].view(n, 3)[used]
+    work = s[6 * n:9 * n].view(n, 3)[used]
+    head = (13 * n + 8 + 3) // 4 * 4
+    pix = s[head:head + n * 3 * 1024].view(n, 3, 1024)[used]
+    lengths = s[13 * n:13 * n + 8].tolist()
+    items = [s[9 * n + 4 * a:9 * n + 4 * a + m].tolist() for a, m in zip(_xcd_firsts(n), lengths)]
+    assert sum(lengths) == int(counts.sum()) + n
+    return (s[:3 * n].tolist(), pos.tolist(), work.tolist(), pix.view(torch.float32).tolist(),
+            items)
+
+
+def _xcd_firsts(n_tiles):
+    b, r = divmod(n_tiles, 8)
+    return [x * b + min(x, r) for x in range(8)]
+
+
 def test_forward_tile_order_changes_nothing_but_the_launch_order(gpu):
     """rasterize_display_l1 with an earlier call's schedule as forward_schedule (its
     tiles launched heaviest first): image, display, loss and this call's schedule
@@ -132,7 +162,7 @@ def test_forward_tile_order_changes_nothing_but_the_launch_order(gpu):
         got = cr.rasterize_display_l1(*args, schedule=second, forward_schedule=prev)
         for a, b in zip(got, ref):
             assert torch.equal(a, b)
-        assert torch.equal(second, first)
+        assert _written_schedule(second, nt) == _written_schedule(first, nt)
     with pytest.raises(cr.RasterizerError):
         cr.rasterize_display_l1(*args, schedule=first, forward_schedule=first)
 
@@ -406,7 +436,7 @@ def test_tile_schedule(gpu, size):
                                              schedule=sched_d)
         img_r, disp_r = cr.rasterize_display(off, ids, pts, conic, opac, colors, W, H, *thr)
         assert torch.equal(img_d, img_r) and torch.equal(disp_d, disp_r)
-        assert torch.equal(sched_d[:2 * n_tiles], sched[:2 * n_tiles])
+        assert _written_schedule(sched_d, n_tiles) == _written_schedule(sched, n_tiles)
         up = torch.randn((H, W, 3), generator=torch.Generator().manual_seed(5)).to(gpu)
         grads_d = [cr.rasterize_display_backward(up, off, ids, pts, conic, opac, colors, W, H,
                                                  *thr, rendered_image=img_r, schedule=s)
@@ -481,3 +511,46 @@ def test_render_l1_and_render_with_outgrown_capacities(gpu, monkeypatch):
         assert torch.equal(out[mode][2], out["first"][2]), mode
         for k in helpers.PARAMS:
             assert helpers.rel_l2(out[mode][3][k], out["first"][3][k]) <= 1e-5, (mode, k)
+
+
+@pytest.mark.parametrize("size,n", [((256, 192), 60_000), ((800, 608), 150_000)])
+def test_backward_segments_from_checkpoints(gpu, size, n):
+    """Long tile lists: the forward saves up to 3 checkpoints per tile (every 128
+    entries with one wave per tile, every 256 with four), and the backward given
+    the schedule walks those tiles in segments that start from them.  Gradients
+    equal the unsegmented walk's (no schedule) up to float rounding (the running
+    colour-gradient sum restarts from a dot product; atomics reorder), for the
+    L1 seed (fused) and the display seed (drop-in render path)."""
+    W, H = size
+    p, cam, target = helpers.scene_orbit(n, W, H, 1.2 * W, seed=57)
+    a = _raw_leaves(p, gpu)
+    tgt = target.to(gpu)
+    with torch.no_grad():
+        pts, depths, _, conic, radii, mask, opac, colors = cr.preprocess_forward(
+            a["means"], a["log_scales"], a["quats_raw"], a["opacity_logits"], a["sh_dc"],
+            a["sh_rest"], cam["w2c"].to(gpu), cam["K"].to(gpu), 0.01, 100.0, 1 / 255, 0.5, 128.0,
+            W, H)
+        off, ids = cr.compute_tile_intersection(pts, radii, depths, mask, W, H, 16)
+        n_tiles = off.shape[0]
+        sched = cr.tile_schedule(n_tiles, gpu)
+        image, display, loss = cr.rasterize_display_l1(off, ids, pts, conic, opac, colors, W, H,
+                                                       tgt, schedule=sched)
+        counts = sched[2 * n_tiles:3 * n_tiles].cpu()
+        assert int(counts.max()) == 3 and int((counts > 0).sum()) >= n_tiles // 4
+        g = torch.full((1,), 0.9, device=gpu)
+        plain, seg = [cr.rasterize_l1_backward(tgt, g, off, ids, pts, conic, opac, colors, W, H,
+                                               image, schedule=s) for s in (None, sched)]
+        for x, y in zip(plain, seg):
+            assert helpers.rel_l2(y, x) <= 1e-5
+        thr = (16, 1e-4, 1e-4, 9.21)
+        sched_d = cr.tile_schedule(n_tiles, gpu)
+        img_d, _ = cr.rasterize_display(off, ids, pts, conic, opac, colors, W, H, *thr,
+                                        schedule=sched_d)
+        assert torch.equal(img_d, image)
+        up = torch.randn((H, W, 3), generator=torch.Generator().manual_seed(6)).to(gpu)
+        plain, seg = [cr.rasterize_display_backward(up, off, ids, pts, conic, opac, colors, W,
+                                                    H, *thr, rendered_image=img_d, schedule=s)
+                      for s in (None, sched_d)]
+        for x, y in zip(plain, seg):
+            assert helpers.rel_l2(y, x) <= 1e-5
+

@@ -7,7 +7,10 @@ Each replay is checked against an eager call on the same parameter values, with
 in-place parameter updates, eager work and synchronisations between the
 replays: the replay must read the updated parameters.  Loss and display are
 bit-equal (the same kernels on the same inputs; the capped lists do not depend
-on the capacity); gradients within relative L2 1e-5 (float atomics).  A replay
+on the capacity); gradients within relative L2 1e-5, 5e-5 for the raw
+quaternions (the blend backward's float atomics land in a different order, and
+the quaternion normalisation's backward cancels: the bar of the configuration-3
+fused-vs-drop-in test for the same reason).  A replay
 whose lists outgrow the capacities fixed at capture is reported by ok(), and a
 recapture after an eager call covers the larger lists.
 
@@ -30,6 +33,7 @@ from cuda_rasterizer.wrapper import render
 pytestmark = pytest.mark.gpu
 
 W, H = 256, 192
+ORDER_BAR = {k: 5e-5 if k == "quats_raw" else 1e-5 for k in helpers.PARAMS}
 
 
 def _scene(gpu):
@@ -89,7 +93,7 @@ def test_captured_step_replays_match_eager(gpu, path):
         assert float(loss_g) == float(loss_e), (path, i)
         assert torch.equal(disp_g, disp_e), (path, i)
         for k in helpers.PARAMS:
-            assert helpers.rel_l2(b[k].grad, e[k].grad) <= 1e-5, (path, i, k)
+            assert helpers.rel_l2(b[k].grad, e[k].grad) <= ORDER_BAR[k], (path, i, k)
         torch.cuda.synchronize()
 
 
@@ -116,4 +120,4 @@ def test_captured_step_reports_outgrown_lists(gpu):
     assert float(loss_g) == float(loss_e)
     assert torch.equal(disp_g, disp_e)
     for k in helpers.PARAMS:
-        assert helpers.rel_l2(b[k].grad, e[k].grad) <= 1e-5, k
+        assert helpers.rel_l2(b[k].grad, e[k].grad) <= ORDER_BAR[k], k
