@@ -1504,31 +1504,34 @@ __device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tile
     const int base = n_tiles / kXcds, rem = n_tiles % kXcds;
     const int first = x * base + min(x, rem), len = base + (x < rem ? 1 : 0);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    // one stable counting sort pass: the code of each element, then the elements
-    // in chunks of kFinishThreads (one per thread), each placed at its code's
-    // running start plus its rank among the chunk's elements of that code
-    auto scan_codes = [&]() {
+    // one stable counting sort pass over `codes` codes (a multiple of kWave, at
+    // most kOrderCodes) of `bits` bits: the count of each code, their exclusive
+    // scan, then the elements in chunks of kFinishThreads (one per thread), each
+    // placed at its code's running start plus its rank among the chunk's
+    // elements of that code
+    auto scan_codes = [&](int codes) {
         if (threadIdx.x < kWave) {  // exclusive scan of the counts by one wave
+            const int per = codes / kWave;
             uint32_t c[kOrderCodes / kWave], run = 0;
 #pragma unroll
             for (int e = 0; e < kOrderCodes / kWave; ++e) {
-                c[e] = start_of[lane * (kOrderCodes / kWave) + e];
+                c[e] = e < per ? start_of[lane * per + e] : 0u;
                 run += c[e];
             }
             const uint32_t incl = wave_inclusive_scan(run);
             uint32_t at = incl - run;
 #pragma unroll
             for (int e = 0; e < kOrderCodes / kWave; ++e) {
-                start_of[lane * (kOrderCodes / kWave) + e] = at;
+                if (e < per) start_of[lane * per + e] = at;
                 at += c[e];
             }
         }
     };
     // places one element per thread (valid ones), returns its position (or 0)
-    auto place = [&](bool valid, uint32_t d) -> uint32_t {
-        for (int dd = lane; dd < kOrderCodes; dd += kWave) wave_cnt[wave][dd] = 0u;
+    auto place = [&](bool valid, uint32_t d, int codes, int bits) -> uint32_t {
+        for (int dd = lane; dd < codes; dd += kWave) wave_cnt[wave][dd] = 0u;
         __syncthreads();
-        const uint64_t peers = match_digit(d, 9, __ballot(valid));
+        const uint64_t peers = match_digit(d, bits, __ballot(valid));
         if (valid && (peers & lanemask_lt()) == 0) wave_cnt[wave][d] = (uint32_t)__popcll(peers);
         __syncthreads();
         uint32_t pos = 0;
@@ -1537,7 +1540,7 @@ __device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tile
             for (int w = 0; w < wave; ++w) pos += wave_cnt[w][d];
         }
         __syncthreads();
-        for (int dd = threadIdx.x; dd < kOrderCodes; dd += kFinishThreads) {
+        for (int dd = threadIdx.x; dd < codes; dd += kFinishThreads) {
             uint32_t c = 0;
 #pragma unroll
             for (int w = 0; w < kFinishWaves; ++w) c += wave_cnt[w][dd];
@@ -1553,35 +1556,38 @@ __device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tile
     for (int i = threadIdx.x; i < len; i += kFinishThreads)
         atomicAdd(&start_of[order_code(cost[first + i])], 1u);
     __syncthreads();
-    scan_codes();
+    scan_codes(kOrderCodes);
     for (int c0 = 0; c0 < len; c0 += kFinishThreads) {
         const int i = c0 + (int)threadIdx.x;
         const bool valid = i < len;
         const uint32_t d = valid ? order_code(cost[first + i]) : 0u;
-        const uint32_t pos = place(valid, d);
+        const uint32_t pos = place(valid, d, kOrderCodes, 9);
         if (valid) order[first + (int)pos] = first + i;
     }
     if (!ck.count) return;
 
-    // the segments by descending work: segment q of tile t is worked from
-    // checkpoint q - 1 (or the start) to checkpoint q (or the end)
+    // the segments by descending work (a coarser code, 4 steps per octave: the
+    // sort is one of kSegments rounds per chunk): segment q of tile t is worked
+    // from checkpoint q - 1 (or the start) to checkpoint q (or the end)
     auto segment_work = [&](int t, int q, int c) -> uint32_t {
         const uint32_t before = q > 0 ? ck.work[t * kCheckpoints + q - 1] : 0u;
         const uint32_t upto = q < c ? ck.work[t * kCheckpoints + q] : cost[t];
         return upto > before ? upto - before : 1u;
     };
     __syncthreads();
-    for (int d = threadIdx.x; d < kOrderCodes; d += kFinishThreads) start_of[d] = 0u;
+    constexpr int kSegCodes = kOrderCodes / 4;
+    auto seg_code = [&](int t, int q, int c) { return order_code(segment_work(t, q, c)) >> 2; };
+    for (int d = threadIdx.x; d < kSegCodes; d += kFinishThreads) start_of[d] = 0u;
     __syncthreads();
     uint32_t mine = 0;
     for (int i = threadIdx.x; i < len; i += kFinishThreads) {
         const int t = first + i;
         const int c = min(max(ck.count[t], 0), kCheckpoints);
-        for (int q = 0; q <= c; ++q) atomicAdd(&start_of[order_code(segment_work(t, q, c))], 1u);
+        for (int q = 0; q <= c; ++q) atomicAdd(&start_of[seg_code(t, q, c)], 1u);
         mine += (uint32_t)c + 1u;
     }
     __syncthreads();
-    scan_codes();
+    scan_codes(kSegCodes);
     int32_t *items = ck.items + 4 * (int64_t)first;
     for (int c0 = 0; c0 < len; c0 += kFinishThreads) {
         const int i = c0 + (int)threadIdx.x;
@@ -1589,8 +1595,8 @@ __device__ void order_range(int x, const uint32_t *__restrict__ cost, int n_tile
         const int c = i < len ? min(max(ck.count[t], 0), kCheckpoints) : -1;
         for (int q = 0; q < kSegments; ++q) {  // the chunk's q-th segments, one per tile
             const bool valid = q <= c;
-            const uint32_t d = valid ? order_code(segment_work(t, q, c)) : 0u;
-            const uint32_t pos = place(valid, d);
+            const uint32_t d = valid ? (uint32_t)seg_code(t, q, c) : 0u;
+            const uint32_t pos = place(valid, d, kSegCodes, 7);
             if (valid) items[pos] = t * kSegments + q;
         }
     }
