@@ -1030,8 +1030,9 @@ def main(argv=None):
                     help="3 (headline, default) or 1; 2 prints only the 8-camera step, 4 only "
                          "the forward-only sort and blend rates, 5 only the training stress run")
     ap.add_argument("--profile-step", action="store_true",
-                    help="only run warmup + steps fused steps of the chosen configuration (for "
-                         "rocprofv3: every dispatch then belongs to a step) and print the count")
+                    help="only run warmup + steps fused steps of the chosen configuration's first "
+                         "view (for rocprofv3: every dispatch then belongs to a step) and print "
+                         "the count")
     ap.add_argument("--profile-ssim", action="store_true",
                     help="only run warmup + steps SSIM loss terms (forward and backward) at the "
                          "chosen configuration's resolution (for rocprofv3 counter runs)")
@@ -1066,6 +1067,10 @@ def main(argv=None):
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
 
+    if args.profile_step:  # any configuration: its first view
+        return profile_step(CONFIGS[args.config](), args.steps + args.warmup)
+    if args.profile_ssim:
+        return profile_ssim(CONFIGS[args.config](), args.steps + args.warmup)
     if args.config == 5:
         print(json.dumps(train_stress(args.train_steps, args.train_path)), flush=True)
         return 0
@@ -1077,10 +1082,6 @@ def main(argv=None):
         return 0
 
     scene = CONFIGS[args.config]()
-    if args.profile_step:
-        return profile_step(scene, args.steps + args.warmup)
-    if args.profile_ssim:
-        return profile_ssim(scene, args.steps + args.warmup)
     res = run_gpu(scene, args.steps, args.warmup, args.path)
     rl = roofline(res, scene["name"])
     drop_in = None
