@@ -6,7 +6,9 @@ time, more than the GPU spends on many of them.  CapturedStep records a step
 (any callable that renders through `render_l1` or the drop-in `render()` and
 calls backward, e.g. the body of scripts/train.py:133-227's loop without the
 optimizer's host logic) into one HIP graph (torch.cuda.CUDAGraph) and replays it
-with one launch.
+with one launch.  ConcurrentSteps replays several such graphs -- the
+independent views of one step -- on several streams at once, so that one
+view's short launches and tail overlap another's blend.
 
 What the capture fixes, and what each replay must therefore keep:
   * tensor addresses: the inputs the step reads (parameters, camera, target)
@@ -73,3 +75,56 @@ class CapturedStep:
     def ok(self) -> bool:
         torch.cuda.current_stream().synchronize()
         return all(c.replayed_ok() for c in self.checks)
+
+
+class ConcurrentSteps:
+    """Independent parts of one step -- e.g. the cameras of a multi-view batch --
+    each captured into its own HIP graph (CapturedStep) and replayed concurrently
+    on `streams` HIP streams of default priority; a further graph sums their
+    outputs on the caller's stream.
+
+    Each callable in `fns` returns a tuple of tensors of the same shapes (e.g. a
+    view's weighted loss followed by torch.autograd.grad of it with respect to the
+    parameters).  The parts must not write shared tensors: compute gradients with
+    torch.autograd.grad, not .backward() into shared .grad fields.  replay() queues
+    everything on the current stream's timeline and returns the summed tuple
+    (tensors rewritten by every replay); the sum adds the parts in `fns` order, so
+    it equals the sequential accumulation up to float summation order.  ok()
+    synchronises and checks every part's capped sorts, as CapturedStep.ok()."""
+
+    def __init__(self, fns, streams: int = 4, warmup: int = 2):
+        if not fns:
+            raise ValueError("ConcurrentSteps: no parts")
+        if streams < 1:
+            raise ValueError("ConcurrentSteps: streams must be >= 1")
+        self.parts = [CapturedStep(f, warmup=warmup) for f in fns]
+        outs = [p.output for p in self.parts]
+        if any(not isinstance(o, tuple) or len(o) != len(outs[0]) for o in outs):
+            raise ValueError("ConcurrentSteps: every part must return a tuple of the same length")
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self.streams = [torch.cuda.Stream(device=dev) for _ in range(streams)]
+
+        def total():
+            acc = [t.clone() for t in outs[0]]
+            for o in outs[1:]:
+                torch._foreach_add_(acc, list(o))
+            return tuple(acc)
+
+        self._sum = CapturedStep(total, warmup=1)
+        self.output = self._sum.output
+
+    def replay(self):
+        main = torch.cuda.current_stream()
+        for s in self.streams:
+            s.wait_stream(main)
+        for i, part in enumerate(self.parts):
+            with torch.cuda.stream(self.streams[i % len(self.streams)]):
+                part.replay()
+        for s in self.streams:
+            main.wait_stream(s)
+        self._sum.replay()
+        return self.output
+
+    def ok(self) -> bool:
+        torch.cuda.current_stream().synchronize()
+        return all(all(c.replayed_ok() for c in p.checks) for p in self.parts)

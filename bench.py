@@ -422,10 +422,47 @@ def run_cameras(scene: dict, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     n = scene["params"]["means"].shape[0]
+    params = [leaves[k] for k in ("means", "log_scales", "quats_raw", "opacity_logits",
+                                  "sh_dc", "sh_rest")]
+
+    def view(cam, target):  # one camera's weighted loss and its parameter gradients
+        def f():
+            loss, _, _, _ = render_l1(cam["w2c"], cam["K"], cam["width"], cam["height"], *params,
+                                      target, near_plane=cam["near"])
+            return (loss.detach() * weight,) + tuple(torch.autograd.grad(loss * weight, params))
+        return f
+
     return {"ms_per_step": round(ms, 4), "cameras": len(cams),
             "gaussians_per_s": round(n / (ms * 1e-3), 1), "loss": round(float(loss), 6),
             "device_busy": busy(device_time(step, steps), ms),
-            "graph": run_graph(step, steps, warmup, float(loss))}
+            "graph": run_graph(step, steps, warmup, float(loss)),
+            "graph_views": run_views([view(c, t) for c, t in zip(cams, targets)], steps, warmup,
+                                     float(loss))}
+
+
+def run_views(fns, steps: int, warmup: int, eager_loss: float, streams: int = 4) -> dict:
+    """The cameras of one step each captured into a HIP graph and replayed on
+    `streams` streams at once (cuda_rasterizer.graphs.ConcurrentSteps), their losses
+    and gradients summed by a further graph: wall clock over `steps` replays after
+    `warmup`, then the capacity check and the loss against the eager step's."""
+    from cuda_rasterizer.graphs import ConcurrentSteps
+
+    views = ConcurrentSteps(fns, streams=streams, warmup=max(warmup, 1))
+    for _ in range(warmup):
+        views.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = views.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    if not views.ok():
+        raise RuntimeError("bench: a replay's tile lists outgrew the captured capacities")
+    loss = float(out[0])
+    if abs(loss - eager_loss) > 1e-5 * abs(eager_loss):
+        raise RuntimeError(f"bench: concurrent replay loss {loss} != eager loss {eager_loss}")
+    return {"ms_per_step": round(ms, 4), "streams": streams, "loss": round(loss, 6),
+            "device_busy": busy(device_time(views.replay, steps), ms)}
 
 
 def run_graph(step, steps: int, warmup: int, eager_loss: float) -> dict:
