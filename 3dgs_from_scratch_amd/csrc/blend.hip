@@ -193,6 +193,7 @@ struct BatchLds {
     int wave_bad[W];          //   non-finite (the batch then takes the select-based path)
     int wave_flag[W];         // W > 1: per-wave votes of the batch loops (tile_any)
     int wave_flag_once[W];    // W > 1: the backward's one vote before its loop
+    uint32_t wave_work[W];    // W > 1: each wave's work so far, summed at a checkpoint
 };
 
 // Records whose log2 opacity is not finite -- opacity <= 0, +inf or NaN -- are
@@ -656,10 +657,20 @@ __device__ __forceinline__ void blend_accumulate(
     const bool counter = W == 1 || tile_wave() == 0;
     int batch = 0, saved = 0;
     for (int32_t b0 = span.start; b0 < span.end; b0 += kBatch * W, ++batch) {
+        // with W > 1 waves, each one's work joins the vote's barrier, so that a
+        // checkpoint records the tile's work so far, not wave 0's
+        const bool ck_now = ck.data && batch > 0 && batch % checkpoint_spacing<W>() == 0 &&
+                            saved < kCheckpoints;
+        if (W > 1 && ck_now && threadIdx.x % kWave == 0) s.wave_work[tile_wave()] = work;
         if (!tile_any<W>(any_active(T, T_thr), s.wave_flag)) break;
-        if (ck.data && batch > 0 && batch % checkpoint_spacing<W>() == 0 &&
-            saved < kCheckpoints) {
-            save_checkpoint<W>(ck, tile, saved, b0, work, T, cr, cg, cb);
+        if (ck_now) {
+            uint32_t tile_work = work;
+            if constexpr (W > 1) {
+                tile_work = 0;
+#pragma unroll
+                for (int w = 0; w < W; ++w) tile_work += s.wave_work[w];
+            }
+            save_checkpoint<W>(ck, tile, saved, b0, tile_work, T, cr, cg, cb);
             ++saved;
         }
         const Staged st = pipe.advance(s, b0, span, ids, n, points, conics, opac, colors, chi,
@@ -1333,14 +1344,23 @@ static int check_blend_args(const int32_t *indexing_offset, const int32_t *ids, 
 // 256 tiles 101/155 -> 86/118 -> 73/88; 2500 tiles 140/193 -> 138/247 ->
 // 149/352; 3600 tiles 160/210 -> 146/229 -> 152/329; 8160 tiles 159/238 ->
 // 173/396 -> 202/712.
-// Two waves gain only in the 3600-tile forward and lose in every backward, so
-// the default is 4 waves up to kFourWaveTiles tiles and 1 above.
+// Two waves gain in the forward on mid-size grids and lose in every backward, so
+// the backward takes 4 waves up to kFourWaveTiles tiles and 1 above, the forward
+// also 2 up to kCheckpointMaxTiles tiles (the forward's checkpoints and the
+// backward's segments do not depend on either's wave count).  Per-tile timing of
+// the forward with checkpoints (kernel span, us, 1 -> 2 waves): 3600 tiles
+// 161.9 -> 140.9, 2500 tiles 129.7 -> 125.6.
 constexpr int kFourWaveTiles = 1024;
 static int g_blend_waves = 0;  // gs_set_blend_waves: 0 = by tile count
 
 static int blend_waves(int32_t n_tiles) {
     if (g_blend_waves) return g_blend_waves;
     return n_tiles <= kFourWaveTiles ? 4 : 1;
+}
+
+static int blend_waves_forward(int32_t n_tiles) {
+    if (g_blend_waves) return g_blend_waves;
+    return n_tiles <= kFourWaveTiles ? 4 : (n_tiles <= kCheckpointMaxTiles ? 2 : 1);
 }
 
 static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussian_ids_sorted,
@@ -1382,7 +1402,7 @@ static int rasterize_impl(const int32_t *indexing_offset, const int32_t *gaussia
     if (k > 0 && (!points_image || !cov_inv_image || !opacities || !colors))
         return GS_ERR_INVALID_ARGUMENT;
     if (tile_size == kTile) {
-        const int W = blend_waves(n_tiles);
+        const int W = blend_waves_forward(n_tiles);
         auto kern = W == 4 ? blend_forward_kernel<4>
                     : W == 2 ? blend_forward_kernel<2>
                              : blend_forward_kernel<1>;

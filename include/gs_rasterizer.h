@@ -232,7 +232,8 @@ int gs_bin_sort_capped(const float *points_image, const float *radii, const floa
 /*
  * Waves per 16x16 tile of the blend kernels (every gs_rasterize* entry with
  * tile_size 16): 0, the default, picks by the tile count (4 waves for grids of
- * at most 1024 tiles, else 1); 1, 2 or 4 force that count.  With
+ * at most 1024 tiles; above that 1, except the forward entries, which take 2
+ * up to 6144 tiles); 1, 2 or 4 force that count.  With
  * W waves, wave w composites strips w * 4/W .. of the tile's four 16x4 strips
  * and the waves share each staged batch.  Images are bit-equal for every
  * setting; gradients and the per-tile loss sums differ only in float summation
