@@ -58,7 +58,7 @@ extern "C" const char *gs_status_string(int status) {
     }
 }
 
-extern "C" int gs_abi_version(void) { return 19; }
+extern "C" int gs_abi_version(void) { return 20; }
 
 extern "C" int gs_host_device_pointer(void *host, void **device) {
     if (!host || !device) return GS_ERR_INVALID_ARGUMENT;

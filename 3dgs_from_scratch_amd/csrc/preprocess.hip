@@ -180,41 +180,113 @@ __device__ __forceinline__ float sh_render_value(float raw) {
     return v < 0.0f ? 0.0f : v;
 }
 
-// Gradient of the raw colour g (3 channels) into one Gaussian's SH row: the
-// row `lrest` (15 x 3, read in full first) is overwritten with its gradient,
-// gdc receives the DC gradient and gm the gradient of the mean through the
-// view direction (dir = d / |d| -> (I - dir dir^T) / |d|).
-__device__ __forceinline__ void sh_backward_row(const ShView &v, const float (&g)[3], float *lrest,
-                                                float (&gdc)[3], float (&gm)[3]) {
+// d raw_c / d mean for the three channels, through the view direction:
+// m[c] = (J_c - dir (dir . J_c)) / |d| with J_c = sum_k rest_kc d b_k / d dir
+// (dir = d / |d| has the Jacobian (I - dir dir^T) / |d|).  `rest`: 15 x 3.
+// Every path that needs the means' colour gradient forms it from these rows
+// (sh_mean_grad), in the forward's cache or in the backward, so that the
+// cached and the uncached backward agree bit for bit.
+// Basis functions whose derivative along x, y or z is identically zero (bit k):
+// their terms are left out of J (they would add r * 0).
+constexpr uint32_t kShZeroDx = (1u << 0) | (1u << 1) | (1u << 4) | (1u << 5);
+constexpr uint32_t kShZeroDy = (1u << 1) | (1u << 2) | (1u << 5) | (1u << 6);
+constexpr uint32_t kShZeroDz = (1u << 0) | (1u << 2) | (1u << 3) | (1u << 7) | (1u << 8) |
+                               (1u << 14);
+
+__device__ __forceinline__ void sh_mean_rows(const ShView &v, const float *rest,
+                                             float (&m)[3][3]) {
     float bx[15], by[15], bz[15];
     sh_basis_rest_grad(v.x, v.y, v.z, bx, by, bz);
 #pragma unroll
-    for (int c = 0; c < 3; ++c) gdc[c] = kShC0 * g[c];
-    float gdx = 0.f, gdy = 0.f, gdz = 0.f;
+    for (int c = 0; c < 3; ++c) {
+        float jx = 0.f, jy = 0.f, jz = 0.f;
 #pragma unroll
-    for (int k = 0; k < 15; ++k) {
-        const float gk = g[0] * lrest[3 * k] + g[1] * lrest[3 * k + 1] + g[2] * lrest[3 * k + 2];
-        gdx += gk * bx[k];
-        gdy += gk * by[k];
-        gdz += gk * bz[k];
+        for (int k = 0; k < 15; ++k) {
+            const float r = rest[3 * k + c];
+            if (!((kShZeroDx >> k) & 1u)) jx += r * bx[k];
+            if (!((kShZeroDy >> k) & 1u)) jy += r * by[k];
+            if (!((kShZeroDz >> k) & 1u)) jz += r * bz[k];
+        }
+        const float dot = v.x * jx + v.y * jy + v.z * jz;
+        m[c][0] = (jx - v.x * dot) / v.norm;
+        m[c][1] = (jy - v.y * dot) / v.norm;
+        m[c][2] = (jz - v.z * dot) / v.norm;
     }
+}
+
+// The means gradient of the colour gradient g: sum_c g_c m[c].
+__device__ __forceinline__ void sh_mean_grad(const float (&m)[3][3], const float (&g)[3],
+                                             float (&gm)[3]) {
+#pragma unroll
+    for (int d = 0; d < 3; ++d) gm[d] = g[0] * m[0][d] + g[1] * m[1][d] + g[2] * m[2][d];
+}
+
+// Gradient of the raw colour g (3 channels) into one Gaussian's SH row: the
+// row `lrest` (15 x 3, read in full first) is overwritten with its gradient
+// b_k g_c, gdc receives the DC gradient and gm the gradient of the mean through
+// the view direction.
+__device__ __forceinline__ void sh_backward_row(const ShView &v, const float (&g)[3], float *lrest,
+                                                float (&gdc)[3], float (&gm)[3]) {
+    float m[3][3];
+    sh_mean_rows(v, lrest, m);
+    sh_mean_grad(m, g, gm);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) gdc[c] = kShC0 * g[c];
 #pragma unroll
     for (int k = 0; k < 15; ++k) {
         lrest[3 * k] = v.b[k] * g[0];
         lrest[3 * k + 1] = v.b[k] * g[1];
         lrest[3 * k + 2] = v.b[k] * g[2];
     }
-    const float dot = v.x * gdx + v.y * gdy + v.z * gdz;
-    gm[0] = (gdx - v.x * dot) / v.norm;
-    gm[1] = (gdy - v.y * dot) / v.norm;
-    gm[2] = (gdz - v.z * dot) / v.norm;
+}
+
+// Colour-gradient cache of one Gaussian, written where the forward computes its
+// render() colour so that the backward need not read the 45-float SH row again:
+// kShCache floats per Gaussian (rows 8-byte aligned), [0, 9) the rows m of
+// sh_mean_rows, [9] the clamp's pass bits as a uint32 (bit c set where
+// raw_c + 0.5 >= 0, the condition under which max(raw_c + 0.5, 0) passes the
+// gradient).  Rows of Gaussians outside the mask are not written.
+constexpr int kShCache = 10;
+
+__device__ __forceinline__ uint32_t sh_pass_bits(const float (&raw)[3]) {
+    return (raw[0] + 0.5f >= 0.0f ? 1u : 0u) | (raw[1] + 0.5f >= 0.0f ? 2u : 0u) |
+           (raw[2] + 0.5f >= 0.0f ? 4u : 0u);
+}
+
+__device__ __forceinline__ void sh_cache_store(float *__restrict__ cache, int64_t i,
+                                               const ShView &v, const float *rest,
+                                               const float (&raw)[3]) {
+    float m[3][3];
+    sh_mean_rows(v, rest, m);
+    float2 *row = reinterpret_cast<float2 *>(cache + kShCache * i);
+    row[0] = make_float2(m[0][0], m[0][1]);
+    row[1] = make_float2(m[0][2], m[1][0]);
+    row[2] = make_float2(m[1][1], m[1][2]);
+    row[3] = make_float2(m[2][0], m[2][1]);
+    row[4] = make_float2(m[2][2], __uint_as_float(sh_pass_bits(raw)));  // bits moved, never computed on
+}
+
+__device__ __forceinline__ uint32_t sh_cache_load(const float *__restrict__ cache, int64_t i,
+                                                  float (&m)[3][3]) {
+    const float2 *row = reinterpret_cast<const float2 *>(cache + kShCache * i);
+    const float2 r0 = row[0], r1 = row[1], r2 = row[2], r3 = row[3], r4 = row[4];
+    m[0][0] = r0.x;
+    m[0][1] = r0.y;
+    m[0][2] = r1.x;
+    m[1][0] = r1.y;
+    m[1][1] = r2.x;
+    m[1][2] = r2.y;
+    m[2][0] = r3.x;
+    m[2][1] = r3.y;
+    m[2][2] = r4.x;
+    return __float_as_uint(r4.y);
 }
 
 __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(
     int64_t n, const float *__restrict__ cam_pos, const float *__restrict__ w2c,
     const float *__restrict__ means, const float *__restrict__ sh_dc,
     const float *__restrict__ sh_rest, const uint8_t *__restrict__ mask, int mode,
-    float *__restrict__ colors) {
+    float *__restrict__ colors, float *__restrict__ cache) {
     // one Gaussian per thread; a grid smaller than that walks the rest in strides
     for (int64_t i = (int64_t)blockIdx.x * kShBlock + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * kShBlock) {
@@ -226,6 +298,7 @@ __global__ __launch_bounds__(kShBlock) void sh_forward_kernel(
             const float *rest = sh_rest + kRest * i;  // 15 x 12-byte loads per thread
 #pragma unroll
             for (int c = 0; c < 3; ++c) rgb[c] = sh_raw_channel(v, sh_dc + 3 * i, rest, c);
+            if (cache) sh_cache_store(cache, i, v, rest, rgb);  // kShRender only
         }
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
@@ -404,7 +477,7 @@ __global__ __launch_bounds__(kShBlock) void preprocess_forward_kernel(
     int height, float *__restrict__ points_image, float *__restrict__ depths,
     float *__restrict__ cov_image, float *__restrict__ cov_inv_image,
     float *__restrict__ radii, uint8_t *__restrict__ mask, float *__restrict__ opacities,
-    float *__restrict__ colors) {
+    float *__restrict__ colors, float *__restrict__ sh_cache) {
     const int64_t i = (int64_t)blockIdx.x * kShBlock + threadIdx.x;
     if (i >= n) return;
     const Activated a = activate_one(log_scales, quats_raw, logits, i);
@@ -435,6 +508,7 @@ __global__ __launch_bounds__(kShBlock) void preprocess_forward_kernel(
         const float *rest = sh_rest + kRest * i;
 #pragma unroll
         for (int c = 0; c < 3; ++c) rgb[c] = sh_raw_channel(v, sh_dc + 3 * i, rest, c);
+        if (sh_cache) sh_cache_store(sh_cache, i, v, rest, rgb);
     }
 #pragma unroll
     for (int c = 0; c < 3; ++c) colors[3 * i + c] = sh_render_value(rgb[c]);
@@ -446,7 +520,14 @@ __global__ __launch_bounds__(kShBlock) void preprocess_forward_kernel(
 // hold those; logits, grad_opac and grad_logits are unused) -- and the
 // gradients of project_points_backward plus evaluate_sh_render_backward, the
 // means' two terms summed.
-template <bool kRaw>
+// kCached: sh_cache holds the forward's colour-gradient cache (kShCache floats
+// per Gaussian) and sh_dc / sh_rest are not read; LDS then holds each
+// Gaussian's 15 basis values and masked colour gradient, the factors of its
+// SH-rest gradient row, and the rows are written from them with coalesced
+// 12-byte stores (10 KB of LDS per block instead of the 23 KB of staged rows).
+constexpr int kBasisStride = 16;  // LDS floats per Gaussian's basis values (15 used)
+
+template <bool kRaw, bool kCached>
 __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
     int64_t n, const float *__restrict__ grad_points_image,
     const float *__restrict__ grad_cov_inv, const float *__restrict__ grad_opac,
@@ -458,17 +539,22 @@ __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
     const float *__restrict__ K, int width, int height, float *__restrict__ grad_means,
     float *__restrict__ grad_log_scales, float *__restrict__ grad_quats_raw,
     float *__restrict__ grad_logits, float *__restrict__ grad_dc,
-    float *__restrict__ grad_rest) {
-    __shared__ __align__(16) float rest_lds[kShBlock * kRest];
+    float *__restrict__ grad_rest, const float *__restrict__ sh_cache) {
+    constexpr int kLds = kCached ? kShBlock * (kBasisStride + 4) : kShBlock * kRest;
+    __shared__ __align__(16) float lds[kLds];
     __shared__ uint8_t keep[kShBlock];
     const int64_t first = (int64_t)blockIdx.x * kShBlock;
     const int nb = (int)min((int64_t)kShBlock, n - first);
-    keep[threadIdx.x] = threadIdx.x < nb ? mask[first + threadIdx.x] : 0;
-    __syncthreads();
-    block_copy<true>(rest_lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb, keep);
-    __syncthreads();
     const int t = threadIdx.x;
-    float *lrest = rest_lds + kRest * t;
+    if constexpr (!kCached) {
+        keep[t] = t < nb ? mask[first + t] : 0;
+        __syncthreads();
+        block_copy<true>(lds, const_cast<float *>(sh_rest) + kRest * first, kRest * nb, keep);
+        __syncthreads();
+    }
+    float *lrest = lds + kRest * t;                                // !kCached: the row
+    float *lbasis = lds + kBasisStride * t;                        // kCached: b_0..b_14
+    float *lgrad = lds + kShBlock * kBasisStride + 4 * t;          // kCached: g_0..g_2
     if (t < nb) {
         const int64_t i = first + t;
         Activated a;
@@ -494,13 +580,35 @@ __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
             camera_position(nullptr, w2c, cx, cy, cz);
             const ShView v = sh_view(means + 3 * i, cx, cy, cz);
             float g[3];
+            if constexpr (kCached) {
+                float m[3][3];
+                const uint32_t pass = sh_cache_load(sh_cache, i, m);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                g[c] = grad_colors[3 * i + c];
-                const float raw = sh_raw_channel(v, sh_dc + 3 * i, lrest, c);
-                if (!(raw + 0.5f >= 0.0f)) g[c] = 0.0f;
+                for (int c = 0; c < 3; ++c) {
+                    g[c] = grad_colors[3 * i + c];
+                    if (!((pass >> c) & 1u)) g[c] = 0.0f;
+                }
+                sh_mean_grad(m, g, gm);
+#pragma unroll
+                for (int c = 0; c < 3; ++c) gdc[c] = kShC0 * g[c];
+#pragma unroll
+                for (int k = 0; k < 15; ++k) lbasis[k] = v.b[k];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) lgrad[c] = g[c];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    g[c] = grad_colors[3 * i + c];
+                    const float raw = sh_raw_channel(v, sh_dc + 3 * i, lrest, c);
+                    if (!(raw + 0.5f >= 0.0f)) g[c] = 0.0f;
+                }
+                sh_backward_row(v, g, lrest, gdc, gm);
             }
-            sh_backward_row(v, g, lrest, gdc, gm);
+        } else if constexpr (kCached) {  // a zero row: 0 * 0
+#pragma unroll
+            for (int k = 0; k < 15; ++k) lbasis[k] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) lgrad[c] = 0.0f;
         } else {
 #pragma unroll
             for (int k = 0; k < kRest; ++k) lrest[k] = 0.0f;
@@ -532,7 +640,22 @@ __global__ __launch_bounds__(kShBlock) void preprocess_backward_kernel(
         }
     }
     __syncthreads();
-    block_copy<false>(rest_lds, grad_rest + kRest * first, kRest * nb);
+    if constexpr (kCached) {
+        // entry e = 15 t + k of the block is the triple b_k (g_0, g_1, g_2) of
+        // Gaussian t at floats 3e .. 3e + 2 of the block's rows: consecutive
+        // lanes write consecutive 12-byte triples
+        float *out = grad_rest + kRest * first;
+        for (int e = t; e < 15 * nb; e += kShBlock) {
+            const int gt = e / 15, k = e - 15 * gt;
+            const float b = lds[kBasisStride * gt + k];
+            const float *gg = lds + kShBlock * kBasisStride + 4 * gt;
+            out[3 * e] = b * gg[0];
+            out[3 * e + 1] = b * gg[1];
+            out[3 * e + 2] = b * gg[2];
+        }
+    } else {
+        block_copy<false>(lds, grad_rest + kRest * first, kRest * nb);
+    }
 }
 
 }  // namespace gs
@@ -582,18 +705,21 @@ extern "C" int gs_project_points_backward(
 }
 
 // max_blocks > 0 caps the grid (its workgroups then take several Gaussians each).
+// cache: null, or the colour-gradient cache to write (kShRender only).
 static int launch_sh_forward(const float *camera_pos, const float *w2c, const float *means,
                              const float *sh_dc, const float *sh_rest, const uint8_t *mask,
                              int64_t n, int mode, float *colors, hipStream_t stream,
-                             int64_t max_blocks = 0) {
+                             int64_t max_blocks = 0, float *cache = nullptr) {
     if (n < 0 || max_blocks < 0) return GS_ERR_INVALID_ARGUMENT;
     if (n == 0) return GS_OK;
-    if ((!camera_pos && !w2c) || !means || !sh_dc || !sh_rest || !mask || !colors)
+    if ((!camera_pos && !w2c) || !means || !sh_dc || !sh_rest || !mask || !colors ||
+        (cache && mode != kShRender) || (reinterpret_cast<uintptr_t>(cache) & 7))
         return GS_ERR_INVALID_ARGUMENT;
     int64_t blocks = ceil_div(n, kShBlock);
     if (max_blocks > 0 && blocks > max_blocks) blocks = max_blocks;
     hipLaunchKernelGGL(sh_forward_kernel, dim3((unsigned)blocks), dim3(kShBlock), 0,
-                       stream, n, camera_pos, w2c, means, sh_dc, sh_rest, mask, mode, colors);
+                       stream, n, camera_pos, w2c, means, sh_dc, sh_rest, mask, mode, colors,
+                       cache);
     return launch_status();
 }
 
@@ -657,21 +783,36 @@ static int device_cus() {
     return cus[dev];
 }
 
+// The grid of a colour launch beside other work: one workgroup per compute
+// unit (measured at config 3 beside binning: 256 workgroups 0.693 ms per fused
+// step, 192 0.698, 320 0.704, 512 0.697, one per 128 Gaussians 0.714), more
+// when a thread would take over 32 Gaussians.
+static int64_t beside_blocks(int64_t n) {
+    const int cus = device_cus();
+    int64_t blocks = cus > 0 ? cus : 256;
+    const int64_t per32 = (n + 32 * kShBlock - 1) / (32 * kShBlock);
+    return per32 > blocks ? per32 : blocks;
+}
+
 extern "C" int gs_evaluate_sh_render_beside(const float *world_to_camera, const float *means,
                                             const float *sh_dc, const float *sh_rest,
                                             const uint8_t *mask, int64_t n, float *colors,
                                             hipStream_t stream) {
     if (!world_to_camera && n > 0) return GS_ERR_INVALID_ARGUMENT;
     if (n <= 0) return n < 0 ? GS_ERR_INVALID_ARGUMENT : GS_OK;  // no device query
-    // one workgroup per compute unit (measured at config 3 beside binning: 256
-    // workgroups 0.693 ms per fused step, 192 0.698, 320 0.704, 512 0.697, one
-    // per 128 Gaussians 0.714), more when a thread would take over 32 Gaussians
-    const int cus = device_cus();
-    int64_t blocks = cus > 0 ? cus : 256;
-    const int64_t per32 = (n + 32 * kShBlock - 1) / (32 * kShBlock);
-    if (per32 > blocks) blocks = per32;
     return launch_sh_forward(nullptr, world_to_camera, means, sh_dc, sh_rest, mask, n,
-                             kShRender, colors, stream, blocks);
+                             kShRender, colors, stream, beside_blocks(n));
+}
+
+extern "C" int gs_evaluate_sh_render_cache(const float *world_to_camera, const float *means,
+                                           const float *sh_dc, const float *sh_rest,
+                                           const uint8_t *mask, int64_t n, int32_t beside,
+                                           float *colors, float *sh_cache, hipStream_t stream) {
+    if ((!world_to_camera || !sh_cache) && n > 0) return GS_ERR_INVALID_ARGUMENT;
+    if (n <= 0) return n < 0 ? GS_ERR_INVALID_ARGUMENT : GS_OK;  // no device query
+    return launch_sh_forward(nullptr, world_to_camera, means, sh_dc, sh_rest, mask, n,
+                             kShRender, colors, stream, beside ? beside_blocks(n) : 0,
+                             sh_cache);
 }
 
 extern "C" int gs_evaluate_sh_render_backward(const float *grad_colors,
@@ -727,19 +868,20 @@ extern "C" int gs_preprocess_forward(const float *means, const float *log_scales
                                      int32_t width, int32_t height, float *points_image,
                                      float *depths, float *cov_image, float *cov_inv_image,
                                      float *radii, uint8_t *mask, float *opacities,
-                                     float *colors, hipStream_t stream) {
+                                     float *colors, float *sh_cache, hipStream_t stream) {
     if (n < 0 || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
     if (n == 0) return GS_OK;
     if (!means || !log_scales || !quats_raw || !opacity_logits ||
-        (colors && (!sh_dc || !sh_rest)) || !world_to_camera || !intrinsic || !points_image ||
-        !depths || !cov_image || !cov_inv_image || !radii || !mask || !opacities ||
-        (reinterpret_cast<uintptr_t>(quats_raw) & 15))
+        (colors && (!sh_dc || !sh_rest)) || (sh_cache && !colors) || !world_to_camera ||
+        !intrinsic || !points_image || !depths || !cov_image || !cov_inv_image || !radii ||
+        !mask || !opacities || (reinterpret_cast<uintptr_t>(quats_raw) & 15) ||
+        (reinterpret_cast<uintptr_t>(sh_cache) & 7))
         return GS_ERR_INVALID_ARGUMENT;
     hipLaunchKernelGGL(preprocess_forward_kernel, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0,
                        stream, n, means, log_scales, quats_raw, opacity_logits, sh_dc, sh_rest,
                        world_to_camera, intrinsic, near_plane, far_plane, min_opacity,
                        min_radius, max_radius, width, height, points_image, depths, cov_image,
-                       cov_inv_image, radii, mask, opacities, colors);
+                       cov_inv_image, radii, mask, opacities, colors, sh_cache);
     return launch_status();
 }
 
@@ -750,22 +892,25 @@ extern "C" int gs_preprocess_backward(
     const float *sh_dc, const float *sh_rest, const float *cov_image, const uint8_t *mask,
     const float *world_to_camera, const float *intrinsic, int64_t n, int32_t width,
     int32_t height, float *grad_means, float *grad_log_scales, float *grad_quats_raw,
-    float *grad_opacity_logits, float *grad_sh_dc, float *grad_sh_rest, hipStream_t stream) {
+    float *grad_opacity_logits, float *grad_sh_dc, float *grad_sh_rest, const float *sh_cache,
+    hipStream_t stream) {
     if (n < 0 || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
     if (n == 0) return GS_OK;
     if (!grad_points_image || !grad_cov_inv_image || !grad_opacities || !grad_colors || !means ||
-        !log_scales || !quats_raw || !opacity_logits || !sh_dc || !sh_rest || !cov_image ||
-        !mask || !world_to_camera || !intrinsic || !grad_means || !grad_log_scales ||
-        !grad_quats_raw || !grad_opacity_logits || !grad_sh_dc || !grad_sh_rest ||
-        (reinterpret_cast<uintptr_t>(quats_raw) & 15) ||
-        (reinterpret_cast<uintptr_t>(grad_quats_raw) & 15))
+        !log_scales || !quats_raw || !opacity_logits || (!sh_cache && (!sh_dc || !sh_rest)) ||
+        !cov_image || !mask || !world_to_camera || !intrinsic || !grad_means ||
+        !grad_log_scales || !grad_quats_raw || !grad_opacity_logits || !grad_sh_dc ||
+        !grad_sh_rest || (reinterpret_cast<uintptr_t>(quats_raw) & 15) ||
+        (reinterpret_cast<uintptr_t>(grad_quats_raw) & 15) ||
+        (reinterpret_cast<uintptr_t>(sh_cache) & 7))
         return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(preprocess_backward_kernel<true>, dim3(ceil_div(n, kShBlock)),
-                       dim3(kShBlock), 0, stream, n, grad_points_image, grad_cov_inv_image,
-                       grad_opacities, grad_colors, means, log_scales, quats_raw, opacity_logits,
-                       sh_dc, sh_rest, cov_image, mask, world_to_camera, intrinsic, width, height,
-                       grad_means, grad_log_scales, grad_quats_raw, grad_opacity_logits,
-                       grad_sh_dc, grad_sh_rest);
+    auto kern = sh_cache ? preprocess_backward_kernel<true, true>
+                         : preprocess_backward_kernel<true, false>;
+    hipLaunchKernelGGL(kern, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0, stream, n,
+                       grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors, means,
+                       log_scales, quats_raw, opacity_logits, sh_dc, sh_rest, cov_image, mask,
+                       world_to_camera, intrinsic, width, height, grad_means, grad_log_scales,
+                       grad_quats_raw, grad_opacity_logits, grad_sh_dc, grad_sh_rest, sh_cache);
     return launch_status();
 }
 
@@ -775,18 +920,20 @@ extern "C" int gs_render_preprocess_backward(
     const float *sh_rest, const float *cov_image, const uint8_t *mask,
     const float *world_to_camera, const float *intrinsic, int64_t n, int32_t width,
     int32_t height, float *grad_means, float *grad_scales, float *grad_quaternions,
-    float *grad_sh_dc, float *grad_sh_rest, hipStream_t stream) {
+    float *grad_sh_dc, float *grad_sh_rest, const float *sh_cache, hipStream_t stream) {
     if (n < 0 || width <= 0 || height <= 0) return GS_ERR_INVALID_ARGUMENT;
     if (n == 0) return GS_OK;
     if (!grad_points_image || !grad_cov_inv_image || !grad_colors || !means || !scales ||
-        !quaternions || !sh_dc || !sh_rest || !cov_image || !mask || !world_to_camera ||
-        !intrinsic || !grad_means || !grad_scales || !grad_quaternions || !grad_sh_dc ||
-        !grad_sh_rest)
+        !quaternions || (!sh_cache && (!sh_dc || !sh_rest)) || !cov_image || !mask ||
+        !world_to_camera || !intrinsic || !grad_means || !grad_scales || !grad_quaternions ||
+        !grad_sh_dc || !grad_sh_rest || (reinterpret_cast<uintptr_t>(sh_cache) & 7))
         return GS_ERR_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(preprocess_backward_kernel<false>, dim3(ceil_div(n, kShBlock)),
-                       dim3(kShBlock), 0, stream, n, grad_points_image, grad_cov_inv_image,
-                       nullptr, grad_colors, means, scales, quaternions, nullptr, sh_dc, sh_rest,
-                       cov_image, mask, world_to_camera, intrinsic, width, height, grad_means,
-                       grad_scales, grad_quaternions, nullptr, grad_sh_dc, grad_sh_rest);
+    auto kern = sh_cache ? preprocess_backward_kernel<false, true>
+                         : preprocess_backward_kernel<false, false>;
+    hipLaunchKernelGGL(kern, dim3(ceil_div(n, kShBlock)), dim3(kShBlock), 0, stream, n,
+                       grad_points_image, grad_cov_inv_image, nullptr, grad_colors, means, scales,
+                       quaternions, nullptr, sh_dc, sh_rest, cov_image, mask, world_to_camera,
+                       intrinsic, width, height, grad_means, grad_scales, grad_quaternions,
+                       nullptr, grad_sh_dc, grad_sh_rest, sh_cache);
     return launch_status();
 }

@@ -48,6 +48,7 @@ __all__ = [
     "rasterize_backward",
     "rasterize_work",
     "evaluate_spherical_harmonics_render",
+    "sh_cache_empty",
     "evaluate_spherical_harmonics_render_backward",
     "rasterize_display",
     "rasterize_display_backward",
@@ -868,16 +869,39 @@ def sh_render_inputs(world_to_camera, points_world, sh_coeffs_dc, sh_coeffs_rest
             _prep(mask, "mask", torch.bool, (n,), dev))
 
 
+SH_CACHE_FLOATS = 10
+
+
+def sh_cache_empty(n: int, device) -> torch.Tensor:
+    """An uninitialised colour-gradient cache for n Gaussians: (N, 10) float32,
+    written by evaluate_spherical_harmonics_render(sh_cache=...) or
+    preprocess_forward(sh_cache=...) for the Gaussians in their mask."""
+    return torch.empty((n, SH_CACHE_FLOATS), dtype=torch.float32, device=device)
+
+
+def _check_sh_cache(sh_cache, n, dev, who):
+    if (not isinstance(sh_cache, torch.Tensor) or sh_cache.dtype != torch.float32
+            or sh_cache.shape != (n, SH_CACHE_FLOATS) or sh_cache.device != dev
+            or not sh_cache.is_contiguous() or sh_cache.data_ptr() % 8):
+        raise RuntimeError(f"{who}: sh_cache must be a contiguous ({n}, {SH_CACHE_FLOATS}) "
+                           f"float32 tensor on {dev} (sh_cache_empty)")
+    return sh_cache
+
+
 def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs_dc,
                                         sh_coeffs_rest, mask, out=None, beside=False,
-                                        stream=None):
+                                        stream=None, sh_cache=None):
     """max(evaluate_spherical_harmonics(-R^T t, ...) + 0.5, 0) in one kernel
     (src/cuda/wrapper.py:260-265).  Masked rows are 0.5.  out: a contiguous
     (N, 3) float32 tensor to write instead of a new one.  beside: launch it for a
     stream that runs beside other work (gs_evaluate_sh_render_beside: one
     workgroup per compute unit; the same values).  stream: a torch.cuda.Stream
     of the tensors' device to launch on (default: the current stream); the
-    caller orders it against the producers and consumers of the tensors."""
+    caller orders it against the producers and consumers of the tensors.
+    sh_cache: an (N, 10) float32 tensor (sh_cache_empty) that also receives the
+    colour-gradient cache (gs_evaluate_sh_render_cache), which
+    render_preprocess_backward and preprocess_backward take in place of the SH
+    coefficients."""
     dev = _device_of(points_world)
     n = points_world.shape[0]
     f32 = torch.float32
@@ -891,18 +915,22 @@ def evaluate_spherical_harmonics_render(world_to_camera, points_world, sh_coeffs
             raise RuntimeError("evaluate_spherical_harmonics_render: out must be a contiguous "
                                f"({n}, 3) float32 tensor on {dev}")
         colors = out
+    if sh_cache is not None:
+        _check_sh_cache(sh_cache, n, dev, "evaluate_spherical_harmonics_render")
     with torch.cuda.device(dev):
         ev = _lib.timer.record("evaluate_sh_render", dev, stream)
         lib = _lib.load()
-        fn = lib.gs_evaluate_sh_render_beside if beside else lib.gs_evaluate_sh_render
-        _lib.check(
-            fn(
+        launch = _stream(dev) if stream is None else stream.cuda_stream
+        if sh_cache is not None:
+            status = lib.gs_evaluate_sh_render_cache(
                 _ptr(world_to_camera), _ptr(points_world), _ptr(sh_coeffs_dc),
-                _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(colors),
-                _stream(dev) if stream is None else stream.cuda_stream,
-            ),
-            "evaluate_spherical_harmonics_render",
-        )
+                _ptr(sh_coeffs_rest), _ptr(mask), n, 1 if beside else 0, _ptr(colors),
+                _ptr(sh_cache), launch)
+        else:
+            fn = lib.gs_evaluate_sh_render_beside if beside else lib.gs_evaluate_sh_render
+            status = fn(_ptr(world_to_camera), _ptr(points_world), _ptr(sh_coeffs_dc),
+                        _ptr(sh_coeffs_rest), _ptr(mask), n, _ptr(colors), launch)
+        _lib.check(status, "evaluate_spherical_harmonics_render")
         _lib.timer.stop(ev, dev, stream)
     return colors
 
@@ -1063,11 +1091,14 @@ def activate_backward(grad_scales, grad_quats, grad_opacities, scales, quats_raw
 
 def preprocess_forward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
                        sh_coeffs_rest, world_to_camera, intrinsic, near_plane, far_plane,
-                       min_opacity, min_radius, max_radius, width, height, with_colors=True):
+                       min_opacity, min_radius, max_radius, width, height, with_colors=True,
+                       sh_cache=None):
     """activate -> project_points -> evaluate_spherical_harmonics_render in one kernel
     (gs_preprocess_forward).  Returns (points_image, depths, cov_image, cov_inv_image,
     radii, mask, opacities, colors); with_colors=False skips the colours (None;
-    evaluate_spherical_harmonics_render gives the same values)."""
+    evaluate_spherical_harmonics_render gives the same values).  sh_cache (with
+    the colours): an (N, 10) float32 tensor (sh_cache_empty) that also receives
+    the colour-gradient cache for preprocess_backward."""
     dev = _device_of(means)
     n = means.shape[0]
     f32 = torch.float32
@@ -1080,6 +1111,10 @@ def preprocess_forward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_d
         dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
         rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
         colors = torch.empty((n, 3), dtype=f32, device=dev)
+    if sh_cache is not None:
+        if not with_colors:
+            raise RuntimeError("preprocess_forward: sh_cache is written with the colours only")
+        _check_sh_cache(sh_cache, n, dev, "preprocess_forward")
     world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
     intrinsic = _prep(intrinsic, "intrinsic", f32, (3, 3), dev)
     out = [torch.empty(shape, dtype=f32, device=dev)
@@ -1093,18 +1128,30 @@ def preprocess_forward(means, log_scales, quats_raw, opacity_logits, sh_coeffs_d
             _ptr(rest), _ptr(world_to_camera), _ptr(intrinsic), n, float(near_plane),
             float(far_plane), float(min_opacity), float(min_radius), float(max_radius), int(width),
             int(height), *[_ptr(t) for t in out], _ptr(mask), _ptr(opac), _ptr(colors),
-            _stream(dev)), "preprocess_forward")
+            _ptr(sh_cache), _stream(dev)), "preprocess_forward")
         _lib.timer.stop(ev, dev)
     return (*out, mask, opac, colors)
+
+
+def _sh_or_cache(sh_coeffs_dc, sh_coeffs_rest, sh_cache, n, dev, who):
+    """The SH coefficients a backward reads, or (None, None) with a valid cache."""
+    if sh_cache is not None:
+        _check_sh_cache(sh_cache, n, dev, who)
+        return None, None
+    f32 = torch.float32
+    return (_prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev),
+            _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev))
 
 
 def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, grad_colors,
                         means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc,
                         sh_coeffs_rest, cov_image, mask, world_to_camera, intrinsic, width,
-                        height):
+                        height, sh_cache=None):
     """Gradients of preprocess_forward's points_image, cov_inv_image, opacities and
     colors w.r.t. the raw parameters (gs_preprocess_backward).  Returns (d means,
-    d log_scales, d quats_raw, d logits, d sh_dc, d sh_rest)."""
+    d log_scales, d quats_raw, d logits, d sh_dc, d sh_rest).  sh_cache: the
+    forward's colour-gradient cache; the SH coefficients are then not read (and
+    may be None), the results are the same bit for bit."""
     dev = _device_of(means)
     n = means.shape[0]
     f32 = torch.float32
@@ -1116,8 +1163,8 @@ def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, g
     log_scales = _prep(log_scales, "log_scales", f32, (n, 3), dev)
     quats_raw = _prep(quats_raw, "quats_raw", f32, (n, 4), dev)
     opacity_logits = _prep(opacity_logits, "opacity_logits", f32, (n,), dev)
-    dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
-    rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    dc, rest = _sh_or_cache(sh_coeffs_dc, sh_coeffs_rest, sh_cache, n, dev,
+                            "preprocess_backward")
     cov_image = _prep(cov_image, "cov_image", f32, (n, 3), dev)
     mask = _prep(mask, "mask", torch.bool, (n,), dev)
     world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
@@ -1130,18 +1177,21 @@ def preprocess_backward(grad_points_image, grad_cov_inv_image, grad_opacities, g
             _ptr(g_pts), _ptr(g_conic), _ptr(g_opac), _ptr(g_col), _ptr(means), _ptr(log_scales),
             _ptr(quats_raw), _ptr(opacity_logits), _ptr(dc), _ptr(rest), _ptr(cov_image),
             _ptr(mask), _ptr(world_to_camera), _ptr(intrinsic), n, int(width), int(height),
-            *[_ptr(t) for t in outs], _stream(dev)), "preprocess_backward")
+            *[_ptr(t) for t in outs], _ptr(sh_cache), _stream(dev)), "preprocess_backward")
         _lib.timer.stop(ev, dev)
     return tuple(outs)
 
 
 def render_preprocess_backward(grad_points_image, grad_cov_inv_image, grad_colors, means, scales,
                                quaternions, sh_coeffs_dc, sh_coeffs_rest, cov_image, mask,
-                               world_to_camera, intrinsic, width, height):
+                               world_to_camera, intrinsic, width, height, sh_cache=None):
     """project_points_backward and evaluate_sh_render_backward in one kernel
     (gs_render_preprocess_backward): gradients of render()'s points_image,
     cov_inv_image and colours w.r.t. (means, scales, quaternions, sh_dc,
-    sh_rest), the means' two terms summed.  Returns those five tensors."""
+    sh_rest), the means' two terms summed.  Returns those five tensors.
+    sh_cache: the colour-gradient cache evaluate_spherical_harmonics_render
+    wrote for the same inputs; the SH coefficients are then not read (and may be
+    None), the results are the same bit for bit."""
     dev = _device_of(means)
     n = means.shape[0]
     f32 = torch.float32
@@ -1151,8 +1201,8 @@ def render_preprocess_backward(grad_points_image, grad_cov_inv_image, grad_color
     means = _prep(means, "means", f32, (n, 3), dev)
     scales = _prep(scales, "scales", f32, (n, 3), dev)
     quaternions = _prep(quaternions, "quaternions", f32, (n, 4), dev)
-    dc = _prep(sh_coeffs_dc, "sh_coeffs_dc", f32, (n, 3), dev)
-    rest = _prep(sh_coeffs_rest, "sh_coeffs_rest", f32, (n, 15, 3), dev)
+    dc, rest = _sh_or_cache(sh_coeffs_dc, sh_coeffs_rest, sh_cache, n, dev,
+                            "render_preprocess_backward")
     cov_image = _prep(cov_image, "cov_image", f32, (n, 3), dev)
     mask = _prep(mask, "mask", torch.bool, (n,), dev)
     world_to_camera = _prep(world_to_camera, "world_to_camera", f32, (4, 4), dev)
@@ -1165,7 +1215,7 @@ def render_preprocess_backward(grad_points_image, grad_cov_inv_image, grad_color
             _ptr(g_pts), _ptr(g_conic), _ptr(g_col), _ptr(means), _ptr(scales),
             _ptr(quaternions), _ptr(dc), _ptr(rest), _ptr(cov_image), _ptr(mask),
             _ptr(world_to_camera), _ptr(intrinsic), n, int(width), int(height),
-            *[_ptr(t) for t in outs], _stream(dev)), "render_preprocess_backward")
+            *[_ptr(t) for t in outs], _ptr(sh_cache), _stream(dev)), "render_preprocess_backward")
         _lib.timer.stop(ev, dev)
     return tuple(outs)
 

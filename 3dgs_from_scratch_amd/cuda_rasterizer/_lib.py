@@ -41,11 +41,12 @@ SIGNATURES = {
     + [_P, _P, _P],
     "gs_evaluate_sh_render": [_P] * 5 + [_I64, _P, _P],
     "gs_evaluate_sh_render_beside": [_P] * 5 + [_I64, _P, _P],
+    "gs_evaluate_sh_render_cache": [_P] * 5 + [_I64, _I32, _P, _P, _P],
     "gs_evaluate_sh_render_backward": [_P] * 6 + [_I64, _I32] + [_P] * 3 + [_P],
     "gs_activate": [_P] * 3 + [_I64] + [_P] * 3 + [_P],
-    "gs_preprocess_forward": [_P] * 8 + [_I64, _F, _F, _F, _F, _F, _I32, _I32] + [_P] * 8 + [_P],
-    "gs_preprocess_backward": [_P] * 14 + [_I64, _I32, _I32] + [_P] * 6 + [_P],
-    "gs_render_preprocess_backward": [_P] * 12 + [_I64, _I32, _I32] + [_P] * 5 + [_P],
+    "gs_preprocess_forward": [_P] * 8 + [_I64, _F, _F, _F, _F, _F, _I32, _I32] + [_P] * 9 + [_P],
+    "gs_preprocess_backward": [_P] * 14 + [_I64, _I32, _I32] + [_P] * 7 + [_P],
+    "gs_render_preprocess_backward": [_P] * 12 + [_I64, _I32, _I32] + [_P] * 6 + [_P],
     "gs_activate_backward": [_P] * 6 + [_I64] + [_P] * 3 + [_P],
     "gs_rasterize_display_l1": [_P, _P, _I32, _I64] + [_P] * 4
     + [_I64, _I32, _I32, _I32, _F, _F, _F] + [_P] * 7 + [_I64, _P, _P],

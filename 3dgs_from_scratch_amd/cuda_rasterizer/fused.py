@@ -11,7 +11,8 @@ same values with the library's kernels only:
             (SH +0.5 and clamp) run on a second stream beside binning, whose
             chain of small launches leaves most of the GPU idle
   backward  blend backward seeded by the L1 gradient -> preprocess backward
-            (projection, SH and activation gradients: one kernel)
+            (projection, SH and activation gradients: one kernel, which reads
+            the colour pass's colour-gradient cache instead of the SH rows)
 
 Values equal the unfused sequence up to floating-point summation order (the
 loss sum and the gradient atomics); tests/test_gpu_fused.py checks both
@@ -70,10 +71,11 @@ class ColorsBeside:
     colours are read, and in a `finally` so that an exception between the fork
     and the join leaves no kernel writing into freed memory."""
 
-    __slots__ = ("colors", "_main", "_join", "_held")
+    __slots__ = ("colors", "sh_cache", "_main", "_join", "_held")
 
-    def __init__(self, colors, main, join, held):
-        self.colors, self._main, self._join, self._held = colors, main, join, held
+    def __init__(self, colors, sh_cache, main, join, held):
+        self.colors, self.sh_cache = colors, sh_cache
+        self._main, self._join, self._held = main, join, held
 
     def wait(self):
         if self._held is not None:
@@ -81,10 +83,12 @@ class ColorsBeside:
             self._held = None
 
 
-def colors_beside(world_to_camera, means, sh_dc, sh_rest, mask) -> ColorsBeside:
+def colors_beside(world_to_camera, means, sh_dc, sh_rest, mask,
+                  with_cache=False) -> ColorsBeside:
     """The render colours max(SH + 0.5, 0) of the Gaussians in `mask`, computed on
     the calling thread's second stream once the current stream has produced
-    `mask`.  Every input is validated and made contiguous on the current stream
+    `mask` (with_cache: and the colour-gradient cache, `sh_cache` of the returned
+    object).  Every input is validated and made contiguous on the current stream
     before the fork, so a copy is ordered before the colour kernel reads it.
     The events are reused: each record comes after the previous wait was queued
     (the returned object's wait())."""
@@ -93,13 +97,14 @@ def colors_beside(world_to_camera, means, sh_dc, sh_rest, mask) -> ColorsBeside:
     w2c, means, sh_dc, sh_rest, mask = _cr.sh_render_inputs(world_to_camera, means, sh_dc,
                                                             sh_rest, mask)
     colors = torch.empty((means.shape[0], 3), dtype=torch.float32, device=dev)
+    cache = _cr.sh_cache_empty(means.shape[0], dev) if with_cache else None
     side, fork, join = _side_stream(dev)
     fork.record(main)
     side.wait_event(fork)
-    pending = ColorsBeside(colors, main, join, (w2c, means, sh_dc, sh_rest, mask))
+    pending = ColorsBeside(colors, cache, main, join, (w2c, means, sh_dc, sh_rest, mask))
     try:
         _cr.evaluate_spherical_harmonics_render(w2c, means, sh_dc, sh_rest, mask, out=colors,
-                                                beside=True, stream=side)
+                                                beside=True, stream=side, sh_cache=cache)
     finally:
         join.record(side)
     return pending
@@ -118,12 +123,15 @@ class RenderL1Function(torch.autograd.Function):
                 transmittance_threshold, chi_squared_threshold, ssim_lambda, ssim_padding,
                 schedule_cache, view_id):
         beside = means.shape[0] >= BESIDE_MIN_GAUSSIANS
+        # the colour pass also writes the colour-gradient cache: the backward then
+        # reads 40 bytes per Gaussian instead of its 180-byte SH row
+        cache = None if beside else _cr.sh_cache_empty(means.shape[0], means.device)
         pts, depths, cov, conic, radii, mask, opac, colors = _cr.preprocess_forward(
             means, log_scales, quats_raw, opacity_logits, sh_coeffs_dc, sh_coeffs_rest,
             world_to_camera, intrinsic, near_plane, far_plane, min_opacity, min_radius,
-            max_radius, width, height, with_colors=not beside)
+            max_radius, width, height, with_colors=not beside, sh_cache=cache)
         pending = colors_beside(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest,
-                                mask) if beside else None
+                                mask, with_cache=True) if beside else None
         check = None
         try:
             # with a launch order for the forward's tiles from the list lengths; sized
@@ -137,7 +145,7 @@ class RenderL1Function(torch.autograd.Function):
         finally:
             if pending is not None:
                 pending.wait()
-                colors = pending.colors
+                colors, cache = pending.colors, pending.sh_cache
         # and, kept per view, the next forward of the same view
         previous = None
         if schedule_cache is not None and view_id is not None:
@@ -177,6 +185,7 @@ class RenderL1Function(torch.autograd.Function):
                               sh_coeffs_rest, world_to_camera, intrinsic, target, opac, pts, cov,
                               conic, mask, colors, off, ids, image, acc, sched, *ssim_saved)
         ctx.ssim_lambda = ssim_lambda
+        ctx.sh_cache = cache  # written by the forward only, read by the backward
         # acc is zeroed once, by the forward launch: only the first backward may add
         # into it (the gradients it returns are views of it)
         ctx.acc_fresh = True
@@ -216,7 +225,7 @@ class RenderL1Function(torch.autograd.Function):
             ctx.densifier.update(g_pts, ctx.radii, width, height)
         g_means, g_ls, g_qr, g_logit, g_dc, g_rest = _cr.preprocess_backward(
             g_pts, g_conic, g_opac, g_col, means, log_scales, quats_raw, logits, dc, rest, cov,
-            mask, w2c, K, width, height)
+            mask, w2c, K, width, height, sh_cache=ctx.sh_cache)
         return (g_means, g_ls, g_qr, g_logit, g_dc, g_rest) + (None,) * 18
 
 

@@ -90,26 +90,31 @@ class RenderPreprocessFunction(torch.autograd.Function):
     second stream, beside binning, when `beside` is a list: it receives the
     fused.ColorsBeside to wait on), the backward one kernel for both
     (render_preprocess_backward), so the means' two gradient terms are summed in
-    it rather than by autograd."""
+    it rather than by autograd.  With `with_cache` the colour kernel also writes
+    the colour-gradient cache (40 bytes per Gaussian), which the backward reads
+    in place of the 180-byte SH rows."""
 
     @staticmethod
     def forward(ctx, means, scales, quaternions, opacities, world_to_camera, intrinsic,
                 sh_coeffs_dc, sh_coeffs_rest, near_plane, far_plane, min_opacity, min_radius,
-                max_radius, width, height, beside=None):
+                max_radius, width, height, beside=None, with_cache=False):
         points_img, depths, cov_img, cov_inv_img, radii, mask = _cr.project_points(
             means, scales, quaternions, opacities, world_to_camera, intrinsic, near_plane,
             far_plane, min_opacity, min_radius, max_radius, width, height)
         if beside is not None:
             from cuda_rasterizer.fused import colors_beside
 
-            pending = colors_beside(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask)
+            pending = colors_beside(world_to_camera, means, sh_coeffs_dc, sh_coeffs_rest, mask,
+                                    with_cache=with_cache)
             beside.append(pending)
-            colors = pending.colors
+            colors, cache = pending.colors, pending.sh_cache
         else:
+            cache = _cr.sh_cache_empty(means.shape[0], means.device) if with_cache else None
             colors = _cr.evaluate_spherical_harmonics_render(world_to_camera, means,
-                                                             sh_coeffs_dc, sh_coeffs_rest, mask)
+                                                             sh_coeffs_dc, sh_coeffs_rest, mask,
+                                                             sh_cache=cache)
         ctx.save_for_backward(means, scales, quaternions, world_to_camera, intrinsic,
-                              sh_coeffs_dc, sh_coeffs_rest, cov_img, mask)
+                              sh_coeffs_dc, sh_coeffs_rest, cov_img, mask, cache)
         ctx.width = width
         ctx.height = height
         ctx.mark_non_differentiable(depths, radii, mask)
@@ -119,9 +124,9 @@ class RenderPreprocessFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_points_img, grad_depths, grad_cov_inv_img, grad_radii, grad_mask,
                  grad_colors):
-        means, scales, quaternions, w2c, K, dc, rest, cov_img, mask = ctx.saved_tensors
+        means, scales, quaternions, w2c, K, dc, rest, cov_img, mask, cache = ctx.saved_tensors
         if grad_points_img is None and grad_cov_inv_img is None and grad_colors is None:
-            return (None,) * 16
+            return (None,) * 17
         n = means.shape[0]
 
         def zeros(w):
@@ -131,8 +136,8 @@ class RenderPreprocessFunction(torch.autograd.Function):
             zeros(2) if grad_points_img is None else grad_points_img,
             zeros(3) if grad_cov_inv_img is None else grad_cov_inv_img,
             zeros(3) if grad_colors is None else grad_colors, means, scales, quaternions, dc,
-            rest, cov_img, mask, w2c, K, ctx.width, ctx.height)
-        return (g_means, g_scales, g_quats, None, None, None, g_dc, g_rest) + (None,) * 8
+            rest, cov_img, mask, w2c, K, ctx.width, ctx.height, sh_cache=cache)
+        return (g_means, g_scales, g_quats, None, None, None, g_dc, g_rest) + (None,) * 9
 
 
 class RenderRasterizeFunction(torch.autograd.Function):
@@ -227,11 +232,12 @@ def render(
     else:  # projection and max(sh + 0.5, 0) as one node (colours beside binning in training)
         from cuda_rasterizer.fused import BESIDE_MIN_GAUSSIANS
 
-        sink = [] if torch.is_grad_enabled() and means.shape[0] >= BESIDE_MIN_GAUSSIANS else None
+        training = torch.is_grad_enabled()
+        sink = [] if training and means.shape[0] >= BESIDE_MIN_GAUSSIANS else None
         points_img, depths, cov_inv_img, radii, mask, colors = RenderPreprocessFunction.apply(
             means, scales, quaternions, opacities, world_to_camera, intrinsic, sh_coeffs_dc,
             sh_coeffs_rest, near_plane, far_plane, min_opacity, min_radius, max_radius, width,
-            height, sink)
+            height, sink, training)
         colors_ready = sink[0] if sink else None
 
     tile_size = 16

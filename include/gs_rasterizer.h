@@ -295,6 +295,15 @@ int gs_rasterize_backward(const float *grad_image, const float *image,
  *   launches: one workgroup per compute unit (more beyond 32 Gaussians per
  *   thread) walks the Gaussians, leaving the rest of each unit's slots to the
  *   other stream.
+ * gs_evaluate_sh_render_cache: gs_evaluate_sh_render (beside = 0) or
+ *   gs_evaluate_sh_render_beside (beside != 0) that also writes the colour-
+ *   gradient cache sh_cache: 10 floats per Gaussian (8-byte aligned), the
+ *   rows d raw_c / d mean (c = 0..2, through the view direction) and, in the
+ *   tenth, the clamp's pass bits as a uint32 (bit c where raw_c + 0.5 >= 0);
+ *   rows outside the mask are not written.  gs_render_preprocess_backward and
+ *   gs_preprocess_backward take it in place of sh_dc and sh_rest, which they
+ *   then do not read (the same results, bit for bit).  No counterpart in the
+ *   reference extension.
  * gs_evaluate_sh_render_backward: its gradient (the clamp passes the gradient
  *   where raw + 0.5 >= 0, as torch.clamp_min does); accumulate_means != 0 adds
  *   the means gradient to grad_means instead of overwriting it.
@@ -317,6 +326,10 @@ int gs_evaluate_sh_render(const float *world_to_camera, const float *means, cons
 int gs_evaluate_sh_render_beside(const float *world_to_camera, const float *means,
                                  const float *sh_dc, const float *sh_rest, const uint8_t *mask,
                                  int64_t n, float *colors, hipStream_t stream);
+int gs_evaluate_sh_render_cache(const float *world_to_camera, const float *means,
+                                const float *sh_dc, const float *sh_rest, const uint8_t *mask,
+                                int64_t n, int32_t beside, float *colors, float *sh_cache,
+                                hipStream_t stream);
 int gs_evaluate_sh_render_backward(const float *grad_colors, const float *world_to_camera,
                                    const float *means, const float *sh_dc, const float *sh_rest,
                                    const uint8_t *mask, int64_t n, int32_t accumulate_means,
@@ -357,7 +370,10 @@ int gs_rasterize_display_backward(const float *grad_display, const float *image,
  * quats_raw and grad_quats_raw must be 16-byte aligned.  With colors NULL the
  * forward skips the colours (sh_dc and sh_rest may then be NULL): a caller can
  * compute them with gs_evaluate_sh_render_beside on another stream, beside
- * binning.
+ * binning.  sh_cache: NULL, or (with colors) the colour-gradient cache that
+ * gs_evaluate_sh_render_cache describes, written beside the colours; given to
+ * gs_preprocess_backward (sh_dc and sh_rest may then be NULL) it replaces the
+ * backward's read of the 180-byte SH rows with 40 bytes per Gaussian.
  */
 int gs_preprocess_forward(const float *means, const float *log_scales, const float *quats_raw,
                           const float *opacity_logits, const float *sh_dc, const float *sh_rest,
@@ -365,7 +381,8 @@ int gs_preprocess_forward(const float *means, const float *log_scales, const flo
                           float near_plane, float far_plane, float min_opacity, float min_radius,
                           float max_radius, int32_t width, int32_t height, float *points_image,
                           float *depths, float *cov_image, float *cov_inv_image, float *radii,
-                          uint8_t *mask, float *opacities, float *colors, hipStream_t stream);
+                          uint8_t *mask, float *opacities, float *colors, float *sh_cache,
+                          hipStream_t stream);
 int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov_inv_image,
                            const float *grad_opacities, const float *grad_colors,
                            const float *means, const float *log_scales, const float *quats_raw,
@@ -375,7 +392,7 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
                            int32_t width, int32_t height, float *grad_means,
                            float *grad_log_scales, float *grad_quats_raw,
                            float *grad_opacity_logits, float *grad_sh_dc, float *grad_sh_rest,
-                           hipStream_t stream);
+                           const float *sh_cache, hipStream_t stream);
 
 /*
  * The drop-in render()'s backward of projection and colours in one pass:
@@ -387,7 +404,9 @@ int gs_preprocess_backward(const float *grad_points_image, const float *grad_cov
  * from gs_project_points, sh_rest (N, 15, 3).  Each output equals the
  * corresponding output of the two entries (the means: their sum).  No
  * counterpart in the reference extension, whose wrapper runs the two
- * backwards as separate autograd nodes.
+ * backwards as separate autograd nodes.  sh_cache: NULL, or the cache
+ * gs_evaluate_sh_render_cache wrote for the same inputs (sh_dc and sh_rest may
+ * then be NULL).
  */
 int gs_render_preprocess_backward(const float *grad_points_image,
                                   const float *grad_cov_inv_image, const float *grad_colors,
@@ -398,7 +417,7 @@ int gs_render_preprocess_backward(const float *grad_points_image,
                                   const float *intrinsic, int64_t n, int32_t width,
                                   int32_t height, float *grad_means, float *grad_scales,
                                   float *grad_quaternions, float *grad_sh_dc, float *grad_sh_rest,
-                                  hipStream_t stream);
+                                  const float *sh_cache, hipStream_t stream);
 
 /*
  * The caller-side glue of a training step (scripts/train.py:135-143,187-191),

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_strings(lib):
-    assert lib.gs_abi_version() == 19
+    assert lib.gs_abi_version() == 20
     assert lib.gs_status_string(0) == b"success"
     for code in (-1, -2, -3, -4):
         assert lib.gs_status_string(code) not in (b"", b"unknown status")
@@ -90,6 +90,14 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.gs_evaluate_sh_render_beside(*([null] * 5), 10, null, null) == -1
     assert lib.gs_evaluate_sh_render_beside(*([null] * 5), -1, null, null) == -1
     assert lib.gs_evaluate_sh_render_beside(*([null] * 5), 0, null, null) == 0  # nothing to do
+    # the colour launch that also writes the colour-gradient cache: the cache is
+    # required and must be 8-byte aligned (rows of 10 floats read as float2)
+    some = ctypes.c_void_p(4096)  # never dereferenced: every call below is rejected first
+    assert lib.gs_evaluate_sh_render_cache(*([some] * 5), 10, 0, some, null, null) == -1
+    assert lib.gs_evaluate_sh_render_cache(*([some] * 5), 10, 0, some,
+                                           ctypes.c_void_p(4100), null) == -1
+    assert lib.gs_evaluate_sh_render_cache(*([null] * 5), 0, 1, null, null, null) == 0
+    assert lib.gs_evaluate_sh_render_cache(*([null] * 5), -1, 0, null, null, null) == -1
     assert lib.gs_rasterize(null, null, 4, 10, *([null] * 4), 10, 32, 32, 16, 1e-4, 1e-4, 9.21,
                             null, null) == -1
     assert lib.gs_rasterize(null, null, 4, 2**31, *([null] * 4), 10, 32, 32, 16, 1e-4, 1e-4,

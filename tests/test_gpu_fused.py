@@ -101,6 +101,32 @@ def test_fused_preprocess_equals_unfused_sequence(gpu):
     gls, gqr, glog = cr.activate_backward(gsc, gq, ups[2], s, raw["quats_raw"], o)
     for a, b in zip(got, (gm, gls, gqr, glog, gdc, grest)):
         assert torch.equal(a, b)
+    # the colour-gradient cache, written by the joint forward or the grid-capped
+    # colour launch (identical rows), replaces the SH rows in the backward: the
+    # same gradients, bit for bit, without reading sh_dc / sh_rest
+    keep = ref[5]
+    cache = torch.full((n, 10), float("nan"), device=dev)
+    fwd_c = cr.preprocess_forward(raw["means"], raw["log_scales"], raw["quats_raw"],
+                                  raw["opacity_logits"], raw["sh_dc"], raw["sh_rest"], w2c, K,
+                                  *args, sh_cache=cache)
+    for a, b in zip(fwd_c, fwd):
+        assert torch.equal(a, b)
+    cache_b = torch.full((n, 10), float("nan"), device=dev)
+    col_b = cr.evaluate_spherical_harmonics_render(w2c, raw["means"], raw["sh_dc"],
+                                                   raw["sh_rest"], keep, beside=True,
+                                                   sh_cache=cache_b)
+    assert torch.equal(col_b, col)
+    assert torch.equal(cache[keep].view(torch.int32), cache_b[keep].view(torch.int32))
+    assert bool(torch.isnan(cache[~keep]).all())  # rows outside the mask are not written
+    got_c = cr.preprocess_backward(*ups, raw["means"], raw["log_scales"], raw["quats_raw"],
+                                   raw["opacity_logits"], None, None, ref[2], keep, w2c, K, W,
+                                   H, sh_cache=cache)
+    for a, b in zip(got_c, got):
+        assert torch.equal(a, b)
+    with pytest.raises(RuntimeError, match="sh_cache"):
+        cr.preprocess_forward(raw["means"], raw["log_scales"], raw["quats_raw"],
+                              raw["opacity_logits"], raw["sh_dc"], raw["sh_rest"], w2c, K, *args,
+                              with_colors=False, sh_cache=cache)
 
 
 def _written_schedule(sched, n_tiles):

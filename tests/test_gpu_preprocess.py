@@ -122,6 +122,48 @@ def test_sh_forward_backward(gpu, sh_sigmoid):
         assert helpers.rel_l2(a, b) <= 1e-4, nm
 
 
+def test_sh_cache_rows_and_pass_bits(gpu):
+    """The colour-gradient cache the render colour kernel writes: rows 0..2 are
+    d raw_c / d mean (through the view direction), checked against float64
+    autograd of the oracle's SH evaluation; the pass bits are those of the clamp
+    max(raw + 0.5, 0) (set where raw + 0.5 >= 0), checked against the oracle's
+    raw colours away from the boundary and against the kernel's own colours."""
+    g = torch.Generator().manual_seed(41)
+    n = 4000
+    w2c = torch.eye(4)
+    w2c[:3, 3] = torch.tensor([0.2, -0.1, 3.0])
+    means = torch.randn(n, 3, generator=g)
+    dc = torch.randn(n, 3, generator=g)
+    rest = torch.randn(n, 15, 3, generator=g) * 0.3
+    mask = torch.rand(n, generator=g) > 0.1
+    d = lambda t: t.to(gpu)  # noqa: E731
+    cache = cr.sh_cache_empty(n, gpu)
+    col = cr.evaluate_spherical_harmonics_render(d(w2c), d(means), d(dc), d(rest), d(mask),
+                                                 sh_cache=cache)
+    cache = cache.cpu()
+    m = cache[:, :9].reshape(n, 3, 3)[mask].double()
+    bits = cache[:, 9].view(torch.int32)[mask]
+
+    cam = preprocess.camera_position(w2c.double())
+    mu = means[mask].double().requires_grad_(True)
+    raw = preprocess.sh_raw(dc[mask].double(), rest[mask].double(),
+                            preprocess.view_directions(mu, cam))
+    jac = torch.stack([torch.autograd.grad(raw[:, c].sum(), mu, retain_graph=True)[0]
+                       for c in range(3)], dim=1)  # (kept, 3 channels, 3 coords)
+    err = (m - jac).norm(dim=2) / jac.norm(dim=2).clamp_min(1e-6)
+    assert float(err.max()) <= 1e-4
+    raw = raw.detach()
+    want = ((raw + 0.5 >= 0).int() * torch.tensor([1, 2, 4])).sum(dim=1).int()
+    clear = ((raw + 0.5).abs() > 1e-4).all(dim=1)
+    assert int(clear.sum()) > 0.9 * int(mask.sum())
+    assert torch.equal(bits[clear], want[clear])
+    assert int((bits & ~7).abs().sum()) == 0
+    # a positive colour always passes its gradient
+    pos = col.cpu()[mask] > 0
+    for c in range(3):
+        assert bool(((bits[pos[:, c]] >> c) & 1).all())
+
+
 def test_project_points_bitexact_headline(gpu):
     """BASELINE config 3 at full size (1M Gaussians, 1920x1080, near 0.2): every
     projection output bit-identical to the oracle."""

@@ -309,6 +309,14 @@ def test_render_preprocess_backward_equals_the_two_entries(gpu):
     assert torch.equal(fm, pm + sm)
     assert torch.equal(fs, ps) and torch.equal(fq, pq)
     assert torch.equal(fdc, sdc) and torch.equal(frest, srest)
+    # from the forward's colour-gradient cache instead of the SH rows: bit-equal
+    cache = cr.sh_cache_empty(n, gpu)
+    col_c = cr.evaluate_spherical_harmonics_render(w2c, means, dc, rest, mask, sh_cache=cache)
+    assert torch.equal(col_c, cr.evaluate_spherical_harmonics_render(w2c, means, dc, rest, mask))
+    cached = cr.render_preprocess_backward(gp, gc, gcol, means, scales, quats, None, None, cov,
+                                           mask, w2c, K, 200, 150, sh_cache=cache)
+    for a, b in zip(cached, (fm, fs, fq, fdc, frest)):
+        assert torch.equal(a, b)
     # a quaternion view that is not 16-byte aligned (the entry takes any row start)
     wide = torch.zeros(n * 4 + 1, device=gpu)
     wide[1:] = quats.flatten()
