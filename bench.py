@@ -1132,6 +1132,16 @@ def main(argv=None):
         drop_in = {"ms_per_step": round(d["ms"], 3), "loss": d["loss"],
                    "device_busy": d["device_busy"],
                    "stages": roofline(d, scene["name"])["per_stage"]}
+    graph = None
+    if args.path == "fused":  # the same step captured once and replayed from a HIP graph
+        dev = torch.device("cuda:0")
+        leaves = {k: v.to(dev).requires_grad_(True) for k, v in scene["params"].items()}
+        cam = dict(scene["camera"], w2c=scene["camera"]["w2c"].to(dev),
+                   K=scene["camera"]["K"].to(dev))
+        target = scene["target"].to(dev)
+        graph = run_graph(lambda: fused_step(leaves, cam, target), args.steps, args.warmup,
+                          res["loss"])
+        del leaves, target
     view_cache = None
     if args.path == "fused":
         v = run_gpu(scene, args.steps, args.warmup, "fused", schedule_cache=True)
@@ -1179,6 +1189,7 @@ def main(argv=None):
         "stages": rl["per_stage"],
         "loss": res["loss"],
         "drop_in": drop_in,
+        "graph": graph,
         "view_schedule_cache": view_cache,
         "ssim": ssim,
         "train_stress": train,
