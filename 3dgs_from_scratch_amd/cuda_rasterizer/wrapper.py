@@ -234,10 +234,14 @@ def render(
 
         training = torch.is_grad_enabled()
         sink = [] if training and means.shape[0] >= BESIDE_MIN_GAUSSIANS else None
+        # the colour-gradient cache only when the node will have a backward
+        with_cache = training and any(
+            isinstance(t, torch.Tensor) and t.requires_grad
+            for t in (means, scales, quaternions, sh_coeffs_dc, sh_coeffs_rest))
         points_img, depths, cov_inv_img, radii, mask, colors = RenderPreprocessFunction.apply(
             means, scales, quaternions, opacities, world_to_camera, intrinsic, sh_coeffs_dc,
             sh_coeffs_rest, near_plane, far_plane, min_opacity, min_radius, max_radius, width,
-            height, sink, training)
+            height, sink, with_cache)
         colors_ready = sink[0] if sink else None
 
     tile_size = 16
