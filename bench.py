@@ -849,6 +849,31 @@ def profiled_traffic(stage: str, workload: str):
     return None
 
 
+# kernels of the HBM-bound stages (preprocess, the colours, binning, preprocess backward)
+# of the fused step, by name prefix
+HBM_STAGE_KERNELS = ("preprocess_forward_kernel", "sh_forward_kernel", "count_tiles_kernel",
+                     "depth_upsweep0_kernel", "radix_upsweep_kernel", "radix_downsweep_kernel",
+                     "digit_scan_kernel", "segment_sort_kernel", "l1_count_kernel",
+                     "l1_scatter_kernel", "l2_count_kernel", "l2_prefix_kernel",
+                     "l2_scatter_kernel", "preprocess_backward_kernel")
+
+
+def counter_stage_bytes(workload: str) -> float | None:
+    """HBM bytes per fused step of the HBM-stage kernels by the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE profile (launches per step x bytes per launch), or None
+    without the profile."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.md")
+    if not os.path.exists(path):
+        return None
+    rows = re.findall(r"^step_kernel\[(.+?)\]:\s*([0-9.eE+]+)\s+([0-9.eE+]+)\s*$",
+                      open(path).read(), re.M)
+    total = sum(float(launches) * float(nbytes) for name, launches, nbytes in rows
+                if name.split("<")[0] in HBM_STAGE_KERNELS)
+    return total or None
+
+
 def roofline(res: dict, workload: str) -> dict:
     n, k, nt = res["n"], res["keys"], res["n_tiles"]
     hw = res["width"] * res["height"]
@@ -893,6 +918,14 @@ def roofline(res: dict, workload: str) -> dict:
                ms=round(ht * 1e3, 4))
     if beside:
         hbm["beside_binning"] = sorted(beside)
+    # the same window with the bytes the counters measured for those stages' kernels
+    # (FETCH_SIZE + WRITE_SIZE per launch, profiles/hbm_traffic_<workload>.md): wasted
+    # re-reads count here, so it is the DRAM traffic rate, not algorithmic work
+    counted = counter_stage_bytes(workload)
+    if counted and ht:
+        hbm["counter_bytes"] = int(counted)
+        hbm["counter_achieved"] = round(counted / ht / 1e9, 1)
+        hbm["counter_frac"] = round(counted / ht / 1e9 / HBM_PEAK_GBS, 4)
     # the reference binning algorithm's bytes per second of this build's binning
     bt = sum(res["stages"][s][1] for s in ("bin_count", "bin_sort") if s in res["stages"]) * 1e-3
     if bt:
