@@ -795,6 +795,20 @@ void blend_forward_kernel(
     if ((unsigned)tile >= (unsigned)n_tiles) return;  // uniform across the workgroup
     const LanePixels<S> pix = lane_pixels<W>(tile, tiles_x, width, height);
     const TileSpan span = tile_span(offsets, n_tiles, k, tile);
+    if (n_tiles <= kCheckpointMaxTiles) {
+        // Grids whose tiles all start at once end with their longest walks: give
+        // the tiles with long lists (their walks' upper bound) more of the SIMDs'
+        // issue slots while they share them.  On larger grids the raised
+        // priority delays the tiles that start later and the kernel ends later.
+        const int64_t mean = (k - (int64_t)offsets[0]) / n_tiles;  // offsets[0]: the capped shift
+        const int64_t len = span.end - span.start;
+        if (len >= 3 * mean / 2)
+            __builtin_amdgcn_s_setprio(3);
+        else if (len >= 6 * mean / 5)
+            __builtin_amdgcn_s_setprio(2);
+        else if (len >= 9 * mean / 10)
+            __builtin_amdgcn_s_setprio(1);
+    }
     float cr[S], cg[S], cb[S];
     uint32_t work = 0;
     int n_ck = 0;
