@@ -1641,6 +1641,35 @@ __device__ void tile_launch_order(int x, int n_tiles, int64_t k, const int32_t *
     }
 }
 
+// The level-2 scatter's loop over the 64 local tiles: the lanes covering tile j
+// (the AND of its row and column ballots) store their id at the tile's base for
+// this wave plus their rank among those lanes.  kCheck: skip a tile whose run
+// would end past ids_out.
+template <bool k32, bool kCheck>
+__device__ __forceinline__ void scatter_runs(const uint64_t (&rows)[kSuper],
+                                             const uint64_t (&cols)[kSuper], uint32_t my_base,
+                                             uint32_t k_lo, int64_t k, int32_t g,
+                                             int32_t *__restrict__ ids_out) {
+#pragma unroll
+    for (int j = 0; j < kSuperLocal; ++j) {
+        const uint64_t bal = rows[j / kSuper] & cols[j % kSuper];
+        if (bal == 0) continue;  // uniform: no lane covers tile j
+        const uint32_t b = __builtin_amdgcn_readlane(my_base, j);
+        if (kCheck) {
+            const uint32_t cnt = (uint32_t)__popcll(bal);
+            if (k32 ? (b + cnt > k_lo) : ((int64_t)b + cnt > k)) continue;  // run inside ids_out
+        }
+        if (__builtin_amdgcn_inverse_ballot_w64(bal)) {
+            const uint32_t p = __builtin_amdgcn_mbcnt_hi(
+                (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, b));
+            if (k32)  // byte offset p * 4 < 2^32: a 32-bit offset from the uniform base
+                *reinterpret_cast<int32_t *>(reinterpret_cast<char *>(ids_out) + (p << 2)) = g;
+            else
+                ids_out[(int64_t)p] = g;
+        }
+    }
+}
+
 // With launch_order, the grid has kBinXcds more workgroups than the scatter
 // needs (the first ones, one per XCD): each writes the blend launch order of
 // one XCD range while the scatter runs.
@@ -1659,7 +1688,8 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
     if (!l2_block(a, x, launch_order ? kBinXcds : 0, table)) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     uint64_t rows[kSuper], cols[kSuper];
-    base[wave][lane] = wave_masks(x, rows, cols);
+    const uint32_t my_cnt = wave_masks(x, rows, cols);  // lane j: this wave's entries of tile j
+    base[wave][lane] = my_cnt;
     __syncthreads();
     if (threadIdx.x < kSuperLocal) {  // first position of each wave's entries of tile j
         uint32_t pos = x.trow;  // from l2_prefix_kernel
@@ -1674,22 +1704,15 @@ __global__ __launch_bounds__(kL2Threads) void l2_scatter_kernel(L2Args a,
     const uint32_t my_base = base[wave][lane];  // lane j: tile j
     // k32: K < 2^30, so b + count cannot wrap in 32 bits (a scalar compare)
     const uint32_t k_lo = (uint32_t)(a.k < 0xffffffffLL ? a.k : 0xffffffffLL);
-#pragma unroll
-    for (int j = 0; j < kSuperLocal; ++j) {
-        const uint64_t bal = rows[j / kSuper] & cols[j % kSuper];
-        if (bal == 0) continue;  // uniform: no lane covers tile j
-        const uint32_t b = __builtin_amdgcn_readlane(my_base, j);
-        const uint32_t cnt = (uint32_t)__popcll(bal);
-        if (k32 ? (b + cnt > k_lo) : ((int64_t)b + cnt > a.k)) continue;  // run inside ids_out
-        if (__builtin_amdgcn_inverse_ballot_w64(bal)) {
-            const uint32_t p = __builtin_amdgcn_mbcnt_hi(
-                (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, b));
-            if (k32)  // byte offset p * 4 < 2^32: a 32-bit offset from the uniform base
-                *reinterpret_cast<int32_t *>(reinterpret_cast<char *>(ids_out) + (p << 2)) = x.g;
-            else
-                ids_out[(int64_t)p] = x.g;
-        }
-    }
+    // every run of the wave inside ids_out (always, for consistent counts): one
+    // check for the wave instead of one per tile, which leaves the loop's scalar
+    // work (the per-tile masks and the exec mask) at about two thirds
+    const bool outside = my_cnt != 0u && (k32 ? my_base + my_cnt > k_lo
+                                               : (int64_t)my_base + my_cnt > a.k);
+    if (__ballot(outside) == 0)
+        scatter_runs<k32, false>(rows, cols, my_base, k_lo, a.k, x.g, ids_out);
+    else
+        scatter_runs<k32, true>(rows, cols, my_base, k_lo, a.k, x.g, ids_out);
 }
 
 // Level-1 entries: for the Gaussian at depth-order position r, one entry per
