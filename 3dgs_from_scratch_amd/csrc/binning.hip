@@ -1660,12 +1660,13 @@ __device__ __forceinline__ void scatter_runs(const uint64_t (&rows)[kSuper],
             if (k32 ? (b + cnt > k_lo) : ((int64_t)b + cnt > k)) continue;  // run inside ids_out
         }
         if (__builtin_amdgcn_inverse_ballot_w64(bal)) {
-            const uint32_t p = __builtin_amdgcn_mbcnt_hi(
-                (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, b));
-            if (k32)  // byte offset p * 4 < 2^32: a 32-bit offset from the uniform base
-                *reinterpret_cast<int32_t *>(reinterpret_cast<char *>(ids_out) + (p << 2)) = g;
+            // rank among the tile's lanes; the run's start joins as a scalar
+            const uint32_t r = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (k32)  // byte offset (b + r) * 4 < 2^32: a 32-bit offset from the uniform base
+                *reinterpret_cast<int32_t *>(reinterpret_cast<char *>(ids_out) + ((r << 2) + (b << 2))) = g;
             else
-                ids_out[(int64_t)p] = g;
+                ids_out[(int64_t)b + r] = g;
         }
     }
 }
