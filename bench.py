@@ -40,6 +40,9 @@ for _p in (ROOT, os.path.join(ROOT, "3dgs_from_scratch_amd")):
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# untimed work before each timed region's warm-up: the GPU lowers its clocks
+# while idle, and the steps right after an idle pause run up to 10% slower
+SETTLE_S = 0.2
 FP32_PEAK_TFLOPS = 157.3
 
 METRIC = "fwd+bwd ms/iter at 1M Gaussians 1080p SH3; achieved HBM GB/s vs peak"
@@ -246,9 +249,25 @@ def busy(device_ms, wall_ms: float):
     return {"device_ms": round(device_ms, 4), "busy": round(device_ms / wall_ms, 3)}
 
 
+def settle(step, seconds: float = SETTLE_S) -> int:
+    """Untimed calls of `step` for at least `seconds` of wall time (the host waits
+    on the device within each step, so this is GPU time too), after which the
+    GPU runs at its working clocks; returns the number of calls."""
+    n = 0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        step()
+        n += 1
+    torch.cuda.synchronize()
+    return n
+
+
 def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
             schedule_cache: bool = False) -> dict:
-    """Times `steps` steps after `warmup`; path "fused" (fused_step) or "drop-in"
+    """Runs `warmup` steps, the profiler's kernel time (`steps` steps), untimed
+    steps for SETTLE_S seconds (so that the timed region's warm-up follows GPU
+    work, not a GPU idling at low clocks), `warmup` steps, times `steps` steps,
+    then the per-stage breakdown (`steps` steps).  path: "fused" (fused_step) or "drop-in"
     (gpu_step: PyTorch activations and loss around the drop-in render()).
     schedule_cache: the fused step with a per-view schedule cache (the view
     repeats every step, as a training view does every epoch)."""
@@ -270,14 +289,26 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
         step()
     torch.cuda.synchronize()
 
+    # the kernel time per step from the profiler first; then untimed steps for a
+    # while, since the GPU's clocks drop while it idles (the profiler's host-side
+    # processing, the uploads) and the steps after such a pause run up to 10%
+    # slower until they are back up; then the timed region's warm-up
+    device_ms = device_time(step, steps)
+    settle(step)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
     # timed region: wall clock with a synchronize on both sides, plus HIP events
-    # around the blend backward (the dominant kernel) on the stream it runs on
+    # around the blend backward (the dominant kernel) on the stream it runs on, on
+    # every other step: each event pair adds about 3 us to its step, and the
+    # sampled launches' average is the kernel's launch duration
     _lib.timer.reset()
     _lib.timer.only = DOMINANT_STAGES
-    _lib.timer.enabled = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for i in range(steps):
+        _lib.timer.enabled = i % 2 == 0
         loss, image = step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -293,7 +324,6 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
         step()
     _lib.timer.enabled = False
     stages = _lib.timer.summary()
-    device_ms = device_time(step, steps)
 
     # workload statistics of one step
     from cuda_rasterizer import compute_tile_intersection, project_points, rasterize_work
@@ -306,7 +336,7 @@ def run_gpu(scene: dict, steps: int, warmup: int, path: str = "fused",
         visited, composited = rasterize_work(off, ids, pts, conic, opac, cam["width"],
                                              cam["height"], 16, 1e-4, 1e-4, 9.21)
     return dict(ms=ms, stages={k: (c, t / steps) for k, (c, t) in stages.items()},
-                main_stages={k: (c, t / steps) for k, (c, t) in main_stages.items()}, steps=steps,
+                main_launch_ms={k: t / c for k, (c, t) in main_stages.items() if c}, steps=steps,
                 n=scene["params"]["means"].shape[0], n_visible=int(mask.sum()), keys=int(ids.numel()),
                 n_tiles=int(off.numel()), visited=visited, composited=composited,
                 loss=float(loss.detach()), width=cam["width"], height=cam["height"],
@@ -323,6 +353,7 @@ def run_full_loss(scene: dict, steps: int, warmup: int, ssim_lambda: float = 0.2
     cam["w2c"] = cam["w2c"].to(dev)
     cam["K"] = cam["K"].to(dev)
     target = scene["target"].to(dev)
+    settle(lambda: fused_step(leaves, cam, target, ssim_lambda))  # as in run_gpu
     for _ in range(warmup):
         fused_step(leaves, cam, target, ssim_lambda)
     torch.cuda.synchronize()
@@ -467,13 +498,18 @@ def run_views(fns, steps: int, warmup: int, eager_loss: float, streams: int = 4)
 
 def run_graph(step, steps: int, warmup: int, eager_loss: float) -> dict:
     """The same step captured into a HIP graph (cuda_rasterizer.graphs.CapturedStep)
-    and replayed: wall clock over `steps` replays after `warmup`, synchronised on
-    both sides; every capped sort of the last replay is checked against its
+    and replayed: wall clock over `steps` replays after `warmup` (which follow the
+    profiler's replays and SETTLE_S seconds of untimed ones), synchronised on both
+    sides; every capped sort of the last replay is checked against its
     capacities afterwards, and its loss against the eager step's (the parameters
     do not change between steps, so the two agree up to float summation order)."""
     from cuda_rasterizer.graphs import CapturedStep
 
     captured = CapturedStep(step, warmup=max(warmup, 1))
+    # the profiler's kernel time first, then untimed replays that keep the GPU at
+    # its working clocks up to the timed region's warm-up (as in run_gpu)
+    device_ms = device_time(captured.replay, steps)
+    settle(captured.replay)
     for _ in range(warmup):
         captured.replay()
     torch.cuda.synchronize()
@@ -489,7 +525,7 @@ def run_graph(step, steps: int, warmup: int, eager_loss: float) -> dict:
     if abs(loss - eager_loss) > 1e-5 * abs(eager_loss):
         raise RuntimeError(f"bench: graph replay loss {loss} != eager loss {eager_loss}")
     return {"ms_per_step": round(ms, 4), "loss": round(loss, 6),
-            "device_busy": busy(device_time(captured.replay, steps), ms)}
+            "device_busy": busy(device_ms, ms)}
 
 
 def run_small_configs(steps: int, warmup: int, cpu: bool) -> dict:
@@ -889,8 +925,11 @@ def roofline(res: dict, workload: str) -> dict:
 
     dominant = max(res["stages"].items(), key=lambda kv: kv[1][1])[0]
     # the timed loop's own events when they cover the dominant stage
-    calls, ms = res.get("main_stages", {}).get(dominant, res["stages"][dominant])
-    per_launch_s = ms / max(calls / steps, 1) * 1e-3
+    launch_ms = res.get("main_launch_ms", {}).get(dominant)
+    if launch_ms is None:
+        calls, ms = res["stages"][dominant]
+        launch_ms = ms / max(calls / steps, 1)
+    per_launch_s = launch_ms * 1e-3
     traffic = profiled_traffic(dominant, workload)
     if dominant in BLEND_FLOP_PER_PAIR:
         achieved = res["visited"] * BLEND_FLOP_PER_PAIR[dominant] / per_launch_s / 1e12
