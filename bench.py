@@ -249,14 +249,18 @@ def busy(device_ms, wall_ms: float):
     return {"device_ms": round(device_ms, 4), "busy": round(device_ms / wall_ms, 3)}
 
 
-def settle(step, seconds: float = SETTLE_S) -> int:
-    """Untimed calls of `step` for at least `seconds` of wall time (the host waits
-    on the device within each step, so this is GPU time too), after which the
-    GPU runs at its working clocks; returns the number of calls."""
+def settle(step, seconds: float = SETTLE_S, wait_each: bool = False) -> int:
+    """Untimed calls of `step` for at least `seconds` of wall time, after which the
+    GPU runs at its working clocks; returns the number of calls.  An eager step
+    waits on the device within each call (the capped sort's check), so the host
+    stays at most a step ahead; a graph replay does not, and is waited for after
+    each call (`wait_each`) so that the loop does not queue thousands."""
     n = 0
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end:
         step()
+        if wait_each:
+            torch.cuda.synchronize()
         n += 1
     torch.cuda.synchronize()
     return n
@@ -388,11 +392,16 @@ def run_ssim(scene: dict, steps: int, warmup: int) -> dict:
     x1 = img.detach().permute(2, 0, 1).unsqueeze(0)
     x2 = target.permute(2, 0, 1).unsqueeze(0)
 
-    v = None
-    for _ in range(max(warmup, 1)):
+    def loss_term():
         img.grad = None
         v = 1.0 - fused_ssim(img.permute(2, 0, 1).unsqueeze(0), x2, padding="valid")
         v.backward()
+        return v
+
+    settle(loss_term)
+    v = None
+    for _ in range(max(warmup, 1)):
+        v = loss_term()
     mean, maps = ssim_forward(x1, x2, "valid")
     grad_mean = torch.ones((), device=dev)
     torch.cuda.synchronize()
@@ -444,6 +453,7 @@ def run_cameras(scene: dict, steps: int, warmup: int) -> dict:
             total = total + loss.detach() * weight
         return total
 
+    settle(step)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -479,6 +489,7 @@ def run_views(fns, steps: int, warmup: int, eager_loss: float, streams: int = 4)
     from cuda_rasterizer.graphs import ConcurrentSteps
 
     views = ConcurrentSteps(fns, streams=streams, warmup=max(warmup, 1))
+    settle(views.replay, wait_each=True)
     for _ in range(warmup):
         views.replay()
     torch.cuda.synchronize()
@@ -509,7 +520,7 @@ def run_graph(step, steps: int, warmup: int, eager_loss: float) -> dict:
     # the profiler's kernel time first, then untimed replays that keep the GPU at
     # its working clocks up to the timed region's warm-up (as in run_gpu)
     device_ms = device_time(captured.replay, steps)
-    settle(captured.replay)
+    settle(captured.replay, wait_each=True)
     for _ in range(warmup):
         captured.replay()
     torch.cuda.synchronize()
@@ -575,6 +586,7 @@ def run_forward(scene: dict, steps: int, warmup: int) -> dict:
             return render(w2c, K, W, H, p["means"], scales, quats, opac, p["sh_dc"],
                           p["sh_rest"], near_plane=cam["near"])
 
+        settle(step)
         for _ in range(warmup):
             step()
         torch.cuda.synchronize()
