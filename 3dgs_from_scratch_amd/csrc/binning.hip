@@ -859,6 +859,10 @@ struct SegArgs {
     const uint2 *rects;             // packed tile rectangle per Gaussian
     uint64_t *counts_out;           // general level 1: supertile count per depth position
     uint2 *rects_out;               // one-pass level 1: rectangle per depth position
+    // one-pass level 1: its (supertile, block) entry counts, added here per emitted
+    // position (hist_index(s, p / kL1Threads, l1_nblocks), zeroed by count_tiles_kernel)
+    uint32_t *l1_hist;
+    int super_x, l1_nblocks;
 };
 
 // Per-position outputs of the sorted order: the rectangle or the supertile
@@ -871,6 +875,49 @@ __device__ __forceinline__ void seg_store(const SegArgs &a, int64_t p, uint2 r) 
 __device__ __forceinline__ void seg_emit(const SegArgs &a, int64_t p, uint32_t val) {
     seg_store(a, p, rect_or_empty(a.rects, val, a.n));
 }
+
+// Level-1 positions per workgroup (the blocks of the one-pass level 1's counts).
+constexpr int kL1Threads = 512;
+
+// Calls f(s) for every supertile the packed tile rectangle r meets (none when empty).
+template <typename F>
+__device__ __forceinline__ void for_each_supertile(uint2 r, int super_x, F f) {
+    const TileRect t = unpack_rect(r);
+    if (t.tx0 > t.tx1) return;
+    for (int y = t.ty0 / kSuper; y <= t.ty1 / kSuper; ++y)
+        for (int x = t.tx0 / kSuper; x <= t.tx1 / kSuper; ++x) f(y * super_x + x);
+}
+
+// The LDS path's level-1 counts: the chunk [start, start + size) meets at most
+// three kL1Threads-position blocks (size <= kSegMax); each is counted per
+// supertile in the now free key buffer and its non-zero counts added to the
+// table.  Every thread of the workgroup calls it (it contains barriers).
+__device__ void seg_l1_counts(const SegArgs &a, uint32_t start, uint32_t size,
+                              const uint2 (&r)[kSegItems], const bool (&valid)[kSegItems],
+                              int ipw, SegLds &s) {
+    uint32_t *cnt = s.keys[0];  // 3 x kRadixMax counters
+    const uint32_t b0 = start / kL1Threads;
+    const uint32_t nb = (start + size - 1) / kL1Threads - b0 + 1;  // 1..3
+    __syncthreads();  // every thread has read its sorted keys out of the buffers
+    for (int i = threadIdx.x; i < 3 * kRadixMax; i += kSegThreads) cnt[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kSegItems; ++it) {
+        if (!valid[it]) continue;
+        const uint32_t row = (start + (uint32_t)seg_slot(it, ipw)) / kL1Threads - b0;
+        for_each_supertile(r[it], a.super_x,
+                           [&](int st) { atomicAdd(&cnt[row * kRadixMax + st], 1u); });
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nb * kRadixMax; i += kSegThreads) {
+        const uint32_t c = cnt[i];
+        if (c)
+            atomicAdd(&a.l1_hist[hist_index((int)(i % kRadixMax), (int)(b0 + i / kRadixMax),
+                                            a.l1_nblocks)],
+                      c);
+    }
+}
+
 
 // The chunk [start, end) (more than kSegMax keys) sorted by this workgroup
 // through global memory: LSD passes over the varying digits at the chunk's
@@ -954,7 +1001,15 @@ __device__ void seg_sort_global(const SegArgs &a, uint32_t start, uint32_t end, 
     if (src_v != a.vals)
         for (uint32_t t = threadIdx.x; t < size; t += kSegThreads) a.vals[start + t] = src_v[start + t];
     __syncthreads();
-    for (uint32_t t = threadIdx.x; t < size; t += kSegThreads) seg_emit(a, start + t, a.vals[start + t]);
+    for (uint32_t t = threadIdx.x; t < size; t += kSegThreads) {
+        const uint32_t p = start + t;
+        const uint2 r = rect_or_empty(a.rects, a.vals[p], a.n);
+        seg_store(a, p, r);
+        if (a.l1_hist)  // a rare path: one table atomic per (position, supertile)
+            for_each_supertile(r, a.super_x, [&](int st) {
+                atomicAdd(&a.l1_hist[hist_index(st, (int)(p / kL1Threads), a.l1_nblocks)], 1u);
+            });
+    }
 }
 
 __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(SegArgs a) {
@@ -1078,6 +1133,7 @@ __global__ __launch_bounds__(kSegThreads) void segment_sort_kernel(SegArgs a) {
         a.vals[p] = v[it];
         seg_store(a, p, r[it]);
     }
+    if (a.l1_hist) seg_l1_counts(a, start, size, r, valid, ipw, s);  // uniform
 }
 
 // ------------------------------------------------------------- binning
@@ -1097,7 +1153,11 @@ __global__ __launch_bounds__(kSortThreads) void count_tiles_kernel(
     int tile_size, uint2 *__restrict__ rects, uint32_t *__restrict__ depth_keys,
     unsigned long long *__restrict__ block_sums, uint32_t *__restrict__ block_minmax,
     uint32_t hint_kmin, int hint_shift, uint32_t *__restrict__ hist,
-    uint32_t *__restrict__ xform) {
+    uint32_t *__restrict__ xform, uint32_t *__restrict__ zero_words, int64_t zero_count) {
+    // the one-pass level 1's count table, which the segment sort adds into
+    for (int64_t i = (int64_t)blockIdx.x * kSortThreads + threadIdx.x; i < zero_count;
+         i += (int64_t)gridDim.x * kSortThreads)
+        zero_words[i] = 0u;
     // per-wave tiles and supertile entries; Gaussians with tiles, least and
     // greatest key
     __shared__ unsigned long long wave_sum[2][kSortThreads / kWave];
@@ -1749,12 +1809,12 @@ __global__ __launch_bounds__(256) void emit_super_kernel(
 // lanes[w][s] has bit L set when lane L of wave w meets supertile s; the
 // block's count of s is the sum of popcounts over its waves, and an entry's
 // rank among the block's entries of s is the popcount of the lanes before it.
-// l1_count_kernel writes the counts to a digit-major table, digit_scan_kernel
-// turns them into positions, and l1_scatter_kernel writes every entry's id and
-// packed tile rectangle at its position in the supertile-sorted list, which is
-// stable: (supertile, depth order).
+// The segment sort adds each block's counts to a digit-major table as it emits
+// the depth order (seg_l1_counts), digit_scan_kernel turns them into positions,
+// and l1_scatter_kernel writes every entry's id and packed tile rectangle at
+// its position in the supertile-sorted list, which is stable: (supertile, depth
+// order).
 
-constexpr int kL1Threads = 512;
 constexpr int kL1Waves = kL1Threads / kWave;
 
 struct L1Args {
@@ -1810,27 +1870,6 @@ __device__ __forceinline__ bool l1_lane_masks(const L1Args &a, int64_t blk,
                          (unsigned long long)bit);
     __syncthreads();
     return has;
-}
-
-// hist[s * nblocks + b] = entries of supertile s in block b.
-__global__ __launch_bounds__(kL1Threads) void l1_count_kernel(L1Args a,
-                                                              uint32_t *__restrict__ hist) {
-    __shared__ uint64_t lanes[kL1Waves][kRadixMax];
-    const int64_t blk = xcd_block_live(blockIdx.x, l1_live_blocks(a));
-    if (!l1_live_block(a, blk)) {  // no entries: a zero histogram column
-        if (threadIdx.x < kRadixMax) hist[hist_index(threadIdx.x, (int)blk, a.nblocks)] = 0u;
-        return;
-    }
-    uint32_t g;
-    uint2 packed;
-    TileRect sr;
-    l1_lane_masks(a, blk, lanes, g, packed, sr);
-    if (threadIdx.x < kRadixMax) {
-        uint32_t c = 0;
-#pragma unroll
-        for (int w = 0; w < kL1Waves; ++w) c += (uint32_t)__popcll(lanes[w][threadIdx.x]);
-        hist[hist_index(threadIdx.x, (int)blk, a.nblocks)] = c;
-    }
 }
 
 // The level-2 block plan, from block 0 of l1_scatter_kernel (thread d holds
@@ -2200,8 +2239,8 @@ int check_count_call(const CountCall &c, CountWs &w) {
 }
 
 // Up to kRadixMax supertiles level 1 enumerates the entries from the depth
-// order directly (l1_count_kernel), reading the tile rectangles that the last
-// pass writes in depth order; otherwise it places them with the supertile
+// order directly (counted as the segment sort emits it, scattered by
+// l1_scatter_kernel), reading the tile rectangles written in depth order; otherwise it places them with the supertile
 // counts' exclusive scan in depth order, also written by the last pass.
 bool one_pass_level1(const CountCall &c, Grid &grid) {
     return make_grid(c.width, c.height, c.tile_size, grid) && grid.n_super <= kRadixMax;
@@ -2255,10 +2294,16 @@ int bin_count_begin(const CountCall &c, hipStream_t stream) {
     // with a depth hint the count kernel writes the transform and the first
     // pass's histogram itself; otherwise the upsweep derives the transform from
     // the keys' least and greatest value
+    // the one-pass level 1 adds its counts into a table the count kernel zeroes
+    // (its rows of the grid's supertiles: the level-1 scan reads no others)
+    Grid grid;
+    const bool one_pass_l1 = one_pass_level1(c, grid);
     hipLaunchKernelGGL((count_tiles_kernel<kDepthItems>), dim3(nblocks), dim3(kSortThreads), 0,
                        stream, c.n, c.points_image, c.radii, c.depths, c.mask, c.width, c.height,
                        c.tile_size, w.rects, w.dkeys_a, w.block_sums, w.block_minmax,
-                       c.hint_kmin, hinted ? c.hint_shift : 0, hinted ? hist : nullptr, w.xform);
+                       c.hint_kmin, hinted ? c.hint_shift : 0, hinted ? hist : nullptr, w.xform,
+                       one_pass_l1 ? w.l1_hist : nullptr,
+                       one_pass_l1 ? (int64_t)grid.n_super * l1_blocks(c.n) : (int64_t)0);
     st = launch_status();
     if (st) return st;
     if (!hinted) {
@@ -2294,16 +2339,17 @@ int bin_count_finish(const CountCall &c, hipStream_t stream) {
     sa.rects = w.rects;
     sa.counts_out = one_pass_l1 ? nullptr : w.counts;
     sa.rects_out = one_pass_l1 ? w.rects_depth : nullptr;
+    // the one-pass level 1's (supertile, block) counts, added as the positions are
+    // emitted into the table count_tiles_kernel zeroed
+    sa.l1_hist = one_pass_l1 ? w.l1_hist : nullptr;
+    sa.super_x = grid.super_x;
+    sa.l1_nblocks = (int)l1_blocks(c.n);
     hipLaunchKernelGGL(segment_sort_kernel, dim3(ceil_div(c.n, kSegChunk)), dim3(kSegThreads), 0,
                        stream, sa);
     st = launch_status();
     if (st) return st;
     if (one_pass_l1) {
         const L1Args la = l1_args(w, c.n, 0, grid.super_x);
-        hipLaunchKernelGGL(l1_count_kernel, dim3(la.nblocks), dim3(kL1Threads), 0, stream, la,
-                           w.l1_hist);
-        st = launch_status();
-        if (st) return st;
         hipLaunchKernelGGL(digit_scan_kernel, dim3(grid.n_super), dim3(kScanThreads), 0, stream,
                            w.l1_hist, la.nblocks, w.l1_totals, nullptr, nullptr, 0, nullptr,
                            nullptr, nullptr);

@@ -899,7 +899,7 @@ def profiled_traffic(stage: str, workload: str):
 # of the fused step, by name prefix
 HBM_STAGE_KERNELS = ("preprocess_forward_kernel", "sh_forward_kernel", "count_tiles_kernel",
                      "depth_upsweep0_kernel", "radix_upsweep_kernel", "radix_downsweep_kernel",
-                     "digit_scan_kernel", "segment_sort_kernel", "l1_count_kernel",
+                     "digit_scan_kernel", "segment_sort_kernel",
                      "l1_scatter_kernel", "l2_count_kernel", "l2_prefix_kernel",
                      "l2_scatter_kernel", "preprocess_backward_kernel")
 
